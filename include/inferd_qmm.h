@@ -1,0 +1,145 @@
+/* inferd_qmm.h — C ABI of the MI355X (gfx950) W4 quantized-matmul hot path.
+ *
+ * Drop-in for the kernels under inferd's engine-facing operators
+ *   void Qwen35::gemm(Enc&, const BufRef& A, const QLinear& W, const BufRef& C, int M, int mode, bool defer)
+ *        (reference engine/src/qwen35.h:1465)
+ *   void Qwen35::encode_moe(Enc&, const Layer&, int T)            (reference engine/src/qwen35.h:1869)
+ * The C++ shim that keeps those signatures is inferd_amd/csrc/qwen35_ops.h.
+ *
+ * Conventions (all entry points):
+ *  - Pointers are caller-owned DEVICE pointers; nothing is allocated, freed or synchronised inside. Work is enqueued
+ *    on `stream` (a hipStream_t; NULL = the default stream) in call order, as the reference encodes into the
+ *    caller's serial compute encoder (engine/src/gpu.h:122-163).
+ *  - bf16 tensors are 16-bit bit patterns (uint16_t storage), row-major.
+ *  - Weights: MLX affine 4-bit, group 64 (reference engine/src/weights.h:226-236): wq uint32 [N][ldk/8] with element
+ *    j of a little-endian word at bits 4j; s, b bf16 [N][ldk/64]; w[n][k] = s[n][k/64] * q[n][k] + b[n][k/64].
+ *    ldk = 0 means ldk = K; ldk > K is a K-slice view (reference kslice_of, weights.h:259-268).
+ *    xr = 0x88888888 when the nibbles were flipped in place by ifd_flip_w4 (reference QLinear::flipped), else 0.
+ *  - GEMM store modes (reference engine/kernels/core.metal:14-15): 0 C = bf16(y); 1 C = bf16(y + C) (residual);
+ *    2 C = y as fp32.
+ *  - Every entry point returns IFD_OK or an error code and never exits the process (the reference prints and calls
+ *    exit(1), qwen35.h:1469, 1477); ifd_last_error() returns a message for the calling thread.
+ */
+#ifndef INFERD_QMM_H
+#define INFERD_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  IFD_OK = 0,
+  IFD_ERR_ARG = 1,         /* bad shape, stride, null or misaligned pointer */
+  IFD_ERR_WORKSPACE = 2,   /* workspace missing or smaller than the *_workspace() query */
+  IFD_ERR_LAUNCH = 3,      /* HIP reported an error launching a kernel */
+  IFD_ERR_UNSUPPORTED = 4  /* valid request outside what this build implements */
+};
+
+int ifd_version(void);
+const char* ifd_status_str(int status);
+const char* ifd_last_error(void);
+
+/* ---- dense linears (reference Qwen35::gemm and its sub-paths, engine/src/qwen35.h:1465-1558) ---------------- */
+
+/* Bytes of workspace ifd_gemm_w4 / ifd_qmv_w4 / ifd_qmm_w4 need for this shape (split-K partials). */
+size_t ifd_gemm_w4_workspace(int M, int N, int K);
+
+/* Decode GEMV path, M <= 128 (replaces qmv4 / qmm_splitk + splitk_reduce, core.metal:85-171,
+ * qmm_splitk.metal:14-107; host qwen35.h:1520-1556). A bf16 [M][lda]. */
+int ifd_qmv_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+               int ldk, uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes,
+               void* stream);
+
+/* Prefill GEMM path, any M (replaces MLX affine_qmm_t_nax, quantized_nax.h:1206-1267; host mlx_qmm,
+ * qwen35.h:1427-1462). */
+int ifd_qmm_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+               int ldk, uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes,
+               void* stream);
+
+/* Routed GEMM: picks the GEMV path for M <= 128 and the prefill path above (reference Qwen35::gemm,
+ * qwen35.h:1465). */
+int ifd_gemm_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+                int ldk, uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes,
+                void* stream);
+
+/* In-place nibble flip, wq[i] ^= mask for i < n32 (reference w_flip, w4a8.metal:19-22; flip, qwen35.h:1306-1322). */
+int ifd_flip_w4(uint32_t* wq, size_t n32, uint32_t mask, void* stream);
+
+/* SwiGLU h[r][i] = bf16(float(bf16(g * sigmoid(g))) * u) over rows gu = [gate (I) | up (I)]
+ * (reference silu_mul, core.metal:777-787; moe_silu_mul, moe.metal:103-111). */
+int ifd_silu_mul(const void* gu, void* h, int I, int rows, void* stream);
+
+/* ---- W4A8 (reference a8_quant + w4a8_gemm, w4a8.metal:24-98; host w4a8, qwen35.h:1323-1366) ------------------ */
+
+/* Activation quantizer: U int8 [M][K], XS float [M][K/64][2] = (sx, sx * sum xq) per row and group.
+ * per_token = 0: one scale per row and 64-group (the reference's a8_quant); 1: one scale per row (amax over K),
+ * repeated in every group's XS entry. sx = amax / 127 (1 if amax == 0), xq = rint(x / sx). */
+int ifd_a8_quant(const void* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, void* stream);
+
+/* C (mode) = sum_g [ s sx P + b (sx sum xq) ], P = sum q xq over the group (exact int32); U, XS from
+ * ifd_a8_quant with the same per_token. */
+int ifd_qmm_w4a8(const int8_t* U, const float* XS, int per_token, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N,
+                 int K, int ldk, uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes,
+                 void* stream);
+size_t ifd_qmm_w4a8_workspace(int M, int N, int K);
+
+/* ---- MoE (reference encode_moe sorted path, qwen35.h:1869-1980; kernels moe.metal:60-187) -------------------- */
+
+/* Router logits [T][E1] = x [T][H] . W [E1][H]^T, bf16 operands, fp32 accumulation; out_bf16 = 1 rounds to bf16
+ * (reference: bf16 GEMM logits for >= 64 rows, qwen35.h:1919-1929), 0 writes fp32 (moe_qmv16f, moe.metal:198-213). */
+int ifd_moe_router_logits(const void* x, const void* w, int T, int H, int E1, int out_bf16, void* logits,
+                          void* stream);
+
+/* Softmax top-k (reference moe_route / moe_route_bf, moe.metal:60-101, qwen4.metal:1462-1503): idx int [T][k],
+ * wt float [T][k] (renormalised over the picks when norm != 0), sg float [T] = sigmoid(logit[E]) when
+ * shared_gate == 1, 1.0 when 0 (always-on shared expert). Ties go to the lowest expert index. E <= 512, k <= 16. */
+int ifd_moe_route(const void* logits, int logits_bf16, int T, int E, int k, int stride, int norm, int shared_gate,
+                  int* idx, float* wt, float* sg, void* stream);
+
+/* Stable counting sort of routed rows r = t*k + j by expert (reference moe_sort, moe.metal:130-161, whose order
+ * inside a segment is atomic-order; this one keeps row order): offsets int [E+1], perm int [R] (sorted position ->
+ * r), inv int [R] (r -> sorted position). tiles int [ifd_moe_tiles_max(R, E)][2] = (expert, first sorted row) of
+ * every 32-row tile of every expert segment and ntiles int [1]: the schedule of ifd_moe_gather_qmm
+ * (reference schedule_row_tile, third_party/mlx/.../steel/utils.h:502-542). Workspace: ifd_moe_dispatch_workspace. */
+int ifd_moe_tiles_max(int R, int E);
+size_t ifd_moe_dispatch_workspace(int R, int E);
+int ifd_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
+                     void* workspace, size_t ws_bytes, void* stream);
+
+/* xs[q][:] = x[perm[q] / div][:] (reference moe_gather, moe.metal:163-170). */
+int ifd_moe_gather(const void* x, const int* perm, int div, int R, int H, void* xs, void* stream);
+
+/* Gathered expert GEMM over expert-sorted rows (reference affine_gather_qmm_rhs, quantized_nax.h:1467-1681):
+ * C[q][n] = bf16( sum_k A_row(q)[k] * w_e[n][k] ), e = expert of sorted row q, A_row(q) = A[perm[q] / div] when
+ * perm != NULL else A[q]; offsets/tiles/ntiles from ifd_moe_dispatch, max_tiles = ifd_moe_tiles_max(R, E).
+ * Stacks wq [E][N][K/8], s/b [E][N][K/64] (reference MoeW, moe.h:8-11). silu != 0 (N even): the stack holds [gate (N/2) | up (N/2)] rows per expert and C receives
+ * SwiGLU(gate, up) [R][N/2] directly. */
+int ifd_moe_gather_qmm(const void* A, const int* perm, int div, const int* offsets, const int* tiles,
+                       const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int E,
+                       int N, int K, int silu, void* C, int R, void* stream);
+
+/* out[t][h] = bf16(acc) (assign) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] yd[inv[t*k+j]][h] + sg[t] ys[t][h]
+ * (ys may be NULL) (reference moe_combine_sorted, moe.metal:172-187). */
+int ifd_moe_combine(void* out, const void* yd, const float* wt, const void* ys, const float* sg, const int* inv,
+                    int T, int H, int k, int assign, void* stream);
+
+/* One-shot MoE FFN on normalised tokens xn [T][H] (reference encode_moe after rmsnorm_for, qwen35.h:1909-1980):
+ * router (bf16 [E + (shared_gate ? 1 : 0)][H]) -> route -> dispatch -> gathered gate/up + SwiGLU -> gathered down
+ * -> combine with the shared expert (dense 4-bit gate_up [2 Is][H], down [H][Is]; sh_* may be NULL for none).
+ * logits_bf16 selects the router's output rounding. Routing outputs are written to the caller's idx/wt/sg if
+ * non-NULL. Workspace: ifd_moe_ffn_workspace. */
+size_t ifd_moe_ffn_workspace(int T, int H, int I, int E, int k, int Is);
+int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
+                int logits_bf16, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
+                const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I,
+                const uint32_t* sgu_wq, const uint16_t* sgu_s, const uint16_t* sgu_b, const uint32_t* sdn_wq,
+                const uint16_t* sdn_s, const uint16_t* sdn_b, int Is, void* out, int assign, int* idx, float* wt,
+                float* sg, void* workspace, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INFERD_QMM_H */

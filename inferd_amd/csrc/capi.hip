@@ -1,0 +1,254 @@
+// The C ABI (include/inferd_qmm.h): argument checks, routing, workspace layout, and the one-shot MoE FFN.
+#include <algorithm>
+
+#include "host.h"
+#include "kernels.h"
+
+using namespace ifd;
+
+namespace {
+
+inline hipStream_t S(void* st) { return (hipStream_t)st; }
+
+int fill_gemm(W4Gemm& g, const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N,
+              int K, int ldk, uint32_t xr, void* C, int ldc, int M, int mode) {
+  IFD_TRY(check_w4_args(A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode, 2));
+  g.A = A;
+  g.lda = lda;
+  g.wq = wq;
+  g.s = s;
+  g.b = b;
+  g.N = N;
+  g.K = K;
+  g.ldk = ldk ? ldk : K;
+  g.xr = xr;
+  g.C = C;
+  g.ldc = ldc;
+  g.M = M;
+  g.mode = mode;
+  return IFD_OK;
+}
+
+// The decode path serves up to this many rows (one to four 32-row MFMA tiles); above it the prefill GEMM.
+constexpr int kQmvMaxRows = 128;
+
+}  // namespace
+
+extern "C" {
+
+int ifd_version(void) { return 1; }
+
+const char* ifd_status_str(int status) {
+  switch (status) {
+    case IFD_OK: return "ok";
+    case IFD_ERR_ARG: return "invalid argument";
+    case IFD_ERR_WORKSPACE: return "workspace too small";
+    case IFD_ERR_LAUNCH: return "kernel launch failed";
+    case IFD_ERR_UNSUPPORTED: return "unsupported";
+    default: return "unknown status";
+  }
+}
+
+const char* ifd_last_error(void) { return last_error_buf(); }
+
+size_t ifd_gemm_w4_workspace(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  return M <= kQmvMaxRows ? qmv_workspace(M, N, K) : qmm_workspace(M, N, K);
+}
+
+int ifd_qmv_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk,
+               uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes, void* stream) {
+  W4Gemm g;
+  IFD_TRY(fill_gemm(g, A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
+  IFD_CHECK(M <= kQmvMaxRows, "ifd_qmv_w4 takes M <= %d (M=%d)", kQmvMaxRows, M);
+  return launch_qmv(g, workspace, ws_bytes, S(stream));
+}
+
+int ifd_qmm_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk,
+               uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes, void* stream) {
+  W4Gemm g;
+  IFD_TRY(fill_gemm(g, A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
+  return launch_qmm(g, workspace, ws_bytes, S(stream));
+}
+
+int ifd_gemm_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk,
+                uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes, void* stream) {
+  W4Gemm g;
+  IFD_TRY(fill_gemm(g, A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
+  if (M <= kQmvMaxRows) return launch_qmv(g, workspace, ws_bytes, S(stream));
+  return launch_qmm(g, workspace, ws_bytes, S(stream));
+}
+
+int ifd_flip_w4(uint32_t* wq, size_t n32, uint32_t mask, void* stream) {
+  IFD_CHECK(n32 == 0 || wq, "null pointer");
+  return launch_flip(wq, n32, mask, S(stream));
+}
+
+int ifd_silu_mul(const void* gu, void* h, int I, int rows, void* stream) {
+  IFD_CHECK(I > 0 && I % 8 == 0 && rows >= 0, "bad shape I=%d rows=%d (I must be a multiple of 8)", I, rows);
+  IFD_CHECK(rows == 0 || (gu && h && aligned(gu, 16) && aligned(h, 16)), "gu and h must be 16-byte aligned");
+  return launch_silu_mul((const uint16_t*)gu, (uint16_t*)h, I, rows, S(stream));
+}
+
+int ifd_a8_quant(const void* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, void* stream) {
+  IFD_CHECK(M >= 0 && K > 0 && K % 64 == 0 && lda >= K, "bad shape M=%d K=%d lda=%d", M, K, lda);
+  IFD_CHECK(M == 0 || (A && U && XS), "null pointer");
+  return launch_a8_quant((const uint16_t*)A, lda, M, K, per_token ? 1 : 0, U, XS, S(stream));
+}
+
+size_t ifd_qmm_w4a8_workspace(int M, int N, int K) { return w4a8_workspace(M, N, K); }
+
+int ifd_qmm_w4a8(const int8_t* U, const float* XS, int per_token, const uint32_t* wq, const uint16_t* s,
+                 const uint16_t* b, int N, int K, int ldk, uint32_t xr, void* C, int ldc, int M, int mode,
+                 void* workspace, size_t ws_bytes, void* stream) {
+  W4Gemm g;
+  IFD_TRY(fill_gemm(g, U, K, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
+  IFD_CHECK(M == 0 || XS, "null XS");
+  g.XS = XS;
+  return launch_w4a8(g, per_token ? 1 : 0, workspace, ws_bytes, S(stream));
+}
+
+int ifd_moe_router_logits(const void* x, const void* w, int T, int H, int E1, int out_bf16, void* logits,
+                          void* stream) {
+  IFD_CHECK(T >= 0 && H > 0 && H % 64 == 0 && E1 > 0, "bad shape T=%d H=%d E1=%d (H multiple of 64)", T, H, E1);
+  IFD_CHECK(T == 0 || (x && w && logits && aligned(x, 16) && aligned(w, 16)), "x and w must be 16-byte aligned");
+  return launch_router_logits((const uint16_t*)x, (const uint16_t*)w, T, H, E1, out_bf16, logits, S(stream));
+}
+
+int ifd_moe_route(const void* logits, int logits_bf16, int T, int E, int k, int stride, int norm, int shared_gate,
+                  int* idx, float* wt, float* sg, void* stream) {
+  IFD_CHECK(E > 0 && E <= 512 && k > 0 && k <= 16 && k <= E && T >= 0, "bad routing shape E=%d k=%d", E, k);
+  IFD_CHECK(stride >= E + (shared_gate ? 1 : 0), "stride=%d too small for E=%d (+ shared gate)", stride, E);
+  IFD_CHECK(T == 0 || (logits && idx && wt && sg), "null pointer");
+  return launch_moe_route(logits, logits_bf16, T, E, k, stride, norm, shared_gate, idx, wt, sg, S(stream));
+}
+
+int ifd_moe_tiles_max(int R, int E) { return moe_tiles_max(R, E); }
+size_t ifd_moe_dispatch_workspace(int R, int E) { return moe_dispatch_workspace(R, E); }
+
+int ifd_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
+                     void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(R >= 0 && E > 0 && E <= 1024, "bad dispatch shape R=%d E=%d (E <= 1024)", R, E);
+  IFD_CHECK(offsets && tiles && ntiles && (R == 0 || (idx && perm && inv)), "null pointer");
+  return launch_moe_dispatch(idx, R, E, offsets, perm, inv, tiles, ntiles, workspace, ws_bytes, S(stream));
+}
+
+int ifd_moe_gather(const void* x, const int* perm, int div, int R, int H, void* xs, void* stream) {
+  IFD_CHECK(R >= 0 && H > 0 && H % 8 == 0 && div > 0, "bad shape R=%d H=%d div=%d", R, H, div);
+  IFD_CHECK(R == 0 || (x && perm && xs && aligned(x, 16) && aligned(xs, 16)), "x, xs must be 16-byte aligned");
+  return launch_moe_gather((const uint16_t*)x, perm, div, R, H, (uint16_t*)xs, S(stream));
+}
+
+int ifd_moe_gather_qmm(const void* A, const int* perm, int div, const int* offsets, const int* tiles,
+                       const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int E,
+                       int N, int K, int silu, void* C, int R, void* stream) {
+  IFD_CHECK(R >= 0 && E > 0 && N > 0 && K > 0 && K % 64 == 0 && div > 0, "bad shape E=%d N=%d K=%d", E, N, K);
+  IFD_CHECK(!silu || N % 2 == 0, "silu needs an even N (gate | up)");
+  IFD_CHECK(max_tiles >= 0, "bad max_tiles");
+  IFD_CHECK(R == 0 || (A && offsets && tiles && ntiles && wq && s && b && C), "null pointer");
+  IFD_CHECK(R == 0 || (aligned(A, 16) && aligned(wq, 16)), "A and wq must be 16-byte aligned");
+  return launch_moe_gather_qmm((const uint16_t*)A, perm, div, tiles, ntiles, offsets, max_tiles, wq, s, b, N, K,
+                               silu ? 1 : 0, (uint16_t*)C, R, S(stream));
+}
+
+int ifd_moe_combine(void* out, const void* yd, const float* wt, const void* ys, const float* sg, const int* inv, int T,
+                    int H, int k, int assign, void* stream) {
+  IFD_CHECK(T >= 0 && H > 0 && H % 8 == 0 && k > 0, "bad shape T=%d H=%d k=%d", T, H, k);
+  IFD_CHECK(T == 0 || (out && yd && wt && inv && (!ys || sg)), "null pointer");
+  IFD_CHECK(T == 0 || (aligned(out, 16) && aligned(yd, 16) && (!ys || aligned(ys, 16))), "bf16 rows must be aligned");
+  return launch_moe_combine((uint16_t*)out, (const uint16_t*)yd, wt, (const uint16_t*)ys, sg, inv, T, H, k, assign,
+                            S(stream));
+}
+
+// ---- one-shot MoE FFN ------------------------------------------------------------------------------------------
+namespace {
+struct MoeLayout {
+  size_t logits, idx, wt, sg, offsets, perm, inv, tiles, ntiles, disp, sh_gu, sh_act, sh_ws, ys, eact, edn, total;
+};
+MoeLayout moe_layout(int T, int H, int I, int E, int k, int Is) {
+  MoeLayout L{};
+  const int R = T * k, E1 = E + 1;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align_up(std::max<size_t>(bytes, 1), 256);
+    return at;
+  };
+  L.logits = take((size_t)T * E1 * 4);
+  L.idx = take((size_t)R * 4);
+  L.wt = take((size_t)R * 4);
+  L.sg = take((size_t)T * 4);
+  L.offsets = take((size_t)(E + 1) * 4);
+  L.perm = take((size_t)R * 4);
+  L.inv = take((size_t)R * 4);
+  L.tiles = take((size_t)moe_tiles_max(R, E) * 2 * 4);
+  L.ntiles = take(4);
+  L.disp = take(moe_dispatch_workspace(R, E));
+  L.sh_gu = take(Is ? (size_t)T * 2 * Is * 2 : 0);
+  L.sh_act = take(Is ? (size_t)T * Is * 2 : 0);
+  L.sh_ws = take(Is ? std::max(ifd_gemm_w4_workspace(T, 2 * Is, H), ifd_gemm_w4_workspace(T, H, Is)) : 0);
+  L.ys = take(Is ? (size_t)T * H * 2 : 0);
+  L.eact = take((size_t)R * I * 2);
+  L.edn = take((size_t)R * H * 2);
+  L.total = o;
+  return L;
+}
+}  // namespace
+
+size_t ifd_moe_ffn_workspace(int T, int H, int I, int E, int k, int Is) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  return moe_layout(T, H, I, E, k, Is).total;
+}
+
+int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
+                int logits_bf16, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
+                const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I, const uint32_t* sgu_wq,
+                const uint16_t* sgu_s, const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s,
+                const uint16_t* sdn_b, int Is, void* out, int assign, int* idx, float* wt, float* sg,
+                void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(T >= 0 && H > 0 && H % 64 == 0 && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 && k <= 16,
+            "bad MoE shape T=%d H=%d I=%d E=%d k=%d", T, H, I, E, k);
+  const bool shared = sgu_wq != nullptr;
+  IFD_CHECK(!shared || (Is > 0 && Is % 64 == 0 && sgu_s && sgu_b && sdn_wq && sdn_s && sdn_b), "bad shared expert");
+  IFD_CHECK(!shared_gate || shared, "a shared gate needs a shared expert");
+  if (T == 0) return IFD_OK;
+  IFD_CHECK(xn && router && egu_wq && egu_s && egu_b && edn_wq && edn_s && edn_b && out, "null pointer");
+  const MoeLayout L = moe_layout(T, H, I, E, k, shared ? Is : 0);
+  if (!workspace || ws_bytes < L.total)
+    return fail(IFD_ERR_WORKSPACE, "moe_ffn needs %zu bytes of workspace, got %zu", L.total, ws_bytes);
+  char* w = (char*)workspace;
+  hipStream_t st = S(stream);
+  const int R = T * k, E1 = E + (shared_gate ? 1 : 0);
+  int* ridx = idx ? idx : (int*)(w + L.idx);
+  float* rwt = wt ? wt : (float*)(w + L.wt);
+  float* rsg = sg ? sg : (float*)(w + L.sg);
+  // router -> routing (row E of the router, when present, is the shared expert's gate)
+  IFD_TRY(launch_router_logits((const uint16_t*)xn, (const uint16_t*)router, T, H, E1, logits_bf16, w + L.logits, st));
+  IFD_TRY(launch_moe_route(w + L.logits, logits_bf16, T, E, k, E1, norm, shared_gate, ridx, rwt, rsg, st));
+  // shared expert: gate_up -> SwiGLU -> down into ys
+  const uint16_t* ys = nullptr;
+  if (shared) {
+    IFD_TRY(ifd_gemm_w4(xn, H, sgu_wq, sgu_s, sgu_b, 2 * Is, H, 0, 0, w + L.sh_gu, 2 * Is, T, 0, w + L.sh_ws,
+                        ifd_gemm_w4_workspace(T, 2 * Is, H), stream));
+    IFD_TRY(launch_silu_mul((const uint16_t*)(w + L.sh_gu), (uint16_t*)(w + L.sh_act), Is, T, st));
+    IFD_TRY(ifd_gemm_w4(w + L.sh_act, Is, sdn_wq, sdn_s, sdn_b, H, Is, 0, 0, w + L.ys, H, T, 0, w + L.sh_ws,
+                        ifd_gemm_w4_workspace(T, H, Is), stream));
+    ys = (const uint16_t*)(w + L.ys);
+  }
+  // dispatch -> gathered gate/up with fused SwiGLU -> gathered down -> combine
+  int* offsets = (int*)(w + L.offsets);
+  int* perm = (int*)(w + L.perm);
+  int* inv = (int*)(w + L.inv);
+  int* tiles = (int*)(w + L.tiles);
+  int* ntiles = (int*)(w + L.ntiles);
+  IFD_TRY(launch_moe_dispatch(ridx, R, E, offsets, perm, inv, tiles, ntiles, w + L.disp, moe_dispatch_workspace(R, E),
+                              st));
+  const int mt = moe_tiles_max(R, E);
+  IFD_TRY(launch_moe_gather_qmm((const uint16_t*)xn, perm, k, tiles, ntiles, offsets, mt, egu_wq, egu_s, egu_b, 2 * I,
+                                H, 1, (uint16_t*)(w + L.eact), R, st));
+  IFD_TRY(launch_moe_gather_qmm((const uint16_t*)(w + L.eact), nullptr, 1, tiles, ntiles, offsets, mt, edn_wq, edn_s,
+                                edn_b, H, I, 0, (uint16_t*)(w + L.edn), R, st));
+  return launch_moe_combine((uint16_t*)out, (const uint16_t*)(w + L.edn), rwt, ys, rsg, inv, T, H, k, assign, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,121 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of the W4 quantized-matmul path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ifd {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(4))) int32_t i32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(16))) int32_t i32x16;
+
+constexpr int kGroup = 64;  // MLX affine group size along K
+
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// D(32x32 fp32) += A(32x16 bf16) * B(16x32 bf16). Lane l holds A row (l % 32), B column (l % 32), eight consecutive
+// k values 8 * (l / 32) .. +7 of the 16; D row 8 * (r / 4) + 4 * (l / 32) + (r % 4), column l % 32, for r = 0..15.
+__device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+// D(32x32 int32) += A(32x32 int8) * B(32x32 int8); lane l: sixteen consecutive k values 16 * (l / 32) .. +15.
+__device__ __forceinline__ i32x16 mfma_i8(u32x4 a, u32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
+                                               0);
+}
+
+// Eight 4-bit codes of one word (k order 0..7, low nibble first) as eight bf16 values (off + q) in natural k order:
+// bf16 0x4300 | q == 128 + q exactly. The caller corrects with bias' = bias - 128 * scale.
+__device__ __forceinline__ u32x4 codes_bf16_off128(uint32_t w) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;  // bytes: q0 q2 q4 q6 / q1 q3 q5 q7
+  u32x4 r;
+  // v_perm_b32(S0 = hi, S1 = lo): selector bytes 0-3 pick lo, 4-7 pick hi, 0x0c gives 0
+  r[0] = __builtin_amdgcn_perm(hi, lo, 0x0c040c00u) | 0x43004300u;  // (q0, q1)
+  r[1] = __builtin_amdgcn_perm(hi, lo, 0x0c050c01u) | 0x43004300u;  // (q2, q3)
+  r[2] = __builtin_amdgcn_perm(hi, lo, 0x0c060c02u) | 0x43004300u;  // (q4, q5)
+  r[3] = __builtin_amdgcn_perm(hi, lo, 0x0c070c03u) | 0x43004300u;  // (q6, q7)
+  return r;
+}
+
+// Eight 4-bit codes of one word as eight int8 values 0..15 in natural k order (two dwords).
+__device__ __forceinline__ u32x2 codes_i8(uint32_t w) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  u32x2 r;
+  r[0] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // q0 q1 q2 q3
+  r[1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // q4 q5 q6 q7
+  return r;
+}
+
+// Dequantize eight codes to bf16(s * q + b) in natural k order (MLX's qmm loader rounding, quantized.h:528-535).
+__device__ __forceinline__ u32x4 dequant8_bf16(uint32_t w, float s, float b) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float q0 = (float)((lo >> (8 * i)) & 0xFFu), q1 = (float)((hi >> (8 * i)) & 0xFFu);
+    r[i] = pack_bf2(__builtin_fmaf(s, q0, b), __builtin_fmaf(s, q1, b));
+  }
+  return r;
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; i++) z[i] = 0.f;
+  return z;
+}
+__device__ __forceinline__ i32x16 izero16() {
+  i32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; i++) z[i] = 0;
+  return z;
+}
+
+// Store one fp32 result with the GEMM store mode (0 bf16, 1 bf16 residual add, 2 fp32).
+__device__ __forceinline__ void store_mode(void* C, size_t o, float v, int mode) {
+  if (mode == 2) {
+    ((float*)C)[o] = v;
+  } else if (mode == 1) {
+    uint16_t* c = (uint16_t*)C + o;
+    *c = f2bf(v + bf2f(*c));
+  } else {
+    ((uint16_t*)C)[o] = f2bf(v);
+  }
+}
+
+// Wave64 reductions.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Bijective remap of a 1-D block id so that each XCD (blocks are dealt round-robin over 8 XCDs) runs a contiguous
+// range of logical tiles: neighbouring tiles then share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  constexpr int X = 8;
+  const int per = nblocks / X, rem = nblocks % X, x = bid % X, i = bid / X;
+  return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
+}  // namespace ifd

@@ -1,0 +1,54 @@
+// Internal launcher interface between the C ABI (capi.hip) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ifd {
+
+// One dense 4-bit GEMM request: C (mode) = A . W^T. A is bf16 [M][lda] (or int8 [M][K] + XS for W4A8).
+struct W4Gemm {
+  const void* A = nullptr;
+  int lda = 0;
+  const float* XS = nullptr;  // W4A8 only: (sx, sx * sum xq) per row and group
+  const uint32_t* wq = nullptr;
+  const uint16_t* s = nullptr;
+  const uint16_t* b = nullptr;
+  int N = 0, K = 0, ldk = 0;  // ldk: weight row length in values (K-slice views), never 0 here
+  uint32_t xr = 0;
+  void* C = nullptr;
+  int ldc = 0, M = 0, mode = 0;
+};
+
+// Decode GEMV path (M <= 128).
+size_t qmv_workspace(int M, int N, int K);
+int launch_qmv(const W4Gemm& g, void* ws, size_t ws_bytes, hipStream_t st);
+// Prefill GEMM path (any M).
+size_t qmm_workspace(int M, int N, int K);
+int launch_qmm(const W4Gemm& g, void* ws, size_t ws_bytes, hipStream_t st);
+// W4A8.
+int launch_a8_quant(const uint16_t* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, hipStream_t st);
+size_t w4a8_workspace(int M, int N, int K);
+int launch_w4a8(const W4Gemm& g, int per_token, void* ws, size_t ws_bytes, hipStream_t st);
+int launch_flip(uint32_t* wq, size_t n32, uint32_t mask, hipStream_t st);
+int launch_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows, hipStream_t st);
+// Split-K reduction: C (mode) = sum over S partials [S][M][N] fp32.
+int launch_splitk_reduce(const float* part, int S, int M, int N, void* C, int ldc, int mode, hipStream_t st);
+
+// MoE.
+int launch_router_logits(const uint16_t* x, const uint16_t* w, int T, int H, int E1, int out_bf16, void* logits,
+                         hipStream_t st);
+int launch_moe_route(const void* logits, int logits_bf16, int T, int E, int k, int stride, int norm, int shared_gate,
+                     int* idx, float* wt, float* sg, hipStream_t st);
+int moe_tiles_max(int R, int E);
+size_t moe_dispatch_workspace(int R, int E);
+int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
+                        void* ws, size_t ws_bytes, hipStream_t st);
+int launch_moe_gather(const uint16_t* x, const int* perm, int div, int R, int H, uint16_t* xs, hipStream_t st);
+int launch_moe_gather_qmm(const uint16_t* A, const int* perm, int div, const int* tiles, const int* ntiles,
+                          const int* offsets, int max_tiles, const uint32_t* wq, const uint16_t* s,
+                          const uint16_t* b, int N, int K, int silu, uint16_t* C, int R, hipStream_t st);
+int launch_moe_combine(uint16_t* out, const uint16_t* yd, const float* wt, const uint16_t* ys, const float* sg,
+                       const int* inv, int T, int H, int k, int assign, hipStream_t st);
+
+}  // namespace ifd

@@ -1,0 +1,384 @@
+// MoE FFN kernels: router logits, softmax top-k routing, stable counting-sort dispatch, the gathered expert GEMM
+// over expert-sorted rows (with SwiGLU fused into the gate/up product), gather and weighted combine.
+//
+// Replaces the reference's sorted MoE path (engine/src/qwen35.h:1909-1980): moe_qmv16f / bf16 router GEMM
+// (moe.metal:198-213, qwen35.h:1919-1929), moe_route / moe_route_bf (moe.metal:60-101, qwen4.metal:1462-1503),
+// moe_sort (moe.metal:130-161), moe_gather (:163-170), MLX affine_gather_qmm_rhs (quantized_nax.h:1467-1681) driven by
+// schedule_row_tile (steel/utils.h:502-542), moe_silu_mul (:103-111) and moe_combine_sorted (:172-187).
+#include "common.h"
+#include "host.h"
+#include "kernels.h"
+
+namespace ifd {
+
+// ---- router logits: [T][E1] = x [T][H] . W [E1][H]^T ------------------------------------------------------------
+// One wave per 32 x 32 output tile; operands straight from global memory (x and W are small and L2-resident).
+// Lane (j, h) supplies k = 32 h + 8 t .. +7 of every 64-wide K block in step t (same k assignment for both
+// operands), so each lane reads 64 contiguous bytes of its row per block.
+__global__ __launch_bounds__(256) void k_router_logits(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                       int T, int H, int E1, int out_bf16, void* out, int tiles_e) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int tile = blockIdx.x * 4 + wave;
+  const int tt = tile / tiles_e, te = tile % tiles_e;
+  const int t0 = tt * 32, e0 = te * 32;
+  if (t0 >= T) return;
+  const bool tok = t0 + j < T, eok = e0 + j < E1;
+  const uint16_t* xa = x + (size_t)(tok ? t0 + j : 0) * H + 32 * h;
+  const uint16_t* wb = w + (size_t)(eok ? e0 + j : 0) * H + 32 * h;
+  f32x16 acc = zero16();
+  for (int k = 0; k < H; k += 64) {
+    u32x4 a[4], b[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      a[t] = tok ? *(const u32x4*)(xa + k + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+      b[t] = eok ? *(const u32x4*)(wb + k + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) acc = mfma_bf16(a[t], b[t], acc);
+  }
+  const int e = e0 + j;
+  if (e >= E1) return;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int t = t0 + 8 * (r / 4) + 4 * h + (r % 4);
+    if (t >= T) continue;
+    if (out_bf16) ((uint16_t*)out)[(size_t)t * E1 + e] = f2bf(acc[r]);
+    else ((float*)out)[(size_t)t * E1 + e] = acc[r];
+  }
+}
+
+int launch_router_logits(const uint16_t* x, const uint16_t* w, int T, int H, int E1, int out_bf16, void* logits,
+                         hipStream_t st) {
+  if (T == 0) return IFD_OK;
+  const int tiles_e = (E1 + 31) / 32, tiles = (T + 31) / 32 * tiles_e;
+  hipLaunchKernelGGL(k_router_logits, dim3((tiles + 3) / 4), dim3(256), 0, st, x, w, T, H, E1, out_bf16, logits,
+                     tiles_e);
+  return check_launch("router_logits");
+}
+
+// ---- routing: one wave per token, E <= 512 (8 logits per lane) -------------------------------------------------
+template <bool BF>
+__global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ logits, int T, int E, int k, int stride,
+                                                   int norm, int shared_gate, int* __restrict__ idx,
+                                                   float* __restrict__ wt, float* __restrict__ sg) {
+  const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  auto L = [&](int c) -> float {
+    return BF ? bf2f(((const uint16_t*)logits)[(size_t)t * stride + c]) : ((const float*)logits)[(size_t)t * stride + c];
+  };
+  float v[8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int c = i * 64 + lane;
+    v[i] = c < E ? L(c) : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const bool ok = i * 64 + lane < E;
+    const float ex = ok ? expf(v[i] - mx) : 0.f;
+    sum += ex;
+    v[i] = ok ? ex : -2.f;  // padding never wins a pick (picks need v > -1)
+  }
+  sum = wave_sum(sum);
+  float tot = 0.f, picked[16];
+  int who_j[16];
+  for (int jj = 0; jj < k; jj++) {
+    float best = -1.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (v[i] > best) best = v[i], bi = i * 64 + lane;  // strict >: lowest index of this lane wins a tie
+    const float m = wave_max(best);
+    const int who = wave_min_i(best == m ? bi : 0x7fffffff);
+    if ((who & 63) == lane) {
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (i == who / 64) v[i] = -1.f;
+    }
+    picked[jj] = m / sum;
+    who_j[jj] = who;
+    tot += m / sum;
+  }
+  if (lane == 0) {
+    for (int jj = 0; jj < k; jj++) {
+      idx[(size_t)t * k + jj] = who_j[jj];
+      wt[(size_t)t * k + jj] = norm ? picked[jj] / tot : picked[jj];
+    }
+    sg[t] = shared_gate ? 1.f / (1.f + expf(-L(E))) : 1.f;
+  }
+}
+
+int launch_moe_route(const void* logits, int logits_bf16, int T, int E, int k, int stride, int norm, int shared_gate,
+                     int* idx, float* wt, float* sg, hipStream_t st) {
+  if (T == 0) return IFD_OK;
+  dim3 grid((T + 3) / 4), block(256);
+  if (logits_bf16)
+    hipLaunchKernelGGL(k_moe_route<true>, grid, block, 0, st, logits, T, E, k, stride, norm, shared_gate, idx, wt, sg);
+  else
+    hipLaunchKernelGGL(k_moe_route<false>, grid, block, 0, st, logits, T, E, k, stride, norm, shared_gate, idx, wt,
+                       sg);
+  return check_launch("moe_route");
+}
+
+// ---- dispatch: stable counting sort by expert ------------------------------------------------------------------
+// Pass 1 (one block per chunk of 256 rows): rank of each row among the earlier rows of its chunk with the same
+// expert, and the chunk's histogram. Pass 2 (one block): per expert, exclusive prefix of the chunk counts; expert
+// offsets; the tile schedule. Pass 3 (one block per chunk): perm / inv. Every step is order-independent or ordered
+// by row index, so the result is deterministic and stable.
+constexpr int kDispChunk = 256;
+
+__global__ __launch_bounds__(256) void k_disp_count(const int* __restrict__ idx, int R, int E, int* __restrict__ bcnt,
+                                                    int* __restrict__ rank) {
+  __shared__ int ex[kDispChunk];
+  extern __shared__ int cnt[];  // [E]
+  const int tid = threadIdx.x, r = blockIdx.x * kDispChunk + tid;
+  for (int e = tid; e < E; e += 256) cnt[e] = 0;
+  // expert ids must lie in [0, E); out-of-range ids are clamped so that bad input cannot index out of bounds
+  const int e = r < R ? min(max(idx[r], 0), E - 1) : -1;
+  ex[tid] = e;
+  __syncthreads();
+  if (e >= 0) {
+    int rk = 0;
+    for (int i = 0; i < tid; i++) rk += ex[i] == e;
+    rank[r] = rk;
+    atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  for (int c = tid; c < E; c += 256) bcnt[(size_t)blockIdx.x * E + c] = cnt[c];
+}
+
+__global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int nchunks, int E, int R, int tile_rows,
+                                                    int* __restrict__ offsets, int* __restrict__ tiles,
+                                                    int* __restrict__ ntiles) {
+  __shared__ int part[1024], tpart[1024];
+  const int e = threadIdx.x;
+  int total = 0;
+  if (e < E)
+    for (int c = 0; c < nchunks; c++) {
+      const int v = bcnt[(size_t)c * E + e];
+      bcnt[(size_t)c * E + e] = total;  // exclusive prefix within the expert
+      total += v;
+    }
+  const int nt = (total + tile_rows - 1) / tile_rows;
+  part[e] = e < E ? total : 0;
+  tpart[e] = e < E ? nt : 0;
+  __syncthreads();
+  // inclusive Hillis-Steele scans over 1024 entries
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int a = e >= o ? part[e - o] : 0, b = e >= o ? tpart[e - o] : 0;
+    __syncthreads();
+    part[e] += a;
+    tpart[e] += b;
+    __syncthreads();
+  }
+  const int off = part[e] - (e < E ? total : 0), toff = tpart[e] - (e < E ? nt : 0);
+  if (e < E) {
+    offsets[e] = off;
+    for (int c = 0; c < nchunks; c++) bcnt[(size_t)c * E + e] += off;
+    for (int i = 0; i < nt; i++) {
+      tiles[2 * (toff + i)] = e;
+      tiles[2 * (toff + i) + 1] = off + i * tile_rows;
+    }
+  }
+  if (e == 0) {
+    offsets[E] = R;
+    ntiles[0] = tpart[1023];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_disp_scatter(const int* __restrict__ idx, int R, int E,
+                                                      const int* __restrict__ bbase, const int* __restrict__ rank,
+                                                      int* __restrict__ perm, int* __restrict__ inv) {
+  const int r = blockIdx.x * kDispChunk + threadIdx.x;
+  if (r >= R) return;
+  const int q = bbase[(size_t)blockIdx.x * E + min(max(idx[r], 0), E - 1)] + rank[r];
+  perm[q] = r;
+  inv[r] = q;
+}
+
+int moe_tiles_max(int R, int E) { return (R + 31) / 32 + std::min(E, R); }
+
+size_t moe_dispatch_workspace(int R, int E) {
+  const size_t nchunks = (R + kDispChunk - 1) / kDispChunk;
+  return align_up(nchunks * E * sizeof(int), 256) + align_up((size_t)R * sizeof(int), 256);
+}
+
+int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
+                        void* ws, size_t ws_bytes, hipStream_t st, int tile_rows) {
+  const int nchunks = (R + kDispChunk - 1) / kDispChunk;
+  if (moe_dispatch_workspace(R, E) > ws_bytes || !ws)
+    return fail(IFD_ERR_WORKSPACE, "moe_dispatch needs %zu bytes of workspace", moe_dispatch_workspace(R, E));
+  int* bcnt = (int*)ws;
+  int* rank = (int*)((char*)ws + align_up((size_t)nchunks * E * sizeof(int), 256));
+  if (R > 0) {
+    hipLaunchKernelGGL(k_disp_count, dim3(nchunks), dim3(256), E * sizeof(int), st, idx, R, E, bcnt, rank);
+    IFD_TRY(check_launch("moe_dispatch count"));
+  }
+  hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, st, bcnt, nchunks, E, R, tile_rows, offsets, tiles, ntiles);
+  IFD_TRY(check_launch("moe_dispatch scan"));
+  if (R > 0) {
+    hipLaunchKernelGGL(k_disp_scatter, dim3(nchunks), dim3(256), 0, st, idx, R, E, bcnt, rank, perm, inv);
+    IFD_TRY(check_launch("moe_dispatch scatter"));
+  }
+  return IFD_OK;
+}
+
+int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
+                        void* ws, size_t ws_bytes, hipStream_t st) {
+  return launch_moe_dispatch(idx, R, E, offsets, perm, inv, tiles, ntiles, ws, ws_bytes, st, 32);
+}
+
+// ---- gather ----------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_moe_gather(const uint16_t* __restrict__ x, const int* __restrict__ perm,
+                                                    int div, int R, int H, uint16_t* __restrict__ xs) {
+  const int per_row = H / 8;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)R * per_row) return;
+  const int q = (int)(i / per_row), c = (int)(i % per_row) * 8;
+  *(u32x4*)(xs + (size_t)q * H + c) = *(const u32x4*)(x + (size_t)(perm[q] / div) * H + c);
+}
+int launch_moe_gather(const uint16_t* x, const int* perm, int div, int R, int H, uint16_t* xs, hipStream_t st) {
+  if (R == 0) return IFD_OK;
+  const size_t n = (size_t)R * (H / 8);
+  hipLaunchKernelGGL(k_moe_gather, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, perm, div, R, H, xs);
+  return check_launch("moe_gather");
+}
+
+// ---- gathered expert GEMM ----------------------------------------------------------------------------------------
+// Block = one (expert, 32-row tile) of the dispatch schedule x 128 output columns (4 waves x 32). The wave layout is
+// the decode kernel's dequant variant: per 64-group each lane loads 16 bytes of codes of its column, dequantizes
+// them to bf16(s q + b) (MLX's gather_qmm rounding) and runs four 32x32x16 MFMA steps against the tile's activation
+// rows, read through perm (row q of the tile is token perm[q] / div) or directly (perm == null).
+// SILU: the wave also runs the matching up-projection column (n + N/2) and stores
+// bf16(float(bf16(g sigmoid g)) * u) of the bf16-rounded products, as moe_silu_mul does on gqmm's bf16 output.
+template <bool SILU>
+__global__ __launch_bounds__(256) void k_gqmm(const uint16_t* __restrict__ A, const int* __restrict__ perm, int div,
+                                              const int* __restrict__ tiles, const int* __restrict__ ntiles,
+                                              const uint32_t* __restrict__ wq, const uint16_t* __restrict__ s,
+                                              const uint16_t* __restrict__ b, int N, int K,
+                                              const int* __restrict__ offsets, uint16_t* __restrict__ C, int ncb) {
+  const int tile = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+  if (tile >= ntiles[0]) return;
+  const int e = tiles[2 * tile], q0 = tiles[2 * tile + 1], q1 = min(offsets[e + 1], q0 + 32);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int NO = SILU ? N / 2 : N;  // output columns
+  const int n0 = cb * 128 + wave * 32;
+  if (n0 >= NO) return;
+  const int n = min(n0 + j, NO - 1);
+  const int G = K / kGroup, ldw = K / 8;
+  const size_t erow = (size_t)e * N;
+  const uint32_t* wrow = wq + (erow + n) * ldw + 4 * h;
+  const uint16_t* srow = s + (erow + n) * G;
+  const uint16_t* brow = b + (erow + n) * G;
+  const uint32_t* wrow2 = wq + (erow + n + NO) * ldw + 4 * h;
+  const uint16_t* srow2 = s + (erow + n + NO) * G;
+  const uint16_t* brow2 = b + (erow + n + NO) * G;
+  const int q = q0 + j;
+  const bool aok = q < q1;
+  const int arow_i = aok ? (perm ? perm[q] / div : q) : 0;
+  const uint16_t* arow = A + (size_t)arow_i * K + 32 * h;
+
+  f32x16 acc = zero16(), acc2 = zero16();
+  for (int g = 0; g < G; g++) {
+    const u32x4 wv = *(const u32x4*)(wrow + (size_t)g * 8);
+    const float sc = bf2f(srow[g]), bi = bf2f(brow[g]);
+    u32x4 wv2;
+    float sc2 = 0.f, bi2 = 0.f;
+    if (SILU) {
+      wv2 = *(const u32x4*)(wrow2 + (size_t)g * 8);
+      sc2 = bf2f(srow2[g]);
+      bi2 = bf2f(brow2[g]);
+    }
+    u32x4 af[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) af[t] = aok ? *(const u32x4*)(arow + (size_t)g * 64 + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      acc = mfma_bf16(af[t], dequant8_bf16(wv[t], sc, bi), acc);
+      if (SILU) acc2 = mfma_bf16(af[t], dequant8_bf16(wv2[t], sc2, bi2), acc2);
+    }
+  }
+  const int col = n0 + j;
+  if (col >= NO) return;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int row = q0 + 8 * (r / 4) + 4 * h + (r % 4);
+    if (row >= q1) continue;
+    float v = acc[r];
+    if (SILU) {
+      const float gg = bf2f(f2bf(acc[r])), uu = bf2f(f2bf(acc2[r]));
+      v = bf2f(f2bf(gg / (1.f + expf(-gg)))) * uu;
+    }
+    C[(size_t)row * NO + col] = f2bf(v);
+  }
+}
+
+int launch_moe_gather_qmm(const uint16_t* A, const int* perm, int div, const int* tiles, const int* ntiles,
+                              const int* offsets, int max_tiles, const uint32_t* wq, const uint16_t* s,
+                              const uint16_t* b, int N, int K, int silu, uint16_t* C, int R, hipStream_t st) {
+  if (R == 0 || max_tiles == 0) return IFD_OK;
+  const int NO = silu ? N / 2 : N, ncb = (NO + 127) / 128;
+  dim3 grid((unsigned)(max_tiles * ncb)), block(256);
+  if (silu)
+    hipLaunchKernelGGL(k_gqmm<true>, grid, block, 0, st, A, perm, div, tiles, ntiles, wq, s, b, N, K, offsets, C, ncb);
+  else
+    hipLaunchKernelGGL(k_gqmm<false>, grid, block, 0, st, A, perm, div, tiles, ntiles, wq, s, b, N, K, offsets, C,
+                       ncb);
+  return check_launch("moe_gather_qmm");
+}
+
+// ---- combine -----------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_moe_combine(uint16_t* __restrict__ out, const uint16_t* __restrict__ yd,
+                                                     const float* __restrict__ wt, const uint16_t* __restrict__ ys,
+                                                     const float* __restrict__ sg, const int* __restrict__ inv, int T,
+                                                     int H, int k, int assign) {
+  const int per_row = H / 8;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)T * per_row) return;
+  const int t = (int)(i / per_row), c = (int)(i % per_row) * 8;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) acc[e] = 0.f;
+  for (int jj = 0; jj < k; jj++) {
+    const float w = wt[(size_t)t * k + jj];
+    const u32x4 y = *(const u32x4*)(yd + (size_t)inv[(size_t)t * k + jj] * H + c);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] = __builtin_fmaf(w, bf2f((uint16_t)(y[e / 2] >> (16 * (e & 1)))), acc[e]);
+  }
+  if (ys) {
+    const float w = sg[t];
+    const u32x4 y = *(const u32x4*)(ys + (size_t)t * H + c);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] = __builtin_fmaf(w, bf2f((uint16_t)(y[e / 2] >> (16 * (e & 1)))), acc[e]);
+  }
+  uint16_t* o = out + (size_t)t * H + c;
+  u32x4 ov = *(const u32x4*)o, res;
+#pragma unroll
+  for (int e2 = 0; e2 < 4; e2++) {
+    float v[2];
+#pragma unroll
+    for (int f = 0; f < 2; f++) {
+      const int e = 2 * e2 + f;
+      v[f] = assign ? acc[e] : bf2f((uint16_t)(ov[e2] >> (16 * f))) + bf2f(f2bf(acc[e]));
+    }
+    res[e2] = pack_bf2(v[0], v[1]);
+  }
+  *(u32x4*)o = res;
+}
+
+int launch_moe_combine(uint16_t* out, const uint16_t* yd, const float* wt, const uint16_t* ys, const float* sg,
+                       const int* inv, int T, int H, int k, int assign, hipStream_t st) {
+  if (T == 0) return IFD_OK;
+  const size_t n = (size_t)T * (H / 8);
+  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, yd, wt, ys, sg, inv, T,
+                     H, k, assign);
+  return check_launch("moe_combine");
+}
+
+}  // namespace ifd

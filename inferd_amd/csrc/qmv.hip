@@ -1,0 +1,240 @@
+// Decode path (M <= 128 rows of concurrent agents): 4-bit GEMV/skinny GEMM on bf16 MFMA.
+//
+// Replaces the reference's qmv4 (engine/kernels/core.metal:85-171) and its split-K neighbours (qmm_splitk +
+// splitk_reduce, engine/kernels/qmm_splitk.metal:14-107; host choice engine/src/qwen35.h:1520-1556).
+//
+// Layout per wave: 32 output columns (weight rows n) x a K range; lane l owns column l % 32 and half h = l / 32 of
+// every 64-group: the 16 bytes (32 codes) at words 4h..4h+3 of the group, one global_load_dwordx4 per group.
+// A 64-group is four 32x32x16 bf16 MFMA steps; in step t the lane supplies codes of word 4h + t, i.e. the k slots of
+// a step are k = 32h + 8t + 0..7 of the group, and the activation fragment follows the same k assignment (16 bytes
+// of row m at 32h + 8t), so every MFMA stays inside one group.
+//
+// Two variants:
+//  * affine (M <= 32): codes enter the MFMA as bf16 (128 + q) (exact), a second MFMA against ones gives the
+//    activation group sums X, and the group epilogue adds s * P + (b - 128 s) * X in fp32: the qmv4 arithmetic
+//    (s * sum q x + b * sum x per group, fp32) with fp32 MFMA accumulation.
+//  * dequant (32 < M <= 128): codes are dequantized in registers to bf16(s q + b), MLX's qmm rounding
+//    (quantized.h:528-535), and accumulate over the whole K range; one dequant feeds all 32-row M tiles.
+// Narrow outputs split K over blockIdx.y and write fp32 partials [S][M][N]; k_splitk_reduce applies the store mode.
+#include "common.h"
+#include "host.h"
+#include "kernels.h"
+
+namespace ifd {
+
+struct QmvArgs {
+  const uint16_t* A;
+  int lda;
+  const uint32_t* wq;
+  const uint16_t* s;
+  const uint16_t* b;
+  int N, K, ldk;
+  uint32_t xr;
+  void* C;
+  int ldc, M, mode;
+  float* part;  // split partials (gridDim.y > 1)
+  int gps;      // 64-groups per split
+};
+
+constexpr int kQmvPF = 4;  // groups of weights in flight per lane
+
+template <int RACT>
+__global__ __launch_bounds__(256) void k_qmv_affine(QmvArgs p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * 128 + wave * 32;
+  if (n0 >= p.N) return;
+  const int n = min(n0 + j, p.N - 1);
+  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+  const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps);
+  const uint32_t* wrow = p.wq + (size_t)n * ldw + 4 * h;
+  const uint16_t* srow = p.s + (size_t)n * ldg;
+  const uint16_t* brow = p.b + (size_t)n * ldg;
+  const bool aok = j < p.M;
+  const uint16_t* arow = p.A + (size_t)(aok ? j : 0) * p.lda + 32 * h;
+  const uint32_t xr = p.xr;
+  u32x4 ones;
+  ones[0] = ones[1] = ones[2] = ones[3] = 0x3F803F80u;  // bf16 1.0 pairs
+
+  f32x16 acc = zero16();
+  u32x4 wbuf[kQmvPF];
+  uint32_t sbuf[kQmvPF];
+#pragma unroll
+  for (int i = 0; i < kQmvPF; i++) {
+    const int g = g0 + i;
+    if (g < g1) {
+      wbuf[i] = *(const u32x4*)(wrow + (size_t)g * 8);
+      sbuf[i] = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
+    }
+  }
+  for (int gb = g0; gb < g1; gb += kQmvPF) {
+#pragma unroll
+    for (int i = 0; i < kQmvPF; i++) {
+      const int g = gb + i;
+      if (g >= g1) break;
+      const u32x4 wv = wbuf[i];
+      const uint32_t sb = sbuf[i];
+      if (g + kQmvPF < g1) {
+        wbuf[i] = *(const u32x4*)(wrow + (size_t)(g + kQmvPF) * 8);
+        sbuf[i] = (uint32_t)srow[g + kQmvPF] | ((uint32_t)brow[g + kQmvPF] << 16);
+      }
+      u32x4 af[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        if (aok) af[t] = *(const u32x4*)(arow + (size_t)g * 64 + 8 * t);
+        else af[t] = u32x4{0u, 0u, 0u, 0u};
+      }
+      f32x16 P = zero16(), X = zero16();
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        P = mfma_bf16(af[t], codes_bf16_off128(wv[t] ^ xr), P);
+        X = mfma_bf16(af[t], ones, X);
+      }
+      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16));
+      const float bp = __builtin_fmaf(-128.f, sc, bi);
+#pragma unroll
+      for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, X[r], acc[r]));
+    }
+  }
+  const int col = n0 + j;
+  if (col >= p.N) return;
+  const bool split = gridDim.y > 1;
+#pragma unroll
+  for (int r = 0; r < RACT; r++) {
+    const int row = 8 * (r / 4) + 4 * h + (r % 4);
+    if (row >= p.M) continue;
+    if (split) p.part[((size_t)blockIdx.y * p.M + row) * p.N + col] = acc[r];
+    else store_mode(p.C, (size_t)row * p.ldc + col, acc[r], p.mode);
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void k_qmv_deq(QmvArgs p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * 128 + wave * 32;
+  if (n0 >= p.N) return;
+  const int n = min(n0 + j, p.N - 1);
+  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+  const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps);
+  const uint32_t* wrow = p.wq + (size_t)n * ldw + 4 * h;
+  const uint16_t* srow = p.s + (size_t)n * ldg;
+  const uint16_t* brow = p.b + (size_t)n * ldg;
+  const uint16_t* arow[MT];
+  bool aok[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    const int m = 32 * mt + j;
+    aok[mt] = m < p.M;
+    arow[mt] = p.A + (size_t)(aok[mt] ? m : 0) * p.lda + 32 * h;
+  }
+  const uint32_t xr = p.xr;
+
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) acc[mt] = zero16();
+  u32x4 wbuf[kQmvPF];
+  uint32_t sbuf[kQmvPF];
+#pragma unroll
+  for (int i = 0; i < kQmvPF; i++) {
+    const int g = g0 + i;
+    if (g < g1) {
+      wbuf[i] = *(const u32x4*)(wrow + (size_t)g * 8);
+      sbuf[i] = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
+    }
+  }
+  for (int gb = g0; gb < g1; gb += kQmvPF) {
+#pragma unroll
+    for (int i = 0; i < kQmvPF; i++) {
+      const int g = gb + i;
+      if (g >= g1) break;
+      const u32x4 wv = wbuf[i];
+      const uint32_t sb = sbuf[i];
+      if (g + kQmvPF < g1) {
+        wbuf[i] = *(const u32x4*)(wrow + (size_t)(g + kQmvPF) * 8);
+        sbuf[i] = (uint32_t)srow[g + kQmvPF] | ((uint32_t)brow[g + kQmvPF] << 16);
+      }
+      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16));
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const u32x4 bfr = dequant8_bf16(wv[t] ^ xr, sc, bi);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+          u32x4 af = u32x4{0u, 0u, 0u, 0u};
+          if (aok[mt]) af = *(const u32x4*)(arow[mt] + (size_t)g * 64 + 8 * t);
+          acc[mt] = mfma_bf16(af, bfr, acc[mt]);
+        }
+      }
+    }
+  }
+  const int col = n0 + j;
+  if (col >= p.N) return;
+  const bool split = gridDim.y > 1;
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = 32 * mt + 8 * (r / 4) + 4 * h + (r % 4);
+      if (row >= p.M) continue;
+      if (split) p.part[((size_t)blockIdx.y * p.M + row) * p.N + col] = acc[mt][r];
+      else store_mode(p.C, (size_t)row * p.ldc + col, acc[mt][r], p.mode);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, int S, int M, int N, void* C,
+                                                       int ldc, int mode) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, mn = (size_t)M * N;
+  if (i >= mn) return;
+  const int m = (int)(i / N), n = (int)(i % N);
+  float v = 0.f;
+  for (int z = 0; z < S; z++) v += part[(size_t)z * mn + i];
+  store_mode(C, (size_t)m * ldc + n, v, mode);
+}
+
+int launch_splitk_reduce(const float* part, int S, int M, int N, void* C, int ldc, int mode, hipStream_t st) {
+  const size_t mn = (size_t)M * N;
+  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, part, S, M, N, C, ldc,
+                     mode);
+  return check_launch("splitk_reduce");
+}
+
+// K splits for a decode GEMM: enough blocks (~2 per CU on 256 CUs) while every split keeps >= 4 groups and the
+// partials stay small (S * M <= 1024 rows, the reference's kSplitRows, qwen35.h:77).
+static int qmv_splits(int M, int N, int K) {
+  const int G = K / kGroup, bx = (N + 127) / 128;
+  int S = (512 + bx - 1) / bx;
+  S = std::min(S, std::max(1, G / 4));
+  S = std::min(S, std::max(1, 1024 / std::max(M, 1)));
+  if (S <= 1) return 1;
+  const int gps = (G + S - 1) / S;
+  return (G + gps - 1) / gps;
+}
+
+size_t qmv_workspace(int M, int N, int K) {
+  const int S = qmv_splits(M, N, K);
+  return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+}
+
+int launch_qmv(const W4Gemm& g, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (g.M == 0) return IFD_OK;
+  if (g.M > 128) return fail(IFD_ERR_ARG, "qmv path takes M <= 128 (M=%d)", g.M);
+  const int G = g.K / kGroup;
+  int S = qmv_splits(g.M, g.N, g.K);
+  const size_t need = S > 1 ? (size_t)S * g.M * g.N * sizeof(float) : 0;
+  if (need > ws_bytes || (need && !ws))
+    return fail(IFD_ERR_WORKSPACE, "qmv needs %zu bytes of workspace, got %zu", need, ws_bytes);
+  const int gps = (G + S - 1) / S;
+  QmvArgs p{(const uint16_t*)g.A, g.lda, g.wq, g.s, g.b, g.N, g.K, g.ldk, g.xr, g.C, g.ldc, g.M, g.mode,
+            (float*)ws, gps};
+  dim3 grid((g.N + 127) / 128, S), block(256);
+  if (g.M <= 8) hipLaunchKernelGGL(k_qmv_affine<4>, grid, block, 0, st, p);
+  else if (g.M <= 16) hipLaunchKernelGGL(k_qmv_affine<8>, grid, block, 0, st, p);
+  else if (g.M <= 32) hipLaunchKernelGGL(k_qmv_affine<16>, grid, block, 0, st, p);
+  else if (g.M <= 64) hipLaunchKernelGGL(k_qmv_deq<2>, grid, block, 0, st, p);
+  else hipLaunchKernelGGL(k_qmv_deq<4>, grid, block, 0, st, p);
+  IFD_TRY(check_launch("qmv"));
+  if (S > 1) return launch_splitk_reduce((const float*)ws, S, g.M, g.N, g.C, g.ldc, g.mode, st);
+  return IFD_OK;
+}
+
+}  // namespace ifd

@@ -1,0 +1,270 @@
+// W4A8: int8 activations x the checkpoint's 4-bit weights on int8 MFMA, plus the elementwise kernels of the path
+// (activation quantizer, in-place nibble flip, SwiGLU).
+//
+// Replaces the reference's a8_quant + w4a8_gemm (engine/kernels/w4a8.metal:24-98; host w4a8,
+// engine/src/qwen35.h:1323-1366), w_flip (w4a8.metal:19-22) and silu_mul (engine/kernels/core.metal:777-787).
+//
+// Per 64-group g the GEMM forms the exact int32 P = sum_k q[n,k] xq[m,k] (q unsigned 0..15 after undoing a flip)
+// on v_mfma_i32_32x32x32_i8, then applies the affine correction in fp32:
+//   y[m,n] += s[n,g] sx[m,g] P + b[n,g] (sx[m,g] sum_k xq[m,k])
+// which is the reference's identity (w4a8.metal:7-8) written with unsigned codes. With per-token scales (sx constant
+// along the row) sx is factored out of the group loop.
+// Block: 256 threads (2 x 2 waves), tile 128 x 128, one group per step, int8 tiles and the group's (s, b) / XS
+// staged in LDS, double-buffered.
+#include "common.h"
+#include "host.h"
+#include "kernels.h"
+
+namespace ifd {
+
+// ---- activation quantizer --------------------------------------------------------------------------------------
+// One block of 256 threads per row. per_token: amax over the row; else per 64-group. sx = amax / 127 (1 if 0),
+// xq = rint(x / sx) (IEEE division and round-half-even: bit-identical to the CPU reference), XS = (sx, sx * sum xq).
+__global__ __launch_bounds__(256) void k_a8_quant(const uint16_t* __restrict__ A, int lda, int K, int per_token,
+                                                  int8_t* __restrict__ U, float* __restrict__ XS) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint16_t* a = A + (size_t)m * lda;
+  const int G = K / kGroup;
+  float row_sx = 1.f;
+  if (per_token) {
+    float mx = 0.f;
+    for (int k = tid; k < K; k += 256) mx = fmaxf(mx, fabsf(bf2f(a[k])));
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    row_sx = mx > 0.f ? mx / 127.f : 1.f;
+  }
+  for (int g = wave; g < G; g += 4) {
+    const float x = bf2f(a[g * kGroup + lane]);
+    float sx = row_sx;
+    if (!per_token) {
+      const float amax = wave_max(fabsf(x));
+      sx = amax > 0.f ? amax / 127.f : 1.f;
+    }
+    const float q = rintf(x / sx);
+    U[(size_t)m * K + g * kGroup + lane] = (int8_t)q;
+    const float qs = wave_sum(q);
+    if (lane == 0) {
+      XS[((size_t)m * G + g) * 2] = sx;
+      XS[((size_t)m * G + g) * 2 + 1] = sx * qs;
+    }
+  }
+}
+
+int launch_a8_quant(const uint16_t* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, hipStream_t st) {
+  if (M == 0) return IFD_OK;
+  hipLaunchKernelGGL(k_a8_quant, dim3(M), dim3(256), 0, st, A, lda, K, per_token, U, XS);
+  return check_launch("a8_quant");
+}
+
+// ---- flip / SwiGLU ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_flip(uint32_t* wq, size_t n32, uint32_t mask) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n32) wq[i] ^= mask;
+}
+int launch_flip(uint32_t* wq, size_t n32, uint32_t mask, hipStream_t st) {
+  if (n32 == 0) return IFD_OK;
+  hipLaunchKernelGGL(k_flip, dim3((unsigned)((n32 + 255) / 256)), dim3(256), 0, st, wq, n32, mask);
+  return check_launch("flip");
+}
+
+// h = bf16(float(bf16(g / (1 + exp(-g)))) * u), 8 values per thread.
+__global__ __launch_bounds__(256) void k_silu_mul(const uint16_t* __restrict__ gu, uint16_t* __restrict__ h, int I,
+                                                  int rows) {
+  const int per_row = I / 8;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)rows * per_row) return;
+  const int r = (int)(i / per_row), c = (int)(i % per_row) * 8;
+  const u32x4 gv = *(const u32x4*)(gu + (size_t)r * 2 * I + c);
+  const u32x4 uv = *(const u32x4*)(gu + (size_t)r * 2 * I + I + c);
+  u32x4 o;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    float res[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const float g = bf2f((uint16_t)(gv[t] >> (16 * e))), u = bf2f((uint16_t)(uv[t] >> (16 * e)));
+      res[e] = bf2f(f2bf(g / (1.f + expf(-g)))) * u;
+    }
+    o[t] = pack_bf2(res[0], res[1]);
+  }
+  *(u32x4*)(h + (size_t)r * I + c) = o;
+}
+int launch_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows, hipStream_t st) {
+  if (rows == 0) return IFD_OK;
+  const size_t n = (size_t)rows * (I / 8);
+  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, h, I, rows);
+  return check_launch("silu_mul");
+}
+
+// ---- W4A8 GEMM -------------------------------------------------------------------------------------------------
+constexpr int kA8BM = 128, kA8BN = 128, kA8Ld = 80;  // LDS row: 64 int8 + 16 pad
+constexpr int kA8Band = 4;
+
+struct W4A8Args {
+  const int8_t* U;
+  const float* XS;
+  const uint32_t* wq;
+  const uint16_t* s;
+  const uint16_t* b;
+  int N, K, ldk;
+  uint32_t xr;
+  void* C;
+  int ldc, M, mode;
+  int tiles_m, tiles_n;
+};
+
+template <bool PT>
+__global__ __launch_bounds__(256) void k_w4a8(W4A8Args p) {
+  __shared__ __align__(16) int8_t Us[2][kA8BM * kA8Ld];
+  __shared__ __align__(16) int8_t Ws[2][kA8BN * kA8Ld];
+  __shared__ __align__(16) float Sb[2][kA8BN][2];   // (s, b) of the group per column
+  __shared__ __align__(16) float Xq[2][kA8BM][2];   // (sx, sx * sum xq) of the group per row
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int L = xcd_remap(blockIdx.x, ntiles);
+  const int per_band = kA8Band * p.tiles_n;
+  const int band = L / per_band, within = L % per_band;
+  const int bm = min(kA8Band, p.tiles_m - band * kA8Band);
+  const int tm = band * kA8Band + within % bm, tn = within / bm;
+  const int m0 = tm * kA8BM, n0 = tn * kA8BN;
+  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+
+  // activation tile: 128 rows x 64 B, two 16 B chunks per thread: c = tid + 256 i -> row c / 4, part c % 4
+  const int8_t* uptr[2];
+  bool uok[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int c = tid + 256 * i, m = m0 + (c >> 2);
+    uok[i] = m < p.M;
+    uptr[i] = p.U + (size_t)(uok[i] ? m : 0) * p.K + 16 * (c & 3);
+  }
+  // weight tile: row tid / 2, half tid % 2 (32 codes)
+  const int wr = tid >> 1, wh = tid & 1;
+  const int nw = min(n0 + wr, p.N - 1);
+  const uint32_t* wptr = p.wq + (size_t)nw * ldw + 4 * wh;
+  const uint16_t* sptr = p.s + (size_t)nw * ldg;
+  const uint16_t* bptr = p.b + (size_t)nw * ldg;
+  const int xm = min(m0 + (tid & 127), max(p.M - 1, 0));
+
+  u32x4 ureg[2], wreg;
+  uint32_t sbreg = 0;
+  float xsreg[2] = {0.f, 0.f};
+  auto gload = [&](int g) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) ureg[i] = uok[i] ? *(const u32x4*)(uptr[i] + (size_t)g * 64) : u32x4{0u, 0u, 0u, 0u};
+    wreg = *(const u32x4*)(wptr + (size_t)g * 8);
+    if (wh == 0) sbreg = (uint32_t)sptr[g] | ((uint32_t)bptr[g] << 16);
+    if (tid < 128) {
+      xsreg[0] = p.XS[((size_t)xm * G + g) * 2];
+      xsreg[1] = p.XS[((size_t)xm * G + g) * 2 + 1];
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int c = tid + 256 * i;
+      *(u32x4*)(&Us[buf][(c >> 2) * kA8Ld + 16 * (c & 3)]) = ureg[i];
+    }
+    int8_t* ws = &Ws[buf][wr * kA8Ld + 32 * wh];
+#pragma unroll
+    for (int t = 0; t < 4; t++) *(u32x2*)(ws + 8 * t) = codes_i8(wreg[t] ^ p.xr);
+    if (wh == 0) {
+      Sb[buf][wr][0] = bf2f((uint16_t)(sbreg & 0xFFFFu));
+      Sb[buf][wr][1] = bf2f((uint16_t)(sbreg >> 16));
+    }
+    if (tid < 128) {
+      Xq[buf][tid][0] = xsreg[0];
+      // per-token: the exact integer sum xq (|sum| <= 8128), sx is applied once after the loop
+      Xq[buf][tid][1] = PT ? rintf(xsreg[1] / xsreg[0]) : xsreg[1];
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; a++)
+#pragma unroll
+    for (int c = 0; c < 2; c++) acc[a][c] = zero16();
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int g = 0; g < G; g++) {
+    const int buf = g & 1;
+    if (g + 1 < G) gload(g + 1);
+    const int8_t* us = &Us[buf][(wm * 64 + j) * kA8Ld + 16 * h];
+    const int8_t* ws = &Ws[buf][(wn * 64 + j) * kA8Ld + 16 * h];
+    i32x16 P[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+      for (int c = 0; c < 2; c++) P[a][c] = izero16();
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      u32x4 af[2], bf[2];
+#pragma unroll
+      for (int a = 0; a < 2; a++) af[a] = *(const u32x4*)(us + a * 32 * kA8Ld + 32 * kk);
+#pragma unroll
+      for (int c = 0; c < 2; c++) bf[c] = *(const u32x4*)(ws + c * 32 * kA8Ld + 32 * kk);
+#pragma unroll
+      for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) P[a][c] = mfma_i8(af[a], bf[c], P[a][c]);
+    }
+    // epilogue of the group
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const float sc = Sb[buf][wn * 64 + 32 * c + j][0], bi = Sb[buf][wn * 64 + 32 * c + j][1];
+#pragma unroll
+      for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; r4++) {
+          const int row = wm * 64 + 32 * a + 8 * r4 + 4 * h;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float sx = Xq[buf][row + e][0], sq = Xq[buf][row + e][1];
+            const float pf = (float)P[a][c][4 * r4 + e];
+            float v = acc[a][c][4 * r4 + e];
+            if (PT) v = __builtin_fmaf(sc, pf, v);  // y / sx = sum_g s P + b sum xq
+            else v = __builtin_fmaf(sx, sc * pf, v);
+            acc[a][c][4 * r4 + e] = __builtin_fmaf(bi, sq, v);
+          }
+        }
+    }
+    if (g + 1 < G) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int a = 0; a < 2; a++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = m0 + wm * 64 + 32 * a + 8 * (r / 4) + 4 * h + (r % 4);
+      if (row >= p.M) continue;
+      const float sx = PT ? p.XS[(size_t)row * G * 2] : 1.f;
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const int col = n0 + wn * 64 + 32 * c + j;
+        if (col >= p.N) continue;
+        store_mode(p.C, (size_t)row * p.ldc + col, PT ? sx * acc[a][c][r] : acc[a][c][r], p.mode);
+      }
+    }
+}
+
+size_t w4a8_workspace(int, int, int) { return 0; }
+
+int launch_w4a8(const W4Gemm& g, int per_token, void*, size_t, hipStream_t st) {
+  if (g.M == 0) return IFD_OK;
+  W4A8Args p{(const int8_t*)g.A, g.XS, g.wq, g.s, g.b, g.N, g.K, g.ldk, g.xr, g.C, g.ldc, g.M, g.mode,
+             (g.M + kA8BM - 1) / kA8BM, (g.N + kA8BN - 1) / kA8BN};
+  if (per_token) hipLaunchKernelGGL(k_w4a8<true>, dim3(p.tiles_m * p.tiles_n), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL(k_w4a8<false>, dim3(p.tiles_m * p.tiles_n), dim3(256), 0, st, p);
+  return check_launch("w4a8");
+}
+
+}  // namespace ifd

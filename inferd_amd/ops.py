@@ -1,0 +1,197 @@
+"""Python mirror of the engine-facing operators over the C ABI (include/inferd_qmm.h).
+
+torch supplies device memory and the current HIP stream; every computation runs in libinferd_amd.so.
+Names follow the reference engine: ``QLinear`` (engine/src/weights.h:226-236), ``MoeW`` (engine/src/moe.h:8-11),
+``gemm`` (Qwen35::gemm, engine/src/qwen35.h:1465) and ``moe_ffn`` (Qwen35::encode_moe, qwen35.h:1869).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from ._lib import check, lib
+
+FLIP_MASK = 0x88888888
+
+
+def _p(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+_ws_cache: dict = {}
+
+
+def workspace(nbytes: int, device) -> torch.Tensor:
+    """A cached uint8 device buffer of at least nbytes (grown on demand), reused across calls on one stream."""
+    key = str(device)
+    buf = _ws_cache.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _ws_cache[key] = buf
+    return buf
+
+
+@dataclass
+class QLinear:
+    """MLX affine 4-bit group-64 linear [N, K]: wq int32 [N, K/8] (uint32 bit patterns), s/b bf16 [N, K/64]."""
+    wq: torch.Tensor
+    s: torch.Tensor
+    b: torch.Tensor
+    N: int
+    K: int
+    flipped: bool = False
+
+    @property
+    def xr(self) -> int:
+        return FLIP_MASK if self.flipped else 0
+
+
+@dataclass
+class MoeW:
+    """Stacked experts [E, N, K] in the same affine layout (engine/src/moe.h:8-11)."""
+    wq: torch.Tensor
+    s: torch.Tensor
+    b: torch.Tensor
+    E: int
+    N: int
+    K: int
+
+
+# ---- dense ----------------------------------------------------------------------------------------------------------
+def gemm(A: torch.Tensor, W: QLinear, C: Optional[torch.Tensor] = None, mode: int = 0, path: str = "auto") -> torch.Tensor:
+    """C (mode) = A . W^T. mode 0 bf16 out, 1 bf16 residual add into C, 2 fp32 out. path: auto | qmv | qmm."""
+    M, K = A.shape
+    assert K == W.K and A.dtype == torch.bfloat16 and A.is_contiguous()
+    if C is None:
+        C = torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=A.device)
+    fn = {"auto": lib().ifd_gemm_w4, "qmv": lib().ifd_qmv_w4, "qmm": lib().ifd_qmm_w4}[path]
+    need = lib().ifd_gemm_w4_workspace(M, W.N, W.K)
+    ws = workspace(need, A.device) if need else None
+    check(fn(_p(A), K, _p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, W.xr, _p(C), C.shape[1], M, mode, _p(ws),
+             ws.numel() if ws is not None else 0, _stream()))
+    return C
+
+
+def flip(W: QLinear) -> None:
+    """In-place nibble flip (reference w_flip / Qwen35::flip)."""
+    check(lib().ifd_flip_w4(_p(W.wq), W.wq.numel(), FLIP_MASK, _stream()))
+    W.flipped = not W.flipped
+
+
+def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    R, I2 = gu.shape
+    h = torch.empty((R, I2 // 2), dtype=torch.bfloat16, device=gu.device)
+    check(lib().ifd_silu_mul(_p(gu), _p(h), I2 // 2, R, _stream()))
+    return h
+
+
+def a8_quant(A: torch.Tensor, per_token: bool):
+    M, K = A.shape
+    U = torch.empty((M, K), dtype=torch.int8, device=A.device)
+    XS = torch.empty((M, K // 64, 2), dtype=torch.float32, device=A.device)
+    check(lib().ifd_a8_quant(_p(A), K, M, K, 1 if per_token else 0, _p(U), _p(XS), _stream()))
+    return U, XS
+
+
+def qmm_w4a8(U: torch.Tensor, XS: torch.Tensor, per_token: bool, W: QLinear, C: Optional[torch.Tensor] = None,
+             mode: int = 0) -> torch.Tensor:
+    M, K = U.shape
+    if C is None:
+        C = torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=U.device)
+    check(lib().ifd_qmm_w4a8(_p(U), _p(XS), 1 if per_token else 0, _p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, W.xr,
+                             _p(C), C.shape[1], M, mode, None, 0, _stream()))
+    return C
+
+
+# ---- MoE ------------------------------------------------------------------------------------------------------------
+def moe_router_logits(x: torch.Tensor, w: torch.Tensor, out_bf16: bool) -> torch.Tensor:
+    T, H = x.shape
+    E1 = w.shape[0]
+    out = torch.empty((T, E1), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=x.device)
+    check(lib().ifd_moe_router_logits(_p(x), _p(w), T, H, E1, 1 if out_bf16 else 0, _p(out), _stream()))
+    return out
+
+
+def moe_route(logits: torch.Tensor, E: int, k: int, norm: bool = True, shared_gate: bool = True):
+    T, stride = logits.shape
+    idx = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+    wt = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+    sg = torch.empty((T,), dtype=torch.float32, device=logits.device)
+    check(lib().ifd_moe_route(_p(logits), 1 if logits.dtype == torch.bfloat16 else 0, T, E, k, stride,
+                              1 if norm else 0, 1 if shared_gate else 0, _p(idx), _p(wt), _p(sg), _stream()))
+    return idx, wt, sg
+
+
+def moe_dispatch(idx: torch.Tensor, E: int):
+    R = idx.numel()
+    dev = idx.device
+    offsets = torch.empty((E + 1,), dtype=torch.int32, device=dev)
+    perm = torch.empty((max(R, 1),), dtype=torch.int32, device=dev)
+    inv = torch.empty((max(R, 1),), dtype=torch.int32, device=dev)
+    mt = lib().ifd_moe_tiles_max(R, E)
+    tiles = torch.empty((max(mt, 1), 2), dtype=torch.int32, device=dev)
+    ntiles = torch.empty((1,), dtype=torch.int32, device=dev)
+    need = lib().ifd_moe_dispatch_workspace(R, E)
+    ws = torch.empty((max(need, 256),), dtype=torch.uint8, device=dev)
+    check(lib().ifd_moe_dispatch(_p(idx), R, E, _p(offsets), _p(perm), _p(inv), _p(tiles), _p(ntiles), _p(ws),
+                                 ws.numel(), _stream()))
+    return offsets, perm[:R], inv[:R], tiles, ntiles, mt
+
+
+def moe_gather(x: torch.Tensor, perm: torch.Tensor, div: int) -> torch.Tensor:
+    R = perm.numel()
+    H = x.shape[1]
+    xs = torch.empty((R, H), dtype=torch.bfloat16, device=x.device)
+    check(lib().ifd_moe_gather(_p(x), _p(perm), div, R, H, _p(xs), _stream()))
+    return xs
+
+
+def moe_gather_qmm(A: torch.Tensor, perm: Optional[torch.Tensor], div: int, disp, W: MoeW, silu: bool) -> torch.Tensor:
+    offsets, perm_sorted, _, tiles, ntiles, mt = disp
+    R = perm_sorted.numel()
+    NO = W.N // 2 if silu else W.N
+    C = torch.empty((R, NO), dtype=torch.bfloat16, device=A.device)
+    check(lib().ifd_moe_gather_qmm(_p(A), _p(perm), div, _p(offsets), _p(tiles), _p(ntiles), mt, _p(W.wq), _p(W.s),
+                                   _p(W.b), W.E, W.N, W.K, 1 if silu else 0, _p(C), R, _stream()))
+    return C
+
+
+def moe_combine(out: torch.Tensor, yd: torch.Tensor, wt: torch.Tensor, ys: Optional[torch.Tensor],
+                sg: Optional[torch.Tensor], inv: torch.Tensor, k: int, assign: bool) -> torch.Tensor:
+    T, H = out.shape
+    check(lib().ifd_moe_combine(_p(out), _p(yd), _p(wt), _p(ys), _p(sg), _p(inv), T, H, k, 1 if assign else 0,
+                                _stream()))
+    return out
+
+
+def moe_ffn(xn: torch.Tensor, router: torch.Tensor, egu: MoeW, edn: MoeW, k: int,
+            shared: Optional[tuple] = None, shared_gate: bool = True, norm: bool = True,
+            logits_bf16: bool = True, out: Optional[torch.Tensor] = None, assign: bool = True):
+    """One-shot MoE FFN (reference encode_moe's sorted path). shared = (QLinear gate_up [2Is, H], QLinear down [H, Is]).
+
+    Returns (out, idx, wt, sg)."""
+    T, H = xn.shape
+    E, I = egu.E, egu.N // 2
+    dev = xn.device
+    if out is None:
+        out = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    wt = torch.empty((T, k), dtype=torch.float32, device=dev)
+    sg = torch.empty((T,), dtype=torch.float32, device=dev)
+    Is = shared[1].K if shared is not None else 0
+    need = lib().ifd_moe_ffn_workspace(T, H, I, E, k, Is)
+    ws = workspace(need, dev)
+    sgu, sdn = shared if shared is not None else (None, None)
+    check(lib().ifd_moe_ffn(
+        _p(xn), T, H, _p(router), E, k, 1 if norm else 0, 1 if shared_gate else 0, 1 if logits_bf16 else 0,
+        _p(egu.wq), _p(egu.s), _p(egu.b), _p(edn.wq), _p(edn.s), _p(edn.b), I,
+        _p(sgu.wq) if sgu else None, _p(sgu.s) if sgu else None, _p(sgu.b) if sgu else None,
+        _p(sdn.wq) if sdn else None, _p(sdn.s) if sdn else None, _p(sdn.b) if sdn else None, Is,
+        _p(out), 1 if assign else 0, _p(idx), _p(wt), _p(sg), _p(ws), ws.numel(), _stream()))
+    return out, idx, wt, sg

@@ -1,0 +1,64 @@
+"""Seeded synthetic inputs shared by the tests (numpy PCG64 generators; bf16 as uint16 bit patterns).
+
+Distributions follow BASELINE config 0: codes q ~ U{0..15}; scales s ~ U(smin, smax) rounded to bf16; biases
+b = bf16(-8 s) computed from the bf16 scale; activations x ~ N(0, 1) rounded to bf16 (RNE).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (numpy, independent of the oracle library)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def pack_codes(codes: np.ndarray) -> np.ndarray:
+    """codes uint8 [N, K] -> uint32 [N, K/8], element j at bits 4j (numpy restatement of the MLX layout)."""
+    N, K = codes.shape
+    c = codes.reshape(N, K // 8, 8).astype(np.uint32)
+    w = np.zeros((N, K // 8), np.uint32)
+    for j in range(8):
+        w |= c[:, :, j] << np.uint32(4 * j)
+    return w
+
+
+def qlinear(N: int, K: int, seed: int, smin: float = 0.005, smax: float = 0.02, bias: str = "minus8"):
+    """Returns (codes uint8 [N,K], wq uint32 [N,K/8], s bf16 [N,K/64], b bf16 [N,K/64])."""
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    s = f32_to_bf16(rng.uniform(smin, smax, size=(N, K // 64)).astype(np.float32))
+    if bias == "minus8":
+        b = f32_to_bf16(-8.0 * bf16_to_f32(s))
+    else:  # independent biases, as the reference's qa8_dbg / gemm_dbg generators (b = bf16(0.05 U(-1,1)))
+        b = f32_to_bf16((0.05 * rng.uniform(-1, 1, size=(N, K // 64))).astype(np.float32))
+    return codes, pack_codes(codes), s, b
+
+
+def activations(M: int, K: int, seed: int, row_scale: bool = False) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if row_scale:  # rows scaled by U(0.5, 2)
+        x *= rng.uniform(0.5, 2.0, size=(M, 1)).astype(np.float32)
+    return f32_to_bf16(x)
+
+
+def dequant_f64(codes, s, b) -> np.ndarray:
+    """float64 dequant w = s q + b (the math, for textbook references)."""
+    N, K = codes.shape
+    sf = np.repeat(bf16_to_f32(s).astype(np.float64), 64, axis=1)
+    bf = np.repeat(bf16_to_f32(b).astype(np.float64), 64, axis=1)
+    return sf * codes.astype(np.float64) + bf
+
+
+def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
+    """max |got - ref| / RMS(ref), the BASELINE tolerance measure."""
+    ref = np.asarray(ref, np.float64)
+    rms = float(np.sqrt(np.mean(ref * ref))) or 1.0
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref))) / rms

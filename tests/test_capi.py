@@ -1,0 +1,85 @@
+"""CPU checks of the C ABI boundary: the library loads, exports every symbol include/inferd_qmm.h declares, and
+rejects invalid requests with status codes before touching the GPU (no compute runs here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from inferd_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "inferd_qmm.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ifd_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    for s in ["ifd_gemm_w4", "ifd_qmv_w4", "ifd_qmm_w4", "ifd_a8_quant", "ifd_qmm_w4a8", "ifd_moe_route",
+              "ifd_moe_dispatch", "ifd_moe_gather_qmm", "ifd_moe_combine", "ifd_moe_ffn"]:
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [s for s in declared_symbols() if not hasattr(L, s)]
+    assert not missing, missing
+    # and the Python binding covers the same set
+    assert set(declared_symbols()) == set(_lib.SIGNATURES)
+
+
+def test_status_strings_and_version():
+    L = _lib.lib()
+    assert L.ifd_version() == 1
+    assert L.ifd_status_str(0) == b"ok"
+    assert L.ifd_status_str(2) == b"workspace too small"
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(K=100), b"multiple of the group size"),
+    (dict(mode=3), b"mode=3"),
+    (dict(xr=0x1234), b"xr="),
+    (dict(lda=64), b"lda="),
+    (dict(ldk=96), b"ldk="),
+    (dict(wq=None), b"null pointer"),
+    (dict(wq=8), b"16-byte aligned"),
+])
+def test_gemm_rejects_bad_arguments(kw, msg):
+    L = _lib.lib()
+    a = dict(A=4096, lda=128, wq=4096, s=4096, b=4096, N=64, K=128, ldk=0, xr=0, C=4096, ldc=64, M=4, mode=0)
+    a.update(kw)
+    if "K" in kw and "lda" not in kw:
+        a["lda"] = max(a["lda"], kw["K"] + (-kw["K"]) % 8)
+    for fn in (L.ifd_gemm_w4, L.ifd_qmv_w4, L.ifd_qmm_w4):
+        rc = fn(a["A"], a["lda"], a["wq"], a["s"], a["b"], a["N"], a["K"], a["ldk"], a["xr"], a["C"], a["ldc"], a["M"],
+                a["mode"], None, 0, None)
+        assert rc == _lib.IFD_ERR_ARG
+        assert msg in L.ifd_last_error()
+
+
+def test_qmv_rejects_large_m_and_moe_rejects_bad_shapes():
+    L = _lib.lib()
+    rc = L.ifd_qmv_w4(4096, 128, 4096, 4096, 4096, 64, 128, 0, 0, 4096, 64, 129, 0, None, 0, None)
+    assert rc == _lib.IFD_ERR_ARG and b"M <= 128" in L.ifd_last_error()
+    assert L.ifd_moe_route(4096, 0, 4, 600, 10, 601, 1, 1, 4096, 4096, 4096, None) == _lib.IFD_ERR_ARG
+    assert L.ifd_moe_route(4096, 0, 4, 512, 17, 513, 1, 1, 4096, 4096, 4096, None) == _lib.IFD_ERR_ARG
+    assert L.ifd_moe_route(4096, 0, 4, 512, 10, 512, 1, 1, 4096, 4096, 4096, None) == _lib.IFD_ERR_ARG
+    assert L.ifd_moe_dispatch(4096, 10, 2000, 4096, 4096, 4096, 4096, 4096, None, 0, None) == _lib.IFD_ERR_ARG
+
+
+def test_workspace_queries():
+    L = _lib.lib()
+    # decode shapes split K: partials S * M * N fp32
+    ws = L.ifd_gemm_w4_workspace(1, 5120, 5120)
+    assert ws > 0 and ws % (5120 * 4) == 0
+    assert L.ifd_gemm_w4_workspace(4096, 17408, 5120) == 0
+    assert L.ifd_moe_ffn_workspace(2048, 2048, 512, 512, 10, 512) > 2048 * 10 * 2048 * 2
+    assert L.ifd_moe_tiles_max(20480, 512) == 640 + 512
+    # a too-small workspace is refused before any launch
+    rc = L.ifd_qmv_w4(4096, 5120, 4096, 4096, 4096, 5120, 5120, 0, 0, 4096, 5120, 1, 0, None, 0, None)
+    assert rc == _lib.IFD_ERR_WORKSPACE

@@ -1,0 +1,166 @@
+"""GPU parity of the MoE path (router, routing, dispatch, gathered expert GEMM, combine, one-shot FFN) against the
+CPU oracle, through the C ABI. Indices and permutations bit-exact; floats within 1e-2 RMS.
+
+Routing is compared on the same logits (the GPU's): router logits from two different summation orders may
+legitimately break a near-tie differently, so the end-to-end FFN check runs the oracle on the GPU's routing.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import gen
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _gu():
+    from tests import gpu_util
+    return gpu_util
+
+
+def _ops():
+    from inferd_amd import ops
+    return ops
+
+
+def experts(E, N, K, seed):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 16, size=(E, N, K), dtype=np.uint8)
+    wq = gen.pack_codes(codes.reshape(E * N, K)).reshape(E, N, K // 8)
+    s = gen.f32_to_bf16(rng.uniform(0.005, 0.02, size=(E, N, K // 64)).astype(np.float32))
+    b = gen.f32_to_bf16(-8.0 * gen.bf16_to_f32(s))
+    return wq, s, b
+
+
+def router(E1, H, seed):
+    rng = np.random.default_rng(seed)
+    return gen.f32_to_bf16((rng.standard_normal((E1, H)) * 0.02).astype(np.float32))
+
+
+@pytest.mark.parametrize("T,out_bf16", [(16, False), (128, True), (70, True)])
+def test_router_logits(T, out_bf16):
+    g, ops = _gu(), _ops()
+    H, E1 = 2048, 513
+    x = gen.activations(T, H, seed=T)
+    W = router(E1, H, seed=1)
+    got = g.host(ops.moe_router_logits(g.dev(x), g.dev(W), out_bf16))
+    ref = orc.gemm_bf16(x, W)
+    if out_bf16:
+        got = gen.bf16_to_f32(got)
+        ref = gen.bf16_to_f32(gen.f32_to_bf16(ref))
+    assert gen.rel_err(got, ref) < 1e-2
+
+
+@pytest.mark.parametrize("bf,shared_gate", [(False, True), (True, True), (True, False)])
+def test_route_bit_exact(bf, shared_gate):
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(2)
+    T, E, k = 300, 512, 10
+    l = (rng.standard_normal((T, E + 1)) * 0.9).astype(np.float32)
+    if bf:
+        l = gen.f32_to_bf16(l)
+        l[:5, :40] = l[:5, 40:80]  # duplicated logits: exact ties, lowest index must win
+    idx, wt, sg = ops.moe_route(g.dev(l), E, k, shared_gate=shared_gate)
+    ri, rw, rs = orc.moe_route(l, E, k, shared_gate=shared_gate)
+    assert np.array_equal(g.host(idx), ri)
+    assert np.allclose(g.host(wt), rw, rtol=1e-5, atol=1e-7)
+    assert np.allclose(g.host(sg), rs, rtol=1e-5)
+
+
+@pytest.mark.parametrize("T,E", [(16, 512), (128, 512), (2048, 512), (1, 8), (37, 64)])
+def test_dispatch_bit_exact(T, E):
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(T)
+    k = min(10, E)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    offsets, perm, inv, tiles, ntiles, mt = ops.moe_dispatch(g.dev(idx), E)
+    ro, rp, ri = orc.moe_dispatch(idx, E)
+    assert np.array_equal(g.host(offsets), ro)
+    assert np.array_equal(g.host(perm), rp)
+    assert np.array_equal(g.host(inv), ri)
+    # tile schedule: every 32-row tile of every non-empty segment, in expert order
+    nt = int(g.host(ntiles)[0])
+    want = [(e, q) for e in range(E) for q in range(ro[e], ro[e + 1], 32)]
+    assert nt == len(want) <= mt
+    assert [tuple(t) for t in g.host(tiles)[:nt].tolist()] == want
+
+
+@pytest.mark.parametrize("T,E,silu", [(16, 64, True), (40, 16, False), (200, 32, True)])
+def test_gather_qmm(T, E, silu):
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(E + T)
+    H, I, k = 256, 128, 4
+    x = gen.activations(T, H, seed=3)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    disp = ops.moe_dispatch(g.dev(idx), E)
+    ro, rp, ri = orc.moe_dispatch(idx, E)
+    if silu:
+        wq, s, b = experts(E, 2 * I, H, seed=4)
+        got = g.host(ops.moe_gather_qmm(g.dev(x), disp[1], k, disp, g.moew(wq, s, b), silu=True))
+        y = orc.moe_gather_qmm(x, rp, k, ro, wq, s, b, 2 * I, H)
+        ref = orc.silu_mul(gen.f32_to_bf16(y))
+    else:
+        wq, s, b = experts(E, H, H, seed=5)
+        xs = g.host(ops.moe_gather(g.dev(x), disp[1], k))
+        assert np.array_equal(xs, x[rp // k])
+        got = g.host(ops.moe_gather_qmm(g.dev(xs), None, 1, disp, g.moew(wq, s, b), silu=False))
+        ref = gen.f32_to_bf16(orc.moe_gather_qmm(xs, None, 1, ro, wq, s, b, H, H))
+    assert gen.rel_err(gen.bf16_to_f32(got), gen.bf16_to_f32(ref)) < 1e-2
+
+
+def test_combine():
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(6)
+    T, H, k = 50, 512, 10
+    yd = gen.f32_to_bf16(rng.standard_normal((T * k, H)).astype(np.float32))
+    ys = gen.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    wt = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    sg = rng.uniform(0, 1, T).astype(np.float32)
+    inv = rng.permutation(T * k).astype(np.int32)
+    x0 = gen.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    for assign in (True, False):
+        out = g.dev(x0)
+        ops.moe_combine(out, g.dev(yd), g.dev(wt), g.dev(ys), g.dev(sg), g.dev(inv), k, assign)
+        ref = orc.moe_combine(x0, yd, wt, ys, sg, inv, k, assign)
+        got = gen.bf16_to_f32(g.host(out))
+        assert gen.rel_err(got, gen.bf16_to_f32(ref)) < 1e-2
+
+
+def _ffn_case(T, E, H, I, k, shared_gate, seed):
+    g, ops = _gu(), _ops()
+    egu = experts(E, 2 * I, H, seed=seed)
+    edn = experts(E, H, I, seed=seed + 1)
+    sgu = experts(1, 2 * I, H, seed=seed + 2)
+    sdn = experts(1, H, I, seed=seed + 3)
+    R = router(E + (1 if shared_gate else 0), H, seed=seed + 4)
+    xn = gen.activations(T, H, seed=seed + 5)
+    shared = (g.qlinear(sgu[0][0], sgu[1][0], sgu[2][0]), g.qlinear(sdn[0][0], sdn[1][0], sdn[2][0]))
+    out, idx, wt, sg = ops.moe_ffn(g.dev(xn), g.dev(R), g.moew(*egu), g.moew(*edn), k, shared=shared,
+                                   shared_gate=shared_gate, logits_bf16=T >= 64)
+    torch.cuda.synchronize()
+    # routing on the GPU's own logits must be bit-exact
+    logits = ops.moe_router_logits(g.dev(xn), g.dev(R), out_bf16=T >= 64)
+    ri, rw, rs = orc.moe_route(g.host(logits), E, k, shared_gate=shared_gate)
+    assert np.array_equal(g.host(idx), ri)
+    assert np.allclose(g.host(wt), rw, rtol=1e-5, atol=1e-7)
+    ref = orc.moe_experts(xn, ri, rw, rs, egu, edn,
+                          ((sgu[0][0], sgu[1][0], sgu[2][0]), (sdn[0][0], sdn[1][0], sdn[2][0])), I)
+    err = gen.rel_err(gen.bf16_to_f32(g.host(out)), gen.bf16_to_f32(ref))
+    assert err < 1e-2, err
+
+
+@pytest.mark.parametrize("T,shared_gate", [(16, True), (128, False)])
+def test_moe_ffn_baseline_geometry(T, shared_gate):
+    """BASELINE config 4 geometry: H=2048, E=512, top-10, I=512, plus a shared expert."""
+    _ffn_case(T, 512, 2048, 512, 10, shared_gate, seed=80 + T)
+
+
+def test_moe_ffn_t2048():
+    """BASELINE config 4 at T=2048: within tolerance of the CPU reference (the north star's MoE bar)."""
+    _ffn_case(2048, 512, 2048, 512, 10, False, seed=90)
+
+
+def test_moe_ffn_small_odd():
+    _ffn_case(5, 8, 128, 64, 2, True, seed=95)
