@@ -61,7 +61,7 @@ def lib():
         L.orc_moe_combine.argtypes = [_u16p, _u16p, _f32p, _vp, _f32p, _i32p, _i, _i, _i, _i]
         L.orc_moe_experts.argtypes = [_u16p, _i, _i, _i, _i, _i, _i32p, _f32p, _f32p,
                                       _u32p, _u16p, _u16p, _u32p, _u16p, _u16p,
-                                      _vp, _vp, _vp, _vp, _vp, _vp, _u16p, _i, _i]
+                                      _vp, _vp, _vp, _vp, _vp, _vp, _i, _u16p, _i, _i]
         _lib = L
     return _lib
 
@@ -243,10 +243,12 @@ def moe_combine(x, yd, wt, ys, sg, inv, k: int, assign: bool) -> np.ndarray:
     return out
 
 
-def moe_experts(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: bool = True, nthreads: int = 0):
+def moe_experts(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: bool = True, nthreads: int = 0,
+                shared_qmv: bool = False):
     """Sorted-path MoE FFN composition (engine/src/qwen35.h:1869-1980) for given routing.
 
     egu / edn / shared: tuples (wq, s, b) — routed stacks [E, 2I, H/8] and [E, H, I/8]; shared = ((gu), (dn)) or None.
+    shared_qmv: the shared expert's dense GEMMs take the decode GEMV semantics (else qmm's).
     """
     xn = _c(xn, np.uint16)
     T, H = xn.shape
@@ -272,5 +274,5 @@ def moe_experts(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: boo
     lib().orc_moe_experts(xn, T, H, I, E, k, idx, _c(wt, np.float32), _c(sg, np.float32),
                           _c(egu[0], np.uint32), _c(egu[1], np.uint16), _c(egu[2], np.uint16),
                           _c(edn[0], np.uint32), _c(edn[1], np.uint16), _c(edn[2], np.uint16),
-                          *sh, o, 1 if assign else 0, nthreads)
+                          *sh, 1 if shared_qmv else 0, o, 1 if assign else 0, nthreads)
     return o

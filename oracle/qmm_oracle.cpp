@@ -352,24 +352,25 @@ void orc_moe_combine(uint16_t* x, const uint16_t* yd, const float* wt, const uin
 }
 
 // The MoE FFN composition (engine/src/qwen35.h:1869-1980, sorted path): given routing (idx, wt, sg) for T tokens,
-// shared expert (dense gate_up [2I, H] and down [H, I], qmm semantics) -> ys; dispatch; gathered gate/up qmm ->
-// SwiGLU -> gathered down qmm -> combine. Writes out bf16 [T, H] (assign) or adds into it (assign == 0).
-// Shared weights may be null (no shared expert).
+// shared expert (dense gate_up [2I, H] and down [H, I], through Qwen35::gemm: the decode GEMV semantics when
+// shared_qmv != 0, else qmm's) -> ys; dispatch; gathered gate/up qmm -> SwiGLU -> gathered down qmm -> combine.
+// Writes out bf16 [T, H] (assign) or adds into it (assign == 0). Shared weights may be null (no shared expert).
 void orc_moe_experts(const uint16_t* xn, int T, int H, int I, int E, int k, const int* idx, const float* wt,
                      const float* sg, const uint32_t* gu_wq, const uint16_t* gu_s, const uint16_t* gu_b,
                      const uint32_t* dn_wq, const uint16_t* dn_s, const uint16_t* dn_b, const uint32_t* sh_gu_wq,
                      const uint16_t* sh_gu_s, const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq, const uint16_t* sh_dn_s,
-                     const uint16_t* sh_dn_b, uint16_t* out, int assign, int nthreads) {
+                     const uint16_t* sh_dn_b, int shared_qmv, uint16_t* out, int assign, int nthreads) {
   const int R = T * k;
   std::vector<uint16_t> ys;
   if (sh_gu_wq) {
+    auto dense = shared_qmv ? orc_qmv : orc_qmm;
     std::vector<float> y((size_t)T * 2 * I);
-    orc_qmm(xn, H, sh_gu_wq, sh_gu_s, sh_gu_b, 2 * I, H, 0, y.data(), T, nthreads);
+    dense(xn, H, sh_gu_wq, sh_gu_s, sh_gu_b, 2 * I, H, 0, y.data(), T, nthreads);
     std::vector<uint16_t> gu((size_t)T * 2 * I), act((size_t)T * I);
     for (size_t i = 0; i < y.size(); i++) gu[i] = f2bf(y[i]);
     orc_silu_mul(gu.data(), act.data(), I, T);
     std::vector<float> yd((size_t)T * H);
-    orc_qmm(act.data(), I, sh_dn_wq, sh_dn_s, sh_dn_b, H, I, 0, yd.data(), T, nthreads);
+    dense(act.data(), I, sh_dn_wq, sh_dn_s, sh_dn_b, H, I, 0, yd.data(), T, nthreads);
     ys.resize((size_t)T * H);
     for (size_t i = 0; i < yd.size(); i++) ys[i] = f2bf(yd[i]);
   }

@@ -62,3 +62,19 @@ def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
     ref = np.asarray(ref, np.float64)
     rms = float(np.sqrt(np.mean(ref * ref))) or 1.0
     return float(np.max(np.abs(np.asarray(got, np.float64) - ref))) / rms
+
+
+def bf16_ulp(v: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 values at |v| (8 significant bits)."""
+    a = np.maximum(np.abs(np.asarray(v, np.float64)), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(a)) - 7)
+
+
+def bf16_err(got_bf16: np.ndarray, ref: np.ndarray, ref_is_bf16: bool = False) -> float:
+    """BASELINE's max |err| / RMS(ref) for a bf16 output, net of the output's own quantization: each element may sit
+    half a bf16 step from an fp32 reference (one step from a reference that is itself bf16-rounded)."""
+    got = bf16_to_f32(got_bf16).astype(np.float64)
+    r = bf16_to_f32(ref).astype(np.float64) if ref_is_bf16 else np.asarray(ref, np.float64)
+    rms = float(np.sqrt(np.mean(r * r))) or 1.0
+    slack = bf16_ulp(r) * (1.0 if ref_is_bf16 else 0.5)
+    return float(np.max(np.maximum(np.abs(got - r) - slack, 0.0))) / rms
