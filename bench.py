@@ -1,0 +1,279 @@
+"""Benchmark of the MI355X W4 quantized-matmul hot path (one JSON line on stdout).
+
+Headline workload ("batched-agent decode MLP"): one step runs the decode MLP at each
+M in {1, 8, 32, 128}: A[M, 5120] -> gate_up (4-bit, N = 2 x 17408, K = 5120) -> SwiGLU -> down (4-bit, N = 5120,
+K = 17408), all through the C ABI (libinferd_amd.so). Weights are seeded synthetic MLX-affine 4-bit group-64
+(q ~ U{0..15}, s ~ U(0.005, 0.02) bf16, b = bf16(-8 s)); activations bf16 N(0, 1). Weight copies are rotated so the
+timed loop streams >= 3x the 256 MB Infinity Cache, as the reference cycles copies (engine/tools/moe_bench.mm:4-5).
+
+value = algorithmic HBM bytes of the step / step time (GB/s): 150,405,120 weight bytes per M plus 229,376 activation
+bytes per row (A, the gate/up output written and read, the SwiGLU output written and read, the result).
+The other BASELINE configs are reported under "breakdown" (prefill TFLOP/s, W4A8 TOPS, MoE tok/s, config-0 GB/s).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0
+LLC_BYTES = 256 << 20
+
+H_DEC, I_DEC = 5120, 17408
+W_BYTES_PER_WEIGHT = 0.5625  # packed nibbles + bf16 scale and bias per 64
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--no-breakdown", action="store_true", help="headline workload only")
+    p.add_argument("--only", default="", help="profiling: run one config only (c0, c1, c2, c3, c4)")
+    return p.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU design is in DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from inferd_amd import ops
+    from inferd_amd.ops import MoeW, QLinear
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+
+    def qlin(N, K):
+        wq = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 8), dtype=torch.int32, device=dev, generator=gen)
+        s = (torch.rand((N, K // 64), device=dev, generator=gen) * 0.015 + 0.005).to(torch.bfloat16)
+        b = (-8.0 * s.float()).to(torch.bfloat16)
+        return QLinear(wq, s, b, N, K)
+
+    def copies_for(nbytes):
+        return max(1, -(-3 * LLC_BYTES // nbytes))
+
+    def act(M, K, scale_rows=False):
+        x = torch.randn((M, K), device=dev, generator=gen)
+        if scale_rows:
+            x = x * (torch.rand((M, 1), device=dev, generator=gen) * 1.5 + 0.5)
+        return x.to(torch.bfloat16)
+
+    def timed(fn, n, warm):
+        for i in range(warm):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n  # ms per call
+
+    out = {}
+    Ms = (1, 8, 32, 128)
+
+    # ---- headline: decode MLP (config 1) -----------------------------------------------------------------------
+    if args.only in ("", "c1"):
+        w_bytes = (2 * I_DEC * H_DEC + H_DEC * I_DEC) * W_BYTES_PER_WEIGHT
+        ncp = copies_for(int(w_bytes))
+        layers = [(qlin(2 * I_DEC, H_DEC), qlin(H_DEC, I_DEC)) for _ in range(ncp)]
+        A = {M: act(M, H_DEC) for M in Ms}
+        GU = {M: torch.empty((M, 2 * I_DEC), dtype=torch.bfloat16, device=dev) for M in Ms}
+        Hh = {M: torch.empty((M, I_DEC), dtype=torch.bfloat16, device=dev) for M in Ms}
+        Y = {M: torch.empty((M, H_DEC), dtype=torch.bfloat16, device=dev) for M in Ms}
+
+        def mlp(M, i):
+            gu, dn = layers[i % ncp]
+            ops.gemm(A[M], gu, GU[M])
+            ops.silu_mul(GU[M], out=Hh[M])
+            ops.gemm(Hh[M], dn, Y[M])
+
+        def step(i):
+            for M in Ms:
+                mlp(M, i)
+
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            step(i)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_step = e0.elapsed_time(e1) / args.steps
+        step_bytes = sum(w_bytes + M * 229376 for M in Ms)
+        value = step_bytes / (ms_step * 1e-3) / 1e9
+
+        # per-call timing (HIP events on the launch stream): the dominant call is the roofline kernel
+        calls = {}
+        for M in Ms:
+            gu_b = 2 * I_DEC * H_DEC * W_BYTES_PER_WEIGHT + M * H_DEC * 2 + M * 2 * I_DEC * 2
+            dn_b = H_DEC * I_DEC * W_BYTES_PER_WEIGHT + M * I_DEC * 2 + M * H_DEC * 2
+            ms_gu = timed(lambda i: ops.gemm(A[M], layers[i % ncp][0], GU[M]), args.steps * 2, 3)
+            ms_dn = timed(lambda i: ops.gemm(Hh[M], layers[i % ncp][1], Y[M]), args.steps * 2, 3)
+            calls[f"gate_up_M{M}"] = (ms_gu, gu_b, 2.0 * M * 2 * I_DEC * H_DEC)
+            calls[f"down_M{M}"] = (ms_dn, dn_b, 2.0 * M * H_DEC * I_DEC)
+        dom = max(calls, key=lambda k: calls[k][0])
+        ms_d, b_d, f_d = calls[dom]
+        achieved = b_d / (ms_d * 1e-3) / 1e9
+        out["headline"] = dict(ms_step=ms_step, value=value, step_bytes=step_bytes, copies=ncp)
+        out["dominant"] = dict(name=dom, ms=ms_d, bytes=b_d, flops=f_d, gbs=achieved,
+                               tflops=f_d / (ms_d * 1e-3) / 1e12)
+        out["per_M"] = {
+            f"M{M}": dict(
+                gate_up_us=calls[f"gate_up_M{M}"][0] * 1e3, down_us=calls[f"down_M{M}"][0] * 1e3,
+                gate_up_gbs=calls[f"gate_up_M{M}"][1] / (calls[f"gate_up_M{M}"][0] * 1e-3) / 1e9,
+                down_gbs=calls[f"down_M{M}"][1] / (calls[f"down_M{M}"][0] * 1e-3) / 1e9)
+            for M in Ms}
+        host_layer = (layers[0][0], layers[0][1])
+        del layers
+    else:
+        host_layer = None
+
+    breakdown = {}
+    if not args.no_breakdown or args.only:
+        # ---- config 0: single qmv M=1, K=N=5120 ---------------------------------------------------------------
+        if args.only in ("", "c0"):
+            nb = int(5120 * 5120 * W_BYTES_PER_WEIGHT)
+            ncp = copies_for(nb)
+            Ws = [qlin(5120, 5120) for _ in range(ncp)]
+            A0 = act(1, 5120)
+            C0 = torch.empty((1, 5120), dtype=torch.bfloat16, device=dev)
+            ms = timed(lambda i: ops.gemm(A0, Ws[i % ncp], C0), 200, 20)
+            byts = nb + 5120 * 2 * 2
+            breakdown["c0_qmv_M1"] = dict(us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9,
+                                          frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, copies=ncp)
+            del Ws
+        # ---- config 2: prefill qmm M=4096, K=5120, N=17408 ----------------------------------------------------
+        if args.only in ("", "c2"):
+            W2 = [qlin(17408, 5120) for _ in range(2)]
+            A2 = act(4096, 5120, scale_rows=True)
+            C2 = torch.empty((4096, 17408), dtype=torch.bfloat16, device=dev)
+            ms = timed(lambda i: ops.gemm(A2, W2[i % 2], C2), 10, 2)
+            fl = 2.0 * 4096 * 17408 * 5120
+            breakdown["c2_qmm_M4096"] = dict(us=ms * 1e3, tflops=fl / (ms * 1e-3) / 1e12,
+                                             frac_bf16=fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS)
+            del W2, A2, C2
+        # ---- config 3: W4A8 M=2048, K=N=5120, per-token int8 --------------------------------------------------
+        if args.only in ("", "c3"):
+            W3 = [qlin(5120, 5120) for _ in range(4)]
+            A3 = act(2048, 5120)
+            U3, XS3 = ops.a8_quant(A3, True)
+            C3 = torch.empty((2048, 5120), dtype=torch.bfloat16, device=dev)
+            ms = timed(lambda i: ops.qmm_w4a8(U3, XS3, True, W3[i % 4], C3), 20, 3)
+            ms_q = timed(lambda i: ops.a8_quant(A3, True), 20, 3)
+            op = 2.0 * 2048 * 5120 * 5120
+            breakdown["c3_w4a8_M2048"] = dict(us=ms * 1e3, tops=op / (ms * 1e-3) / 1e12,
+                                              frac_int8=op / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+                                              a8_quant_us=ms_q * 1e3)
+            del W3
+        # ---- config 4: MoE FFN H=2048, E=512, top-10, I=512, + shared expert ----------------------------------
+        if args.only in ("", "c4"):
+            E, H, I, k = 512, 2048, 512, 10
+
+            def moew(N, K):
+                q = qlin(E * N, K)
+                return MoeW(q.wq.view(E, N, K // 8), q.s.view(E, N, K // 64), q.b.view(E, N, K // 64), E, N, K)
+
+            ncp = 2
+            lay = [(moew(2 * I, H), moew(H, I), qlin(2 * I, H), qlin(H, I)) for _ in range(ncp)]
+            router = (torch.randn((E, H), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+            moe = {}
+            for T in (16, 128, 2048):
+                xn = act(T, H)
+                outb = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+
+                def run(i):
+                    egu, edn, sgu, sdn = lay[i % ncp]
+                    ops.moe_ffn(xn, router, egu, edn, k, shared=(sgu, sdn), shared_gate=False,
+                                logits_bf16=T >= 64, out=outb)
+
+                ms = timed(run, 10, 3)
+                moe[f"T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3))
+            breakdown["c4_moe"] = moe
+            del lay
+
+    if breakdown:
+        out["breakdown"] = breakdown
+
+    # ---- CPU baseline: the oracle on this host's cores, bounded sample ---------------------------------------------
+    cpu = None
+    if not args.no_cpu and host_layer is not None:
+        from oracle import oracle as orc
+        ncores = len(os.sched_getaffinity(0))
+        gu, dn = host_layer
+
+        def h16(t):
+            return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+        def h32(t):
+            return t.detach().cpu().numpy().view(np.uint32)
+
+        gw = (h32(gu.wq), h16(gu.s), h16(gu.b))
+        dw = (h32(dn.wq), h16(dn.s), h16(dn.b))
+        # sample: the full decode MLP at M = 1 and M = 8 (the oracle's qmv semantics), all weights streamed
+        sample_M = (1, 8)
+        rng = np.random.default_rng(0)
+        t0 = time.perf_counter()
+        nbytes = 0
+        for M in sample_M:
+            Ah = orc.f32_to_bf16(rng.standard_normal((M, H_DEC)).astype(np.float32))
+            gy = orc.qmv(Ah, *gw, nthreads=ncores)
+            hh = orc.silu_mul(orc.f32_to_bf16(gy))
+            orc.qmv(hh, *dw, nthreads=ncores)
+            nbytes += (2 * I_DEC * H_DEC + H_DEC * I_DEC) * W_BYTES_PER_WEIGHT + M * 229376
+        dt = time.perf_counter() - t0
+        cpu = dict(value=nbytes / dt / 1e9, unit="GB/s", cores=ncores, kind="port",
+                   sample=f"decode MLP at M={sample_M} (gate_up 5120->34816, SwiGLU, down 17408->5120), "
+                          f"oracle qmv semantics, {ncores} threads, {dt:.2f} s")
+
+    line = {
+        "metric": "W4 qmatmul HBM GB/s at decode M<=128; TFLOP/s at prefill M=4096; MoE tok/s",
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded 4-bit affine weights, bf16 N(0,1) activations)",
+    }
+    if "headline" in out:
+        h, d = out["headline"], out["dominant"]
+        line.update({
+            "value": round(h["value"], 1),
+            "ms_per_step": round(h["ms_step"], 4),
+            "config": {"workload": "decode MLP (BASELINE config 1): M in {1,8,32,128}, gate_up 5120->34816, "
+                                   "SwiGLU, down 17408->5120, 4-bit g64 weights", "weight_copies": h["copies"]},
+            "roofline": {"kernel": d["name"], "bound": "hbm", "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                         "us": round(d["ms"] * 1e3, 2), "tflops": round(d["tflops"], 1)},
+            "per_M": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in out["per_M"].items()},
+        })
+    if cpu:
+        line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()}
+    if "breakdown" in out:
+        line["breakdown"] = json.loads(json.dumps(out["breakdown"]), parse_float=lambda x: round(float(x), 4))
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -84,9 +84,9 @@ def flip(W: QLinear) -> None:
     W.flipped = not W.flipped
 
 
-def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+def silu_mul(gu: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     R, I2 = gu.shape
-    h = torch.empty((R, I2 // 2), dtype=torch.bfloat16, device=gu.device)
+    h = torch.empty((R, I2 // 2), dtype=torch.bfloat16, device=gu.device) if out is None else out
     check(lib().ifd_silu_mul(_p(gu), _p(h), I2 // 2, R, _stream()))
     return h
 
