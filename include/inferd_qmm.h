@@ -72,6 +72,19 @@ int ifd_flip_w4(uint32_t* wq, size_t n32, uint32_t mask, void* stream);
  * (reference silu_mul, core.metal:777-787; moe_silu_mul, moe.metal:103-111). */
 int ifd_silu_mul(const void* gu, void* h, int I, int rows, void* stream);
 
+/* ---- T64: the MI355X weight layout (no counterpart in the reference; its role is that of the reference's
+ * load-time weight transforms, flip and the lane4/qmst copies, qwen35.h:1209-1322) -------------------------------
+ * A one-time repack of the MLX layout into 1152-byte tiles (per 64-group and 32-column band: the codes in MFMA
+ * fragment order + the (s, b) pairs), group-major, so that decode streams HBM in 1 KB contiguous wave loads.
+ * Same size as the source (0.5625 B per weight); E stacked experts are packed expert by expert. */
+size_t ifd_t64_bytes(int N, int K, int E);
+int ifd_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr, int E,
+                 void* out, void* stream);
+size_t ifd_gemm_t64_workspace(int M, int N, int K);
+/* C (mode) = A . W^T with W in T64 layout (K % 256 == 0). */
+int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                 void* workspace, size_t ws_bytes, void* stream);
+
 /* ---- W4A8 (reference a8_quant + w4a8_gemm, w4a8.metal:24-98; host w4a8, qwen35.h:1323-1366) ------------------ */
 
 /* Activation quantizer: U int8 [M][K], XS float [M][K/64][2] = (sx, sx * sum xq) per row and group.

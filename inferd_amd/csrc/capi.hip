@@ -3,6 +3,7 @@
 
 #include "host.h"
 #include "kernels.h"
+#include "t64.h"
 
 using namespace ifd;
 
@@ -106,6 +107,38 @@ int ifd_qmm_w4a8(const int8_t* U, const float* XS, int per_token, const uint32_t
   IFD_CHECK(M == 0 || XS, "null XS");
   g.XS = XS;
   return launch_w4a8(g, per_token ? 1 : 0, workspace, ws_bytes, S(stream));
+}
+
+// ---- T64 layout ------------------------------------------------------------------------------------------------
+size_t ifd_t64_bytes(int N, int K, int E) {
+  if (N <= 0 || K <= 0 || K % 64 || E <= 0) return 0;
+  return (size_t)E * t64_bytes(N, K);
+}
+
+int ifd_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr, int E,
+                 void* out, void* stream) {
+  IFD_CHECK(N > 0 && K > 0 && K % 64 == 0 && E > 0, "bad shape N=%d K=%d E=%d", N, K, E);
+  IFD_CHECK(ldk == 0 || (ldk >= K && ldk % 64 == 0), "ldk=%d must be 0 or a multiple of 64 >= K", ldk);
+  IFD_CHECK(xr == 0u || xr == 0x88888888u, "xr=0x%x must be 0 or 0x88888888", xr);
+  IFD_CHECK(wq && s && b && out && aligned(out, 16), "null or misaligned pointer");
+  return launch_pack_t64(wq, s, b, N, K, ldk ? ldk : K, xr, E, out, S(stream));
+}
+
+size_t ifd_gemm_t64_workspace(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  return M <= 16 ? qmv_t_workspace(M, N, K) : gemm_t_workspace(M, N, K);
+}
+
+int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                 void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(M >= 0 && N > 0 && K > 0 && K % 256 == 0, "bad shape M=%d N=%d K=%d (K multiple of 256)", M, N, K);
+  IFD_CHECK(mode >= 0 && mode <= 2, "mode=%d must be 0, 1 or 2", mode);
+  IFD_CHECK(lda >= K && lda % 8 == 0 && ldc >= N, "bad strides lda=%d ldc=%d", lda, ldc);
+  if (M == 0) return IFD_OK;
+  IFD_CHECK(A && wt && C && aligned(A, 16) && aligned(wt, 16), "null or misaligned pointer");
+  if (M <= 16)
+    return launch_qmv_t((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, workspace, ws_bytes, S(stream));
+  return launch_gemm_t((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, workspace, ws_bytes, S(stream));
 }
 
 int ifd_moe_router_logits(const void* x, const void* w, int T, int H, int E1, int out_bf16, void* logits,

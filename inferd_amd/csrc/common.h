@@ -47,6 +47,26 @@ __device__ __forceinline__ u32x4 codes_bf16_off128(uint32_t w) {
   return r;
 }
 
+// Eight 4-bit codes of one word as eight bf16 values (128 + q) in the paired k order (0,4,1,5,2,6,3,7): one
+// v_and_or_b32 (+ one shift) per pair. The activation fragment must use the same order (see perm_pairs04).
+__device__ __forceinline__ u32x4 codes_bf16_off128_p04(uint32_t w) {
+  u32x4 r;
+  r[0] = (w & 0x000F000Fu) | 0x43004300u;          // (q0, q4)
+  r[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;   // (q1, q5)
+  r[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;   // (q2, q6)
+  r[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;  // (q3, q7)
+  return r;
+}
+// Eight consecutive bf16 values (x0..x7) reordered to (x0,x4,x1,x5,x2,x6,x3,x7).
+__device__ __forceinline__ u32x4 perm_pairs04(u32x4 v) {
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+  r[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+  r[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+  r[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+  return r;
+}
+
 // Eight 4-bit codes of one word as eight int8 values 0..15 in natural k order (two dwords).
 __device__ __forceinline__ u32x2 codes_i8(uint32_t w) {
   const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;

@@ -35,6 +35,16 @@ int launch_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows, hipStream_
 // Split-K reduction: C (mode) = sum over S partials [S][M][N] fp32.
 int launch_splitk_reduce(const float* part, int S, int M, int N, void* C, int ldc, int mode, hipStream_t st);
 
+// T64 layout (t64.h).
+int launch_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr,
+                    int E, void* out, hipStream_t st);
+size_t qmv_t_workspace(int M, int N, int K);
+size_t gemm_t_workspace(int M, int N, int K);
+int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                  void* ws, size_t ws_bytes, hipStream_t st);
+int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode, void* ws,
+                 size_t ws_bytes, hipStream_t st);
+
 // MoE.
 int launch_router_logits(const uint16_t* x, const uint16_t* w, int T, int H, int E1, int out_bf16, void* logits,
                          hipStream_t st);

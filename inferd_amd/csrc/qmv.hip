@@ -58,13 +58,14 @@ __global__ __launch_bounds__(256) void k_qmv_affine(QmvArgs p) {
 
   f32x16 acc = zero16();
   u32x4 wbuf[kQmvPF];
-  uint32_t sbuf[kQmvPF];
+  uint16_t sbuf[kQmvPF], bbuf[kQmvPF];  // raw bf16 bits: converted at use so the loads stay in flight
 #pragma unroll
   for (int i = 0; i < kQmvPF; i++) {
     const int g = g0 + i;
     if (g < g1) {
       wbuf[i] = *(const u32x4*)(wrow + (size_t)g * 8);
-      sbuf[i] = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
+      sbuf[i] = srow[g];
+      bbuf[i] = brow[g];
     }
   }
   for (int gb = g0; gb < g1; gb += kQmvPF) {
@@ -73,10 +74,11 @@ __global__ __launch_bounds__(256) void k_qmv_affine(QmvArgs p) {
       const int g = gb + i;
       if (g >= g1) break;
       const u32x4 wv = wbuf[i];
-      const uint32_t sb = sbuf[i];
+      const uint16_t sraw = sbuf[i], braw = bbuf[i];
       if (g + kQmvPF < g1) {
         wbuf[i] = *(const u32x4*)(wrow + (size_t)(g + kQmvPF) * 8);
-        sbuf[i] = (uint32_t)srow[g + kQmvPF] | ((uint32_t)brow[g + kQmvPF] << 16);
+        sbuf[i] = srow[g + kQmvPF];
+        bbuf[i] = brow[g + kQmvPF];
       }
       u32x4 af[4];
 #pragma unroll
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(256) void k_qmv_affine(QmvArgs p) {
         P = mfma_bf16(af[t], codes_bf16_off128(wv[t] ^ xr), P);
         X = mfma_bf16(af[t], ones, X);
       }
-      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16));
+      const float sc = bf2f(sraw), bi = bf2f(braw);
       const float bp = __builtin_fmaf(-128.f, sc, bi);
 #pragma unroll
       for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, X[r], acc[r]));
@@ -134,13 +136,14 @@ __global__ __launch_bounds__(256) void k_qmv_deq(QmvArgs p) {
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) acc[mt] = zero16();
   u32x4 wbuf[kQmvPF];
-  uint32_t sbuf[kQmvPF];
+  uint16_t sbuf[kQmvPF], bbuf[kQmvPF];  // raw bf16 bits: converted at use so the loads stay in flight
 #pragma unroll
   for (int i = 0; i < kQmvPF; i++) {
     const int g = g0 + i;
     if (g < g1) {
       wbuf[i] = *(const u32x4*)(wrow + (size_t)g * 8);
-      sbuf[i] = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
+      sbuf[i] = srow[g];
+      bbuf[i] = brow[g];
     }
   }
   for (int gb = g0; gb < g1; gb += kQmvPF) {
@@ -149,12 +152,13 @@ __global__ __launch_bounds__(256) void k_qmv_deq(QmvArgs p) {
       const int g = gb + i;
       if (g >= g1) break;
       const u32x4 wv = wbuf[i];
-      const uint32_t sb = sbuf[i];
+      const uint16_t sraw = sbuf[i], braw = bbuf[i];
       if (g + kQmvPF < g1) {
         wbuf[i] = *(const u32x4*)(wrow + (size_t)(g + kQmvPF) * 8);
-        sbuf[i] = (uint32_t)srow[g + kQmvPF] | ((uint32_t)brow[g + kQmvPF] << 16);
+        sbuf[i] = srow[g + kQmvPF];
+        bbuf[i] = brow[g + kQmvPF];
       }
-      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16));
+      const float sc = bf2f(sraw), bi = bf2f(braw);
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const u32x4 bfr = dequant8_bf16(wv[t] ^ xr, sc, bi);
@@ -181,6 +185,121 @@ __global__ __launch_bounds__(256) void k_qmv_deq(QmvArgs p) {
     }
 }
 
+// Small-M decode (M <= 16): the block's activation rows for its K range are staged once in LDS, reordered to the
+// (0,4,1,5,2,6,3,7) pair order of codes_bf16_off128_p04 (one and-or per code pair), together with their 64-group
+// sums X. Afterwards each wave only streams its weights (two 8-group blocks in flight per lane) and reads
+// activations from LDS, so the weight loads are the only vector-memory traffic in the main loop.
+// Requires K % 512 == 0, ldk % 512 == 0, 16-byte aligned scales/biases and splits of whole 8-group blocks.
+
+__device__ __forceinline__ size_t small_lds_x_offset(int M, int Kz) {
+  return ((size_t)M * (Kz + 8) * 2 + 15) / 16 * 16;  // bytes: A rows (Kz + 8 bf16 each), then X
+}
+
+template <int RACT>
+__global__ __launch_bounds__(256, 2) void k_qmv_small(QmvArgs p) {
+  extern __shared__ __align__(16) uint16_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+  const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps), Gz = g1 - g0;
+  const int Kz = Gz * kGroup, ldA = Kz + 8, M = p.M;
+  uint16_t* As = lds;
+  float* Xs = (float*)((char*)lds + small_lds_x_offset(M, Kz));  // [Gz][16]
+
+  // ---- stage A[0:M][g0*64 : g1*64] (pair-ordered) and the group sums
+  const int cpr = Kz / 8, total = M * cpr;  // 16-byte chunks; a multiple of 8 (one group = 8 chunks)
+  for (int c0 = 0; c0 < total; c0 += 256) {
+    const int c = c0 + tid;
+    const bool ok = c < total;
+    const int m = ok ? c / cpr : 0, kc = ok ? c % cpr : 0;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (ok) v = *(const u32x4*)(p.A + (size_t)m * p.lda + (size_t)g0 * kGroup + 8 * kc);
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) sum += bf2f((uint16_t)(v[e] & 0xFFFFu)) + bf2f((uint16_t)(v[e] >> 16));
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    if (ok) {
+      *(u32x4*)(As + (size_t)m * ldA + 8 * kc) = perm_pairs04(v);
+      if ((kc & 7) == 0) Xs[(kc >> 3) * 16 + m] = sum;
+    }
+  }
+  for (int i = tid; i < Gz * 16; i += 256)
+    if ((i & 15) >= M) Xs[i] = 0.f;
+  __syncthreads();
+
+  const int n0 = blockIdx.x * 128 + wave * 32;
+  if (n0 >= p.N) return;  // no barrier follows
+  const int n = min(n0 + j, p.N - 1);
+  const uint32_t* wrow = p.wq + (size_t)n * ldw + 4 * h;
+  const uint16_t* srow = p.s + (size_t)n * ldg;
+  const uint16_t* brow = p.b + (size_t)n * ldg;
+  const bool aok = j < M;
+  const uint16_t* arow = As + (size_t)(aok ? j : 0) * ldA + 32 * h;
+  const uint32_t xr = p.xr;
+
+  f32x16 acc = zero16();
+  // Ping-pong register blocks of 8 groups: 8 x 16 B of codes plus the 8 scales and 8 biases of this column as one
+  // 16 B vector each (ldg % 8 == 0, g0 % 8 == 0: checked by the host). Loads land where they are used, so the
+  // only waits are for a block issued one block earlier.
+  struct Blk {
+    u32x4 w[8];
+    u32x4 s, b;
+  };
+  auto load_blk = [&](Blk& B, int g) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) B.w[i] = *(const u32x4*)(wrow + (size_t)(g + i) * 8);
+    B.s = *(const u32x4*)(srow + g);
+    B.b = *(const u32x4*)(brow + g);
+  };
+  auto compute_blk = [&](const Blk& B, int g) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int gl = g + i - g0;
+      u32x4 af[4];
+      const uint16_t* ag = arow + (size_t)gl * 64;
+#pragma unroll
+      for (int t = 0; t < 4; t++) af[t] = aok ? *(const u32x4*)(ag + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+      const float4 x0 = *(const float4*)(Xs + gl * 16 + 4 * h);
+      float4 x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (RACT > 4) x1 = *(const float4*)(Xs + gl * 16 + 8 + 4 * h);
+      f32x16 P = zero16();
+#pragma unroll
+      for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], codes_bf16_off128_p04(B.w[i][t] ^ xr), P);
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      const float sc = bf2f((uint16_t)(B.s[i / 2] >> (16 * (i & 1))));
+      const float bi = bf2f((uint16_t)(B.b[i / 2] >> (16 * (i & 1))));
+      const float bp = __builtin_fmaf(-128.f, sc, bi);
+#pragma unroll
+      for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[r]));
+    }
+  };
+  // The prefetches are unconditional (the last block is re-read past the end) so that every path leaves the same
+  // number of loads outstanding and the waits can stay one block behind.
+  const int glast = g1 - 8;
+  Blk b0, b1;
+  load_blk(b0, g0);
+  for (int g = g0;; g += 16) {
+    load_blk(b1, min(g + 8, glast));
+    compute_blk(b0, g);
+    if (g + 8 >= g1) break;
+    load_blk(b0, min(g + 16, glast));
+    compute_blk(b1, g + 8);
+    if (g + 16 >= g1) break;
+  }
+  const int col = n0 + j;
+  if (col >= p.N) return;
+  const bool split = gridDim.y > 1;
+#pragma unroll
+  for (int r = 0; r < RACT; r++) {
+    const int row = 8 * (r / 4) + 4 * h + (r % 4);
+    if (row >= M) continue;
+    if (split) p.part[((size_t)blockIdx.y * M + row) * p.N + col] = acc[r];
+    else store_mode(p.C, (size_t)row * p.ldc + col, acc[r], p.mode);
+  }
+}
+
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, int S, int M, int N, void* C,
                                                        int ldc, int mode) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, mn = (size_t)M * N;
@@ -200,38 +319,58 @@ int launch_splitk_reduce(const float* part, int S, int M, int N, void* C, int ld
 
 // K splits for a decode GEMM: enough blocks (~2 per CU on 256 CUs) while every split keeps >= 4 groups and the
 // partials stay small (S * M <= 1024 rows, the reference's kSplitRows, qwen35.h:77).
-static int qmv_splits(int M, int N, int K) {
+// K split plan for a decode GEMM: enough blocks (~2 per CU on 256 CUs) while every split keeps >= 4 groups and the
+// partials stay small (S * M <= 1024 rows, the reference's kSplitRows, qwen35.h:77). With M <= 16 the staged
+// activations take at most ~40 KB of LDS per block, and when G % 8 == 0 splits hold whole 8-group blocks.
+struct QmvPlan {
+  int S, gps;
+};
+static QmvPlan qmv_plan(int M, int N, int K) {
   const int G = K / kGroup, bx = (N + 127) / 128;
-  int S = (512 + bx - 1) / bx;
-  S = std::min(S, std::max(1, G / 4));
-  S = std::min(S, std::max(1, 1024 / std::max(M, 1)));
-  if (S <= 1) return 1;
-  const int gps = (G + S - 1) / S;
-  return (G + gps - 1) / gps;
+  long S = (512 + bx - 1) / bx;
+  if (M <= 16) S = std::max<long>(S, ((long)M * K * 2 + 40959) / 40960);
+  S = std::min<long>(S, std::max(1, G / 4));
+  S = std::min<long>(S, std::max(1, 1024 / std::max(M, 1)));
+  int gps = (int)((G + S - 1) / S);
+  if (M <= 16 && G % 8 == 0) gps = (gps + 7) / 8 * 8;
+  return QmvPlan{(G + gps - 1) / gps, gps};
 }
 
 size_t qmv_workspace(int M, int N, int K) {
-  const int S = qmv_splits(M, N, K);
-  return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+  const QmvPlan pl = qmv_plan(M, N, K);
+  return pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
 }
 
 int launch_qmv(const W4Gemm& g, void* ws, size_t ws_bytes, hipStream_t st) {
   if (g.M == 0) return IFD_OK;
   if (g.M > 128) return fail(IFD_ERR_ARG, "qmv path takes M <= 128 (M=%d)", g.M);
-  const int G = g.K / kGroup;
-  int S = qmv_splits(g.M, g.N, g.K);
+  const QmvPlan pl = qmv_plan(g.M, g.N, g.K);
+  const int S = pl.S, gps = pl.gps;
   const size_t need = S > 1 ? (size_t)S * g.M * g.N * sizeof(float) : 0;
   if (need > ws_bytes || (need && !ws))
     return fail(IFD_ERR_WORKSPACE, "qmv needs %zu bytes of workspace, got %zu", need, ws_bytes);
-  const int gps = (G + S - 1) / S;
   QmvArgs p{(const uint16_t*)g.A, g.lda, g.wq, g.s, g.b, g.N, g.K, g.ldk, g.xr, g.C, g.ldc, g.M, g.mode,
             (float*)ws, gps};
   dim3 grid((g.N + 127) / 128, S), block(256);
-  if (g.M <= 8) hipLaunchKernelGGL(k_qmv_affine<4>, grid, block, 0, st, p);
-  else if (g.M <= 16) hipLaunchKernelGGL(k_qmv_affine<8>, grid, block, 0, st, p);
-  else if (g.M <= 32) hipLaunchKernelGGL(k_qmv_affine<16>, grid, block, 0, st, p);
-  else if (g.M <= 64) hipLaunchKernelGGL(k_qmv_deq<2>, grid, block, 0, st, p);
-  else hipLaunchKernelGGL(k_qmv_deq<4>, grid, block, 0, st, p);
+  const bool small_ok = g.M <= 16 && g.K % 512 == 0 && g.ldk % 512 == 0 && gps % 8 == 0 && aligned(g.s, 16) &&
+                        aligned(g.b, 16);
+  if (small_ok) {
+    const int Kz = gps * kGroup;
+    const size_t lds = ((size_t)g.M * (Kz + 8) * 2 + 15) / 16 * 16 + (size_t)gps * 16 * sizeof(float);
+    if (lds > 64 * 1024) return fail(IFD_ERR_UNSUPPORTED, "qmv: %zu bytes of LDS needed", lds);
+    if (g.M <= 8) hipLaunchKernelGGL(k_qmv_small<4>, grid, block, lds, st, p);
+    else hipLaunchKernelGGL(k_qmv_small<8>, grid, block, lds, st, p);
+  } else if (g.M <= 8) {
+    hipLaunchKernelGGL(k_qmv_affine<4>, grid, block, 0, st, p);
+  } else if (g.M <= 16) {
+    hipLaunchKernelGGL(k_qmv_affine<8>, grid, block, 0, st, p);
+  } else if (g.M <= 32) {
+    hipLaunchKernelGGL(k_qmv_affine<16>, grid, block, 0, st, p);
+  } else if (g.M <= 64) {
+    hipLaunchKernelGGL(k_qmv_deq<2>, grid, block, 0, st, p);
+  } else {
+    hipLaunchKernelGGL(k_qmv_deq<4>, grid, block, 0, st, p);
+  }
   IFD_TRY(check_launch("qmv"));
   if (S > 1) return launch_splitk_reduce((const float*)ws, S, g.M, g.N, g.C, g.ldc, g.mode, st);
   return IFD_OK;

@@ -53,6 +53,35 @@ class QLinear:
 
 
 @dataclass
+class T64Linear:
+    """A linear [N, K] repacked into the T64 layout (inferd_amd/csrc/t64.h): a uint8 device buffer."""
+    wt: torch.Tensor
+    N: int
+    K: int
+
+
+def pack_t64(W: "QLinear") -> T64Linear:
+    """One-time repack of an MLX-layout linear into the T64 layout (undoes a flip)."""
+    nbytes = lib().ifd_t64_bytes(W.N, W.K, 1)
+    wt = torch.empty((nbytes,), dtype=torch.uint8, device=W.wq.device)
+    check(lib().ifd_pack_t64(_p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, W.xr, 1, _p(wt), _stream()))
+    return T64Linear(wt, W.N, W.K)
+
+
+def gemm_t64(A: torch.Tensor, W: T64Linear, C: Optional[torch.Tensor] = None, mode: int = 0) -> torch.Tensor:
+    """C (mode) = A . W^T for T64 weights."""
+    M, K = A.shape
+    assert K == W.K and A.dtype == torch.bfloat16 and A.is_contiguous()
+    if C is None:
+        C = torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=A.device)
+    need = lib().ifd_gemm_t64_workspace(M, W.N, W.K)
+    ws = workspace(need, A.device) if need else None
+    check(lib().ifd_gemm_t64(_p(A), K, _p(W.wt), W.N, W.K, _p(C), C.shape[1], M, mode, _p(ws),
+                             ws.numel() if ws is not None else 0, _stream()))
+    return C
+
+
+@dataclass
 class MoeW:
     """Stacked experts [E, N, K] in the same affine layout (engine/src/moe.h:8-11)."""
     wq: torch.Tensor

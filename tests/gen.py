@@ -78,3 +78,27 @@ def bf16_err(got_bf16: np.ndarray, ref: np.ndarray, ref_is_bf16: bool = False) -
     rms = float(np.sqrt(np.mean(r * r))) or 1.0
     slack = bf16_ulp(r) * (1.0 if ref_is_bf16 else 0.5)
     return float(np.max(np.maximum(np.abs(got - r) - slack, 0.0))) / rms
+
+
+T64_NIB = (0, 4, 1, 5, 2, 6, 3, 7)  # nibble of code e (e = 0..7) inside a T64 word
+
+
+def pack_t64(codes: np.ndarray, s: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """numpy restatement of the T64 layout (inferd_amd/csrc/t64.h) from unflipped codes [N, K]: uint8 bytes."""
+    N, K = codes.shape
+    G, nb = K // 64, (N + 31) // 32
+    cp = np.zeros((nb * 32, K), np.uint8)
+    cp[:N] = codes
+    sp = np.zeros((nb * 32, G), np.uint16)
+    bp = np.zeros((nb * 32, G), np.uint16)
+    sp[:N], bp[:N] = s, b
+    c = cp.reshape(nb, 32, G, 2, 4, 8).astype(np.uint32)  # band, j, g, h, t, e
+    words = np.zeros(c.shape[:-1], np.uint32)
+    for e in range(8):
+        words |= c[..., e] << np.uint32(4 * T64_NIB[e])
+    w = np.ascontiguousarray(words.transpose(2, 0, 3, 1, 4))  # g, band, h, j, t  (lane = 32 h + j)
+    sb = (sp.astype(np.uint32) | (bp.astype(np.uint32) << np.uint32(16))).reshape(nb, 32, G).transpose(2, 0, 1)
+    out = np.zeros((G, nb, 1152), np.uint8)
+    out[:, :, :1024] = w.reshape(G, nb, 256).view(np.uint8).reshape(G, nb, 1024)
+    out[:, :, 1024:] = np.ascontiguousarray(sb).view(np.uint8).reshape(G, nb, 128)
+    return out.reshape(-1)

@@ -1,0 +1,114 @@
+"""GPU checks of the T64 weight layout: the repack is bit-exact against a numpy restatement of the layout, and
+GEMMs on T64 weights match the CPU oracle (decode GEMV semantics) through the C ABI."""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import gen
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _gu():
+    from tests import gpu_util
+    return gpu_util
+
+
+def _ops():
+    from inferd_amd import ops
+    return ops
+
+
+@pytest.mark.parametrize("N,K,flipped", [(64, 256, False), (200, 512, True), (5120, 1024, False)])
+def test_pack_t64_bit_exact(N, K, flipped):
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear(N, K, seed=N + K, bias="free")
+    W = g.qlinear(wq ^ np.uint32(0x88888888) if flipped else wq, s, b, flipped)
+    T = ops.pack_t64(W)
+    torch.cuda.synchronize()
+    assert np.array_equal(g.host(T.wt), gen.pack_t64(codes, s, b))
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 16])
+@pytest.mark.parametrize("N,K", [(200, 512), (5120, 5120), (384, 17408)])
+def test_gemm_t64_decode(M, N, K):
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear(N, K, seed=M * 7 + N)
+    A = gen.activations(M, K, seed=M + K)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    out = g.host(ops.gemm_t64(g.dev(A), T))
+    Y = orc.qmv(A, wq, s, b)
+    err = gen.bf16_err(out, Y)
+    assert err <= 1e-2, (M, N, K, err)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_gemm_t64_modes(mode):
+    g, ops = _gu(), _ops()
+    M, N, K = 4, 256, 1024
+    codes, wq, s, b = gen.qlinear(N, K, seed=mode)
+    A = gen.activations(M, K, seed=mode + 1)
+    C0 = gen.activations(M, N, seed=mode + 2)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    out = g.host(ops.gemm_t64(g.dev(A), T, g.dev(C0) if mode == 1 else None, mode=mode))
+    Y = orc.qmv(A, wq, s, b)
+    err = gen.rel_err(out, Y) if mode == 2 else gen.bf16_err(out, Y + gen.bf16_to_f32(C0))
+    assert err <= 1e-2, err
+
+
+def _t64_semantics(M):
+    """The T64 GEMM's arithmetic by M: exact affine (decode GEMV) up to 64 rows, bf16 dequant (MLX qmm) above."""
+    return orc.qmv if M <= 64 else orc.qmm
+
+
+@pytest.mark.parametrize("M", [17, 32, 33, 64, 65, 128, 129, 300])
+@pytest.mark.parametrize("N,K", [(200, 512), (1024, 2048)])
+def test_gemm_t64_rows(M, N, K):
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear(N, K, seed=M + N + K)
+    A = gen.activations(M, K, seed=M)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    out = g.host(ops.gemm_t64(g.dev(A), T))
+    err = gen.bf16_err(out, _t64_semantics(M)(A, wq, s, b))
+    assert err <= 1e-2, (M, N, K, err)
+
+
+@pytest.mark.parametrize("M,mode", [(40, 1), (128, 2), (260, 1)])
+def test_gemm_t64_big_modes(M, mode):
+    g, ops = _gu(), _ops()
+    N, K = 320, 1024
+    codes, wq, s, b = gen.qlinear(N, K, seed=M + mode)
+    A = gen.activations(M, K, seed=M + 5)
+    C0 = gen.activations(M, N, seed=M + 6)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    out = g.host(ops.gemm_t64(g.dev(A), T, g.dev(C0) if mode == 1 else None, mode=mode))
+    Y = _t64_semantics(M)(A, wq, s, b)
+    err = gen.rel_err(out, Y) if mode == 2 else gen.bf16_err(out, Y + gen.bf16_to_f32(C0))
+    assert err <= 1e-2, err
+
+
+@pytest.mark.parametrize("M", [32, 128])
+def test_gemm_t64_decode_mlp_sampled(M):
+    """BASELINE config 1 shapes on T64 weights (oracle on 8 sampled rows)."""
+    g, ops = _gu(), _ops()
+    for (N, K, seed) in [(34816, 5120, 23), (5120, 17408, 24)]:
+        codes, wq, s, b = gen.qlinear(N, K, seed=seed)
+        A = gen.activations(M, K, seed=seed + M)
+        out = g.host(ops.gemm_t64(g.dev(A), ops.pack_t64(g.qlinear(wq, s, b))))
+        rows = np.unique(np.linspace(0, M - 1, 8).astype(int))
+        err = gen.bf16_err(out[rows], _t64_semantics(M)(A[rows], wq, s, b))
+        assert err <= 1e-2, (M, N, K, err)
+
+
+def test_gemm_t64_config2_sampled():
+    """BASELINE config 2 (M=4096, K=5120, N=17408) on T64 weights; oracle on 16 sampled rows."""
+    g, ops = _gu(), _ops()
+    M, N, K = 4096, 17408, 5120
+    codes, wq, s, b = gen.qlinear(N, K, seed=33)
+    A = gen.activations(M, K, seed=34, row_scale=True)
+    out = g.host(ops.gemm_t64(g.dev(A), ops.pack_t64(g.qlinear(wq, s, b))))
+    rows = np.linspace(0, M - 1, 16).astype(int)
+    err = gen.bf16_err(out[rows], orc.qmm(A[rows], wq, s, b))
+    assert err <= 1e-2, err
