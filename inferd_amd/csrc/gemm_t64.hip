@@ -1,0 +1,290 @@
+// GEMM on T64 weights for any M (decode batches above 16 rows and prefill): C (mode) = A . W^T.
+//
+// Replaces the reference's MLX affine_qmm_t_nax (third_party/mlx/.../quantized_nax.h:938-1076, 1206-1267) and its
+// split-K variant (engine/kernels/qmm_splitk.metal:14-107) for T64-packed weights.
+//
+// Block: 4 waves (one per SIMD); block tile BM = 32 MT rows x 4 NB bands (128 NB columns), each wave owning NB bands;
+// grid x = tiles (XCD-contiguous runs, bands of kGtBand M tiles walked M-fastest), grid y = K splits.
+// K advances in chunks of two 64-groups through a kGtNS-stage LDS ring filled by direct global->LDS DMA
+// (global_load_lds_dwordx4): per chunk the activation slab [BM][128 bf16] (16-byte columns XOR-swizzled by row so
+// that the MFMA fragment reads are bank-conflict free), the code halves of the two groups' T64 tiles of the block's
+// bands, and per wave one 1 KB area with the (s, b) dwords of its 2 NB tiles. Loads run kGtNS - 1 chunks ahead and
+// cost no VGPRs; each chunk needs one s_barrier.
+// Every DMA is issued by the full wave under uniform control flow: the LDS destination goes to M0, which is one value
+// per wave, and a DMA under a lane-dependent branch may be merged by the compiler with another one whose destination
+// differs, leaving one M0 for both.
+//  DEQ = false (affine): codes enter the MFMA as exact bf16 (128 + q); per group the fp32 epilogue adds
+//    s P + (b - 128 s) X, with X (the activation group sums) from a second MFMA against ones: the decode GEMV
+//    arithmetic (engine/kernels/core.metal:85-171).
+//  DEQ = true: codes are dequantized in registers to bf16(s q + b) (MLX qmm rounding, quantized.h:528-535) and
+//    accumulate over K; one dequant feeds MT MFMA tiles: the cheaper choice from 4 M tiles up.
+#include <algorithm>
+
+#include "common.h"
+#include "host.h"
+#include "kernels.h"
+#include "t64.h"
+
+namespace ifd {
+
+struct GemmTArgs {
+  const uint16_t* A;
+  int lda;
+  const uint8_t* wt;
+  int N, K;
+  void* C;
+  int ldc, M, mode;
+  float* part;
+  int gps;
+  int tiles_m, tiles_n;
+};
+
+constexpr int kGtBand = 4;  // M tiles per band of the tile order
+constexpr int kGtNS = 3;    // LDS pipeline stages
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
+}
+// Wait until at most N DMA/vector loads of this wave are outstanding and all its LDS reads are done, then barrier.
+// One asm statement with a memory clobber: the compiler may not move LDS accesses across it, and it adds no wait of
+// its own (a __syncthreads() would drain every outstanding DMA).
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ u32x4 t64_off128(uint32_t w) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; i++) r[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
+  return r;
+}
+// eight T64 codes (one word) -> bf16(s q + b) in natural k order
+__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float s, float b) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t pr = (w >> (4 * i)) & 0x000F000Fu;
+    r[i] = pack_bf2(__builtin_fmaf(s, (float)(pr & 0xFFu), b), __builtin_fmaf(s, (float)(pr >> 16), b));
+  }
+  return r;
+}
+
+template <int MT, int NB, bool DEQ>
+__global__ __launch_bounds__(256, 1) void k_gemm_t(GemmTArgs p) {
+  static_assert(NB >= 1 && NB <= 4, "one (s, b) DMA per wave covers at most 8 tiles");
+  constexpr int BM = 32 * MT, NBB = 4 * NB;
+  constexpr int A_BYTES = BM * 256;             // [BM][128 bf16]
+  constexpr int C_BYTES = 2 * NBB * kT64Codes;  // [2 groups][NBB bands][1024]
+  constexpr int ST = A_BYTES + C_BYTES + 4 * 1024;  // + [4 waves][1 KB] (s, b) areas
+  constexpr int AI = BM / 16;                   // activation DMA instructions per wave per chunk (4 rows each)
+  constexpr int VPC = AI + 2 * NB + 1;          // DMA instructions per wave per chunk
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, h = lane >> 5;
+
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int L = xcd_remap(blockIdx.x, ntiles);
+  const int per_band = kGtBand * p.tiles_n;
+  const int bandi = L / per_band, within = L % per_band;
+  const int bm = min(kGtBand, p.tiles_m - bandi * kGtBand);
+  const int tm = bandi * kGtBand + within % bm, tn = within / bm;
+  const int m0 = tm * BM;
+  const int nbands = t64_bands(p.N);
+  const int G = p.K / kGroup;
+  const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps);
+  const int nch = (g1 - g0) / 2, lastg = g0 + 2 * (nch - 1);
+
+  // activation DMA: instruction i of this wave covers rows 4 (wave AI + i) .. + 3; lane -> LDS slot lane of that
+  // 1 KB: row r = 4 (wave AI + i) + lane / 16, physical 16-byte column lane % 16 holding logical column
+  // (lane % 16) ^ (r % 16). Rows past M re-read row M - 1 (finite data; their outputs are not stored).
+  const uint16_t* asrc[AI];
+#pragma unroll
+  for (int i = 0; i < AI; i++) {
+    const int r = 4 * (wave * AI + i) + lane / 16;
+    const int c = (lane & 15) ^ (r & 15);
+    asrc[i] = p.A + (size_t)min(m0 + r, p.M - 1) * p.lda + 8 * c;
+  }
+  // code DMA: this wave's NB bands (bands past the end re-read the last band; their outputs are not stored)
+  const uint8_t* tb[NB];
+#pragma unroll
+  for (int b = 0; b < NB; b++) tb[b] = p.wt + (size_t)min(tn * NBB + wave * NB + b, nbands - 1) * kT64Tile;
+  const size_t gstride = (size_t)nbands * kT64Tile;
+  // (s, b) DMA: lane -> tile q = (lane mod 16 NB) / 8 = gi NB + b, 16-byte part lane % 8 of its 128 bytes; lanes
+  // from 16 NB on repeat the first ones (the full wave issues every DMA)
+  const uint8_t* sbsrc;
+  {
+    const int q = (lane % (16 * NB)) / 8, gi = q / NB, b = q % NB;
+    sbsrc = p.wt + (size_t)min(tn * NBB + wave * NB + b, nbands - 1) * kT64Tile + kT64Codes + 16 * (lane & 7) +
+            (size_t)gi * gstride;
+  }
+
+  auto issue = [&](int chunk, int stage) {
+    const size_t g = (size_t)min(g0 + 2 * chunk, lastg);
+    uint8_t* st = lds + stage * ST;
+#pragma unroll
+    for (int i = 0; i < AI; i++) dma16(asrc[i] + g * kGroup, st + (wave * AI + i) * 1024);
+#pragma unroll
+    for (int gi = 0; gi < 2; gi++)
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+        dma16(tb[b] + (g + gi) * gstride + 16 * lane, st + A_BYTES + (gi * NBB + wave * NB + b) * kT64Codes);
+    dma16(sbsrc + g * gstride, st + A_BYTES + C_BYTES + wave * 1024);
+  };
+
+  f32x16 acc[MT][NB];
+#pragma unroll
+  for (int a = 0; a < MT; a++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[a][b] = zero16();
+  u32x4 ones;
+  ones[0] = ones[1] = ones[2] = ones[3] = 0x3F803F80u;
+
+  auto compute = [&](int stage) {
+    const uint8_t* st = lds + stage * ST;
+#pragma unroll
+    for (int gi = 0; gi < 2; gi++) {
+      float sc[NB], bp[NB];
+      u32x4 bfr[NB][4];
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        const u32x4 codes = *(const u32x4*)(st + A_BYTES + (gi * NBB + wave * NB + b) * kT64Codes + 16 * lane);
+        const uint32_t sb = *(const uint32_t*)(st + A_BYTES + C_BYTES + wave * 1024 + (gi * NB + b) * 128 + 4 * j);
+        sc[b] = bf2f((uint16_t)(sb & 0xFFFFu));
+        const float bi = bf2f((uint16_t)(sb >> 16));
+        bp[b] = DEQ ? bi : __builtin_fmaf(-128.f, sc[b], bi);
+#pragma unroll
+        for (int t = 0; t < 4; t++) bfr[b][t] = DEQ ? t64_dequant(codes[t], sc[b], bi) : t64_off128(codes[t]);
+      }
+#pragma unroll
+      for (int a = 0; a < MT; a++) {
+        const int r = a * 32 + j;
+        const uint8_t* arow = st + r * 256;
+        u32x4 af[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) af[t] = *(const u32x4*)(arow + 16 * ((gi * 8 + 4 * h + t) ^ (r & 15)));
+        if (DEQ) {
+#pragma unroll
+          for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc[a][b] = mfma_bf16(af[t], bfr[b][t], acc[a][b]);
+        } else {
+          f32x16 X = zero16();
+#pragma unroll
+          for (int t = 0; t < 4; t++) X = mfma_bf16(af[t], ones, X);
+#pragma unroll
+          for (int b = 0; b < NB; b++) {
+            f32x16 P = zero16();
+#pragma unroll
+            for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], bfr[b][t], P);
+#pragma unroll
+            for (int r2 = 0; r2 < 16; r2++)
+              acc[a][b][r2] = __builtin_fmaf(sc[b], P[r2], __builtin_fmaf(bp[b], X[r2], acc[a][b][r2]));
+          }
+        }
+      }
+    }
+  };
+
+  // Every iteration issues one chunk (past the end: a re-read of the last chunk into a stage nobody reads again), so
+  // the count of outstanding DMA instructions is the same on every path: waiting for VPC * (kGtNS - 2) leaves the
+  // younger chunks in flight. The LDS reads of the previous chunk finish before the barrier that lets any wave
+  // overwrite that stage.
+#pragma unroll
+  for (int s = 0; s < kGtNS - 1; s++) issue(s, s);
+  for (int c = 0; c < nch; c++) {
+    wait_vm_barrier<VPC * (kGtNS - 2)>();
+    issue(c + kGtNS - 1, (c + kGtNS - 1) % kGtNS);
+    compute(c % kGtNS);
+  }
+  wait_vm<0>();  // no DMA may still target this block's LDS when it exits
+
+  const bool split = gridDim.y > 1;
+#pragma unroll
+  for (int a = 0; a < MT; a++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const int col = (tn * NBB + wave * NB + b) * 32 + j;
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + a * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        if (row >= p.M) continue;
+        if (split) p.part[((size_t)blockIdx.y * p.M + row) * p.N + col] = acc[a][b][r];
+        else store_mode(p.C, (size_t)row * p.ldc + col, acc[a][b][r], p.mode);
+      }
+    }
+}
+
+// Tile/split plan: (MT, NB, DEQ) by M; the K split S (whole 2-group chunks) maximises the occupancy of the last
+// round of blocks over 256 CUs, with fp32 partials of at most 64 MB.
+struct GtPlan {
+  int MT, NB, S, gps;
+  bool deq;
+};
+static GtPlan gemm_t_plan(int M, int N, int K) {
+  GtPlan pl{};
+  pl.MT = M <= 32 ? 1 : M <= 64 ? 2 : 4;
+  pl.NB = 2;
+  pl.deq = pl.MT == 4;
+  const int G = K / kGroup;
+  const long tiles = (long)((M + 32 * pl.MT - 1) / (32 * pl.MT)) * ((t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB));
+  const long smax = std::max(1L, std::min<long>(G / 8, (64L << 20) / ((long)M * N * 4)));
+  long best = 1;
+  double best_eff = 0.0;
+  for (long S = 1; S <= smax && tiles * (S - 1) < 4 * 256; S++) {
+    const long blocks = tiles * S, rounds = (blocks + 255) / 256;
+    const double eff = (double)blocks / (rounds * 256.0) - 0.02 * (S - 1);  // small cost per extra split
+    if (eff > best_eff + 1e-9) best_eff = eff, best = S;
+  }
+  int gps = (int)((G + best - 1) / best);
+  gps = (gps + 1) / 2 * 2;
+  pl.S = (G + gps - 1) / gps;
+  pl.gps = gps;
+  return pl;
+}
+
+size_t gemm_t_workspace(int M, int N, int K) {
+  const GtPlan pl = gemm_t_plan(M, N, K);
+  return pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
+}
+
+template <int MT, int NB, bool DEQ>
+static int launch_gemm_t_cfg(const GemmTArgs& p, int S, hipStream_t st) {
+  const size_t lds = (size_t)kGtNS * (32 * MT * 256 + 2 * 4 * NB * kT64Codes + 4 * 1024);
+  static bool attr = false;
+  if (!attr) {
+    hipFuncSetAttribute((const void*)k_gemm_t<MT, NB, DEQ>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_gemm_t<MT, NB, DEQ>), dim3(p.tiles_m * p.tiles_n, S), dim3(256), lds, st, p);
+  return check_launch("gemm_t64");
+}
+
+int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                  void* ws, size_t ws_bytes, hipStream_t st) {
+  if (M == 0) return IFD_OK;
+  if (K % 128) return fail(IFD_ERR_ARG, "T64 GEMM needs K %% 128 == 0 (K=%d)", K);
+  const GtPlan pl = gemm_t_plan(M, N, K);
+  const size_t need = pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
+  if (need > ws_bytes || (need && !ws))
+    return fail(IFD_ERR_WORKSPACE, "gemm_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
+  GemmTArgs p{A, lda, (const uint8_t*)wt, N, K, C, ldc, M, mode, (float*)ws, pl.gps,
+              (M + 32 * pl.MT - 1) / (32 * pl.MT), (t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB)};
+  int rc;
+  if (pl.MT == 1) rc = launch_gemm_t_cfg<1, 2, false>(p, pl.S, st);
+  else if (pl.MT == 2) rc = launch_gemm_t_cfg<2, 2, false>(p, pl.S, st);
+  else rc = launch_gemm_t_cfg<4, 2, true>(p, pl.S, st);
+  IFD_TRY(rc);
+  if (pl.S > 1) return launch_splitk_reduce((const float*)ws, pl.S, M, N, C, ldc, mode, st);
+  return IFD_OK;
+}
+
+}  // namespace ifd

@@ -169,273 +169,6 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   }
 }
 
-// ---- GEMM on T64 weights, any M ------------------------------------------------------------------------------
-// Block: 4 waves; block tile BM = 32 MT rows x 4 NB bands (128 NB columns); grid x = tiles (XCD-contiguous, bands of
-// kGtBand M tiles walked M-fastest), grid y = K splits. K advances in chunks of two 64-groups: the block stages the
-// activation chunk [BM][128] in LDS (double-buffered, one barrier per chunk) while each wave streams its NB bands'
-// T64 tiles straight into registers (ping-pong, one chunk ahead; no weight staging in LDS).
-//  DEQ = false (affine): codes enter the MFMA as exact bf16 (128 + q); per group the fp32 epilogue adds
-//    s P + (b - 128 s) X with the group's activation sums X staged beside the chunk: the decode GEMV arithmetic.
-//  DEQ = true: codes are dequantized in registers to bf16(s q + b) (MLX qmm rounding, quantized.h:528-535) and
-//    accumulate over K: one dequant feeds MT MFMA tiles, the cheaper choice from 4 M tiles up.
-struct GemmTArgs {
-  const uint16_t* A;
-  int lda;
-  const uint8_t* wt;
-  int N, K;
-  void* C;
-  int ldc, M, mode;
-  float* part;
-  int gps;
-  int tiles_m, tiles_n;
-};
-
-constexpr int kGtBand = 4;
-constexpr int kGtCK = 128, kGtLd = kGtCK + 8;  // chunk: 2 groups; LDS row stride (bf16)
-
-// eight T64 codes (one word) -> bf16(s q + b) in natural k order
-__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float s, float b) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint32_t pr = (w >> (4 * i)) & 0x000F000Fu;
-    r[i] = pack_bf2(__builtin_fmaf(s, (float)(pr & 0xFFu), b), __builtin_fmaf(s, (float)(pr >> 16), b));
-  }
-  return r;
-}
-
-template <int MT, int NB, bool DEQ>
-__global__ __launch_bounds__(256, 1) void k_gemm_t(GemmTArgs p) {
-  constexpr int BM = 32 * MT;
-  constexpr int ACH = BM * (kGtCK / 8) / 256;  // 16-byte activation chunks per thread per K chunk
-  extern __shared__ __align__(16) uint16_t lds[];
-  uint16_t* As = lds;                                         // [2][BM][kGtLd]
-  float* Xs = (float*)(lds + 2 * BM * kGtLd);                 // [2][2 groups][BM] (affine only)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int j = lane & 31, h = lane >> 5;
-
-  const int ntiles = p.tiles_m * p.tiles_n;
-  const int L = xcd_remap(blockIdx.x, ntiles);
-  const int per_band = kGtBand * p.tiles_n;
-  const int bandi = L / per_band, within = L % per_band;
-  const int bm = min(kGtBand, p.tiles_m - bandi * kGtBand);
-  const int tm = bandi * kGtBand + within % bm, tn = within / bm;
-  const int m0 = tm * BM;
-  const int nbands = t64_bands(p.N);
-
-  const int G = p.K / kGroup;
-  const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps);
-  const int nch = (g1 - g0) / 2;  // gps and G are even (K % 128 == 0)
-
-  // activation staging: chunk c = tid + 256 i -> row c / 16, 16-byte column c % 16 of the 128-wide K chunk
-  const uint16_t* aptr[ACH];
-  bool aok[ACH];
-#pragma unroll
-  for (int i = 0; i < ACH; i++) {
-    const int c = tid + 256 * i, m = m0 + c / 16;
-    aok[i] = m < p.M;
-    aptr[i] = p.A + (size_t)(aok[i] ? m : 0) * p.lda + 8 * (c % 16);
-  }
-  // weight tiles of this wave's bands
-  const uint8_t* tb[NB];
-  bool bok[NB];
-#pragma unroll
-  for (int b = 0; b < NB; b++) {
-    const int band = tn * 4 * NB + wave * NB + b;
-    bok[b] = band < nbands;
-    tb[b] = p.wt + (size_t)(bok[b] ? band : 0) * kT64Tile;
-  }
-  const size_t gstride = (size_t)nbands * kT64Tile;
-
-  struct WB {
-    u32x4 w[2][NB];
-    uint32_t sb[2][NB];
-  };
-  auto load_w = [&](WB& B, int g) {
-#pragma unroll
-    for (int gi = 0; gi < 2; gi++)
-#pragma unroll
-      for (int b = 0; b < NB; b++) {
-        const uint8_t* t = tb[b] + (size_t)(g + gi) * gstride;
-        B.w[gi][b] = *(const u32x4*)(t + 16 * lane);
-        B.sb[gi][b] = *(const uint32_t*)(t + kT64Codes + 4 * j);
-      }
-  };
-  u32x4 areg[ACH];
-  auto load_a = [&](int g) {
-#pragma unroll
-    for (int i = 0; i < ACH; i++)
-      areg[i] = aok[i] ? *(const u32x4*)(aptr[i] + (size_t)g * kGroup) : u32x4{0u, 0u, 0u, 0u};
-  };
-  auto store_a = [&](int buf) {
-    uint16_t* as = As + buf * BM * kGtLd;
-#pragma unroll
-    for (int i = 0; i < ACH; i++) {
-      const int c = tid + 256 * i;
-      *(u32x4*)(as + (c / 16) * kGtLd + 8 * (c % 16)) = areg[i];
-      if (!DEQ) {
-        // group sums of this row: 8 consecutive 16-byte chunks (8 consecutive lanes) per group
-        float sum = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; e++) sum += bf2f((uint16_t)(areg[i][e] & 0xFFFFu)) + bf2f((uint16_t)(areg[i][e] >> 16));
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
-        if ((c & 7) == 0) Xs[(buf * 2 + ((c % 16) >> 3)) * BM + c / 16] = sum;
-      }
-    }
-  };
-
-  f32x16 acc[MT][NB];
-#pragma unroll
-  for (int a = 0; a < MT; a++)
-#pragma unroll
-    for (int b = 0; b < NB; b++) acc[a][b] = zero16();
-
-  auto compute = [&](const WB& B, int buf) {
-    const uint16_t* as = As + buf * BM * kGtLd + j * kGtLd + 32 * h;
-#pragma unroll
-    for (int gi = 0; gi < 2; gi++) {
-      float sc[NB], bp[NB];
-      u32x4 bfr[NB][4];
-#pragma unroll
-      for (int b = 0; b < NB; b++) {
-        sc[b] = bf2f((uint16_t)(B.sb[gi][b] & 0xFFFFu));
-        const float bi = bf2f((uint16_t)(B.sb[gi][b] >> 16));
-        bp[b] = DEQ ? bi : __builtin_fmaf(-128.f, sc[b], bi);
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-          bfr[b][t] = DEQ ? t64_dequant(B.w[gi][b][t], sc[b], bi) : t64_bf16_off128(B.w[gi][b][t]);
-      }
-#pragma unroll
-      for (int a = 0; a < MT; a++) {
-        u32x4 af[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) af[t] = *(const u32x4*)(as + a * 32 * kGtLd + gi * 64 + 8 * t);
-        if (DEQ) {
-#pragma unroll
-          for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int t = 0; t < 4; t++) acc[a][b] = mfma_bf16(af[t], bfr[b][t], acc[a][b]);
-        } else {
-          const float* xs = Xs + (buf * 2 + gi) * BM + a * 32 + 4 * h;
-          float xv[16];
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const float4 x4 = *(const float4*)(xs + 8 * q);
-            xv[4 * q] = x4.x, xv[4 * q + 1] = x4.y, xv[4 * q + 2] = x4.z, xv[4 * q + 3] = x4.w;
-          }
-#pragma unroll
-          for (int b = 0; b < NB; b++) {
-            f32x16 P = zero16();
-#pragma unroll
-            for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], bfr[b][t], P);
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-              acc[a][b][r] = __builtin_fmaf(sc[b], P[r], __builtin_fmaf(bp[b], xv[r], acc[a][b][r]));
-          }
-        }
-      }
-    }
-  };
-
-  // pipeline: unconditional (clamped) prefetches keep the outstanding-load count uniform on every path
-  const int last = g0 + 2 * (nch - 1);
-  WB w0, w1;
-  load_a(g0);
-  load_w(w0, g0);
-  store_a(0);
-  __syncthreads();
-  for (int c = 0;; c += 2) {
-    load_a(min(g0 + 2 * (c + 1), last));
-    load_w(w1, min(g0 + 2 * (c + 1), last));
-    compute(w0, c & 1);
-    if (c + 1 >= nch) break;
-    store_a((c + 1) & 1);
-    __syncthreads();
-    load_a(min(g0 + 2 * (c + 2), last));
-    load_w(w0, min(g0 + 2 * (c + 2), last));
-    compute(w1, (c + 1) & 1);
-    if (c + 2 >= nch) break;
-    store_a(c & 1);
-    __syncthreads();
-  }
-
-  const bool split = gridDim.y > 1;
-#pragma unroll
-  for (int a = 0; a < MT; a++)
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-      const int col = (tn * 4 * NB + wave * NB + b) * 32 + j;
-      if (col >= p.N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + a * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-        if (row >= p.M) continue;
-        if (split) p.part[((size_t)blockIdx.y * p.M + row) * p.N + col] = acc[a][b][r];
-        else store_mode(p.C, (size_t)row * p.ldc + col, acc[a][b][r], p.mode);
-      }
-    }
-}
-
-// Tile/split plan of the T64 GEMM: (MT, NB, DEQ) by M; enough blocks for ~256 CUs; partials S * M <= 1024 rows.
-struct GtPlan {
-  int MT, NB, S, gps;
-  bool deq;
-};
-static GtPlan gemm_t_plan(int M, int N, int K) {
-  GtPlan pl{};
-  pl.MT = M <= 32 ? 1 : M <= 64 ? 2 : 4;
-  pl.NB = 2;
-  pl.deq = pl.MT == 4;
-  const int G = K / kGroup;
-  const long tiles = (long)((M + 32 * pl.MT - 1) / (32 * pl.MT)) * ((t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB));
-  long S = tiles >= 256 ? 1 : (256 + tiles - 1) / tiles;
-  S = std::min<long>(S, std::max(1, G / 8));
-  S = std::min<long>(S, std::max(1, 1024 / std::max(M, 1)));
-  int gps = (int)((G + S - 1) / S);
-  gps = (gps + 1) / 2 * 2;
-  pl.S = (G + gps - 1) / gps;
-  pl.gps = gps;
-  return pl;
-}
-
-size_t gemm_t_workspace(int M, int N, int K) {
-  const GtPlan pl = gemm_t_plan(M, N, K);
-  return pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
-}
-
-template <int MT, int NB, bool DEQ>
-static int launch_gemm_t_cfg(const GemmTArgs& p, int S, hipStream_t st) {
-  const size_t lds = (size_t)2 * 32 * MT * kGtLd * 2 + (DEQ ? 0 : (size_t)2 * 2 * 32 * MT * sizeof(float));
-  static bool attr = false;
-  if (!attr) {
-    hipFuncSetAttribute((const void*)k_gemm_t<MT, NB, DEQ>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    attr = true;
-  }
-  hipLaunchKernelGGL((k_gemm_t<MT, NB, DEQ>), dim3(p.tiles_m * p.tiles_n, S), dim3(256), lds, st, p);
-  return check_launch("gemm_t64");
-}
-
-int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
-                  void* ws, size_t ws_bytes, hipStream_t st) {
-  if (M == 0) return IFD_OK;
-  if (K % 128) return fail(IFD_ERR_ARG, "T64 GEMM needs K %% 128 == 0 (K=%d)", K);
-  const GtPlan pl = gemm_t_plan(M, N, K);
-  const size_t need = pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
-  if (need > ws_bytes || (need && !ws))
-    return fail(IFD_ERR_WORKSPACE, "gemm_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
-  GemmTArgs p{A, lda, (const uint8_t*)wt, N, K, C, ldc, M, mode, (float*)ws, pl.gps,
-              (M + 32 * pl.MT - 1) / (32 * pl.MT), (t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB)};
-  int rc;
-  if (pl.MT == 1) rc = launch_gemm_t_cfg<1, 2, false>(p, pl.S, st);
-  else if (pl.MT == 2) rc = launch_gemm_t_cfg<2, 2, false>(p, pl.S, st);
-  else rc = launch_gemm_t_cfg<4, 2, true>(p, pl.S, st);
-  IFD_TRY(rc);
-  if (pl.S > 1) return launch_splitk_reduce((const float*)ws, pl.S, M, N, C, ldc, mode, st);
-  return IFD_OK;
-}
-
 // Split plan: ~2 blocks per CU, whole kTB-group blocks per split, <= ~40 KB of staged activations per block.
 struct TPlan {
   int S, gps;
