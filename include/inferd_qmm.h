@@ -72,6 +72,13 @@ int ifd_flip_w4(uint32_t* wq, size_t n32, uint32_t mask, void* stream);
  * (reference silu_mul, core.metal:777-787; moe_silu_mul, moe.metal:103-111). */
 int ifd_silu_mul(const void* gu, void* h, int I, int rows, void* stream);
 
+/* RMS norm over rows of D bf16 values: out[r][i] = bf16(float(x[r][i]) * rsqrt(sum_i x^2 / D + eps) * float(w[i])),
+ * fp32 sum of squares (reference rmsnorm, core.metal:486-500; host Qwen35::rmsnorm, qwen35.h:2004-2012; the
+ * normalisation encode_moe applies first, rmsnorm_for, qwen35.h:1982-2002). Rows are in_stride / out_stride
+ * values apart. */
+int ifd_rmsnorm(const void* x, int in_stride, const void* w, void* out, int out_stride, int rows, int D, float eps,
+                void* stream);
+
 /* ---- T64: the MI355X weight layout (no counterpart in the reference; its role is that of the reference's
  * load-time weight transforms, flip and the lane4/qmst copies, qwen35.h:1209-1322) -------------------------------
  * A one-time repack of the MLX layout into 1152-byte tiles (per 64-group and 32-column band: the codes in MFMA

@@ -29,6 +29,7 @@ SIGNATURES = {
     "ifd_gemm_w4": (_i, _GEMM_ARGS),
     "ifd_flip_w4": (_i, [_vp, _sz, _u32, _vp]),
     "ifd_silu_mul": (_i, [_vp, _vp, _i, _i, _vp]),
+    "ifd_rmsnorm": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp]),
     "ifd_a8_quant": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "ifd_qmm_w4a8": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _u32, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_qmm_w4a8_workspace": (_sz, [_i, _i, _i]),

@@ -91,6 +91,16 @@ int ifd_silu_mul(const void* gu, void* h, int I, int rows, void* stream) {
   return launch_silu_mul((const uint16_t*)gu, (uint16_t*)h, I, rows, S(stream));
 }
 
+int ifd_rmsnorm(const void* x, int in_stride, const void* w, void* out, int out_stride, int rows, int D, float eps,
+                void* stream) {
+  IFD_CHECK(rows >= 0 && D > 0 && in_stride >= D && out_stride >= D, "bad shape rows=%d D=%d strides %d/%d", rows, D,
+            in_stride, out_stride);
+  IFD_CHECK(rows == 0 || (x && w && out), "null pointer");
+  IFD_CHECK(eps >= 0.f, "eps must be >= 0");
+  return launch_rmsnorm((const uint16_t*)x, in_stride, (const uint16_t*)w, (uint16_t*)out, out_stride, rows, D, eps,
+                        S(stream));
+}
+
 int ifd_a8_quant(const void* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, void* stream) {
   IFD_CHECK(M >= 0 && K > 0 && K % 64 == 0 && lda >= K, "bad shape M=%d K=%d lda=%d", M, K, lda);
   IFD_CHECK(M == 0 || (A && U && XS), "null pointer");

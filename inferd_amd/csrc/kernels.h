@@ -32,6 +32,8 @@ size_t w4a8_workspace(int M, int N, int K);
 int launch_w4a8(const W4Gemm& g, int per_token, void* ws, size_t ws_bytes, hipStream_t st);
 int launch_flip(uint32_t* wq, size_t n32, uint32_t mask, hipStream_t st);
 int launch_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows, hipStream_t st);
+int launch_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows,
+                   int D, float eps, hipStream_t st);
 // Split-K reduction: C (mode) = sum over S partials [S][M][N] fp32.
 int launch_splitk_reduce(const float* part, int S, int M, int N, void* C, int ldc, int mode, hipStream_t st);
 

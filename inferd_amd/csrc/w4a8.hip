@@ -99,6 +99,32 @@ int launch_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows, hipStream_
   return check_launch("silu_mul");
 }
 
+// RMS norm, one block per row: out = bf16(float(x) * rsqrt(sum x^2 / D + eps) * float(w)), fp32 sum of squares
+// (reference rmsnorm, core.metal:486-500).
+__global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x, int in_stride,
+                                                 const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                                                 int out_stride, int D, float eps) {
+  __shared__ float red[4];
+  const uint16_t* xr = x + (size_t)blockIdx.x * in_stride;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < D; i += 256) {
+    const float v = bf2f(xr[i]);
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float r = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + eps);
+  uint16_t* o = out + (size_t)blockIdx.x * out_stride;
+  for (int i = threadIdx.x; i < D; i += 256) o[i] = f2bf(bf2f(xr[i]) * r * bf2f(w[i]));
+}
+int launch_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows,
+                   int D, float eps, hipStream_t st) {
+  if (rows == 0) return IFD_OK;
+  hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, st, x, in_stride, w, out, out_stride, D, eps);
+  return check_launch("rmsnorm");
+}
+
 // ---- W4A8 GEMM -------------------------------------------------------------------------------------------------
 constexpr int kA8BM = 128, kA8BN = 128, kA8Ld = 80;  // LDS row: 64 int8 + 16 pad
 constexpr int kA8Band = 4;

@@ -120,6 +120,14 @@ def silu_mul(gu: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tens
     return h
 
 
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Row RMS norm of bf16 x [R, D] with bf16 weight w [D] (reference rmsnorm, core.metal:486-500)."""
+    R, D = x.shape
+    y = torch.empty((R, D), dtype=torch.bfloat16, device=x.device) if out is None else out
+    check(lib().ifd_rmsnorm(_p(x), x.stride(0), _p(w), _p(y), y.stride(0), R, D, float(eps), _stream()))
+    return y
+
+
 def a8_quant(A: torch.Tensor, per_token: bool):
     M, K = A.shape
     U = torch.empty((M, K), dtype=torch.int8, device=A.device)

@@ -54,6 +54,7 @@ def lib():
         L.orc_a8_quant.argtypes = [_u16p, _i, _i, _i, _i, _i8p, _f32p]
         L.orc_w4a8.argtypes = [_i8p, _f32p, _u32p, _u16p, _u16p, _i, _i, _u, _f32p, _i, _i]
         L.orc_silu_mul.argtypes = [_u16p, _u16p, _i, _i]
+        L.orc_rmsnorm.argtypes = [_u16p, _i, _u16p, _u16p, _i, _i, _i, ctypes.c_float]
         L.orc_gemm_bf16.argtypes = [_u16p, _u16p, _f32p, _i, _i, _i, _i]
         L.orc_moe_route.argtypes = [_vp, _i, _i, _i, _i, _i, _i, _i, _i32p, _f32p, _f32p]
         L.orc_moe_dispatch.argtypes = [_i32p, _i, _i, _i32p, _i32p, _i32p]
@@ -186,6 +187,14 @@ def silu_mul(gu) -> np.ndarray:
     h = np.empty((R, I2 // 2), np.uint16)
     lib().orc_silu_mul(gu, h, I2 // 2, R)
     return h
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    x = _c(x, np.uint16)
+    R, D = x.shape
+    out = np.empty((R, D), np.uint16)
+    lib().orc_rmsnorm(x, D, _c(w, np.uint16), out, D, R, D, eps)
+    return out
 
 
 def gemm_bf16(A, W, nthreads: int = 0) -> np.ndarray:

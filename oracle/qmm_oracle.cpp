@@ -15,7 +15,8 @@
 // Pinning (tests/test_oracle.py): nibble unpack is checked exhaustively and against a hand-built vector; dequant by a
 // one-hot activation probe and the all-8 (b = -8s) zero case; qmv/qmm/w4a8 against float64 textbook GEMMs in numpy
 // and exact-rational known answers (tests/golden/); routing against a brute-force lexsort; dispatch against numpy's
-// stable argsort; SwiGLU and combine against their closed forms.
+// stable argsort; SwiGLU and combine against their closed forms; RMS norm against constant, one-hot and
+// power-of-two-scaled rows whose outputs are exact.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -235,6 +236,20 @@ void orc_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows) {
       const float g = bf2f(gu[(size_t)r * 2 * I + i]), u = bf2f(gu[(size_t)r * 2 * I + I + i]);
       h[(size_t)r * I + i] = f2bf(bfround(g / (1.f + std::exp(-g))) * u);
     }
+}
+
+// RMS norm (engine/kernels/core.metal:486-500): out = bf16(float(x) * r * float(w)), r = rsqrt(sum x^2 / D + eps).
+// The sum of squares is taken in double (the reference sums in fp32 in an unspecified order); r is rounded to fp32
+// and the products are fp32, left to right, as the reference writes them.
+void orc_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows, int D,
+                 float eps) {
+  for (int r = 0; r < rows; r++) {
+    const uint16_t* xr = x + (size_t)r * in_stride;
+    double ss = 0.0;
+    for (int i = 0; i < D; i++) ss += (double)bf2f(xr[i]) * bf2f(xr[i]);
+    const float rs = (float)(1.0 / std::sqrt(ss / D + (double)eps));
+    for (int i = 0; i < D; i++) out[(size_t)r * out_stride + i] = f2bf(bf2f(xr[i]) * rs * bf2f(w[i]));
+  }
 }
 
 // bf16 x bf16 GEMM with fp32 accumulation (router logits, engine/kernels/moe.metal:198-213 / qwen35.h:1919-1929):

@@ -1,0 +1,326 @@
+// Parity test of the C++ operator shim (inferd_amd/csrc/qwen35_ops.h) against the CPU oracle (oracle/liboracle.so),
+// written like the reference's seeded inline kernel tests (engine/tools/gemm_dbg.mm:14-55, qa8_dbg.mm:14-66): build a
+// layer from a fixed seed, run the operator, compare with the host reference, print one line per case.
+//
+//   qwen35_ops_test             every GPU case; exit 0 when all pass
+//   qwen35_ops_test --bad-bits  gemm() on an 8-bit QLinear: must print its error and exit(1) (no GPU needed)
+//
+// Tolerances are BASELINE's: max |err| <= 1e-2 RMS(ref) after the output's own bf16 rounding; routing indices
+// bit-exact.
+#include <cmath>
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "qwen35_ops.h"
+
+extern "C" {
+void orc_pack_w4(const uint8_t* codes, uint32_t* wq, int N, int K);
+void orc_flip(uint32_t* wq, int64_t n32, uint32_t mask);
+void orc_qmv(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+             uint32_t xr, float* Y, int M, int nthreads);
+void orc_qmm(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+             uint32_t xr, float* Y, int M, int nthreads);
+void orc_store(const float* Y, void* C, int ldc, int M, int N, int mode);
+void orc_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows, int D,
+                 float eps);
+void orc_moe_route(const void* logits, int logits_bf16, int T, int E, int k, int stride, int norm, int shared_gate,
+                   int* idx, float* wt, float* sg);
+void orc_moe_experts(const uint16_t* xn, int T, int H, int I, int E, int k, const int* idx, const float* wt,
+                     const float* sg, const uint32_t* gu_wq, const uint16_t* gu_s, const uint16_t* gu_b,
+                     const uint32_t* dn_wq, const uint16_t* dn_s, const uint16_t* dn_b, const uint32_t* sh_gu_wq,
+                     const uint16_t* sh_gu_s, const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq,
+                     const uint16_t* sh_dn_s, const uint16_t* sh_dn_b, int shared_qmv, uint16_t* out, int assign,
+                     int nthreads);
+}
+
+using namespace inferd;
+
+namespace {
+
+int failures = 0;
+
+void report(bool pass, const std::string& what, double err) {
+  printf("%s %-60s err %.3e\n", pass ? "ok  " : "FAIL", what.c_str(), err);
+  fflush(stdout);
+  if (!pass) failures++;
+}
+
+float bf2f(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+uint16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <class T>
+BufRef upload(const std::vector<T>& v) {
+  void* p = nullptr;
+  hip_ok(hipMalloc(&p, std::max<size_t>(v.size() * sizeof(T), 256)), "upload");
+  hip_ok(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice), "upload");
+  return BufRef(p);
+}
+template <class T>
+std::vector<T> download(const BufRef& r, size_t n) {
+  std::vector<T> v(n);
+  hip_ok(hipDeviceSynchronize(), "download");
+  hip_ok(hipMemcpy(v.data(), r.ptr<void>(), n * sizeof(T), hipMemcpyDeviceToHost), "download");
+  return v;
+}
+
+// max |got - ref| / RMS(ref), less half a bf16 step of ref (one step when ref is itself bf16)
+double bf16_err(const std::vector<uint16_t>& got, const std::vector<float>& ref, bool ref_is_bf16) {
+  double ss = 0, worst = 0;
+  for (float r : ref) ss += (double)r * r;
+  const double rms = std::sqrt(ss / std::max<size_t>(ref.size(), 1));
+  for (size_t i = 0; i < ref.size(); i++) {
+    const double r = ref[i];
+    const double ulp = r == 0 ? 0 : std::ldexp(1.0, std::ilogb(r) - 7);
+    const double e = std::fabs(bf2f(got[i]) - r) - (ref_is_bf16 ? ulp : 0.5 * ulp);
+    worst = std::max(worst, e);
+  }
+  return worst / (rms > 0 ? rms : 1);
+}
+
+struct HostLinear {
+  int N, K;
+  std::vector<uint32_t> wq;
+  std::vector<uint16_t> s, b;
+};
+
+HostLinear make_linear(int N, int K, std::mt19937& rng) {
+  HostLinear h{N, K, {}, {}, {}};
+  std::vector<uint8_t> codes((size_t)N * K);
+  std::uniform_int_distribution<int> q(0, 15);
+  for (auto& c : codes) c = (uint8_t)q(rng);
+  h.wq.resize((size_t)N * K / 8);
+  orc_pack_w4(codes.data(), h.wq.data(), N, K);
+  std::uniform_real_distribution<float> su(0.005f, 0.02f);
+  h.s.resize((size_t)N * K / 64);
+  h.b.resize(h.s.size());
+  for (size_t i = 0; i < h.s.size(); i++) {
+    h.s[i] = f2bf(su(rng));
+    h.b[i] = f2bf(-8.f * bf2f(h.s[i]));
+  }
+  return h;
+}
+
+QLinear device_linear(const HostLinear& h) {
+  QLinear W;
+  W.wq = upload(h.wq);
+  W.s = upload(h.s);
+  W.b = upload(h.b);
+  W.N = h.N;
+  W.K = h.K;
+  return W;
+}
+
+std::vector<uint16_t> activations(int M, int K, std::mt19937& rng) {
+  std::normal_distribution<float> nd(0.f, 1.f);
+  std::vector<uint16_t> a((size_t)M * K);
+  for (auto& v : a) v = f2bf(nd(rng));
+  return a;
+}
+
+// fp32 y (before the store) of the GEMM semantics the routed kernel implements
+std::vector<float> ref_gemm(const std::vector<uint16_t>& A, const HostLinear& h, int M, bool qmv_semantics) {
+  std::vector<float> y((size_t)M * h.N);
+  (qmv_semantics ? orc_qmv : orc_qmm)(A.data(), h.K, h.wq.data(), h.s.data(), h.b.data(), h.N, h.K, 0, y.data(), M,
+                                      0);
+  return y;
+}
+
+void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
+  const int N = 384, K = 1024;
+  const HostLinear h = make_linear(N, K, rng);
+  QLinear W = device_linear(h);
+  // MLX layout: decode GEMV semantics up to 32 rows, the prefill GEMM's (bf16-rounded dequant) above
+  for (int M : {1, 8, 32, 33, 128, 200}) {
+    const auto A = activations(M, K, rng);
+    BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
+    m.gemm(e, dA, W, dC, M, 0);
+    const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), ref_gemm(A, h, M, M <= 32), false);
+    report(err <= 1e-2, "gemm MLX layout M=" + std::to_string(M) + " mode 0", err);
+    (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+  }
+  // modes 1 (residual add) and 2 (fp32)
+  {
+    const int M = 8;
+    const auto A = activations(M, K, rng);
+    const auto C0 = activations(M, N, rng);
+    BufRef dA = upload(A), dC = upload(C0), dF = upload(std::vector<float>((size_t)M * N));
+    m.gemm(e, dA, W, dC, M, 1);
+    m.gemm(e, dA, W, dF, M, 2);
+    const auto y = ref_gemm(A, h, M, true);
+    std::vector<float> yr((size_t)M * N);
+    for (size_t i = 0; i < yr.size(); i++) yr[i] = y[i] + bf2f(C0[i]);  // mode 1 rounds y + C once
+    const double e1 = bf16_err(download<uint16_t>(dC, (size_t)M * N), yr, false);
+    report(e1 <= 1e-2, "gemm mode 1 (C += y)", e1);
+    const auto f = download<float>(dF, (size_t)M * N);
+    double ss = 0, worst = 0;
+    for (size_t i = 0; i < y.size(); i++) ss += (double)y[i] * y[i], worst = std::max(worst, (double)std::fabs(f[i] - y[i]));
+    const double e2 = worst / std::sqrt(ss / y.size());
+    report(e2 <= 1e-3, "gemm mode 2 (fp32)", e2);
+    (void)hipFree(dA.buf), (void)hipFree(dC.buf), (void)hipFree(dF.buf);
+  }
+  // flipped in place: the same products
+  {
+    HostLinear hf = h;
+    orc_flip(hf.wq.data(), (int64_t)hf.wq.size(), 0x88888888u);
+    QLinear Wf = device_linear(hf);
+    Wf.flipped = true;
+    const int M = 5;
+    const auto A = activations(M, K, rng);
+    BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
+    m.gemm(e, dA, Wf, dC, M, 0);
+    const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), ref_gemm(A, h, M, true), false);
+    report(err <= 1e-2, "gemm flipped weights", err);
+    (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+  }
+  // T64 copy: decode GEMV semantics up to 64 rows, prefill semantics above
+  {
+    void* t = nullptr;
+    hip_ok(hipMalloc(&t, ifd_t64_bytes(N, K, 1)), "t64");
+    ok(ifd_pack_t64(W.wq.ptr<uint32_t>(), W.s.ptr<uint16_t>(), W.b.ptr<uint16_t>(), N, K, 0, 0, 1, t, e.stream),
+       "pack_t64");
+    QLinear Wt = W;
+    Wt.t64 = BufRef(t);
+    for (int M : {1, 16, 17, 64, 65, 128, 300}) {
+      const auto A = activations(M, K, rng);
+      BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
+      m.gemm(e, dA, Wt, dC, M, 0);
+      const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), ref_gemm(A, h, M, M <= 64), false);
+      report(err <= 1e-2, "gemm T64 M=" + std::to_string(M), err);
+      (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+    }
+    // K-slice [256, 768) of the T64 copy and of the MLX layout
+    for (bool use_t64 : {true, false}) {
+      const int M = 8, k0 = 256, kn = 512;
+      QLinear Ws = kslice_of(use_t64 ? Wt : W, k0, kn);
+      const auto A = activations(M, kn, rng);
+      HostLinear hs{N, kn, std::vector<uint32_t>((size_t)N * kn / 8), std::vector<uint16_t>((size_t)N * kn / 64),
+                    std::vector<uint16_t>((size_t)N * kn / 64)};
+      for (int n = 0; n < N; n++) {
+        memcpy(&hs.wq[(size_t)n * kn / 8], &h.wq[(size_t)n * K / 8 + k0 / 8], kn / 2);
+        memcpy(&hs.s[(size_t)n * kn / 64], &h.s[(size_t)n * K / 64 + k0 / 64], kn / 32);
+        memcpy(&hs.b[(size_t)n * kn / 64], &h.b[(size_t)n * K / 64 + k0 / 64], kn / 32);
+      }
+      BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
+      m.gemm(e, dA, Ws, dC, M, 0);
+      const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), ref_gemm(A, hs, M, true), false);
+      report(err <= 1e-2, std::string("gemm kslice_of ") + (use_t64 ? "(T64)" : "(MLX layout)"), err);
+      (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+    }
+    (void)hipFree(t);
+  }
+  // rows_of: output rows [128, 256)
+  {
+    const int M = 4, lo = 128, n = 128;
+    QLinear Wr = rows_of(W, lo, n);
+    const auto A = activations(M, K, rng);
+    BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * n));
+    m.gemm(e, dA, Wr, dC, M, 0);
+    const auto y = ref_gemm(A, h, M, true);
+    std::vector<float> yr((size_t)M * n);
+    for (int r = 0; r < M; r++)
+      for (int c = 0; c < n; c++) yr[(size_t)r * n + c] = y[(size_t)r * N + lo + c];
+    const double err = bf16_err(download<uint16_t>(dC, (size_t)M * n), yr, false);
+    report(err <= 1e-2, "gemm rows_of [128, 256)", err);
+    (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+  }
+  (void)hipFree(W.wq.buf), (void)hipFree(W.s.buf), (void)hipFree(W.b.buf);
+}
+
+void test_encode_moe(std::mt19937& rng) {
+  Config c;
+  c.hidden = 256, c.experts = 32, c.topk = 4, c.moe_inter = 128, c.eps = 1e-6f;
+  const int H = c.hidden, E = c.experts, k = c.topk, I = c.moe_inter, Is = 128;
+  // layer: stacked experts [E, 2I, H] and [E, H, I], shared expert, bf16 router with the shared gate row
+  const HostLinear egu = make_linear(E * 2 * I, H, rng), edn = make_linear(E * H, I, rng);
+  const HostLinear sgu = make_linear(2 * Is, H, rng), sdn = make_linear(H, Is, rng);
+  std::normal_distribution<float> nr(0.f, 0.02f);
+  std::vector<uint16_t> router((size_t)(E + 1) * H), post((size_t)H);
+  for (auto& v : router) v = f2bf(nr(rng));
+  std::uniform_real_distribution<float> pw(0.5f, 2.f);
+  for (auto& v : post) v = f2bf(pw(rng));
+  Layer ly;
+  ly.post_norm = upload(post);
+  ly.gate_up = device_linear(sgu);
+  ly.down = device_linear(sdn);
+  ly.router.wq = upload(router);
+  ly.router.E = 1, ly.router.N = E + 1, ly.router.K = H, ly.router.bits = 16;
+  const QLinear g = device_linear(egu), d = device_linear(edn);
+  ly.egu.wq = g.wq, ly.egu.s = g.s, ly.egu.b = g.b, ly.egu.E = E, ly.egu.N = 2 * I, ly.egu.K = H, ly.egu.bits = 4;
+  ly.edown.wq = d.wq, ly.edown.s = d.s, ly.edown.b = d.b, ly.edown.E = E, ly.edown.N = H, ly.edown.K = I,
+  ly.edown.bits = 4;
+  for (int T : {16, 100}) {
+    Qwen35 m(c, T, Is, 0);
+    Enc e;
+    const auto x0 = activations(T, H, rng);
+    hip_ok(hipMemcpy(m.x.ptr<void>(), x0.data(), x0.size() * 2, hipMemcpyHostToDevice), "x");
+    m.encode_moe(e, ly, T);
+    const auto x1 = download<uint16_t>(m.x, (size_t)T * H);
+    const auto xn = download<uint16_t>(m.xn, (size_t)T * H);
+    const auto logits = download<float>(m.rlog, (size_t)T * (E + 1));
+    const auto idx = download<int>(m.ridx, (size_t)T * k);
+    const auto wt = download<float>(m.rw, (size_t)T * k);
+    const auto sg = download<float>(m.rsg, (size_t)T);
+    const std::string tag = " T=" + std::to_string(T);
+    // rmsnorm: within one bf16 step of the oracle
+    std::vector<uint16_t> xr((size_t)T * H);
+    orc_rmsnorm(x0.data(), H, post.data(), xr.data(), H, T, H, c.eps);
+    std::vector<float> xrf(xr.size());
+    for (size_t i = 0; i < xr.size(); i++) xrf[i] = bf2f(xr[i]);
+    const double en = bf16_err(xn, xrf, true);
+    report(en == 0.0, "encode_moe rmsnorm" + tag, en);
+    // routing on the GPU's own logits: bit-exact indices
+    std::vector<int> ri((size_t)T * k);
+    std::vector<float> rwt((size_t)T * k), rsg((size_t)T);
+    orc_moe_route(logits.data(), 0, T, E, k, E + 1, 1, 1, ri.data(), rwt.data(), rsg.data());
+    double ew = 0;
+    for (size_t i = 0; i < rwt.size(); i++) ew = std::max(ew, (double)std::fabs(rwt[i] - wt[i]));
+    for (int t = 0; t < T; t++) ew = std::max(ew, (double)std::fabs(rsg[t] - sg[t]));
+    report(ri == idx && ew <= 1e-5, "encode_moe routing (indices bit-exact)" + tag, ew);
+    // the block's output added into x, from the GPU's normalised rows and routing
+    std::vector<uint16_t> want = x0;
+    orc_moe_experts(xn.data(), T, H, I, E, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
+                    egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu.wq.data(), sgu.s.data(), sgu.b.data(),
+                    sdn.wq.data(), sdn.s.data(), sdn.b.data(), T <= 32 ? 1 : 0, want.data(), 0, 0);
+    std::vector<float> wf(want.size());
+    for (size_t i = 0; i < want.size(); i++) wf[i] = bf2f(want[i]);
+    const double ex = bf16_err(x1, wf, true);
+    report(ex <= 1e-2, "encode_moe x += moe(xn)" + tag, ex);
+  }
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc > 1 && std::string(argv[1]) == "--bad-bits") {
+    Config c;
+    Qwen35 m(c, 0, 0, 0);  // no state, no GPU call
+    Enc e;
+    QLinear W;
+    W.bits = 8, W.N = 64, W.K = 64;
+    m.gemm(e, BufRef(), W, BufRef(), 1, 0);
+    printf("gemm returned for an 8-bit linear\n");
+    return 0;
+  }
+  std::mt19937 rng(20251201);
+  {
+    Config c;
+    Qwen35 m(c, 0, 0, 64 << 20);
+    Enc e;
+    test_gemm(m, e, rng);
+  }
+  test_encode_moe(rng);
+  printf(failures ? "%d FAILED\n" : "ALL OK\n", failures);
+  return failures ? 1 : 0;
+}

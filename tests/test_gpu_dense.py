@@ -180,3 +180,16 @@ def test_silu_mul_and_flip():
     W = g.qlinear(wq, s, b)
     ops.flip(W)
     assert W.flipped and np.array_equal(g.host(W.wq).view(np.uint32), wq ^ np.uint32(0x88888888))
+
+
+@pytest.mark.parametrize("R,D,eps", [(1, 2048, 1e-6), (16, 5120, 1e-6), (37, 333, 0.0), (5, 64, 7.0)])
+def test_rmsnorm(R, D, eps):
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(80 + R)
+    x = gen.f32_to_bf16((rng.standard_normal((R, D)) * rng.uniform(0.1, 10, (R, 1))).astype(np.float32))
+    w = gen.f32_to_bf16(rng.uniform(0.5, 2.0, D).astype(np.float32))
+    y = g.host(ops.rmsnorm(g.dev(x), g.dev(w), eps))
+    yr = orc.rmsnorm(x, w, eps)
+    # the fp32 sum of squares runs in another order than the oracle's: within one bf16 step of its output
+    assert gen.bf16_err(y, yr, ref_is_bf16=True) == 0.0
+    assert np.mean(y == yr) > 0.98

@@ -194,6 +194,37 @@ def test_silu_mul_closed_form():
     assert np.all(np.abs(h - ref) <= 2 ** -7 * np.abs(ref) + 1e-30)
 
 
+def test_rmsnorm_exact_rows():
+    """Rows whose RMS norm is exact: a mistake in the mean (D vs D - 1), the root, where eps enters, or the weight
+    index changes one of these outputs."""
+    rng = np.random.default_rng(3)
+    D = 16
+    w = gen.f32_to_bf16(rng.uniform(0.5, 2.0, D).astype(np.float32))
+    wf = gen.bf16_to_f32(w)
+    x = np.zeros((3, D), np.float32)
+    x[0, :] = 4.0                   # constant 2^k, eps = 0: r = 1/4, out = w exactly
+    x[1, 5] = 2.0                   # one-hot c e_i: mean = c^2 / D, r = sqrt(D) / c = 2, out_i = 4 w_i
+    x[2, :] = -0.5                  # sign kept
+    out = gen.bf16_to_f32(orc.rmsnorm(gen.f32_to_bf16(x), w, 0.0))
+    assert np.array_equal(out[0], wf)
+    want1 = np.zeros(D, np.float32)
+    want1[5] = 4.0 * wf[5]
+    assert np.array_equal(out[1], want1)
+    assert np.array_equal(out[2], -wf)
+    # eps inside the root, added to the mean square: c = 3, eps = 7 -> r = 1 / 4, out = 0.75 w
+    x3 = np.full((1, D), 3.0, np.float32)
+    out3 = gen.bf16_to_f32(orc.rmsnorm(gen.f32_to_bf16(x3), w, 7.0))
+    assert np.array_equal(out3[0], gen.bf16_to_f32(gen.f32_to_bf16(0.75 * wf)))
+
+
+def test_rmsnorm_scale_invariance():
+    rng = np.random.default_rng(4)
+    x = gen.f32_to_bf16(rng.standard_normal((3, 64)).astype(np.float32))
+    w = gen.f32_to_bf16(rng.uniform(0.5, 2.0, 64).astype(np.float32))
+    xs = gen.f32_to_bf16(gen.bf16_to_f32(x) * 8.0)  # exact power-of-two scaling
+    assert np.array_equal(orc.rmsnorm(x, w, 0.0), orc.rmsnorm(xs, w, 0.0))
+
+
 # ---- MoE ------------------------------------------------------------------------------------------------------------
 def _brute_topk(l: np.ndarray, k: int):
     order = np.lexsort((np.arange(l.size), -l.astype(np.float64)))  # logit desc, then index asc

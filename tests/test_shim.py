@@ -1,0 +1,33 @@
+"""The C++ operator shim (inferd_amd/csrc/qwen35_ops.h: Qwen35::gemm / Qwen35::encode_moe with the reference's
+signatures, engine/src/qwen35.h:1465, 1869) through its C++ test program, tests/cpp/qwen35_ops_test.cpp.
+
+The program is built by tests/cpp/build.py (``__graft_entry__.build()`` runs it)."""
+import os
+import subprocess
+
+import pytest
+
+BIN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "qwen35_ops_test")
+
+
+def _need_bin():
+    if not os.path.exists(BIN):
+        pytest.skip("tests/cpp/qwen35_ops_test is not built (python tests/cpp/build.py)")
+
+
+def test_gemm_rejects_non_4bit_like_the_reference():
+    """The reference prints the reason and exits with status 1 on a route it cannot take (qwen35.h:1469, 1477)."""
+    _need_bin()
+    r = subprocess.run([BIN, "--bad-bits"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
+    assert "8-bit weights are outside this path" in r.stderr
+
+
+@pytest.mark.gpu
+def test_shim_gemm_and_encode_moe_parity():
+    """gemm() on the MLX layout (every mode, flipped, rows_of / kslice_of views) and on the T64 copy, and encode_moe()
+    (rmsnorm, bit-exact routing, x += MoE output) against the CPU oracle."""
+    assert os.path.exists(BIN), "tests/cpp/qwen35_ops_test is not built"
+    r = subprocess.run([BIN], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    assert r.returncode == 0 and "ALL OK" in r.stdout, r.stdout + r.stderr
