@@ -231,6 +231,24 @@ def _brute_topk(l: np.ndarray, k: int):
     return order[:k]
 
 
+def test_router_gemm_one_hot_and_numpy():
+    """Router logits (bf16 x bf16, fp32 accumulation): a one-hot row returns one weight column exactly; random rows
+    match numpy's float64 matmul of the same bf16 values within fp32 accumulation error."""
+    rng = np.random.default_rng(11)
+    E1, H = 33, 256
+    W = gen.f32_to_bf16((rng.standard_normal((E1, H)) * 0.02).astype(np.float32))
+    x = np.zeros((2, H), np.float32)
+    x[0, 17] = 1.0
+    x[1, 200] = -2.0
+    y = orc.gemm_bf16(gen.f32_to_bf16(x), W)
+    Wf = gen.bf16_to_f32(W)
+    assert np.array_equal(y[0], Wf[:, 17]) and np.array_equal(y[1], -2.0 * Wf[:, 200])
+    A = gen.activations(9, H, seed=12)
+    y = orc.gemm_bf16(A, W).astype(np.float64)
+    ref = gen.bf16_to_f32(A).astype(np.float64) @ Wf.astype(np.float64).T
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.sqrt(np.mean(ref ** 2))
+
+
 @pytest.mark.parametrize("bf", [False, True])
 def test_route_brute_force(bf):
     rng = np.random.default_rng(3)
