@@ -112,3 +112,22 @@ def test_gemm_t64_config2_sampled():
     rows = np.linspace(0, M - 1, 16).astype(int)
     err = gen.bf16_err(out[rows], orc.qmm(A[rows], wq, s, b))
     assert err <= 1e-2, err
+
+
+def test_split_k_is_deterministic():
+    """K-split T64 GEMMs (fp32 partials, then a reduce in split order) give identical bits on repeated calls and match
+    the oracle on sampled rows, at the decode MLP's split shapes."""
+    from inferd_amd._lib import lib
+    g, ops = _gu(), _ops()
+    shapes = [(1, 5120, 17408), (8, 34816, 5120), (32, 5120, 17408), (128, 5120, 17408)]
+    assert all(lib().ifd_gemm_t64_workspace(M, N, K) > 0 for M, N, K in shapes)  # all of them split K
+    for M, N, K in shapes:
+        codes, wq, s, b = gen.qlinear(N, K, seed=M + 3)
+        T = ops.pack_t64(g.qlinear(wq, s, b))
+        A = g.dev(gen.activations(M, K, seed=M + 4))
+        outs = [g.host(ops.gemm_t64(A, T)) for _ in range(3)]
+        torch.cuda.synchronize()
+        assert all(np.array_equal(outs[0], o) for o in outs[1:]), (M, N, K)
+        rows = np.arange(0, M, max(1, M // 4))
+        Y = (orc.qmv if M <= 64 else orc.qmm)(np.ascontiguousarray(g.host(A)[rows]), wq, s, b)
+        assert gen.bf16_err(outs[0][rows], Y) <= 1e-2, (M, N, K)
