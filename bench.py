@@ -37,7 +37,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--no-breakdown", action="store_true", help="headline workload only")
-    p.add_argument("--only", default="", help="profiling: run one config only (c0, c1, c2, c3, c4)")
+    p.add_argument("--only", default="",
+                   help="profiling: run one config only (c0, c1, c2, c3, c4), or 'copy' (256 MiB device copy that "
+                        "calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
 
 
@@ -87,6 +89,15 @@ def main():
 
     out = {}
     Ms = (1, 8, 32, 128)
+
+    if args.only == "copy":
+        # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain device copy of exactly 256 MiB each way
+        src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).normal_(generator=gen)
+        dst = torch.empty_like(src)
+        ms = timed(lambda i: dst.copy_(src), 20, 3)
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 2, "us": round(ms * 1e3, 2),
+                          "gbs": round(2 * src.numel() * 2 / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return
 
     # ---- headline: decode MLP (config 1) -----------------------------------------------------------------------
     if args.only in ("", "c1"):

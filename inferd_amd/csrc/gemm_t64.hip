@@ -3,15 +3,19 @@
 // Replaces the reference's MLX affine_qmm_t_nax (third_party/mlx/.../quantized_nax.h:938-1076, 1206-1267) and its
 // split-K variant (engine/kernels/qmm_splitk.metal:14-107) for T64-packed weights.
 //
-// Block: 4 waves (one per SIMD); block tile BM = 32 MT rows x 4 NB bands (128 NB columns), each wave owning NB bands;
-// grid x = tiles (XCD-contiguous runs, bands of kGtBand M tiles walked M-fastest), grid y = K splits.
-// K advances in chunks of two 64-groups through a kGtNS-stage LDS ring filled by direct global->LDS DMA
-// (global_load_lds_dwordx4): per chunk the activation slab [BM][128 bf16] (16-byte columns XOR-swizzled by row so
-// that the MFMA fragment reads are bank-conflict free), the code halves of the two groups' T64 tiles of the block's
-// bands, and per wave one 1 KB area with the (s, b) dwords of its 2 NB tiles. Loads run kGtNS - 1 chunks ahead and
-// cost no VGPRs; each chunk needs one s_barrier.
-// Every DMA is issued by the full wave under uniform control flow: the LDS destination goes to M0, which is one value
-// per wave, and a DMA under a lane-dependent branch may be merged by the compiler with another one whose destination
+// Block: 8 waves, two per SIMD; block tile BM = 32 MT rows x NBB = 4 NB bands (128 NB columns); grid x = tiles
+// (XCD-contiguous runs, bands of kGtBand M tiles walked M-fastest), grid y = K splits.
+// K advances in chunks of two 64-groups. The waves form two quads: quad kq (= wave / 4) takes group kq of every
+// chunk, and wave wq (= wave % 4) of a quad the bands wq NB .. + NB - 1 over all BM rows. The two waves on a SIMD thus
+// work on the same outputs at different K, and their instruction streams interleave (one's dequant VALU and LDS
+// reads under the other's MFMAs). At the end quad 1 adds its sums into quad 0's through LDS.
+// Chunks flow through a kGtNS-stage LDS ring filled by direct global->LDS DMA (global_load_lds_dwordx4), kGtNS - 1
+// chunks ahead, at no VGPR cost, with one s_barrier per chunk. A stage holds the activation slab [BM][128 bf16]
+// (16-byte columns XOR-swizzled by row: conflict-free fragment reads), the code halves of the chunk's 2 NBB T64
+// tiles, and their (s, b) dwords [2 groups][1 KB]. Per chunk every wave DMAs MT activation row quads and its own NB
+// code tiles; waves 0 and 1 also the (s, b) dwords of group 0 and 1.
+// Every DMA is issued by a whole wave under wave-uniform control flow: the LDS destination goes to M0, one value per
+// wave, and a DMA under a lane-dependent branch may be merged by the compiler with another one whose destination
 // differs, leaving one M0 for both.
 //  DEQ = false (affine): codes enter the MFMA as exact bf16 (128 + q); per group the fp32 epilogue adds
 //    s P + (b - 128 s) X, with X (the activation group sums) from a second MFMA against ones: the decode GEMV
@@ -41,8 +45,11 @@ struct GemmTArgs {
 
 constexpr int kGtBand = 4;  // M tiles per band of the tile order
 constexpr int kGtNS = 3;    // LDS pipeline stages
+constexpr int kGtThreads = 512;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
 
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
@@ -54,10 +61,6 @@ template <int N>
 __device__ __forceinline__ void wait_vm_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 __device__ __forceinline__ u32x4 t64_off128(uint32_t w) {
   u32x4 r;
@@ -65,29 +68,50 @@ __device__ __forceinline__ u32x4 t64_off128(uint32_t w) {
   for (int i = 0; i < 4; i++) r[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
   return r;
 }
-// eight T64 codes (one word) -> bf16(s q + b) in natural k order
-__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float s, float b) {
+// Masks for t64_dequant, held in VGPRs: a VOP3 and-or takes at most one scalar or literal operand on this ISA, so
+// with both constants in VGPRs each code costs one v_and_or_b32 (the opaque moves keep the compiler from folding them
+// back into literals).
+struct DeqMasks {
+  uint32_t nib16, f128;
+};
+__device__ __forceinline__ DeqMasks deq_masks() {
+  DeqMasks m;
+  asm volatile("v_mov_b32 %0, 0x000f0000" : "=v"(m.nib16));
+  asm volatile("v_mov_b32 %0, 0x43000000" : "=v"(m.f128));
+  return m;
+}
+// Eight T64 codes (one word) -> bf16(s q + b) in natural k order, with bp = b - 128 s. Each code is shifted to bits
+// 16-19 and masked into the fp32 value 128 + q (0x43000000 | q << 16); s (128 + q) is exact, so fma(s, 128 + q, bp)
+// rounds s q + b once whenever b - 128 s is exact in fp32 (always for b = -8 s). Pairs are packed by one two-input
+// conversion. Code 2i sits in nibble i, code 2i + 1 in nibble i + 4 (t64.h).
+__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float s, float bp, DeqMasks m) {
+  const uint32_t lo_src[4] = {w << 16, w << 12, w << 8, w << 4};  // nibble i at bits 16-19
+  const uint32_t hi_src[4] = {w, w >> 4, w >> 8, w >> 12};        // nibble i + 4 at bits 16-19
   u32x4 r;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const uint32_t pr = (w >> (4 * i)) & 0x000F000Fu;
-    r[i] = pack_bf2(__builtin_fmaf(s, (float)(pr & 0xFFu), b), __builtin_fmaf(s, (float)(pr >> 16), b));
+    f32x2 f;
+    f.x = __builtin_fmaf(s, __uint_as_float((lo_src[i] & m.nib16) | m.f128), bp);
+    f.y = __builtin_fmaf(s, __uint_as_float((hi_src[i] & m.nib16) | m.f128), bp);
+    r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
   }
   return r;
 }
 
 template <int MT, int NB, bool DEQ>
-__global__ __launch_bounds__(256, 1) void k_gemm_t(GemmTArgs p) {
-  static_assert(NB >= 1 && NB <= 4, "one (s, b) DMA per wave covers at most 8 tiles");
+__global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
+  static_assert(NB >= 1 && NB <= 2, "one (s, b) DMA covers a group's NBB <= 8 tiles");
   constexpr int BM = 32 * MT, NBB = 4 * NB;
   constexpr int A_BYTES = BM * 256;             // [BM][128 bf16]
   constexpr int C_BYTES = 2 * NBB * kT64Codes;  // [2 groups][NBB bands][1024]
-  constexpr int ST = A_BYTES + C_BYTES + 4 * 1024;  // + [4 waves][1 KB] (s, b) areas
-  constexpr int AI = BM / 16;                   // activation DMA instructions per wave per chunk (4 rows each)
-  constexpr int VPC = AI + 2 * NB + 1;          // DMA instructions per wave per chunk
+  constexpr int ST = A_BYTES + C_BYTES + 2 * 1024;  // + [2 groups][1 KB] (s, b)
+  constexpr int VPC = MT + NB;                  // DMA instructions per wave per chunk (waves 0, 1: one more)
+  constexpr int NE = MT * NB * 16;              // accumulators per lane
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
+  // wave-uniform (SGPR) so that every DMA destination, which goes to M0, is computed as a scalar
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kq = wave >> 2, wq = wave & 3;
   const int j = lane & 31, h = lane >> 5;
 
   const int ntiles = p.tiles_m * p.tiles_n;
@@ -102,41 +126,37 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(GemmTArgs p) {
   const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps);
   const int nch = (g1 - g0) / 2, lastg = g0 + 2 * (nch - 1);
 
-  // activation DMA: instruction i of this wave covers rows 4 (wave AI + i) .. + 3; lane -> LDS slot lane of that
-  // 1 KB: row r = 4 (wave AI + i) + lane / 16, physical 16-byte column lane % 16 holding logical column
+  // activation DMA: instruction i of this wave covers rows 4 (wave MT + i) .. + 3; lane -> LDS slot lane of that
+  // 1 KB: row r = 4 (wave MT + i) + lane / 16, physical 16-byte column lane % 16 holding logical column
   // (lane % 16) ^ (r % 16). Rows past M re-read row M - 1 (finite data; their outputs are not stored).
-  const uint16_t* asrc[AI];
+  const uint16_t* asrc[MT];
 #pragma unroll
-  for (int i = 0; i < AI; i++) {
-    const int r = 4 * (wave * AI + i) + lane / 16;
+  for (int i = 0; i < MT; i++) {
+    const int r = 4 * (wave * MT + i) + lane / 16;
     const int c = (lane & 15) ^ (r & 15);
     asrc[i] = p.A + (size_t)min(m0 + r, p.M - 1) * p.lda + 8 * c;
   }
-  // code DMA: this wave's NB bands (bands past the end re-read the last band; their outputs are not stored)
+  // code DMA: this wave's NB bands of group kq (bands past the end re-read the last band; not stored)
+  const size_t gstride = (size_t)nbands * kT64Tile;
   const uint8_t* tb[NB];
 #pragma unroll
-  for (int b = 0; b < NB; b++) tb[b] = p.wt + (size_t)min(tn * NBB + wave * NB + b, nbands - 1) * kT64Tile;
-  const size_t gstride = (size_t)nbands * kT64Tile;
-  // (s, b) DMA: lane -> tile q = (lane mod 16 NB) / 8 = gi NB + b, 16-byte part lane % 8 of its 128 bytes; lanes
-  // from 16 NB on repeat the first ones (the full wave issues every DMA)
-  const uint8_t* sbsrc;
-  {
-    const int q = (lane % (16 * NB)) / 8, gi = q / NB, b = q % NB;
-    sbsrc = p.wt + (size_t)min(tn * NBB + wave * NB + b, nbands - 1) * kT64Tile + kT64Codes + 16 * (lane & 7) +
-            (size_t)gi * gstride;
-  }
+  for (int b = 0; b < NB; b++)
+    tb[b] = p.wt + (size_t)min(tn * NBB + wq * NB + b, nbands - 1) * kT64Tile + (size_t)kq * gstride + 16 * lane;
+  // (s, b) DMA (waves 0 and 1, group = wave): lane -> band (lane mod 8 NBB) / 8, 16-byte part lane % 8; lanes from
+  // 8 NBB on repeat the first ones
+  const uint8_t* sbsrc = p.wt +
+                         (size_t)min(tn * NBB + (lane % (8 * NBB)) / 8, nbands - 1) * kT64Tile + kT64Codes +
+                         16 * (lane & 7) + (size_t)(wave & 1) * gstride;
 
   auto issue = [&](int chunk, int stage) {
     const size_t g = (size_t)min(g0 + 2 * chunk, lastg);
     uint8_t* st = lds + stage * ST;
 #pragma unroll
-    for (int i = 0; i < AI; i++) dma16(asrc[i] + g * kGroup, st + (wave * AI + i) * 1024);
+    for (int i = 0; i < MT; i++) dma16(asrc[i] + g * kGroup, st + (wave * MT + i) * 1024);
 #pragma unroll
-    for (int gi = 0; gi < 2; gi++)
-#pragma unroll
-      for (int b = 0; b < NB; b++)
-        dma16(tb[b] + (g + gi) * gstride + 16 * lane, st + A_BYTES + (gi * NBB + wave * NB + b) * kT64Codes);
-    dma16(sbsrc + g * gstride, st + A_BYTES + C_BYTES + wave * 1024);
+    for (int b = 0; b < NB; b++)
+      dma16(tb[b] + g * gstride, st + A_BYTES + (kq * NBB + wq * NB + b) * kT64Codes);
+    if (wave < 2) dma16(sbsrc + g * gstride, st + A_BYTES + C_BYTES + wave * 1024);
   };
 
   f32x16 acc[MT][NB];
@@ -146,72 +166,116 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(GemmTArgs p) {
     for (int b = 0; b < NB; b++) acc[a][b] = zero16();
   u32x4 ones;
   ones[0] = ones[1] = ones[2] = ones[3] = 0x3F803F80u;
+  const DeqMasks dm = deq_masks();
+
+  // B fragments of band b (of this wave's NB) of group kq in a stage: codes -> bf16 (dequant or 128 + q), and
+  // (s, b - 128 s)
+  auto load_band = [&](const uint8_t* st, int b, u32x4 (&bf)[4], float& sc, float& bp) {
+    const int band = wq * NB + b;
+    const u32x4 codes = *(const u32x4*)(st + A_BYTES + (kq * NBB + band) * kT64Codes + 16 * lane);
+    const uint32_t sb = *(const uint32_t*)(st + A_BYTES + C_BYTES + kq * 1024 + band * 128 + 4 * j);
+    sc = bf2f((uint16_t)(sb & 0xFFFFu));
+    bp = __builtin_fmaf(-128.f, sc, bf2f((uint16_t)(sb >> 16)));
+#pragma unroll
+    for (int t = 0; t < 4; t++) bf[t] = DEQ ? t64_dequant(codes[t], sc, bp, dm) : t64_off128(codes[t]);
+  };
+  // activation fragments of M tile a of group kq in a stage
+  auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) {
+    const int r = a * 32 + j;
+#pragma unroll
+    for (int t = 0; t < 4; t++) af[t] = *(const u32x4*)(st + r * 256 + 16 * ((kq * 8 + 4 * h + t) ^ (r & 15)));
+  };
 
   auto compute = [&](int stage) {
     const uint8_t* st = lds + stage * ST;
+    if (DEQ) {
+      // bands outermost: one band's fragments live at a time, and band b + 1's dequant (VALU) overlaps band b's
+      // MFMAs; the activation fragments are re-read per band (LDS has the bandwidth) and double-buffered
+      u32x4 bcur[4], bnext[4];
+      float sc0, bp0, sc1, bp1;
+      load_band(st, 0, bcur, sc0, bp0);
 #pragma unroll
-    for (int gi = 0; gi < 2; gi++) {
+      for (int b = 0; b < NB; b++) {
+        if (b + 1 < NB) load_band(st, b + 1, bnext, sc1, bp1);
+        u32x4 af[2][4];
+        load_a(st, 0, af[0]);
+#pragma unroll
+        for (int a = 0; a < MT; a++) {
+          if (a + 1 < MT) load_a(st, a + 1, af[(a + 1) & 1]);
+#pragma unroll
+          for (int t = 0; t < 4; t++) acc[a][b] = mfma_bf16(af[a & 1][t], bcur[t], acc[a][b]);
+        }
+        if (b + 1 < NB) {
+#pragma unroll
+          for (int t = 0; t < 4; t++) bcur[t] = bnext[t];
+        }
+      }
+      (void)sc0, (void)bp0, (void)sc1, (void)bp1;
+    } else {
       float sc[NB], bp[NB];
       u32x4 bfr[NB][4];
 #pragma unroll
-      for (int b = 0; b < NB; b++) {
-        const u32x4 codes = *(const u32x4*)(st + A_BYTES + (gi * NBB + wave * NB + b) * kT64Codes + 16 * lane);
-        const uint32_t sb = *(const uint32_t*)(st + A_BYTES + C_BYTES + wave * 1024 + (gi * NB + b) * 128 + 4 * j);
-        sc[b] = bf2f((uint16_t)(sb & 0xFFFFu));
-        const float bi = bf2f((uint16_t)(sb >> 16));
-        bp[b] = DEQ ? bi : __builtin_fmaf(-128.f, sc[b], bi);
-#pragma unroll
-        for (int t = 0; t < 4; t++) bfr[b][t] = DEQ ? t64_dequant(codes[t], sc[b], bi) : t64_off128(codes[t]);
-      }
+      for (int b = 0; b < NB; b++) load_band(st, b, bfr[b], sc[b], bp[b]);
 #pragma unroll
       for (int a = 0; a < MT; a++) {
-        const int r = a * 32 + j;
-        const uint8_t* arow = st + r * 256;
         u32x4 af[4];
+        load_a(st, a, af);
+        f32x16 X = zero16();
 #pragma unroll
-        for (int t = 0; t < 4; t++) af[t] = *(const u32x4*)(arow + 16 * ((gi * 8 + 4 * h + t) ^ (r & 15)));
-        if (DEQ) {
+        for (int t = 0; t < 4; t++) X = mfma_bf16(af[t], ones, X);
 #pragma unroll
-          for (int b = 0; b < NB; b++)
+        for (int b = 0; b < NB; b++) {
+          f32x16 P = zero16();
 #pragma unroll
-            for (int t = 0; t < 4; t++) acc[a][b] = mfma_bf16(af[t], bfr[b][t], acc[a][b]);
-        } else {
-          f32x16 X = zero16();
+          for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], bfr[b][t], P);
 #pragma unroll
-          for (int t = 0; t < 4; t++) X = mfma_bf16(af[t], ones, X);
-#pragma unroll
-          for (int b = 0; b < NB; b++) {
-            f32x16 P = zero16();
-#pragma unroll
-            for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], bfr[b][t], P);
-#pragma unroll
-            for (int r2 = 0; r2 < 16; r2++)
-              acc[a][b][r2] = __builtin_fmaf(sc[b], P[r2], __builtin_fmaf(bp[b], X[r2], acc[a][b][r2]));
-          }
+          for (int r2 = 0; r2 < 16; r2++)
+            acc[a][b][r2] = __builtin_fmaf(sc[b], P[r2], __builtin_fmaf(bp[b], X[r2], acc[a][b][r2]));
         }
       }
     }
   };
 
   // Every iteration issues one chunk (past the end: a re-read of the last chunk into a stage nobody reads again), so
-  // the count of outstanding DMA instructions is the same on every path: waiting for VPC * (kGtNS - 2) leaves the
-  // younger chunks in flight. The LDS reads of the previous chunk finish before the barrier that lets any wave
-  // overwrite that stage.
+  // each wave's count of outstanding DMA instructions is the same on every iteration: waiting for its DMAs of
+  // kGtNS - 2 chunks leaves the younger chunks in flight. The LDS reads of the previous chunk finish before the
+  // barrier that lets any wave overwrite that stage.
 #pragma unroll
   for (int s = 0; s < kGtNS - 1; s++) issue(s, s);
   for (int c = 0; c < nch; c++) {
-    wait_vm_barrier<VPC * (kGtNS - 2)>();
+    if (wave < 2) wait_vm_barrier<(VPC + 1) * (kGtNS - 2)>();
+    else wait_vm_barrier<VPC * (kGtNS - 2)>();
     issue(c + kGtNS - 1, (c + kGtNS - 1) % kGtNS);
     compute(c % kGtNS);
   }
-  wait_vm<0>();  // no DMA may still target this block's LDS when it exits
+  // no DMA may still target LDS and every wave's fragment reads are done before LDS is reused for the sums
+  wait_vm_barrier<0>();
+
+  // quad 1 hands its sums to quad 0 (lane-contiguous dwords: conflict-free)
+  float* red = (float*)lds + (size_t)wq * NE * 64 + lane;
+  if (kq == 1) {
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) red[((a * NB + b) * 16 + r) * 64] = acc[a][b][r];
+  }
+  __syncthreads();
+  if (kq == 1) return;
+#pragma unroll
+  for (int a = 0; a < MT; a++)
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[a][b][r] += red[((a * NB + b) * 16 + r) * 64];
 
   const bool split = gridDim.y > 1;
 #pragma unroll
   for (int a = 0; a < MT; a++)
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-      const int col = (tn * NBB + wave * NB + b) * 32 + j;
+      const int col = (tn * NBB + wq * NB + b) * 32 + j;
       if (col >= p.N) continue;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
@@ -258,13 +322,15 @@ size_t gemm_t_workspace(int M, int N, int K) {
 
 template <int MT, int NB, bool DEQ>
 static int launch_gemm_t_cfg(const GemmTArgs& p, int S, hipStream_t st) {
-  const size_t lds = (size_t)kGtNS * (32 * MT * 256 + 2 * 4 * NB * kT64Codes + 4 * 1024);
+  const size_t pipe = (size_t)kGtNS * (32 * MT * 256 + 2 * 4 * NB * kT64Codes + 2 * 1024);
+  const size_t red = (size_t)4 * MT * NB * 16 * 64 * sizeof(float);  // quad 1's sums, after the K loop
+  const size_t lds = std::max(pipe, red);
   static bool attr = false;
   if (!attr) {
     hipFuncSetAttribute((const void*)k_gemm_t<MT, NB, DEQ>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr = true;
   }
-  hipLaunchKernelGGL((k_gemm_t<MT, NB, DEQ>), dim3(p.tiles_m * p.tiles_n, S), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((k_gemm_t<MT, NB, DEQ>), dim3(p.tiles_m * p.tiles_n, S), dim3(kGtThreads), lds, st, p);
   return check_launch("gemm_t64");
 }
 
