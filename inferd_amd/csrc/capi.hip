@@ -88,7 +88,7 @@ int ifd_flip_w4(uint32_t* wq, size_t n32, uint32_t mask, void* stream) {
 int ifd_silu_mul(const void* gu, void* h, int I, int rows, void* stream) {
   IFD_CHECK(I > 0 && I % 8 == 0 && rows >= 0, "bad shape I=%d rows=%d (I must be a multiple of 8)", I, rows);
   IFD_CHECK(rows == 0 || (gu && h && aligned(gu, 16) && aligned(h, 16)), "gu and h must be 16-byte aligned");
-  return launch_silu_mul((const uint16_t*)gu, (uint16_t*)h, I, rows, S(stream));
+  return launch_silu_mul((const uint16_t*)gu, 2 * I, (uint16_t*)h, I, I, rows, S(stream));
 }
 
 int ifd_rmsnorm(const void* x, int in_stride, const void* w, void* out, int out_stride, int rows, int D, float eps,
@@ -136,7 +136,25 @@ int ifd_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N
 
 size_t ifd_gemm_t64_workspace(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  return M <= 16 ? qmv_t_workspace(M, N, K) : gemm_t_workspace(M, N, K);
+  return M <= 16 ? qmv_t_workspace(M, N, K, 0) : gemm_t_workspace(M, N, K, 0);
+}
+
+size_t ifd_gemm_t64_swiglu_workspace(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  return M <= 16 ? qmv_t_workspace(M, N, K, kModeSwiglu) : gemm_t_workspace(M, N, K, kModeSwiglu);
+}
+
+int ifd_gemm_t64_swiglu(const void* A, int lda, const void* wt, int N, int K, void* H, int ldh, int M,
+                        void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(M >= 0 && N > 0 && K > 0 && K % 256 == 0 && N % 16 == 0,
+            "bad shape M=%d N=%d K=%d (K multiple of 256, N = 2 I with I a multiple of 8)", M, N, K);
+  IFD_CHECK(lda >= K && lda % 8 == 0 && ldh >= N / 2 && ldh % 8 == 0, "bad strides lda=%d ldh=%d", lda, ldh);
+  if (M == 0) return IFD_OK;
+  IFD_CHECK(A && wt && H && aligned(A, 16) && aligned(wt, 16) && aligned(H, 16), "null or misaligned pointer");
+  IFD_CHECK(!workspace || aligned(workspace, 16), "workspace must be 16-byte aligned");
+  if (M <= 16)
+    return launch_qmv_t((const uint16_t*)A, lda, wt, N, K, H, ldh, M, kModeSwiglu, workspace, ws_bytes, S(stream));
+  return launch_gemm_t((const uint16_t*)A, lda, wt, N, K, H, ldh, M, kModeSwiglu, workspace, ws_bytes, S(stream));
 }
 
 int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
@@ -273,7 +291,7 @@ int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, 
   if (shared) {
     IFD_TRY(ifd_gemm_w4(xn, H, sgu_wq, sgu_s, sgu_b, 2 * Is, H, 0, 0, w + L.sh_gu, 2 * Is, T, 0, w + L.sh_ws,
                         ifd_gemm_w4_workspace(T, 2 * Is, H), stream));
-    IFD_TRY(launch_silu_mul((const uint16_t*)(w + L.sh_gu), (uint16_t*)(w + L.sh_act), Is, T, st));
+    IFD_TRY(launch_silu_mul((const uint16_t*)(w + L.sh_gu), 2 * Is, (uint16_t*)(w + L.sh_act), Is, Is, T, st));
     IFD_TRY(ifd_gemm_w4(w + L.sh_act, Is, sdn_wq, sdn_s, sdn_b, H, Is, 0, 0, w + L.ys, H, T, 0, w + L.sh_ws,
                         ifd_gemm_w4_workspace(T, H, Is), stream));
     ys = (const uint16_t*)(w + L.ys);

@@ -18,9 +18,16 @@ constexpr int kGroup = 64;  // MLX affine group size along K
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 // fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
 __device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+// two fp32 -> packed bf16 pair (lo in bits 0-15), round to nearest even: one two-input v_cvt_pk_bf16_f32
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  const f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
+// SwiGLU of one bf16 (gate, up) pair: bf16(float(bf16(g / (1 + exp(-g)))) * u) (reference silu_mul,
+// engine/kernels/core.metal:777-787)
+__device__ __forceinline__ float swiglu_f(float g, float u) { return bf2f(f2bf(g / (1.f + expf(-g)))) * u; }
 
 // D(32x32 fp32) += A(32x16 bf16) * B(16x32 bf16). Lane l holds A row (l % 32), B column (l % 32), eight consecutive
 // k values 8 * (l / 32) .. +7 of the 16; D row 8 * (r / 4) + 4 * (l / 32) + (r % 4), column l % 32, for r = 0..15.

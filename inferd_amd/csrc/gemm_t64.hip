@@ -48,8 +48,6 @@ constexpr int kGtNS = 3;    // LDS pipeline stages
 constexpr int kGtThreads = 512;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-typedef __attribute__((ext_vector_type(2))) float f32x2;
 
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
@@ -68,34 +66,22 @@ __device__ __forceinline__ u32x4 t64_off128(uint32_t w) {
   for (int i = 0; i < 4; i++) r[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
   return r;
 }
-// Masks for t64_dequant, held in VGPRs: a VOP3 and-or takes at most one scalar or literal operand on this ISA, so
-// with both constants in VGPRs each code costs one v_and_or_b32 (the opaque moves keep the compiler from folding them
-// back into literals).
-struct DeqMasks {
-  uint32_t nib16, f128;
-};
-__device__ __forceinline__ DeqMasks deq_masks() {
-  DeqMasks m;
-  asm volatile("v_mov_b32 %0, 0x000f0000" : "=v"(m.nib16));
-  asm volatile("v_mov_b32 %0, 0x43000000" : "=v"(m.f128));
-  return m;
-}
-// Eight T64 codes (one word) -> bf16(s q + b) in natural k order, with bp = b - 128 s. Each code is shifted to bits
-// 16-19 and masked into the fp32 value 128 + q (0x43000000 | q << 16); s (128 + q) is exact, so fma(s, 128 + q, bp)
-// rounds s q + b once whenever b - 128 s is exact in fp32 (always for b = -8 s). Pairs are packed by one two-input
-// conversion. Code 2i sits in nibble i, code 2i + 1 in nibble i + 4 (t64.h).
-__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float s, float bp, DeqMasks m) {
-  const uint32_t lo_src[4] = {w << 16, w << 12, w << 8, w << 4};  // nibble i at bits 16-19
-  const uint32_t hi_src[4] = {w, w >> 4, w >> 8, w >> 12};        // nibble i + 4 at bits 16-19
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    f32x2 f;
-    f.x = __builtin_fmaf(s, __uint_as_float((lo_src[i] & m.nib16) | m.f128), bp);
-    f.y = __builtin_fmaf(s, __uint_as_float((hi_src[i] & m.nib16) | m.f128), bp);
-    r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
-  }
-  return r;
+// Eight T64 codes (one word) -> bf16(s q + b) in natural k order. Code 2i sits in nibble i, code 2i + 1 in nibble
+// i + 4 (t64.h), so the low nibbles of the four bytes hold codes 0, 4, 1, 5 and the high nibbles codes 2, 6, 3, 7.
+// Two masks split the word into bytes; one byte -> fp32 conversion per code (v_cvt_f32_ubyte0..3) gives q, or 16 q for
+// the high nibbles, which take s / 16 (exact: a power-of-two scaling of a bf16); fma rounds s q + b once in fp32, as
+// the bf16(fp32(s q + b)) of the MLX loader. 22 VALU instructions per 8 codes, two of them integer ops: integer VALU
+// co-issues poorly beside MFMA, conversions and fma well. The masks go through opaque moves so that the compiler
+// selects the byte conversions instead of folding the masks into bitfield extracts.
+__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float s, float s16, float b) {
+  uint32_t lo, hi;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
+  asm("v_and_b32 %0, 0xf0f0f0f0, %1" : "=v"(hi) : "v"(w));
+  const float c0 = __builtin_fmaf(s, (float)(lo & 0xFFu), b), c4 = __builtin_fmaf(s, (float)((lo >> 8) & 0xFFu), b);
+  const float c1 = __builtin_fmaf(s, (float)((lo >> 16) & 0xFFu), b), c5 = __builtin_fmaf(s, (float)(lo >> 24), b);
+  const float c2 = __builtin_fmaf(s16, (float)(hi & 0xFFu), b), c6 = __builtin_fmaf(s16, (float)((hi >> 8) & 0xFFu), b);
+  const float c3 = __builtin_fmaf(s16, (float)((hi >> 16) & 0xFFu), b), c7 = __builtin_fmaf(s16, (float)(hi >> 24), b);
+  return u32x4{pack_bf2(c0, c1), pack_bf2(c2, c3), pack_bf2(c4, c5), pack_bf2(c6, c7)};
 }
 
 template <int MT, int NB, bool DEQ>
@@ -166,7 +152,6 @@ __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
     for (int b = 0; b < NB; b++) acc[a][b] = zero16();
   u32x4 ones;
   ones[0] = ones[1] = ones[2] = ones[3] = 0x3F803F80u;
-  const DeqMasks dm = deq_masks();
 
   // B fragments of band b (of this wave's NB) of group kq in a stage: codes -> bf16 (dequant or 128 + q), and
   // (s, b - 128 s)
@@ -175,9 +160,16 @@ __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
     const u32x4 codes = *(const u32x4*)(st + A_BYTES + (kq * NBB + band) * kT64Codes + 16 * lane);
     const uint32_t sb = *(const uint32_t*)(st + A_BYTES + C_BYTES + kq * 1024 + band * 128 + 4 * j);
     sc = bf2f((uint16_t)(sb & 0xFFFFu));
-    bp = __builtin_fmaf(-128.f, sc, bf2f((uint16_t)(sb >> 16)));
+    const float bi = bf2f((uint16_t)(sb >> 16));
+    if (DEQ) {
+      const float s16 = sc * 0.0625f;
 #pragma unroll
-    for (int t = 0; t < 4; t++) bf[t] = DEQ ? t64_dequant(codes[t], sc, bp, dm) : t64_off128(codes[t]);
+      for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sc, s16, bi);
+    } else {
+      bp = __builtin_fmaf(-128.f, sc, bi);
+#pragma unroll
+      for (int t = 0; t < 4; t++) bf[t] = t64_off128(codes[t]);
+    }
   };
   // activation fragments of M tile a of group kq in a stage
   auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) {
@@ -315,9 +307,8 @@ static GtPlan gemm_t_plan(int M, int N, int K) {
   return pl;
 }
 
-size_t gemm_t_workspace(int M, int N, int K) {
-  const GtPlan pl = gemm_t_plan(M, N, K);
-  return pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
+size_t gemm_t_workspace(int M, int N, int K, int mode) {
+  return epilogue_ws_bytes(gemm_t_plan(M, N, K).S, M, N, mode);
 }
 
 template <int MT, int NB, bool DEQ>
@@ -339,18 +330,19 @@ int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void
   if (M == 0) return IFD_OK;
   if (K % 128) return fail(IFD_ERR_ARG, "T64 GEMM needs K %% 128 == 0 (K=%d)", K);
   const GtPlan pl = gemm_t_plan(M, N, K);
-  const size_t need = pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
+  const size_t need = epilogue_ws_bytes(pl.S, M, N, mode);
   if (need > ws_bytes || (need && !ws))
     return fail(IFD_ERR_WORKSPACE, "gemm_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
-  GemmTArgs p{A, lda, (const uint8_t*)wt, N, K, C, ldc, M, mode, (float*)ws, pl.gps,
-              (M + 32 * pl.MT - 1) / (32 * pl.MT), (t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB)};
+  // the SwiGLU mode without a split stores the bf16 product into the workspace for silu_mul
+  const bool via_ws = mode == kModeSwiglu && pl.S == 1;
+  GemmTArgs p{A, lda, (const uint8_t*)wt, N, K, via_ws ? ws : C, via_ws ? N : ldc, M, via_ws ? 0 : mode, (float*)ws,
+              pl.gps, (M + 32 * pl.MT - 1) / (32 * pl.MT), (t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB)};
   int rc;
   if (pl.MT == 1) rc = launch_gemm_t_cfg<1, 2, false>(p, pl.S, st);
   else if (pl.MT == 2) rc = launch_gemm_t_cfg<2, 2, false>(p, pl.S, st);
   else rc = launch_gemm_t_cfg<4, 2, true>(p, pl.S, st);
   IFD_TRY(rc);
-  if (pl.S > 1) return launch_splitk_reduce((const float*)ws, pl.S, M, N, C, ldc, mode, st);
-  return IFD_OK;
+  return launch_epilogue(ws, pl.S, M, N, C, ldc, mode, st);
 }
 
 }  // namespace ifd

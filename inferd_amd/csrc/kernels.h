@@ -31,17 +31,27 @@ int launch_a8_quant(const uint16_t* A, int lda, int M, int K, int per_token, int
 size_t w4a8_workspace(int M, int N, int K);
 int launch_w4a8(const W4Gemm& g, int per_token, void* ws, size_t ws_bytes, hipStream_t st);
 int launch_flip(uint32_t* wq, size_t n32, uint32_t mask, hipStream_t st);
-int launch_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows, hipStream_t st);
+int launch_silu_mul(const uint16_t* gu, int ldgu, uint16_t* h, int ldh, int I, int rows, hipStream_t st);
 int launch_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows,
                    int D, float eps, hipStream_t st);
-// Split-K reduction: C (mode) = sum over S partials [S][M][N] fp32.
+// Library-internal store mode past the public 0 (bf16), 1 (bf16 residual add) and 2 (fp32): the GEMM's N columns are
+// [gate (N/2) | up (N/2)] and C receives the SwiGLU h [M][N/2] (ldc = its row stride), bit-identical to a mode-0 GEMM
+// followed by silu_mul.
+constexpr int kModeSwiglu = 3;
+// Split-K reduction: C (mode) = sum over S partials [S][M][N] fp32, in split order.
 int launch_splitk_reduce(const float* part, int S, int M, int N, void* C, int ldc, int mode, hipStream_t st);
+// Workspace of a GEMM epilogue with S K-splits: the fp32 partials, or for the SwiGLU mode without a split the bf16
+// product [M][N] that silu_mul then reads.
+size_t epilogue_ws_bytes(int S, int M, int N, int mode);
+// After a GEMM kernel that wrote partials (S > 1) or, in the SwiGLU mode, the bf16 product into ws: the reduction or
+// silu_mul into C. Nothing to do otherwise.
+int launch_epilogue(const void* ws, int S, int M, int N, void* C, int ldc, int mode, hipStream_t st);
 
 // T64 layout (t64.h).
 int launch_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr,
                     int E, void* out, hipStream_t st);
-size_t qmv_t_workspace(int M, int N, int K);
-size_t gemm_t_workspace(int M, int N, int K);
+size_t qmv_t_workspace(int M, int N, int K, int mode);
+size_t gemm_t_workspace(int M, int N, int K, int mode);
 int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   void* ws, size_t ws_bytes, hipStream_t st);
 int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode, void* ws,

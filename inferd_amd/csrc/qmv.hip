@@ -300,21 +300,102 @@ __global__ __launch_bounds__(256, 2) void k_qmv_small(QmvArgs p) {
   }
 }
 
+// Sum of the S partials [S][M][N] of V consecutive columns n .. n + V - 1 of row m, in split order.
+template <int V>
+__device__ __forceinline__ void splitk_sum(const float* __restrict__ part, int S, size_t mn, size_t o, float (&v)[V]) {
+#pragma unroll
+  for (int e = 0; e < V; e++) v[e] = 0.f;
+  for (int z = 0; z < S; z++) {
+    const float* q = part + (size_t)z * mn + o;
+    if (V == 4) {
+      const float4 t = *(const float4*)q;
+      v[0] += t.x, v[1] += t.y, v[2] += t.z, v[3] += t.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; e++) v[e] += q[e];
+    }
+  }
+}
+
+// C (mode 0-2) = the split sum; V = 4 columns per thread when N, ldc and C allow vector accesses, else 1.
+template <int V>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, int S, int M, int N, void* C,
                                                        int ldc, int mode) {
+  const int nv = N / V;
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, mn = (size_t)M * N;
-  if (i >= mn) return;
-  const int m = (int)(i / N), n = (int)(i % N);
-  float v = 0.f;
-  for (int z = 0; z < S; z++) v += part[(size_t)z * mn + i];
-  store_mode(C, (size_t)m * ldc + n, v, mode);
+  if (i >= (size_t)M * nv) return;
+  const int m = (int)(i / nv), n = (int)(i % nv) * V;
+  float v[V];
+  splitk_sum<V>(part, S, mn, (size_t)m * N + n, v);
+  const size_t o = (size_t)m * ldc + n;
+  if (V == 4 && mode == 2) {
+    *(float4*)((float*)C + o) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (V == 4 && mode == 0) {
+    *(uint2*)((uint16_t*)C + o) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+  } else {
+#pragma unroll
+    for (int e = 0; e < V; e++) store_mode(C, o + e, v[e], mode);
+  }
+}
+
+// SwiGLU epilogue: N = 2 I partial columns [gate | up]; h[m][i] = swiglu(bf16(sum gate), bf16(sum up)), the bf16
+// rounding of each sum being the mode-0 store of the unfused GEMM.
+template <int V>
+__global__ __launch_bounds__(256) void k_splitk_swiglu(const float* __restrict__ part, int S, int M, int I,
+                                                       uint16_t* __restrict__ H, int ldh) {
+  const int iv = I / V;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, mn = (size_t)M * 2 * I;
+  if (i >= (size_t)M * iv) return;
+  const int m = (int)(i / iv), c = (int)(i % iv) * V;
+  float g[V], u[V];
+  splitk_sum<V>(part, S, mn, (size_t)m * 2 * I + c, g);
+  splitk_sum<V>(part, S, mn, (size_t)m * 2 * I + I + c, u);
+  float h[V];
+#pragma unroll
+  for (int e = 0; e < V; e++) h[e] = swiglu_f(bf2f(f2bf(g[e])), bf2f(f2bf(u[e])));
+  uint16_t* o = H + (size_t)m * ldh + c;
+  if (V == 4) {
+    *(uint2*)o = make_uint2(pack_bf2(h[0], h[1]), pack_bf2(h[2], h[3]));
+  } else {
+#pragma unroll
+    for (int e = 0; e < V; e++) o[e] = f2bf(h[e]);
+  }
 }
 
 int launch_splitk_reduce(const float* part, int S, int M, int N, void* C, int ldc, int mode, hipStream_t st) {
-  const size_t mn = (size_t)M * N;
-  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, part, S, M, N, C, ldc,
-                     mode);
+  if (M == 0) return IFD_OK;
+  if (mode == kModeSwiglu) {
+    const int I = N / 2;
+    const bool vec = I % 4 == 0 && ldc % 4 == 0 && ((uintptr_t)C & 7) == 0;
+    const size_t n = (size_t)M * (vec ? I / 4 : I);
+    if (vec)
+      hipLaunchKernelGGL(k_splitk_swiglu<4>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, S, M, I,
+                         (uint16_t*)C, ldc);
+    else
+      hipLaunchKernelGGL(k_splitk_swiglu<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, S, M, I,
+                         (uint16_t*)C, ldc);
+    return check_launch("splitk_swiglu");
+  }
+  const bool vec = N % 4 == 0 && ldc % 4 == 0 && mode != 1 && ((uintptr_t)C & (mode == 2 ? 15 : 7)) == 0;
+  const size_t n = (size_t)M * (vec ? N / 4 : N);
+  if (vec)
+    hipLaunchKernelGGL(k_splitk_reduce<4>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, S, M, N, C, ldc,
+                       mode);
+  else
+    hipLaunchKernelGGL(k_splitk_reduce<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, S, M, N, C, ldc,
+                       mode);
   return check_launch("splitk_reduce");
+}
+
+size_t epilogue_ws_bytes(int S, int M, int N, int mode) {
+  if (S > 1) return (size_t)S * M * N * sizeof(float);
+  return mode == kModeSwiglu ? (size_t)M * N * sizeof(uint16_t) : 0;
+}
+
+int launch_epilogue(const void* ws, int S, int M, int N, void* C, int ldc, int mode, hipStream_t st) {
+  if (S > 1) return launch_splitk_reduce((const float*)ws, S, M, N, C, ldc, mode, st);
+  if (mode == kModeSwiglu) return launch_silu_mul((const uint16_t*)ws, N, (uint16_t*)C, ldc, N / 2, M, st);
+  return IFD_OK;
 }
 
 // K splits for a decode GEMM: enough blocks (~2 per CU on 256 CUs) while every split keeps >= 4 groups and the

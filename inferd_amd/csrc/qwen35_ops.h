@@ -146,6 +146,7 @@ struct Qwen35 {
         need = std::max(need, ifd_gemm_w4_workspace(max_rows, 2 * shared_inter, H));
         need = std::max(need, ifd_gemm_w4_workspace(max_rows, H, shared_inter));
         need = std::max(need, ifd_gemm_t64_workspace(max_rows, 2 * shared_inter, H));
+        need = std::max(need, ifd_gemm_t64_swiglu_workspace(max_rows, 2 * shared_inter, H));
         need = std::max(need, ifd_gemm_t64_workspace(max_rows, H, shared_inter));
       }
       x = alloc((size_t)max_rows * H * 2);
@@ -177,6 +178,21 @@ struct Qwen35 {
   }
   Qwen35(const Qwen35&) = delete;
   Qwen35& operator=(const Qwen35&) = delete;
+
+  // H [M][N/2] = SwiGLU of A . W^T for a [gate | up] linear: one fused call on T64 weights, else the reference's
+  // gemm into proj + silu_mul (qwen35.h:1910-1912).
+  void gemm_swiglu(Enc& e, const BufRef& A, const QLinear& W, const BufRef& H, int M) {
+    if (W.bits == 4 && W.t64 && W.K % 256 == 0 && W.N % 16 == 0) {
+      const size_t need = ifd_gemm_t64_swiglu_workspace(M, W.N, W.K);
+      if (need > splitk_bytes) die("gemm_swiglu", "split-K scratch smaller than this shape needs");
+      ok(ifd_gemm_t64_swiglu(A.ptr<void>(), W.K, W.t64.ptr<void>(), W.N, W.K, H.ptr<void>(), W.N / 2, M,
+                             splitk.ptr<void>(), splitk_bytes, e.stream),
+         "gemm_swiglu");
+      return;
+    }
+    gemm(e, A, W, proj, M, 0);
+    ok(ifd_silu_mul(proj.ptr<void>(), H.ptr<void>(), W.N / 2, M, e.stream), "gemm_swiglu");
+  }
 
   // C (mode) = A . W^T for M rows: mode 0 writes bf16, 1 adds into bf16 C, 2 writes fp32. A is [M][K] (row stride
   // K), C [M][N] (row stride N).
@@ -220,9 +236,7 @@ struct Qwen35 {
     // shared expert -> sh_out
     const bool shared = ly.gate_up.N > 0;
     if (shared) {
-      const int Is = ly.gate_up.N / 2;
-      gemm(e, xn, ly.gate_up, proj, T, 0);
-      ok(ifd_silu_mul(proj.ptr<void>(), act.ptr<void>(), Is, T, e.stream), "encode_moe");
+      gemm_swiglu(e, xn, ly.gate_up, act, T);
       gemm(e, act, ly.down, sh_out, T, 0);
     }
     // router

@@ -184,10 +184,9 @@ static TPlan qmv_t_plan(int M, int N, int K) {
   return TPlan{(G + gps - 1) / gps, gps};
 }
 
-size_t qmv_t_workspace(int M, int N, int K) {
+size_t qmv_t_workspace(int M, int N, int K, int mode) {
   if (M > 16) return 0;
-  const TPlan pl = qmv_t_plan(M, N, K);
-  return pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
+  return epilogue_ws_bytes(qmv_t_plan(M, N, K).S, M, N, mode);
 }
 
 int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode, void* ws,
@@ -196,10 +195,13 @@ int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void*
   if (M > 16) return fail(IFD_ERR_UNSUPPORTED, "T64 decode kernel takes M <= 16");
   if (K % (kGroup * kTB)) return fail(IFD_ERR_ARG, "T64 decode needs K %% %d == 0 (K=%d)", kGroup * kTB, K);
   const TPlan pl = qmv_t_plan(M, N, K);
-  const size_t need = pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0;
+  const size_t need = epilogue_ws_bytes(pl.S, M, N, mode);
   if (need > ws_bytes || (need && !ws))
     return fail(IFD_ERR_WORKSPACE, "qmv_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
-  QmvTArgs p{A, lda, (const uint8_t*)wt, N, K, C, ldc, M, mode, (float*)ws, pl.gps};
+  // the SwiGLU mode without a split stores the bf16 product into the workspace for silu_mul
+  const bool via_ws = mode == kModeSwiglu && pl.S == 1;
+  QmvTArgs p{A, lda, (const uint8_t*)wt, N, K, via_ws ? ws : C, via_ws ? N : ldc, M, via_ws ? 0 : mode, (float*)ws,
+             pl.gps};
   const int Kz = pl.gps * kGroup;
   const size_t lds = ((size_t)M * (Kz + 8) * 2 + 15) / 16 * 16 + (size_t)pl.gps * 16 * sizeof(float);
   if (lds > 64 * 1024) return fail(IFD_ERR_UNSUPPORTED, "qmv_t64: %zu bytes of LDS needed", lds);
@@ -207,8 +209,7 @@ int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void*
   if (M <= 8) hipLaunchKernelGGL(k_qmv_t<4>, grid, block, lds, st, p);
   else hipLaunchKernelGGL(k_qmv_t<8>, grid, block, lds, st, p);
   IFD_TRY(check_launch("qmv_t64"));
-  if (pl.S > 1) return launch_splitk_reduce((const float*)ws, pl.S, M, N, C, ldc, mode, st);
-  return IFD_OK;
+  return launch_epilogue(ws, pl.S, M, N, C, ldc, mode, st);
 }
 
 }  // namespace ifd

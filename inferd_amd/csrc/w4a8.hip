@@ -70,32 +70,27 @@ int launch_flip(uint32_t* wq, size_t n32, uint32_t mask, hipStream_t st) {
   return check_launch("flip");
 }
 
-// h = bf16(float(bf16(g / (1 + exp(-g)))) * u), 8 values per thread.
-__global__ __launch_bounds__(256) void k_silu_mul(const uint16_t* __restrict__ gu, uint16_t* __restrict__ h, int I,
-                                                  int rows) {
+// h = bf16(float(bf16(g / (1 + exp(-g)))) * u), 8 values per thread; rows of gu are ldgu apart (gate at 0, up at I),
+// rows of h ldh apart (I, ldgu and ldh multiples of 8).
+__global__ __launch_bounds__(256) void k_silu_mul(const uint16_t* __restrict__ gu, int ldgu, uint16_t* __restrict__ h,
+                                                  int ldh, int I, int rows) {
   const int per_row = I / 8;
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (size_t)rows * per_row) return;
   const int r = (int)(i / per_row), c = (int)(i % per_row) * 8;
-  const u32x4 gv = *(const u32x4*)(gu + (size_t)r * 2 * I + c);
-  const u32x4 uv = *(const u32x4*)(gu + (size_t)r * 2 * I + I + c);
+  const u32x4 gv = *(const u32x4*)(gu + (size_t)r * ldgu + c);
+  const u32x4 uv = *(const u32x4*)(gu + (size_t)r * ldgu + I + c);
   u32x4 o;
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
-    float res[2];
-#pragma unroll
-    for (int e = 0; e < 2; e++) {
-      const float g = bf2f((uint16_t)(gv[t] >> (16 * e))), u = bf2f((uint16_t)(uv[t] >> (16 * e)));
-      res[e] = bf2f(f2bf(g / (1.f + expf(-g)))) * u;
-    }
-    o[t] = pack_bf2(res[0], res[1]);
-  }
-  *(u32x4*)(h + (size_t)r * I + c) = o;
+  for (int t = 0; t < 4; t++)
+    o[t] = pack_bf2(swiglu_f(bf2f((uint16_t)gv[t]), bf2f((uint16_t)uv[t])),
+                    swiglu_f(bf2f((uint16_t)(gv[t] >> 16)), bf2f((uint16_t)(uv[t] >> 16))));
+  *(u32x4*)(h + (size_t)r * ldh + c) = o;
 }
-int launch_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows, hipStream_t st) {
+int launch_silu_mul(const uint16_t* gu, int ldgu, uint16_t* h, int ldh, int I, int rows, hipStream_t st) {
   if (rows == 0) return IFD_OK;
   const size_t n = (size_t)rows * (I / 8);
-  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, h, I, rows);
+  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, ldgu, h, ldh, I, rows);
   return check_launch("silu_mul");
 }
 

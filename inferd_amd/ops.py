@@ -81,6 +81,18 @@ def gemm_t64(A: torch.Tensor, W: T64Linear, C: Optional[torch.Tensor] = None, mo
     return C
 
 
+def gemm_t64_swiglu(A: torch.Tensor, W: T64Linear, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """h = silu_mul(bf16(A . W^T)) for T64 weights holding [gate | up] rows: the fused gate/up projection."""
+    M, K = A.shape
+    assert K == W.K and A.dtype == torch.bfloat16 and A.is_contiguous() and W.N % 2 == 0
+    h = torch.empty((M, W.N // 2), dtype=torch.bfloat16, device=A.device) if out is None else out
+    need = lib().ifd_gemm_t64_swiglu_workspace(M, W.N, W.K)
+    ws = workspace(need, A.device) if need else None
+    check(lib().ifd_gemm_t64_swiglu(_p(A), K, _p(W.wt), W.N, W.K, _p(h), h.stride(0), M, _p(ws),
+                                    ws.numel() if ws is not None else 0, _stream()))
+    return h
+
+
 @dataclass
 class MoeW:
     """Stacked experts [E, N, K] in the same affine layout (engine/src/moe.h:8-11)."""

@@ -260,7 +260,16 @@ void test_encode_moe(std::mt19937& rng) {
   ly.egu.wq = g.wq, ly.egu.s = g.s, ly.egu.b = g.b, ly.egu.E = E, ly.egu.N = 2 * I, ly.egu.K = H, ly.egu.bits = 4;
   ly.edown.wq = d.wq, ly.edown.s = d.s, ly.edown.b = d.b, ly.edown.E = E, ly.edown.N = H, ly.edown.K = I,
   ly.edown.bits = 4;
-  for (int T : {16, 100}) {
+  // the shared expert's gate/up also as a T64 copy: encode_moe then takes the fused gate/up + SwiGLU call
+  void* sgu_t64 = nullptr;
+  hip_ok(hipMalloc(&sgu_t64, ifd_t64_bytes(2 * Is, H, 1)), "t64");
+  ok(ifd_pack_t64(ly.gate_up.wq.ptr<uint32_t>(), ly.gate_up.s.ptr<uint16_t>(), ly.gate_up.b.ptr<uint16_t>(), 2 * Is, H,
+                  0, 0, 1, sgu_t64, nullptr),
+     "pack_t64");
+  const QLinear sgu_mlx = ly.gate_up;
+  for (int T : {16, 100, -16, -100}) {
+    ly.gate_up = sgu_mlx;
+    if (T < 0) ly.gate_up.t64 = BufRef(sgu_t64), T = -T;
     Qwen35 m(c, T, Is, 0);
     Enc e;
     const auto x0 = activations(T, H, rng);
@@ -272,7 +281,7 @@ void test_encode_moe(std::mt19937& rng) {
     const auto idx = download<int>(m.ridx, (size_t)T * k);
     const auto wt = download<float>(m.rw, (size_t)T * k);
     const auto sg = download<float>(m.rsg, (size_t)T);
-    const std::string tag = " T=" + std::to_string(T);
+    const std::string tag = " T=" + std::to_string(T) + (ly.gate_up.t64 ? " (T64 shared gate/up)" : "");
     // rmsnorm: within one bf16 step of the oracle
     std::vector<uint16_t> xr((size_t)T * H);
     orc_rmsnorm(x0.data(), H, post.data(), xr.data(), H, T, H, c.eps);
@@ -298,6 +307,7 @@ void test_encode_moe(std::mt19937& rng) {
     const double ex = bf16_err(x1, wf, true);
     report(ex <= 1e-2, "encode_moe x += moe(xn)" + tag, ex);
   }
+  (void)hipFree(sgu_t64);
 }
 
 }  // namespace

@@ -131,3 +131,50 @@ def test_split_k_is_deterministic():
         rows = np.arange(0, M, max(1, M // 4))
         Y = (orc.qmv if M <= 64 else orc.qmm)(np.ascontiguousarray(g.host(A)[rows]), wq, s, b)
         assert gen.bf16_err(outs[0][rows], Y) <= 1e-2, (M, N, K)
+
+
+@pytest.mark.parametrize("M,N,K,split", [
+    (1, 1024, 2048, True),     # decode kernel, K split: SwiGLU in the split-K reduction
+    (4, 1024, 256, False),     # decode kernel, no split: bf16 product in the workspace, then silu_mul
+    (16, 2048, 1024, True),
+    (40, 1024, 2048, False),   # GEMM kernel (affine)
+    (40, 34816, 5120, True),
+    (128, 1024, 2048, False),  # GEMM kernel (dequant)
+    (128, 8192, 2048, True),
+    (1024, 8192, 256, False),
+])
+def test_gemm_t64_swiglu_matches_unfused(M, N, K, split):
+    """The fused gate/up projection gives the bits of gemm_t64 (mode 0) + silu_mul on both epilogues (split-K
+    reduction, workspace + silu_mul). Against the oracle, as a chain: the bf16 product is within the GEMM bar, and the
+    fused h within one bf16 step of the oracle's SwiGLU of that product (expf may differ in its last ulp; a product
+    of two rounded values is no place for a max-error / RMS bar, whose tail a single gate rounding flip can exceed)."""
+    g, ops = _gu(), _ops()
+    from inferd_amd._lib import lib
+    codes, wq, s, b = gen.qlinear(N, K, seed=M + N)
+    A = g.dev(gen.activations(M, K, seed=M + 1))
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    assert (lib().ifd_gemm_t64_workspace(M, N, K) > 0) == split
+    fused = g.host(ops.gemm_t64_swiglu(A, T))
+    gu = g.host(ops.gemm_t64(A, T))
+    assert np.array_equal(fused, g.host(ops.silu_mul(g.dev(gu)))), (M, N, K)
+    rows = np.unique(np.linspace(0, M - 1, 8).astype(int))
+    Y = _t64_semantics(M)(np.ascontiguousarray(g.host(A)[rows]), wq, s, b)
+    assert gen.bf16_err(gu[rows], Y) <= 1e-2
+    h, hr = gen.bf16_to_f32(fused), gen.bf16_to_f32(orc.silu_mul(gu))
+    assert np.all(np.abs(h - hr) <= 2 ** -7 * np.abs(hr) + 1e-30)
+    assert np.mean(h == hr) > 0.99
+
+
+def test_gemm_t64_swiglu_strided_output():
+    """h written into a wider buffer (row stride ldh > N / 2) leaves the padding columns untouched."""
+    g, ops = _gu(), _ops()
+    M, N, K = 8, 512, 1024
+    codes, wq, s, b = gen.qlinear(N, K, seed=5)
+    A = g.dev(gen.activations(M, K, seed=6))
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    wide = torch.full((M, N // 2 + 8), -1.0, dtype=torch.bfloat16, device="cuda")
+    ops.gemm_t64_swiglu(A, T, out=wide[:, : N // 2])
+    ref = g.host(ops.silu_mul(ops.gemm_t64(A, T)))
+    out = g.host(wide)
+    assert np.array_equal(out[:, : N // 2], ref)
+    assert np.all(gen.bf16_to_f32(out[:, N // 2:]) == -1.0)
