@@ -19,6 +19,10 @@
  *    2 C = y as fp32.
  *  - Every entry point returns IFD_OK or an error code and never exits the process (the reference prints and calls
  *    exit(1), qwen35.h:1469, 1477); ifd_last_error() returns a message for the calling thread.
+ *  - Workspaces (the *_workspace() queries give the bytes, 0 = none needed; pass at least that many): the first 4096
+ *    bytes of a workspace are completion counters that the library keeps at zero between calls. ZERO THEM ONCE when
+ *    the workspace is allocated (hipMemset, or allocate zeroed); the rest is scratch, any content. One workspace may
+ *    serve every entry point, but calls that share a workspace must not run concurrently.
  */
 #ifndef INFERD_QMM_H
 #define INFERD_QMM_H

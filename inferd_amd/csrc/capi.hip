@@ -52,9 +52,25 @@ const char* ifd_status_str(int status) {
 
 const char* ifd_last_error(void) { return last_error_buf(); }
 
+namespace {
+// A public workspace: [kWsHeader bytes of counters, kept zero][kernel scratch]. Sizes reported to callers include
+// the header whenever any scratch is needed.
+size_t with_header(size_t body) { return body ? body + kWsHeader : 0; }
+struct WsView {
+  unsigned* cnt = nullptr;
+  void* body = nullptr;
+  size_t bytes = 0;
+};
+WsView ws_view(void* w, size_t bytes) {
+  WsView v;
+  if (w && bytes >= kWsHeader) v.cnt = (unsigned*)w, v.body = (char*)w + kWsHeader, v.bytes = bytes - kWsHeader;
+  return v;
+}
+}  // namespace
+
 size_t ifd_gemm_w4_workspace(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  return M <= kQmvMaxRows ? qmv_workspace(M, N, K) : qmm_workspace(M, N, K);
+  return with_header(M <= kQmvMaxRows ? qmv_workspace(M, N, K) : qmm_workspace(M, N, K));
 }
 
 int ifd_qmv_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk,
@@ -62,22 +78,25 @@ int ifd_qmv_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, co
   W4Gemm g;
   IFD_TRY(fill_gemm(g, A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
   IFD_CHECK(M <= kQmvMaxRows, "ifd_qmv_w4 takes M <= %d (M=%d)", kQmvMaxRows, M);
-  return launch_qmv(g, workspace, ws_bytes, S(stream));
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_qmv(g, w.body, w.bytes, S(stream));
 }
 
 int ifd_qmm_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk,
                uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes, void* stream) {
   W4Gemm g;
   IFD_TRY(fill_gemm(g, A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
-  return launch_qmm(g, workspace, ws_bytes, S(stream));
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_qmm(g, w.body, w.bytes, S(stream));
 }
 
 int ifd_gemm_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk,
                 uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes, void* stream) {
   W4Gemm g;
   IFD_TRY(fill_gemm(g, A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
-  if (M <= kQmvMaxRows) return launch_qmv(g, workspace, ws_bytes, S(stream));
-  return launch_qmm(g, workspace, ws_bytes, S(stream));
+  const WsView w = ws_view(workspace, ws_bytes);
+  if (M <= kQmvMaxRows) return launch_qmv(g, w.body, w.bytes, S(stream));
+  return launch_qmm(g, w.body, w.bytes, S(stream));
 }
 
 int ifd_flip_w4(uint32_t* wq, size_t n32, uint32_t mask, void* stream) {
@@ -107,7 +126,7 @@ int ifd_a8_quant(const void* A, int lda, int M, int K, int per_token, int8_t* U,
   return launch_a8_quant((const uint16_t*)A, lda, M, K, per_token ? 1 : 0, U, XS, S(stream));
 }
 
-size_t ifd_qmm_w4a8_workspace(int M, int N, int K) { return w4a8_workspace(M, N, K); }
+size_t ifd_qmm_w4a8_workspace(int M, int N, int K) { return with_header(w4a8_workspace(M, N, K)); }
 
 int ifd_qmm_w4a8(const int8_t* U, const float* XS, int per_token, const uint32_t* wq, const uint16_t* s,
                  const uint16_t* b, int N, int K, int ldk, uint32_t xr, void* C, int ldc, int M, int mode,
@@ -116,7 +135,8 @@ int ifd_qmm_w4a8(const int8_t* U, const float* XS, int per_token, const uint32_t
   IFD_TRY(fill_gemm(g, U, K, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
   IFD_CHECK(M == 0 || XS, "null XS");
   g.XS = XS;
-  return launch_w4a8(g, per_token ? 1 : 0, workspace, ws_bytes, S(stream));
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_w4a8(g, per_token ? 1 : 0, w.body, w.bytes, S(stream));
 }
 
 // ---- T64 layout ------------------------------------------------------------------------------------------------
@@ -136,12 +156,12 @@ int ifd_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N
 
 size_t ifd_gemm_t64_workspace(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  return M <= 16 ? qmv_t_workspace(M, N, K, 0) : gemm_t_workspace(M, N, K, 0);
+  return with_header(M <= 16 ? qmv_t_workspace(M, N, K, 0) : gemm_t_workspace(M, N, K, 0));
 }
 
 size_t ifd_gemm_t64_swiglu_workspace(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  return M <= 16 ? qmv_t_workspace(M, N, K, kModeSwiglu) : gemm_t_workspace(M, N, K, kModeSwiglu);
+  return with_header(M <= 16 ? qmv_t_workspace(M, N, K, kModeSwiglu) : gemm_t_workspace(M, N, K, kModeSwiglu));
 }
 
 int ifd_gemm_t64_swiglu(const void* A, int lda, const void* wt, int N, int K, void* H, int ldh, int M,
@@ -152,9 +172,10 @@ int ifd_gemm_t64_swiglu(const void* A, int lda, const void* wt, int N, int K, vo
   if (M == 0) return IFD_OK;
   IFD_CHECK(A && wt && H && aligned(A, 16) && aligned(wt, 16) && aligned(H, 16), "null or misaligned pointer");
   IFD_CHECK(!workspace || aligned(workspace, 16), "workspace must be 16-byte aligned");
+  const WsView w = ws_view(workspace, ws_bytes);
   if (M <= 16)
-    return launch_qmv_t((const uint16_t*)A, lda, wt, N, K, H, ldh, M, kModeSwiglu, workspace, ws_bytes, S(stream));
-  return launch_gemm_t((const uint16_t*)A, lda, wt, N, K, H, ldh, M, kModeSwiglu, workspace, ws_bytes, S(stream));
+    return launch_qmv_t((const uint16_t*)A, lda, wt, N, K, H, ldh, M, kModeSwiglu, w.cnt, w.body, w.bytes, S(stream));
+  return launch_gemm_t((const uint16_t*)A, lda, wt, N, K, H, ldh, M, kModeSwiglu, w.body, w.bytes, S(stream));
 }
 
 int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
@@ -164,9 +185,11 @@ int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, 
   IFD_CHECK(lda >= K && lda % 8 == 0 && ldc >= N, "bad strides lda=%d ldc=%d", lda, ldc);
   if (M == 0) return IFD_OK;
   IFD_CHECK(A && wt && C && aligned(A, 16) && aligned(wt, 16), "null or misaligned pointer");
+  IFD_CHECK(!workspace || aligned(workspace, 16), "workspace must be 16-byte aligned");
+  const WsView w = ws_view(workspace, ws_bytes);
   if (M <= 16)
-    return launch_qmv_t((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, workspace, ws_bytes, S(stream));
-  return launch_gemm_t((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, workspace, ws_bytes, S(stream));
+    return launch_qmv_t((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, w.cnt, w.body, w.bytes, S(stream));
+  return launch_gemm_t((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, w.body, w.bytes, S(stream));
 }
 
 int ifd_moe_router_logits(const void* x, const void* w, int T, int H, int E1, int out_bf16, void* logits,
@@ -185,13 +208,14 @@ int ifd_moe_route(const void* logits, int logits_bf16, int T, int E, int k, int 
 }
 
 int ifd_moe_tiles_max(int R, int E) { return moe_tiles_max(R, E); }
-size_t ifd_moe_dispatch_workspace(int R, int E) { return moe_dispatch_workspace(R, E); }
+size_t ifd_moe_dispatch_workspace(int R, int E) { return with_header(moe_dispatch_workspace(R, E)); }
 
 int ifd_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
                      void* workspace, size_t ws_bytes, void* stream) {
   IFD_CHECK(R >= 0 && E > 0 && E <= 1024, "bad dispatch shape R=%d E=%d (E <= 1024)", R, E);
   IFD_CHECK(offsets && tiles && ntiles && (R == 0 || (idx && perm && inv)), "null pointer");
-  return launch_moe_dispatch(idx, R, E, offsets, perm, inv, tiles, ntiles, workspace, ws_bytes, S(stream));
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_moe_dispatch(idx, R, E, offsets, perm, inv, tiles, ntiles, w.body, w.bytes, S(stream));
 }
 
 int ifd_moe_gather(const void* x, const int* perm, int div, int R, int H, void* xs, void* stream) {
@@ -258,7 +282,7 @@ MoeLayout moe_layout(int T, int H, int I, int E, int k, int Is) {
 
 size_t ifd_moe_ffn_workspace(int T, int H, int I, int E, int k, int Is) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
-  return moe_layout(T, H, I, E, k, Is).total;
+  return with_header(moe_layout(T, H, I, E, k, Is).total);
 }
 
 int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
@@ -275,9 +299,12 @@ int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, 
   if (T == 0) return IFD_OK;
   IFD_CHECK(xn && router && egu_wq && egu_s && egu_b && edn_wq && edn_s && edn_b && out, "null pointer");
   const MoeLayout L = moe_layout(T, H, I, E, k, shared ? Is : 0);
-  if (!workspace || ws_bytes < L.total)
-    return fail(IFD_ERR_WORKSPACE, "moe_ffn needs %zu bytes of workspace, got %zu", L.total, ws_bytes);
-  char* w = (char*)workspace;
+  const WsView wv = ws_view(workspace, ws_bytes);
+  if (!wv.body || wv.bytes < L.total)
+    return fail(IFD_ERR_WORKSPACE, "moe_ffn needs %zu bytes of workspace, got %zu", with_header(L.total), ws_bytes);
+  // the layout is carved from the scratch after the header; the shared expert's GEMMs get a sub-area sized by their
+  // own public query, whose leading counter bytes are not kept zero: only counter-free GEMM paths may run there
+  char* w = (char*)wv.body;
   hipStream_t st = S(stream);
   const int R = T * k, E1 = E + (shared_gate ? 1 : 0);
   int* ridx = idx ? idx : (int*)(w + L.idx);

@@ -34,6 +34,11 @@ int launch_flip(uint32_t* wq, size_t n32, uint32_t mask, hipStream_t st);
 int launch_silu_mul(const uint16_t* gu, int ldgu, uint16_t* h, int ldh, int I, int rows, hipStream_t st);
 int launch_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows,
                    int D, float eps, hipStream_t st);
+// Every public workspace starts with kWsHeader bytes of completion counters (uint32), which the library keeps at zero
+// between calls: the caller zeroes them once when the workspace is allocated. Kernel scratch follows the header.
+constexpr size_t kWsHeader = 4096;
+constexpr int kWsCounters = (int)(kWsHeader / sizeof(unsigned));
+
 // Library-internal store mode past the public 0 (bf16), 1 (bf16 residual add) and 2 (fp32): the GEMM's N columns are
 // [gate (N/2) | up (N/2)] and C receives the SwiGLU h [M][N/2] (ldc = its row stride), bit-identical to a mode-0 GEMM
 // followed by silu_mul.
@@ -54,8 +59,9 @@ size_t qmv_t_workspace(int M, int N, int K, int mode);
 size_t gemm_t_workspace(int M, int N, int K, int mode);
 int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   void* ws, size_t ws_bytes, hipStream_t st);
-int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode, void* ws,
-                 size_t ws_bytes, hipStream_t st);
+// cnt: kWsCounters zeroed counters (the workspace header) for the in-kernel split-K fixup; null -> a reduction kernel
+int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                 unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st);
 
 // MoE.
 int launch_router_logits(const uint16_t* x, const uint16_t* w, int T, int H, int E1, int out_bf16, void* logits,

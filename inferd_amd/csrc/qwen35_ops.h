@@ -168,7 +168,10 @@ struct Qwen35 {
       eact = alloc((size_t)R * I * 2);
       edown_out = alloc((size_t)R * H * 2);
     }
-    if (need) splitk = alloc(need);
+    if (need) {
+      splitk = alloc(need);
+      hip_ok(hipMemset(splitk.buf, 0, need), "Qwen35");  // the workspace's leading counters start at zero
+    }
     splitk_bytes = need;
   }
   ~Qwen35() {

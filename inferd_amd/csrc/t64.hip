@@ -51,6 +51,10 @@ int launch_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, in
 // ping-pong blocks of kTB groups (one 16-byte code load + one (s, b) dword per lane per group) and reads
 // activations from LDS. Prefetch loads are unconditional (the last block is re-read past the end) so every path
 // leaves the same number of loads outstanding and the waits stay one block behind.
+// With a K split the blocks store fp32 partials [S][M][N]; given completion counters (the workspace header), the
+// last block to finish a 128-column tile sums its S partials in split order and stores the result (SwiGLU mode:
+// gate tile t and up tile t + sw_half share one counter, and the last of their 2 S blocks writes h), so no
+// reduction kernel follows. The sums are those of k_splitk_reduce / k_splitk_swiglu, bit for bit.
 struct QmvTArgs {
   const uint16_t* A;
   int lda;
@@ -59,10 +63,18 @@ struct QmvTArgs {
   void* C;
   int ldc, M, mode;
   float* part;
+  uint32_t part_bytes;
+  unsigned* cnt;  // null: partials only, a reduction kernel follows
+  int sw_half;    // SwiGLU fixup: number of gate column tiles (0: plain store mode)
   int gps;
 };
 
-constexpr int kTB = 4;  // groups per pipeline block
+constexpr int kTB = 2;     // groups per pipeline block
+constexpr int kMaxS = 16;  // K splits at most
+#ifndef QMV_FIXB
+#define QMV_FIXB 8
+#endif
+constexpr int kFixB = QMV_FIXB;  // partial loads in flight per thread in the split-K fixup
 
 __device__ __forceinline__ u32x4 t64_bf16_off128(uint32_t w) {
   u32x4 r;
@@ -71,9 +83,18 @@ __device__ __forceinline__ u32x4 t64_bf16_off128(uint32_t w) {
   return r;
 }
 
+// Device-coherent (sc1) buffer accesses to the partials, which blocks on different XCDs (separate L2s) exchange:
+// stores write through to memory, loads do not hit a stale line of the local L2. Plain loads batch, unlike atomic
+// loads, which the compiler orders one after another.
+constexpr int kSc1 = 16;  // cache-policy operand: SC1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const float* part, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, (int)bytes, 0x00020000);
+}
+
 template <int RACT>
 __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   extern __shared__ __align__(16) uint16_t lds[];
+  __shared__ unsigned s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
   const int G = p.K / kGroup, nb = t64_bands(p.N);
@@ -82,37 +103,12 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   uint16_t* As = lds;
   float* Xs = (float*)((char*)lds + ((size_t)M * ldA * 2 + 15) / 16 * 16);  // [Gz][16]
 
-  // ---- stage A[0:M][g0*64 : g1*64] and the 64-group sums
-  const int cpr = Kz / 8, total = M * cpr;
-  for (int c0 = 0; c0 < total; c0 += 256) {
-    const int c = c0 + tid;
-    const bool ok = c < total;
-    const int m = ok ? c / cpr : 0, kc = ok ? c % cpr : 0;
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (ok) v = *(const u32x4*)(p.A + (size_t)m * p.lda + (size_t)g0 * kGroup + 8 * kc);
-    float sum = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; e++) sum += bf2f((uint16_t)(v[e] & 0xFFFFu)) + bf2f((uint16_t)(v[e] >> 16));
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
-    if (ok) {
-      *(u32x4*)(As + (size_t)m * ldA + 8 * kc) = v;
-      if ((kc & 7) == 0) Xs[(kc >> 3) * 16 + m] = sum;
-    }
-  }
-  for (int i = tid; i < Gz * 16; i += 256)
-    if ((i & 15) >= M) Xs[i] = 0.f;
-  __syncthreads();
-
+  // this wave's band; its first block of tiles is requested before the activations are staged, so the weight
+  // stream starts one memory latency earlier
   const int band = blockIdx.x * 4 + wave;
-  if (band >= nb) return;  // no barrier follows
-  const bool aok = j < M;
-  const uint16_t* arow = As + (size_t)(aok ? j : 0) * ldA + 32 * h;
-  const uint8_t* tcol = p.wt + (size_t)band * kT64Tile;  // + g * nb * kT64Tile
+  const bool live = band < nb;
+  const uint8_t* tcol = p.wt + (size_t)(live ? band : 0) * kT64Tile;  // + g * nb * kT64Tile
   const size_t gstride = (size_t)nb * kT64Tile;
-
-  f32x16 acc = zero16();
   struct Blk {
     u32x4 w[kTB];
     uint32_t sb[kTB];
@@ -125,6 +121,46 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
       B.sb[i] = *(const uint32_t*)(t + kT64Codes + 4 * j);
     }
   };
+  Blk b0, b1;
+  if (live) load_blk(b0, g0);
+
+  // ---- stage A[0:M][g0*64 : g1*64] and the 64-group sums; kStageU 16-byte chunks per thread are loaded before any
+  // is used (one memory latency per kStageU passes); 8 consecutive threads hold one row's 64-group
+  constexpr int kStageU = 4;
+  const int cpr = Kz / 8, total = M * cpr;
+  for (int c0 = 0; c0 < total; c0 += 256 * kStageU) {
+    u32x4 v[kStageU];
+#pragma unroll
+    for (int u = 0; u < kStageU; u++) {
+      const int c = c0 + 256 * u + tid;
+      v[u] = u32x4{0u, 0u, 0u, 0u};
+      if (c < total) v[u] = *(const u32x4*)(p.A + (size_t)(c / cpr) * p.lda + (size_t)g0 * kGroup + 8 * (c % cpr));
+    }
+#pragma unroll
+    for (int u = 0; u < kStageU; u++) {
+      const int c = c0 + 256 * u + tid;
+      const bool ok = c < total;
+      const int m = ok ? c / cpr : 0, kc = ok ? c % cpr : 0;
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) sum += bf2f((uint16_t)(v[u][e] & 0xFFFFu)) + bf2f((uint16_t)(v[u][e] >> 16));
+      sum += __shfl_xor(sum, 1, 64);
+      sum += __shfl_xor(sum, 2, 64);
+      sum += __shfl_xor(sum, 4, 64);
+      if (ok) {
+        *(u32x4*)(As + (size_t)m * ldA + 8 * kc) = v[u];
+        if ((kc & 7) == 0) Xs[(kc >> 3) * 16 + m] = sum;
+      }
+    }
+  }
+  for (int i = tid; i < Gz * 16; i += 256)
+    if ((i & 15) >= M) Xs[i] = 0.f;
+  __syncthreads();
+
+  const bool aok = j < M;
+  const uint16_t* arow = As + (size_t)(aok ? j : 0) * ldA + 32 * h;
+
+  f32x16 acc = zero16();
   auto compute_blk = [&](const Blk& B, int g) {
 #pragma unroll
     for (int i = 0; i < kTB; i++) {
@@ -146,42 +182,121 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
       for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[r]));
     }
   };
-  const int glast = g1 - kTB;
-  Blk b0, b1;
-  load_blk(b0, g0);
-  for (int g = g0;; g += 2 * kTB) {
-    load_blk(b1, min(g + kTB, glast));
-    compute_blk(b0, g);
-    if (g + kTB >= g1) break;
-    load_blk(b0, min(g + 2 * kTB, glast));
-    compute_blk(b1, g + kTB);
-    if (g + 2 * kTB >= g1) break;
+  if (live) {  // waves past the last band skip the stream but take part in the fixup's barriers
+    const int glast = g1 - kTB;
+    for (int g = g0;; g += 2 * kTB) {
+      load_blk(b1, min(g + kTB, glast));
+      compute_blk(b0, g);
+      if (g + kTB >= g1) break;
+      load_blk(b0, min(g + 2 * kTB, glast));
+      compute_blk(b1, g + kTB);
+      if (g + 2 * kTB >= g1) break;
+    }
   }
   const int col = band * 32 + j;
-  if (col >= p.N) return;
-  const bool split = gridDim.y > 1;
+  if (gridDim.y == 1) {
+    if (!live || col >= p.N) return;
 #pragma unroll
-  for (int r = 0; r < RACT; r++) {
-    const int row = 8 * (r / 4) + 4 * h + (r % 4);
-    if (row >= M) continue;
-    if (split) p.part[((size_t)blockIdx.y * M + row) * p.N + col] = acc[r];
-    else store_mode(p.C, (size_t)row * p.ldc + col, acc[r], p.mode);
+    for (int r = 0; r < RACT; r++) {
+      const int row = 8 * (r / 4) + 4 * h + (r % 4);
+      if (row < M) store_mode(p.C, (size_t)row * p.ldc + col, acc[r], p.mode);
+    }
+    return;
+  }
+
+  // ---- K split: partials, then (with counters) the fixup by the tile's last block
+  const __amdgpu_buffer_rsrc_t rs = part_rsrc(p.part, p.part_bytes);
+  if (live && col < p.N) {
+#pragma unroll
+    for (int r = 0; r < RACT; r++) {
+      const int row = 8 * (r / 4) + 4 * h + (r % 4);
+      if (row < M)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[r]),  rs,
+                                              (int)((((size_t)blockIdx.y * M + row) * p.N + col) * 4), 0, kSc1);
+    }
+  }
+  if (!p.cnt) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete (written through)
+  __syncthreads();
+  const int tile = p.sw_half ? (int)blockIdx.x % p.sw_half : (int)blockIdx.x;
+  const unsigned arrivals = (p.sw_half ? 2u : 1u) * gridDim.y;
+  if (tid == 0) {
+    const unsigned old = __hip_atomic_fetch_add(p.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1 == arrivals;
+    if (last) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next call
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int S = (int)gridDim.y;
+  const size_t mn = (size_t)M * p.N;
+  // four columns of one row per thread and pass (16-byte partial loads, N % 4 == 0), the loads of kFixB splits in
+  // flight at once (their registers count against the occupancy the stream needs), summed in split order
+  auto sum4 = [&](size_t o) {
+    float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z0 = 0; z0 < S; z0 += kFixB) {
+      u32x4 v[kFixB];
+#pragma unroll
+      for (int z = 0; z < kFixB; z++)
+        if (z0 + z < S)
+          v[z] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rs, (int)(((z0 + z) * mn + o) * 4), 0, kSc1));
+#pragma unroll
+      for (int z = 0; z < kFixB; z++)
+        if (z0 + z < S) {
+          acc4.x += __uint_as_float(v[z][0]);
+          acc4.y += __uint_as_float(v[z][1]);
+          acc4.z += __uint_as_float(v[z][2]);
+          acc4.w += __uint_as_float(v[z][3]);
+        }
+    }
+    return acc4;
+  };
+  for (int e = tid; e < M * 32; e += 256) {
+    const int row = e >> 5, c4 = (e & 31) * 4;
+    if (!p.sw_half) {
+      const int c = (int)blockIdx.x * 128 + c4;
+      if (c >= p.N) continue;
+      const float4 v = sum4((size_t)row * p.N + c);
+      const size_t o = (size_t)row * p.ldc + c;
+      store_mode(p.C, o, v.x, p.mode);
+      store_mode(p.C, o + 1, v.y, p.mode);
+      store_mode(p.C, o + 2, v.z, p.mode);
+      store_mode(p.C, o + 3, v.w, p.mode);
+    } else {
+      const int I = p.N / 2, c = tile * 128 + c4;
+      const float4 g = sum4((size_t)row * p.N + c), u = sum4((size_t)row * p.N + I + c);
+      uint16_t* o = (uint16_t*)p.C + (size_t)row * p.ldc + c;
+      o[0] = f2bf(swiglu_f(bf2f(f2bf(g.x)), bf2f(f2bf(u.x))));
+      o[1] = f2bf(swiglu_f(bf2f(f2bf(g.y)), bf2f(f2bf(u.y))));
+      o[2] = f2bf(swiglu_f(bf2f(f2bf(g.z)), bf2f(f2bf(u.z))));
+      o[3] = f2bf(swiglu_f(bf2f(f2bf(g.w)), bf2f(f2bf(u.w))));
+    }
   }
 }
 
-// Split plan: ~2 blocks per CU, whole kTB-group blocks per split, <= ~40 KB of staged activations per block.
+// Split plan: about 6 waves per SIMD (the stream is latency-bound: more waves, more bytes in flight), whole kTB-group
+// blocks of at least two per split, at most kMaxS splits, <= ~40 KB of staged activations per block.
 struct TPlan {
   int S, gps;
 };
 static TPlan qmv_t_plan(int M, int N, int K) {
-  const int G = K / kGroup, bx = (t64_bands(N) + 3) / 4;
-  long S = (512 + bx - 1) / bx;
+  const int G = K / kGroup, waves = 4 * ((t64_bands(N) + 3) / 4);
+  long S = (6144 + waves - 1) / waves;
   S = std::max<long>(S, ((long)M * K * 2 + 40959) / 40960);
   S = std::min<long>(S, std::max(1, G / (2 * kTB)));
-  S = std::min<long>(S, std::max(1, 1024 / std::max(M, 1)));
+  S = std::min<long>(S, kMaxS);
   int gps = (int)((G + S - 1) / S);
   gps = (gps + kTB - 1) / kTB * kTB;
   return TPlan{(G + gps - 1) / gps, gps};
+}
+
+// The in-kernel fixup applies with counters for every tile and rows of whole 16-byte partial quads (N % 4 == 0); the
+// SwiGLU pairing needs gate and up halves of whole 128-column tiles.
+static bool qmv_t_fixup(int N, int mode, int S) {
+  const int tiles = (t64_bands(N) + 3) / 4;
+  if (S <= 1 || tiles > kWsCounters || N % 4) return false;
+  return mode != kModeSwiglu || (N % 256 == 0);
 }
 
 size_t qmv_t_workspace(int M, int N, int K, int mode) {
@@ -189,8 +304,8 @@ size_t qmv_t_workspace(int M, int N, int K, int mode) {
   return epilogue_ws_bytes(qmv_t_plan(M, N, K).S, M, N, mode);
 }
 
-int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode, void* ws,
-                 size_t ws_bytes, hipStream_t st) {
+int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                 unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
   if (M == 0) return IFD_OK;
   if (M > 16) return fail(IFD_ERR_UNSUPPORTED, "T64 decode kernel takes M <= 16");
   if (K % (kGroup * kTB)) return fail(IFD_ERR_ARG, "T64 decode needs K %% %d == 0 (K=%d)", kGroup * kTB, K);
@@ -198,9 +313,22 @@ int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void*
   const size_t need = epilogue_ws_bytes(pl.S, M, N, mode);
   if (need > ws_bytes || (need && !ws))
     return fail(IFD_ERR_WORKSPACE, "qmv_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
+  const bool fix = cnt && qmv_t_fixup(N, mode, pl.S);
   // the SwiGLU mode without a split stores the bf16 product into the workspace for silu_mul
   const bool via_ws = mode == kModeSwiglu && pl.S == 1;
-  QmvTArgs p{A, lda, (const uint8_t*)wt, N, K, via_ws ? ws : C, via_ws ? N : ldc, M, via_ws ? 0 : mode, (float*)ws,
+  QmvTArgs p{A,
+             lda,
+             (const uint8_t*)wt,
+             N,
+             K,
+             via_ws ? ws : C,
+             via_ws ? N : ldc,
+             M,
+             via_ws ? 0 : mode,
+             (float*)ws,
+             (uint32_t)(pl.S > 1 ? need : 0),
+             fix ? cnt : nullptr,
+             fix && mode == kModeSwiglu ? (t64_bands(N) + 3) / 4 / 2 : 0,
              pl.gps};
   const int Kz = pl.gps * kGroup;
   const size_t lds = ((size_t)M * (Kz + 8) * 2 + 15) / 16 * 16 + (size_t)pl.gps * 16 * sizeof(float);
@@ -209,6 +337,7 @@ int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void*
   if (M <= 8) hipLaunchKernelGGL(k_qmv_t<4>, grid, block, lds, st, p);
   else hipLaunchKernelGGL(k_qmv_t<8>, grid, block, lds, st, p);
   IFD_TRY(check_launch("qmv_t64"));
+  if (fix) return IFD_OK;
   return launch_epilogue(ws, pl.S, M, N, C, ldc, mode, st);
 }
 

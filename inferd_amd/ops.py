@@ -28,11 +28,12 @@ _ws_cache: dict = {}
 
 
 def workspace(nbytes: int, device) -> torch.Tensor:
-    """A cached uint8 device buffer of at least nbytes (grown on demand), reused across calls on one stream."""
+    """A cached uint8 device buffer of at least nbytes (grown on demand), reused across calls on one stream.
+    Allocated zeroed: a workspace's leading counters must start at zero, and the library keeps them there."""
     key = str(device)
     buf = _ws_cache.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
         _ws_cache[key] = buf
     return buf
 
@@ -187,7 +188,7 @@ def moe_dispatch(idx: torch.Tensor, E: int):
     tiles = torch.empty((max(mt, 1), 2), dtype=torch.int32, device=dev)
     ntiles = torch.empty((1,), dtype=torch.int32, device=dev)
     need = lib().ifd_moe_dispatch_workspace(R, E)
-    ws = torch.empty((max(need, 256),), dtype=torch.uint8, device=dev)
+    ws = workspace(need, dev)
     check(lib().ifd_moe_dispatch(_p(idx), R, E, _p(offsets), _p(perm), _p(inv), _p(tiles), _p(ntiles), _p(ws),
                                  ws.numel(), _stream()))
     return offsets, perm[:R], inv[:R], tiles, ntiles, mt

@@ -72,14 +72,24 @@ def test_qmv_rejects_large_m_and_moe_rejects_bad_shapes():
     assert L.ifd_moe_dispatch(4096, 10, 2000, 4096, 4096, 4096, 4096, 4096, None, 0, None) == _lib.IFD_ERR_ARG
 
 
+HEADER_BYTES = 4096  # the counters every workspace starts with
+
+
 def test_workspace_queries():
     L = _lib.lib()
-    # decode shapes split K: partials S * M * N fp32
+    # decode shapes split K: the counter header + partials S * M * N fp32
     ws = L.ifd_gemm_w4_workspace(1, 5120, 5120)
-    assert ws > 0 and ws % (5120 * 4) == 0
+    assert ws > HEADER_BYTES and (ws - HEADER_BYTES) % (5120 * 4) == 0
     assert L.ifd_gemm_w4_workspace(4096, 17408, 5120) == 0
+    ws = L.ifd_gemm_t64_workspace(1, 34816, 5120)
+    assert ws > HEADER_BYTES and (ws - HEADER_BYTES) % (34816 * 4) == 0
+    # the SwiGLU entry needs the bf16 product in the workspace even without a split
+    assert L.ifd_gemm_t64_workspace(4, 1024, 256) == 0
+    assert L.ifd_gemm_t64_swiglu_workspace(4, 1024, 256) == HEADER_BYTES + 4 * 1024 * 2
     assert L.ifd_moe_ffn_workspace(2048, 2048, 512, 512, 10, 512) > 2048 * 10 * 2048 * 2
     assert L.ifd_moe_tiles_max(20480, 512) == 640 + 512
     # a too-small workspace is refused before any launch
     rc = L.ifd_qmv_w4(4096, 5120, 4096, 4096, 4096, 5120, 5120, 0, 0, 4096, 5120, 1, 0, None, 0, None)
+    assert rc == _lib.IFD_ERR_WORKSPACE
+    rc = L.ifd_gemm_t64(4096, 5120, 4096, 34816, 5120, 4096, 34816, 1, 0, 4096, HEADER_BYTES, None)
     assert rc == _lib.IFD_ERR_WORKSPACE
