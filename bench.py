@@ -193,11 +193,11 @@ def main():
             del W2, A2, C2
         # ---- config 3: W4A8 M=2048, K=N=5120, per-token int8 --------------------------------------------------
         if args.only in ("", "c3"):
-            W3 = [qlin(5120, 5120) for _ in range(4)]
+            W3 = [ops.pack_t64(qlin(5120, 5120)) for _ in range(4)]
             A3 = act(2048, 5120)
             U3, XS3 = ops.a8_quant(A3, True)
             C3 = torch.empty((2048, 5120), dtype=torch.bfloat16, device=dev)
-            ms = timed(lambda i: ops.qmm_w4a8(U3, XS3, True, W3[i % 4], C3), 20, 3)
+            ms = timed(lambda i: ops.gemm_t64_w4a8(U3, XS3, W3[i % 4], C3), 20, 3)
             ms_q = timed(lambda i: ops.a8_quant(A3, True), 20, 3)
             op = 2.0 * 2048 * 5120 * 5120
             breakdown["c3_w4a8_M2048"] = dict(us=ms * 1e3, tops=op / (ms * 1e-3) / 1e12,

@@ -118,6 +118,13 @@ int ifd_qmm_w4a8(const int8_t* U, const float* XS, int per_token, const uint32_t
                  void* stream);
 size_t ifd_qmm_w4a8_workspace(int M, int N, int K);
 
+/* W4A8 on T64 weights (per-token activations from ifd_a8_quant with per_token = 1; W packed by ifd_pack_t64):
+ * C (mode) = sx[m] * sum_g (S P_g + B X_g) on int8 MFMA, the w4a8_gemm identity (w4a8.metal:8, 78-87) with unflipped
+ * codes. K % 256 == 0. per_token = 0 returns IFD_ERR_UNSUPPORTED. */
+size_t ifd_gemm_t64_w4a8_workspace(int M, int N, int K);
+int ifd_gemm_t64_w4a8(const int8_t* U, const float* XS, int per_token, const void* wt, int N, int K, void* C, int ldc,
+                      int M, int mode, void* workspace, size_t ws_bytes, void* stream);
+
 /* ---- MoE (reference encode_moe sorted path, qwen35.h:1869-1980; kernels moe.metal:60-187) -------------------- */
 
 /* Router logits [T][E1] = x [T][H] . W [E1][H]^T, bf16 operands, fp32 accumulation; out_bf16 = 1 rounds to bf16

@@ -25,6 +25,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "dma.h"
 #include "host.h"
 #include "kernels.h"
 #include "t64.h"
@@ -46,19 +47,6 @@ struct GemmTArgs {
 constexpr int kGtBand = 4;  // M tiles per band of the tile order
 constexpr int kGtNS = 3;    // LDS pipeline stages
 constexpr int kGtThreads = 512;
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
-}
-// Wait until at most N DMA/vector loads of this wave are outstanding and all its LDS reads are done, then barrier.
-// One asm statement with a memory clobber: the compiler may not move LDS accesses across it, and it adds no wait of
-// its own (a __syncthreads() would drain every outstanding DMA).
-template <int N>
-__device__ __forceinline__ void wait_vm_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
 
 __device__ __forceinline__ u32x4 t64_off128(uint32_t w) {
   u32x4 r;

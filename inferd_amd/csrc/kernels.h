@@ -59,6 +59,10 @@ size_t qmv_t_workspace(int M, int N, int K, int mode);
 size_t gemm_t_workspace(int M, int N, int K, int mode);
 int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   void* ws, size_t ws_bytes, hipStream_t st);
+// W4A8 on T64 weights, per-token int8 activations (U [M][K], XS [M][G][2] from a8_quant).
+size_t w4a8_t_workspace(int M, int N, int K);
+int launch_w4a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                  void* ws, size_t ws_bytes, hipStream_t st);
 // cnt: kWsCounters zeroed counters (the workspace header) for the in-kernel split-K fixup; null -> a reduction kernel
 int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                  unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st);

@@ -1,0 +1,314 @@
+// W4A8 GEMM on T64 weights with per-token int8 activations, on int8 MFMA.
+//
+// Replaces the reference's w4a8_gemm (engine/kernels/w4a8.metal:43-98) and its identity (:8, epilogue :78-87):
+//   y[m][n] = sx[m] * sum_g ( s_g[n] * P_g[m][n] + b_g[n] * X_g[m] ),  P_g = sum_{k in g} q xq,  X_g = sum_{k in g} xq
+// with q the unflipped 4-bit code (T64 stores codes unflipped), xq the int8 activation and sx the row's scale.
+//
+// Block and pipeline as k_gemm_t (gemm_t64.hip): 8 waves in two K-quads (quad kq takes group kq of every two-group
+// chunk; wave wq of a quad the bands wq NB .. + NB - 1 over all BM = 32 MT rows), a kWaNS-stage LDS ring filled by
+// direct global -> LDS DMA, one barrier per chunk. A stage holds the int8 activation slab [BM][128] (16-byte columns
+// XOR-swizzled by row pair: conflict-free fragment reads), the code halves of the chunk's 2 NBB tiles and their
+// (s, b) dwords.
+// Per group and (M tile, band): two v_mfma_i32_32x32x32_i8 give P exactly (the codes unpack to bytes with two masks
+// and two byte permutes per word), and acc += s * float(P): two VALU per accumulator per group, the floor of any
+// per-group-scaled integer product. The bias part sum_g b_g X_g[m] is a GEMM over the groups (K = G): it runs once
+// per tile after the K loop, as bf16 MFMAs into the same accumulators, with X = 256 hi + lo split into two exact
+// bf16 integer planes (prepared by k_w4a8_xprep) and b collected in LDS during the loop (exact products, fp32 sums).
+#include <algorithm>
+
+#include "common.h"
+#include "dma.h"
+#include "host.h"
+#include "kernels.h"
+#include "t64.h"
+
+namespace ifd {
+
+constexpr int kWaNS = 3;        // LDS pipeline stages
+constexpr int kWaMaxGz = 96;    // groups per K split at most (the per-tile bias matrix lives in LDS)
+constexpr int kWaThreads = 512;
+constexpr int kWaBand = 4;      // M tiles per band of the tile order
+
+// X_g = sum xq of each (row, group), recovered exactly from XS = (sx, sx * sum xq) (|sum| <= 8128), split as
+// 256 hi + lo and stored as two bf16 planes [2][M][Gx] (both parts exact in bf16); groups past G are zero.
+__global__ __launch_bounds__(256) void k_w4a8_xprep(const float* __restrict__ XS, int M, int G, int Gx,
+                                                    uint16_t* __restrict__ Xhl) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)M * Gx) return;
+  const int m = (int)(i / Gx), g = (int)(i % Gx);
+  float hi = 0.f, lo = 0.f;
+  if (g < G) {
+    const float x = rintf(XS[((size_t)m * G + g) * 2 + 1] / XS[((size_t)m * G + g) * 2]);
+    hi = floorf(x * (1.f / 256.f));
+    lo = x - 256.f * hi;
+    hi *= 256.f;
+  }
+  Xhl[i] = f2bf(hi);
+  Xhl[(size_t)M * Gx + i] = f2bf(lo);
+}
+
+struct W4A8TArgs {
+  const int8_t* U;    // [M][K] int8, row stride K
+  const float* XS;    // [M][G][2]: sx = XS[m][0][0] (per token)
+  const uint16_t* Xhl;  // [2][M][Gx] bf16
+  int Gx;
+  const uint8_t* wt;
+  int N, K;
+  void* C;
+  int ldc, M, mode;
+  float* part;
+  int gps, tiles_m, tiles_n;
+};
+
+// eight codes of one T64 word -> eight unsigned bytes in k order (code e in nibble (0,4,1,5,2,6,3,7)[e]): the low
+// nibbles of the bytes hold codes 0, 4, 1, 5 and the high nibbles 2, 6, 3, 7
+__device__ __forceinline__ void t64_bytes(uint32_t w, uint32_t& d0, uint32_t& d1) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  d0 = __builtin_amdgcn_perm(hi, lo, 0x06040200u);  // codes 0 1 2 3
+  d1 = __builtin_amdgcn_perm(hi, lo, 0x07050301u);  // codes 4 5 6 7
+}
+
+template <int MT, int NB>
+__global__ __launch_bounds__(kWaThreads, 1) void k_w4a8_t(W4A8TArgs p) {
+  static_assert(MT == 2 || MT == 4, "activation DMAs: MT / 2 per wave");
+  static_assert(NB >= 1 && NB <= 2, "one (s, b) DMA covers a group's NBB <= 8 tiles");
+  constexpr int BM = 32 * MT, NBB = 4 * NB;
+  constexpr int A_BYTES = BM * 128;             // [BM][128 int8]
+  constexpr int C_BYTES = 2 * NBB * kT64Codes;  // [2 groups][NBB bands][1024]
+  constexpr int ST = A_BYTES + C_BYTES + 2 * 1024;
+  constexpr int VPC = MT / 2 + NB;              // DMA instructions per wave per chunk (waves 0, 1: one more)
+  constexpr int NE = MT * NB * 16;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kq = wave >> 2, wq = wave & 3;
+  const int j = lane & 31, h = lane >> 5;
+
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int L = xcd_remap(blockIdx.x, ntiles);
+  const int per_band = kWaBand * p.tiles_n;
+  const int bandi = L / per_band, within = L % per_band;
+  const int bm = min(kWaBand, p.tiles_m - bandi * kWaBand);
+  const int tm = bandi * kWaBand + within % bm, tn = within / bm;
+  const int m0 = tm * BM;
+  const int nbands = t64_bands(p.N);
+  const int G = p.K / kGroup;
+  const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps), Gz = g1 - g0;
+  const int Gzp = (Gz + 15) / 16 * 16;
+  const int nch = Gz / 2, lastg = g0 + 2 * (nch - 1);
+  // b of the tile's columns and this split's groups: [NBB * 32 columns][Gzp] bf16, after the pipeline stages
+  uint16_t* bb = (uint16_t*)(lds + kWaNS * ST);
+
+  // activation DMA: instruction i of this wave covers rows 8 (wave MT / 2 + i) .. + 7; lane -> LDS slot lane of that
+  // 1 KB: row r = 8 (wave MT / 2 + i) + lane / 8, physical 16-byte column lane % 8 holding logical column
+  // (lane % 8) ^ ((r / 2) % 8). Rows past M re-read row M - 1 (their outputs are not stored).
+  const int8_t* asrc[MT / 2];
+#pragma unroll
+  for (int i = 0; i < MT / 2; i++) {
+    const int r = 8 * (wave * (MT / 2) + i) + lane / 8;
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    asrc[i] = p.U + (size_t)min(m0 + r, p.M - 1) * p.K + 16 * c;
+  }
+  const size_t gstride = (size_t)nbands * kT64Tile;
+  const uint8_t* tb[NB];
+#pragma unroll
+  for (int b = 0; b < NB; b++)
+    tb[b] = p.wt + (size_t)min(tn * NBB + wq * NB + b, nbands - 1) * kT64Tile + (size_t)kq * gstride + 16 * lane;
+  const uint8_t* sbsrc = p.wt +
+                         (size_t)min(tn * NBB + (lane % (8 * NBB)) / 8, nbands - 1) * kT64Tile + kT64Codes +
+                         16 * (lane & 7) + (size_t)(wave & 1) * gstride;
+
+  auto issue = [&](int chunk, int stage) {
+    const size_t g = (size_t)min(g0 + 2 * chunk, lastg);
+    uint8_t* st = lds + stage * ST;
+#pragma unroll
+    for (int i = 0; i < MT / 2; i++) dma16(asrc[i] + g * kGroup, st + (wave * (MT / 2) + i) * 1024);
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+      dma16(tb[b] + g * gstride, st + A_BYTES + (kq * NBB + wq * NB + b) * kT64Codes);
+    if (wave < 2) dma16(sbsrc + g * gstride, st + A_BYTES + C_BYTES + wave * 1024);
+  };
+
+  // zero b for the padding groups [Gz, Gzp) (ordered before the loop's writes by its first barrier)
+  for (int i = tid; i < NBB * 32 * (Gzp - Gz); i += kWaThreads)
+    bb[(i / (Gzp - Gz)) * Gzp + Gz + i % (Gzp - Gz)] = 0;
+
+  f32x16 acc[MT][NB];
+#pragma unroll
+  for (int a = 0; a < MT; a++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[a][b] = zero16();
+
+  auto compute = [&](int c, int stage) {
+    const uint8_t* st = lds + stage * ST;
+    const int gl = 2 * c + kq;  // this quad's group, relative to g0
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const int band = wq * NB + b;
+      const u32x4 codes = *(const u32x4*)(st + A_BYTES + (kq * NBB + band) * kT64Codes + 16 * lane);
+      const uint32_t sb = *(const uint32_t*)(st + A_BYTES + C_BYTES + kq * 1024 + band * 128 + 4 * j);
+      const float sc = bf2f((uint16_t)(sb & 0xFFFFu));
+      if (h == 0) bb[(band * 32 + j) * Gzp + gl] = (uint16_t)(sb >> 16);
+      // B fragments: step s takes words 2s, 2s + 1 (k = 32 h + 16 s + 0..15)
+      u32x4 bf[2];
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        uint32_t d[4];
+        t64_bytes(codes[2 * s], d[0], d[1]);
+        t64_bytes(codes[2 * s + 1], d[2], d[3]);
+        bf[s] = u32x4{d[0], d[1], d[2], d[3]};
+      }
+#pragma unroll
+      for (int a = 0; a < MT; a++) {
+        const int r = a * 32 + j;
+        i32x16 P = izero16();
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+          const int col = (4 * kq + 2 * h + s) ^ ((r >> 1) & 7);
+          const u32x4 af = *(const u32x4*)(st + r * 128 + 16 * col);
+          P = mfma_i8(af, bf[s], P);
+        }
+#pragma unroll
+        for (int r2 = 0; r2 < 16; r2++) acc[a][b][r2] = __builtin_fmaf(sc, (float)P[r2], acc[a][b][r2]);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < kWaNS - 1; s++) issue(s, s);
+  for (int c = 0; c < nch; c++) {
+    if (wave < 2) wait_vm_barrier<(VPC + 1) * (kWaNS - 2)>();
+    else wait_vm_barrier<VPC * (kWaNS - 2)>();
+    issue(c + kWaNS - 1, (c + kWaNS - 1) % kWaNS);
+    compute(c, c % kWaNS);
+  }
+  // every DMA landed, every fragment read and b write done
+  wait_vm_barrier<0>();
+
+  // bias part over this split's groups: quad kq takes M tiles [kq MT / 2, (kq + 1) MT / 2) of every band
+  const size_t plane = (size_t)p.M * p.Gx;
+#pragma unroll
+  for (int a = 0; a < MT; a++) {
+    if (a / (MT / 2) != kq) continue;  // wave-uniform; acc stays statically indexed (registers, not scratch)
+    const uint16_t* xr = p.Xhl + (size_t)min(m0 + a * 32 + j, p.M - 1) * p.Gx + g0 + 8 * h;
+    for (int kk = 0; kk < Gzp / 16; kk++) {
+      const u32x4 xhi = *(const u32x4*)(xr + 16 * kk), xlo = *(const u32x4*)(xr + plane + 16 * kk);
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        const u32x4 bv = *(const u32x4*)(bb + ((wq * NB + b) * 32 + j) * Gzp + 16 * kk + 8 * h);
+        acc[a][b] = mfma_bf16(xhi, bv, acc[a][b]);
+        acc[a][b] = mfma_bf16(xlo, bv, acc[a][b]);
+      }
+    }
+  }
+  __syncthreads();  // bb and the stages are free: LDS is reused for the quad reduction
+
+  // quad 1 hands its sums to quad 0
+  float* red = (float*)lds + (size_t)wq * NE * 64 + lane;
+  if (kq == 1) {
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) red[((a * NB + b) * 16 + r) * 64] = acc[a][b][r];
+  }
+  __syncthreads();
+  if (kq == 1) return;
+
+  const bool split = gridDim.y > 1;
+#pragma unroll
+  for (int a = 0; a < MT; a++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = m0 + a * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+      if (row >= p.M) continue;
+      const float sx = p.XS[(size_t)row * G * 2];
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        const int col = (tn * NBB + wq * NB + b) * 32 + j;
+        if (col >= p.N) continue;
+        const float v = sx * (acc[a][b][r] + red[((a * NB + b) * 16 + r) * 64]);
+        if (split) p.part[((size_t)blockIdx.y * p.M + row) * p.N + col] = v;
+        else store_mode(p.C, (size_t)row * p.ldc + col, v, p.mode);
+      }
+    }
+}
+
+// Tile/split plan: MT by M, NB = 2; the K split S (whole 8-group blocks, at most kWaMaxGz groups each) maximises the
+// occupancy of the last round of blocks over 256 CUs, with fp32 partials of at most 64 MB.
+struct WaPlan {
+  int MT, S, gps;
+};
+static WaPlan w4a8_t_plan(int M, int N, int K) {
+  WaPlan pl{};
+  pl.MT = M <= 64 ? 2 : 4;
+  const int G = K / kGroup;
+  const long tiles = (long)((M + 32 * pl.MT - 1) / (32 * pl.MT)) * ((t64_bands(N) + 7) / 8);
+  const long smin = (G + kWaMaxGz - 1) / kWaMaxGz;
+  const long smax = std::max(smin, std::min<long>(G / 8, (64L << 20) / ((long)M * N * 4)));
+  long best = smin;
+  double best_eff = -1.0;
+  for (long S = smin; S <= smax && (S == smin || tiles * (S - 1) < 4 * 256); S++) {
+    const long blocks = tiles * S, rounds = (blocks + 255) / 256;
+    const double eff = (double)blocks / (rounds * 256.0) - 0.02 * (S - 1);
+    if (eff > best_eff + 1e-9) best_eff = eff, best = S;
+  }
+  // whole multiples of 8 groups: the bias pass loads a split's X rows 8 groups (16 bytes) at a time from its start
+  int gps = (int)((G + best - 1) / best);
+  gps = (gps + 7) / 8 * 8;
+  pl.S = (G + gps - 1) / gps;
+  pl.gps = gps;
+  return pl;
+}
+
+static size_t xprep_bytes(int M, int K) {
+  const int Gx = (K / kGroup + 15) / 16 * 16 + 16;
+  return align_up((size_t)2 * M * Gx * sizeof(uint16_t), 256);
+}
+
+size_t w4a8_t_workspace(int M, int N, int K) {
+  const WaPlan pl = w4a8_t_plan(M, N, K);
+  return xprep_bytes(M, K) + (pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0);
+}
+
+template <int MT>
+static int launch_w4a8_t_cfg(const W4A8TArgs& p, int S, hipStream_t st) {
+  constexpr int NB = 2;
+  const size_t pipe = (size_t)kWaNS * (32 * MT * 128 + 2 * 4 * NB * kT64Codes + 2 * 1024);
+  const size_t bbb = (size_t)4 * NB * 32 * ((p.gps + 15) / 16 * 16) * sizeof(uint16_t);
+  const size_t red = (size_t)4 * MT * NB * 16 * 64 * sizeof(float);
+  const size_t lds = std::max(pipe + bbb, red);
+  if (lds > 160 * 1024) return fail(IFD_ERR_UNSUPPORTED, "w4a8_t64: %zu bytes of LDS needed", lds);
+  static bool attr = false;
+  if (!attr) {
+    hipFuncSetAttribute((const void*)k_w4a8_t<MT, NB>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_w4a8_t<MT, NB>), dim3(p.tiles_m * p.tiles_n, S), dim3(kWaThreads), lds, st, p);
+  return check_launch("w4a8_t64");
+}
+
+int launch_w4a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                  void* ws, size_t ws_bytes, hipStream_t st) {
+  if (M == 0) return IFD_OK;
+  if (K % 128) return fail(IFD_ERR_ARG, "T64 W4A8 needs K %% 128 == 0 (K=%d)", K);
+  const WaPlan pl = w4a8_t_plan(M, N, K);
+  const size_t need = w4a8_t_workspace(M, N, K);
+  if (need > ws_bytes || !ws)
+    return fail(IFD_ERR_WORKSPACE, "w4a8_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
+  const int G = K / kGroup, Gx = (G + 15) / 16 * 16 + 16;
+  uint16_t* Xhl = (uint16_t*)ws;
+  float* part = (float*)((char*)ws + xprep_bytes(M, K));
+  const size_t nx = (size_t)M * Gx;
+  hipLaunchKernelGGL(k_w4a8_xprep, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, st, XS, M, G, Gx, Xhl);
+  IFD_TRY(check_launch("w4a8_xprep"));
+  const int nbx = (t64_bands(N) + 7) / 8;
+  W4A8TArgs p{U, XS, Xhl, Gx, (const uint8_t*)wt, N, K, C, ldc, M, mode, part, pl.gps,
+              (M + 32 * pl.MT - 1) / (32 * pl.MT), nbx};
+  IFD_TRY(pl.MT == 2 ? launch_w4a8_t_cfg<2>(p, pl.S, st) : launch_w4a8_t_cfg<4>(p, pl.S, st));
+  if (pl.S > 1) return launch_splitk_reduce(part, pl.S, M, N, C, ldc, mode, st);
+  return IFD_OK;
+}
+
+}  // namespace ifd

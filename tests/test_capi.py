@@ -93,3 +93,9 @@ def test_workspace_queries():
     assert rc == _lib.IFD_ERR_WORKSPACE
     rc = L.ifd_gemm_t64(4096, 5120, 4096, 34816, 5120, 4096, 34816, 1, 0, 4096, HEADER_BYTES, None)
     assert rc == _lib.IFD_ERR_WORKSPACE
+
+
+def test_t64_w4a8_refuses_per_group_activations():
+    L = _lib.lib()
+    rc = L.ifd_gemm_t64_w4a8(4096, 4096, 0, 4096, 256, 256, 4096, 256, 4, 0, None, 0, None)
+    assert rc == _lib.IFD_ERR_UNSUPPORTED and b"per-token" in L.ifd_last_error()

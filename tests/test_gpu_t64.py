@@ -178,3 +178,41 @@ def test_gemm_t64_swiglu_strided_output():
     out = g.host(wide)
     assert np.array_equal(out[:, : N // 2], ref)
     assert np.all(gen.bf16_to_f32(out[:, N // 2:]) == -1.0)
+
+
+@pytest.mark.parametrize("M,N,K", [(37, 200, 512), (128, 384, 1024), (300, 256, 5120), (64, 512, 17408)])
+def test_gemm_t64_w4a8(M, N, K):
+    """W4A8 on T64 weights (int8 MFMA, per-token activations) against the oracle's w4a8_gemm semantics, all store
+    modes; K = 17408 splits K (bias part per split, fp32 partials)."""
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear(N, K, seed=M + 7)
+    A = gen.activations(M, K, seed=M + 8)
+    U, XS = orc.a8_quant(A, True)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    Y = orc.w4a8(U, XS, wq, s, b)
+    C0 = gen.activations(M, N, seed=M + 9)
+    for mode in (0, 1, 2):
+        C = g.dev(C0) if mode == 1 else None
+        out = g.host(ops.gemm_t64_w4a8(g.dev(U), g.dev(XS), T, C, mode=mode))
+        if mode == 0:
+            err = gen.bf16_err(out, Y)
+        elif mode == 1:
+            err = gen.bf16_err(out, Y + gen.bf16_to_f32(C0))
+        else:
+            err = gen.rel_err(out, Y)
+        assert err <= 2e-2, (M, N, K, mode, err)
+
+
+def test_gemm_t64_w4a8_config3_sampled():
+    """BASELINE config 3 (M=2048, K=N=5120, per-token int8) on T64 weights; oracle on 16 sampled rows."""
+    g, ops = _gu(), _ops()
+    M, N, K = 2048, 5120, 5120
+    codes, wq, s, b = gen.qlinear(N, K, seed=60)
+    A = gen.activations(M, K, seed=61)
+    U, XS = ops.a8_quant(g.dev(A), True)
+    out = g.host(ops.gemm_t64_w4a8(U, XS, ops.pack_t64(g.qlinear(wq, s, b))))
+    rows = np.linspace(0, M - 1, 16).astype(int)
+    Ur, XSr = orc.a8_quant(A[rows], True)
+    assert np.array_equal(g.host(U)[rows], Ur)
+    err = gen.bf16_err(out[rows], orc.w4a8(Ur, XSr, wq, s, b))
+    assert err <= 2e-2, err
