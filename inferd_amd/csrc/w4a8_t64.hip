@@ -56,9 +56,19 @@ struct W4A8TArgs {
   int N, K;
   void* C;
   int ldc, M, mode;
-  float* part;
+  float* part;       // K-split partials: [S][M][N] (ntail == 0) or compact [S][ntail][BM][BN] (tail tiles)
   int gps, tiles_m, tiles_n;
+  int tile0, ntail;  // this launch covers tiles tile0 .. tile0 + gridDim.x - 1 of the tile order
 };
+
+// Tile order: bands of kWaBand M tiles walked M-fastest (neighbouring blocks share weight tiles in L2).
+__host__ __device__ inline void wa_tile(int L, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int per_band = kWaBand * tiles_n;
+  const int bandi = L / per_band, within = L % per_band;
+  const int bm = tiles_m - bandi * kWaBand < kWaBand ? tiles_m - bandi * kWaBand : kWaBand;
+  tm = bandi * kWaBand + within % bm;
+  tn = within / bm;
+}
 
 // eight codes of one T64 word -> eight unsigned bytes in k order (code e in nibble (0,4,1,5,2,6,3,7)[e]): the low
 // nibbles of the bytes hold codes 0, 4, 1, 5 and the high nibbles 2, 6, 3, 7
@@ -84,12 +94,9 @@ __global__ __launch_bounds__(kWaThreads, 1) void k_w4a8_t(W4A8TArgs p) {
   const int kq = wave >> 2, wq = wave & 3;
   const int j = lane & 31, h = lane >> 5;
 
-  const int ntiles = p.tiles_m * p.tiles_n;
-  const int L = xcd_remap(blockIdx.x, ntiles);
-  const int per_band = kWaBand * p.tiles_n;
-  const int bandi = L / per_band, within = L % per_band;
-  const int bm = min(kWaBand, p.tiles_m - bandi * kWaBand);
-  const int tm = bandi * kWaBand + within % bm, tn = within / bm;
+  const int Lrel = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  wa_tile(p.tile0 + Lrel, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * BM;
   const int nbands = t64_bands(p.N);
   const int G = p.K / kGroup;
@@ -139,38 +146,57 @@ __global__ __launch_bounds__(kWaThreads, 1) void k_w4a8_t(W4A8TArgs p) {
 #pragma unroll
     for (int b = 0; b < NB; b++) acc[a][b] = zero16();
 
+  // One group per quad and chunk, as MT x NB steps (a, b), a-major. Software-pipelined: the two MFMAs of step t are
+  // issued before the epilogue of step t - 1 (P double-buffered), so the matrix unit works under the cvt/fma VALU;
+  // the activation fragments of M tile a + 1 are read while tile a computes.
   auto compute = [&](int c, int stage) {
     const uint8_t* st = lds + stage * ST;
     const int gl = 2 * c + kq;  // this quad's group, relative to g0
+    u32x4 bf[NB][2];
+    float sc[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
       const int band = wq * NB + b;
       const u32x4 codes = *(const u32x4*)(st + A_BYTES + (kq * NBB + band) * kT64Codes + 16 * lane);
       const uint32_t sb = *(const uint32_t*)(st + A_BYTES + C_BYTES + kq * 1024 + band * 128 + 4 * j);
-      const float sc = bf2f((uint16_t)(sb & 0xFFFFu));
+      sc[b] = bf2f((uint16_t)(sb & 0xFFFFu));
       if (h == 0) bb[(band * 32 + j) * Gzp + gl] = (uint16_t)(sb >> 16);
       // B fragments: step s takes words 2s, 2s + 1 (k = 32 h + 16 s + 0..15)
-      u32x4 bf[2];
 #pragma unroll
       for (int s = 0; s < 2; s++) {
         uint32_t d[4];
         t64_bytes(codes[2 * s], d[0], d[1]);
         t64_bytes(codes[2 * s + 1], d[2], d[3]);
-        bf[s] = u32x4{d[0], d[1], d[2], d[3]};
+        bf[b][s] = u32x4{d[0], d[1], d[2], d[3]};
       }
+    }
+    auto afrag = [&](int a, int s) {
+      const int r = a * 32 + j;
+      return *(const u32x4*)(st + r * 128 + 16 * ((4 * kq + 2 * h + s) ^ ((r >> 1) & 7)));
+    };
+    u32x4 af[2][2];  // M tiles a and a + 1 (tile a + 1 read when step (a, 0) issues, from a = 1 on)
+    af[0][0] = afrag(0, 0);
+    af[0][1] = afrag(0, 1);
+    af[1][0] = afrag(1, 0);
+    af[1][1] = afrag(1, 1);
+    i32x16 P[2];
+    P[0] = mfma_i8(af[0][0], bf[0][0], izero16());
+    P[0] = mfma_i8(af[0][1], bf[0][1], P[0]);
 #pragma unroll
-      for (int a = 0; a < MT; a++) {
-        const int r = a * 32 + j;
-        i32x16 P = izero16();
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-          const int col = (4 * kq + 2 * h + s) ^ ((r >> 1) & 7);
-          const u32x4 af = *(const u32x4*)(st + r * 128 + 16 * col);
-          P = mfma_i8(af, bf[s], P);
+    for (int t = 1; t <= MT * NB; t++) {
+      if (t < MT * NB) {
+        const int a = t / NB, b = t % NB;
+        if (b == 0 && a >= 1 && a + 1 < MT) {
+          af[(a + 1) & 1][0] = afrag(a + 1, 0);
+          af[(a + 1) & 1][1] = afrag(a + 1, 1);
         }
-#pragma unroll
-        for (int r2 = 0; r2 < 16; r2++) acc[a][b][r2] = __builtin_fmaf(sc, (float)P[r2], acc[a][b][r2]);
+        P[t & 1] = mfma_i8(af[a & 1][0], bf[b][0], izero16());
+        P[t & 1] = mfma_i8(af[a & 1][1], bf[b][1], P[t & 1]);
       }
+      const int ap = (t - 1) / NB, bp = (t - 1) % NB;
+#pragma unroll
+      for (int r2 = 0; r2 < 16; r2++)
+        acc[ap][bp][r2] = __builtin_fmaf(sc[bp], (float)P[(t - 1) & 1][r2], acc[ap][bp][r2]);
     }
   };
 
@@ -191,8 +217,12 @@ __global__ __launch_bounds__(kWaThreads, 1) void k_w4a8_t(W4A8TArgs p) {
   for (int a = 0; a < MT; a++) {
     if (a / (MT / 2) != kq) continue;  // wave-uniform; acc stays statically indexed (registers, not scratch)
     const uint16_t* xr = p.Xhl + (size_t)min(m0 + a * 32 + j, p.M - 1) * p.Gx + g0 + 8 * h;
+    auto ld8 = [](const uint16_t* q) {  // 8 bf16 from an 8-byte aligned address (g0 is a multiple of 4 groups)
+      const u32x2 x0 = *(const u32x2*)q, x1 = *(const u32x2*)(q + 4);
+      return u32x4{x0[0], x0[1], x1[0], x1[1]};
+    };
     for (int kk = 0; kk < Gzp / 16; kk++) {
-      const u32x4 xhi = *(const u32x4*)(xr + 16 * kk), xlo = *(const u32x4*)(xr + plane + 16 * kk);
+      const u32x4 xhi = ld8(xr + 16 * kk), xlo = ld8(xr + plane + 16 * kk);
 #pragma unroll
       for (int b = 0; b < NB; b++) {
         const u32x4 bv = *(const u32x4*)(bb + ((wq * NB + b) * 32 + j) * Gzp + 16 * kk + 8 * h);
@@ -229,36 +259,44 @@ __global__ __launch_bounds__(kWaThreads, 1) void k_w4a8_t(W4A8TArgs p) {
         const int col = (tn * NBB + wq * NB + b) * 32 + j;
         if (col >= p.N) continue;
         const float v = sx * (acc[a][b][r] + red[((a * NB + b) * 16 + r) * 64]);
-        if (split) p.part[((size_t)blockIdx.y * p.M + row) * p.N + col] = v;
-        else store_mode(p.C, (size_t)row * p.ldc + col, v, p.mode);
+        if (!split)
+          store_mode(p.C, (size_t)row * p.ldc + col, v, p.mode);
+        else if (p.ntail)
+          p.part[(((size_t)blockIdx.y * p.ntail + Lrel) * BM + (row - m0)) * (NBB * 32) + (col - tn * NBB * 32)] = v;
+        else
+          p.part[((size_t)blockIdx.y * p.M + row) * p.N + col] = v;
       }
     }
 }
 
-// Tile/split plan: MT by M, NB = 2; the K split S (whole 8-group blocks, at most kWaMaxGz groups each) maximises the
-// occupancy of the last round of blocks over 256 CUs, with fp32 partials of at most 64 MB.
+// Tile/split plan: MT by M, NB = 2 (128 x 256 or 64 x 256 tiles). K is split only when a split would exceed
+// kWaMaxGz groups (the per-tile bias matrix lives in LDS); splits are whole multiples of 4 groups. When whole rounds
+// of 256 tiles leave a tail of at most half a round, the tail tiles run in a second launch with K split St ways
+// (St tail blocks per CU instead of one long block), their fp32 partials in a compact [St][tail][BM][BN] buffer.
 struct WaPlan {
-  int MT, S, gps;
+  int MT, S, gps;       // main launch
+  int tiles, full;      // tiles in all; tiles of the main launch (the rest is the tail)
+  int St, gpt;          // tail split and its groups per split (St == 0: no tail launch)
 };
+static int round4(int g) { return (g + 3) / 4 * 4; }
 static WaPlan w4a8_t_plan(int M, int N, int K) {
   WaPlan pl{};
   pl.MT = M <= 64 ? 2 : 4;
   const int G = K / kGroup;
-  const long tiles = (long)((M + 32 * pl.MT - 1) / (32 * pl.MT)) * ((t64_bands(N) + 7) / 8);
-  const long smin = (G + kWaMaxGz - 1) / kWaMaxGz;
-  const long smax = std::max(smin, std::min<long>(G / 8, (64L << 20) / ((long)M * N * 4)));
-  long best = smin;
-  double best_eff = -1.0;
-  for (long S = smin; S <= smax && (S == smin || tiles * (S - 1) < 4 * 256); S++) {
-    const long blocks = tiles * S, rounds = (blocks + 255) / 256;
-    const double eff = (double)blocks / (rounds * 256.0) - 0.02 * (S - 1);
-    if (eff > best_eff + 1e-9) best_eff = eff, best = S;
+  pl.tiles = ((M + 32 * pl.MT - 1) / (32 * pl.MT)) * ((t64_bands(N) + 7) / 8);
+  pl.S = (G + kWaMaxGz - 1) / kWaMaxGz;
+  pl.gps = round4((G + pl.S - 1) / pl.S);
+  pl.S = (G + pl.gps - 1) / pl.gps;
+  pl.full = pl.tiles;
+  const int tail = pl.tiles % 256;
+  if (pl.S == 1 && pl.tiles >= 256 && tail > 0 && tail <= 128) {
+    int St = std::min(std::min(256 / tail, 8), G / 8);
+    if (St >= 2) {
+      pl.gpt = round4((G + St - 1) / St);
+      pl.St = (G + pl.gpt - 1) / pl.gpt;
+      pl.full = pl.tiles - tail;
+    }
   }
-  // whole multiples of 8 groups: the bias pass loads a split's X rows 8 groups (16 bytes) at a time from its start
-  int gps = (int)((G + best - 1) / best);
-  gps = (gps + 7) / 8 * 8;
-  pl.S = (G + gps - 1) / gps;
-  pl.gps = gps;
   return pl;
 }
 
@@ -267,13 +305,39 @@ static size_t xprep_bytes(int M, int K) {
   return align_up((size_t)2 * M * Gx * sizeof(uint16_t), 256);
 }
 
+static size_t wa_part_bytes(const WaPlan& pl, int M, int N) {
+  if (pl.S > 1) return (size_t)pl.S * M * N * sizeof(float);
+  if (pl.St) return (size_t)pl.St * (pl.tiles - pl.full) * (32 * pl.MT) * 256 * sizeof(float);
+  return 0;
+}
+
 size_t w4a8_t_workspace(int M, int N, int K) {
   const WaPlan pl = w4a8_t_plan(M, N, K);
-  return xprep_bytes(M, K) + (pl.S > 1 ? (size_t)pl.S * M * N * sizeof(float) : 0);
+  return xprep_bytes(M, K) + wa_part_bytes(pl, M, N);
+}
+
+// C (mode) = the split sum of the compact tail partials, 4 columns per thread, in split order.
+__global__ __launch_bounds__(256) void k_wa_tail_reduce(const float* __restrict__ part, int St, int ntail, int tile0,
+                                                         int tiles_m, int tiles_n, int BM, int M, int N, void* C,
+                                                         int ldc, int mode) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, per_tile = (size_t)BM * 64;
+  if (i >= (size_t)ntail * per_tile) return;
+  const int t = (int)(i / per_tile), e = (int)(i % per_tile), r = e / 64, c = (e % 64) * 4;
+  int tm, tn;
+  wa_tile(tile0 + t, tiles_m, tiles_n, tm, tn);
+  const int row = tm * BM + r, col = tn * 256 + c;
+  if (row >= M || col >= N) return;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int z = 0; z < St; z++) {
+    const float4 q = *(const float4*)(part + (((size_t)z * ntail + t) * BM + r) * 256 + c);
+    v.x += q.x, v.y += q.y, v.z += q.z, v.w += q.w;
+  }
+  const float vv[4] = {v.x, v.y, v.z, v.w};
+  for (int k = 0; k < 4 && col + k < N; k++) store_mode(C, (size_t)row * ldc + col + k, vv[k], mode);
 }
 
 template <int MT>
-static int launch_w4a8_t_cfg(const W4A8TArgs& p, int S, hipStream_t st) {
+static int launch_w4a8_t_cfg(const W4A8TArgs& p, int blocks, int S, hipStream_t st) {
   constexpr int NB = 2;
   const size_t pipe = (size_t)kWaNS * (32 * MT * 128 + 2 * 4 * NB * kT64Codes + 2 * 1024);
   const size_t bbb = (size_t)4 * NB * 32 * ((p.gps + 15) / 16 * 16) * sizeof(uint16_t);
@@ -285,7 +349,7 @@ static int launch_w4a8_t_cfg(const W4A8TArgs& p, int S, hipStream_t st) {
     hipFuncSetAttribute((const void*)k_w4a8_t<MT, NB>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     attr = true;
   }
-  hipLaunchKernelGGL((k_w4a8_t<MT, NB>), dim3(p.tiles_m * p.tiles_n, S), dim3(kWaThreads), lds, st, p);
+  hipLaunchKernelGGL((k_w4a8_t<MT, NB>), dim3(blocks, S), dim3(kWaThreads), lds, st, p);
   return check_launch("w4a8_t64");
 }
 
@@ -303,12 +367,24 @@ int launch_w4a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K
   const size_t nx = (size_t)M * Gx;
   hipLaunchKernelGGL(k_w4a8_xprep, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, st, XS, M, G, Gx, Xhl);
   IFD_TRY(check_launch("w4a8_xprep"));
-  const int nbx = (t64_bands(N) + 7) / 8;
-  W4A8TArgs p{U, XS, Xhl, Gx, (const uint8_t*)wt, N, K, C, ldc, M, mode, part, pl.gps,
-              (M + 32 * pl.MT - 1) / (32 * pl.MT), nbx};
-  IFD_TRY(pl.MT == 2 ? launch_w4a8_t_cfg<2>(p, pl.S, st) : launch_w4a8_t_cfg<4>(p, pl.S, st));
+  const int tiles_m = (M + 32 * pl.MT - 1) / (32 * pl.MT), tiles_n = (t64_bands(N) + 7) / 8;
+  auto launch = [&](const W4A8TArgs& p, int blocks, int S) {
+    return pl.MT == 2 ? launch_w4a8_t_cfg<2>(p, blocks, S, st) : launch_w4a8_t_cfg<4>(p, blocks, S, st);
+  };
+  // main launch: tiles [0, full), K split pl.S ways (full [S][M][N] partials when S > 1)
+  W4A8TArgs p{U, XS, Xhl, Gx, (const uint8_t*)wt, N, K, C, ldc, M, mode, part, pl.gps, tiles_m, tiles_n, 0, 0};
+  IFD_TRY(launch(p, pl.full, pl.S));
   if (pl.S > 1) return launch_splitk_reduce(part, pl.S, M, N, C, ldc, mode, st);
-  return IFD_OK;
+  if (!pl.St) return IFD_OK;
+  // tail launch: tiles [full, tiles), K split St ways into compact partials, then their reduction
+  const int ntail = pl.tiles - pl.full, BM = 32 * pl.MT;
+  W4A8TArgs q{U, XS, Xhl, Gx, (const uint8_t*)wt, N, K, C, ldc, M, mode, part, pl.gpt, tiles_m, tiles_n, pl.full,
+              ntail};
+  IFD_TRY(launch(q, ntail, pl.St));
+  const size_t n = (size_t)ntail * BM * 64;
+  hipLaunchKernelGGL(k_wa_tail_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, pl.St, ntail,
+                     pl.full, tiles_m, tiles_n, BM, M, N, C, ldc, mode);
+  return check_launch("w4a8_tail_reduce");
 }
 
 }  // namespace ifd

@@ -216,3 +216,25 @@ def test_gemm_t64_w4a8_config3_sampled():
     assert np.array_equal(g.host(U)[rows], Ur)
     err = gen.bf16_err(out[rows], orc.w4a8(Ur, XSr, wq, s, b))
     assert err <= 2e-2, err
+
+
+def test_gemm_t64_w4a8_tail_split():
+    """A tile count just past a whole round (9 x 30 = 270 tiles): the last 14 tiles run K-split in a second launch
+    with compact partials; sampled rows against the oracle, all three store modes."""
+    from inferd_amd._lib import lib
+    g, ops = _gu(), _ops()
+    M, N, K = 1152, 7680, 1024
+    codes, wq, s, b = gen.qlinear(N, K, seed=70)
+    A = gen.activations(M, K, seed=71)
+    U, XS = ops.a8_quant(g.dev(A), True)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    rows = np.linspace(0, M - 1, 24).astype(int)
+    Ur, XSr = orc.a8_quant(A[rows], True)
+    Y = orc.w4a8(Ur, XSr, wq, s, b)
+    C0 = gen.activations(M, N, seed=72)
+    assert lib().ifd_gemm_t64_w4a8_workspace(M, N, K) > 4096 + 2 * M * 48 * 2  # tail partials present
+    for mode in (0, 1, 2):
+        out = g.host(ops.gemm_t64_w4a8(U, XS, T, g.dev(C0) if mode == 1 else None, mode=mode))[rows]
+        ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
+        err = gen.rel_err(out, ref) if mode == 2 else gen.bf16_err(out, ref)
+        assert err <= 2e-2, (mode, err)
