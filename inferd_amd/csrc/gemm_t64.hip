@@ -29,6 +29,7 @@
 #include "host.h"
 #include "kernels.h"
 #include "t64.h"
+#include "t64_dev.h"
 
 namespace ifd {
 
@@ -47,30 +48,6 @@ struct GemmTArgs {
 constexpr int kGtBand = 4;  // M tiles per band of the tile order
 constexpr int kGtNS = 3;    // LDS pipeline stages
 constexpr int kGtThreads = 512;
-
-__device__ __forceinline__ u32x4 t64_off128(uint32_t w) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; i++) r[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
-  return r;
-}
-// Eight T64 codes (one word) -> bf16(s q + b) in natural k order. Code 2i sits in nibble i, code 2i + 1 in nibble
-// i + 4 (t64.h), so the low nibbles of the four bytes hold codes 0, 4, 1, 5 and the high nibbles codes 2, 6, 3, 7.
-// Two masks split the word into bytes; one byte -> fp32 conversion per code (v_cvt_f32_ubyte0..3) gives q, or 16 q for
-// the high nibbles, which take s / 16 (exact: a power-of-two scaling of a bf16); fma rounds s q + b once in fp32, as
-// the bf16(fp32(s q + b)) of the MLX loader. 22 VALU instructions per 8 codes, two of them integer ops: integer VALU
-// co-issues poorly beside MFMA, conversions and fma well. The masks go through opaque moves so that the compiler
-// selects the byte conversions instead of folding the masks into bitfield extracts.
-__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float s, float s16, float b) {
-  uint32_t lo, hi;
-  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
-  asm("v_and_b32 %0, 0xf0f0f0f0, %1" : "=v"(hi) : "v"(w));
-  const float c0 = __builtin_fmaf(s, (float)(lo & 0xFFu), b), c4 = __builtin_fmaf(s, (float)((lo >> 8) & 0xFFu), b);
-  const float c1 = __builtin_fmaf(s, (float)((lo >> 16) & 0xFFu), b), c5 = __builtin_fmaf(s, (float)(lo >> 24), b);
-  const float c2 = __builtin_fmaf(s16, (float)(hi & 0xFFu), b), c6 = __builtin_fmaf(s16, (float)((hi >> 8) & 0xFFu), b);
-  const float c3 = __builtin_fmaf(s16, (float)((hi >> 16) & 0xFFu), b), c7 = __builtin_fmaf(s16, (float)(hi >> 24), b);
-  return u32x4{pack_bf2(c0, c1), pack_bf2(c2, c3), pack_bf2(c4, c5), pack_bf2(c6, c7)};
-}
 
 template <int MT, int NB, bool DEQ>
 __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
@@ -295,7 +272,13 @@ static GtPlan gemm_t_plan(int M, int N, int K) {
   return pl;
 }
 
+// Prefill shapes that fill at least one round of 256 CUs with 256-row tiles go to k_gemm_t8 (gemm_t8.hip): half the
+// dequant VALU per MFMA.
+static bool use_t8(int M, int N) { return (long)((M + 255) / 256) * ((t64_bands(N) + 7) / 8) >= 256; }
+
 size_t gemm_t_workspace(int M, int N, int K, int mode) {
+  if (use_t8(M, N))
+    return align_up(gemm_t8_workspace(M, N, K), 256) + (mode == kModeSwiglu ? (size_t)M * N * sizeof(uint16_t) : 0);
   return epilogue_ws_bytes(gemm_t_plan(M, N, K).S, M, N, mode);
 }
 
@@ -317,6 +300,16 @@ int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void
                   void* ws, size_t ws_bytes, hipStream_t st) {
   if (M == 0) return IFD_OK;
   if (K % 128) return fail(IFD_ERR_ARG, "T64 GEMM needs K %% 128 == 0 (K=%d)", K);
+  if (use_t8(M, N)) {
+    const size_t need = gemm_t_workspace(M, N, K, mode), t8ws = gemm_t8_workspace(M, N, K);
+    if (need > ws_bytes || (need && !ws))
+      return fail(IFD_ERR_WORKSPACE, "gemm_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
+    if (mode != kModeSwiglu) return launch_gemm_t8(A, lda, wt, N, K, C, ldc, M, mode, ws, t8ws, st);
+    // SwiGLU: the bf16 product into the workspace (after the tail partials), then silu_mul
+    uint16_t* gu = (uint16_t*)((char*)ws + align_up(t8ws, 256));
+    IFD_TRY(launch_gemm_t8(A, lda, wt, N, K, gu, N, M, 0, ws, t8ws, st));
+    return launch_silu_mul(gu, N, (uint16_t*)C, ldc, N / 2, M, st);
+  }
   const GtPlan pl = gemm_t_plan(M, N, K);
   const size_t need = epilogue_ws_bytes(pl.S, M, N, mode);
   if (need > ws_bytes || (need && !ws))

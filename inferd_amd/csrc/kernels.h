@@ -57,6 +57,10 @@ int launch_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, in
                     int E, void* out, hipStream_t st);
 size_t qmv_t_workspace(int M, int N, int K, int mode);
 size_t gemm_t_workspace(int M, int N, int K, int mode);
+// 256-row-tile prefill GEMM on T64 weights (modes 0-2); gemm_t routes prefill shapes to it.
+size_t gemm_t8_workspace(int M, int N, int K);
+int launch_gemm_t8(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                   void* ws, size_t ws_bytes, hipStream_t st);
 int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   void* ws, size_t ws_bytes, hipStream_t st);
 // W4A8 on T64 weights, per-token int8 activations (U [M][K], XS [M][G][2] from a8_quant).

@@ -238,3 +238,32 @@ def test_gemm_t64_w4a8_tail_split():
         ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
         err = gen.rel_err(out, ref) if mode == 2 else gen.bf16_err(out, ref)
         assert err <= 2e-2, (mode, err)
+
+
+def test_gemm_t64_prefill_tiles_with_tail():
+    """A prefill shape on the 256-row-tile kernel whose last round holds 4 tiles (5 x 52 = 260): those run K-split
+    in a second launch. Sampled rows against the qmm oracle, all three store modes."""
+    g, ops = _gu(), _ops()
+    M, N, K = 1280, 13312, 1024
+    codes, wq, s, b = gen.qlinear(N, K, seed=80)
+    A = gen.activations(M, K, seed=81, row_scale=True)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    rows = np.linspace(0, M - 1, 24).astype(int)
+    Y = orc.qmm(np.ascontiguousarray(A[rows]), wq, s, b)
+    C0 = gen.activations(M, N, seed=82)
+    for mode in (0, 1, 2):
+        out = g.host(ops.gemm_t64(g.dev(A), T, g.dev(C0) if mode == 1 else None, mode=mode))[rows]
+        ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
+        err = gen.rel_err(out, ref) if mode == 2 else gen.bf16_err(out, ref)
+        assert err <= 1e-2, (mode, err)
+
+
+def test_gemm_t64_swiglu_prefill_tiles():
+    """The fused gate/up entry on a prefill shape (256-row tiles, 4 x 64 = 256 tiles): bit-identical to gemm_t64 +
+    silu_mul."""
+    g, ops = _gu(), _ops()
+    M, N, K = 1024, 16384, 256
+    codes, wq, s, b = gen.qlinear(N, K, seed=83)
+    A = g.dev(gen.activations(M, K, seed=84))
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    assert np.array_equal(g.host(ops.gemm_t64_swiglu(A, T)), g.host(ops.silu_mul(ops.gemm_t64(A, T))))
