@@ -278,13 +278,18 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded 4-bit affine weights, bf16 N(0,1) activations)",
     }
+    # HBM bytes per call of a bench call, from the FETCH_SIZE / WRITE_SIZE counter runs of the same workload scaled by
+    # a plain 256 MiB device copy (profiles/traffic_decode_mlp.md); calls not measured report null
+    measured_traffic = {"gate_up_swiglu_M128": 236426212}
+
     def roofline(d):
         # the bound is the larger of the call's two floors: its algorithmic bytes at HBM peak, its flops at dense
         # bf16 MFMA peak
         mfma = d["flops"] / (BF16_PEAK_TFLOPS * 1e12) > d["bytes"] / (HBM_PEAK_GBS * 1e9)
         ach, peak = (d["tflops"], BF16_PEAK_TFLOPS) if mfma else (d["gbs"], HBM_PEAK_GBS)
         return {"kernel": d["name"], "bound": "mfma" if mfma else "hbm", "achieved": round(ach, 1), "peak": peak,
-                "unit": "TFLOP/s" if mfma else "GB/s", "frac": round(ach / peak, 4), "traffic": None,
+                "unit": "TFLOP/s" if mfma else "GB/s", "frac": round(ach / peak, 4),
+                "traffic": measured_traffic.get(d["name"]),
                 "us": round(d["ms"] * 1e3, 2), "gbs": round(d["gbs"], 1), "tflops": round(d["tflops"], 1)}
 
     if "headline" in out:
