@@ -9,8 +9,9 @@
 // chunk, and wave wq (= wave % 4) of a quad the bands wq NB .. + NB - 1 over all BM rows. The two waves on a SIMD thus
 // work on the same outputs at different K, and their instruction streams interleave (one's dequant VALU and LDS
 // reads under the other's MFMAs). At the end quad 1 adds its sums into quad 0's through LDS.
-// Chunks flow through a kGtNS-stage LDS ring filled by direct global->LDS DMA (global_load_lds_dwordx4), kGtNS - 1
-// chunks ahead, at no VGPR cost, with one s_barrier per chunk. A stage holds the activation slab [BM][128 bf16]
+// Chunks flow through an NS-stage LDS ring filled by direct global->LDS DMA (global_load_lds_dwordx4), NS - 1 chunks
+// ahead, at no VGPR cost, with one s_barrier per chunk; NS is as deep as 160 KB of LDS allows for the tile height, so
+// that the short tiles keep more weight bytes in flight. A stage holds the activation slab [BM][128 bf16]
 // (16-byte columns XOR-swizzled by row: conflict-free fragment reads), the code halves of the chunk's 2 NBB T64
 // tiles, and their (s, b) dwords [2 groups][1 KB]. Per chunk every wave DMAs MT activation row quads and its own NB
 // code tiles; waves 0 and 1 also the (s, b) dwords of group 0 and 1.
@@ -46,16 +47,23 @@ struct GemmTArgs {
 };
 
 constexpr int kGtBand = 4;  // M tiles per band of the tile order
-constexpr int kGtNS = 3;    // LDS pipeline stages
 constexpr int kGtThreads = 512;
+
+// bytes of one pipeline stage, and the stages that fit in 160 KB of LDS
+__host__ __device__ constexpr int gt_stage_bytes(int MT, int NB) { return MT * 32 * 256 + 2 * 4 * NB * kT64Codes + 2 * 1024; }
+__host__ __device__ constexpr int gt_stages(int MT, int NB) {
+  return 160 * 1024 / gt_stage_bytes(MT, NB) < 6 ? 160 * 1024 / gt_stage_bytes(MT, NB) : 6;
+}
 
 template <int MT, int NB, bool DEQ>
 __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
+  constexpr int NS = gt_stages(MT, NB);
   static_assert(NB >= 1 && NB <= 2, "one (s, b) DMA covers a group's NBB <= 8 tiles");
   constexpr int BM = 32 * MT, NBB = 4 * NB;
   constexpr int A_BYTES = BM * 256;             // [BM][128 bf16]
   constexpr int C_BYTES = 2 * NBB * kT64Codes;  // [2 groups][NBB bands][1024]
   constexpr int ST = A_BYTES + C_BYTES + 2 * 1024;  // + [2 groups][1 KB] (s, b)
+  static_assert(ST == gt_stage_bytes(MT, NB) && NS >= 3, "stage layout");
   constexpr int VPC = MT + NB;                  // DMA instructions per wave per chunk (waves 0, 1: one more)
   constexpr int NE = MT * NB * 16;              // accumulators per lane
   extern __shared__ __align__(16) uint8_t lds[];
@@ -194,16 +202,16 @@ __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
   };
 
   // Every iteration issues one chunk (past the end: a re-read of the last chunk into a stage nobody reads again), so
-  // each wave's count of outstanding DMA instructions is the same on every iteration: waiting for its DMAs of
-  // kGtNS - 2 chunks leaves the younger chunks in flight. The LDS reads of the previous chunk finish before the
-  // barrier that lets any wave overwrite that stage.
+  // each wave's count of outstanding DMA instructions is the same on every iteration: waiting for all but its DMAs of
+  // the NS - 2 youngest chunks leaves those in flight. The LDS reads of the previous chunk finish before the barrier
+  // that lets any wave overwrite that stage.
 #pragma unroll
-  for (int s = 0; s < kGtNS - 1; s++) issue(s, s);
+  for (int s = 0; s < NS - 1; s++) issue(s, s);
   for (int c = 0; c < nch; c++) {
-    if (wave < 2) wait_vm_barrier<(VPC + 1) * (kGtNS - 2)>();
-    else wait_vm_barrier<VPC * (kGtNS - 2)>();
-    issue(c + kGtNS - 1, (c + kGtNS - 1) % kGtNS);
-    compute(c % kGtNS);
+    if (wave < 2) wait_vm_barrier<(VPC + 1) * (NS - 2)>();
+    else wait_vm_barrier<VPC * (NS - 2)>();
+    issue(c + NS - 1, (c + NS - 1) % NS);
+    compute(c % NS);
   }
   // no DMA may still target LDS and every wave's fragment reads are done before LDS is reused for the sums
   wait_vm_barrier<0>();
@@ -277,6 +285,7 @@ static GtPlan gemm_t_plan(int M, int N, int K) {
 static bool use_t8(int M, int N) { return (long)((M + 255) / 256) * ((t64_bands(N) + 7) / 8) >= 256; }
 
 size_t gemm_t_workspace(int M, int N, int K, int mode) {
+  if (!use_t8(M, N) && gemm_sk_applies(M, N, K, mode)) return gemm_sk_workspace(M, N, K, mode);
   if (use_t8(M, N))
     return align_up(gemm_t8_workspace(M, N, K), 256) + (mode == kModeSwiglu ? (size_t)M * N * sizeof(uint16_t) : 0);
   return epilogue_ws_bytes(gemm_t_plan(M, N, K).S, M, N, mode);
@@ -284,7 +293,7 @@ size_t gemm_t_workspace(int M, int N, int K, int mode) {
 
 template <int MT, int NB, bool DEQ>
 static int launch_gemm_t_cfg(const GemmTArgs& p, int S, hipStream_t st) {
-  const size_t pipe = (size_t)kGtNS * (32 * MT * 256 + 2 * 4 * NB * kT64Codes + 2 * 1024);
+  const size_t pipe = (size_t)gt_stages(MT, NB) * gt_stage_bytes(MT, NB);
   const size_t red = (size_t)4 * MT * NB * 16 * 64 * sizeof(float);  // quad 1's sums, after the K loop
   const size_t lds = std::max(pipe, red);
   static bool attr = false;
@@ -300,6 +309,9 @@ int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void
                   void* ws, size_t ws_bytes, hipStream_t st) {
   if (M == 0) return IFD_OK;
   if (K % 128) return fail(IFD_ERR_ARG, "T64 GEMM needs K %% 128 == 0 (K=%d)", K);
+  // decode batches: the stream-K kernel (every CU streams an equal share of the weights, fixup in the kernel)
+  if (!use_t8(M, N) && gemm_sk_applies(M, N, K, mode))
+    return launch_gemm_sk(A, lda, wt, N, K, C, ldc, M, mode, ws, ws_bytes, st);
   if (use_t8(M, N)) {
     const size_t need = gemm_t_workspace(M, N, K, mode), t8ws = gemm_t8_workspace(M, N, K);
     if (need > ws_bytes || (need && !ws))

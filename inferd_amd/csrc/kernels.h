@@ -63,6 +63,12 @@ int launch_gemm_t8(const uint16_t* A, int lda, const void* wt, int N, int K, voi
                    void* ws, size_t ws_bytes, hipStream_t st);
 int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   void* ws, size_t ws_bytes, hipStream_t st);
+// Stream-K GEMM for decode batches (gemm_sk.hip): every CU streams an equal share of the weights; the cut tiles are
+// summed by a fixup kernel.
+bool gemm_sk_applies(int M, int N, int K, int mode);
+size_t gemm_sk_workspace(int M, int N, int K, int mode);
+int launch_gemm_sk(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                   void* ws, size_t ws_bytes, hipStream_t st);
 // W4A8 on T64 weights, per-token int8 activations (U [M][K], XS [M][G][2] from a8_quant).
 size_t w4a8_t_workspace(int M, int N, int K);
 int launch_w4a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
