@@ -39,17 +39,23 @@ constexpr int kSkLds = 160 * 1024;  // LDS per CU
 constexpr int kSkRow = 256 + 4;  // staged tile row stride (floats): rows h = 0, 1 of one store fall in other banks
 
 // 32-row tiles run two blocks per CU (four waves per SIMD hide the latency of their short steps); a ring of four or
-// more stages keeps the weight stream at full rate
+// more stages keeps the weight stream at full rate. 128-row tiles favour a deeper activation ring (16 KB slabs) over a
+// deeper weight ring (measured).
 __host__ __device__ constexpr int sk_bpc(int MT) { return MT == 1 ? 2 : 1; }
 __host__ __device__ constexpr int sk_abytes(int MT) { return MT * 32 * 128; }
-__host__ __device__ constexpr int sk_na(int MT) { return MT == 1 ? 4 : MT == 2 ? 5 : 4; }
+__host__ __device__ constexpr int sk_na(int MT) { return MT == 1 ? 4 : MT == 2 ? 5 : 6; }
 __host__ __device__ constexpr int sk_nw(int MT) {
-  return (kSkLds / sk_bpc(MT) - 64 - sk_na(MT) * sk_abytes(MT)) / kSkWBytes < 15
+  return MT == 4 ? 5
+         : (kSkLds / sk_bpc(MT) - 64 - sk_na(MT) * sk_abytes(MT)) / kSkWBytes < 15
              ? (kSkLds / sk_bpc(MT) - 64 - sk_na(MT) * sk_abytes(MT)) / kSkWBytes
              : 15;
 }
-__host__ __device__ constexpr size_t sk_lds(int MT) {
+__host__ __device__ constexpr size_t sk_rings(int MT) {
   return (size_t)sk_na(MT) * sk_abytes(MT) + (size_t)sk_nw(MT) * kSkWBytes;
+}
+// the rings, and after the K loop the staged tile [32 MT][kSkRow] fp32 in the same memory
+__host__ __device__ constexpr size_t sk_lds(int MT) {
+  return sk_rings(MT) > (size_t)MT * 32 * kSkRow * 4 ? sk_rings(MT) : (size_t)MT * 32 * kSkRow * 4;
 }
 
 struct GemmSkArgs {
@@ -85,7 +91,6 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
   constexpr int NE = MT * 16;  // accumulators per lane
   static_assert(NA >= 3 && NW >= 4 && sk_lds(MT) + 64 <= kSkLds / sk_bpc(MT), "LDS plan");
   static_assert(3 * (NW - 2) <= 63 && MT * (NA - 2) <= 63, "vmcnt range");
-  static_assert((size_t)BM * kSkRow * 4 <= sk_lds(MT), "the staged tile fits the rings");
   extern __shared__ __align__(16) uint8_t lds[];
   uint8_t* const aring = lds;
   uint8_t* const wring = lds + NA * A_BYTES;
