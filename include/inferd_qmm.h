@@ -83,6 +83,24 @@ int ifd_silu_mul(const void* gu, void* h, int I, int rows, void* stream);
 int ifd_rmsnorm(const void* x, int in_stride, const void* w, void* out, int out_stride, int rows, int D, float eps,
                 void* stream);
 
+/* ---- fused producers of the decode step (bit-identical to their unfused sequences) -------------------------------
+ * rmsnorm fused with the W4A8 activation quantization of the next GEMM: out as ifd_rmsnorm, and U int8 [rows][D] /
+ * XS float [rows][D/64][2] as ifd_a8_quant of out (per_token as there). Replaces the reference's rmsnorm_a8
+ * (engine/kernels/core.metal:502-537, per group there), issued by rmsnorm_for (engine/src/qwen35.h:1982-2000).
+ * D % 64 == 0. */
+int ifd_rmsnorm_a8(const void* x, int in_stride, const void* w, void* out, int out_stride, int rows, int D, float eps,
+                   int per_token, int8_t* U, float* XS, void* stream);
+/* silu_mul fused with the W4A8 activation quantization of the down projection: U [rows][I] / XS [rows][I/64][2] of
+ * h = silu_mul(gu) (h is not written), as ifd_silu_mul then ifd_a8_quant. Replaces silu_mul_a8
+ * (core.metal:789-814; issued at qwen35.h:2874). I % 64 == 0. */
+int ifd_silu_mul_a8(const void* gu, int I, int rows, int per_token, int8_t* U, float* XS, void* stream);
+/* A deferred split-K residual reduce fused into the next rmsnorm: x[r] = bf16(sum_z part[z][r] + x[r]) in split
+ * order (as the split-K reduction with mode 1), then out = rmsnorm(x) and, when U is not null, U / XS as
+ * ifd_a8_quant of out. part fp32 [S][rows][D]. Replaces splitk_res_norm / splitk_res_norm_a8 (core.metal:539-595),
+ * issued by rmsnorm_for (qwen35.h:1982-1998). With U, D % 64 == 0. */
+int ifd_splitk_res_norm(const float* part, int S, void* x, int ldx, const void* w, void* out, int out_stride, int rows,
+                        int D, float eps, int per_token, int8_t* U, float* XS, void* stream);
+
 /* ---- T64: the MI355X weight layout (no counterpart in the reference; its role is that of the reference's
  * load-time weight transforms, flip and the lane4/qmst copies, qwen35.h:1209-1322) -------------------------------
  * A one-time repack of the MLX layout into 1152-byte tiles (per 64-group and 32-column band: the codes in MFMA

@@ -31,6 +31,9 @@ SIGNATURES = {
     "ifd_silu_mul": (_i, [_vp, _vp, _i, _i, _vp]),
     "ifd_rmsnorm": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp]),
     "ifd_a8_quant": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "ifd_rmsnorm_a8": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, ctypes.c_float, _i, _vp, _vp, _vp]),
+    "ifd_silu_mul_a8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "ifd_splitk_res_norm": (_i, [_vp, _i, _vp, _i, _vp, _vp, _i, _i, _i, ctypes.c_float, _i, _vp, _vp, _vp]),
     "ifd_qmm_w4a8": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _u32, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_qmm_w4a8_workspace": (_sz, [_i, _i, _i]),
     "ifd_t64_bytes": (_sz, [_i, _i, _i]),

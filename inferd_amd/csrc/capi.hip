@@ -120,6 +120,33 @@ int ifd_rmsnorm(const void* x, int in_stride, const void* w, void* out, int out_
                         S(stream));
 }
 
+int ifd_rmsnorm_a8(const void* x, int in_stride, const void* w, void* out, int out_stride, int rows, int D, float eps,
+                   int per_token, int8_t* U, float* XS, void* stream) {
+  IFD_CHECK(rows >= 0 && D > 0 && D % 64 == 0 && in_stride >= D && out_stride >= D,
+            "bad shape rows=%d D=%d strides %d/%d (D multiple of 64)", rows, D, in_stride, out_stride);
+  IFD_CHECK(rows == 0 || (x && w && out && U && XS), "null pointer");
+  IFD_CHECK(eps >= 0.f, "eps must be >= 0");
+  return launch_rmsnorm_a8((const uint16_t*)x, in_stride, (const uint16_t*)w, (uint16_t*)out, out_stride, rows, D, eps,
+                           per_token ? 1 : 0, U, XS, S(stream));
+}
+
+int ifd_silu_mul_a8(const void* gu, int I, int rows, int per_token, int8_t* U, float* XS, void* stream) {
+  IFD_CHECK(I > 0 && I % 64 == 0 && rows >= 0, "bad shape I=%d rows=%d (I multiple of 64)", I, rows);
+  IFD_CHECK(rows == 0 || (gu && U && XS), "null pointer");
+  return launch_silu_mul_a8((const uint16_t*)gu, 2 * I, I, rows, per_token ? 1 : 0, U, XS, S(stream));
+}
+
+int ifd_splitk_res_norm(const float* part, int S_, void* x, int ldx, const void* w, void* out, int out_stride, int rows,
+                        int D, float eps, int per_token, int8_t* U, float* XS, void* stream) {
+  IFD_CHECK(rows >= 0 && D > 0 && S_ >= 1 && ldx >= D && out_stride >= D, "bad shape rows=%d D=%d S=%d strides %d/%d",
+            rows, D, S_, ldx, out_stride);
+  IFD_CHECK(rows == 0 || (part && x && w && out), "null pointer");
+  IFD_CHECK(!U || (XS && D % 64 == 0), "quantized output needs XS and D %% 64 == 0 (D=%d)", D);
+  IFD_CHECK(eps >= 0.f, "eps must be >= 0");
+  return launch_splitk_res_norm(part, S_, (uint16_t*)x, ldx, (const uint16_t*)w, (uint16_t*)out, out_stride, rows, D,
+                                eps, U ? (per_token ? 2 : 1) : 0, U, XS, S(stream));
+}
+
 int ifd_a8_quant(const void* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, void* stream) {
   IFD_CHECK(M >= 0 && K > 0 && K % 64 == 0 && lda >= K, "bad shape M=%d K=%d lda=%d", M, K, lda);
   IFD_CHECK(M == 0 || (A && U && XS), "null pointer");

@@ -34,6 +34,13 @@ int launch_flip(uint32_t* wq, size_t n32, uint32_t mask, hipStream_t st);
 int launch_silu_mul(const uint16_t* gu, int ldgu, uint16_t* h, int ldh, int I, int rows, hipStream_t st);
 int launch_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows,
                    int D, float eps, hipStream_t st);
+// Fused producers (fused.hip).
+int launch_rmsnorm_a8(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows,
+                      int D, float eps, int per_token, int8_t* U, float* XS, hipStream_t st);
+int launch_silu_mul_a8(const uint16_t* gu, int ldgu, int I, int rows, int per_token, int8_t* U, float* XS,
+                       hipStream_t st);
+int launch_splitk_res_norm(const float* part, int S, uint16_t* x, int ldx, const uint16_t* w, uint16_t* out,
+                           int out_stride, int rows, int D, float eps, int a8, int8_t* U, float* XS, hipStream_t st);
 // Every public workspace starts with kWsHeader bytes of completion counters (uint32), which the library keeps at zero
 // between calls: the caller zeroes them once when the workspace is allocated. Kernel scratch follows the header.
 constexpr size_t kWsHeader = 4096;

@@ -155,6 +155,43 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: Optional[torch.Te
     return y
 
 
+def rmsnorm_a8(x: torch.Tensor, w: torch.Tensor, eps: float, per_token: bool):
+    """rmsnorm of bf16 x [R, D] and the W4A8 quantization of its output (reference rmsnorm_a8, core.metal:502-537):
+    returns (out bf16 [R, D], U int8 [R, D], XS fp32 [R, D/64, 2])."""
+    R, D = x.shape
+    y = torch.empty((R, D), dtype=torch.bfloat16, device=x.device)
+    U = torch.empty((R, D), dtype=torch.int8, device=x.device)
+    XS = torch.empty((R, D // 64, 2), dtype=torch.float32, device=x.device)
+    check(lib().ifd_rmsnorm_a8(_p(x), x.stride(0), _p(w), _p(y), D, R, D, float(eps), 1 if per_token else 0, _p(U),
+                               _p(XS), _stream()))
+    return y, U, XS
+
+
+def silu_mul_a8(gu: torch.Tensor, per_token: bool):
+    """The W4A8 quantization of silu_mul(gu) without writing h (reference silu_mul_a8, core.metal:789-814)."""
+    R, I2 = gu.shape
+    I = I2 // 2
+    U = torch.empty((R, I), dtype=torch.int8, device=gu.device)
+    XS = torch.empty((R, I // 64, 2), dtype=torch.float32, device=gu.device)
+    check(lib().ifd_silu_mul_a8(_p(gu), I, R, 1 if per_token else 0, _p(U), _p(XS), _stream()))
+    return U, XS
+
+
+def splitk_res_norm(part: torch.Tensor, x: torch.Tensor, w: torch.Tensor, eps: float, a8: Optional[bool] = None):
+    """x += the split sum of part [S, R, D] (in place, bf16), then rmsnorm of x and, with a8 set (per_token), its W4A8
+    quantization (reference splitk_res_norm, core.metal:539-595): returns out or (out, U, XS)."""
+    S, R, D = part.shape
+    y = torch.empty((R, D), dtype=torch.bfloat16, device=x.device)
+    U = XS = None
+    if a8 is not None:
+        U = torch.empty((R, D), dtype=torch.int8, device=x.device)
+        XS = torch.empty((R, D // 64, 2), dtype=torch.float32, device=x.device)
+    check(lib().ifd_splitk_res_norm(_p(part), S, _p(x), x.stride(0), _p(w), _p(y), D, R, D, float(eps),
+                                    1 if a8 else 0, _p(U) if U is not None else None,
+                                    _p(XS) if XS is not None else None, _stream()))
+    return y if a8 is None else (y, U, XS)
+
+
 def a8_quant(A: torch.Tensor, per_token: bool):
     M, K = A.shape
     U = torch.empty((M, K), dtype=torch.int8, device=A.device)

@@ -197,6 +197,40 @@ def rmsnorm(x, w, eps: float) -> np.ndarray:
     return out
 
 
+def rmsnorm_a8(x, w, eps: float, per_token: bool):
+    """rmsnorm_a8 (engine/kernels/core.metal:502-537): rmsnorm, then a8_quant of its bf16 output (the reference states
+    the fused kernel bit-identical to that pair)."""
+    out = rmsnorm(x, w, eps)
+    U, XS = a8_quant(out, per_token)
+    return out, U, XS
+
+
+def silu_mul_a8(gu, per_token: bool):
+    """silu_mul_a8 (core.metal:789-814): a8_quant of the bf16 silu_mul output, which is not kept."""
+    return a8_quant(silu_mul(gu), per_token)
+
+
+def splitk_res(part, x) -> np.ndarray:
+    """The residual split-K reduce of splitk_res_norm (core.metal:564-572; splitk_reduce with add,
+    qmm_splitk.metal:90-107): bf16(sum_z part[z] + x), the fp32 sum taken in split order."""
+    part = _c(part, np.float32)
+    acc = np.zeros(part.shape[1:], np.float32)
+    for z in range(part.shape[0]):
+        acc = (acc + part[z]).astype(np.float32)
+    return f32_to_bf16(acc + bf16_to_f32(x))
+
+
+def splitk_res_norm(part, x, w, eps: float, a8=None):
+    """splitk_res_norm / splitk_res_norm_a8 (core.metal:539-595): the residual reduce, then rmsnorm of the updated rows
+    (and, with a8 = per_token, a8_quant of the output). Returns (x', out) or (x', out, U, XS)."""
+    xn = splitk_res(part, x)
+    out = rmsnorm(xn, w, eps)
+    if a8 is None:
+        return xn, out
+    U, XS = a8_quant(out, a8)
+    return xn, out, U, XS
+
+
 def gemm_bf16(A, W, nthreads: int = 0) -> np.ndarray:
     A = _c(A, np.uint16)
     W = _c(W, np.uint16)

@@ -182,6 +182,65 @@ def test_silu_mul_and_flip():
     assert W.flipped and np.array_equal(g.host(W.wq).view(np.uint32), wq ^ np.uint32(0x88888888))
 
 
+@pytest.mark.parametrize("per_token", [False, True])
+@pytest.mark.parametrize("R,D", [(1, 2048), (16, 5120), (37, 320)])
+def test_rmsnorm_a8(R, D, per_token):
+    """The fused rmsnorm_a8 gives the bits of ifd_rmsnorm then ifd_a8_quant; its quantization is the oracle's a8_quant
+    of the normalised rows, bit for bit, and the rows are the oracle's rmsnorm within one bf16 step."""
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(90 + R)
+    x = gen.f32_to_bf16((rng.standard_normal((R, D)) * rng.uniform(0.1, 10, (R, 1))).astype(np.float32))
+    x[0, : D // 2] = 0  # a zero half: groups with amax 0 (sx = 1)
+    w = gen.f32_to_bf16(rng.uniform(0.5, 2.0, D).astype(np.float32))
+    xd, wd = g.dev(x), g.dev(w)
+    y, U, XS = ops.rmsnorm_a8(xd, wd, 1e-6, per_token)
+    y0 = ops.rmsnorm(xd, wd, 1e-6)
+    U0, XS0 = ops.a8_quant(y0, per_token)
+    y, U, XS, y0 = g.host(y), g.host(U), g.host(XS), g.host(y0)
+    assert np.array_equal(y, y0) and np.array_equal(U, g.host(U0)) and np.array_equal(XS, g.host(XS0))
+    Ur, XSr = orc.a8_quant(y, per_token)
+    assert np.array_equal(U, Ur) and np.array_equal(XS, XSr)
+    assert gen.bf16_err(y, orc.rmsnorm(x, w, 1e-6), ref_is_bf16=True) == 0.0
+
+
+@pytest.mark.parametrize("per_token", [False, True])
+def test_silu_mul_a8(per_token):
+    """silu_mul_a8 gives the bits of ifd_silu_mul then ifd_a8_quant, and the oracle's a8_quant of that product."""
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(95)
+    gu = gen.f32_to_bf16((rng.standard_normal((9, 2 * 17408)) * 3).astype(np.float32))
+    gu[2, 17408:] = 0  # up = 0: a zero row
+    gd = g.dev(gu)
+    U, XS = ops.silu_mul_a8(gd, per_token)
+    h = ops.silu_mul(gd)
+    U0, XS0 = ops.a8_quant(h, per_token)
+    assert np.array_equal(g.host(U), g.host(U0)) and np.array_equal(g.host(XS), g.host(XS0))
+    Ur, XSr = orc.a8_quant(g.host(h), per_token)
+    assert np.array_equal(g.host(U), Ur) and np.array_equal(g.host(XS), XSr)
+
+
+@pytest.mark.parametrize("a8", [None, False, True])
+@pytest.mark.parametrize("S,R,D", [(1, 3, 256), (12, 32, 5120), (4, 128, 2048)])
+def test_splitk_res_norm(S, R, D, a8):
+    """splitk_res_norm: the updated residual rows are the oracle's split-order fp32 sum plus x, bit for bit; the
+    normalised rows are ifd_rmsnorm of them and the quantization ifd_a8_quant of those, bit for bit."""
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(100 + S + R)
+    part = (rng.standard_normal((S, R, D)) * 0.3).astype(np.float32)
+    x = gen.f32_to_bf16(rng.standard_normal((R, D)).astype(np.float32))
+    w = gen.f32_to_bf16(rng.uniform(0.5, 2.0, D).astype(np.float32))
+    xd, wd = g.dev(x), g.dev(w)
+    res = ops.splitk_res_norm(torch.from_numpy(part).cuda(), xd, wd, 1e-6, a8)
+    y = res if a8 is None else res[0]
+    xn = g.host(xd)
+    assert np.array_equal(xn, orc.splitk_res(part, x))
+    y0 = ops.rmsnorm(g.dev(xn), wd, 1e-6)
+    assert np.array_equal(g.host(y), g.host(y0))
+    if a8 is not None:
+        U0, XS0 = ops.a8_quant(y0, a8)
+        assert np.array_equal(g.host(res[1]), g.host(U0)) and np.array_equal(g.host(res[2]), g.host(XS0))
+
+
 @pytest.mark.parametrize("R,D,eps", [(1, 2048, 1e-6), (16, 5120, 1e-6), (37, 333, 0.0), (5, 64, 7.0)])
 def test_rmsnorm(R, D, eps):
     g, ops = _gu(), _ops()

@@ -225,6 +225,56 @@ def test_rmsnorm_scale_invariance():
     assert np.array_equal(orc.rmsnorm(x, w, 0.0), orc.rmsnorm(xs, w, 0.0))
 
 
+def test_rmsnorm_a8_exact_rows():
+    """rmsnorm_a8 composes rmsnorm and a8_quant on the bf16 output: a constant 2^k row with w = 1 normalises to 1.0
+    exactly (eps = 1e-6 vanishes in the fp32 mean 64), so every group has amax 1, sx = 1/127, q = 127 and
+    XS = (1/127, 64 * 127 * sx) in fp32; a row of zeros quantizes with sx = 1 and q = 0."""
+    D = 128
+    x = np.zeros((2, D), np.float32)
+    x[0, :] = 8.0
+    w = gen.f32_to_bf16(np.ones(D, np.float32))
+    for per_token in (False, True):
+        out, U, XS = orc.rmsnorm_a8(gen.f32_to_bf16(x), w, 1e-6, per_token)
+        assert np.all(gen.bf16_to_f32(out[0]) == 1.0) and np.all(out[1] == 0)
+        sx = np.float32(1.0) / np.float32(127.0)
+        assert np.all(U[0] == 127) and np.all(U[1] == 0)
+        assert np.all(XS[0, :, 0] == sx) and np.all(XS[0, :, 1] == sx * np.float32(64 * 127))
+        assert np.all(XS[1, :, 0] == 1.0) and np.all(XS[1, :, 1] == 0.0)
+        Ur, XSr = orc.a8_quant(out, per_token)
+        assert np.array_equal(U, Ur) and np.array_equal(XS, XSr)
+
+
+def test_silu_mul_a8_composes():
+    """silu_mul_a8 is a8_quant of the bf16 silu_mul output: u = 0 rows quantize to zeros with sx = 1, and random rows
+    match the explicit composition."""
+    rng = np.random.default_rng(5)
+    gu = gen.f32_to_bf16((rng.standard_normal((4, 256)) * 2).astype(np.float32))
+    gu[1, 128:] = 0  # up = 0: h = 0
+    for per_token in (False, True):
+        U, XS = orc.silu_mul_a8(gu, per_token)
+        assert np.all(U[1] == 0) and np.all(XS[1, :, 0] == 1.0)
+        Ur, XSr = orc.a8_quant(orc.silu_mul(gu), per_token)
+        assert np.array_equal(U, Ur) and np.array_equal(XS, XSr)
+
+
+def test_splitk_res_exact_sums():
+    """The residual split-K reduce of splitk_res_norm: on dyadic values whose fp32 sums are exact the result is
+    bf16(sum + x) of the float64 sum (a dropped split, a wrong residual or a missing rounding fails); on random values
+    the fp32 sum runs in split order (((p0 + p1) + p2) + x), not in another association."""
+    rng = np.random.default_rng(6)
+    S, R, D = 3, 2, 64
+    part = (rng.integers(-64, 64, (S, R, D)) / 8.0).astype(np.float32)
+    x = gen.f32_to_bf16((rng.integers(-32, 32, (R, D)) / 4.0).astype(np.float32))
+    want = gen.f32_to_bf16((part.astype(np.float64).sum(0) + gen.bf16_to_f32(x)).astype(np.float32))
+    assert np.array_equal(orc.splitk_res(part, x), want)
+    # split order: 1 + 2^-24 + 2^-24 - 1 is 0 in order ((1 + e) + e) - 1 but 2^-23 when the e's are added first
+    e = np.float32(2.0 ** -24)
+    p = np.array([[[1.0]], [[e]], [[e]], [[-1.0]]], np.float32)
+    assert gen.bf16_to_f32(orc.splitk_res(p, gen.f32_to_bf16(np.zeros((1, 1), np.float32))))[0, 0] == 0.0
+    xn, out = orc.splitk_res_norm(part, x, gen.f32_to_bf16(np.ones(D, np.float32)), 1e-6)
+    assert np.array_equal(xn, want) and np.array_equal(out, orc.rmsnorm(want, gen.f32_to_bf16(np.ones(D, np.float32)), 1e-6))
+
+
 # ---- MoE ------------------------------------------------------------------------------------------------------------
 def _brute_topk(l: np.ndarray, k: int):
     order = np.lexsort((np.arange(l.size), -l.astype(np.float64)))  # logit desc, then index asc
