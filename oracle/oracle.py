@@ -319,3 +319,43 @@ def moe_experts(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: boo
                           _c(edn[0], np.uint32), _c(edn[1], np.uint16), _c(edn[2], np.uint16),
                           *sh, 1 if shared_qmv else 0, o, 1 if assign else 0, nthreads)
     return o
+
+
+# ---- checkpoint formats (host-side restatement of the loader's arithmetic) ----------------------------------------
+def expand_groups(sb, gs: int) -> np.ndarray:
+    """A group of gs values becomes gs / 64 groups of 64 with its scale (or bias) repeated (load_moe, moe.h:69-83):
+    [..., K / gs] -> [..., K / 64]."""
+    if gs % 64:
+        raise ValueError("group size must be a multiple of 64")
+    return np.repeat(_c(sb, np.uint16), gs // 64, axis=-1)
+
+
+def pack_affine(codes, bits: int) -> np.ndarray:
+    """Codes [N, K] -> uint32 words [N, K bits / 32], element j of a word at bits bits * j, low first
+    (weights.h:349-350)."""
+    codes = np.asarray(codes, np.uint32)
+    N, K = codes.shape
+    per = 32 // bits
+    c = codes.reshape(N, K // per, per)
+    return np.bitwise_or.reduce(c << (bits * np.arange(per, dtype=np.uint32)), axis=-1).astype(np.uint32)
+
+
+def quantize_affine(w_bf16, bits: int):
+    """Load-time affine quantization, group 64 (load_qlinear_bf16_q8, weights.h:349-406): per group lo / hi the
+    min / max, sc = (hi - lo) / (2^bits - 1) in fp32 (1e-8 when 0), sc and lo rounded to bf16 (nearest even), then
+    q = clamp(round_half_away((w - lo_bf16) / sc_bf16), 0, 2^bits - 1) in fp32. Returns (wq, s, b, codes)."""
+    w = bf16_to_f32(w_bf16)
+    N, K = w.shape
+    levels = np.float32((1 << bits) - 1)
+    g = w.reshape(N, K // 64, 64)
+    lo = g.min(axis=-1)
+    hi = g.max(axis=-1)
+    sc = ((hi - lo) / levels).astype(np.float32)
+    sc[sc == 0] = np.float32(1e-8)
+    sb = f32_to_bf16(sc)
+    bb = f32_to_bf16(lo)
+    v = ((g - bf16_to_f32(bb)[..., None]) / bf16_to_f32(sb)[..., None]).astype(np.float32)
+    v64 = v.astype(np.float64)
+    r = np.trunc(v64 + np.copysign(0.5, v64))  # std::round: half away from zero (exact in float64)
+    codes = np.clip(r, 0, float(levels)).astype(np.uint32).reshape(N, K)
+    return pack_affine(codes, bits), sb, bb, codes

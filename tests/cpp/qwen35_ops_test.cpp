@@ -4,6 +4,8 @@
 //
 //   qwen35_ops_test             every GPU case; exit 0 when all pass
 //   qwen35_ops_test --bad-bits  gemm() on an 8-bit QLinear: must print its error and exit(1) (no GPU needed)
+//   qwen35_ops_test --ckpt DIR  the device loaders (ckpt_dev.h) on a checkpoint written by tests/test_shim.py:
+//                               uploads bit-identical to the host loader, and gemm() on the loaded layer
 //
 // Tolerances are BASELINE's: max |err| <= 1e-2 RMS(ref) after the output's own bf16 rounding; routing indices
 // bit-exact.
@@ -13,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "ckpt_dev.h"
 #include "qwen35_ops.h"
 
 extern "C" {
@@ -310,6 +313,51 @@ void test_encode_moe(std::mt19937& rng) {
   (void)hipFree(sgu_t64);
 }
 
+template <class T>
+bool same_as_device(const std::vector<T>& host, const BufRef& d) {
+  return host.empty() || download<T>(d, host.size()) == host;
+}
+
+// The device loaders against the host loader (bit-exact uploads) and gemm() on what they loaded. The checkpoint holds
+// mlp.gate_proj / mlp.up_proj (4-bit, fused N = 2 x 256, K = 1024, group 128 from config.json), a bf16 x.weight
+// [128, 512] and a switch_mlp gate stack [4, 64, 256].
+void test_load(const std::string& dir, std::mt19937& rng) {
+  Checkpoint ck(dir);
+  Gpu g;
+  const std::vector<std::string> gu = {"mlp.gate_proj", "mlp.up_proj"};
+  const HostQLinear hq = load_qlinear(ck, gu);
+  const QLinear W = load_qlinear(g, ck, gu);
+  report(W.N == hq.N && W.K == hq.K && W.bits == 4 && same_as_device(hq.wq, W.wq) && same_as_device(hq.s, W.s) &&
+             same_as_device(hq.b, W.b) && (bool)W.t64,
+         "load_qlinear upload (fused, group 128 expanded, T64 packed)", 0);
+  const HostLinear h{hq.N, hq.K, hq.wq, hq.s, hq.b};
+  Config c;
+  Qwen35 m(c, 0, 0, 64 << 20);
+  Enc e{g.stream};
+  for (int M : {1, 128}) {
+    const auto A = activations(M, h.K, rng);
+    BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * h.N));
+    m.gemm(e, dA, W, dC, M, 0);
+    const double err = bf16_err(download<uint16_t>(dC, (size_t)M * h.N), ref_gemm(A, h, M, M <= 64), false);
+    report(err <= 1e-2, "gemm on the loaded layer M=" + std::to_string(M), err);
+    (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+  }
+  const HostQLinear h8 = load_qlinear_bf16(ck, {"x.weight"}, 8);
+  const QLinear W8 = load_qlinear_bf16_q8(g, ck, {"x.weight"}, 8);
+  report(W8.bits == 8 && !W8.t64 && same_as_device(h8.wq, W8.wq) && same_as_device(h8.s, W8.s) &&
+             same_as_device(h8.b, W8.b),
+         "load_qlinear_bf16_q8 upload (8-bit, no T64 copy)", 0);
+  const HostQLinear h16 = load_qlinear(ck, {"x"});
+  const QLinear W16 = load_qlinear(g, ck, {"x"});
+  report(W16.bits == 16 && same_as_device(h16.w16, W16.wq), "load_qlinear bf16 passthrough upload", 0);
+  const HostMoeW hm = load_moe(ck, {"mlp.switch_mlp.gate_proj"});
+  const MoeW mw = load_moe(g, ck, {"mlp.switch_mlp.gate_proj"});
+  report(mw.E == hm.E && mw.N == hm.N && mw.K == hm.K && same_as_device(hm.wq, mw.wq) && same_as_device(hm.s, mw.s) &&
+             same_as_device(hm.b, mw.b),
+         "load_moe upload", 0);
+  g.release();
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -324,6 +372,11 @@ int main(int argc, char** argv) {
     return 0;
   }
   std::mt19937 rng(20251201);
+  if (argc > 2 && std::string(argv[1]) == "--ckpt") {
+    test_load(argv[2], rng);
+    printf(failures ? "%d FAILED\n" : "ALL OK\n", failures);
+    return failures ? 1 : 0;
+  }
   {
     Config c;
     Qwen35 m(c, 0, 0, 64 << 20);

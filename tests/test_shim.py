@@ -1,5 +1,6 @@
 """The C++ operator shim (inferd_amd/csrc/qwen35_ops.h: Qwen35::gemm / Qwen35::encode_moe with the reference's
-signatures, engine/src/qwen35.h:1465, 1869) through its C++ test program, tests/cpp/qwen35_ops_test.cpp.
+signatures, engine/src/qwen35.h:1465, 1869) and the device loaders (ckpt_dev.h) through their C++ test program,
+tests/cpp/qwen35_ops_test.cpp.
 
 The program is built by tests/cpp/build.py (``__graft_entry__.build()`` runs it)."""
 import os
@@ -29,5 +30,28 @@ def test_shim_gemm_and_encode_moe_parity():
     (rmsnorm, bit-exact routing, x += MoE output) against the CPU oracle."""
     assert os.path.exists(BIN), "tests/cpp/qwen35_ops_test is not built"
     r = subprocess.run([BIN], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    assert r.returncode == 0 and "ALL OK" in r.stdout, r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+def test_device_loaders_upload_and_gemm(tmp_path):
+    """The device loaders (inferd_amd/csrc/ckpt_dev.h: load_qlinear / load_qlinear_bf16_q8 / load_moe with the
+    reference's signatures, weights.h:271-406, moe.h:14-87) upload exactly what the host loader reads, pack the T64
+    copy, and gemm() on the loaded layer matches the oracle."""
+    import json
+    import numpy as np
+    from oracle import oracle as orc
+    from tests.test_ckpt import _put, _qpart, _save
+    assert os.path.exists(BIN), "tests/cpp/qwen35_ops_test is not built"
+    rng = np.random.default_rng(11)
+    d = {}
+    _put(d, "mlp.gate_proj", _qpart(rng, 256, 1024, gs=128))
+    _put(d, "mlp.up_proj", _qpart(rng, 256, 1024, gs=128))
+    _put(d, "mlp.switch_mlp.gate_proj", _qpart(rng, 64, 256, gs=128, lead=(4,)))
+    d["x.weight"] = ("bf16", orc.f32_to_bf16(rng.standard_normal((128, 512)).astype(np.float32)))
+    _save(tmp_path / "model.safetensors", d)
+    (tmp_path / "config.json").write_text(json.dumps({"quantization": {"bits": 4, "group_size": 128}}))
+    r = subprocess.run([BIN, "--ckpt", str(tmp_path)], capture_output=True, text=True, timeout=300)
     print(r.stdout)
     assert r.returncode == 0 and "ALL OK" in r.stdout, r.stdout + r.stderr
