@@ -38,7 +38,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--no-breakdown", action="store_true", help="headline workload only")
     p.add_argument("--only", default="",
-                   help="profiling: run one config only (c0, c1, c2, c3, c4), or 'copy' (256 MiB device copy that "
+                   help="profiling: run one config only (c0, c1, c2, c3, c4, w8), or 'copy' (256 MiB device copy that "
                         "calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
 
@@ -204,6 +204,48 @@ def main():
                                               frac_int8=op / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
                                               a8_quant_us=ms_q * 1e3)
             del W3
+        # ---- 8-bit weights (config 0's shape and config 3's W8A8 shape) -----------------------------------------
+        if args.only in ("", "w8"):
+            def qlin8(N, K):
+                wq = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 4), dtype=torch.int32, device=dev, generator=gen)
+                s = ((torch.rand((N, K // 64), device=dev, generator=gen) * 0.015 + 0.005) / 16).to(torch.bfloat16)
+                b = (-128.0 * s.float()).to(torch.bfloat16)
+                return QLinear(wq, s, b, N, K, bits=8)
+
+            nb8 = int(5120 * 5120 * (1 + 4 / 64))
+            ncp = copies_for(nb8)
+            W8 = [qlin8(5120, 5120) for _ in range(ncp)]
+            w8 = {}
+            for M in (1, 8, 32):
+                A8 = act(M, 5120)
+                C8 = torch.empty((M, 5120), dtype=torch.bfloat16, device=dev)
+                ms = timed(lambda i: ops.gemm(A8, W8[i % ncp], C8), 200, 20)
+                byts = nb8 + M * 5120 * 2 * 2
+                w8[f"M{M}"] = dict(us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9,
+                                   frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+            A8 = act(2048, 5120)
+            U8, XS8 = ops.a8_quant(A8, True)
+            C8 = torch.empty((2048, 5120), dtype=torch.bfloat16, device=dev)
+            ms = timed(lambda i: ops.qmm_w4a8(U8, XS8, True, W8[i % 4], C8), 20, 3)
+            op = 2.0 * 2048 * 5120 * 5120
+            w8["w8a8_M2048"] = dict(us=ms * 1e3, tops=op / (ms * 1e-3) / 1e12,
+                                    frac_int8=op / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS)
+            breakdown["w8_5120x5120"] = dict(w8, copies=ncp)
+            del W8
+            # the decode MLP's gate_up shape (N = 34816, K = 5120): long enough to stream at bandwidth
+            nbg = int(34816 * 5120 * (1 + 4 / 64))
+            ncg = copies_for(nbg)
+            Wg = [qlin8(34816, 5120) for _ in range(ncg)]
+            wg = {}
+            for M in (1, 8, 32, 128):
+                Ag = act(M, 5120)
+                Cg = torch.empty((M, 34816), dtype=torch.bfloat16, device=dev)
+                ms = timed(lambda i: ops.gemm(Ag, Wg[i % ncg], Cg), 40, 5)
+                byts = nbg + M * (5120 + 34816) * 2
+                wg[f"M{M}"] = dict(us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9,
+                                   frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+            breakdown["w8_34816x5120"] = dict(wg, copies=ncg)
+            del Wg
         # ---- config 4: MoE FFN H=2048, E=512, top-10, I=512, + shared expert ----------------------------------
         if args.only in ("", "c4"):
             E, H, I, k = 512, 2048, 512, 10

@@ -69,7 +69,8 @@ int ifd_gemm_w4(const void* A, int lda, const uint32_t* wq, const uint16_t* s, c
                 int ldk, uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes,
                 void* stream);
 
-/* In-place nibble flip, wq[i] ^= mask for i < n32 (reference w_flip, w4a8.metal:19-22; flip, qwen35.h:1306-1322). */
+/* In-place flip, wq[i] ^= mask for i < n32 (reference w_flip, w4a8.metal:19-22; flip, qwen35.h:1306-1322): mask
+ * 0x88888888 for 4-bit weights, 0x80808080 for 8-bit. */
 int ifd_flip_w4(uint32_t* wq, size_t n32, uint32_t mask, void* stream);
 
 /* SwiGLU h[r][i] = bf16(float(bf16(g * sigmoid(g))) * u) over rows gu = [gate (I) | up (I)]
@@ -100,6 +101,24 @@ int ifd_silu_mul_a8(const void* gu, int I, int rows, int per_token, int8_t* U, f
  * issued by rmsnorm_for (qwen35.h:1982-1998). With U, D % 64 == 0. */
 int ifd_splitk_res_norm(const float* part, int S, void* x, int ldx, const void* w, void* out, int out_stride, int rows,
                         int D, float eps, int per_token, int8_t* U, float* XS, void* stream);
+
+/* ---- 8-bit weights (reference qmv8, core.metal:175-248; w4a8_gemm with BITS = 8, w4a8.metal:43-98, 104-109; the
+ * 8-bit routes of Qwen35::gemm, qwen35.h:1520-1558) --------------------------------------------------------------
+ * MLX affine 8-bit, group 64: wq uint32 [N][ldk/4] with element j of a little-endian word in byte j; s, b as for
+ * 4 bits; w = s q + b, q in 0..255. xr = 0x80808080 when the bytes were flipped in place (ifd_flip_w4 with that
+ * mask: q ^ 0x80), else 0. Same arguments, workspace and store modes as the 4-bit entry points. */
+size_t ifd_gemm_w8_workspace(int M, int N, int K);
+/* Routed GEMM: the qmv8 arithmetic (s sum q x + b sum x per group, fp32) for M <= 32, bf16(s q + b) dequant with
+ * fp32 accumulation (MLX's 8-bit qmm) above. */
+int ifd_gemm_w8(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+                int ldk, uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes,
+                void* stream);
+/* W8A8: C (mode) = sum_g [ s sx P + (b + 128 s) (sx sum xq) ], P = sum (q - 128) xq over the group (exact int32);
+ * U, XS from ifd_a8_quant with the same per_token. */
+int ifd_qmm_w8a8(const int8_t* U, const float* XS, int per_token, const uint32_t* wq, const uint16_t* s,
+                 const uint16_t* b, int N, int K, int ldk, uint32_t xr, void* C, int ldc, int M, int mode,
+                 void* workspace, size_t ws_bytes, void* stream);
+size_t ifd_qmm_w8a8_workspace(int M, int N, int K);
 
 /* ---- T64: the MI355X weight layout (no counterpart in the reference; its role is that of the reference's
  * load-time weight transforms, flip and the lane4/qmst copies, qwen35.h:1209-1322) -------------------------------

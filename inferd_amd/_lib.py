@@ -36,6 +36,10 @@ SIGNATURES = {
     "ifd_splitk_res_norm": (_i, [_vp, _i, _vp, _i, _vp, _vp, _i, _i, _i, ctypes.c_float, _i, _vp, _vp, _vp]),
     "ifd_qmm_w4a8": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _u32, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_qmm_w4a8_workspace": (_sz, [_i, _i, _i]),
+    "ifd_gemm_w8_workspace": (_sz, [_i, _i, _i]),
+    "ifd_gemm_w8": (_i, _GEMM_ARGS),
+    "ifd_qmm_w8a8": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _u32, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "ifd_qmm_w8a8_workspace": (_sz, [_i, _i, _i]),
     "ifd_t64_bytes": (_sz, [_i, _i, _i]),
     "ifd_pack_t64": (_i, [_vp, _vp, _vp, _i, _i, _i, _u32, _i, _vp, _vp]),
     "ifd_gemm_t64_workspace": (_sz, [_i, _i, _i]),

@@ -12,8 +12,9 @@ namespace {
 inline hipStream_t S(void* st) { return (hipStream_t)st; }
 
 int fill_gemm(W4Gemm& g, const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N,
-              int K, int ldk, uint32_t xr, void* C, int ldc, int M, int mode) {
-  IFD_TRY(check_w4_args(A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode, 2));
+              int K, int ldk, uint32_t xr, void* C, int ldc, int M, int mode, int bits = 4) {
+  IFD_TRY(check_w4_args(A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode, 2, bits));
+  g.bits = bits;
   g.A = A;
   g.lda = lda;
   g.wq = wq;
@@ -160,6 +161,31 @@ int ifd_qmm_w4a8(const int8_t* U, const float* XS, int per_token, const uint32_t
                  void* workspace, size_t ws_bytes, void* stream) {
   W4Gemm g;
   IFD_TRY(fill_gemm(g, U, K, wq, s, b, N, K, ldk, xr, C, ldc, M, mode));
+  IFD_CHECK(M == 0 || XS, "null XS");
+  g.XS = XS;
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_w4a8(g, per_token ? 1 : 0, w.body, w.bytes, S(stream));
+}
+
+// ---- 8-bit weights -----------------------------------------------------------------------------------------------
+size_t ifd_gemm_w8_workspace(int M, int N, int K) { return ifd_gemm_w4_workspace(M, N, K); }
+
+int ifd_gemm_w8(const void* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk,
+                uint32_t xr, void* C, int ldc, int M, int mode, void* workspace, size_t ws_bytes, void* stream) {
+  W4Gemm g;
+  IFD_TRY(fill_gemm(g, A, lda, wq, s, b, N, K, ldk, xr, C, ldc, M, mode, 8));
+  const WsView w = ws_view(workspace, ws_bytes);
+  if (M <= kQmvMaxRows) return launch_qmv(g, w.body, w.bytes, S(stream));
+  return launch_qmm(g, w.body, w.bytes, S(stream));
+}
+
+size_t ifd_qmm_w8a8_workspace(int M, int N, int K) { return with_header(w4a8_workspace(M, N, K)); }
+
+int ifd_qmm_w8a8(const int8_t* U, const float* XS, int per_token, const uint32_t* wq, const uint16_t* s,
+                 const uint16_t* b, int N, int K, int ldk, uint32_t xr, void* C, int ldc, int M, int mode,
+                 void* workspace, size_t ws_bytes, void* stream) {
+  W4Gemm g;
+  IFD_TRY(fill_gemm(g, U, K, wq, s, b, N, K, ldk, xr, C, ldc, M, mode, 8));
   IFD_CHECK(M == 0 || XS, "null XS");
   g.XS = XS;
   const WsView w = ws_view(workspace, ws_bytes);

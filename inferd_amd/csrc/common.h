@@ -95,6 +95,69 @@ __device__ __forceinline__ u32x4 dequant8_bf16(uint32_t w, float s, float b) {
   return r;
 }
 
+// ---- 8-bit codes (MLX affine 8-bit: byte i of a row is element i) ----
+// Eight 8-bit codes of two words (k order 0..7) as eight bf16 values q (exact: every integer 0..255 is a bf16):
+// v_cvt_f32_ubyte per code, then the high halves of two floats packed by one v_perm_b32.
+__device__ __forceinline__ u32x4 codes8_bf16(uint32_t w0, uint32_t w1) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const uint32_t w = i ? w1 : w0;
+    const uint32_t f0 = __float_as_uint((float)(w & 0xFFu)), f1 = __float_as_uint((float)((w >> 8) & 0xFFu));
+    const uint32_t f2 = __float_as_uint((float)((w >> 16) & 0xFFu)), f3 = __float_as_uint((float)(w >> 24));
+    r[2 * i] = __builtin_amdgcn_perm(f1, f0, 0x07060302u);
+    r[2 * i + 1] = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
+  }
+  return r;
+}
+// Eight 8-bit codes of two words dequantized to bf16(s * q + b) in natural k order.
+__device__ __forceinline__ u32x4 dequant8x8_bf16(uint32_t w0, uint32_t w1, float s, float b) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const uint32_t w = i ? w1 : w0;
+    const float q0 = (float)(w & 0xFFu), q1 = (float)((w >> 8) & 0xFFu);
+    const float q2 = (float)((w >> 16) & 0xFFu), q3 = (float)(w >> 24);
+    r[2 * i] = pack_bf2(__builtin_fmaf(s, q0, b), __builtin_fmaf(s, q1, b));
+    r[2 * i + 1] = pack_bf2(__builtin_fmaf(s, q2, b), __builtin_fmaf(s, q3, b));
+  }
+  return r;
+}
+
+// The codes one lane holds for one 64-group in the MLX layout: 32 codes = BITS words, loaded as one (4 bits) or two
+// (8 bits) 16 B pieces at word offsets 4 h (+ 8) of the group, so that each load instruction of a wave covers 32
+// contiguous bytes of every row. Step t of the four 32x32x16 MFMA steps takes the eight codes at k = kofs(t, h) + 0..7:
+// 32 h + 8 t for 4 bits (one 16 B piece = 32 codes), 32 (t / 2) + 16 h + 8 (t % 2) for 8 bits (a piece = 16 codes).
+// The activation fragment of a step is read at the same k.
+template <int BITS>
+struct GroupCodes {
+  u32x4 w[BITS / 4];
+  static __device__ __forceinline__ int kofs(int t, int h) {
+    return BITS == 4 ? 32 * h + 8 * t : 32 * (t >> 1) + 16 * h + 8 * (t & 1);
+  }
+  // the row's words for group g from `row` (already offset to this lane's first piece: 4 h words)
+  __device__ __forceinline__ void load(const uint32_t* row, int g) {
+#pragma unroll
+    for (int i = 0; i < BITS / 4; i++) w[i] = *(const u32x4*)(row + (size_t)g * 2 * BITS + 8 * i);
+  }
+  __device__ __forceinline__ uint32_t word(int i) const { return w[i / 4][i % 4]; }
+  // step t as bf16 MFMA operand, offset so that it is exact: 128 + q (4 bits) or q (8 bits)
+  __device__ __forceinline__ u32x4 step_affine(int t, uint32_t xr) const {
+    if (BITS == 4) return codes_bf16_off128(word(t) ^ xr);
+    return codes8_bf16(word(2 * t) ^ xr, word(2 * t + 1) ^ xr);
+  }
+  // step t dequantized to bf16(s q + b)
+  __device__ __forceinline__ u32x4 step_dequant(int t, uint32_t xr, float s, float b) const {
+    if (BITS == 4) return dequant8_bf16(word(t) ^ xr, s, b);
+    return dequant8x8_bf16(word(2 * t) ^ xr, word(2 * t + 1) ^ xr, s, b);
+  }
+};
+// the bias correction of step_affine's offset: b - 128 s (4 bits) or b (8 bits)
+template <int BITS>
+__device__ __forceinline__ float affine_bias(float s, float b) {
+  return BITS == 4 ? __builtin_fmaf(-128.f, s, b) : b;
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll

@@ -39,13 +39,14 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
     if (_rc != IFD_OK) return _rc;   \
   } while (0)
 
-// Validates the common arguments of a dense 4-bit GEMM.
+// Validates the common arguments of a dense 4- or 8-bit GEMM (the flip mask xr: 0x88888888 or 0x80808080).
 inline int check_w4_args(const void* A, int lda, const void* wq, const void* s, const void* b, int N, int K, int ldk,
-                         uint32_t xr, const void* C, int ldc, int M, int mode, int a_elem_bytes) {
+                         uint32_t xr, const void* C, int ldc, int M, int mode, int a_elem_bytes, int bits = 4) {
   IFD_CHECK(M >= 0 && N > 0 && K > 0, "bad shape M=%d N=%d K=%d", M, N, K);
   IFD_CHECK(K % 64 == 0, "K=%d is not a multiple of the group size 64", K);
   IFD_CHECK(ldk == 0 || (ldk >= K && ldk % 64 == 0), "ldk=%d must be 0 or a multiple of 64 >= K", ldk);
-  IFD_CHECK(xr == 0u || xr == 0x88888888u, "xr=0x%x must be 0 or 0x88888888", xr);
+  const uint32_t flip = bits == 8 ? 0x80808080u : 0x88888888u;
+  IFD_CHECK(xr == 0u || xr == flip, "xr=0x%x must be 0 or 0x%x", xr, flip);
   IFD_CHECK(mode >= 0 && mode <= 2, "mode=%d must be 0, 1 or 2", mode);
   IFD_CHECK(lda >= K && lda % 8 == 0, "lda=%d must be >= K and a multiple of 8", lda);
   IFD_CHECK(ldc >= N, "ldc=%d must be >= N=%d", ldc, N);

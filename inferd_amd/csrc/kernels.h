@@ -6,7 +6,7 @@
 
 namespace ifd {
 
-// One dense 4-bit GEMM request: C (mode) = A . W^T. A is bf16 [M][lda] (or int8 [M][K] + XS for W4A8).
+// One dense 4- or 8-bit GEMM request: C (mode) = A . W^T. A is bf16 [M][lda] (or int8 [M][K] + XS for W4A8 / W8A8).
 struct W4Gemm {
   const void* A = nullptr;
   int lda = 0;
@@ -18,6 +18,7 @@ struct W4Gemm {
   uint32_t xr = 0;
   void* C = nullptr;
   int ldc = 0, M = 0, mode = 0;
+  int bits = 4;  // 4 or 8 (MLX affine, group 64)
 };
 
 // Decode GEMV path (M <= 128).

@@ -1,4 +1,4 @@
-// Prefill path: 4-bit weights x bf16 activations on bf16 MFMA, for any M (used above 128 rows).
+// Prefill path: 4- or 8-bit weights x bf16 activations on bf16 MFMA, for any M (used above 128 rows).
 //
 // Replaces MLX's affine_qmm_t_nax (third_party/mlx/.../quantized_nax.h:938-1076, 1206-1267; instances
 // engine/kernels/mlx_qmm.metal:9-14; host mlx_qmm, engine/src/qwen35.h:1427-1462), with the same numerics: every
@@ -32,6 +32,7 @@ struct QmmArgs {
   int tiles_m, tiles_n;
 };
 
+template <int BITS>
 __global__ __launch_bounds__(256) void k_qmm(QmmArgs p) {
   extern __shared__ __align__(16) uint16_t smem[];
   uint16_t* As = smem;                         // [2][256][72]
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(256) void k_qmm(QmmArgs p) {
   const int tm = band * kQmmBand + within % bm, tn = within / bm;
   const int m0 = tm * kQmmBM, n0 = tn * kQmmBN;
 
-  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+  const int G = p.K / kGroup, ldw = p.ldk * BITS / 32, ldg = p.ldk / kGroup;
   // activation loads: 8 chunks of 16 B per thread, chunk c = tid + 256 i -> row c / 8, column 8 (c % 8)
   const uint16_t* aptr[8];
   bool aok[8];
@@ -59,7 +60,7 @@ __global__ __launch_bounds__(256) void k_qmm(QmmArgs p) {
     aok[i] = m < p.M;
     aptr[i] = p.A + (size_t)(aok[i] ? m : 0) * p.lda + 8 * (c & 7);
   }
-  // weight loads: row tid / 2, half tid % 2 (16 codes... 32 codes = 4 words)
+  // weight loads: row tid / 2, half tid % 2 (32 codes = BITS words)
   const int wr = tid >> 1, wh = tid & 1;
   const int nw = min(n0 + wr, p.N - 1);
   const uint32_t* wptr = p.wq + (size_t)nw * ldw + 4 * wh;
@@ -67,12 +68,12 @@ __global__ __launch_bounds__(256) void k_qmm(QmmArgs p) {
   const uint16_t* bptr = p.b + (size_t)nw * ldg;
 
   u32x4 areg[8];
-  u32x4 wreg;
+  GroupCodes<BITS> wreg;
   uint32_t sbreg;
   auto gload = [&](int g) {
 #pragma unroll
     for (int i = 0; i < 8; i++) areg[i] = aok[i] ? *(const u32x4*)(aptr[i] + (size_t)g * 64) : u32x4{0u, 0u, 0u, 0u};
-    wreg = *(const u32x4*)(wptr + (size_t)g * 8);
+    wreg.load(wptr, g);
     sbreg = (uint32_t)sptr[g] | ((uint32_t)bptr[g] << 16);
   };
   auto lstore = [&](int buf) {
@@ -83,9 +84,10 @@ __global__ __launch_bounds__(256) void k_qmm(QmmArgs p) {
       *(u32x4*)(as + (c >> 3) * kQmmLd + 8 * (c & 7)) = areg[i];
     }
     const float sc = bf2f((uint16_t)(sbreg & 0xFFFFu)), bi = bf2f((uint16_t)(sbreg >> 16));
-    uint16_t* ws = Ws + buf * kQmmBN * kQmmLd + wr * kQmmLd + 32 * wh;
+    uint16_t* ws = Ws + buf * kQmmBN * kQmmLd + wr * kQmmLd;
 #pragma unroll
-    for (int t = 0; t < 4; t++) *(u32x4*)(ws + 8 * t) = dequant8_bf16(wreg[t] ^ p.xr, sc, bi);
+    for (int t = 0; t < 4; t++)
+      *(u32x4*)(ws + GroupCodes<BITS>::kofs(t, wh)) = wreg.step_dequant(t, p.xr, sc, bi);
   };
 
   f32x16 acc[4][2];
@@ -141,10 +143,12 @@ int launch_qmm(const W4Gemm& g, void*, size_t, hipStream_t st) {
   const size_t lds = (size_t)2 * (kQmmBM + kQmmBN) * kQmmLd * sizeof(uint16_t);
   static bool attr = false;
   if (!attr) {
-    hipFuncSetAttribute((const void*)k_qmm, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)k_qmm<4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)k_qmm<8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr = true;
   }
-  hipLaunchKernelGGL(k_qmm, dim3(p.tiles_m * p.tiles_n), dim3(256), lds, st, p);
+  if (g.bits == 8) hipLaunchKernelGGL(k_qmm<8>, dim3(p.tiles_m * p.tiles_n), dim3(256), lds, st, p);
+  else hipLaunchKernelGGL(k_qmm<4>, dim3(p.tiles_m * p.tiles_n), dim3(256), lds, st, p);
   return check_launch("qmm");
 }
 

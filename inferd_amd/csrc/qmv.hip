@@ -1,18 +1,20 @@
-// Decode path (M <= 128 rows of concurrent agents): 4-bit GEMV/skinny GEMM on bf16 MFMA.
+// Decode path (M <= 128 rows of concurrent agents): 4- and 8-bit GEMV/skinny GEMM on bf16 MFMA.
 //
-// Replaces the reference's qmv4 (engine/kernels/core.metal:85-171) and its split-K neighbours (qmm_splitk +
+// Replaces the reference's qmv4 / qmv8 (engine/kernels/core.metal:85-171, 175-248) and its split-K neighbours (qmm_splitk +
 // splitk_reduce, engine/kernels/qmm_splitk.metal:14-107; host choice engine/src/qwen35.h:1520-1556).
 //
 // Layout per wave: 32 output columns (weight rows n) x a K range; lane l owns column l % 32 and half h = l / 32 of
-// every 64-group: the 16 bytes (32 codes) at words 4h..4h+3 of the group, one global_load_dwordx4 per group.
-// A 64-group is four 32x32x16 bf16 MFMA steps; in step t the lane supplies codes of word 4h + t, i.e. the k slots of
-// a step are k = 32h + 8t + 0..7 of the group, and the activation fragment follows the same k assignment (16 bytes
-// of row m at 32h + 8t), so every MFMA stays inside one group.
+// every 64-group's codes: 16 bytes (4 bits, words 4h..4h+3 of the group) or 2 x 16 bytes (8 bits, words 4h..4h+3
+// and 8+4h..8+4h+3), one or two global_load_dwordx4 per group, each covering 32 contiguous bytes of every row across
+// the wave. A 64-group is four 32x32x16 bf16 MFMA steps; in step t the lane supplies eight codes of the group
+// (GroupCodes::kofs) and the activation fragment of row m at the same k (16 bytes), so every MFMA stays inside one
+// group.
 //
 // Two variants:
-//  * affine (M <= 32): codes enter the MFMA as bf16 (128 + q) (exact), a second MFMA against ones gives the
-//    activation group sums X, and the group epilogue adds s * P + (b - 128 s) * X in fp32: the qmv4 arithmetic
-//    (s * sum q x + b * sum x per group, fp32) with fp32 MFMA accumulation.
+//  * affine (M <= 32): codes enter the MFMA as exact bf16 values, 128 + q (4 bits) or q (8 bits), a second MFMA
+//    against ones gives the activation group sums X, and the group epilogue adds s * P + (b - 128 s) * X (4 bits) or
+//    s * P + b * X (8 bits) in fp32: the qmv4 / qmv8 arithmetic (s * sum q x + b * sum x, fp32) with fp32 MFMA
+//    accumulation.
 //  * dequant (32 < M <= 128): codes are dequantized in registers to bf16(s q + b), MLX's qmm rounding
 //    (quantized.h:528-535), and accumulate over the whole K range; one dequant feeds all 32-row M tiles.
 // Narrow outputs split K over blockIdx.y and write fp32 partials [S][M][N]; k_splitk_reduce applies the store mode.
@@ -38,32 +40,32 @@ struct QmvArgs {
 
 constexpr int kQmvPF = 4;  // groups of weights in flight per lane
 
-template <int RACT>
+template <int RACT, int BITS>
 __global__ __launch_bounds__(256) void k_qmv_affine(QmvArgs p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, h = lane >> 5;
   const int n0 = blockIdx.x * 128 + wave * 32;
   if (n0 >= p.N) return;
   const int n = min(n0 + j, p.N - 1);
-  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+  const int G = p.K / kGroup, ldw = p.ldk * BITS / 32, ldg = p.ldk / kGroup;
   const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps);
   const uint32_t* wrow = p.wq + (size_t)n * ldw + 4 * h;
   const uint16_t* srow = p.s + (size_t)n * ldg;
   const uint16_t* brow = p.b + (size_t)n * ldg;
   const bool aok = j < p.M;
-  const uint16_t* arow = p.A + (size_t)(aok ? j : 0) * p.lda + 32 * h;
+  const uint16_t* arow = p.A + (size_t)(aok ? j : 0) * p.lda;
   const uint32_t xr = p.xr;
   u32x4 ones;
   ones[0] = ones[1] = ones[2] = ones[3] = 0x3F803F80u;  // bf16 1.0 pairs
 
   f32x16 acc = zero16();
-  u32x4 wbuf[kQmvPF];
+  GroupCodes<BITS> wbuf[kQmvPF];
   uint16_t sbuf[kQmvPF], bbuf[kQmvPF];  // raw bf16 bits: converted at use so the loads stay in flight
 #pragma unroll
   for (int i = 0; i < kQmvPF; i++) {
     const int g = g0 + i;
     if (g < g1) {
-      wbuf[i] = *(const u32x4*)(wrow + (size_t)g * 8);
+      wbuf[i].load(wrow, g);
       sbuf[i] = srow[g];
       bbuf[i] = brow[g];
     }
@@ -73,27 +75,27 @@ __global__ __launch_bounds__(256) void k_qmv_affine(QmvArgs p) {
     for (int i = 0; i < kQmvPF; i++) {
       const int g = gb + i;
       if (g >= g1) break;
-      const u32x4 wv = wbuf[i];
+      const GroupCodes<BITS> wv = wbuf[i];
       const uint16_t sraw = sbuf[i], braw = bbuf[i];
       if (g + kQmvPF < g1) {
-        wbuf[i] = *(const u32x4*)(wrow + (size_t)(g + kQmvPF) * 8);
+        wbuf[i].load(wrow, g + kQmvPF);
         sbuf[i] = srow[g + kQmvPF];
         bbuf[i] = brow[g + kQmvPF];
       }
       u32x4 af[4];
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        if (aok) af[t] = *(const u32x4*)(arow + (size_t)g * 64 + 8 * t);
+        if (aok) af[t] = *(const u32x4*)(arow + (size_t)g * 64 + GroupCodes<BITS>::kofs(t, h));
         else af[t] = u32x4{0u, 0u, 0u, 0u};
       }
       f32x16 P = zero16(), X = zero16();
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        P = mfma_bf16(af[t], codes_bf16_off128(wv[t] ^ xr), P);
+        P = mfma_bf16(af[t], wv.step_affine(t, xr), P);
         X = mfma_bf16(af[t], ones, X);
       }
       const float sc = bf2f(sraw), bi = bf2f(braw);
-      const float bp = __builtin_fmaf(-128.f, sc, bi);
+      const float bp = affine_bias<BITS>(sc, bi);
 #pragma unroll
       for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, X[r], acc[r]));
     }
@@ -110,14 +112,14 @@ __global__ __launch_bounds__(256) void k_qmv_affine(QmvArgs p) {
   }
 }
 
-template <int MT>
+template <int MT, int BITS>
 __global__ __launch_bounds__(256) void k_qmv_deq(QmvArgs p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, h = lane >> 5;
   const int n0 = blockIdx.x * 128 + wave * 32;
   if (n0 >= p.N) return;
   const int n = min(n0 + j, p.N - 1);
-  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+  const int G = p.K / kGroup, ldw = p.ldk * BITS / 32, ldg = p.ldk / kGroup;
   const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps);
   const uint32_t* wrow = p.wq + (size_t)n * ldw + 4 * h;
   const uint16_t* srow = p.s + (size_t)n * ldg;
@@ -128,20 +130,20 @@ __global__ __launch_bounds__(256) void k_qmv_deq(QmvArgs p) {
   for (int mt = 0; mt < MT; mt++) {
     const int m = 32 * mt + j;
     aok[mt] = m < p.M;
-    arow[mt] = p.A + (size_t)(aok[mt] ? m : 0) * p.lda + 32 * h;
+    arow[mt] = p.A + (size_t)(aok[mt] ? m : 0) * p.lda;
   }
   const uint32_t xr = p.xr;
 
   f32x16 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) acc[mt] = zero16();
-  u32x4 wbuf[kQmvPF];
+  GroupCodes<BITS> wbuf[kQmvPF];
   uint16_t sbuf[kQmvPF], bbuf[kQmvPF];  // raw bf16 bits: converted at use so the loads stay in flight
 #pragma unroll
   for (int i = 0; i < kQmvPF; i++) {
     const int g = g0 + i;
     if (g < g1) {
-      wbuf[i] = *(const u32x4*)(wrow + (size_t)g * 8);
+      wbuf[i].load(wrow, g);
       sbuf[i] = srow[g];
       bbuf[i] = brow[g];
     }
@@ -151,21 +153,21 @@ __global__ __launch_bounds__(256) void k_qmv_deq(QmvArgs p) {
     for (int i = 0; i < kQmvPF; i++) {
       const int g = gb + i;
       if (g >= g1) break;
-      const u32x4 wv = wbuf[i];
+      const GroupCodes<BITS> wv = wbuf[i];
       const uint16_t sraw = sbuf[i], braw = bbuf[i];
       if (g + kQmvPF < g1) {
-        wbuf[i] = *(const u32x4*)(wrow + (size_t)(g + kQmvPF) * 8);
+        wbuf[i].load(wrow, g + kQmvPF);
         sbuf[i] = srow[g + kQmvPF];
         bbuf[i] = brow[g + kQmvPF];
       }
       const float sc = bf2f(sraw), bi = bf2f(braw);
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        const u32x4 bfr = dequant8_bf16(wv[t] ^ xr, sc, bi);
+        const u32x4 bfr = wv.step_dequant(t, xr, sc, bi);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
           u32x4 af = u32x4{0u, 0u, 0u, 0u};
-          if (aok[mt]) af = *(const u32x4*)(arow[mt] + (size_t)g * 64 + 8 * t);
+          if (aok[mt]) af = *(const u32x4*)(arow[mt] + (size_t)g * 64 + GroupCodes<BITS>::kofs(t, h));
           acc[mt] = mfma_bf16(af, bfr, acc[mt]);
         }
       }
@@ -185,28 +187,29 @@ __global__ __launch_bounds__(256) void k_qmv_deq(QmvArgs p) {
     }
 }
 
-// Small-M decode (M <= 16): the block's activation rows for its K range are staged once in LDS, reordered to the
-// (0,4,1,5,2,6,3,7) pair order of codes_bf16_off128_p04 (one and-or per code pair), together with their 64-group
-// sums X. Afterwards each wave only streams its weights (two 8-group blocks in flight per lane) and reads
-// activations from LDS, so the weight loads are the only vector-memory traffic in the main loop.
+// Small-M decode (M <= 16): the block's activation rows for its K range are staged once in LDS together with their
+// 64-group sums X; for 4-bit codes the rows are reordered to the (0,4,1,5,2,6,3,7) pair order of
+// codes_bf16_off128_p04 (one and-or per code pair), 8-bit codes keep the natural order. Afterwards each wave only
+// streams its weights (two 8-group blocks in flight per lane, with the blocks' scales and biases as one 16 B load
+// each) and reads activations from LDS, so the weight loads are the only vector-memory traffic in the main loop.
 // Requires K % 512 == 0, ldk % 512 == 0, 16-byte aligned scales/biases and splits of whole 8-group blocks.
 
 __device__ __forceinline__ size_t small_lds_x_offset(int M, int Kz) {
   return ((size_t)M * (Kz + 8) * 2 + 15) / 16 * 16;  // bytes: A rows (Kz + 8 bf16 each), then X
 }
 
-template <int RACT>
+template <int RACT, int BITS>
 __global__ __launch_bounds__(256, 2) void k_qmv_small(QmvArgs p) {
   extern __shared__ __align__(16) uint16_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
-  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+  const int G = p.K / kGroup, ldw = p.ldk * BITS / 32, ldg = p.ldk / kGroup;
   const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps), Gz = g1 - g0;
   const int Kz = Gz * kGroup, ldA = Kz + 8, M = p.M;
   uint16_t* As = lds;
   float* Xs = (float*)((char*)lds + small_lds_x_offset(M, Kz));  // [Gz][16]
 
-  // ---- stage A[0:M][g0*64 : g1*64] (pair-ordered) and the group sums
+  // ---- stage A[0:M][g0*64 : g1*64] (pair-ordered for 4 bits) and the group sums
   const int cpr = Kz / 8, total = M * cpr;  // 16-byte chunks; a multiple of 8 (one group = 8 chunks)
   for (int c0 = 0; c0 < total; c0 += 256) {
     const int c = c0 + tid;
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(256, 2) void k_qmv_small(QmvArgs p) {
     sum += __shfl_xor(sum, 2, 64);
     sum += __shfl_xor(sum, 4, 64);
     if (ok) {
-      *(u32x4*)(As + (size_t)m * ldA + 8 * kc) = perm_pairs04(v);
+      *(u32x4*)(As + (size_t)m * ldA + 8 * kc) = BITS == 4 ? perm_pairs04(v) : v;
       if ((kc & 7) == 0) Xs[(kc >> 3) * 16 + m] = sum;
     }
   }
@@ -236,20 +239,20 @@ __global__ __launch_bounds__(256, 2) void k_qmv_small(QmvArgs p) {
   const uint16_t* srow = p.s + (size_t)n * ldg;
   const uint16_t* brow = p.b + (size_t)n * ldg;
   const bool aok = j < M;
-  const uint16_t* arow = As + (size_t)(aok ? j : 0) * ldA + 32 * h;
+  const uint16_t* arow = As + (size_t)(aok ? j : 0) * ldA;
   const uint32_t xr = p.xr;
 
   f32x16 acc = zero16();
-  // Ping-pong register blocks of 8 groups: 8 x 16 B of codes plus the 8 scales and 8 biases of this column as one
-  // 16 B vector each (ldg % 8 == 0, g0 % 8 == 0: checked by the host). Loads land where they are used, so the
-  // only waits are for a block issued one block earlier.
+  // Ping-pong register blocks of 8 groups: the lane's codes of 8 groups plus the 8 scales and 8 biases of this
+  // column as one 16 B vector each (ldg % 8 == 0, g0 % 8 == 0: checked by the host). Loads land where they are used,
+  // so the only waits are for a block issued one block earlier.
   struct Blk {
-    u32x4 w[8];
+    GroupCodes<BITS> w[8];
     u32x4 s, b;
   };
   auto load_blk = [&](Blk& B, int g) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) B.w[i] = *(const u32x4*)(wrow + (size_t)(g + i) * 8);
+    for (int i = 0; i < 8; i++) B.w[i].load(wrow, g + i);
     B.s = *(const u32x4*)(srow + g);
     B.b = *(const u32x4*)(brow + g);
   };
@@ -260,17 +263,21 @@ __global__ __launch_bounds__(256, 2) void k_qmv_small(QmvArgs p) {
       u32x4 af[4];
       const uint16_t* ag = arow + (size_t)gl * 64;
 #pragma unroll
-      for (int t = 0; t < 4; t++) af[t] = aok ? *(const u32x4*)(ag + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+      for (int t = 0; t < 4; t++)
+        af[t] = aok ? *(const u32x4*)(ag + GroupCodes<BITS>::kofs(t, h)) : u32x4{0u, 0u, 0u, 0u};
       const float4 x0 = *(const float4*)(Xs + gl * 16 + 4 * h);
       float4 x1 = make_float4(0.f, 0.f, 0.f, 0.f);
       if (RACT > 4) x1 = *(const float4*)(Xs + gl * 16 + 8 + 4 * h);
       f32x16 P = zero16();
 #pragma unroll
-      for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], codes_bf16_off128_p04(B.w[i][t] ^ xr), P);
+      for (int t = 0; t < 4; t++) {
+        const u32x4 bop = BITS == 4 ? codes_bf16_off128_p04(B.w[i].word(t) ^ xr) : B.w[i].step_affine(t, xr);
+        P = mfma_bf16(af[t], bop, P);
+      }
       const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       const float sc = bf2f((uint16_t)(B.s[i / 2] >> (16 * (i & 1))));
       const float bi = bf2f((uint16_t)(B.b[i / 2] >> (16 * (i & 1))));
-      const float bp = __builtin_fmaf(-128.f, sc, bi);
+      const float bp = affine_bias<BITS>(sc, bi);
 #pragma unroll
       for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[r]));
     }
@@ -439,18 +446,29 @@ int launch_qmv(const W4Gemm& g, void* ws, size_t ws_bytes, hipStream_t st) {
     const int Kz = gps * kGroup;
     const size_t lds = ((size_t)g.M * (Kz + 8) * 2 + 15) / 16 * 16 + (size_t)gps * 16 * sizeof(float);
     if (lds > 64 * 1024) return fail(IFD_ERR_UNSUPPORTED, "qmv: %zu bytes of LDS needed", lds);
-    if (g.M <= 8) hipLaunchKernelGGL(k_qmv_small<4>, grid, block, lds, st, p);
-    else hipLaunchKernelGGL(k_qmv_small<8>, grid, block, lds, st, p);
+    if (g.bits == 8) {
+      if (g.M <= 8) hipLaunchKernelGGL((k_qmv_small<4, 8>), grid, block, lds, st, p);
+      else hipLaunchKernelGGL((k_qmv_small<8, 8>), grid, block, lds, st, p);
+    } else {
+      if (g.M <= 8) hipLaunchKernelGGL((k_qmv_small<4, 4>), grid, block, lds, st, p);
+      else hipLaunchKernelGGL((k_qmv_small<8, 4>), grid, block, lds, st, p);
+    }
+  } else if (g.bits == 8) {
+    if (g.M <= 8) hipLaunchKernelGGL((k_qmv_affine<4, 8>), grid, block, 0, st, p);
+    else if (g.M <= 16) hipLaunchKernelGGL((k_qmv_affine<8, 8>), grid, block, 0, st, p);
+    else if (g.M <= 32) hipLaunchKernelGGL((k_qmv_affine<16, 8>), grid, block, 0, st, p);
+    else if (g.M <= 64) hipLaunchKernelGGL((k_qmv_deq<2, 8>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((k_qmv_deq<4, 8>), grid, block, 0, st, p);
   } else if (g.M <= 8) {
-    hipLaunchKernelGGL(k_qmv_affine<4>, grid, block, 0, st, p);
+    hipLaunchKernelGGL((k_qmv_affine<4, 4>), grid, block, 0, st, p);
   } else if (g.M <= 16) {
-    hipLaunchKernelGGL(k_qmv_affine<8>, grid, block, 0, st, p);
+    hipLaunchKernelGGL((k_qmv_affine<8, 4>), grid, block, 0, st, p);
   } else if (g.M <= 32) {
-    hipLaunchKernelGGL(k_qmv_affine<16>, grid, block, 0, st, p);
+    hipLaunchKernelGGL((k_qmv_affine<16, 4>), grid, block, 0, st, p);
   } else if (g.M <= 64) {
-    hipLaunchKernelGGL(k_qmv_deq<2>, grid, block, 0, st, p);
+    hipLaunchKernelGGL((k_qmv_deq<2, 4>), grid, block, 0, st, p);
   } else {
-    hipLaunchKernelGGL(k_qmv_deq<4>, grid, block, 0, st, p);
+    hipLaunchKernelGGL((k_qmv_deq<4, 4>), grid, block, 0, st, p);
   }
   IFD_TRY(check_launch("qmv"));
   if (S > 1) return launch_splitk_reduce((const float*)ws, S, g.M, g.N, g.C, g.ldc, g.mode, st);

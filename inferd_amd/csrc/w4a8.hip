@@ -1,5 +1,5 @@
-// W4A8: int8 activations x the checkpoint's 4-bit weights on int8 MFMA, plus the elementwise kernels of the path
-// (activation quantizer, in-place nibble flip, SwiGLU).
+// W4A8 / W8A8: int8 activations x the checkpoint's 4- or 8-bit weights on int8 MFMA, plus the elementwise kernels of
+// the path (activation quantizer, in-place flip, SwiGLU).
 //
 // Replaces the reference's a8_quant + w4a8_gemm (engine/kernels/w4a8.metal:24-98; host w4a8,
 // engine/src/qwen35.h:1323-1366), w_flip (w4a8.metal:19-22) and silu_mul (engine/kernels/core.metal:777-787).
@@ -137,7 +137,9 @@ struct W4A8Args {
   int tiles_m, tiles_n;
 };
 
-template <bool PT>
+// BITS 4: codes 0..15 enter the int8 MFMA as they are; BITS 8: as signed q - 128 (the stored byte ^ 0x80 once the
+// flip is undone), with the bias b + 128 s (reference w4a8_gemm BITS = 8, w4a8.metal:57, 78-87).
+template <bool PT, int BITS>
 __global__ __launch_bounds__(256) void k_w4a8(W4A8Args p) {
   __shared__ __align__(16) int8_t Us[2][kA8BM * kA8Ld];
   __shared__ __align__(16) int8_t Ws[2][kA8BN * kA8Ld];
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(256) void k_w4a8(W4A8Args p) {
   const int bm = min(kA8Band, p.tiles_m - band * kA8Band);
   const int tm = band * kA8Band + within % bm, tn = within / bm;
   const int m0 = tm * kA8BM, n0 = tn * kA8BN;
-  const int G = p.K / kGroup, ldw = p.ldk / 8, ldg = p.ldk / kGroup;
+  const int G = p.K / kGroup, ldw = p.ldk * BITS / 32, ldg = p.ldk / kGroup;
 
   // activation tile: 128 rows x 64 B, two 16 B chunks per thread: c = tid + 256 i -> row c / 4, part c % 4
   const int8_t* uptr[2];
@@ -165,7 +167,7 @@ __global__ __launch_bounds__(256) void k_w4a8(W4A8Args p) {
     uok[i] = m < p.M;
     uptr[i] = p.U + (size_t)(uok[i] ? m : 0) * p.K + 16 * (c & 3);
   }
-  // weight tile: row tid / 2, half tid % 2 (32 codes)
+  // weight tile: row tid / 2, half tid % 2 (32 codes = BITS words)
   const int wr = tid >> 1, wh = tid & 1;
   const int nw = min(n0 + wr, p.N - 1);
   const uint32_t* wptr = p.wq + (size_t)nw * ldw + 4 * wh;
@@ -173,13 +175,14 @@ __global__ __launch_bounds__(256) void k_w4a8(W4A8Args p) {
   const uint16_t* bptr = p.b + (size_t)nw * ldg;
   const int xm = min(m0 + (tid & 127), max(p.M - 1, 0));
 
-  u32x4 ureg[2], wreg;
+  u32x4 ureg[2];
+  GroupCodes<BITS> wreg;
   uint32_t sbreg = 0;
   float xsreg[2] = {0.f, 0.f};
   auto gload = [&](int g) {
 #pragma unroll
     for (int i = 0; i < 2; i++) ureg[i] = uok[i] ? *(const u32x4*)(uptr[i] + (size_t)g * 64) : u32x4{0u, 0u, 0u, 0u};
-    wreg = *(const u32x4*)(wptr + (size_t)g * 8);
+    wreg.load(wptr, g);
     if (wh == 0) sbreg = (uint32_t)sptr[g] | ((uint32_t)bptr[g] << 16);
     if (tid < 128) {
       xsreg[0] = p.XS[((size_t)xm * G + g) * 2];
@@ -192,9 +195,15 @@ __global__ __launch_bounds__(256) void k_w4a8(W4A8Args p) {
       const int c = tid + 256 * i;
       *(u32x4*)(&Us[buf][(c >> 2) * kA8Ld + 16 * (c & 3)]) = ureg[i];
     }
-    int8_t* ws = &Ws[buf][wr * kA8Ld + 32 * wh];
+    int8_t* ws = &Ws[buf][wr * kA8Ld];
+    if (BITS == 4) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) *(u32x2*)(ws + 8 * t) = codes_i8(wreg[t] ^ p.xr);
+      for (int t = 0; t < 4; t++) *(u32x2*)(ws + 32 * wh + 8 * t) = codes_i8(wreg.word(t) ^ p.xr);
+    } else {
+      const uint32_t sx = p.xr ^ 0x80808080u;  // stored byte -> q - 128 as int8
+#pragma unroll
+      for (int i = 0; i < 2; i++) *(u32x4*)(ws + 32 * i + 16 * wh) = wreg.w[i % (BITS / 4)] ^ u32x4{sx, sx, sx, sx};
+    }
     if (wh == 0) {
       Sb[buf][wr][0] = bf2f((uint16_t)(sbreg & 0xFFFFu));
       Sb[buf][wr][1] = bf2f((uint16_t)(sbreg >> 16));
@@ -240,7 +249,8 @@ __global__ __launch_bounds__(256) void k_w4a8(W4A8Args p) {
     // epilogue of the group
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      const float sc = Sb[buf][wn * 64 + 32 * c + j][0], bi = Sb[buf][wn * 64 + 32 * c + j][1];
+      const float sc = Sb[buf][wn * 64 + 32 * c + j][0];
+      const float bi = BITS == 4 ? Sb[buf][wn * 64 + 32 * c + j][1] : __builtin_fmaf(128.f, sc, Sb[buf][wn * 64 + 32 * c + j][1]);
 #pragma unroll
       for (int a = 0; a < 2; a++)
 #pragma unroll
@@ -283,8 +293,14 @@ int launch_w4a8(const W4Gemm& g, int per_token, void*, size_t, hipStream_t st) {
   if (g.M == 0) return IFD_OK;
   W4A8Args p{(const int8_t*)g.A, g.XS, g.wq, g.s, g.b, g.N, g.K, g.ldk, g.xr, g.C, g.ldc, g.M, g.mode,
              (g.M + kA8BM - 1) / kA8BM, (g.N + kA8BN - 1) / kA8BN};
-  if (per_token) hipLaunchKernelGGL(k_w4a8<true>, dim3(p.tiles_m * p.tiles_n), dim3(256), 0, st, p);
-  else hipLaunchKernelGGL(k_w4a8<false>, dim3(p.tiles_m * p.tiles_n), dim3(256), 0, st, p);
+  const dim3 grid(p.tiles_m * p.tiles_n);
+  if (g.bits == 8) {
+    if (per_token) hipLaunchKernelGGL((k_w4a8<true, 8>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((k_w4a8<false, 8>), grid, dim3(256), 0, st, p);
+  } else {
+    if (per_token) hipLaunchKernelGGL((k_w4a8<true, 4>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((k_w4a8<false, 4>), grid, dim3(256), 0, st, p);
+  }
   return check_launch("w4a8");
 }
 

@@ -14,6 +14,7 @@ import torch
 from ._lib import check, lib
 
 FLIP_MASK = 0x88888888
+FLIP_MASK_8 = 0x80808080
 
 
 def _p(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -40,17 +41,23 @@ def workspace(nbytes: int, device) -> torch.Tensor:
 
 @dataclass
 class QLinear:
-    """MLX affine 4-bit group-64 linear [N, K]: wq int32 [N, K/8] (uint32 bit patterns), s/b bf16 [N, K/64]."""
+    """MLX affine group-64 linear [N, K]: wq int32 [N, K bits/32] (uint32 bit patterns), s/b bf16 [N, K/64];
+    bits 4 (nibbles) or 8 (bytes)."""
     wq: torch.Tensor
     s: torch.Tensor
     b: torch.Tensor
     N: int
     K: int
     flipped: bool = False
+    bits: int = 4
+
+    @property
+    def flip_mask(self) -> int:
+        return FLIP_MASK_8 if self.bits == 8 else FLIP_MASK
 
     @property
     def xr(self) -> int:
-        return FLIP_MASK if self.flipped else 0
+        return self.flip_mask if self.flipped else 0
 
 
 @dataclass
@@ -126,8 +133,12 @@ def gemm(A: torch.Tensor, W: QLinear, C: Optional[torch.Tensor] = None, mode: in
     assert K == W.K and A.dtype == torch.bfloat16 and A.is_contiguous()
     if C is None:
         C = torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=A.device)
-    fn = {"auto": lib().ifd_gemm_w4, "qmv": lib().ifd_qmv_w4, "qmm": lib().ifd_qmm_w4}[path]
-    need = lib().ifd_gemm_w4_workspace(M, W.N, W.K)
+    if W.bits == 8:
+        assert path == "auto", "8-bit weights take the routed entry point"
+        fn, need = lib().ifd_gemm_w8, lib().ifd_gemm_w8_workspace(M, W.N, W.K)
+    else:
+        fn = {"auto": lib().ifd_gemm_w4, "qmv": lib().ifd_qmv_w4, "qmm": lib().ifd_qmm_w4}[path]
+        need = lib().ifd_gemm_w4_workspace(M, W.N, W.K)
     ws = workspace(need, A.device) if need else None
     check(fn(_p(A), K, _p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, W.xr, _p(C), C.shape[1], M, mode, _p(ws),
              ws.numel() if ws is not None else 0, _stream()))
@@ -135,8 +146,8 @@ def gemm(A: torch.Tensor, W: QLinear, C: Optional[torch.Tensor] = None, mode: in
 
 
 def flip(W: QLinear) -> None:
-    """In-place nibble flip (reference w_flip / Qwen35::flip)."""
-    check(lib().ifd_flip_w4(_p(W.wq), W.wq.numel(), FLIP_MASK, _stream()))
+    """In-place flip: nibbles q ^ 8 or bytes q ^ 0x80 (reference w_flip / Qwen35::flip)."""
+    check(lib().ifd_flip_w4(_p(W.wq), W.wq.numel(), W.flip_mask, _stream()))
     W.flipped = not W.flipped
 
 
@@ -205,8 +216,9 @@ def qmm_w4a8(U: torch.Tensor, XS: torch.Tensor, per_token: bool, W: QLinear, C: 
     M, K = U.shape
     if C is None:
         C = torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=U.device)
-    check(lib().ifd_qmm_w4a8(_p(U), _p(XS), 1 if per_token else 0, _p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, W.xr,
-                             _p(C), C.shape[1], M, mode, None, 0, _stream()))
+    fn = lib().ifd_qmm_w8a8 if W.bits == 8 else lib().ifd_qmm_w4a8
+    check(fn(_p(U), _p(XS), 1 if per_token else 0, _p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, W.xr,
+             _p(C), C.shape[1], M, mode, None, 0, _stream()))
     return C
 
 

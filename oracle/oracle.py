@@ -50,6 +50,12 @@ def lib():
         L.orc_dequant_bf16.argtypes = [_u32p, _u16p, _u16p, _i, _i, _u, _u16p]
         for f in (L.orc_qmv, L.orc_qmm):
             f.argtypes = [_u16p, _i, _u32p, _u16p, _u16p, _i, _i, _u, _f32p, _i, _i]
+        for f in (L.orc_qmv_b, L.orc_qmm_b):
+            f.argtypes = [_u16p, _i, _u32p, _u16p, _u16p, _i, _i, _i, _u, _f32p, _i, _i]
+        L.orc_wxa8.argtypes = [_i8p, _f32p, _u32p, _u16p, _u16p, _i, _i, _i, _u, _f32p, _i, _i]
+        L.orc_pack_w8.argtypes = [_u8p, _u32p, _i, _i]
+        L.orc_unpack_w8.argtypes = [_u32p, _u8p, _i, _i, _u]
+        L.orc_dequant_f32_b.argtypes = [_u32p, _u16p, _u16p, _i, _i, _i, _u, _f32p]
         L.orc_store.argtypes = [_f32p, _vp, _i, _i, _i, _i]
         L.orc_a8_quant.argtypes = [_u16p, _i, _i, _i, _i, _i8p, _f32p]
         L.orc_w4a8.argtypes = [_i8p, _f32p, _u32p, _u16p, _u16p, _i, _i, _u, _f32p, _i, _i]
@@ -126,24 +132,55 @@ def dequant_bf16(wq, s, b, K: int, xr: int = 0) -> np.ndarray:
 
 
 # ---- GEMMs (fp32 results before the store) ------------------------------------------------------------------------
-def qmv(A, wq, s, b, xr: int = 0, nthreads: int = 0) -> np.ndarray:
-    """qmv4 semantics (engine/kernels/core.metal:85-171)."""
+def qmv(A, wq, s, b, xr: int = 0, nthreads: int = 0, bits: int = 4) -> np.ndarray:
+    """qmv4 / qmv8 semantics (engine/kernels/core.metal:85-171, 175-248)."""
     A = _c(A, np.uint16)
     M, K = A.shape
     N = wq.shape[0]
     Y = np.empty((M, N), np.float32)
-    lib().orc_qmv(A, K, _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, xr, Y, M, nthreads)
+    if bits == 4:
+        lib().orc_qmv(A, K, _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, xr, Y, M, nthreads)
+    else:
+        lib().orc_qmv_b(A, K, _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, bits, xr, Y, M, nthreads)
     return Y
 
 
-def qmm(A, wq, s, b, xr: int = 0, nthreads: int = 0) -> np.ndarray:
+def qmm(A, wq, s, b, xr: int = 0, nthreads: int = 0, bits: int = 4) -> np.ndarray:
     """MLX affine_qmm_t semantics (bf16-rounded dequant; quantized.h:528-535, quantized_nax.h:938-1076)."""
     A = _c(A, np.uint16)
     M, K = A.shape
     N = wq.shape[0]
     Y = np.empty((M, N), np.float32)
-    lib().orc_qmm(A, K, _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, xr, Y, M, nthreads)
+    if bits == 4:
+        lib().orc_qmm(A, K, _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, xr, Y, M, nthreads)
+    else:
+        lib().orc_qmm_b(A, K, _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, bits, xr, Y, M, nthreads)
     return Y
+
+
+def pack_w8(codes) -> np.ndarray:
+    """codes uint8 [N, K] -> uint32 [N, K/4], byte j of a word = element j (MLX affine 8-bit)."""
+    codes = _c(codes, np.uint8)
+    N, K = codes.shape
+    wq = np.empty((N, K // 4), np.uint32)
+    lib().orc_pack_w8(codes, wq, N, K)
+    return wq
+
+
+def unpack_w8(wq, K: int, xr: int = 0) -> np.ndarray:
+    wq = _c(wq, np.uint32)
+    N = wq.shape[0]
+    codes = np.empty((N, K), np.uint8)
+    lib().orc_unpack_w8(wq, codes, N, K, xr)
+    return codes
+
+
+def dequant_f32_bits(wq, s, b, K: int, bits: int, xr: int = 0) -> np.ndarray:
+    wq = _c(wq, np.uint32)
+    N = wq.shape[0]
+    w = np.empty((N, K), np.float32)
+    lib().orc_dequant_f32_b(wq, _c(s, np.uint16), _c(b, np.uint16), N, K, bits, xr, w)
+    return w
 
 
 def store(Y, mode: int, C=None) -> np.ndarray:
@@ -170,14 +207,18 @@ def a8_quant(A, per_token: bool):
     return U, XS
 
 
-def w4a8(U, XS, wq, s, b, xr: int = 0, nthreads: int = 0) -> np.ndarray:
-    """w4a8_gemm semantics (engine/kernels/w4a8.metal:7-8, 78-87)."""
+def w4a8(U, XS, wq, s, b, xr: int = 0, nthreads: int = 0, bits: int = 4) -> np.ndarray:
+    """w4a8_gemm semantics (engine/kernels/w4a8.metal:7-8, 78-87); bits = 8: W8A8 (offset 128, :57)."""
     U = _c(U, np.int8)
     M, K = U.shape
     N = wq.shape[0]
     Y = np.empty((M, N), np.float32)
-    lib().orc_w4a8(U, _c(XS, np.float32), _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, xr, Y, M,
-                   nthreads)
+    if bits == 4:
+        lib().orc_w4a8(U, _c(XS, np.float32), _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, xr, Y, M,
+                       nthreads)
+    else:
+        lib().orc_wxa8(U, _c(XS, np.float32), _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), N, K, bits, xr,
+                       Y, M, nthreads)
     return Y
 
 

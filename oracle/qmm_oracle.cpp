@@ -62,6 +62,11 @@ void parallel_for(int n, int nthreads, F fn) {
 }
 
 inline int code_at(const uint32_t* wrow, int k, uint32_t xr) { return (int)(((wrow[k >> 3] ^ xr) >> (4 * (k & 7))) & 15u); }
+// 8-bit: byte k % 4 of word k / 4 (MLX affine 8-bit; reference qmv8, engine/kernels/core.metal:173-174, 224-228)
+inline int code8_at(const uint32_t* wrow, int k, uint32_t xr) { return (int)(((wrow[k >> 2] ^ xr) >> (8 * (k & 3))) & 255u); }
+inline int code_b(const uint32_t* wrow, int k, uint32_t xr, int bits) {
+  return bits == 8 ? code8_at(wrow, k, xr) : code_at(wrow, k, xr);
+}
 
 }  // namespace
 
@@ -91,7 +96,20 @@ void orc_unpack_w4(const uint32_t* wq, uint8_t* codes, int N, int K, uint32_t xr
   for (int n = 0; n < N; n++)
     for (int k = 0; k < K; k++) codes[(size_t)n * K + k] = (uint8_t)code_at(wq + (size_t)n * (K / 8), k, xr);
 }
-// In-place flip, engine/kernels/w4a8.metal:19-22 (mask 0x88888888 for 4-bit).
+// codes uint8 [N, K] (0..255) -> Wq uint32 [N, K/4], byte j of a word = element j (MLX affine 8-bit).
+void orc_pack_w8(const uint8_t* codes, uint32_t* wq, int N, int K) {
+  for (int n = 0; n < N; n++)
+    for (int w = 0; w < K / 4; w++) {
+      uint32_t v = 0;
+      for (int j = 0; j < 4; j++) v |= (uint32_t)codes[(size_t)n * K + 4 * w + j] << (8 * j);
+      wq[(size_t)n * (K / 4) + w] = v;
+    }
+}
+void orc_unpack_w8(const uint32_t* wq, uint8_t* codes, int N, int K, uint32_t xr) {
+  for (int n = 0; n < N; n++)
+    for (int k = 0; k < K; k++) codes[(size_t)n * K + k] = (uint8_t)code8_at(wq + (size_t)n * (K / 4), k, xr);
+}
+// In-place flip, engine/kernels/w4a8.metal:19-22 (mask 0x88888888 for 4-bit, 0x80808080 for 8-bit).
 void orc_flip(uint32_t* wq, int64_t n32, uint32_t mask) {
   for (int64_t i = 0; i < n32; i++) wq[i] ^= mask;
 }
@@ -104,6 +122,16 @@ void orc_dequant_f32(const uint32_t* wq, const uint16_t* s, const uint16_t* b, i
       w[(size_t)n * K + k] = sc * (float)code_at(wq + (size_t)n * (K / 8), k, xr) + bi;
     }
 }
+// Either width: w = S*q + B in fp32 (bits 4 or 8).
+void orc_dequant_f32_b(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int bits, uint32_t xr,
+                       float* w) {
+  const int kg = K / 64, kw = K * bits / 32;
+  for (int n = 0; n < N; n++)
+    for (int k = 0; k < K; k++) {
+      const float sc = bf2f(s[(size_t)n * kg + k / 64]), bi = bf2f(b[(size_t)n * kg + k / 64]);
+      w[(size_t)n * K + k] = sc * (float)code_b(wq + (size_t)n * kw, k, xr, bits) + bi;
+    }
+}
 // Dequantize to bf16 as MLX's qmm loader does: bf16(fp32(S*q + B)) (third_party/mlx/.../quantized.h:528-535).
 void orc_dequant_bf16(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, uint32_t xr, uint16_t* w) {
   const int kg = K / 64;
@@ -114,12 +142,12 @@ void orc_dequant_bf16(const uint32_t* wq, const uint16_t* s, const uint16_t* b, 
     }
 }
 
-// Decode GEMV semantics (engine/kernels/core.metal:85-171, qmv4): per 64-group g,
+// Decode GEMV semantics (engine/kernels/core.metal:85-171 qmv4, 175-248 qmv8): per 64-group g,
 //   y[m,n] += S[n,g] * sum_{k in g} q[n,k] x[m,k] + B[n,g] * sum_{k in g} x[m,k], fp32 throughout.
-// A bf16 [M, lda], Y fp32 [M, N] (the value before the bf16 store; see orc_store).
-void orc_qmv(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
-             uint32_t xr, float* Y, int M, int nthreads) {
-  const int kg = K / 64, kw = K / 8;
+// A bf16 [M, lda], Y fp32 [M, N] (the value before the bf16 store; see orc_store). bits 4 or 8.
+void orc_qmv_b(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+               int bits, uint32_t xr, float* Y, int M, int nthreads) {
+  const int kg = K / 64, kw = K * bits / 32;
   std::vector<float> xf((size_t)M * K);
   for (int m = 0; m < M; m++)
     for (int k = 0; k < K; k++) xf[(size_t)m * K + k] = bf2f(A[(size_t)m * lda + k]);
@@ -131,7 +159,7 @@ void orc_qmv(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, 
       for (int g = 0; g < kg; g++) {
         float qx = 0.f, sx = 0.f;
         for (int k = g * 64; k < g * 64 + 64; k++) {
-          qx += (float)code_at(wr, k, xr) * x[k];
+          qx += (float)code_b(wr, k, xr, bits) * x[k];
           sx += x[k];
         }
         acc += bf2f(s[(size_t)n * kg + g]) * qx + bf2f(b[(size_t)n * kg + g]) * sx;
@@ -140,12 +168,17 @@ void orc_qmv(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, 
     }
   });
 }
+void orc_qmv(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+             uint32_t xr, float* Y, int M, int nthreads) {
+  orc_qmv_b(A, lda, wq, s, b, N, K, 4, xr, Y, M, nthreads);
+}
 
 // Prefill GEMM semantics (MLX affine_qmm_t: third_party/mlx/.../quantized_nax.h:938-1076 with the dequant of
 // quantized.h:528-535): every weight is dequantized to bf16(S*q + B), activations are bf16, fp32 accumulation over K.
-void orc_qmm(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
-             uint32_t xr, float* Y, int M, int nthreads) {
-  const int kg = K / 64, kw = K / 8;
+// bits 4 or 8 (MLX instantiates the same loader for both, quantized.h:486-576).
+void orc_qmm_b(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+               int bits, uint32_t xr, float* Y, int M, int nthreads) {
+  const int kg = K / 64, kw = K * bits / 32;
   std::vector<float> xf((size_t)M * K);
   for (int m = 0; m < M; m++)
     for (int k = 0; k < K; k++) xf[(size_t)m * K + k] = bf2f(A[(size_t)m * lda + k]);
@@ -153,7 +186,8 @@ void orc_qmm(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, 
     const uint32_t* wr = wq + (size_t)n * kw;
     std::vector<float> wrow(K);
     for (int k = 0; k < K; k++)
-      wrow[k] = bfround(bf2f(s[(size_t)n * kg + k / 64]) * (float)code_at(wr, k, xr) + bf2f(b[(size_t)n * kg + k / 64]));
+      wrow[k] = bfround(bf2f(s[(size_t)n * kg + k / 64]) * (float)code_b(wr, k, xr, bits) +
+                        bf2f(b[(size_t)n * kg + k / 64]));
     for (int m = 0; m < M; m++) {
       const float* x = xf.data() + (size_t)m * K;
       float acc = 0.f;
@@ -161,6 +195,10 @@ void orc_qmm(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, 
       Y[(size_t)m * N + n] = acc;
     }
   });
+}
+void orc_qmm(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+             uint32_t xr, float* Y, int M, int nthreads) {
+  orc_qmm_b(A, lda, wq, s, b, N, K, 4, xr, Y, M, nthreads);
 }
 
 // Store epilogue shared by every GEMM (engine/kernels/core.metal:14-15): mode 0 C = bf16(y), 1 C = bf16(y + C),
@@ -204,28 +242,34 @@ void orc_a8_quant(const uint16_t* A, int lda, int M, int K, int per_token, int8_
   }
 }
 
-// W4A8 GEMM (engine/kernels/w4a8.metal:7-8, 78-87): per group g, P = sum (q - 8) xq exactly (integers), then
-//   y += S sx P + (B + 8 S) (sx sum xq)   in fp32, in group order.
-void orc_w4a8(const int8_t* U, const float* XS, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
-              uint32_t xr, float* Y, int M, int nthreads) {
-  const int kg = K / 64, kw = K / 8;
+// W4A8 / W8A8 GEMM (engine/kernels/w4a8.metal:7-8, 57, 78-87): per group g, P = sum (q - off) xq exactly (integers,
+// off = 8 for 4 bits, 128 for 8 bits), then
+//   y += S sx P + (B + off S) (sx sum xq)   in fp32, in group order.
+void orc_wxa8(const int8_t* U, const float* XS, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+              int bits, uint32_t xr, float* Y, int M, int nthreads) {
+  const int kg = K / 64, kw = K * bits / 32;
+  const int off = bits == 8 ? 128 : 8;
   parallel_for(N, nthreads, [&](int n) {
     const uint32_t* wr = wq + (size_t)n * kw;
     std::vector<int8_t> qs(K);
-    for (int k = 0; k < K; k++) qs[k] = (int8_t)(code_at(wr, k, xr) - 8);
+    for (int k = 0; k < K; k++) qs[k] = (int8_t)(code_b(wr, k, xr, bits) - off);
     for (int m = 0; m < M; m++) {
       const int8_t* u = U + (size_t)m * K;
       float acc = 0.f;
       for (int g = 0; g < kg; g++) {
         int32_t P = 0;
         for (int k = g * 64; k < g * 64 + 64; k++) P += (int32_t)qs[k] * (int32_t)u[k];
-        const float sw = bf2f(s[(size_t)n * kg + g]), bw = bf2f(b[(size_t)n * kg + g]) + 8.f * sw;
+        const float sw = bf2f(s[(size_t)n * kg + g]), bw = bf2f(b[(size_t)n * kg + g]) + (float)off * sw;
         const float sx = XS[((size_t)m * kg + g) * 2], sq = XS[((size_t)m * kg + g) * 2 + 1];
         acc += sw * sx * (float)P + bw * sq;
       }
       Y[(size_t)m * N + n] = acc;
     }
   });
+}
+void orc_w4a8(const int8_t* U, const float* XS, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+              uint32_t xr, float* Y, int M, int nthreads) {
+  orc_wxa8(U, XS, wq, s, b, N, K, 4, xr, Y, M, nthreads);
 }
 
 // SwiGLU on rows of [gate (I) | up (I)] (engine/kernels/core.metal:777-787, moe.metal:103-111):

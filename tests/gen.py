@@ -41,6 +41,25 @@ def qlinear(N: int, K: int, seed: int, smin: float = 0.005, smax: float = 0.02, 
     return codes, pack_codes(codes), s, b
 
 
+def pack_codes8(codes: np.ndarray) -> np.ndarray:
+    """codes uint8 [N, K] -> uint32 [N, K/4], element j in byte j (numpy restatement of MLX's 8-bit layout)."""
+    N, K = codes.shape
+    return np.ascontiguousarray(codes, dtype=np.uint8).reshape(N, K // 4, 4).view("<u4").reshape(N, K // 4).astype(np.uint32)
+
+
+def qlinear8(N: int, K: int, seed: int, bias: str = "minus128"):
+    """An 8-bit layer with the same weight range as qlinear: q ~ U{0..255}, s ~ U(0.005, 0.02) / 16 in bf16, and
+    b = bf16(-128 s) (or independent biases). Returns (codes, wq uint32 [N, K/4], s, b)."""
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 256, size=(N, K), dtype=np.uint8)
+    s = f32_to_bf16((rng.uniform(0.005, 0.02, size=(N, K // 64)) / 16).astype(np.float32))
+    if bias == "minus128":
+        b = f32_to_bf16(-128.0 * bf16_to_f32(s))
+    else:
+        b = f32_to_bf16((0.05 * rng.uniform(-1, 1, size=(N, K // 64))).astype(np.float32))
+    return codes, pack_codes8(codes), s, b
+
+
 def activations(M: int, K: int, seed: int, row_scale: bool = False) -> np.ndarray:
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((M, K)).astype(np.float32)

@@ -24,9 +24,9 @@ def host(t: torch.Tensor) -> np.ndarray:
     return t.numpy()
 
 
-def qlinear(wq, s, b, flipped=False) -> QLinear:
+def qlinear(wq, s, b, flipped=False, bits=4) -> QLinear:
     N = wq.shape[0]
-    return QLinear(dev(wq), dev(s), dev(b), N, wq.shape[1] * 8, flipped)
+    return QLinear(dev(wq), dev(s), dev(b), N, wq.shape[1] * 32 // bits, flipped, bits)
 
 
 def moew(wq, s, b) -> MoeW:

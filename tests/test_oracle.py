@@ -175,6 +175,81 @@ def test_w4a8_identity(per_token):
     assert gen.rel_err(orc.w4a8(U, XS, wq ^ np.uint32(0x88888888), s, b, xr=0x88888888), ref) < 1e-5
 
 
+# ---- 8-bit weights (qmv8, core.metal:175-248; MLX 8-bit qmm; W8A8, w4a8.metal BITS = 8) ----------------------------
+def test_unpack8_exhaustive_every_code_every_position():
+    """Every code 0..255 in each of the four byte positions; flipped storage (q ^ 0x80) undone by xr."""
+    rows = [code << (8 * pos) for pos in range(4) for code in range(256)]
+    wq = np.array(rows, np.uint32).reshape(-1, 1)
+    codes = orc.unpack_w8(wq, 4)
+    i = 0
+    for pos in range(4):
+        for code in range(256):
+            want = [0] * 4
+            want[pos] = code
+            assert codes[i].tolist() == want
+            i += 1
+    assert np.array_equal(orc.unpack_w8(wq ^ np.uint32(0x80808080), 4, 0x80808080), codes)
+    c = np.arange(256, dtype=np.uint8).reshape(2, 128)
+    assert np.array_equal(orc.pack_w8(c), gen.pack_codes8(c))
+    assert int(orc.pack_w8(c)[0, 0]) == 0x03020100
+
+
+def test_one_hot_probe_is_dequant_8bit():
+    N, K = 16, 256
+    codes, wq, s, b = gen.qlinear8(N, K, seed=12, bias="free")
+    ks = [0, 1, 3, 4, 63, 64, 129, 255]
+    A = np.zeros((len(ks), K), np.uint16)
+    for i, k in enumerate(ks):
+        A[i, k] = 0x3F80
+    w32 = orc.dequant_f32_bits(wq, s, b, K, 8)
+    yv, ym = orc.qmv(A, wq, s, b, bits=8), orc.qmm(A, wq, s, b, bits=8)
+    for i, k in enumerate(ks):
+        sk = gen.bf16_to_f32(s[:, k // 64]).astype(np.float64)
+        bk = gen.bf16_to_f32(b[:, k // 64]).astype(np.float64)
+        exact = sk * codes[:, k] + bk
+        assert np.allclose(yv[i], exact, rtol=2 ** -22, atol=0)
+        assert np.array_equal(yv[i], w32[:, k])
+        assert np.array_equal(gen.f32_to_bf16(ym[i]), gen.f32_to_bf16((sk * codes[:, k] + bk).astype(np.float32)))
+
+
+def test_all_128_is_exactly_zero_8bit():
+    N, K = 8, 512
+    _, _, s, b = gen.qlinear8(N, K, seed=5)  # b = -128 s (exact: 128 s is a power-of-two multiple)
+    wq = gen.pack_codes8(np.full((N, K), 128, np.uint8))
+    A = gen.activations(4, K, seed=6)
+    assert np.all(orc.qmv(A, wq, s, b, bits=8) == 0)
+    assert np.all(orc.qmm(A, wq, s, b, bits=8) == 0)
+    U, XS = orc.a8_quant(A, False)
+    assert np.all(np.abs(orc.w4a8(U, XS, wq, s, b, bits=8)) < 1e-3)
+
+
+@pytest.mark.parametrize("M,N,K", [(37, 200, 512), (1, 64, 5120)])
+def test_gemms_8bit_match_float64_textbook(M, N, K):
+    codes, wq, s, b = gen.qlinear8(N, K, seed=M + N + 1, bias="free")
+    A = gen.activations(M, K, seed=K + 1)
+    x64 = gen.bf16_to_f32(A).astype(np.float64)
+    w64 = gen.dequant_f64(codes, s, b)
+    assert gen.rel_err(orc.qmv(A, wq, s, b, bits=8), x64 @ w64.T) < 1e-5
+    wbf = gen.bf16_to_f32(gen.f32_to_bf16(w64.astype(np.float32))).astype(np.float64)
+    assert gen.rel_err(orc.qmm(A, wq, s, b, bits=8), x64 @ wbf.T) < 1e-5
+    # a 4-bit reading of the same words is a different matrix: the width is not silently ignored
+    assert gen.rel_err(orc.qmv(A, wq[:, : K // 8], s, b), x64 @ w64.T) > 0.1
+
+
+@pytest.mark.parametrize("per_token", [False, True])
+def test_w8a8_identity(per_token):
+    """The W8A8 identity (w4a8.metal:8 with offset 128): float64 GEMM of the dequantized 8-bit weights against
+    sx * xq; flipped storage (q ^ 0x80) gives the same result."""
+    M, N, K = 9, 48, 640
+    codes, wq, s, b = gen.qlinear8(N, K, seed=3, bias="free")
+    A = gen.activations(M, K, seed=5)
+    U, XS = orc.a8_quant(A, per_token)
+    xd = U.astype(np.float64) * np.repeat(XS[:, :, 0], 64, axis=1)
+    ref = xd @ gen.dequant_f64(codes, s, b).T
+    assert gen.rel_err(orc.w4a8(U, XS, wq, s, b, bits=8), ref) < 1e-5
+    assert gen.rel_err(orc.w4a8(U, XS, wq ^ np.uint32(0x80808080), s, b, xr=0x80808080, bits=8), ref) < 1e-5
+
+
 def test_store_modes():
     Y = np.array([[1.5, -2.25], [3.0e-3, 7.0]], np.float32)
     C = gen.f32_to_bf16(np.array([[1.0, 1.0], [1.0, -7.0]], np.float32))
