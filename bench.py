@@ -269,6 +269,17 @@ def main():
 
                 ms = timed(run, 10, 3)
                 moe[f"T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3))
+            # decode batches (T <= 8): the four-launch decode MoE, each distinct expert read once
+            for T in (1, 2, 4, 8):
+                xn = act(T, H)
+                outb = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+
+                def run_dec(i):
+                    egu, edn, sgu, sdn = lay[i % ncp]
+                    ops.moe_decode(xn, router, egu, edn, k, shared=(sgu, sdn), shared_gate=False, out=outb)
+
+                ms = timed(run_dec, 50, 5)
+                moe[f"decode_T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3))
             breakdown["c4_moe"] = moe
             del lay
 

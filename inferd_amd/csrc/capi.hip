@@ -410,4 +410,34 @@ int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, 
   return launch_moe_combine((uint16_t*)out, (const uint16_t*)(w + L.edn), rwt, ys, rsg, inv, T, H, k, assign, st);
 }
 
+// ---- decode MoE (T <= 8) ---------------------------------------------------------------------------------------
+size_t ifd_moe_decode_workspace(int T, int H, int I, int E, int k) {
+  if (T <= 0 || T > 8 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  return with_header(mdec_layout(T, H, I, E, k).total);
+}
+
+int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
+                   const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
+                   const uint16_t* edn_s, const uint16_t* edn_b, int I, const uint32_t* sgu_wq, const uint16_t* sgu_s,
+                   const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b,
+                   void* out, int assign, int* idx, float* wt, float* sg, float* logits, void* workspace,
+                   size_t ws_bytes, void* stream) {
+  IFD_CHECK(T >= 0 && T <= 8, "the decode MoE takes T <= 8 tokens (T=%d): larger batches use ifd_moe_ffn", T);
+  IFD_CHECK(H > 0 && H % 256 == 0 && H <= 131072 && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 && k <= 16 &&
+                k <= E,
+            "bad decode MoE shape H=%d I=%d E=%d k=%d (H multiple of 256, I of 64, E <= 512, k <= 16)", H, I, E, k);
+  const bool shared = sgu_wq != nullptr;
+  IFD_CHECK(!shared || (sgu_s && sgu_b && sdn_wq && sdn_s && sdn_b), "bad shared expert");
+  IFD_CHECK(!shared_gate || shared, "a shared gate needs a shared expert");
+  if (T == 0) return IFD_OK;
+  IFD_CHECK(xn && router && egu_wq && egu_s && egu_b && edn_wq && edn_s && edn_b && out, "null pointer");
+  IFD_CHECK(aligned(xn, 16) && aligned(router, 16) && aligned(egu_wq, 16) && aligned(edn_wq, 16) &&
+                (!shared || (aligned(sgu_wq, 16) && aligned(sdn_wq, 16))),
+            "tokens, router and weights must be 16-byte aligned");
+  const WsView wv = ws_view(workspace, ws_bytes);
+  MdecCall c{xn, router, T, H, E, k, I, norm ? 1 : 0, shared_gate ? 1 : 0, assign ? 1 : 0, egu_wq, egu_s, egu_b,
+             edn_wq, edn_s, edn_b, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, out, idx, wt, sg, logits};
+  return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
+}
+
 }  // extern "C"

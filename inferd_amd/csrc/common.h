@@ -200,6 +200,14 @@ __device__ __forceinline__ int wave_min_i(int v) {
   return v;
 }
 
+// Device-coherent (sc1) buffer accesses to data that blocks on different XCDs (separate L2s) exchange within one
+// kernel: stores write through to memory, loads do not hit a stale line of the local L2. Plain loads batch, unlike
+// atomic loads, which the compiler orders one after another.
+constexpr int kSc1 = 16;  // cache-policy operand: SC1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const void* part, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, (int)bytes, 0x00020000);
+}
+
 // Bijective remap of a 1-D block id so that each XCD (blocks are dealt round-robin over 8 XCDs) runs a contiguous
 // range of logical tiles: neighbouring tiles then share that XCD's L2.
 __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {

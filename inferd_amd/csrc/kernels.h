@@ -101,4 +101,34 @@ int launch_moe_gather_qmm(const uint16_t* A, const int* perm, int div, const int
 int launch_moe_combine(uint16_t* out, const uint16_t* yd, const float* wt, const uint16_t* ys, const float* sg,
                        const int* inv, int T, int H, int k, int assign, hipStream_t st);
 
+// Decode MoE for T <= 8 tokens (moe_dec.hip): router, routing + distinct-expert plan, gate/up + SwiGLU, down +
+// combine; the combine's counters are H / 128 uint32 of the workspace header.
+struct MdecCall {
+  const void* xn;
+  const void* router;
+  int T, H, E, k, I, norm, shared_gate, assign;
+  const uint32_t* egu_wq;
+  const uint16_t* egu_s;
+  const uint16_t* egu_b;
+  const uint32_t* edn_wq;
+  const uint16_t* edn_s;
+  const uint16_t* edn_b;
+  const uint32_t* sgu_wq;
+  const uint16_t* sgu_s;
+  const uint16_t* sgu_b;
+  const uint32_t* sdn_wq;
+  const uint16_t* sdn_s;
+  const uint16_t* sdn_b;
+  void* out;
+  int* idx;
+  float* wt;
+  float* sg;
+  float* logits;
+};
+struct MdecLayout {
+  size_t part, plan, act, d, idx, wt, sg, total;
+};
+MdecLayout mdec_layout(int T, int H, int I, int E, int k);
+int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st);
+
 }  // namespace ifd

@@ -8,6 +8,7 @@
 #include "common.h"
 #include "host.h"
 #include "kernels.h"
+#include "moe_dev.h"
 
 namespace ifd {
 
@@ -62,52 +63,21 @@ template <bool BF>
 __global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ logits, int T, int E, int k, int stride,
                                                    int norm, int shared_gate, int* __restrict__ idx,
                                                    float* __restrict__ wt, float* __restrict__ sg) {
-  const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   auto L = [&](int c) -> float {
     return BF ? bf2f(((const uint16_t*)logits)[(size_t)t * stride + c]) : ((const float*)logits)[(size_t)t * stride + c];
   };
   float v[8];
-  float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int c = i * 64 + lane;
-    v[i] = c < E ? L(c) : -INFINITY;
-    mx = fmaxf(mx, v[i]);
-  }
-  mx = wave_max(mx);
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const bool ok = i * 64 + lane < E;
-    const float ex = ok ? expf(v[i] - mx) : 0.f;
-    sum += ex;
-    v[i] = ok ? ex : -2.f;  // padding never wins a pick (picks need v > -1)
-  }
-  sum = wave_sum(sum);
-  float tot = 0.f, picked[16];
-  int who_j[16];
-  for (int jj = 0; jj < k; jj++) {
-    float best = -1.f;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      if (v[i] > best) best = v[i], bi = i * 64 + lane;  // strict >: lowest index of this lane wins a tie
-    const float m = wave_max(best);
-    const int who = wave_min_i(best == m ? bi : 0x7fffffff);
-    if ((who & 63) == lane) {
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-        if (i == who / 64) v[i] = -1.f;
-    }
-    picked[jj] = m / sum;
-    who_j[jj] = who;
-    tot += m / sum;
-  }
-  if (lane == 0) {
+  for (int i = 0; i < 8; i++) v[i] = i * 64 + (int)(threadIdx.x & 63) < E ? L(i * 64 + (threadIdx.x & 63)) : 0.f;
+  int who[16];
+  float p[16];
+  route_token(v, E, k, norm, who, p);
+  if ((threadIdx.x & 63) == 0) {
     for (int jj = 0; jj < k; jj++) {
-      idx[(size_t)t * k + jj] = who_j[jj];
-      wt[(size_t)t * k + jj] = norm ? picked[jj] / tot : picked[jj];
+      idx[(size_t)t * k + jj] = who[jj];
+      wt[(size_t)t * k + jj] = p[jj];
     }
     sg[t] = shared_gate ? 1.f / (1.f + expf(-L(E))) : 1.f;
   }

@@ -1,0 +1,484 @@
+// Decode MoE for T <= 8 tokens in four launches, each distinct expert's weights read once for every token that
+// picked it.
+//
+// Replaces the reference's four-launch decode MoE (engine/kernels/moe.metal:267-293 router, 326-368 moe_plan,
+// 370-488 moe_gu2, 490-551 moe_dn2; host engine/src/qwen35.h:1876-1908):
+//  1. k_mdec_router: router logits (bf16 router [E1][H] x bf16 tokens) as K-split fp32 partials [KS][T][E1]. One
+//     32-expert tile x a K range per wave (32x32x16 bf16 MFMA, tokens in the A rows), the block's four waves summed
+//     in wave order.
+//  2. k_mdec_plan (one block): wave t sums token t's partials in split order and routes it (route_token, as
+//     k_moe_route); one thread per pick then lists the distinct experts in pick order: plan = [nuniq, expert[T k],
+//     pick[T k][8]] (pick[u][t] = token t's pick index of unique expert u, or -1).
+//  3. k_mdec_gu: one block per (32 gate/up column pairs, unique expert or the shared expert). Its four waves split K;
+//     each stages the token rows of its K range in LDS and streams the 32 gate and 32 up rows of its expert (16 B
+//     of codes per lane and group, all loads of a chunk issued before the first wait), runs the qmv4 arithmetic on
+//     bf16 MFMA (codes as 128 + q, the group sums X from the staged rows, s P + (b - 128 s) X in fp32), and the waves'
+//     sums are added in wave order. The SwiGLU of the bf16-rounded gate and up goes to act[t][j] for every token t
+//     that picked the expert as its j-th (j = k: the shared expert).
+//  4. k_mdec_dn: one block per (128 output columns, unique expert or the shared expert): the down rows of the expert
+//     against act of the tokens that picked it (same arithmetic), d[t][j] = bf16(result), stored write-through. The
+//     last block of each 128-column chunk (a counter in the workspace header) combines:
+//     out[t][h] = bf16(acc) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] d[t][j][h] + sg[t] d[t][k][h], in j order.
+// Every sum runs in a fixed order, so results do not depend on block timing.
+#include <algorithm>
+
+#include "common.h"
+#include "host.h"
+#include "kernels.h"
+#include "moe_dev.h"
+
+namespace ifd {
+
+constexpr int kMdecMaxT = 8, kMdecMaxK = 16, kMdecKG = 8;  // tokens, picks, groups per wave and chunk
+constexpr int kMdecMaxKS = 4;                                 // K splits of the router
+
+struct MdecArgs {
+  const uint16_t* x;       // normalised tokens [T][H]
+  const uint16_t* router;  // bf16 [E1][H]
+  int T, H, E, E1, k, I, norm, shared_gate, assign, KS;
+  const uint32_t* egu_wq;  // routed experts [E][2I][H] (gate rows, then up rows), MLX affine 4-bit
+  const uint16_t* egu_s;
+  const uint16_t* egu_b;
+  const uint32_t* edn_wq;  // [E][H][I]
+  const uint16_t* edn_s;
+  const uint16_t* edn_b;
+  const uint32_t* sgu_wq;  // shared expert [2I][H] and [H][I], or null
+  const uint16_t* sgu_s;
+  const uint16_t* sgu_b;
+  const uint32_t* sdn_wq;
+  const uint16_t* sdn_s;
+  const uint16_t* sdn_b;
+  uint16_t* out;           // [T][H]
+  int* idx;                // routing outputs [T][k], [T][k], [T]
+  float* wt;
+  float* sg;
+  float* logits;           // optional [T][E1]: the summed logits the routing used
+  float* part;             // [KS][T][E1]
+  int* plan;               // [1 + T k + T k 8]
+  uint16_t* act;           // [T][k + 1][I]
+  uint16_t* d;             // [T][k + 1][H]
+  uint32_t d_bytes;
+  unsigned* cnt;           // H / 128 counters, zero between calls
+  int sb16_gu, sb16_dn;    // a wave's 8 scales (biases) of a row are one aligned 16 B load
+};
+
+// The 8 bf16 values at v (16-byte aligned) as 8 raw halves.
+__device__ __forceinline__ void load8h(const uint16_t* v, uint16_t (&o)[kMdecKG]) {
+  const u32x4 w = *(const u32x4*)v;
+#pragma unroll
+  for (int i = 0; i < 8; i++) o[i] = (uint16_t)(w[i / 2] >> (16 * (i & 1)));
+}
+
+// ---- 1. router logits --------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_mdec_router(MdecArgs p) {
+  __shared__ float red[4][64][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 31, h = lane >> 5;
+  const int e0 = blockIdx.x * 32, ks = blockIdx.y;
+  const int Kc = p.H / (4 * p.KS), k0 = (ks * 4 + wave) * Kc;
+  const bool tok = j < p.T, eok = e0 + j < p.E1;
+  const uint16_t* xa = p.x + (size_t)(tok ? j : 0) * p.H + k0 + 32 * h;
+  const uint16_t* wb = p.router + (size_t)(eok ? e0 + j : 0) * p.H + k0 + 32 * h;
+  f32x16 acc = zero16();
+  for (int kb = 0; kb < Kc; kb += 64) {
+    u32x4 a[4], b[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      a[t] = tok ? *(const u32x4*)(xa + kb + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+      b[t] = eok ? *(const u32x4*)(wb + kb + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) acc = mfma_bf16(a[t], b[t], acc);
+  }
+  // D rows 4 h + r (r < 4) are tokens 0..7, column j is expert e0 + j
+#pragma unroll
+  for (int r = 0; r < 4; r++) red[wave][lane][r] = acc[r];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float v = red[0][lane][r] + red[1][lane][r] + red[2][lane][r] + red[3][lane][r];
+    const int t = 4 * h + r, e = e0 + j;
+    if (t < p.T && e < p.E1) p.part[((size_t)ks * p.T + t) * p.E1 + e] = v;
+  }
+}
+
+// ---- 2. routing and the distinct-expert plan ---------------------------------------------------------------------
+__global__ __launch_bounds__(512) void k_mdec_plan(MdecArgs p) {
+  __shared__ int tidx[kMdecMaxT * kMdecMaxK], urank[kMdecMaxT * kMdecMaxK], firstpick[512], wcount[2];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int T = p.T, k = p.k, NU = T * k;
+  int* upick = p.plan + 1 + NU;
+  for (int i = tid; i < NU * 8; i += 512) upick[i] = -1;
+  for (int i = tid; i < p.E; i += 512) firstpick[i] = 0x7fffffff;
+  if (wave < T) {
+    // token t's logits, the K-split partials summed in split order: every load issued before the first add
+    const int t = wave;
+    float part[kMdecMaxKS][9];
+#pragma unroll
+    for (int z = 0; z < kMdecMaxKS; z++)
+#pragma unroll
+      for (int i = 0; i < 9; i++) {
+        const int c = i < 8 ? i * 64 + lane : p.E;  // slot 8: the shared expert's gate logit
+        part[z][i] = z < p.KS && c < p.E1 ? p.part[((size_t)z * T + t) * p.E1 + c] : 0.f;
+      }
+    float v[9];
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      v[i] = part[0][i];
+#pragma unroll
+      for (int z = 1; z < kMdecMaxKS; z++)
+        if (z < p.KS) v[i] += part[z][i];
+    }
+    if (p.logits) {
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (i * 64 + lane < p.E1) p.logits[(size_t)t * p.E1 + i * 64 + lane] = v[i];
+      if (p.shared_gate && lane == 0) p.logits[(size_t)t * p.E1 + p.E] = v[8];
+    }
+    const float gate = v[8];
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) r[i] = v[i];
+    int who[16];
+    float pw[16];
+    route_token(r, p.E, k, p.norm, who, pw);
+    if (lane == 0) {
+      for (int jj = 0; jj < k; jj++) {
+        tidx[t * k + jj] = who[jj];
+        p.idx[t * k + jj] = who[jj];
+        p.wt[t * k + jj] = pw[jj];
+      }
+      p.sg[t] = p.shared_gate ? 1.f / (1.f + expf(-gate)) : 1.f;
+    }
+  }
+  __syncthreads();
+  // The distinct experts in pick order, one thread per pick q (q < T k <= 128, waves 0 and 1): its expert's first
+  // pick (an LDS atomic min), then that first pick's rank among the first picks (ballot counts): the unique slot u.
+  if (tid < NU) atomicMin(&firstpick[tidx[tid]], tid);
+  __syncthreads();
+  const int f = tid < NU ? firstpick[tidx[tid]] : 0;
+  const bool first = tid < NU && f == tid;
+  int rank = 0;
+  if (wave < 2) {
+    const unsigned long long m = __ballot(first);
+    if (lane == 0) wcount[wave] = __popcll(m);
+    rank = __popcll(m & ((1ull << lane) - 1));
+  }
+  __syncthreads();
+  if (first) {
+    const int u = rank + (wave == 1 ? wcount[0] : 0);
+    urank[tid] = u;
+    p.plan[1 + u] = tidx[tid];
+  }
+  __syncthreads();
+  if (tid < NU) upick[urank[f] * 8 + tid / k] = tid % k;
+  if (tid == 0) p.plan[0] = wcount[0] + wcount[1];
+}
+
+// The slot of block row u: a distinct routed expert (u < nuniq), the shared expert (u == T k), or nothing.
+struct MdecSlot {
+  int e;       // expert, or -1 for the shared expert
+  bool live;
+};
+__device__ __forceinline__ MdecSlot mdec_slot(const MdecArgs& p, int u) {
+  const int NU = p.T * p.k;
+  if (u == NU) return MdecSlot{-1, p.sgu_wq != nullptr};
+  return MdecSlot{u < p.plan[0] ? p.plan[1 + u] : 0, u < p.plan[0]};
+}
+// token t's pick index of slot u (k for the shared expert), or -1
+__device__ __forceinline__ int mdec_pick(const MdecArgs& p, int u, int t) {
+  const int NU = p.T * p.k;
+  if (t >= p.T) return -1;
+  return u == NU ? p.k : p.plan[1 + NU + u * 8 + t];
+}
+
+// Stage rows [T][ng * 64] (row t from src(t), null = zeros) into LDS As (row stride lda) and their 64-group sums into
+// Xs[g][t] (8 per group). nthr threads starting at thread `first`; every 8 consecutive chunks are one group, so the
+// group sum is a reduction over 8 consecutive lanes.
+template <class Src>
+__device__ __forceinline__ void mdec_stage(Src src, int T, int ng, uint16_t* As, int lda, float* Xs, int first,
+                                           int nthr) {
+  const int cpr = ng * 8, total = T * cpr, me = (int)threadIdx.x - first;
+  for (int c0 = 0; c0 < total; c0 += nthr) {
+    const int c = c0 + me;
+    const bool ok = c < total;
+    const int t = ok ? c / cpr : 0, kc = ok ? c % cpr : 0;
+    const uint16_t* s = ok ? src(t) : nullptr;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (s) v = *(const u32x4*)(s + 8 * kc);
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) sum += bf2f((uint16_t)(v[e] & 0xFFFFu)) + bf2f((uint16_t)(v[e] >> 16));
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    if (ok) {
+      *(u32x4*)(As + (size_t)t * lda + 8 * kc) = v;
+      if ((kc & 7) == 0) Xs[(kc >> 3) * 8 + t] = sum;
+    }
+  }
+}
+
+// One wave's share of a qmv4-arithmetic product: 32 weight rows (wrow: the lane's row, offset 4 h words) over ng
+// groups starting at group g0 of the row, against the staged token rows As (row j of the MFMA A operand = token j,
+// zero past T). Adds s P + (b - 128 s) X of each group into acc[r] (rows 4 h + r, r < 4).
+struct MdecW {
+  const uint32_t* w;  // row words + 4 h
+  const uint16_t* s;  // row scales
+  const uint16_t* b;  // row biases
+};
+
+// ---- 3. gate/up + SwiGLU -------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
+  __shared__ __align__(16) uint16_t As[4][kMdecMaxT][kMdecKG * 64 + 8];
+  __shared__ float Xs[4][kMdecKG * 8];
+  __shared__ float red[4][64][8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
+  const int u = blockIdx.y, T = p.T, I = p.I, H = p.H, G = H / kGroup, Gw = G / 4;
+  const MdecSlot sl = mdec_slot(p, u);
+  if (!sl.live) return;  // block-uniform, before any barrier
+  const int n0 = blockIdx.x * 32;
+  const size_t rows0 = sl.e < 0 ? 0 : (size_t)sl.e * 2 * I;
+  const uint32_t* wq = sl.e < 0 ? p.sgu_wq : p.egu_wq;
+  const uint16_t* ws = sl.e < 0 ? p.sgu_s : p.egu_s;
+  const uint16_t* wb = sl.e < 0 ? p.sgu_b : p.egu_b;
+  const size_t rg = rows0 + n0 + j, ru = rg + I;
+  const MdecW Wg{wq + rg * (H / 8) + 4 * h, ws + rg * G, wb + rg * G};
+  const MdecW Wu{wq + ru * (H / 8) + 4 * h, ws + ru * G, wb + ru * G};
+  const bool aok = j < T;
+
+  float ag[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < Gw; c0 += kMdecKG) {
+    const int gb = wave * Gw + c0, ng = min(kMdecKG, Gw - c0);
+    // every load of the chunk first (clamped re-reads past ng keep the count fixed), then the token rows
+    u32x4 cg[kMdecKG], cu[kMdecKG];
+    uint16_t sgr[kMdecKG], bgr[kMdecKG], sur[kMdecKG], bur[kMdecKG];
+#pragma unroll
+    for (int i = 0; i < kMdecKG; i++) {
+      const int g = gb + min(i, ng - 1);
+      cg[i] = *(const u32x4*)(Wg.w + (size_t)g * 8);
+      cu[i] = *(const u32x4*)(Wu.w + (size_t)g * 8);
+    }
+    if (p.sb16_gu) {  // whole chunks of 8 groups at 16-byte aligned offsets (block-uniform)
+      load8h(Wg.s + gb, sgr), load8h(Wg.b + gb, bgr), load8h(Wu.s + gb, sur), load8h(Wu.b + gb, bur);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMdecKG; i++) {
+        const int g = gb + min(i, ng - 1);
+        sgr[i] = Wg.s[g], bgr[i] = Wg.b[g], sur[i] = Wu.s[g], bur[i] = Wu.b[g];
+      }
+    }
+    if (c0 > 0) __syncthreads();  // the previous chunk's reads of As are done (every wave runs the same chunks)
+    mdec_stage([&](int t) { return p.x + (size_t)t * H + (size_t)gb * 64; }, T, ng, &As[wave][0][0],
+               kMdecKG * 64 + 8, Xs[wave], wave * 64, 64);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kMdecKG; i++) {
+      if (i >= ng) break;
+      f32x16 Pg = zero16(), Pu = zero16();
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const u32x4 af = aok ? *(const u32x4*)(&As[wave][j][64 * i + GroupCodes<4>::kofs(t, h)]) : u32x4{0u, 0u, 0u, 0u};
+        Pg = mfma_bf16(af, codes_bf16_off128(cg[i][t]), Pg);
+        Pu = mfma_bf16(af, codes_bf16_off128(cu[i][t]), Pu);
+      }
+      const float sgf = bf2f(sgr[i]), bgf = __builtin_fmaf(-128.f, sgf, bf2f(bgr[i]));
+      const float suf = bf2f(sur[i]), buf = __builtin_fmaf(-128.f, suf, bf2f(bur[i]));
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float X = Xs[wave][i * 8 + 4 * h + r];
+        ag[r] = __builtin_fmaf(sgf, Pg[r], __builtin_fmaf(bgf, X, ag[r]));
+        au[r] = __builtin_fmaf(suf, Pu[r], __builtin_fmaf(buf, X, au[r]));
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) red[wave][lane][r] = ag[r], red[wave][lane][4 + r] = au[r];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int t = 4 * h + r, pk = mdec_pick(p, u, t);
+    if (pk < 0) continue;
+    const float g = red[0][lane][r] + red[1][lane][r] + red[2][lane][r] + red[3][lane][r];
+    const float v = red[0][lane][4 + r] + red[1][lane][4 + r] + red[2][lane][4 + r] + red[3][lane][4 + r];
+    p.act[((size_t)t * (p.k + 1) + pk) * I + n0 + j] = f2bf(swiglu_f(bf2f(f2bf(g)), bf2f(f2bf(v))));
+  }
+}
+
+// ---- 4. down + combine ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
+  extern __shared__ __align__(16) uint16_t lds[];  // As [T][I + 8], then Xs [I / 64][8]
+  __shared__ unsigned s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
+  const int u = blockIdx.y, T = p.T, I = p.I, H = p.H, Gi = I / kGroup, k = p.k;
+  const MdecSlot sl = mdec_slot(p, u);
+  if (!sl.live) return;  // block-uniform, before any barrier
+  const int lda = I + 8;
+  uint16_t* As = lds;
+  float* Xs = (float*)(lds + (size_t)T * lda + 8);  // 16-byte aligned: T lda + 8 is a multiple of 8
+  const int h0 = blockIdx.x * 128 + wave * 32;
+  const size_t row = (sl.e < 0 ? 0 : (size_t)sl.e * H) + h0 + j;
+  const uint32_t* wq = (sl.e < 0 ? p.sdn_wq : p.edn_wq) + row * (I / 8) + 4 * h;
+  const uint16_t* ws = (sl.e < 0 ? p.sdn_s : p.edn_s) + row * Gi;
+  const uint16_t* wb = (sl.e < 0 ? p.sdn_b : p.edn_b) + row * Gi;
+  const bool aok = j < T;
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < Gi; c0 += kMdecKG) {
+    const int ng = min(kMdecKG, Gi - c0);
+    u32x4 cw[kMdecKG];
+    uint16_t sr[kMdecKG], br[kMdecKG];
+#pragma unroll
+    for (int i = 0; i < kMdecKG; i++) {
+      const int g = c0 + min(i, ng - 1);
+      cw[i] = *(const u32x4*)(wq + (size_t)g * 8);
+    }
+    if (p.sb16_dn) {
+      load8h(ws + c0, sr), load8h(wb + c0, br);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMdecKG; i++) {
+        const int g = c0 + min(i, ng - 1);
+        sr[i] = ws[g], br[i] = wb[g];
+      }
+    }
+    if (c0 == 0) {  // the activation rows of the tokens that picked this slot (zero rows for the others)
+      mdec_stage(
+          [&](int t) -> const uint16_t* {
+            const int pk = mdec_pick(p, u, t);
+            return pk < 0 ? nullptr : p.act + ((size_t)t * (k + 1) + pk) * I;
+          },
+          T, Gi, As, lda, Xs, 0, 256);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kMdecKG; i++) {
+      if (i >= ng) break;
+      const int g = c0 + i;
+      f32x16 P = zero16();
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const u32x4 af = aok ? *(const u32x4*)(As + (size_t)j * lda + 64 * g + GroupCodes<4>::kofs(t, h))
+                             : u32x4{0u, 0u, 0u, 0u};
+        P = mfma_bf16(af, codes_bf16_off128(cw[i][t]), P);
+      }
+      const float sf = bf2f(sr[i]), bf = __builtin_fmaf(-128.f, sf, bf2f(br[i]));
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(sf, P[r], __builtin_fmaf(bf, Xs[g * 8 + 4 * h + r], acc[r]));
+    }
+  }
+  // d[t][pick][h] = bf16(result), written through for the combining block
+  const __amdgpu_buffer_rsrc_t rd = part_rsrc(p.d, p.d_bytes);
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int t = 4 * h + r, pk = mdec_pick(p, u, t);
+    if (pk >= 0)
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(acc[r]), rd, (int)((((size_t)t * (k + 1) + pk) * H + h0 + j) * 2), 0,
+                                            kSc1);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned arrivals = (unsigned)p.plan[0] + (p.sgu_wq ? 1u : 0u);
+    const unsigned old = __hip_atomic_fetch_add(p.cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1 == arrivals;
+    if (last) __hip_atomic_store(p.cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // the chunk's combine: every (token, column) of its 128 columns
+  const int nj = k + (p.sgu_wq ? 1 : 0);
+  for (int i = tid; i < T * 128; i += 256) {
+    const int t = i >> 7, hc = blockIdx.x * 128 + (i & 127);
+    // every slot's value and weight requested before the first is used, then summed in slot order
+    uint16_t dv[kMdecMaxK + 1];
+    float wv[kMdecMaxK + 1];
+#pragma unroll
+    for (int jj = 0; jj <= kMdecMaxK; jj++)
+      if (jj < nj) {
+        dv[jj] = __builtin_amdgcn_raw_buffer_load_b16(rd, (int)((((size_t)t * (k + 1) + jj) * H + hc) * 2), 0, kSc1);
+        wv[jj] = jj < k ? p.wt[t * k + jj] : p.sg[t];
+      }
+    float a = 0.f;
+#pragma unroll
+    for (int jj = 0; jj <= kMdecMaxK; jj++)
+      if (jj < nj) a = __builtin_fmaf(wv[jj], bf2f(dv[jj]), a);
+    uint16_t* o = p.out + (size_t)t * H + hc;
+    *o = p.assign ? f2bf(a) : f2bf(bf2f(*o) + bf2f(f2bf(a)));
+  }
+}
+
+// ---- host ------------------------------------------------------------------------------------------------------------
+static int mdec_ks(int H) {
+  for (int ks : {4, 2, 1})
+    if (H % (256 * ks) == 0 && H / (256 * ks) >= 1 && ks * 512 <= H) return ks;
+  return 1;
+}
+
+MdecLayout mdec_layout(int T, int H, int I, int E, int k) {
+  MdecLayout L{};
+  auto take = [&](size_t& off, size_t bytes) {
+    off = L.total;
+    L.total = align_up(L.total + bytes, 256);
+  };
+  const int E1 = E + 1, KS = mdec_ks(H);
+  take(L.part, (size_t)KS * T * E1 * 4);
+  take(L.plan, (size_t)(1 + 9 * T * k) * 4);
+  take(L.act, (size_t)T * (k + 1) * I * 2);
+  take(L.d, (size_t)T * (k + 1) * H * 2);
+  take(L.idx, (size_t)T * k * 4);
+  take(L.wt, (size_t)T * k * 4);
+  take(L.sg, (size_t)T * 4);
+  return L;
+}
+
+int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (c.T == 0) return IFD_OK;
+  const MdecLayout L = mdec_layout(c.T, c.H, c.I, c.E, c.k);
+  if (!ws || ws_bytes < L.total || !cnt)
+    return fail(IFD_ERR_WORKSPACE, "moe_decode needs %zu bytes of workspace after the header, got %zu", L.total,
+                ws_bytes);
+  char* w = (char*)ws;
+  MdecArgs p{};
+  p.x = (const uint16_t*)c.xn;
+  p.router = (const uint16_t*)c.router;
+  p.T = c.T, p.H = c.H, p.E = c.E, p.E1 = c.E + (c.shared_gate ? 1 : 0), p.k = c.k, p.I = c.I;
+  p.norm = c.norm, p.shared_gate = c.shared_gate, p.assign = c.assign, p.KS = mdec_ks(c.H);
+  p.egu_wq = c.egu_wq, p.egu_s = c.egu_s, p.egu_b = c.egu_b;
+  p.edn_wq = c.edn_wq, p.edn_s = c.edn_s, p.edn_b = c.edn_b;
+  p.sgu_wq = c.sgu_wq, p.sgu_s = c.sgu_s, p.sgu_b = c.sgu_b;
+  p.sdn_wq = c.sdn_wq, p.sdn_s = c.sdn_s, p.sdn_b = c.sdn_b;
+  p.out = (uint16_t*)c.out;
+  p.idx = c.idx ? c.idx : (int*)(w + L.idx);
+  p.wt = c.wt ? c.wt : (float*)(w + L.wt);
+  p.sg = c.sg ? c.sg : (float*)(w + L.sg);
+  p.logits = c.logits;
+  p.part = (float*)(w + L.part);
+  p.plan = (int*)(w + L.plan);
+  p.act = (uint16_t*)(w + L.act);
+  p.d = (uint16_t*)(w + L.d);
+  p.d_bytes = (uint32_t)((size_t)c.T * (c.k + 1) * c.H * 2);
+  p.cnt = cnt;
+  // vector scale / bias loads: every chunk holds 8 groups (the wave's group count a multiple of 8) and rows start
+  // 16-byte aligned
+  const bool shared = c.sgu_wq != nullptr;
+  const int G = c.H / kGroup, Gi = c.I / kGroup;
+  p.sb16_gu = (G / 4) % 8 == 0 && aligned(c.egu_s, 16) && aligned(c.egu_b, 16) &&
+              (!shared || (aligned(c.sgu_s, 16) && aligned(c.sgu_b, 16)));
+  p.sb16_dn = Gi % 8 == 0 && aligned(c.edn_s, 16) && aligned(c.edn_b, 16) &&
+              (!shared || (aligned(c.sdn_s, 16) && aligned(c.sdn_b, 16)));
+  const int slots = c.T * c.k + 1;
+  hipLaunchKernelGGL(k_mdec_router, dim3((p.E1 + 31) / 32, p.KS), dim3(256), 0, st, p);
+  IFD_TRY(check_launch("moe_decode router"));
+  hipLaunchKernelGGL(k_mdec_plan, dim3(1), dim3(512), 0, st, p);
+  IFD_TRY(check_launch("moe_decode plan"));
+  hipLaunchKernelGGL(k_mdec_gu, dim3(c.I / 32, slots), dim3(256), 0, st, p);
+  IFD_TRY(check_launch("moe_decode gate_up"));
+  const size_t lds = ((size_t)c.T * (c.I + 8) + 8) * 2 + (size_t)(c.I / kGroup) * 8 * 4;
+  hipLaunchKernelGGL(k_mdec_dn, dim3(c.H / 128, slots), dim3(256), lds, st, p);
+  return check_launch("moe_decode down");
+}
+
+}  // namespace ifd

@@ -63,12 +63,13 @@ struct Enc {
   hipStream_t stream = nullptr;
 };
 
-// An MLX affine 4-bit group-64 linear [N, K]: wq uint32 [N][K/8], s/b bf16 [N][K/64] (rows ldk long in a K-slice).
+// An MLX affine group-64 linear [N, K], 4 or 8 bits: wq uint32 [N][K bits/32], s/b bf16 [N][K/64] (rows ldk long in a
+// K-slice).
 struct QLinear {
   BufRef wq, s, b;
   BufRef t64;            // optional T64 copy (ifd_pack_t64), read by gemm() when present
   int ldk = 0;           // a K-slice view: the full matrix's row length; 0 = K
-  bool flipped = false;  // nibbles stored q ^ 8 (ifd_flip_w4); readers flip back
+  bool flipped = false;  // codes stored q ^ 8 (4 bits) or q ^ 0x80 (8 bits) (ifd_flip_w4); readers flip back
   int N = 0, K = 0, bits = 4;
 };
 
@@ -79,7 +80,7 @@ inline QLinear rows_of(const QLinear& q, int lo, int n) {
   r.t64 = BufRef();
   r.N = n;
   const size_t ld = q.ldk ? q.ldk : q.K;
-  r.wq = q.wq.at((size_t)lo * ld / 2);
+  r.wq = q.wq.at((size_t)lo * ld * q.bits / 8);
   r.s = q.s.at((size_t)lo * (ld / 64) * 2);
   r.b = q.b.at((size_t)lo * (ld / 64) * 2);
   return r;
@@ -91,7 +92,7 @@ inline QLinear kslice_of(const QLinear& q, int k0, int kn) {
   QLinear r = q;
   r.ldk = q.ldk ? q.ldk : q.K;
   r.K = kn;
-  r.wq = q.wq.at((size_t)k0 / 2);
+  r.wq = q.wq.at((size_t)k0 * q.bits / 8);
   r.s = q.s.at((size_t)k0 / 64 * 2);
   r.b = q.b.at((size_t)k0 / 64 * 2);
   if (q.t64 && k0 % 256 == 0 && kn % 256 == 0)
@@ -201,8 +202,17 @@ struct Qwen35 {
   // K), C [M][N] (row stride N).
   void gemm(Enc& e, const BufRef& A, const QLinear& W, const BufRef& C, int M, int mode, bool defer = false) {
     (void)defer;
+    if (W.bits == 8) {  // the reference's qmv8 / 8-bit qmm routes (qwen35.h:1520-1558)
+      const size_t need = ifd_gemm_w8_workspace(M, W.N, W.K);
+      if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
+      ok(ifd_gemm_w8(A.ptr<void>(), W.K, W.wq.ptr<uint32_t>(), W.s.ptr<uint16_t>(), W.b.ptr<uint16_t>(), W.N, W.K,
+                     W.ldk, W.flipped ? 0x80808080u : 0u, C.ptr<void>(), W.N, M, mode, splitk.ptr<void>(),
+                     splitk_bytes, e.stream),
+         "gemm");
+      return;
+    }
     if (W.bits != 4) {
-      fprintf(stderr, "gemm: %d-bit weights are outside this path (4-bit affine only)\n", W.bits);
+      fprintf(stderr, "gemm: %d-bit weights are outside this path (4- and 8-bit affine only)\n", W.bits);
       exit(1);
     }
     if (W.t64 && W.K % 256 == 0) {

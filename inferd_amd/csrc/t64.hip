@@ -83,13 +83,6 @@ __device__ __forceinline__ u32x4 t64_bf16_off128(uint32_t w) {
   return r;
 }
 
-// Device-coherent (sc1) buffer accesses to the partials, which blocks on different XCDs (separate L2s) exchange:
-// stores write through to memory, loads do not hit a stale line of the local L2. Plain loads batch, unlike atomic
-// loads, which the compiler orders one after another.
-constexpr int kSc1 = 16;  // cache-policy operand: SC1
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const float* part, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, (int)bytes, 0x00020000);
-}
 
 template <int RACT>
 __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {

@@ -308,3 +308,30 @@ def moe_ffn(xn: torch.Tensor, router: torch.Tensor, egu: MoeW, edn: MoeW, k: int
         _p(sdn.wq) if sdn else None, _p(sdn.s) if sdn else None, _p(sdn.b) if sdn else None, Is,
         _p(out), 1 if assign else 0, _p(idx), _p(wt), _p(sg), _p(ws), ws.numel(), _stream()))
     return out, idx, wt, sg
+
+
+def moe_decode(xn: torch.Tensor, router: torch.Tensor, egu: MoeW, edn: MoeW, k: int,
+               shared: Optional[tuple] = None, shared_gate: bool = True, norm: bool = True,
+               out: Optional[torch.Tensor] = None, assign: bool = True):
+    """Decode MoE for T <= 8 tokens (reference moe_plan / moe_gu2 / moe_dn2): each distinct expert read once.
+    shared = (QLinear gate_up [2I, H], QLinear down [H, I]) with the routed experts' I.
+
+    Returns (out, idx, wt, sg, logits)."""
+    T, H = xn.shape
+    E, I = egu.E, egu.N // 2
+    dev = xn.device
+    if out is None:
+        out = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    wt = torch.empty((T, k), dtype=torch.float32, device=dev)
+    sg = torch.empty((T,), dtype=torch.float32, device=dev)
+    logits = torch.empty((T, E + (1 if shared_gate else 0)), dtype=torch.float32, device=dev)
+    ws = workspace(lib().ifd_moe_decode_workspace(T, H, I, E, k), dev)
+    sgu, sdn = shared if shared is not None else (None, None)
+    check(lib().ifd_moe_decode(
+        _p(xn), T, H, _p(router), E, k, 1 if norm else 0, 1 if shared_gate else 0,
+        _p(egu.wq), _p(egu.s), _p(egu.b), _p(edn.wq), _p(edn.s), _p(edn.b), I,
+        _p(sgu.wq) if sgu else None, _p(sgu.s) if sgu else None, _p(sgu.b) if sgu else None,
+        _p(sdn.wq) if sdn else None, _p(sdn.s) if sdn else None, _p(sdn.b) if sdn else None,
+        _p(out), 1 if assign else 0, _p(idx), _p(wt), _p(sg), _p(logits), _p(ws), ws.numel(), _stream()))
+    return out, idx, wt, sg, logits

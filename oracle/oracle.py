@@ -56,6 +56,9 @@ def lib():
         L.orc_pack_w8.argtypes = [_u8p, _u32p, _i, _i]
         L.orc_unpack_w8.argtypes = [_u32p, _u8p, _i, _i, _u]
         L.orc_dequant_f32_b.argtypes = [_u32p, _u16p, _u16p, _i, _i, _i, _u, _f32p]
+        L.orc_moe_decode.argtypes = [_u16p, _i, _i, _i, _i, _i32p, _f32p, _f32p,
+                                     _u32p, _u16p, _u16p, _u32p, _u16p, _u16p,
+                                     _vp, _vp, _vp, _vp, _vp, _vp, _u16p, _i]
         L.orc_store.argtypes = [_f32p, _vp, _i, _i, _i, _i]
         L.orc_a8_quant.argtypes = [_u16p, _i, _i, _i, _i, _i8p, _f32p]
         L.orc_w4a8.argtypes = [_i8p, _f32p, _u32p, _u16p, _u16p, _i, _i, _u, _f32p, _i, _i]
@@ -400,3 +403,32 @@ def quantize_affine(w_bf16, bits: int):
     r = np.trunc(v64 + np.copysign(0.5, v64))  # std::round: half away from zero (exact in float64)
     codes = np.clip(r, 0, float(levels)).astype(np.uint32).reshape(N, K)
     return pack_affine(codes, bits), sb, bb, codes
+
+
+def moe_decode(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: bool = True) -> np.ndarray:
+    """Decode MoE for T <= 8 tokens (engine/kernels/moe.metal:326-551): per token and pick the decode GEMV arithmetic
+    for gate/up and down, SwiGLU, bf16 expert outputs, weighted combine (plus sg * the shared expert).
+    egu / edn: (wq, s, b) stacks [E, 2I, H/8] and [E, H, I/8]; shared = ((gu), (dn)) or None."""
+    xn = _c(xn, np.uint16)
+    T, H = xn.shape
+    idx = _c(idx, np.int32)
+    k = idx.shape[1]
+    o = np.zeros((T, H), np.uint16) if out is None else _c(out, np.uint16).copy()
+    keep = []
+
+    def p(a, dt):
+        a = _c(a, dt)
+        keep.append(a)
+        return a.ctypes.data
+
+    if shared is not None:
+        (sgw, sgs, sgb), (sdw, sds, sdb) = shared
+        sh = [p(sgw, np.uint32), p(sgs, np.uint16), p(sgb, np.uint16), p(sdw, np.uint32), p(sds, np.uint16),
+              p(sdb, np.uint16)]
+    else:
+        sh = [None] * 6
+    lib().orc_moe_decode(xn, T, H, I, k, idx, _c(wt, np.float32), _c(sg, np.float32),
+                         _c(egu[0], np.uint32), _c(egu[1], np.uint16), _c(egu[2], np.uint16),
+                         _c(edn[0], np.uint32), _c(edn[1], np.uint16), _c(edn[2], np.uint16), *sh, o,
+                         1 if assign else 0)
+    return o

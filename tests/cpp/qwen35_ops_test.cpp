@@ -3,7 +3,7 @@
 // layer from a fixed seed, run the operator, compare with the host reference, print one line per case.
 //
 //   qwen35_ops_test             every GPU case; exit 0 when all pass
-//   qwen35_ops_test --bad-bits  gemm() on an 8-bit QLinear: must print its error and exit(1) (no GPU needed)
+//   qwen35_ops_test --bad-bits  gemm() on a 16-bit QLinear: must print its error and exit(1) (no GPU needed)
 //   qwen35_ops_test --ckpt DIR  the device loaders (ckpt_dev.h) on a checkpoint written by tests/test_shim.py:
 //                               uploads bit-identical to the host loader, and gemm() on the loaded layer
 //
@@ -20,6 +20,11 @@
 
 extern "C" {
 void orc_pack_w4(const uint8_t* codes, uint32_t* wq, int N, int K);
+void orc_pack_w8(const uint8_t* codes, uint32_t* wq, int N, int K);
+void orc_qmv_b(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+               int bits, uint32_t xr, float* Y, int M, int nthreads);
+void orc_qmm_b(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+               int bits, uint32_t xr, float* Y, int M, int nthreads);
 void orc_flip(uint32_t* wq, int64_t n32, uint32_t mask);
 void orc_qmv(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
              uint32_t xr, float* Y, int M, int nthreads);
@@ -239,6 +244,44 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
     (void)hipFree(dA.buf), (void)hipFree(dC.buf);
   }
   (void)hipFree(W.wq.buf), (void)hipFree(W.s.buf), (void)hipFree(W.b.buf);
+  // 8-bit weights (qmv8 arithmetic up to 32 rows, MLX 8-bit qmm above), flipped storage and a rows_of view
+  {
+    std::vector<uint8_t> codes((size_t)N * K);
+    std::uniform_int_distribution<int> q(0, 255);
+    for (auto& c : codes) c = (uint8_t)q(rng);
+    std::vector<uint32_t> wq8((size_t)N * K / 4);
+    orc_pack_w8(codes.data(), wq8.data(), N, K);
+    std::uniform_real_distribution<float> su(0.0003f, 0.0012f), bu(-0.1f, 0.1f);
+    std::vector<uint16_t> s8((size_t)N * K / 64), b8(s8.size());
+    for (size_t i = 0; i < s8.size(); i++) s8[i] = f2bf(su(rng)), b8[i] = f2bf(bu(rng));
+    std::vector<uint32_t> wq8f = wq8;
+    for (auto& w : wq8f) w ^= 0x80808080u;
+    for (bool flipped : {false, true}) {
+      QLinear W8;
+      W8.wq = upload(flipped ? wq8f : wq8), W8.s = upload(s8), W8.b = upload(b8);
+      W8.N = N, W8.K = K, W8.bits = 8, W8.flipped = flipped;
+      for (int M : {1, 33, 200}) {
+        const auto A = activations(M, K, rng);
+        std::vector<float> y((size_t)M * N);
+        (M <= 32 ? orc_qmv_b : orc_qmm_b)(A.data(), K, wq8.data(), s8.data(), b8.data(), N, K, 8, 0, y.data(), M, 0);
+        BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
+        m.gemm(e, dA, W8, dC, M, 0);
+        const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), y, false);
+        report(err <= 1e-2, std::string("gemm 8-bit") + (flipped ? " flipped" : "") + " M=" + std::to_string(M), err);
+        if (M == 1) {  // rows_of [128, 256) of the same layer
+          QLinear Wr = rows_of(W8, 128, 128);
+          BufRef dR = upload(std::vector<uint16_t>(128));
+          m.gemm(e, dA, Wr, dR, 1, 0);
+          std::vector<float> yr(y.begin() + 128, y.begin() + 256);
+          const double er = bf16_err(download<uint16_t>(dR, 128), yr, false);
+          report(er <= 1e-2, "gemm 8-bit rows_of [128, 256)", er);
+          (void)hipFree(dR.buf);
+        }
+        (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+      }
+      (void)hipFree(W8.wq.buf), (void)hipFree(W8.s.buf), (void)hipFree(W8.b.buf);
+    }
+  }
 }
 
 void test_encode_moe(std::mt19937& rng) {
@@ -366,9 +409,9 @@ int main(int argc, char** argv) {
     Qwen35 m(c, 0, 0, 0);  // no state, no GPU call
     Enc e;
     QLinear W;
-    W.bits = 8, W.N = 64, W.K = 64;
+    W.bits = 16, W.N = 64, W.K = 64;
     m.gemm(e, BufRef(), W, BufRef(), 1, 0);
-    printf("gemm returned for an 8-bit linear\n");
+    printf("gemm returned for a 16-bit linear\n");
     return 0;
   }
   std::mt19937 rng(20251201);

@@ -165,3 +165,56 @@ def test_moe_ffn_t2048():
 
 def test_moe_ffn_small_odd():
     _ffn_case(5, 8, 128, 64, 2, True, seed=95)
+
+
+# ---- decode MoE (T <= 8): router, routing + plan, gate/up + SwiGLU, down + combine -----------------------------------
+def _decode_case(T, E, H, I, k, shared, shared_gate, seed, assign=True):
+    g, ops = _gu(), _ops()
+    egu = experts(E, 2 * I, H, seed=seed)
+    edn = experts(E, H, I, seed=seed + 1)
+    sgu = experts(1, 2 * I, H, seed=seed + 2)
+    sdn = experts(1, H, I, seed=seed + 3)
+    R = router(E + (1 if shared_gate else 0), H, seed=seed + 4)
+    xn = gen.activations(T, H, seed=seed + 5)
+    x0 = gen.activations(T, H, seed=seed + 6)
+    sh = (g.qlinear(sgu[0][0], sgu[1][0], sgu[2][0]), g.qlinear(sdn[0][0], sdn[1][0], sdn[2][0])) if shared else None
+    outs = []
+    for _ in range(2):  # a second call on the same workspace: the combine counters were left at zero
+        out, idx, wt, sg, logits = ops.moe_decode(g.dev(xn), g.dev(R), g.moew(*egu), g.moew(*edn), k, shared=sh,
+                                                  shared_gate=shared_gate, out=g.dev(x0), assign=assign)
+        torch.cuda.synchronize()
+        outs.append(g.host(out))
+    assert np.array_equal(outs[0], outs[1])
+    # logits within tolerance of the oracle's router GEMM; routing bit-exact on the GPU's own logits
+    lg = g.host(logits)
+    assert gen.rel_err(lg, orc.gemm_bf16(xn, R)) < 1e-4
+    ri, rw, rs = orc.moe_route(lg, E, k, shared_gate=shared_gate)
+    assert np.array_equal(g.host(idx), ri)
+    assert np.allclose(g.host(wt), rw, rtol=1e-5, atol=1e-7)
+    assert np.allclose(g.host(sg), rs, rtol=1e-5)
+    shw = ((sgu[0][0], sgu[1][0], sgu[2][0]), (sdn[0][0], sdn[1][0], sdn[2][0])) if shared else None
+    ref = orc.moe_decode(xn, ri, rw, rs, egu, edn, shw, I, out=x0, assign=assign)
+    got = outs[0]
+    err = gen.bf16_err(got, ref, ref_is_bf16=True)
+    r64 = gen.bf16_to_f32(ref).astype(np.float64)
+    rel_rms = np.sqrt(np.mean((gen.bf16_to_f32(got) - r64) ** 2) / np.mean(r64 ** 2))
+    assert err < 1e-2 and rel_rms < 1e-2, (T, err, rel_rms)
+    return ri
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 8])
+def test_moe_decode_baseline_geometry(T):
+    """BASELINE config 4's layer (H=2048, E=512, top-10, I=512, shared expert with its gate) at decode batch sizes."""
+    _decode_case(T, 512, 2048, 512, 10, True, True, seed=120 + T)
+
+
+@pytest.mark.parametrize("assign", [True, False])
+def test_moe_decode_shared_experts_across_tokens(assign):
+    """8 tokens over 8 experts, top-3: most experts are picked by several tokens (each read once for all of them)."""
+    ri = _decode_case(8, 8, 256, 128, 3, True, False, seed=140, assign=assign)
+    assert len(np.unique(ri)) < ri.size
+
+
+def test_moe_decode_no_shared_expert_long_k():
+    """No shared expert; I = 1152 (two K chunks of 8 groups in the down kernel), H = 4608 (gate/up chunks too), k = 16."""
+    _decode_case(3, 64, 4608, 1152, 16, False, False, seed=150)

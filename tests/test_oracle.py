@@ -482,3 +482,47 @@ def test_moe_experts_composition():
     # expert, weight or row would be an O(1) error
     assert gen.rel_err(got, ref) < 5e-2
     assert np.sqrt(np.mean((got - ref) ** 2) / np.mean(ref ** 2)) < 1e-2
+
+
+def test_moe_decode_composition():
+    """The decode MoE (T <= 8) equals routing-weighted per-token expert MLPs in float64 up to its bf16 rounding points,
+    and its residual form is bf16(x + its assign form) exactly."""
+    rng = np.random.default_rng(21)
+    E, H, I, T, k = 8, 128, 64, 5, 3
+    egu = [gen.qlinear(2 * I, H, seed=500 + e, bias="free") for e in range(E)]
+    edn = [gen.qlinear(H, I, seed=600 + e, bias="free") for e in range(E)]
+    sgu, sdn = gen.qlinear(2 * I, H, seed=700, bias="free"), gen.qlinear(H, I, seed=701, bias="free")
+    st = lambda L, i: np.stack([q[i] for q in L])
+    xn = gen.activations(T, H, seed=22)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    idx[1] = idx[0]  # two tokens with the same experts
+    wt = rng.uniform(0.1, 1, (T, k)).astype(np.float32)
+    wt /= wt.sum(axis=1, keepdims=True)
+    sg = rng.uniform(0, 1, T).astype(np.float32)
+    args = ((st(egu, 1), st(egu, 2), st(egu, 3)), (st(edn, 1), st(edn, 2), st(edn, 3)),
+            ((sgu[1], sgu[2], sgu[3]), (sdn[1], sdn[2], sdn[3])), I)
+    out = orc.moe_decode(xn, idx, wt, sg, *args)
+    x = gen.bf16_to_f32(xn).astype(np.float64)
+
+    def mlp(gu, dn, xr):
+        h = xr @ gen.dequant_f64(gu[0], gu[2], gu[3]).T
+        a = h[:, :I] / (1 + np.exp(-h[:, :I])) * h[:, I:]
+        return a @ gen.dequant_f64(dn[0], dn[2], dn[3]).T
+
+    ref = np.zeros((T, H))
+    for t in range(T):
+        for j in range(k):
+            ref[t] += wt[t, j] * mlp(egu[idx[t, j]], edn[idx[t, j]], x[t:t + 1])[0]
+        ref[t] += sg[t] * mlp(sgu, sdn, x[t:t + 1])[0]
+    got = gen.bf16_to_f32(out).astype(np.float64)
+    assert np.sqrt(np.mean((got - ref) ** 2) / np.mean(ref ** 2)) < 1e-2
+    assert np.array_equal(out[0], out[1]) == np.array_equal(xn[0], xn[1])
+    x0 = gen.activations(T, H, seed=23)
+    res = orc.moe_decode(xn, idx, wt, sg, *args, out=x0, assign=False)
+    want = gen.f32_to_bf16(gen.bf16_to_f32(x0) + gen.bf16_to_f32(out))
+    assert np.array_equal(res, want)
+    # without the shared expert the shared term is absent
+    no_sh = orc.moe_decode(xn, idx, wt, sg, args[0], args[1], None, I)
+    ref2 = ref - sg[:, None] * np.stack([mlp(sgu, sdn, x[t:t + 1])[0] for t in range(T)])
+    got2 = gen.bf16_to_f32(no_sh).astype(np.float64)
+    assert np.sqrt(np.mean((got2 - ref2) ** 2) / np.mean(ref2 ** 2)) < 1e-2

@@ -16,12 +16,12 @@ def _need_bin():
         pytest.skip("tests/cpp/qwen35_ops_test is not built (python tests/cpp/build.py)")
 
 
-def test_gemm_rejects_non_4bit_like_the_reference():
+def test_gemm_rejects_16bit_like_the_reference():
     """The reference prints the reason and exits with status 1 on a route it cannot take (qwen35.h:1469, 1477)."""
     _need_bin()
     r = subprocess.run([BIN, "--bad-bits"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
-    assert "8-bit weights are outside this path" in r.stderr
+    assert "16-bit weights are outside this path" in r.stderr
 
 
 @pytest.mark.gpu
