@@ -151,6 +151,14 @@ def main():
             ms_dn = timed(lambda i: ops.gemm_t64(Hh[M], layers[i % ncp][1], Y[M]), args.steps * 2, 3)
             calls[f"gate_up_swiglu_M{M}"] = (ms_gu, gu_b, 2.0 * M * 2 * I_DEC * H_DEC)
             calls[f"down_M{M}"] = (ms_dn, dn_b, 2.0 * M * H_DEC * I_DEC)
+        # the whole dense MLP block (rmsnorm, gate_up + SwiGLU, down with the residual add) as one operator
+        nw = (torch.rand((H_DEC,), device=dev, generator=gen) + 0.5).to(torch.bfloat16)
+        Xb = {M: act(M, H_DEC) for M in Ms}
+        mlp_block = {}
+        for M in Ms:
+            ms_b = timed(lambda i: ops.mlp_decode(Xb[M], nw, 1e-6, *layers[i % ncp]), args.steps * 2, 3)
+            mlp_block[f"M{M}"] = dict(us=ms_b * 1e3, gbs=(w_bytes + M * (4 * H_DEC + 2 * I_DEC) * 2) / (ms_b * 1e-3) / 1e9)
+        out["mlp_block"] = mlp_block
         dom = max(calls, key=lambda k: calls[k][0])
         ms_d, b_d, f_d = calls[dom]
         achieved = b_d / (ms_d * 1e-3) / 1e9
@@ -355,6 +363,7 @@ def main():
                        "weight_copies": h["copies"]},
             "roofline": roofline(d),
             "per_M": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in out["per_M"].items()},
+            "mlp_block": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in out["mlp_block"].items()},
         })
     if cpu:
         line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()}

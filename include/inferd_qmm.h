@@ -215,6 +215,15 @@ int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, 
                 const uint16_t* sdn_s, const uint16_t* sdn_b, int Is, void* out, int assign, int* idx, float* wt,
                 float* sg, void* workspace, size_t ws_bytes, void* stream);
 
+/* The dense decode MLP block on T64 weights (reference encode_layer's MLP, qwen35.h:2867-2892):
+ * x += down(SwiGLU(gate_up(rmsnorm(x, norm_w, eps)))) for M rows of x [M][ldx] (bf16, updated in place), through
+ * the same kernels as ifd_rmsnorm -> ifd_gemm_t64_swiglu -> ifd_gemm_t64 (mode 1) and bit-identical to that
+ * sequence; the normalised rows and the SwiGLU output stay in the workspace. gu_t64: [2 I][H] (gate rows, then up
+ * rows), dn_t64: [H][I], packed by ifd_pack_t64. H and I multiples of 256. Workspace: ifd_mlp_decode_workspace. */
+size_t ifd_mlp_decode_workspace(int M, int H, int I);
+int ifd_mlp_decode(void* x, int ldx, const void* norm_w, float eps, const void* gu_t64, const void* dn_t64, int M,
+                   int H, int I, void* workspace, size_t ws_bytes, void* stream);
+
 /* Decode MoE for T <= 8 tokens (reference moe_plan / moe_gu2 / moe_dn2 and their router, moe.metal:267-551; host
  * qwen35.h:1876-1908): router logits (fp32) -> routing -> the distinct experts of the step -> gate/up + SwiGLU ->
  * down + combine, four launches, each distinct expert's weights read once for all tokens that picked it. Every

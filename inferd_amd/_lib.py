@@ -56,6 +56,8 @@ SIGNATURES = {
     "ifd_moe_gather": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     "ifd_moe_gather_qmm": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
     "ifd_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "ifd_mlp_decode_workspace": (_sz, [_i, _i, _i]),
+    "ifd_mlp_decode": (_i, [_vp, _i, _vp, ctypes.c_float, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_moe_decode_workspace": (_sz, [_i, _i, _i, _i, _i]),
     "ifd_moe_decode": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i,
                             _vp, _vp, _vp, _vp, _vp, _vp, _i,

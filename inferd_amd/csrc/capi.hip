@@ -410,6 +410,46 @@ int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, 
   return launch_moe_combine((uint16_t*)out, (const uint16_t*)(w + L.edn), rwt, ys, rsg, inv, T, H, k, assign, st);
 }
 
+// ---- the dense decode MLP block -----------------------------------------------------------------------------------
+namespace {
+size_t mlp_gemm_scratch(int M, int H, int I) {
+  const size_t gu = M <= 16 ? qmv_t_workspace(M, 2 * I, H, kModeSwiglu) : gemm_t_workspace(M, 2 * I, H, kModeSwiglu);
+  const size_t dn = M <= 16 ? qmv_t_workspace(M, H, I, 1) : gemm_t_workspace(M, H, I, 1);
+  return align_up(std::max(gu, dn), 256);
+}
+}  // namespace
+
+size_t ifd_mlp_decode_workspace(int M, int H, int I) {
+  if (M <= 0 || H <= 0 || I <= 0) return 0;
+  return with_header(mlp_gemm_scratch(M, H, I) + align_up((size_t)M * H * 2, 256) + (size_t)M * I * 2);
+}
+
+int ifd_mlp_decode(void* x, int ldx, const void* norm_w, float eps, const void* gu_t64, const void* dn_t64, int M,
+                   int H, int I, void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(M >= 0 && H > 0 && H % 256 == 0 && I > 0 && I % 256 == 0, "bad shape M=%d H=%d I=%d (H, I multiples of 256)",
+            M, H, I);
+  IFD_CHECK(ldx >= H && ldx % 8 == 0, "bad stride ldx=%d", ldx);
+  IFD_CHECK(eps >= 0.f, "eps must be >= 0");
+  if (M == 0) return IFD_OK;
+  IFD_CHECK(x && norm_w && gu_t64 && dn_t64 && aligned(x, 16) && aligned(gu_t64, 16) && aligned(dn_t64, 16),
+            "null or misaligned pointer");
+  const size_t need = ifd_mlp_decode_workspace(M, H, I);
+  const WsView w = ws_view(workspace, ws_bytes);
+  if (!workspace || ws_bytes < need || !aligned(workspace, 16))
+    return fail(IFD_ERR_WORKSPACE, "mlp_decode needs %zu bytes of 16-byte aligned workspace, got %zu", need, ws_bytes);
+  hipStream_t st = S(stream);
+  const size_t G = mlp_gemm_scratch(M, H, I);
+  uint16_t* xn = (uint16_t*)((char*)w.body + G);
+  uint16_t* act = (uint16_t*)((char*)w.body + G + align_up((size_t)M * H * 2, 256));
+  IFD_TRY(launch_rmsnorm((const uint16_t*)x, ldx, (const uint16_t*)norm_w, xn, H, M, H, eps, st));
+  if (M <= 16) {
+    IFD_TRY(launch_qmv_t(xn, H, gu_t64, 2 * I, H, act, I, M, kModeSwiglu, w.cnt, w.body, G, st));
+    return launch_qmv_t(act, I, dn_t64, H, I, x, ldx, M, 1, w.cnt, w.body, G, st);
+  }
+  IFD_TRY(launch_gemm_t(xn, H, gu_t64, 2 * I, H, act, I, M, kModeSwiglu, w.body, G, st));
+  return launch_gemm_t(act, I, dn_t64, H, I, x, ldx, M, 1, w.body, G, st);
+}
+
 // ---- decode MoE (T <= 8) ---------------------------------------------------------------------------------------
 size_t ifd_moe_decode_workspace(int T, int H, int I, int E, int k) {
   if (T <= 0 || T > 8 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;

@@ -335,3 +335,14 @@ def moe_decode(xn: torch.Tensor, router: torch.Tensor, egu: MoeW, edn: MoeW, k: 
         _p(sdn.wq) if sdn else None, _p(sdn.s) if sdn else None, _p(sdn.b) if sdn else None,
         _p(out), 1 if assign else 0, _p(idx), _p(wt), _p(sg), _p(logits), _p(ws), ws.numel(), _stream()))
     return out, idx, wt, sg, logits
+
+
+def mlp_decode(x: torch.Tensor, norm_w: torch.Tensor, eps: float, gu: T64Linear, dn: T64Linear) -> torch.Tensor:
+    """The dense decode MLP block in place: x += down(SwiGLU(gate_up(rmsnorm(x)))) (T64 weights)."""
+    M, H = x.shape
+    I = dn.K
+    assert gu.N == 2 * I and gu.K == H and dn.N == H and x.is_contiguous()
+    ws = workspace(lib().ifd_mlp_decode_workspace(M, H, I), x.device)
+    check(lib().ifd_mlp_decode(_p(x), H, _p(norm_w), eps, _p(gu.wt), _p(dn.wt), M, H, I, _p(ws), ws.numel(),
+                               _stream()))
+    return x

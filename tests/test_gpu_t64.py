@@ -330,3 +330,46 @@ def test_gemm_t64_swiglu_prefill_tiles():
     A = g.dev(gen.activations(M, K, seed=84))
     T = ops.pack_t64(g.qlinear(wq, s, b))
     assert np.array_equal(g.host(ops.gemm_t64_swiglu(A, T)), g.host(ops.silu_mul(ops.gemm_t64(A, T))))
+
+
+# ---- the dense decode MLP block -----------------------------------------------------------------------------------
+@pytest.mark.parametrize("M", [1, 8, 32, 128])
+def test_mlp_decode_matches_its_sequence_at_config1(M):
+    """BASELINE config 1's layer (H = 5120, I = 17408): the fused block is bit-identical to rmsnorm ->
+    gemm_t64_swiglu -> gemm_t64 (mode 1) on the same inputs."""
+    g, ops = _gu(), _ops()
+    H, I = 5120, 17408
+    _, wg, sg_, bg = gen.qlinear(2 * I, H, seed=700 + M)
+    _, wd, sd, bd = gen.qlinear(H, I, seed=800 + M)
+    GU, DN = ops.pack_t64(g.qlinear(wg, sg_, bg)), ops.pack_t64(g.qlinear(wd, sd, bd))
+    x0 = gen.activations(M, H, seed=900 + M)
+    nw = gen.f32_to_bf16(np.random.default_rng(M).uniform(0.5, 1.5, H).astype(np.float32))
+    x = g.dev(x0)
+    ops.mlp_decode(x, g.dev(nw), 1e-6, GU, DN)
+    xs = g.dev(x0)
+    h = ops.gemm_t64_swiglu(ops.rmsnorm(xs, g.dev(nw), 1e-6), GU)
+    ops.gemm_t64(h, DN, xs, mode=1)
+    torch.cuda.synchronize()
+    assert np.array_equal(g.host(x), g.host(xs))
+
+
+@pytest.mark.parametrize("M", [1, 9, 40, 128])
+def test_mlp_decode_matches_oracle(M):
+    """x += down(SwiGLU(gate_up(rmsnorm(x)))) against the oracle's composition. At these shapes (too few column tiles
+    for the stream-K kernel) the T64 GEMMs keep the decode GEMV's affine arithmetic up to 64 rows (32- and 64-row
+    tiles) and dequantize above; two chained GEMMs would compound the difference between the two forms."""
+    g, ops = _gu(), _ops()
+    H, I = 1024, 2048
+    _, wg, sg_, bg = gen.qlinear(2 * I, H, seed=710 + M)
+    _, wd, sd, bd = gen.qlinear(H, I, seed=810 + M)
+    GU, DN = ops.pack_t64(g.qlinear(wg, sg_, bg)), ops.pack_t64(g.qlinear(wd, sd, bd))
+    x0 = gen.activations(M, H, seed=910 + M)
+    nw = gen.f32_to_bf16(np.random.default_rng(M).uniform(0.5, 1.5, H).astype(np.float32))
+    x = g.dev(x0)
+    ops.mlp_decode(x, g.dev(nw), 1e-6, GU, DN)
+    xn = orc.rmsnorm(x0, nw, 1e-6)
+    sem = orc.qmv if M <= 64 else orc.qmm
+    h = orc.silu_mul(gen.f32_to_bf16(sem(xn, wg, sg_, bg)))
+    y = sem(h, wd, sd, bd)
+    err = gen.bf16_err(g.host(x), y + gen.bf16_to_f32(x0))
+    assert err <= 1e-2, (M, err)
