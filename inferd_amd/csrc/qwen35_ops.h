@@ -143,6 +143,7 @@ struct Qwen35 {
     size_t need = gemm_scratch;
     if (max_rows > 0 && E > 0) {
       need = std::max(need, ifd_moe_dispatch_workspace(R, E));
+      need = std::max(need, ifd_moe_decode_workspace(std::min(max_rows, 8), H, I, E, k));
       if (shared_inter > 0) {
         need = std::max(need, ifd_gemm_w4_workspace(max_rows, 2 * shared_inter, H));
         need = std::max(need, ifd_gemm_w4_workspace(max_rows, H, shared_inter));
@@ -246,6 +247,30 @@ struct Qwen35 {
     const int E1 = ly.router.E * ly.router.N;  // E, or E + 1 with the shared expert's gate row
     ok(ifd_rmsnorm(x.ptr<void>(), H, ly.post_norm.ptr<void>(), xn.ptr<void>(), H, T, H, cfg.eps, e.stream),
        "encode_moe");
+    // up to 8 tokens: the decode MoE (the reference's moe2 route, qwen35.h:1823-1829, 1876-1908), each distinct expert
+    // read once; it needs the shared expert (if any) unflipped 4-bit with the routed experts' intermediate size
+    const bool has_shared = ly.gate_up.N > 0;
+    const bool shared_fits = !has_shared || (ly.gate_up.bits == 4 && ly.down.bits == 4 && ly.gate_up.N == 2 * I &&
+                                             ly.gate_up.K == H && ly.down.N == H && ly.down.K == I &&
+                                             !ly.gate_up.flipped && !ly.down.flipped && !ly.gate_up.ldk &&
+                                             !ly.down.ldk);
+    if (T <= 8 && k <= 16 && E <= 512 && H % 256 == 0 && I % 64 == 0 && E1 <= E + 1 && shared_fits) {
+      const size_t need = ifd_moe_decode_workspace(T, H, I, E, k);
+      if (need > splitk_bytes) die("encode_moe", "scratch smaller than the decode MoE needs");
+      ok(ifd_moe_decode(xn.ptr<void>(), T, H, ly.router.wq.ptr<void>(), E, k, 1, E1 > E ? 1 : 0,
+                        ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(), ly.egu.b.ptr<uint16_t>(),
+                        ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(), ly.edown.b.ptr<uint16_t>(), I,
+                        has_shared ? ly.gate_up.wq.ptr<uint32_t>() : nullptr,
+                        has_shared ? ly.gate_up.s.ptr<uint16_t>() : nullptr,
+                        has_shared ? ly.gate_up.b.ptr<uint16_t>() : nullptr,
+                        has_shared ? ly.down.wq.ptr<uint32_t>() : nullptr,
+                        has_shared ? ly.down.s.ptr<uint16_t>() : nullptr,
+                        has_shared ? ly.down.b.ptr<uint16_t>() : nullptr, x.ptr<void>(), 0, ridx.ptr<int>(),
+                        rw.ptr<float>(), rsg.ptr<float>(), rlog.ptr<float>(), splitk.ptr<void>(), splitk_bytes,
+                        e.stream),
+         "encode_moe");
+      return;
+    }
     // shared expert -> sh_out
     const bool shared = ly.gate_up.N > 0;
     if (shared) {

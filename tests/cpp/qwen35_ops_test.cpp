@@ -21,6 +21,11 @@
 extern "C" {
 void orc_pack_w4(const uint8_t* codes, uint32_t* wq, int N, int K);
 void orc_pack_w8(const uint8_t* codes, uint32_t* wq, int N, int K);
+void orc_moe_decode(const uint16_t* xn, int T, int H, int I, int k, const int* idx, const float* wt, const float* sg,
+                    const uint32_t* gu_wq, const uint16_t* gu_s, const uint16_t* gu_b, const uint32_t* dn_wq,
+                    const uint16_t* dn_s, const uint16_t* dn_b, const uint32_t* sh_gu_wq, const uint16_t* sh_gu_s,
+                    const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq, const uint16_t* sh_dn_s, const uint16_t* sh_dn_b,
+                    uint16_t* out, int assign);
 void orc_qmv_b(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
                int bits, uint32_t xr, float* Y, int M, int nthreads);
 void orc_qmm_b(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
@@ -313,7 +318,7 @@ void test_encode_moe(std::mt19937& rng) {
                   0, 0, 1, sgu_t64, nullptr),
      "pack_t64");
   const QLinear sgu_mlx = ly.gate_up;
-  for (int T : {16, 100, -16, -100}) {
+  for (int T : {3, 8, 16, 100, -16, -100}) {
     ly.gate_up = sgu_mlx;
     if (T < 0) ly.gate_up.t64 = BufRef(sgu_t64), T = -T;
     Qwen35 m(c, T, Is, 0);
@@ -345,9 +350,14 @@ void test_encode_moe(std::mt19937& rng) {
     report(ri == idx && ew <= 1e-5, "encode_moe routing (indices bit-exact)" + tag, ew);
     // the block's output added into x, from the GPU's normalised rows and routing
     std::vector<uint16_t> want = x0;
-    orc_moe_experts(xn.data(), T, H, I, E, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
-                    egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu.wq.data(), sgu.s.data(), sgu.b.data(),
-                    sdn.wq.data(), sdn.s.data(), sdn.b.data(), T <= 32 ? 1 : 0, want.data(), 0, 0);
+    if (T <= 8)  // the decode MoE route: the decode GEMV arithmetic for every expert product
+      orc_moe_decode(xn.data(), T, H, I, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
+                     egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu.wq.data(), sgu.s.data(),
+                     sgu.b.data(), sdn.wq.data(), sdn.s.data(), sdn.b.data(), want.data(), 0);
+    else
+      orc_moe_experts(xn.data(), T, H, I, E, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
+                      egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu.wq.data(), sgu.s.data(),
+                      sgu.b.data(), sdn.wq.data(), sdn.s.data(), sdn.b.data(), T <= 32 ? 1 : 0, want.data(), 0, 0);
     std::vector<float> wf(want.size());
     for (size_t i = 0; i < want.size(); i++) wf[i] = bf2f(want[i]);
     const double ex = bf16_err(x1, wf, true);
