@@ -144,8 +144,12 @@ int ifd_gemm_t64_swiglu(const void* A, int lda, const void* wt, int N, int K, vo
 /* ---- W4A8 (reference a8_quant + w4a8_gemm, w4a8.metal:24-98; host w4a8, qwen35.h:1323-1366) ------------------ */
 
 /* Activation quantizer: U int8 [M][K], XS float [M][K/64][2] = (sx, sx * sum xq) per row and group.
- * per_token = 0: one scale per row and 64-group (the reference's a8_quant); 1: one scale per row (amax over K),
- * repeated in every group's XS entry. sx = amax / 127 (1 if amax == 0), xq = rint(x / sx). */
+ * per_token = 0: one scale per row and 64-group (the reference's a8_quant, w4a8.metal:24-41); 1: one scale per row
+ * (amax over K), repeated in every group's XS entry. sx = amax / 127 (1 if amax == 0), xq = rint(x / sx).
+ * per_token = 2: the int8 prefill's quantizer (reference qa8_quant, qa8.metal:30-49): per 64-group,
+ * xq = clamp(rint(x * (127 / amax)), -127, 127) (0 if amax == 0), sx = amax / 127; U in natural K order. With
+ * ifd_qmm_w4a8 (per_token = 0) it gives the reference's qa8 path (qa8_gemm, qa8.metal:52-210: the same per-group
+ * identity on unflipped codes). */
 int ifd_a8_quant(const void* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, void* stream);
 
 /* C (mode) = sum_g [ s sx P + b (sx sum xq) ], P = sum q xq over the group (exact int32); U, XS from

@@ -18,10 +18,13 @@
 namespace ifd {
 
 // ---- activation quantizer --------------------------------------------------------------------------------------
-// One block of 256 threads per row. per_token: amax over the row; else per 64-group. sx = amax / 127 (1 if 0),
+// One block of 256 threads per row. form 1: amax over the row; 0: per 64-group. sx = amax / 127 (1 if 0),
 // xq = rint(x / sx) (IEEE division and round-half-even: bit-identical to the CPU reference), XS = (sx, sx * sum xq).
-__global__ __launch_bounds__(256) void k_a8_quant(const uint16_t* __restrict__ A, int lda, int K, int per_token,
+// form 2 (the reference's qa8_quant, qa8.metal:30-49): per 64-group, xq = clamp(rint(x * (127 / amax)), +-127) (0
+// when amax == 0), XS = (amax / 127, amax / 127 * sum xq); stored in natural K order.
+__global__ __launch_bounds__(256) void k_a8_quant(const uint16_t* __restrict__ A, int lda, int K, int form,
                                                   int8_t* __restrict__ U, float* __restrict__ XS) {
+  const int per_token = form == 1;
   __shared__ float red[4];
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint16_t* a = A + (size_t)m * lda;
@@ -38,12 +41,19 @@ __global__ __launch_bounds__(256) void k_a8_quant(const uint16_t* __restrict__ A
   }
   for (int g = wave; g < G; g += 4) {
     const float x = bf2f(a[g * kGroup + lane]);
-    float sx = row_sx;
-    if (!per_token) {
+    float sx = row_sx, q;
+    if (form == 2) {
       const float amax = wave_max(fabsf(x));
-      sx = amax > 0.f ? amax / 127.f : 1.f;
+      const float inv = amax > 0.f ? 127.f / amax : 0.f;
+      q = fminf(fmaxf(rintf(x * inv), -127.f), 127.f);
+      sx = amax / 127.f;
+    } else {
+      if (!per_token) {
+        const float amax = wave_max(fabsf(x));
+        sx = amax > 0.f ? amax / 127.f : 1.f;
+      }
+      q = rintf(x / sx);
     }
-    const float q = rintf(x / sx);
     U[(size_t)m * K + g * kGroup + lane] = (int8_t)q;
     const float qs = wave_sum(q);
     if (lane == 0) {
@@ -53,9 +63,9 @@ __global__ __launch_bounds__(256) void k_a8_quant(const uint16_t* __restrict__ A
   }
 }
 
-int launch_a8_quant(const uint16_t* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, hipStream_t st) {
+int launch_a8_quant(const uint16_t* A, int lda, int M, int K, int form, int8_t* U, float* XS, hipStream_t st) {
   if (M == 0) return IFD_OK;
-  hipLaunchKernelGGL(k_a8_quant, dim3(M), dim3(256), 0, st, A, lda, K, per_token, U, XS);
+  hipLaunchKernelGGL(k_a8_quant, dim3(M), dim3(256), 0, st, A, lda, K, form, U, XS);
   return check_launch("a8_quant");
 }
 

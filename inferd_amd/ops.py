@@ -203,11 +203,13 @@ def splitk_res_norm(part: torch.Tensor, x: torch.Tensor, w: torch.Tensor, eps: f
     return y if a8 is None else (y, U, XS)
 
 
-def a8_quant(A: torch.Tensor, per_token: bool):
+def a8_quant(A: torch.Tensor, per_token):
+    """int8 activations: per_token False (per 64-group), True (per row) or 2 (the int8 prefill's qa8 form)."""
     M, K = A.shape
     U = torch.empty((M, K), dtype=torch.int8, device=A.device)
     XS = torch.empty((M, K // 64, 2), dtype=torch.float32, device=A.device)
-    check(lib().ifd_a8_quant(_p(A), K, M, K, 1 if per_token else 0, _p(U), _p(XS), _stream()))
+    form = 2 if per_token == 2 else (1 if per_token else 0)
+    check(lib().ifd_a8_quant(_p(A), K, M, K, form, _p(U), _p(XS), _stream()))
     return U, XS
 
 

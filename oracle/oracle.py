@@ -200,13 +200,14 @@ def store(Y, mode: int, C=None) -> np.ndarray:
     return out
 
 
-def a8_quant(A, per_token: bool):
-    """a8_quant (engine/kernels/w4a8.metal:24-41); per_token: one amax per row."""
+def a8_quant(A, per_token):
+    """a8_quant (engine/kernels/w4a8.metal:24-41); per_token: one amax per row; per_token = 2: the int8 prefill's
+    qa8_quant form (qa8.metal:30-49)."""
     A = _c(A, np.uint16)
     M, K = A.shape
     U = np.empty((M, K), np.int8)
     XS = np.empty((M, K // 64, 2), np.float32)
-    lib().orc_a8_quant(A, K, M, K, 1 if per_token else 0, U, XS)
+    lib().orc_a8_quant(A, K, M, K, 2 if per_token == 2 else (1 if per_token else 0), U, XS)
     return U, XS
 
 

@@ -218,8 +218,28 @@ void orc_store(const float* Y, void* C, int ldc, int M, int N, int mode) {
 // Activation quantizer (engine/kernels/w4a8.metal:24-41): per row and 64-group, sx = amax/127 (1 if amax == 0),
 // xq = rint(x / sx) (no clamp), XS = (sx, sx * sum xq). per_token != 0: one amax over the whole row of K (the
 // per-token scale BASELINE config 3 asks for); XS still holds one (sx, sx * sum_g xq) pair per group.
+// per_token == 2: the int8 prefill's quantizer (engine/kernels/qa8.metal:30-49): per 64-group,
+// xq = clamp(rint(x * (127 / amax)), -127, 127) (inv = 0 when amax == 0), XS = (amax / 127, amax / 127 * sum xq).
 void orc_a8_quant(const uint16_t* A, int lda, int M, int K, int per_token, int8_t* U, float* XS) {
   const int kg = K / 64;
+  if (per_token == 2) {
+    for (int m = 0; m < M; m++)
+      for (int g = 0; g < kg; g++) {
+        const uint16_t* a = A + (size_t)m * lda + g * 64;
+        float amax = 0.f;
+        for (int k = 0; k < 64; k++) amax = std::max(amax, std::fabs(bf2f(a[k])));
+        const float inv = amax > 0.f ? 127.f / amax : 0.f;
+        float qs = 0.f;
+        for (int k = 0; k < 64; k++) {
+          const float q = std::min(std::max(std::rint(bf2f(a[k]) * inv), -127.f), 127.f);
+          U[(size_t)m * K + g * 64 + k] = (int8_t)q;
+          qs += q;
+        }
+        XS[((size_t)m * kg + g) * 2 + 0] = amax / 127.f;
+        XS[((size_t)m * kg + g) * 2 + 1] = amax / 127.f * qs;
+      }
+    return;
+  }
   for (int m = 0; m < M; m++) {
     const uint16_t* a = A + (size_t)m * lda;
     float row_amax = 0.f;

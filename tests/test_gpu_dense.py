@@ -252,3 +252,23 @@ def test_rmsnorm(R, D, eps):
     # the fp32 sum of squares runs in another order than the oracle's: within one bf16 step of its output
     assert gen.bf16_err(y, yr, ref_is_bf16=True) == 0.0
     assert np.mean(y == yr) > 0.98
+
+
+def test_qa8_quant_bit_exact_and_gemm():
+    """The int8 prefill path (reference qa8_quant + qa8_gemm, qa8.metal:30-210): the qa8 quantizer form is bit-exact,
+    and with the per-group W4A8 GEMM on unflipped and flipped weights it matches the oracle's identity."""
+    g, ops = _gu(), _ops()
+    M, N, K = 300, 256, 1024
+    A = gen.activations(M, K, seed=70, row_scale=True)
+    A[5, 64:128] = 0  # an all-zero group: sx = 0
+    U, XS = ops.a8_quant(g.dev(A), 2)
+    Ur, XSr = orc.a8_quant(A, 2)
+    assert np.array_equal(g.host(U), Ur)
+    assert np.array_equal(g.host(XS), XSr)
+    codes, wq, s, b = gen.qlinear(N, K, seed=71, bias="free")
+    Y = orc.w4a8(Ur, XSr, wq, s, b)
+    for flipped in (False, True):
+        W = g.qlinear(wq ^ np.uint32(0x88888888) if flipped else wq, s, b, flipped)
+        out = g.host(ops.qmm_w4a8(U, XS, False, W))
+        err = gen.bf16_err(out, Y)
+        assert err <= 2e-2, (flipped, err)

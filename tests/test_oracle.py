@@ -526,3 +526,33 @@ def test_moe_decode_composition():
     ref2 = ref - sg[:, None] * np.stack([mlp(sgu, sdn, x[t:t + 1])[0] for t in range(T)])
     got2 = gen.bf16_to_f32(no_sh).astype(np.float64)
     assert np.sqrt(np.mean((got2 - ref2) ** 2) / np.mean(ref2 ** 2)) < 1e-2
+
+
+def test_qa8_quant_form():
+    """The int8 prefill's quantizer (qa8.metal:30-49): q = clamp(rint(x * (127 / amax)), +-127), sx = amax / 127,
+    0 for an all-zero group. amax = 127 makes q = rint(x) exactly (ties to even); a value is picked where multiplying
+    by 127 / amax and dividing by amax / 127 round to different codes, so the two forms cannot be confused."""
+    g0 = np.zeros(64, np.float32)
+    g0[0], g0[1], g0[2], g0[3], g0[4] = 127, 2.5, -3.5, 0.5, -126.75
+    # search a (amax, x) pair in bf16 where the two quotients round to different integers
+    pick = None
+    for amax in np.linspace(1.0, 3.0, 400, dtype=np.float32):
+        a = gen.bf16_to_f32(gen.f32_to_bf16(np.array([amax], np.float32)))[0]
+        xs = gen.bf16_to_f32(gen.f32_to_bf16(np.linspace(-a, a, 257, dtype=np.float32)))
+        m = np.rint(xs * np.float32(127 / np.float32(a))) != np.rint(xs / np.float32(a / np.float32(127)))
+        if m.any():
+            pick = (a, xs[m][0])
+            break
+    assert pick is not None
+    g1 = np.zeros(64, np.float32)
+    g1[0], g1[1] = pick
+    g2 = np.zeros(64, np.float32)
+    A = gen.f32_to_bf16(np.concatenate([g0, g1, g2])[None])
+    U, XS = orc.a8_quant(A, 2)
+    assert U[0, :5].tolist() == [127, 2, -4, 0, -127]
+    a, x = pick
+    assert U[0, 65] == np.clip(np.rint(x * np.float32(127 / np.float32(a))), -127, 127)
+    assert U[0, 65] != np.rint(x / np.float32(a / np.float32(127)))
+    assert XS[0, 0, 0] == np.float32(127) / np.float32(127) and XS[0, 1, 0] == np.float32(a) / np.float32(127)
+    assert XS[0, 2, 0] == 0 and XS[0, 2, 1] == 0 and (U[0, 128:] == 0).all()
+    assert np.isclose(XS[0, 0, 1], XS[0, 0, 0] * U[0, :64].sum())
