@@ -201,6 +201,14 @@ int ifd_moe_gather_qmm(const void* A, const int* perm, int div, const int* offse
                        const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int E,
                        int N, int K, int silu, void* C, int R, void* stream);
 
+/* The gathered expert GEMM on int8 activations (reference qa8g_gemm, qa8.metal:212-397; host qa8g,
+ * qwen35.h:1847-1868): U int8 [rows][K] and XS [rows][K/64][2] from ifd_a8_quant with per-group scales (per_token 0
+ * or 2), sorted row q reads row perm[q] / div (perm NULL: row q); per group y += s sx P + b (sx sum xq),
+ * P = sum q xq exact. Same schedule, weights, silu and output as ifd_moe_gather_qmm; K / 64 * 256 bytes <= 64 KB. */
+int ifd_moe_gather_qmm_a8(const int8_t* U, const float* XS, const int* perm, int div, const int* offsets,
+                          const int* tiles, const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s,
+                          const uint16_t* b, int E, int N, int K, int silu, void* C, int R, void* stream);
+
 /* out[t][h] = bf16(acc) (assign) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] yd[inv[t*k+j]][h] + sg[t] ys[t][h]
  * (ys may be NULL) (reference moe_combine_sorted, moe.metal:172-187). */
 int ifd_moe_combine(void* out, const void* yd, const float* wt, const void* ys, const float* sg, const int* inv,

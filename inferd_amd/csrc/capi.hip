@@ -309,6 +309,18 @@ int ifd_moe_gather_qmm(const void* A, const int* perm, int div, const int* offse
                                silu ? 1 : 0, (uint16_t*)C, R, S(stream));
 }
 
+int ifd_moe_gather_qmm_a8(const int8_t* U, const float* XS, const int* perm, int div, const int* offsets,
+                          const int* tiles, const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s,
+                          const uint16_t* b, int E, int N, int K, int silu, void* C, int R, void* stream) {
+  IFD_CHECK(R >= 0 && E > 0 && N > 0 && K > 0 && K % 64 == 0 && div > 0, "bad shape E=%d N=%d K=%d", E, N, K);
+  IFD_CHECK(!silu || N % 2 == 0, "silu needs an even N (gate | up)");
+  IFD_CHECK(max_tiles >= 0, "bad max_tiles");
+  IFD_CHECK(R == 0 || (U && XS && offsets && tiles && ntiles && wq && s && b && C), "null pointer");
+  IFD_CHECK(R == 0 || (aligned(U, 16) && aligned(XS, 8) && aligned(wq, 16)), "U and wq must be 16-byte aligned");
+  return launch_moe_gather_qmm_a8(U, XS, perm, div, tiles, ntiles, offsets, max_tiles, wq, s, b, N, K, silu ? 1 : 0,
+                                  (uint16_t*)C, R, S(stream));
+}
+
 int ifd_moe_combine(void* out, const void* yd, const float* wt, const void* ys, const float* sg, const int* inv, int T,
                     int H, int k, int assign, void* stream) {
   IFD_CHECK(T >= 0 && H > 0 && H % 8 == 0 && k > 0, "bad shape T=%d H=%d k=%d", T, H, k);

@@ -303,6 +303,117 @@ int launch_moe_gather_qmm(const uint16_t* A, const int* perm, int div, const int
   return check_launch("moe_gather_qmm");
 }
 
+// ---- gathered expert GEMM on int8 activations ------------------------------------------------------------------
+// The int8-activation variant (reference qa8g_gemm, qa8.metal:212-397; host qwen35.h:1847-1868): the rows were
+// quantized once per row and 64-group (U int8 [MQ][K], XS [MQ][K/64][2] = (sx, sx sum xq)); sorted row q reads row
+// perm[q] / div of U (or row q without perm). Per group: P = sum q xq exactly on v_mfma_i32_32x32x32_i8 (codes 0..15
+// unflipped), then y += s sx P + b (sx sum xq) in fp32, group order. Block = (expert, 32-row tile) x 128 columns;
+// lane (j, h) takes k = 32 h + 16 kk .. +15 of the group in step kk (16 bytes of codes per group, two 16-byte int8
+// activation fragments), the tile's (sx, sx sum xq) staged in LDS. SILU as in k_gqmm.
+template <bool SILU>
+__global__ __launch_bounds__(256) void k_gqmm_a8(const int8_t* __restrict__ U, const float* __restrict__ XS,
+                                                 const int* __restrict__ perm, int div, const int* __restrict__ tiles,
+                                                 const int* __restrict__ ntiles, const uint32_t* __restrict__ wq,
+                                                 const uint16_t* __restrict__ s, const uint16_t* __restrict__ b, int N,
+                                                 int K, const int* __restrict__ offsets, uint16_t* __restrict__ C,
+                                                 int ncb) {
+  extern __shared__ float xsl[];  // [G][32][2]
+  const int tile = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+  if (tile >= ntiles[0]) return;  // block-uniform, before the barrier
+  const int e = tiles[2 * tile], q0 = tiles[2 * tile + 1], q1 = min(offsets[e + 1], q0 + 32);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int G = K / kGroup;
+  // the tile's activation scales: row r of the tile, group g
+  for (int i = tid; i < G * 32; i += 256) {
+    const int g = i >> 5, r = i & 31, q = q0 + r;
+    float2 v = make_float2(0.f, 0.f);
+    if (q < q1) {
+      const int ar = perm ? perm[q] / div : q;
+      v = *(const float2*)(XS + ((size_t)ar * G + g) * 2);
+    }
+    *(float2*)(xsl + ((size_t)g * 32 + r) * 2) = v;
+  }
+  __syncthreads();
+  const int NO = SILU ? N / 2 : N;
+  const int n0 = cb * 128 + wave * 32;
+  if (n0 >= NO) return;  // no barrier follows
+  const int n = min(n0 + j, NO - 1);
+  const int ldw = K / 8;
+  const size_t erow = (size_t)e * N;
+  const uint32_t* wrow = wq + (erow + n) * ldw + 4 * h;
+  const uint16_t* srow = s + (erow + n) * G;
+  const uint16_t* brow = b + (erow + n) * G;
+  const uint32_t* wrow2 = wq + (erow + n + NO) * ldw + 4 * h;
+  const uint16_t* srow2 = s + (erow + n + NO) * G;
+  const uint16_t* brow2 = b + (erow + n + NO) * G;
+  const int q = q0 + j;
+  const bool aok = q < q1;
+  const int8_t* arow = U + (size_t)(aok ? (perm ? perm[q] / div : q) : 0) * K + 32 * h;
+
+  float acc[16], acc2[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) acc[r] = acc2[r] = 0.f;
+  for (int g = 0; g < G; g++) {
+    const u32x4 wv = *(const u32x4*)(wrow + (size_t)g * 8);
+    const float sc = bf2f(srow[g]), bi = bf2f(brow[g]);
+    u32x4 wv2 = u32x4{0u, 0u, 0u, 0u};
+    float sc2 = 0.f, bi2 = 0.f;
+    if (SILU) {
+      wv2 = *(const u32x4*)(wrow2 + (size_t)g * 8);
+      sc2 = bf2f(srow2[g]);
+      bi2 = bf2f(brow2[g]);
+    }
+    i32x16 P = izero16(), P2 = izero16();
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      const u32x4 af = aok ? *(const u32x4*)(arow + (size_t)g * 64 + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
+      const u32x2 c0 = codes_i8(wv[2 * kk]), c1 = codes_i8(wv[2 * kk + 1]);
+      P = mfma_i8(af, u32x4{c0[0], c0[1], c1[0], c1[1]}, P);
+      if (SILU) {
+        const u32x2 d0 = codes_i8(wv2[2 * kk]), d1 = codes_i8(wv2[2 * kk + 1]);
+        P2 = mfma_i8(af, u32x4{d0[0], d0[1], d1[0], d1[1]}, P2);
+      }
+    }
+    const float* xg = xsl + (size_t)g * 64;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = 8 * (r / 4) + 4 * h + (r % 4);
+      const float sx = xg[2 * row], sq = xg[2 * row + 1];
+      acc[r] = __builtin_fmaf(sc * sx, (float)P[r], __builtin_fmaf(bi, sq, acc[r]));
+      if (SILU) acc2[r] = __builtin_fmaf(sc2 * sx, (float)P2[r], __builtin_fmaf(bi2, sq, acc2[r]));
+    }
+  }
+  const int col = n0 + j;
+  if (col >= NO) return;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int row = q0 + 8 * (r / 4) + 4 * h + (r % 4);
+    if (row >= q1) continue;
+    float v = acc[r];
+    if (SILU) v = swiglu_f(bf2f(f2bf(acc[r])), bf2f(f2bf(acc2[r])));
+    C[(size_t)row * NO + col] = f2bf(v);
+  }
+}
+
+int launch_moe_gather_qmm_a8(const int8_t* U, const float* XS, const int* perm, int div, const int* tiles,
+                             const int* ntiles, const int* offsets, int max_tiles, const uint32_t* wq,
+                             const uint16_t* s, const uint16_t* b, int N, int K, int silu, uint16_t* C, int R,
+                             hipStream_t st) {
+  if (R == 0 || max_tiles == 0) return IFD_OK;
+  const int NO = silu ? N / 2 : N, ncb = (NO + 127) / 128;
+  const size_t lds = (size_t)(K / kGroup) * 32 * 2 * sizeof(float);
+  if (lds > 64 * 1024) return fail(IFD_ERR_UNSUPPORTED, "moe_gather_qmm_a8: K=%d needs %zu bytes of LDS", K, lds);
+  dim3 grid((unsigned)(max_tiles * ncb)), block(256);
+  if (silu)
+    hipLaunchKernelGGL(k_gqmm_a8<true>, grid, block, lds, st, U, XS, perm, div, tiles, ntiles, wq, s, b, N, K, offsets,
+                       C, ncb);
+  else
+    hipLaunchKernelGGL(k_gqmm_a8<false>, grid, block, lds, st, U, XS, perm, div, tiles, ntiles, wq, s, b, N, K,
+                       offsets, C, ncb);
+  return check_launch("moe_gather_qmm_a8");
+}
+
 // ---- combine -----------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_moe_combine(uint16_t* __restrict__ out, const uint16_t* __restrict__ yd,
                                                      const float* __restrict__ wt, const uint16_t* __restrict__ ys,

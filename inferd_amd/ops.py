@@ -277,6 +277,18 @@ def moe_gather_qmm(A: torch.Tensor, perm: Optional[torch.Tensor], div: int, disp
     return C
 
 
+def moe_gather_qmm_a8(U: torch.Tensor, XS: torch.Tensor, perm: Optional[torch.Tensor], div: int, disp, W: MoeW,
+                      silu: bool) -> torch.Tensor:
+    """The gathered expert GEMM on int8 activations (U, XS from a8_quant with per-group scales)."""
+    offsets, perm_sorted, _, tiles, ntiles, mt = disp
+    R = perm_sorted.numel()
+    NO = W.N // 2 if silu else W.N
+    C = torch.empty((R, NO), dtype=torch.bfloat16, device=U.device)
+    check(lib().ifd_moe_gather_qmm_a8(_p(U), _p(XS), _p(perm), div, _p(offsets), _p(tiles), _p(ntiles), mt, _p(W.wq),
+                                      _p(W.s), _p(W.b), W.E, W.N, W.K, 1 if silu else 0, _p(C), R, _stream()))
+    return C
+
+
 def moe_combine(out: torch.Tensor, yd: torch.Tensor, wt: torch.Tensor, ys: Optional[torch.Tensor],
                 sg: Optional[torch.Tensor], inv: torch.Tensor, k: int, assign: bool) -> torch.Tensor:
     T, H = out.shape

@@ -56,6 +56,7 @@ def lib():
         L.orc_pack_w8.argtypes = [_u8p, _u32p, _i, _i]
         L.orc_unpack_w8.argtypes = [_u32p, _u8p, _i, _i, _u]
         L.orc_dequant_f32_b.argtypes = [_u32p, _u16p, _u16p, _i, _i, _i, _u, _f32p]
+        L.orc_moe_gather_w4a8.argtypes = [_i8p, _f32p, _vp, _i, _i32p, _u32p, _u16p, _u16p, _i, _i, _i, _f32p, _i]
         L.orc_moe_decode.argtypes = [_u16p, _i, _i, _i, _i, _i32p, _f32p, _f32p,
                                      _u32p, _u16p, _u16p, _u32p, _u16p, _u16p,
                                      _vp, _vp, _vp, _vp, _vp, _vp, _u16p, _i]
@@ -433,3 +434,15 @@ def moe_decode(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: bool
                          _c(edn[0], np.uint32), _c(edn[1], np.uint16), _c(edn[2], np.uint16), *sh, o,
                          1 if assign else 0)
     return o
+
+
+def moe_gather_w4a8(U, XS, perm, div: int, offsets, wq, s, b, N: int, K: int, nthreads: int = 0) -> np.ndarray:
+    """qa8g_gemm semantics (engine/kernels/qa8.metal:212-397): the gathered expert GEMM on int8 activations."""
+    offsets = _c(offsets, np.int32)
+    E = len(offsets) - 1
+    R = int(offsets[-1])
+    Y = np.zeros((R, N), np.float32)
+    pp = None if perm is None else _c(perm, np.int32)
+    lib().orc_moe_gather_w4a8(_c(U, np.int8), _c(XS, np.float32), None if pp is None else pp.ctypes.data, div, offsets,
+                              _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16), E, N, K, Y, nthreads)
+    return Y

@@ -415,6 +415,34 @@ void orc_moe_gather_qmm(const uint16_t* A, const int* perm, int div, const int* 
   (void)R;
 }
 
+// Gathered expert GEMM on int8 activations (reference qa8g_gemm, engine/kernels/qa8.metal:212-397): sorted row q
+// of expert e reads quantized row r = perm[q] / div (or q); y[q, n] = sum_g sx[r,g] (S_e[n,g] sum_k q_e[n,k] U[r,k]) +
+// B_e[n,g] (sx sum xq)[r,g], the integer sums exact, fp32 in group order (the W4A8 identity on unflipped codes).
+void orc_moe_gather_w4a8(const int8_t* U, const float* XS, const int* perm, int div, const int* offsets,
+                         const uint32_t* wq, const uint16_t* s, const uint16_t* b, int E, int N, int K, float* Y,
+                         int nthreads) {
+  const int kg = K / 64, kw = K / 8;
+  parallel_for(E, nthreads, [&](int e) {
+    const int q0 = offsets[e], q1 = offsets[e + 1];
+    std::vector<int> codes(K);
+    for (int n = 0; n < N && q0 < q1; n++) {
+      const size_t row = (size_t)e * N + n;
+      for (int k = 0; k < K; k++) codes[k] = code_at(wq + row * kw, k, 0);
+      for (int q = q0; q < q1; q++) {
+        const size_t r = (size_t)(perm ? perm[q] / div : q);
+        float acc = 0.f;
+        for (int g = 0; g < kg; g++) {
+          int32_t P = 0;
+          for (int k = g * 64; k < g * 64 + 64; k++) P += codes[k] * (int32_t)U[r * K + k];
+          const float sx = XS[(r * kg + g) * 2], sq = XS[(r * kg + g) * 2 + 1];
+          acc += bf2f(s[row * kg + g]) * sx * (float)P + bf2f(b[row * kg + g]) * sq;
+        }
+        Y[(size_t)q * N + n] = acc;
+      }
+    }
+  });
+}
+
 // Weighted combine over sorted expert outputs (engine/kernels/moe.metal:172-187):
 //   acc = sum_j w[t,j] yd[inv[t*k+j], h] + sg[t] ys[t,h] in fp32 over bf16 inputs;
 //   out = bf16(acc) (assign) or bf16(x + bf16(acc)) (residual). ys may be null (no shared expert).

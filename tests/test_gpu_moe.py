@@ -218,3 +218,32 @@ def test_moe_decode_shared_experts_across_tokens(assign):
 def test_moe_decode_no_shared_expert_long_k():
     """No shared expert; I = 1152 (two K chunks of 8 groups in the down kernel), H = 4608 (gate/up chunks too), k = 16."""
     _decode_case(3, 64, 4608, 1152, 16, False, False, seed=150)
+
+
+@pytest.mark.parametrize("silu", [True, False])
+def test_gather_qmm_a8(silu):
+    """The gathered expert GEMM on int8 activations (reference qa8g_gemm): token rows quantized once (qa8 form) and
+    read through perm, or sorted rows read directly."""
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(160)
+    T, E, H, I, k = 40, 16, 512, 256, 4
+    x = gen.activations(T, H, seed=161)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    disp = ops.moe_dispatch(g.dev(idx), E)
+    ro, rp, ri = orc.moe_dispatch(idx, E)
+    if silu:
+        wq, s, b = experts(E, 2 * I, H, seed=162)
+        U, XS = ops.a8_quant(g.dev(x), 2)
+        got = g.host(ops.moe_gather_qmm_a8(U, XS, disp[1], k, disp, g.moew(wq, s, b), silu=True))
+        Ur, XSr = orc.a8_quant(x, 2)
+        y = orc.moe_gather_w4a8(Ur, XSr, rp, k, ro, wq, s, b, 2 * I, H)
+        ref = orc.silu_mul(gen.f32_to_bf16(y))
+        assert gen.bf16_err(got, ref, ref_is_bf16=True) < 2e-2
+    else:
+        wq, s, b = experts(E, H, I, seed=163)
+        a = gen.activations(T * k, I, seed=164)  # sorted rows (the SwiGLU output of the gate/up product)
+        U, XS = ops.a8_quant(g.dev(a), 2)
+        got = g.host(ops.moe_gather_qmm_a8(U, XS, None, 1, disp, g.moew(wq, s, b), silu=False))
+        Ur, XSr = orc.a8_quant(a, 2)
+        y = orc.moe_gather_w4a8(Ur, XSr, None, 1, ro, wq, s, b, H, I)
+        assert gen.bf16_err(got, y) < 2e-2

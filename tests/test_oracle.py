@@ -556,3 +556,26 @@ def test_qa8_quant_form():
     assert XS[0, 0, 0] == np.float32(127) / np.float32(127) and XS[0, 1, 0] == np.float32(a) / np.float32(127)
     assert XS[0, 2, 0] == 0 and XS[0, 2, 1] == 0 and (U[0, 128:] == 0).all()
     assert np.isclose(XS[0, 0, 1], XS[0, 0, 0] * U[0, :64].sum())
+
+
+def test_moe_gather_w4a8_is_per_row_w4a8():
+    """The int8 gathered expert GEMM (qa8g) equals, row by row, the W4A8 product of the row's expert on the token row
+    it reads (up to fp32 rounding: W4A8 forms (q - 8) and b + 8 s, qa8g unflipped q and b), and the float64 GEMM of the
+    dequantized weights against sx * xq."""
+    rng = np.random.default_rng(31)
+    E, N, K, T, k = 4, 48, 256, 6, 2
+    parts = [gen.qlinear(N, K, seed=40 + e, bias="free") for e in range(E)]
+    wq = np.stack([p[1] for p in parts]); s = np.stack([p[2] for p in parts]); b = np.stack([p[3] for p in parts])
+    A = gen.activations(T, K, seed=32)
+    U, XS = orc.a8_quant(A, 2)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    offsets, perm, inv = orc.moe_dispatch(idx, E)
+    Y = orc.moe_gather_w4a8(U, XS, perm, k, offsets, wq, s, b, N, K)
+    for q in range(T * k):
+        e = int(np.searchsorted(offsets, q, side="right") - 1)
+        r = perm[q] // k
+        want = orc.w4a8(U[r:r + 1], XS[r:r + 1], wq[e], s[e], b[e])[0]
+        assert gen.rel_err(Y[q:q + 1], want[None]) < 1e-5
+        xd = U[r].astype(np.float64) * np.repeat(XS[r, :, 0], 64)
+        ref = gen.dequant_f64(parts[e][0], parts[e][2], parts[e][3]) @ xd
+        assert gen.rel_err(Y[q:q + 1], ref[None]) < 1e-5
