@@ -238,11 +238,11 @@ int ifd_mlp_decode(void* x, int ldx, const void* norm_w, float eps, const void* 
 
 /* Decode MoE for T <= 8 tokens (reference moe_plan / moe_gu2 / moe_dn2 and their router, moe.metal:267-551; host
  * qwen35.h:1876-1908): router logits (fp32) -> routing -> the distinct experts of the step -> gate/up + SwiGLU ->
- * down + combine, four launches, each distinct expert's weights read once for all tokens that picked it. Every
+ * down + combine, three launches, each distinct expert's weights read once for all tokens that picked it. Every
  * expert product uses the decode GEMV arithmetic (qmv4). The shared expert (sgu [2I][H], sdn [H][I], 4-bit, or NULL)
  * shares the routed experts' I. out = bf16(acc) (assign) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] d_j +
  * sg[t] d_shared. idx / wt / sg / logits ([T][E + shared_gate] fp32, the values routed on) are written if non-NULL.
- * H % 256 == 0, I % 64 == 0, E <= 512, k <= 16. Workspace: ifd_moe_decode_workspace (its header counters zeroed
+ * H % 512 == 0, I % 64 == 0, E <= 512, k <= 16. Workspace: ifd_moe_decode_workspace (its header counters zeroed
  * once, as for every workspace). */
 size_t ifd_moe_decode_workspace(int T, int H, int I, int E, int k);
 int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,

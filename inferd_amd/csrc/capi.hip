@@ -477,9 +477,9 @@ int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int 
                    void* out, int assign, int* idx, float* wt, float* sg, float* logits, void* workspace,
                    size_t ws_bytes, void* stream) {
   IFD_CHECK(T >= 0 && T <= 8, "the decode MoE takes T <= 8 tokens (T=%d): larger batches use ifd_moe_ffn", T);
-  IFD_CHECK(H > 0 && H % 256 == 0 && H <= 131072 && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 && k <= 16 &&
-                k <= E,
-            "bad decode MoE shape H=%d I=%d E=%d k=%d (H multiple of 256, I of 64, E <= 512, k <= 16)", H, I, E, k);
+  IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
+                k <= 16 && k <= E,
+            "bad decode MoE shape H=%d I=%d E=%d k=%d (H multiple of 512, I of 64, E <= 512, k <= 16)", H, I, E, k);
   const bool shared = sgu_wq != nullptr;
   IFD_CHECK(!shared || (sgu_s && sgu_b && sdn_wq && sdn_s && sdn_b), "bad shared expert");
   IFD_CHECK(!shared_gate || shared, "a shared gate needs a shared expert");

@@ -1,21 +1,21 @@
-// Decode MoE for T <= 8 tokens in four launches, each distinct expert's weights read once for every token that
+// Decode MoE for T <= 8 tokens in three launches, each distinct expert's weights read once for every token that
 // picked it.
 //
 // Replaces the reference's four-launch decode MoE (engine/kernels/moe.metal:267-293 router, 326-368 moe_plan,
 // 370-488 moe_gu2, 490-551 moe_dn2; host engine/src/qwen35.h:1876-1908):
 //  1. k_mdec_router: router logits (bf16 router [E1][H] x bf16 tokens) as K-split fp32 partials [KS][T][E1]. One
-//     32-expert tile x a K range per wave (32x32x16 bf16 MFMA, tokens in the A rows), the block's four waves summed
-//     in wave order.
-//  2. k_mdec_plan (one block): wave t sums token t's partials in split order and routes it (route_token, as
-//     k_moe_route); one thread per pick then lists the distinct experts in pick order: plan = [nuniq, expert[T k],
-//     pick[T k][8]] (pick[u][t] = token t's pick index of unique expert u, or -1).
-//  3. k_mdec_gu: one block per (32 gate/up column pairs, unique expert or the shared expert). Its four waves split K;
+//     32-expert tile x a K range per wave (32x32x16 bf16 MFMA, tokens in the A rows), the block's eight waves summed
+//     in wave order. The last block to finish (a counter in the workspace header) then routes: wave w sums token
+//     w's partials in split order and routes it (route_token, as k_moe_route); one thread per pick lists the
+//     distinct experts in pick order: plan = [nuniq, expert[T k], pick[T k][8]] (pick[u][t] = token t's pick index
+//     of unique expert u, or -1).
+//  2. k_mdec_gu: one block per (32 gate/up column pairs, unique expert or the shared expert). Its four waves split K;
 //     each stages the token rows of its K range in LDS and streams the 32 gate and 32 up rows of its expert (16 B
 //     of codes per lane and group, all loads of a chunk issued before the first wait), runs the qmv4 arithmetic on
 //     bf16 MFMA (codes as 128 + q, the group sums X from the staged rows, s P + (b - 128 s) X in fp32), and the waves'
 //     sums are added in wave order. The SwiGLU of the bf16-rounded gate and up goes to act[t][j] for every token t
 //     that picked the expert as its j-th (j = k: the shared expert).
-//  4. k_mdec_dn: one block per (128 output columns, unique expert or the shared expert): the down rows of the expert
+//  3. k_mdec_dn: one block per (128 output columns, unique expert or the shared expert): the down rows of the expert
 //     against act of the tokens that picked it (same arithmetic), d[t][j] = bf16(result), stored write-through. The
 //     last block of each 128-column chunk (a counter in the workspace header) combines:
 //     out[t][h] = bf16(acc) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] d[t][j][h] + sg[t] d[t][k][h], in j order.
@@ -69,57 +69,31 @@ __device__ __forceinline__ void load8h(const uint16_t* v, uint16_t (&o)[kMdecKG]
   for (int i = 0; i < 8; i++) o[i] = (uint16_t)(w[i / 2] >> (16 * (i & 1)));
 }
 
-// ---- 1. router logits --------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_mdec_router(MdecArgs p) {
-  __shared__ float red[4][64][4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 31, h = lane >> 5;
-  const int e0 = blockIdx.x * 32, ks = blockIdx.y;
-  const int Kc = p.H / (4 * p.KS), k0 = (ks * 4 + wave) * Kc;
-  const bool tok = j < p.T, eok = e0 + j < p.E1;
-  const uint16_t* xa = p.x + (size_t)(tok ? j : 0) * p.H + k0 + 32 * h;
-  const uint16_t* wb = p.router + (size_t)(eok ? e0 + j : 0) * p.H + k0 + 32 * h;
-  f32x16 acc = zero16();
-  for (int kb = 0; kb < Kc; kb += 64) {
-    u32x4 a[4], b[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      a[t] = tok ? *(const u32x4*)(xa + kb + 8 * t) : u32x4{0u, 0u, 0u, 0u};
-      b[t] = eok ? *(const u32x4*)(wb + kb + 8 * t) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int t = 0; t < 4; t++) acc = mfma_bf16(a[t], b[t], acc);
-  }
-  // D rows 4 h + r (r < 4) are tokens 0..7, column j is expert e0 + j
-#pragma unroll
-  for (int r = 0; r < 4; r++) red[wave][lane][r] = acc[r];
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const float v = red[0][lane][r] + red[1][lane][r] + red[2][lane][r] + red[3][lane][r];
-    const int t = 4 * h + r, e = e0 + j;
-    if (t < p.T && e < p.E1) p.part[((size_t)ks * p.T + t) * p.E1 + e] = v;
-  }
-}
-
-// ---- 2. routing and the distinct-expert plan ---------------------------------------------------------------------
-__global__ __launch_bounds__(512) void k_mdec_plan(MdecArgs p) {
+// ---- 1 + 2. router logits, then (the last block) routing and the distinct-expert plan -----------------------------
+// Routing and the plan, by one block of NTHR threads: wave w routes tokens w, w + NTHR / 64, ... from the K-split
+// partials (summed in split order; device-coherent loads: other blocks, maybe on other XCDs, wrote them), then one
+// thread per pick numbers the distinct experts in pick order.
+template <int NTHR>
+__device__ __forceinline__ void mdec_plan_block(const MdecArgs& p) {
   __shared__ int tidx[kMdecMaxT * kMdecMaxK], urank[kMdecMaxT * kMdecMaxK], firstpick[512], wcount[2];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int T = p.T, k = p.k, NU = T * k;
   int* upick = p.plan + 1 + NU;
-  for (int i = tid; i < NU * 8; i += 512) upick[i] = -1;
-  for (int i = tid; i < p.E; i += 512) firstpick[i] = 0x7fffffff;
-  if (wave < T) {
-    // token t's logits, the K-split partials summed in split order: every load issued before the first add
-    const int t = wave;
+  for (int i = tid; i < NU * 8; i += NTHR) upick[i] = -1;
+  for (int i = tid; i < p.E; i += NTHR) firstpick[i] = 0x7fffffff;
+  const __amdgpu_buffer_rsrc_t rp = part_rsrc(p.part, (uint32_t)((size_t)p.KS * T * p.E1 * 4));
+  for (int t = wave; t < T; t += NTHR / 64) {
+    // token t's logits: every load issued before the first add
     float part[kMdecMaxKS][9];
 #pragma unroll
     for (int z = 0; z < kMdecMaxKS; z++)
 #pragma unroll
       for (int i = 0; i < 9; i++) {
         const int c = i < 8 ? i * 64 + lane : p.E;  // slot 8: the shared expert's gate logit
-        part[z][i] = z < p.KS && c < p.E1 ? p.part[((size_t)z * T + t) * p.E1 + c] : 0.f;
+        part[z][i] = z < p.KS && c < p.E1
+                         ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                               rp, (int)((((size_t)z * T + t) * p.E1 + c) * 4), 0, kSc1))
+                         : 0.f;
       }
     float v[9];
 #pragma unroll
@@ -173,6 +147,58 @@ __global__ __launch_bounds__(512) void k_mdec_plan(MdecArgs p) {
   __syncthreads();
   if (tid < NU) upick[urank[f] * 8 + tid / k] = tid % k;
   if (tid == 0) p.plan[0] = wcount[0] + wcount[1];
+}
+
+__global__ __launch_bounds__(512) void k_mdec_router(MdecArgs p) {
+  __shared__ float red[8][64][4];
+  __shared__ unsigned s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
+  const int e0 = blockIdx.x * 32, ks = blockIdx.y;
+  const int Kc = p.H / (8 * p.KS), k0 = (ks * 8 + wave) * Kc;
+  const bool tok = j < p.T, eok = e0 + j < p.E1;
+  const uint16_t* xa = p.x + (size_t)(tok ? j : 0) * p.H + k0 + 32 * h;
+  const uint16_t* wb = p.router + (size_t)(eok ? e0 + j : 0) * p.H + k0 + 32 * h;
+  f32x16 acc = zero16();
+  for (int kb = 0; kb < Kc; kb += 64) {
+    u32x4 a[4], b[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      a[t] = tok ? *(const u32x4*)(xa + kb + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+      b[t] = eok ? *(const u32x4*)(wb + kb + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) acc = mfma_bf16(a[t], b[t], acc);
+  }
+  // D rows 4 h + r (r < 4) are tokens 0..7, column j is expert e0 + j; the waves' K ranges summed in wave order and
+  // written through for the block that routes
+#pragma unroll
+  for (int r = 0; r < 4; r++) red[wave][lane][r] = acc[r];
+  __syncthreads();
+  if (wave == 0) {
+    const __amdgpu_buffer_rsrc_t rp = part_rsrc(p.part, (uint32_t)((size_t)p.KS * p.T * p.E1 * 4));
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float v = red[0][lane][r];
+#pragma unroll
+      for (int w = 1; w < 8; w++) v += red[w][lane][r];
+      const int t = 4 * h + r, e = e0 + j;
+      if (t < p.T && e < p.E1)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rp, (int)((((size_t)ks * p.T + t) * p.E1 + e) * 4),
+                                              0, kSc1);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned arrivals = gridDim.x * gridDim.y;
+    unsigned* c = p.cnt + (kWsCounters - 1);
+    const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1 == arrivals;
+    if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (s_last) mdec_plan_block<512>(p);
 }
 
 // The slot of block row u: a distinct routed expert (u < nuniq), the shared expert (u == T k), or nothing.
@@ -411,10 +437,11 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
 }
 
 // ---- host ------------------------------------------------------------------------------------------------------------
+// K splits of the router: each of a block's 8 waves takes H / (8 KS) columns, a multiple of 64
 static int mdec_ks(int H) {
   for (int ks : {4, 2, 1})
-    if (H % (256 * ks) == 0 && H / (256 * ks) >= 1 && ks * 512 <= H) return ks;
-  return 1;
+    if (H % (512 * ks) == 0) return ks;
+  return 0;
 }
 
 MdecLayout mdec_layout(int T, int H, int I, int E, int k) {
@@ -470,10 +497,8 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
   p.sb16_dn = Gi % 8 == 0 && aligned(c.edn_s, 16) && aligned(c.edn_b, 16) &&
               (!shared || (aligned(c.sdn_s, 16) && aligned(c.sdn_b, 16)));
   const int slots = c.T * c.k + 1;
-  hipLaunchKernelGGL(k_mdec_router, dim3((p.E1 + 31) / 32, p.KS), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_mdec_router, dim3((p.E1 + 31) / 32, p.KS), dim3(512), 0, st, p);
   IFD_TRY(check_launch("moe_decode router"));
-  hipLaunchKernelGGL(k_mdec_plan, dim3(1), dim3(512), 0, st, p);
-  IFD_TRY(check_launch("moe_decode plan"));
   hipLaunchKernelGGL(k_mdec_gu, dim3(c.I / 32, slots), dim3(256), 0, st, p);
   IFD_TRY(check_launch("moe_decode gate_up"));
   const size_t lds = ((size_t)c.T * (c.I + 8) + 8) * 2 + (size_t)(c.I / kGroup) * 8 * 4;

@@ -254,7 +254,7 @@ struct Qwen35 {
                                              ly.gate_up.K == H && ly.down.N == H && ly.down.K == I &&
                                              !ly.gate_up.flipped && !ly.down.flipped && !ly.gate_up.ldk &&
                                              !ly.down.ldk);
-    if (T <= 8 && k <= 16 && E <= 512 && H % 256 == 0 && I % 64 == 0 && E1 <= E + 1 && shared_fits) {
+    if (T <= 8 && k <= 16 && E <= 512 && H % 512 == 0 && I % 64 == 0 && E1 <= E + 1 && shared_fits) {
       const size_t need = ifd_moe_decode_workspace(T, H, I, E, k);
       if (need > splitk_bytes) die("encode_moe", "scratch smaller than the decode MoE needs");
       ok(ifd_moe_decode(xn.ptr<void>(), T, H, ly.router.wq.ptr<void>(), E, k, 1, E1 > E ? 1 : 0,

@@ -291,7 +291,7 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
 
 void test_encode_moe(std::mt19937& rng) {
   Config c;
-  c.hidden = 256, c.experts = 32, c.topk = 4, c.moe_inter = 128, c.eps = 1e-6f;
+  c.hidden = 512, c.experts = 32, c.topk = 4, c.moe_inter = 128, c.eps = 1e-6f;
   const int H = c.hidden, E = c.experts, k = c.topk, I = c.moe_inter, Is = 128;
   // layer: stacked experts [E, 2I, H] and [E, H, I], shared expert, bf16 router with the shared gate row
   const HostLinear egu = make_linear(E * 2 * I, H, rng), edn = make_linear(E * H, I, rng);

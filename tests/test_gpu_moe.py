@@ -211,7 +211,7 @@ def test_moe_decode_baseline_geometry(T):
 @pytest.mark.parametrize("assign", [True, False])
 def test_moe_decode_shared_experts_across_tokens(assign):
     """8 tokens over 8 experts, top-3: most experts are picked by several tokens (each read once for all of them)."""
-    ri = _decode_case(8, 8, 256, 128, 3, True, False, seed=140, assign=assign)
+    ri = _decode_case(8, 8, 512, 128, 3, True, False, seed=140, assign=assign)
     assert len(np.unique(ri)) < ri.size
 
 
