@@ -99,3 +99,42 @@ def test_t64_w4a8_refuses_per_group_activations():
     L = _lib.lib()
     rc = L.ifd_gemm_t64_w4a8(4096, 4096, 0, 4096, 256, 256, 4096, 256, 4, 0, None, 0, None)
     assert rc == _lib.IFD_ERR_UNSUPPORTED and b"per-token" in L.ifd_last_error()
+
+
+def test_new_entry_points_reject_bad_arguments():
+    """8-bit GEMM / W8A8, the decode MoE, the MLP block and the int8 gathered GEMM return IFD_ERR_ARG with a reason
+    before any GPU work."""
+    L = _lib.lib()
+    E = _lib.IFD_ERR_ARG
+    # 8-bit weights: the 4-bit flip mask is not an 8-bit one
+    assert L.ifd_gemm_w8(4096, 128, 4096, 4096, 4096, 64, 128, 0, 0x88888888, 4096, 64, 4, 0, None, 0, None) == E
+    assert b"0x80808080" in L.ifd_last_error()
+    assert L.ifd_qmm_w8a8(4096, 4096, 0, 4096, 4096, 4096, 64, 100, 0, 0, 4096, 64, 4, 0, None, 0, None) == E
+    # quantizer forms 0, 1, 2 only
+    assert L.ifd_a8_quant(4096, 128, 4, 128, 3, 4096, 4096, None) == E and b"per_token=3" in L.ifd_last_error()
+    # decode MoE: at most 8 tokens, H a multiple of 512, k <= 16, no shared gate without a shared expert
+    args = [4096, 9, 2048, 4096, 512, 10, 1, 0, 4096, 4096, 4096, 4096, 4096, 4096, 512,
+            None, None, None, None, None, None, 4096, 0, None, None, None, None, None, 0, None]
+    assert L.ifd_moe_decode(*args) == E and b"T <= 8" in L.ifd_last_error()
+    a = list(args); a[1], a[2] = 4, 1280
+    assert L.ifd_moe_decode(*a) == E and b"H multiple of 512" in L.ifd_last_error()
+    a = list(args); a[1], a[5] = 4, 17
+    assert L.ifd_moe_decode(*a) == E
+    a = list(args); a[1], a[7] = 4, 1
+    assert L.ifd_moe_decode(*a) == E and b"shared gate" in L.ifd_last_error()
+    # the MLP block: H and I multiples of 256
+    assert L.ifd_mlp_decode(4096, 5120, 4096, 1e-6, 4096, 4096, 4, 5120, 1000, None, 0, None) == E
+    # int8 gathered GEMM: K a multiple of 64, an even N for silu
+    assert L.ifd_moe_gather_qmm_a8(4096, 4096, None, 1, 4096, 4096, 4096, 4, 4096, 4096, 4096, 8, 64, 100, 0, 4096, 32,
+                                   None) == E
+    assert L.ifd_moe_gather_qmm_a8(4096, 4096, None, 1, 4096, 4096, 4096, 4, 4096, 4096, 4096, 8, 63, 128, 1, 4096, 32,
+                                   None) == E
+
+
+def test_new_workspace_queries():
+    L = _lib.lib()
+    assert L.ifd_moe_decode_workspace(9, 2048, 512, 512, 10) == 0
+    w1, w8 = L.ifd_moe_decode_workspace(1, 2048, 512, 512, 10), L.ifd_moe_decode_workspace(8, 2048, 512, 512, 10)
+    assert HEADER_BYTES < w1 < w8
+    assert L.ifd_mlp_decode_workspace(1, 5120, 17408) > HEADER_BYTES + 5120 * 2 + 17408 * 2
+    assert L.ifd_gemm_w8_workspace(1, 5120, 5120) == L.ifd_gemm_w4_workspace(1, 5120, 5120)
