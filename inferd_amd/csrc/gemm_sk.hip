@@ -387,12 +387,16 @@ static SkPlan gemm_sk_plan(int M, int N, int K) {
 }
 
 // Shapes with tiles for at least a third of the CUs: there each tile is cut into a few pieces. With fewer tiles (long
-// K, narrow N) every tile would be cut into many, and the aligned K split (gemm_t64.hip) moves fewer partial bytes.
+// K, narrow N) every tile is cut into many, and the aligned K split (gemm_t64.hip) moves fewer partial bytes; it is
+// still the faster kernel at 32-row tiles and with two or more 128-row M tiles over a long K (measured: N = 5120,
+// K = 17408, M = 32: 25.9 against 29.5 us; M = 256: 70.8 against 75.4 us). With one 128-row tile (64 < M <= 128)
+// stream-K is faster on every narrow shape measured (K = 17408: 45.9 against 47.6 us; N = K = 5120: 26.0 against
+// 31.2 us; N = 2048, K = 8192: 23.5 against 31.0 us), and both kernels compute bf16(s*q + b) there.
 bool gemm_sk_applies(int M, int N, int K, int mode) {
   if (M <= 16 || K % kGroup) return false;
   if (mode == kModeSwiglu && N % 256) return false;
   const SkPlan pl = gemm_sk_plan(M, N, K);
-  return (long)pl.tiles_m * pl.tiles_n * 3 >= cu_count();
+  return (long)pl.tiles_m * pl.tiles_n * 3 >= cu_count() || (M > 64 && M <= 128);
 }
 
 size_t gemm_sk_workspace(int M, int N, int K, int mode) {

@@ -142,12 +142,14 @@ def test_split_k_is_deterministic():
     (65, 34816, 512, 1),    # 65 rows in one 128-row tile (63 past M); runs of ~4 groups
     (200, 22528, 1024, 2),  # two M tiles per column tile
     (300, 34816, 512, 0),   # 3 x 136 tiles > CUs: every run is one whole tile (no pieces)
+    (128, 5120, 17408, 1),  # decode down at M = 128: 20 tiles, each cut into ~13 pieces; residual add in the fixup
+    (100, 2048, 8192, 2),   # 8 tiles of one 128-row M tile (~32 pieces each), fp32 out
 ])
 def test_gemm_t64_stream_k(M, N, K, mode):
-    """The stream-K kernel (16 < M below the prefill tiles, tiles for at least a third of the CUs) against the oracle on
-    sampled rows, in every store mode, at shapes whose runs cross tile boundaries, cut a tile into several pieces or
-    cover whole tiles; a second call on the same workspace gives the same bits (the fixup sums the pieces in unit
-    order) and leaves the counter header zero."""
+    """The stream-K kernel (16 < M below the prefill tiles, tiles for at least a third of the CUs, or any tile count at
+    64 < M <= 128) against the oracle on sampled rows, in every store mode, at shapes whose runs cross tile boundaries,
+    cut a tile into several or many pieces or cover whole tiles; a second call on the same workspace gives the same
+    bits (the fixup sums the pieces in unit order) and leaves the counter header zero."""
     from inferd_amd._lib import lib
     g, ops = _gu(), _ops()
     assert lib().ifd_gemm_t64_workspace(M, N, K) > 0
