@@ -194,6 +194,40 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+// The two row passes of rmsnorm for a 256-thread block: thread t takes elements t + 256 k, in k order, with 8
+// elements' loads issued before their arithmetic. The loads are unconditional, at an index clamped to the row, and
+// the select comes after them: a load under the bound check became a branch with its own wait, and the serial load
+// latency made a 5120-wide row take about 9 us. An element past D contributes fma(0, 0, ss) = ss (ss >= +0).
+__device__ __forceinline__ float row_sumsq256(const uint16_t* __restrict__ xr, int D) {
+  float ss = 0.f;
+  for (int i0 = (int)threadIdx.x; i0 < D; i0 += 256 * 8) {
+    uint16_t u[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) u[k] = xr[min(i0 + 256 * k, D - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float v = i0 + 256 * k < D ? bf2f(u[k]) : 0.f;
+      ss = __builtin_fmaf(v, v, ss);
+    }
+  }
+  return ss;
+}
+// o[i] = bf16(x[i] r w[i]); each thread writes only the elements it read (o may be x)
+__device__ __forceinline__ void row_norm_store256(const uint16_t* xr, const uint16_t* __restrict__ w, uint16_t* o,
+                                                  int D, float r) {
+  for (int i0 = (int)threadIdx.x; i0 < D; i0 += 256 * 8) {
+    uint16_t xu[8], wu[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = min(i0 + 256 * k, D - 1);
+      xu[k] = xr[i];
+      wu[k] = w[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (i0 + 256 * k < D) o[i0 + 256 * k] = f2bf(bf2f(xu[k]) * r * bf2f(wu[k]));
+  }
+}
 __device__ __forceinline__ int wave_min_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));

@@ -72,14 +72,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm_a8(const uint16_t* __restrict__
   __shared__ float red[4];
   const size_t row = blockIdx.x;
   const uint16_t* xr = x + row * in_stride;
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < D; i += 256) {
-    const float v = bf2f(xr[i]);
-    ss = __builtin_fmaf(v, v, ss);
-  }
-  const float r = rsqrtf(block_sum4(ss, red) / (float)D + eps);
-  uint16_t* o = out + row * out_stride;
-  for (int i = threadIdx.x; i < D; i += 256) o[i] = f2bf(bf2f(xr[i]) * r * bf2f(w[i]));
+  const float r = rsqrtf(block_sum4(row_sumsq256(xr, D), red) / (float)D + eps);
+  row_norm_store256(xr, w, out + row * out_stride, D, r);
   auto value = [&](int i) { return bf2f(f2bf(bf2f(xr[i]) * r * bf2f(w[i]))); };
   quant_row<PT>(value, D, red, U + row * D, XS + row * (D / kGroup) * 2);
 }
@@ -98,7 +92,8 @@ __global__ __launch_bounds__(256) void k_silu_mul_a8(const uint16_t* __restrict_
 
 // A deferred split-K residual reduce inside the next rmsnorm (reference splitk_res_norm, core.metal:539-595):
 // x[row] = bf16(sum_z part[z][row] + x[row]) in split order (k_splitk_reduce, mode 1), then out = rmsnorm(x) and,
-// with U, its quantization. Each thread re-reads only the elements it wrote.
+// with U, its quantization. Each thread uses only the elements it wrote (a load clamped past the row's end reads
+// element D - 1 and discards it).
 template <int A8>  // 0: none, 1: per group, 2: per token
 __global__ __launch_bounds__(256) void k_splitk_res_norm(const float* __restrict__ part, int S, int M, uint16_t* x,
                                                          int ldx, const uint16_t* __restrict__ w,
@@ -108,17 +103,36 @@ __global__ __launch_bounds__(256) void k_splitk_res_norm(const float* __restrict
   const size_t row = blockIdx.x, mn = (size_t)M * D;
   uint16_t* xr = x + row * ldx;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < D; i += 256) {
-    float acc = 0.f;
-    for (int z = 0; z < S; z++) acc += part[z * mn + row * D + i];
-    const uint16_t v = f2bf(acc + bf2f(xr[i]));
-    xr[i] = v;
-    const float f = bf2f(v);
-    ss = __builtin_fmaf(f, f, ss);
+  // 8 elements per thread at a time, their loads at clamped indices issued before the sums (as row_sumsq256); each
+  // element's partials summed in split order, then the residual
+  for (int i0 = threadIdx.x; i0 < D; i0 += 256 * 8) {
+    float acc[8];
+    uint16_t xu[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      acc[k] = 0.f;
+      xu[k] = xr[min(i0 + 256 * k, D - 1)];
+    }
+    for (int z = 0; z < S; z++) {
+      float pv[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) pv[k] = part[z * mn + row * D + min(i0 + 256 * k, D - 1)];
+#pragma unroll
+      for (int k = 0; k < 8; k++) acc[k] += pv[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = i0 + 256 * k;
+      if (i < D) {
+        const uint16_t v = f2bf(acc[k] + bf2f(xu[k]));
+        xr[i] = v;
+        const float f = bf2f(v);
+        ss = __builtin_fmaf(f, f, ss);
+      }
+    }
   }
   const float r = rsqrtf(block_sum4(ss, red) / (float)D + eps);
-  uint16_t* o = out + row * out_stride;
-  for (int i = threadIdx.x; i < D; i += 256) o[i] = f2bf(bf2f(xr[i]) * r * bf2f(w[i]));
+  row_norm_store256(xr, w, out + row * out_stride, D, r);
   if (A8) {
     auto value = [&](int i) { return bf2f(f2bf(bf2f(xr[i]) * r * bf2f(w[i]))); };
     if (A8 == 2) quant_row<true>(value, D, red, U + row * D, XS + row * (D / kGroup) * 2);

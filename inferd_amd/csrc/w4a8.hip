@@ -111,17 +111,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x,
                                                  int out_stride, int D, float eps) {
   __shared__ float red[4];
   const uint16_t* xr = x + (size_t)blockIdx.x * in_stride;
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < D; i += 256) {
-    const float v = bf2f(xr[i]);
-    ss = __builtin_fmaf(v, v, ss);
-  }
-  ss = wave_sum(ss);
+  const float ss = wave_sum(row_sumsq256(xr, D));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float r = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + eps);
-  uint16_t* o = out + (size_t)blockIdx.x * out_stride;
-  for (int i = threadIdx.x; i < D; i += 256) o[i] = f2bf(bf2f(xr[i]) * r * bf2f(w[i]));
+  row_norm_store256(xr, w, out + (size_t)blockIdx.x * out_stride, D, r);
 }
 int launch_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows,
                    int D, float eps, hipStream_t st) {
