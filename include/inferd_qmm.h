@@ -149,7 +149,7 @@ int ifd_gemm_t64_swiglu(const void* A, int lda, const void* wt, int N, int K, vo
  * per_token = 2: the int8 prefill's quantizer (reference qa8_quant, qa8.metal:30-49): per 64-group,
  * xq = clamp(rint(x * (127 / amax)), -127, 127) (0 if amax == 0), sx = amax / 127; U in natural K order. With
  * ifd_qmm_w4a8 (per_token = 0) it gives the reference's qa8 path (qa8_gemm, qa8.metal:52-210: the same per-group
- * identity on unflipped codes). */
+ * identity on unflipped codes). K % 64 == 0; A 16-byte aligned with lda % 8 == 0, U 8-byte aligned. */
 int ifd_a8_quant(const void* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, void* stream);
 
 /* C (mode) = sum_g [ s sx P + b (sx sum xq) ], P = sum q xq over the group (exact int32); U, XS from

@@ -149,8 +149,9 @@ int ifd_splitk_res_norm(const float* part, int S_, void* x, int ldx, const void*
 }
 
 int ifd_a8_quant(const void* A, int lda, int M, int K, int per_token, int8_t* U, float* XS, void* stream) {
-  IFD_CHECK(M >= 0 && K > 0 && K % 64 == 0 && lda >= K, "bad shape M=%d K=%d lda=%d", M, K, lda);
+  IFD_CHECK(M >= 0 && K > 0 && K % 64 == 0 && lda >= K && lda % 8 == 0, "bad shape M=%d K=%d lda=%d", M, K, lda);
   IFD_CHECK(M == 0 || (A && U && XS), "null pointer");
+  IFD_CHECK(M == 0 || (aligned(A, 16) && aligned(U, 8)), "A must be 16-byte and U 8-byte aligned");
   IFD_CHECK(per_token >= 0 && per_token <= 2, "per_token=%d must be 0 (per group), 1 (per token) or 2 (qa8 form)",
             per_token);
   return launch_a8_quant((const uint16_t*)A, lda, M, K, per_token, U, XS, S(stream));

@@ -194,6 +194,34 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+// Wave-wide max / min / sum with DPP: an inclusive scan within rows of 16 lanes (row_shr 1, 2, 4, 8), then across
+// rows (row_bcast 15 into rows 1 and 3, row_bcast 31 into rows 2 and 3), so lane 63 holds the result, which
+// readlane makes wave-uniform. Lanes a step has no source for keep the identity. About a tenth of the latency of the
+// LDS-permute shuffles, which matters in the serial top-k loop.
+template <class Op>
+__device__ __forceinline__ int dpp_reduce_i(int v, int id, Op op) {
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ float dpp_max_f(float v) {
+  return __int_as_float(dpp_reduce_i(__float_as_int(v), __float_as_int(-INFINITY), [](int a, int b) {
+    return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+  }));
+}
+__device__ __forceinline__ float dpp_sum_f(float v) {
+  return __int_as_float(dpp_reduce_i(__float_as_int(v), 0, [](int a, int b) {
+    return __float_as_int(__int_as_float(a) + __int_as_float(b));
+  }));
+}
+__device__ __forceinline__ int dpp_min_i(int v) {
+  return dpp_reduce_i(v, 0x7fffffff, [](int a, int b) { return min(a, b); });
+}
+
 // The two row passes of rmsnorm for a 256-thread block: thread t takes elements t + 256 k, in k order, with 8
 // elements' loads issued before their arithmetic. The loads are unconditional, at an index clamped to the row, and
 // the select comes after them: a load under the bound check became a branch with its own wait, and the serial load

@@ -35,29 +35,44 @@ __device__ __forceinline__ float block_max4(float v, float* red) {
 template <bool PT, class F>
 __device__ __forceinline__ void quant_row(F value, int D, float* red, int8_t* U, float* XS) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // 8 elements' values per thread at a time, at clamped indices, ahead of the reductions, which use DPP (as
+  // k_a8_quant: the group max and the fp32 sum of 64 integer codes are exact in any order)
   float row_sx = 1.f;
   if (PT) {
     float mx = 0.f;
-    for (int i = tid; i < D; i += 256) mx = fmaxf(mx, fabsf(value(i)));
+    for (int i0 = 0; i0 < D; i0 += 256 * 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = value(min(i0 + 256 * j + tid, D - 1));
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        if (i0 + 256 * j + tid < D) mx = fmaxf(mx, fabsf(v[j]));
+    }
     mx = block_max4(mx, red);
     row_sx = mx > 0.f ? mx / 127.f : 1.f;
   }
-  for (int i0 = 0; i0 < D; i0 += 256) {
-    const int i = i0 + tid;
-    if (i0 + 64 * wave >= D) break;  // whole groups: D % 64 == 0
-    const float v = value(i);
-    float sx = row_sx;
-    if (!PT) {
-      const float amax = wave_max(fabsf(v));
-      sx = amax > 0.f ? amax / 127.f : 1.f;
-    }
-    const float q = rintf(v / sx);
-    U[i] = (int8_t)q;
-    const float qs = wave_sum(q);
-    if (lane == 0) {
-      const int g = i / kGroup;
-      XS[2 * g] = sx;
-      XS[2 * g + 1] = sx * qs;
+  for (int i00 = 0; i00 < D; i00 += 256 * 8) {
+    float vv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) vv[j] = value(min(i00 + 256 * j + tid, D - 1));
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int i0 = i00 + 256 * j, i = i0 + tid;
+      if (i0 + 64 * wave >= D) break;  // wave-uniform; whole groups: D % 64 == 0
+      const float v = vv[j];
+      float sx = row_sx;
+      if (!PT) {
+        const float amax = dpp_max_f(fabsf(v));
+        sx = amax > 0.f ? amax / 127.f : 1.f;
+      }
+      const float q = rintf(v / sx);
+      U[i] = (int8_t)q;
+      const float qs = dpp_sum_f(q);
+      if (lane == 0) {
+        const int g = i / kGroup;
+        XS[2 * g] = sx;
+        XS[2 * g + 1] = sx * qs;
+      }
     }
   }
 }

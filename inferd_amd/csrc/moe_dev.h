@@ -7,34 +7,6 @@
 
 namespace ifd {
 
-// Wave-wide max / min / sum with DPP: an inclusive scan within rows of 16 lanes (row_shr 1, 2, 4, 8), then across
-// rows (row_bcast 15 into rows 1 and 3, row_bcast 31 into rows 2 and 3), so lane 63 holds the result, which
-// readlane makes wave-uniform. Lanes a step has no source for keep the identity. About a tenth of the latency of the
-// LDS-permute shuffles, which matters in the serial top-k loop.
-template <class Op>
-__device__ __forceinline__ int dpp_reduce_i(int v, int id, Op op) {
-  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x111, 0xf, 0xf, false));  // row_shr:1
-  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x112, 0xf, 0xf, false));  // row_shr:2
-  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x114, 0xf, 0xf, false));  // row_shr:4
-  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x118, 0xf, 0xf, false));  // row_shr:8
-  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
-  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
-  return __builtin_amdgcn_readlane(v, 63);
-}
-__device__ __forceinline__ float dpp_max_f(float v) {
-  return __int_as_float(dpp_reduce_i(__float_as_int(v), __float_as_int(-INFINITY), [](int a, int b) {
-    return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
-  }));
-}
-__device__ __forceinline__ float dpp_sum_f(float v) {
-  return __int_as_float(dpp_reduce_i(__float_as_int(v), 0, [](int a, int b) {
-    return __float_as_int(__int_as_float(a) + __int_as_float(b));
-  }));
-}
-__device__ __forceinline__ int dpp_min_i(int v) {
-  return dpp_reduce_i(v, 0x7fffffff, [](int a, int b) { return min(a, b); });
-}
-
 // v[i]: logit i * 64 + lane of the token (lanes past E: anything). On return lane 0 holds the picks: who[j], p[j]
 // (j < k <= 16).
 __device__ __forceinline__ void route_token(float (&v)[8], int E, int k, int norm, int (&who)[16], float (&p)[16]) {

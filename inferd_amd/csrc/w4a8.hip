@@ -22,41 +22,87 @@ namespace ifd {
 // xq = rint(x / sx) (IEEE division and round-half-even: bit-identical to the CPU reference), XS = (sx, sx * sum xq).
 // form 2 (the reference's qa8_quant, qa8.metal:30-49): per 64-group, xq = clamp(rint(x * (127 / amax)), +-127) (0
 // when amax == 0), XS = (amax / 127, amax / 127 * sum xq); stored in natural K order.
+// Lane layout: a lane takes 8 consecutive elements (one 16-byte load), so 8 consecutive lanes hold one 64-group and
+// a wave 8 groups per pass. The group max and sum are three DPP steps within those 8 lanes (quad swaps, then the
+// half-row mirror). The group max is exact in any order, and so is the fp32 sum of 64 integer codes (|sum| <= 8128):
+// the bits do not depend on the layout. (One element per lane and a 64-lane shuffle reduction per group left each
+// wave bound by the reductions' latency.)
+template <class Op>
+__device__ __forceinline__ float dpp_reduce8_f(float v, Op op) {
+  v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false)));  // quad_perm 1,0,3,2
+  v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false)));  // quad_perm 2,3,0,1
+  v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false)));  // row_half_mirror
+  return v;
+}
 __global__ __launch_bounds__(256) void k_a8_quant(const uint16_t* __restrict__ A, int lda, int K, int form,
                                                   int8_t* __restrict__ U, float* __restrict__ XS) {
   const int per_token = form == 1;
   __shared__ float red[4];
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint16_t* a = A + (size_t)m * lda;
-  const int G = K / kGroup;
+  const int G = K / kGroup, nc = K / 8;  // 16-byte chunks; chunk c is part c % 8 of group c / 8
+  auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
+  auto add_op = [](float x, float y) { return x + y; };
+  auto unpack = [](const u32x4& w, float (&x)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      x[2 * e] = __uint_as_float(w[e] << 16);
+      x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+    }
+  };
   float row_sx = 1.f;
   if (per_token) {
     float mx = 0.f;
-    for (int k = tid; k < K; k += 256) mx = fmaxf(mx, fabsf(bf2f(a[k])));
+    for (int c = tid; c < nc; c += 256) {
+      float x[8];
+      unpack(*(const u32x4*)(a + 8 * c), x);
+#pragma unroll
+      for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(x[e]));
+    }
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     row_sx = mx > 0.f ? mx / 127.f : 1.f;
   }
-  for (int g = wave; g < G; g += 4) {
-    const float x = bf2f(a[g * kGroup + lane]);
-    float sx = row_sx, q;
+  // a pass covers 256 chunks = 32 groups; the 8 lanes of a group are live or not together (nc % 8 == 0)
+  for (int c = tid; c < nc; c += 256) {
+    float x[8];
+    unpack(*(const u32x4*)(a + 8 * c), x);
+    float sx = row_sx, q[8];
     if (form == 2) {
-      const float amax = wave_max(fabsf(x));
+      float amax = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(x[e]));
+      amax = dpp_reduce8_f(amax, fmax_op);
       const float inv = amax > 0.f ? 127.f / amax : 0.f;
-      q = fminf(fmaxf(rintf(x * inv), -127.f), 127.f);
+#pragma unroll
+      for (int e = 0; e < 8; e++) q[e] = fminf(fmaxf(rintf(x[e] * inv), -127.f), 127.f);
       sx = amax / 127.f;
     } else {
       if (!per_token) {
-        const float amax = wave_max(fabsf(x));
+        float amax = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(x[e]));
+        amax = dpp_reduce8_f(amax, fmax_op);
         sx = amax > 0.f ? amax / 127.f : 1.f;
       }
-      q = rintf(x / sx);
+#pragma unroll
+      for (int e = 0; e < 8; e++) q[e] = rintf(x[e] / sx);
     }
-    U[(size_t)m * K + g * kGroup + lane] = (int8_t)q;
-    const float qs = wave_sum(q);
-    if (lane == 0) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      lo |= ((uint32_t)(int)q[e] & 0xFFu) << (8 * e);
+      hi |= ((uint32_t)(int)q[4 + e] & 0xFFu) << (8 * e);
+    }
+    *(uint2*)(U + (size_t)m * K + 8 * c) = make_uint2(lo, hi);
+    float qs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) qs += q[e];
+    qs = dpp_reduce8_f(qs, add_op);
+    if ((c & 7) == 0) {
+      const int g = c >> 3;
       XS[((size_t)m * G + g) * 2] = sx;
       XS[((size_t)m * G + g) * 2 + 1] = sx * qs;
     }

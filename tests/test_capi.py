@@ -112,6 +112,10 @@ def test_new_entry_points_reject_bad_arguments():
     assert L.ifd_qmm_w8a8(4096, 4096, 0, 4096, 4096, 4096, 64, 100, 0, 0, 4096, 64, 4, 0, None, 0, None) == E
     # quantizer forms 0, 1, 2 only
     assert L.ifd_a8_quant(4096, 128, 4, 128, 3, 4096, 4096, None) == E and b"per_token=3" in L.ifd_last_error()
+    # 16-byte activation loads and 8-byte code stores: aligned A, lda % 8 == 0, aligned U
+    assert L.ifd_a8_quant(4098, 128, 4, 128, 0, 4096, 4096, None) == E and b"aligned" in L.ifd_last_error()
+    assert L.ifd_a8_quant(4096, 132, 4, 128, 0, 4096, 4096, None) == E and b"lda=132" in L.ifd_last_error()
+    assert L.ifd_a8_quant(4096, 128, 4, 128, 0, 4100, 4096, None) == E and b"aligned" in L.ifd_last_error()
     # decode MoE: at most 8 tokens, H a multiple of 512, k <= 16, no shared gate without a shared expert
     args = [4096, 9, 2048, 4096, 512, 10, 1, 0, 4096, 4096, 4096, 4096, 4096, 4096, 512,
             None, None, None, None, None, None, 4096, 0, None, None, None, None, None, 0, None]
