@@ -6,9 +6,13 @@ K = 17408), all through the C ABI (libinferd_amd.so). Weights are seeded synthet
 (q ~ U{0..15}, s ~ U(0.005, 0.02) bf16, b = bf16(-8 s)); activations bf16 N(0, 1). Weight copies are rotated so the
 timed loop streams >= 3x the 256 MB Infinity Cache, as the reference cycles copies (engine/tools/moe_bench.mm:4-5).
 
-value = algorithmic HBM bytes of the step / step time (GB/s): 150,405,120 weight bytes per M plus 229,376 activation
-bytes per row (A, the gate/up output written and read, the SwiGLU output written and read, the result).
-The other BASELINE configs are reported under "breakdown" (prefill TFLOP/s, W4A8 TOPS, MoE tok/s, config-0 GB/s).
+value = algorithmic HBM bytes of the step / step time (GB/s): 150,405,120 weight bytes per M plus 90,112 activation
+bytes per row (A in, the SwiGLU output written and read, the result; the gate/up product is never stored). The
+reference's unfused count (229,376 B per row, with the gate/up product written and read) is reported beside it as
+value_unfused_count. Each call of a step reads a weight copy no call of the previous five MLPs read.
+The line also carries the measured HBM-read and MFMA ceilings of this GPU beside the datasheet peaks ("ceilings";
+roofline.peak_measured / frac_measured). The other BASELINE configs are reported under "breakdown" (prefill TFLOP/s,
+W4A8 TOPS, MoE tok/s, config-0 GB/s).
 """
 from __future__ import annotations
 
@@ -28,6 +32,8 @@ LLC_BYTES = 256 << 20
 
 H_DEC, I_DEC = 5120, 17408
 W_BYTES_PER_WEIGHT = 0.5625  # packed nibbles + bf16 scale and bias per 64
+ROW_BYTES_FUSED = (H_DEC + 2 * I_DEC + H_DEC) * 2  # A in, h out + in, y out: 90,112 B per row
+ROW_BYTES_UNFUSED = (H_DEC + 2 * 2 * I_DEC + 2 * I_DEC + H_DEC) * 2  # + the gate/up product out and in: 229,376 B
 
 
 def parse():
@@ -90,6 +96,27 @@ def main():
     out = {}
     Ms = (1, 8, 32, 128)
 
+    # ---- measured ceilings on this GPU, beside the datasheet peaks: one coalesced read of a 2 GiB buffer (8x the
+    # Infinity Cache) and MFMA-only loops of the two shapes the kernels use (bf16 32x32x16, int8 32x32x32), each on
+    # 512 blocks of 4 waves (two waves per SIMD)
+    ceilings = {}
+    if args.only in ("", "ceilings"):
+        big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+        big.fill_(1)
+        sink = torch.zeros(4096, dtype=torch.uint8, device=dev)
+        ms = timed(lambda i: ops.probe_stream_read(big, sink), 10, 2)
+        ceilings["hbm_read_gbs"] = big.numel() / (ms * 1e-3) / 1e9
+        del big
+        mo = torch.empty(512 * 256, dtype=torch.float32, device=dev)
+        for int8, key, scale in ((False, "bf16_mfma_tflops", 1e12), (True, "int8_mfma_tops", 1e12)):
+            ops_n = ops.probe_mfma(int8, 2000, 512, mo)
+            ms = timed(lambda i: ops.probe_mfma(int8, 2000, 512, mo), 5, 1)
+            ceilings[key] = ops_n / (ms * 1e-3) / scale
+        out["ceilings"] = ceilings
+        if args.only == "ceilings":
+            print(json.dumps({k: round(v, 1) for k, v in ceilings.items()}), flush=True)
+            return
+
     if args.only == "copy":
         # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain device copy of exactly 256 MiB each way
         src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).normal_(generator=gen)
@@ -115,15 +142,16 @@ def main():
         Hh = {M: torch.empty((M, I_DEC), dtype=torch.bfloat16, device=dev) for M in Ms}
         Y = {M: torch.empty((M, H_DEC), dtype=torch.bfloat16, device=dev) for M in Ms}
 
-        def mlp(M, i):
-            # gate_up with its SwiGLU in one call (the reference's gemm + silu_mul pair), then down
-            gu, dn = layers[i % ncp]
+        def mlp(M, c):
+            # gate_up with its SwiGLU in one call (the reference's gemm + silu_mul pair), then down, on weight copy c
+            gu, dn = layers[c % ncp]
             ops.gemm_t64_swiglu(A[M], gu, out=Hh[M])
             ops.gemm_t64(Hh[M], dn, Y[M])
 
         def step(i):
-            for M in Ms:
-                mlp(M, i)
+            # every call of the step reads a copy no call of the previous ncp - 1 MLPs read (ncp x 150 MB > 3 x LLC)
+            for j, M in enumerate(Ms):
+                mlp(M, i * len(Ms) + j)
 
         for i in range(args.warmup):
             step(i)
@@ -135,10 +163,12 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         ms_step = e0.elapsed_time(e1) / args.steps
-        # the workload's bytes per row: the activation traffic of gemm -> silu_mul -> gemm (x, gate_up out, its
-        # re-read, h, its re-read, y), fixed so that values compare across implementations; the fused call skips the
-        # gate_up round trip
-        step_bytes = sum(w_bytes + M * 229376 for M in Ms)
+        # the bytes the step's calls move at minimum: weights, plus per row A in, h out and in, y out (the SwiGLU is
+        # fused into gate_up, which never stores its product): 90,112 B. The reference's unfused sequence
+        # gemm -> silu_mul -> gemm also writes and re-reads the gate/up product (229,376 B per row); that count is
+        # reported beside it, labelled, never as the value.
+        step_bytes = sum(w_bytes + M * ROW_BYTES_FUSED for M in Ms)
+        step_bytes_unfused = sum(w_bytes + M * ROW_BYTES_UNFUSED for M in Ms)
         value = step_bytes / (ms_step * 1e-3) / 1e9
 
         # per-call timing (HIP events on the launch stream): the dominant call is the roofline kernel; bytes are each
@@ -162,7 +192,8 @@ def main():
         dom = max(calls, key=lambda k: calls[k][0])
         ms_d, b_d, f_d = calls[dom]
         achieved = b_d / (ms_d * 1e-3) / 1e9
-        out["headline"] = dict(ms_step=ms_step, value=value, step_bytes=step_bytes, copies=ncp)
+        out["headline"] = dict(ms_step=ms_step, value=value, step_bytes=step_bytes, copies=ncp,
+                               value_unfused_count=step_bytes_unfused / (ms_step * 1e-3) / 1e9)
         out["dominant"] = dict(name=dom, ms=ms_d, bytes=b_d, flops=f_d, gbs=achieved,
                                tflops=f_d / (ms_d * 1e-3) / 1e12)
         out["per_M"] = {
@@ -309,23 +340,23 @@ def main():
 
         gw = (h32(gu.wq), h16(gu.s), h16(gu.b))
         dw = (h32(dn.wq), h16(dn.s), h16(dn.b))
-        # sample: whole decode-MLP passes at M = 1, 8, 32 (the oracle's qmv semantics, all weights streamed each
-        # pass), repeated until ~10 s of CPU work; the same metric (algorithmic bytes / time)
+        # sample: whole headline steps (the decode MLP at M = 1, 8, 32, 128, every weight streamed by every pass, the
+        # oracle's qmv arithmetic), repeated until at least 10 s of CPU work; the same metric and byte count as value
         rng = np.random.default_rng(0)
         t0 = time.perf_counter()
-        nbytes, passes = 0, []
+        nbytes, nsteps = 0, 0
         while time.perf_counter() - t0 < 10.0:
-            for M in (1, 8, 32):
+            for M in Ms:
                 Ah = orc.f32_to_bf16(rng.standard_normal((M, H_DEC)).astype(np.float32))
                 gy = orc.qmv(Ah, *gw, nthreads=ncores)
                 hh = orc.silu_mul(orc.f32_to_bf16(gy))
                 orc.qmv(hh, *dw, nthreads=ncores)
-                nbytes += (2 * I_DEC * H_DEC + H_DEC * I_DEC) * W_BYTES_PER_WEIGHT + M * 229376
-                passes.append(M)
+                nbytes += (2 * I_DEC * H_DEC + H_DEC * I_DEC) * W_BYTES_PER_WEIGHT + M * ROW_BYTES_FUSED
+            nsteps += 1
         dt = time.perf_counter() - t0
         cpu = dict(value=nbytes / dt / 1e9, unit="GB/s", cores=ncores, kind="port",
-                   sample=f"{len(passes)} decode-MLP passes at M in (1, 8, 32) (gate_up 5120->34816, SwiGLU, down "
-                          f"17408->5120), oracle qmv semantics on {ncores} threads, {dt:.1f} s")
+                   sample=f"{nsteps} headline steps (decode MLP at M = 1, 8, 32, 128: gate_up 5120->34816, SwiGLU, "
+                          f"down 17408->5120), the oracle's qmv arithmetic on {ncores} threads, {dt:.1f} s")
 
     line = {
         "metric": "W4 qmatmul HBM GB/s at decode M<=128; TFLOP/s at prefill M=4096; MoE tok/s",
@@ -348,10 +379,15 @@ def main():
         # bf16 MFMA peak
         mfma = d["flops"] / (BF16_PEAK_TFLOPS * 1e12) > d["bytes"] / (HBM_PEAK_GBS * 1e9)
         ach, peak = (d["tflops"], BF16_PEAK_TFLOPS) if mfma else (d["gbs"], HBM_PEAK_GBS)
-        return {"kernel": d["name"], "bound": "mfma" if mfma else "hbm", "achieved": round(ach, 1), "peak": peak,
-                "unit": "TFLOP/s" if mfma else "GB/s", "frac": round(ach / peak, 4),
-                "traffic": measured_traffic.get(d["name"]),
-                "us": round(d["ms"] * 1e3, 2), "gbs": round(d["gbs"], 1), "tflops": round(d["tflops"], 1)}
+        r = {"kernel": d["name"], "bound": "mfma" if mfma else "hbm", "achieved": round(ach, 1), "peak": peak,
+             "unit": "TFLOP/s" if mfma else "GB/s", "frac": round(ach / peak, 4),
+             "traffic": measured_traffic.get(d["name"]),
+             "us": round(d["ms"] * 1e3, 2), "gbs": round(d["gbs"], 1), "tflops": round(d["tflops"], 1)}
+        pm = ceilings.get("bf16_mfma_tflops" if mfma else "hbm_read_gbs")
+        if pm:  # the same achieved figure against this GPU's measured ceiling
+            r["peak_measured"] = round(pm, 1)
+            r["frac_measured"] = round(ach / pm, 4)
+        return r
 
     if "headline" in out:
         h, d = out["headline"], out["dominant"]
@@ -362,11 +398,16 @@ def main():
                                    "SwiGLU, down 17408->5120, 4-bit g64 weights in the T64 layout",
                        "weight_copies": h["copies"]},
             "roofline": roofline(d),
+            "value_unfused_count": round(h["value_unfused_count"], 1),
             "per_M": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in out["per_M"].items()},
             "mlp_block": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in out["mlp_block"].items()},
         })
     if cpu:
         line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()}
+    if ceilings:
+        line["ceilings"] = {"measured": {k: round(v, 1) for k, v in ceilings.items()},
+                            "datasheet": {"hbm_read_gbs": HBM_PEAK_GBS, "bf16_mfma_tflops": BF16_PEAK_TFLOPS,
+                                          "int8_mfma_tops": INT8_PEAK_TOPS}}
     if "breakdown" in out:
         line["breakdown"] = json.loads(json.dumps(out["breakdown"]), parse_float=lambda x: round(float(x), 4))
     print(json.dumps(line), flush=True)

@@ -46,6 +46,15 @@ int ifd_version(void);
 const char* ifd_status_str(int status);
 const char* ifd_last_error(void);
 
+/* ---- workspace counter header (no counterpart in the reference, whose split-K scratch holds no counters) -------
+ * ifd_workspace_check synchronises `stream`, reads the first 4096 bytes of the workspace and returns IFD_OK when
+ * every counter is zero, IFD_ERR_WORKSPACE (with the first non-zero counter in ifd_last_error()) otherwise. A call
+ * that failed after a partial launch, or a kernel that did not finish, can leave counters non-zero, and later
+ * split-K results on that workspace would be wrong. ifd_workspace_reset zeroes the header on `stream` with a fill
+ * kernel (no memset node: it may be captured into a HIP graph). ws_bytes >= 4096. */
+int ifd_workspace_check(const void* workspace, size_t ws_bytes, void* stream);
+int ifd_workspace_reset(void* workspace, size_t ws_bytes, void* stream);
+
 /* ---- dense linears (reference Qwen35::gemm and its sub-paths, engine/src/qwen35.h:1465-1558) ---------------- */
 
 /* Bytes of workspace ifd_gemm_w4 / ifd_qmv_w4 / ifd_qmm_w4 need for this shape (split-K partials). */
@@ -251,6 +260,16 @@ int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int 
                    const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b,
                    void* out, int assign, int* idx, float* wt, float* sg, float* logits, void* workspace,
                    size_t ws_bytes, void* stream);
+
+/* ---- measurement probes (outside the operator path) ----------------------------------------------------------
+ * The HBM and MFMA ceilings a benchmark reports beside the datasheet peaks, in the role of the reference's
+ * micro-benchmarks (bw_read, micro/kernels.metal:8-16; fma_rate, micro/fma_rate.mm).
+ * ifd_probe_stream_read reads `bytes` of src once (coalesced 1 KB wave loads, `blocks` blocks of 256 threads); sink
+ * (4096 bytes) is written only in a case that cannot occur. ifd_probe_mfma runs `blocks` blocks of 4 waves, each wave
+ * 8 independent chains of `iters` MFMAs on register operands: int8 = 0 v_mfma_f32_32x32x16_bf16 (32768 FLOP each),
+ * 1 v_mfma_i32_32x32x32_i8 (65536 OP each); out float [blocks * 256]. */
+int ifd_probe_stream_read(const void* src, size_t bytes, void* sink, int blocks, void* stream);
+int ifd_probe_mfma(int int8, int iters, int blocks, float* out, void* stream);
 
 #ifdef __cplusplus
 }

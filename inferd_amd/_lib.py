@@ -23,6 +23,10 @@ SIGNATURES = {
     "ifd_version": (_i, []),
     "ifd_status_str": (ctypes.c_char_p, [_i]),
     "ifd_last_error": (ctypes.c_char_p, []),
+    "ifd_workspace_check": (_i, [_vp, _sz, _vp]),
+    "ifd_workspace_reset": (_i, [_vp, _sz, _vp]),
+    "ifd_probe_stream_read": (_i, [_vp, _sz, _vp, _i, _vp]),
+    "ifd_probe_mfma": (_i, [_i, _i, _i, _vp, _vp]),
     "ifd_gemm_w4_workspace": (_sz, [_i, _i, _i]),
     "ifd_qmv_w4": (_i, _GEMM_ARGS),
     "ifd_qmm_w4": (_i, _GEMM_ARGS),

@@ -14,7 +14,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libinferd_amd.so")
 OBJ = os.path.join(HERE, "_build")
 
-SOURCES = ["qmv.hip", "qmm.hip", "w4a8.hip", "moe.hip", "t64.hip", "gemm_t64.hip", "gemm_sk.hip", "gemm_t8.hip", "w4a8_t64.hip", "fused.hip", "moe_dec.hip", "capi.hip", "qwen35_ops.hip"]
+SOURCES = ["qmv.hip", "qmm.hip", "w4a8.hip", "moe.hip", "t64.hip", "gemm_t64.hip", "gemm_sk.hip", "gemm_t8.hip",
+           "w4a8_t64.hip", "fused.hip", "moe_dec.hip", "capi.hip", "workspace.hip", "probe.hip"]
 
 # Packed-fp32 VALU forms are kept out of every code object; hipcc's host pass warns that it does not know the
 # feature, which is harmless.
@@ -42,7 +43,10 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
-    srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    missing = [s for s in SOURCES if not os.path.exists(os.path.join(CSRC, s))]
+    if missing:
+        raise RuntimeError(f"sources missing from {CSRC}: {missing}")
+    srcs = list(SOURCES)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = OUT + ".tmp"

@@ -465,6 +465,18 @@ int ifd_mlp_decode(void* x, int ldx, const void* norm_w, float eps, const void* 
   return launch_gemm_t(act, I, dn_t64, H, I, x, ldx, M, 1, w.body, G, st);
 }
 
+// ---- measurement probes ------------------------------------------------------------------------------------------
+int ifd_probe_stream_read(const void* src, size_t bytes, void* sink, int blocks, void* stream) {
+  IFD_CHECK(src && sink && aligned(src, 16) && aligned(sink, 16) && bytes % 16 == 0 && blocks > 0,
+            "probe_stream_read: 16-byte aligned src and sink, bytes %% 16 == 0, blocks > 0");
+  return launch_probe_read(src, bytes, sink, blocks, S(stream));
+}
+
+int ifd_probe_mfma(int int8, int iters, int blocks, float* out, void* stream) {
+  IFD_CHECK(out && iters > 0 && blocks > 0 && (int8 == 0 || int8 == 1), "probe_mfma: bad arguments");
+  return launch_probe_mfma(int8, iters, blocks, out, S(stream));
+}
+
 // ---- decode MoE (T <= 8) ---------------------------------------------------------------------------------------
 size_t ifd_moe_decode_workspace(int T, int H, int I, int E, int k) {
   if (T <= 0 || T > 8 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;

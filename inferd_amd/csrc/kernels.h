@@ -46,6 +46,11 @@ int launch_splitk_res_norm(const float* part, int S, uint16_t* x, int ldx, const
 // between calls: the caller zeroes them once when the workspace is allocated. Kernel scratch follows the header.
 constexpr size_t kWsHeader = 4096;
 constexpr int kWsCounters = (int)(kWsHeader / sizeof(unsigned));
+// Zeroes the kWsHeader-byte counter header at ws with a fill kernel on st (workspace.hip).
+int launch_zero_header(void* ws, hipStream_t st);
+// Measurement probes (probe.hip): a coalesced stream read of `bytes` and an MFMA-only loop.
+int launch_probe_read(const void* src, size_t bytes, void* sink, int blocks, hipStream_t st);
+int launch_probe_mfma(int int8, int iters, int blocks, float* out, hipStream_t st);
 
 // Library-internal store mode past the public 0 (bf16), 1 (bf16 residual add) and 2 (fp32): the GEMM's N columns are
 // [gate (N/2) | up (N/2)] and C receives the SwiGLU h [M][N/2] (ldc = its row stride), bit-identical to a mode-0 GEMM

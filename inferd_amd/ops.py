@@ -360,3 +360,25 @@ def mlp_decode(x: torch.Tensor, norm_w: torch.Tensor, eps: float, gu: T64Linear,
     check(lib().ifd_mlp_decode(_p(x), H, _p(norm_w), eps, _p(gu.wt), _p(dn.wt), M, H, I, _p(ws), ws.numel(),
                                _stream()))
     return x
+
+
+# ---- workspace header and measurement probes ----------------------------------------------------------------------
+def workspace_check(ws: torch.Tensor) -> None:
+    """Raises unless every counter of the workspace header (its first 4096 bytes) is zero (synchronises)."""
+    check(lib().ifd_workspace_check(_p(ws), ws.numel(), _stream()))
+
+
+def workspace_reset(ws: torch.Tensor) -> None:
+    """Zeroes the workspace's counter header on the current stream (a fill kernel)."""
+    check(lib().ifd_workspace_reset(_p(ws), ws.numel(), _stream()))
+
+
+def probe_stream_read(src: torch.Tensor, sink: torch.Tensor, blocks: int = 4096) -> None:
+    """One coalesced read of every byte of src (HBM read ceiling); sink: >= 4096 bytes on the device."""
+    check(lib().ifd_probe_stream_read(_p(src), src.numel() * src.element_size(), _p(sink), blocks, _stream()))
+
+
+def probe_mfma(int8: bool, iters: int, blocks: int, out: torch.Tensor) -> float:
+    """MFMA-only loop; returns the operations it performs (FLOP for bf16, OP for int8). out: float [blocks * 256]."""
+    check(lib().ifd_probe_mfma(1 if int8 else 0, iters, blocks, _p(out), _stream()))
+    return float(blocks) * 4 * 8 * iters * (65536 if int8 else 32768)

@@ -21,6 +21,26 @@ def gpu_available() -> bool:
         return False
 
 
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """The parity figures of the session: max |err| / RMS raw (nothing subtracted), net (the figure the bar applies
+    to: beyond the output's own rounding against an fp32 reference, or over the elements more than one bf16 step
+    from a bf16 reference) and, against bf16 references, the share of elements one step apart."""
+    from tests import gen
+    if not gen.RECORDS:
+        return
+    tr = terminalreporter
+    tr.write_sep("-", "parity: max|err|/RMS(ref) raw / net (bar) / 1- and 2-step shares")
+    worst_ratio = 0.0
+    for tid, what, raw, net, ulp1, tol, ulp2 in gen.RECORDS:
+        u = "" if ulp1 is None else f"  ulp1 {ulp1:.4f}  ulp2 {ulp2:.5f}"
+        tr.write_line(f"{tid} [{what}]  raw {raw:.3e}  net {net:.3e} (<= {tol:.0e}){u}")
+        worst_ratio = max(worst_ratio, net / tol)
+    raws = [r[2] for r in gen.RECORDS]
+    u1 = [r[4] for r in gen.RECORDS if r[4] is not None]
+    tr.write_line(f"{len(gen.RECORDS)} checks; largest net/bar {worst_ratio:.3f}; largest raw {max(raws):.3e}"
+                  + (f"; largest 1-ulp share {max(u1):.4f}" if u1 else ""))
+
+
 def pytest_collection_modifyitems(config, items):
     if gpu_available():
         return

@@ -54,9 +54,17 @@ namespace {
 
 int failures = 0;
 
+// The figures of the last bf16_err call, printed by report(): raw = max |got - ref| / RMS(ref) with nothing
+// subtracted; ulp1 = the share of elements exactly one bf16 step from a bf16 reference (-1 for an fp32 reference).
+double g_raw = 0, g_ulp1 = -1, g_ulp2 = -1, g_far = -1, g_rel_rms = 0;
+
+// err: the figure the bar applies to (net); raw and the one-step share are those of the last bf16_err call
 void report(bool pass, const std::string& what, double err) {
-  printf("%s %-60s err %.3e\n", pass ? "ok  " : "FAIL", what.c_str(), err);
+  printf("%s %-60s net %.3e raw %.3e", pass ? "ok  " : "FAIL", what.c_str(), err, g_raw);
+  if (g_ulp1 >= 0) printf(" ulp1 %.4f ulp2 %.5f far %.1e rel_rms %.1e", g_ulp1, g_ulp2, g_far, g_rel_rms);
+  printf("\n");
   fflush(stdout);
+  g_raw = 0, g_ulp1 = -1, g_ulp2 = -1, g_far = -1, g_rel_rms = 0;
   if (!pass) failures++;
 }
 
@@ -88,18 +96,42 @@ std::vector<T> download(const BufRef& r, size_t n) {
   return v;
 }
 
-// max |got - ref| / RMS(ref), less half a bf16 step of ref (one step when ref is itself bf16)
+// bf16 values -> integers in value order (adjacent bf16 values differ by 1)
+int ord16(uint16_t h) { return (h & 0x8000) ? -(int)(h & 0x7FFF) : (int)(h & 0x7FFF); }
+
+// BASELINE's max |err| / RMS(ref) on a bf16 output. Against an fp32 reference: less half a bf16 step of ref (a
+// correctly rounded output is within half a step of the value it rounds). Against a bf16 reference: over the
+// elements more than one bf16 step away, with no slack; the shares one, two and more steps away go to g_ulp1,
+// g_ulp2 and g_far, RMS(got - ref) / RMS(ref) to g_rel_rms (the figures a chain of bf16 stages compared end to end
+// is held to, since no per-element bar holds there).
 double bf16_err(const std::vector<uint16_t>& got, const std::vector<float>& ref, bool ref_is_bf16) {
-  double ss = 0, worst = 0;
+  double ss = 0, worst = 0, raw = 0, se = 0;
+  size_t one = 0, two = 0, far = 0;
   for (float r : ref) ss += (double)r * r;
   const double rms = std::sqrt(ss / std::max<size_t>(ref.size(), 1));
   for (size_t i = 0; i < ref.size(); i++) {
     const double r = ref[i];
-    const double ulp = r == 0 ? 0 : std::ldexp(1.0, std::ilogb(r) - 7);
-    const double e = std::fabs(bf2f(got[i]) - r) - (ref_is_bf16 ? ulp : 0.5 * ulp);
-    worst = std::max(worst, e);
+    const double d = std::fabs(bf2f(got[i]) - r);
+    raw = std::max(raw, d);
+    se += d * d;
+    if (ref_is_bf16) {
+      const int steps = std::abs(ord16(got[i]) - ord16(f2bf(ref[i])));
+      if (steps == 1) one++;
+      if (steps == 2) two++;
+      if (steps > 2) far++;
+      if (steps > 1) worst = std::max(worst, d);
+    } else {
+      const double ulp = r == 0 ? 0 : std::ldexp(1.0, std::ilogb(r) - 7);
+      worst = std::max(worst, d - 0.5 * ulp);
+    }
   }
-  return worst / (rms > 0 ? rms : 1);
+  const double div = rms > 0 ? rms : 1;
+  g_raw = raw / div;
+  g_ulp1 = ref_is_bf16 ? (double)one / std::max<size_t>(ref.size(), 1) : -1;
+  g_ulp2 = ref_is_bf16 ? (double)two / std::max<size_t>(ref.size(), 1) : -1;
+  g_far = ref_is_bf16 ? (double)far / std::max<size_t>(ref.size(), 1) : -1;
+  g_rel_rms = std::sqrt(se / std::max<size_t>(ref.size(), 1)) / div;
+  return worst / div;
 }
 
 struct HostLinear {
@@ -360,8 +392,11 @@ void test_encode_moe(std::mt19937& rng) {
                       sgu.b.data(), sdn.wq.data(), sdn.s.data(), sdn.b.data(), T <= 32 ? 1 : 0, want.data(), 0, 0);
     std::vector<float> wf(want.size());
     for (size_t i = 0; i < want.size(); i++) wf[i] = bf2f(want[i]);
-    const double ex = bf16_err(x1, wf, true);
-    report(ex <= 1e-2, "encode_moe x += moe(xn)" + tag, ex);
+    // a chain of bf16 stages on both sides, compared end to end: RMS error, raw and the one-step share are bounded
+    // (the stages themselves are checked one by one at the bar in tests/test_gpu_moe.py)
+    (void)bf16_err(x1, wf, true);
+    report(g_rel_rms <= 1e-2 && g_raw <= 5e-2 && g_ulp1 <= 0.05,
+           "encode_moe x += moe(xn) (end to end)" + tag, g_raw);
   }
   (void)hipFree(sgu_t64);
 }

@@ -1,5 +1,7 @@
 """GPU checks of the T64 weight layout: the repack is bit-exact against a numpy restatement of the layout, and
 GEMMs on T64 weights match the CPU oracle (decode GEMV semantics) through the C ABI."""
+import functools
+
 import numpy as np
 import pytest
 
@@ -40,8 +42,7 @@ def test_gemm_t64_decode(M, N, K):
     T = ops.pack_t64(g.qlinear(wq, s, b))
     out = g.host(ops.gemm_t64(g.dev(A), T))
     Y = orc.qmv(A, wq, s, b)
-    err = gen.bf16_err(out, Y)
-    assert err <= 1e-2, (M, N, K, err)
+    gen.check_bf16(out, Y, 1e-2, (M, N, K))
 
 
 @pytest.mark.parametrize("mode", [1, 2])
@@ -54,8 +55,7 @@ def test_gemm_t64_modes(mode):
     T = ops.pack_t64(g.qlinear(wq, s, b))
     out = g.host(ops.gemm_t64(g.dev(A), T, g.dev(C0) if mode == 1 else None, mode=mode))
     Y = orc.qmv(A, wq, s, b)
-    err = gen.rel_err(out, Y) if mode == 2 else gen.bf16_err(out, Y + gen.bf16_to_f32(C0))
-    assert err <= 1e-2, err
+    gen.check_out(out, Y if mode == 2 else Y + gen.bf16_to_f32(C0), 1e-2, mode, fp32=mode == 2)
 
 
 def _t64_semantics(M):
@@ -63,6 +63,96 @@ def _t64_semantics(M):
     rows), bf16 dequant (MLX qmm, which the reference runs above them) beyond. The K-split fallback for shapes past
     the counter header keeps the affine form up to 64 rows; the two forms agree well within the bar."""
     return orc.qmv if M <= 16 else orc.qmm
+
+
+def _t64_arith(M, N, K, cus=256):
+    """The oracle form of the arithmetic ifd_gemm_t64 routes an M x [N, K] product to (capi.hip, gemm_t64.hip,
+    gemm_sk.hip): the decode GEMV's affine form (qmv4: s sum q x + b sum x) in the decode kernel (M <= 16) and in
+    the K-split kernel's 32- and 64-row tiles; bf16(s q + b) dequant (MLX qmm) in the prefill tiles, the stream-K
+    kernel and the K-split kernel's 128-row tiles."""
+    if M <= 16:
+        return orc.qmv
+    bands = (N + 31) // 32
+    if ((M + 255) // 256) * ((bands + 7) // 8) >= cus:
+        return orc.qmm
+    mt = 1 if M <= 32 else 2 if M <= 64 else 4
+    if ((M + 32 * mt - 1) // (32 * mt)) * ((bands + 7) // 8) * 3 >= cus or 64 < M <= 128:
+        return orc.qmm
+    return orc.qmm if mt == 4 else orc.qmv
+
+
+# ---- exactly what bench.py times: config 1's two products at its four M ----------------------------------------
+BENCH_MS = [1, 8, 32, 128]
+H1, I1 = 5120, 17408
+
+
+@functools.lru_cache(maxsize=None)
+def _config1_weights():
+    """Seeded config-1 layer (gate_up [2 I, H] with gate rows first, down [H, I]), host arrays."""
+    _, wg, sg_, bg = gen.qlinear(2 * I1, H1, seed=1000)
+    _, wd, sd, bd = gen.qlinear(H1, I1, seed=1001)
+    return (wg, sg_, bg), (wd, sd, bd)
+
+
+@functools.lru_cache(maxsize=None)
+def _config1_t64():
+    g, ops = _gu(), _ops()
+    (wg, sg_, bg), (wd, sd, bd) = _config1_weights()
+    return ops.pack_t64(g.qlinear(wg, sg_, bg)), ops.pack_t64(g.qlinear(wd, sd, bd))
+
+
+def _rows_of(lin, rows):
+    return tuple(np.ascontiguousarray(a[rows]) for a in lin)
+
+
+@pytest.mark.parametrize("M", BENCH_MS)
+def test_gemm_t64_swiglu_bench_shapes(M):
+    """bench.py's gate_up + SwiGLU call (N = 2 x 17408, K = 5120) at each of its M, every row, against the oracle on
+    768 h columns (gate rows c and up rows I + c): h = silu_mul(bf16(A . W^T)) with the GEMM in the arithmetic of its
+    route. Columns cover the first and last tiles and tile edges."""
+    g, ops = _gu(), _ops()
+    gu_w, _ = _config1_weights()
+    GU, _ = _config1_t64()
+    A = gen.activations(M, H1, seed=1100 + M)
+    h = g.host(ops.gemm_t64_swiglu(g.dev(A), GU))
+    rng = np.random.default_rng(M)
+    cols = np.unique(np.concatenate([np.arange(0, 128), np.arange(I1 - 128, I1), rng.choice(I1, 512, replace=False)]))
+    y = _t64_arith(M, 2 * I1, H1)(A, *_rows_of(gu_w, np.concatenate([cols, I1 + cols])))
+    ref = orc.silu_mul(gen.f32_to_bf16(y))
+    gen.check_bf16(h[:, cols], ref, 1e-2, M, ref_is_bf16=True)
+
+
+@pytest.mark.parametrize("M", BENCH_MS)
+def test_gemm_t64_down_bench_shapes(M):
+    """bench.py's down call (N = 5120, K = 17408) at each of its M, every row, against the oracle on 640 output
+    columns in the arithmetic of its route."""
+    g, ops = _gu(), _ops()
+    _, dn_w = _config1_weights()
+    _, DN = _config1_t64()
+    A = gen.activations(M, I1, seed=1200 + M)
+    out = g.host(ops.gemm_t64(g.dev(A), DN))
+    rng = np.random.default_rng(M + 1)
+    cols = np.unique(np.concatenate([np.arange(0, 128), np.arange(H1 - 128, H1), rng.choice(H1, 384, replace=False)]))
+    y = _t64_arith(M, H1, I1)(A, *_rows_of(dn_w, cols))
+    gen.check_bf16(out[:, cols], y, 1e-2, M)
+
+
+@pytest.mark.parametrize("M", BENCH_MS)
+def test_mlp_decode_config1_matches_oracle(M):
+    """The dense decode MLP block at config 1's shapes, x += down(SwiGLU(gate_up(rmsnorm(x)))), against the oracle's
+    composition on 4 sampled rows (rows are independent through the block), each GEMM in its route's arithmetic."""
+    g, ops = _gu(), _ops()
+    gu_w, dn_w = _config1_weights()
+    GU, DN = _config1_t64()
+    x0 = gen.activations(M, H1, seed=1300 + M)
+    nw = gen.f32_to_bf16(np.random.default_rng(M + 2).uniform(0.5, 1.5, H1).astype(np.float32))
+    x = g.dev(x0)
+    ops.mlp_decode(x, g.dev(nw), 1e-6, GU, DN)
+    rows = np.unique(np.linspace(0, M - 1, 4).astype(int))
+    xr = np.ascontiguousarray(x0[rows])
+    h = orc.silu_mul(gen.f32_to_bf16(_t64_arith(M, 2 * I1, H1)(orc.rmsnorm(xr, nw, 1e-6), *gu_w)))
+    y = _t64_arith(M, H1, I1)(h, *dn_w)
+    gen.check_bf16(g.host(x)[rows], y + gen.bf16_to_f32(xr), 1e-2, M)
 
 
 @pytest.mark.parametrize("M", [17, 32, 33, 64, 65, 128, 129, 300])
@@ -73,8 +163,7 @@ def test_gemm_t64_rows(M, N, K):
     A = gen.activations(M, K, seed=M)
     T = ops.pack_t64(g.qlinear(wq, s, b))
     out = g.host(ops.gemm_t64(g.dev(A), T))
-    err = gen.bf16_err(out, _t64_semantics(M)(A, wq, s, b))
-    assert err <= 1e-2, (M, N, K, err)
+    gen.check_bf16(out, _t64_semantics(M)(A, wq, s, b), 1e-2, (M, N, K))
 
 
 @pytest.mark.parametrize("M,mode", [(40, 1), (128, 2), (260, 1)])
@@ -87,8 +176,7 @@ def test_gemm_t64_big_modes(M, mode):
     T = ops.pack_t64(g.qlinear(wq, s, b))
     out = g.host(ops.gemm_t64(g.dev(A), T, g.dev(C0) if mode == 1 else None, mode=mode))
     Y = _t64_semantics(M)(A, wq, s, b)
-    err = gen.rel_err(out, Y) if mode == 2 else gen.bf16_err(out, Y + gen.bf16_to_f32(C0))
-    assert err <= 1e-2, err
+    gen.check_out(out, Y if mode == 2 else Y + gen.bf16_to_f32(C0), 1e-2, (M, mode), fp32=mode == 2)
 
 
 @pytest.mark.parametrize("M", [32, 128])
@@ -100,8 +188,7 @@ def test_gemm_t64_decode_mlp_sampled(M):
         A = gen.activations(M, K, seed=seed + M)
         out = g.host(ops.gemm_t64(g.dev(A), ops.pack_t64(g.qlinear(wq, s, b))))
         rows = np.unique(np.linspace(0, M - 1, 8).astype(int))
-        err = gen.bf16_err(out[rows], _t64_semantics(M)(A[rows], wq, s, b))
-        assert err <= 1e-2, (M, N, K, err)
+        gen.check_bf16(out[rows], _t64_semantics(M)(A[rows], wq, s, b), 1e-2, (M, N, K))
 
 
 def test_gemm_t64_config2_sampled():
@@ -112,8 +199,7 @@ def test_gemm_t64_config2_sampled():
     A = gen.activations(M, K, seed=34, row_scale=True)
     out = g.host(ops.gemm_t64(g.dev(A), ops.pack_t64(g.qlinear(wq, s, b))))
     rows = np.linspace(0, M - 1, 16).astype(int)
-    err = gen.bf16_err(out[rows], orc.qmm(A[rows], wq, s, b))
-    assert err <= 1e-2, err
+    gen.check_bf16(out[rows], orc.qmm(A[rows], wq, s, b), 1e-2, "config 2")
 
 
 def test_split_k_is_deterministic():
@@ -132,7 +218,7 @@ def test_split_k_is_deterministic():
         assert all(np.array_equal(outs[0], o) for o in outs[1:]), (M, N, K)
         rows = np.arange(0, M, max(1, M // 4))
         Y = _t64_semantics(M)(np.ascontiguousarray(g.host(A)[rows]), wq, s, b)
-        assert gen.bf16_err(outs[0][rows], Y) <= 1e-2, (M, N, K)
+        gen.check_bf16(outs[0][rows], Y, 1e-2, (M, N, K))
 
 
 @pytest.mark.parametrize("M,N,K,mode", [
@@ -168,13 +254,7 @@ def test_gemm_t64_stream_k(M, N, K, mode):
     rows = np.unique(np.linspace(0, M - 1, 8).astype(int))
     Y = orc.qmm(np.ascontiguousarray(A[rows]), wq, s, b)
     out = outs[0][rows]
-    if mode == 2:
-        err = gen.rel_err(out, Y)
-    elif mode == 1:
-        err = gen.bf16_err(out, Y + gen.bf16_to_f32(C0[rows]))
-    else:
-        err = gen.bf16_err(out, Y)
-    assert err <= 1e-2, (M, N, K, mode, err)
+    gen.check_out(out, Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y, 1e-2, (M, N, K, mode), fp32=mode == 2)
 
 
 @pytest.mark.parametrize("M,N,K,split", [
@@ -227,7 +307,7 @@ def test_gemm_t64_swiglu_matches_unfused(M, N, K, split):
         assert np.mean(fused == unfused) > 0.99
     rows = np.unique(np.linspace(0, M - 1, 8).astype(int))
     Y = _t64_semantics(M)(np.ascontiguousarray(g.host(A)[rows]), wq, s, b)
-    assert gen.bf16_err(gu[rows], Y) <= 1e-2
+    gen.check_bf16(gu[rows], Y, 1e-2, (M, N, K))
 
 
 def test_gemm_t64_swiglu_strided_output():
@@ -259,13 +339,7 @@ def test_gemm_t64_w4a8(M, N, K):
     for mode in (0, 1, 2):
         C = g.dev(C0) if mode == 1 else None
         out = g.host(ops.gemm_t64_w4a8(g.dev(U), g.dev(XS), T, C, mode=mode))
-        if mode == 0:
-            err = gen.bf16_err(out, Y)
-        elif mode == 1:
-            err = gen.bf16_err(out, Y + gen.bf16_to_f32(C0))
-        else:
-            err = gen.rel_err(out, Y)
-        assert err <= 2e-2, (M, N, K, mode, err)
+        gen.check_out(out, Y + gen.bf16_to_f32(C0) if mode == 1 else Y, 2e-2, (M, N, K, mode), fp32=mode == 2)
 
 
 def test_gemm_t64_w4a8_config3_sampled():
@@ -279,8 +353,7 @@ def test_gemm_t64_w4a8_config3_sampled():
     rows = np.linspace(0, M - 1, 16).astype(int)
     Ur, XSr = orc.a8_quant(A[rows], True)
     assert np.array_equal(g.host(U)[rows], Ur)
-    err = gen.bf16_err(out[rows], orc.w4a8(Ur, XSr, wq, s, b))
-    assert err <= 2e-2, err
+    gen.check_bf16(out[rows], orc.w4a8(Ur, XSr, wq, s, b), 2e-2, "config 3")
 
 
 def test_gemm_t64_w4a8_tail_split():
@@ -301,8 +374,7 @@ def test_gemm_t64_w4a8_tail_split():
     for mode in (0, 1, 2):
         out = g.host(ops.gemm_t64_w4a8(U, XS, T, g.dev(C0) if mode == 1 else None, mode=mode))[rows]
         ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
-        err = gen.rel_err(out, ref) if mode == 2 else gen.bf16_err(out, ref)
-        assert err <= 2e-2, (mode, err)
+        gen.check_out(out, ref, 2e-2, mode, fp32=mode == 2)
 
 
 def test_gemm_t64_prefill_tiles_with_tail():
@@ -319,8 +391,7 @@ def test_gemm_t64_prefill_tiles_with_tail():
     for mode in (0, 1, 2):
         out = g.host(ops.gemm_t64(g.dev(A), T, g.dev(C0) if mode == 1 else None, mode=mode))[rows]
         ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
-        err = gen.rel_err(out, ref) if mode == 2 else gen.bf16_err(out, ref)
-        assert err <= 1e-2, (mode, err)
+        gen.check_out(out, ref, 1e-2, mode, fp32=mode == 2)
 
 
 def test_gemm_t64_swiglu_prefill_tiles():
@@ -373,5 +444,4 @@ def test_mlp_decode_matches_oracle(M):
     sem = orc.qmv if M <= 64 else orc.qmm
     h = orc.silu_mul(gen.f32_to_bf16(sem(xn, wg, sg_, bg)))
     y = sem(h, wd, sd, bd)
-    err = gen.bf16_err(g.host(x), y + gen.bf16_to_f32(x0))
-    assert err <= 1e-2, (M, err)
+    gen.check_bf16(g.host(x), y + gen.bf16_to_f32(x0), 1e-2, M)

@@ -33,12 +33,9 @@ def _check(M, N, K, mode, seed, flipped=False, bias="minus128"):
     torch.cuda.synchronize()
     Y = orc.qmv(A, wq, s, b, bits=8) if M <= 32 else orc.qmm(A, wq, s, b, bits=8)
     got = g.host(out)
-    if mode == 2:
-        err = gen.rel_err(got, Y)
-    else:
-        err = gen.bf16_err(got, Y + (gen.bf16_to_f32(C0) if mode == 1 else 0))
-    assert err <= 1e-2, (M, N, K, mode, flipped, err)
-    return err
+    ref = Y + gen.bf16_to_f32(C0) if mode == 1 else Y
+    st = gen.check_out(got, ref, 1e-2, (M, N, K, mode, flipped), fp32=mode == 2)
+    return st if mode == 2 else st["net"]
 
 
 @pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 16, 17, 32, 33, 64, 65, 128, 129, 300])
@@ -77,8 +74,7 @@ def test_gemm_w8_k_slice_view():
         ref = orc.qmv if M <= 32 else orc.qmm
         Y = ref(A, sub(wq, k0 // 4, (k0 + kn) // 4), sub(s, k0 // 64, (k0 + kn) // 64), sub(b, k0 // 64, (k0 + kn) // 64),
                 bits=8)
-        err = gen.bf16_err(g.host(C), Y)
-        assert err <= 1e-2, (M, err)
+        gen.check_bf16(g.host(C), Y, 1e-2, M)
 
 
 @pytest.mark.parametrize("per_token", [False, True])
@@ -92,8 +88,7 @@ def test_w8a8(M, N, K, per_token):
     for flipped, mode in ((False, 0), (True, 2), (True, 0)):
         W = g.qlinear(wq ^ np.uint32(FLIP8) if flipped else wq, s, b, flipped, bits=8)
         out = g.host(ops.qmm_w4a8(g.dev(U), g.dev(XS), per_token, W, mode=mode))
-        err = gen.rel_err(out, Y) if mode == 2 else gen.bf16_err(out, Y)
-        assert err <= 2e-2, (M, N, K, per_token, flipped, mode, err)
+        gen.check_out(out, Y, 2e-2, (M, N, K, per_token, flipped, mode), fp32=mode == 2)
 
 
 def test_flip_8bit_in_place():
@@ -105,5 +100,4 @@ def test_flip_8bit_in_place():
     ops.flip(W)
     assert W.flipped and np.array_equal(g.host(W.wq).view(np.uint32), wq ^ np.uint32(FLIP8))
     A = gen.activations(3, 256, seed=401)
-    err = gen.bf16_err(g.host(ops.gemm(g.dev(A), W)), orc.qmv(A, wq, s, b, bits=8))
-    assert err <= 1e-2, err
+    gen.check_bf16(g.host(ops.gemm(g.dev(A), W)), orc.qmv(A, wq, s, b, bits=8), 1e-2, "flipped")
