@@ -146,6 +146,15 @@ int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, 
  * the reference's gemm + silu_mul pair (qwen35.h:1910-1912, shared expert; qwen35.h:2868-2878, dense MLP) with one
  * call that never stores the [M][N] product when K is split (the SwiGLU runs in the split-K reduction).
  * N % 16 == 0, ldh % 8 == 0, A, H and the workspace 16-byte aligned. */
+/* ifd_gemm_t64 without a caller workspace. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * workspace is a static device array of IFD_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; requests
+ * whose ifd_gemm_t64_workspace exceeds it return IFD_ERR_WORKSPACE. Each call clears the array's counter header with
+ * a fill kernel and allocates nothing. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race. Same results, bit for bit, as ifd_gemm_t64. */
+#define IFD_NOALLOC_SCRATCH_BYTES ((size_t)68 << 20)
+int ifd_gemm_t64_noalloc(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                         void* stream);
 size_t ifd_gemm_t64_swiglu_workspace(int M, int N, int K);
 int ifd_gemm_t64_swiglu(const void* A, int lda, const void* wt, int N, int K, void* H, int ldh, int M,
                         void* workspace, size_t ws_bytes, void* stream);
