@@ -245,6 +245,31 @@ int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, 
                 const uint16_t* sdn_s, const uint16_t* sdn_b, int Is, void* out, int assign, int* idx, float* wt,
                 float* sg, void* workspace, size_t ws_bytes, void* stream);
 
+/* ---- the MoE FFN on T64 expert stacks (ifd_pack_t64 with E experts) ------------------------------------------
+ * ifd_moe_dispatch with a tile height (32 or 64 rows) and an optional segment for the shared expert as expert index
+ * E: shared_rows > 0 appends sorted rows [R, R + shared_rows) = tokens 0, 1, ... (perm = t * k), their tiles after
+ * the routed ones, and offsets[E + 1] = R + shared_rows. Sizes: offsets E + 2 entries, perm R + shared_rows, tiles
+ * ifd_moe_tiles_max(R + shared_rows, E + 1) pairs; workspace ifd_moe_dispatch_workspace(R, E). */
+int ifd_moe_dispatch_ex(const int* idx, int R, int E, int k, int tile_rows, int shared_rows, int* offsets, int* perm,
+                        int* inv, int* tiles, int* ntiles, void* workspace, size_t ws_bytes, void* stream);
+/* The gathered expert GEMM of ifd_moe_gather_qmm on T64 stacks (the same bits: bf16(s q + b) dequant, fp32 sums in
+ * the same order): wt = E experts [E][N][K] packed by ifd_pack_t64, wt_shared (may be NULL) the shared expert [N][K]
+ * taking the dispatch's expert-E segment; tiles / ntiles / offsets / tile_rows from ifd_moe_dispatch_ex; rows = the
+ * sorted rows of C (ldc its row stride). silu: the stack holds [gate (N/2) | up (N/2)] and C receives the SwiGLU
+ * [rows][N/2]. Output columns in whole 256-column tiles (N % 256 == 0, with silu N / 2 % 256 == 0), K % 128 == 0. */
+int ifd_moe_gather_qmm_t64(const void* A, int lda, const int* perm, int div, const int* offsets, const int* tiles,
+                           const int* ntiles, int tile_rows, const void* wt, const void* wt_shared, int E, int N, int K,
+                           int silu, void* C, int ldc, int rows, void* stream);
+/* One-shot MoE FFN on T64 stacks (reference encode_moe after rmsnorm_for, qwen35.h:1909-1980): router -> route ->
+ * dispatch with the shared expert (sgu_t64 [2 I][H], sdn_t64 [H][I], the routed experts' I, or NULL) as expert E ->
+ * gathered gate/up + SwiGLU -> gathered down -> combine; the same arithmetic as ifd_moe_ffn. H and I multiples of
+ * 256. Workspace: ifd_moe_ffn_t64_workspace (shared: 1 with a shared expert). */
+size_t ifd_moe_ffn_t64_workspace(int T, int H, int I, int E, int k, int shared);
+int ifd_moe_ffn_t64(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
+                    int logits_bf16, const void* egu_t64, const void* edn_t64, int I, const void* sgu_t64,
+                    const void* sdn_t64, void* out, int assign, int* idx, float* wt, float* sg, void* workspace,
+                    size_t ws_bytes, void* stream);
+
 /* The dense decode MLP block on T64 weights (reference encode_layer's MLP, qwen35.h:2867-2892):
  * x += down(SwiGLU(gate_up(rmsnorm(x, norm_w, eps)))) for M rows of x [M][ldx] (bf16, updated in place), through
  * the same kernels as ifd_rmsnorm -> ifd_gemm_t64_swiglu -> ifd_gemm_t64 (mode 1) and bit-identical to that

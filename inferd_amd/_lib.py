@@ -63,6 +63,12 @@ SIGNATURES = {
     "ifd_moe_gather_qmm_a8": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i,
                                    _vp]),
     "ifd_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "ifd_moe_dispatch_ex": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ifd_moe_gather_qmm_t64": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i,
+                                    _vp]),
+    "ifd_moe_ffn_t64_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "ifd_moe_ffn_t64": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp,
+                             _vp, _sz, _vp]),
     "ifd_mlp_decode_workspace": (_sz, [_i, _i, _i]),
     "ifd_mlp_decode": (_i, [_vp, _i, _vp, ctypes.c_float, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_moe_decode_workspace": (_sz, [_i, _i, _i, _i, _i]),

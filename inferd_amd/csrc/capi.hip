@@ -425,6 +425,114 @@ int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, 
   return launch_moe_combine((uint16_t*)out, (const uint16_t*)(w + L.edn), rwt, ys, rsg, inv, T, H, k, assign, st);
 }
 
+// ---- the MoE FFN on T64 expert stacks ------------------------------------------------------------------------------
+int ifd_moe_dispatch_ex(const int* idx, int R, int E, int k, int tile_rows, int shared_rows, int* offsets, int* perm,
+                        int* inv, int* tiles, int* ntiles, void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(R >= 0 && E > 0 && E <= 1023 && k > 0 && shared_rows >= 0, "bad dispatch shape R=%d E=%d k=%d", R, E, k);
+  IFD_CHECK(tile_rows == 32 || tile_rows == 64, "tile_rows=%d must be 32 or 64", tile_rows);
+  IFD_CHECK(offsets && tiles && ntiles && (R + shared_rows == 0 || perm) && (R == 0 || (idx && inv)), "null pointer");
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_moe_dispatch(idx, R, E, offsets, perm, inv, tiles, ntiles, w.body, w.bytes, S(stream), tile_rows,
+                             shared_rows, k);
+}
+
+int ifd_moe_gather_qmm_t64(const void* A, int lda, const int* perm, int div, const int* offsets, const int* tiles,
+                           const int* ntiles, int tile_rows, const void* wt, const void* wt_shared, int E, int N, int K,
+                           int silu, void* C, int ldc, int rows, void* stream) {
+  IFD_CHECK(rows >= 0 && E > 0 && N > 0 && K > 0 && div > 0, "bad shape E=%d N=%d K=%d rows=%d", E, N, K, rows);
+  IFD_CHECK(lda >= K && lda % 8 == 0 && ldc >= (silu ? N / 2 : N) && ldc % 8 == 0, "bad strides lda=%d ldc=%d", lda,
+            ldc);
+  IFD_CHECK(rows == 0 || (A && offsets && tiles && ntiles && wt && C), "null pointer");
+  IFD_CHECK(rows == 0 || (aligned(A, 16) && aligned(wt, 16) && aligned(C, 16) && (!wt_shared || aligned(wt_shared, 16))),
+            "A, C and the stacks must be 16-byte aligned");
+  return launch_moe_gather_qmm_t64((const uint16_t*)A, lda, perm, div, tiles, ntiles, offsets, tile_rows, wt,
+                                   wt_shared, E, N, K, silu ? 1 : 0, (uint16_t*)C, ldc, rows, S(stream));
+}
+
+namespace {
+// rows per tile of the T64 gathered GEMM: 64-row tiles once an expert holds about 24 routed rows on average
+int moe_t64_tile_rows(int R, int E) { return R >= 24 * E ? 64 : 32; }
+struct MoeT64Layout {
+  size_t logits, idx, wt, sg, offsets, perm, inv, tiles, ntiles, disp, eact, ydn, total;
+};
+MoeT64Layout moe_t64_layout(int T, int H, int I, int E, int k, int shared) {
+  MoeT64Layout L{};
+  const int R = T * k, Rt = R + (shared ? T : 0);
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align_up(std::max<size_t>(bytes, 1), 256);
+    return at;
+  };
+  L.logits = take((size_t)T * (E + 1) * 4);
+  L.idx = take((size_t)R * 4);
+  L.wt = take((size_t)R * 4);
+  L.sg = take((size_t)T * 4);
+  L.offsets = take((size_t)(E + 2) * 4);
+  L.perm = take((size_t)Rt * 4);
+  L.inv = take((size_t)R * 4);
+  L.tiles = take((size_t)moe_tiles_max(Rt, E + 1) * 2 * 4);
+  L.ntiles = take(4);
+  L.disp = take(moe_dispatch_workspace(R, E));
+  L.eact = take((size_t)Rt * I * 2);
+  L.ydn = take((size_t)Rt * H * 2);
+  L.total = o;
+  return L;
+}
+}  // namespace
+
+size_t ifd_moe_ffn_t64_workspace(int T, int H, int I, int E, int k, int shared) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  return with_header(moe_t64_layout(T, H, I, E, k, shared ? 1 : 0).total);
+}
+
+int ifd_moe_ffn_t64(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
+                    int logits_bf16, const void* egu_t64, const void* edn_t64, int I, const void* sgu_t64,
+                    const void* sdn_t64, void* out, int assign, int* idx, float* wt, float* sg, void* workspace,
+                    size_t ws_bytes, void* stream) {
+  IFD_CHECK(T >= 0 && H > 0 && H % 256 == 0 && I > 0 && I % 256 == 0 && E > 0 && E <= 512 && k > 0 && k <= 16 &&
+                k <= E,
+            "bad MoE shape T=%d H=%d I=%d E=%d k=%d (H and I multiples of 256)", T, H, I, E, k);
+  const bool shared = sgu_t64 != nullptr;
+  IFD_CHECK(!shared || sdn_t64, "the shared expert needs both stacks");
+  IFD_CHECK(!shared_gate || shared, "a shared gate needs a shared expert");
+  if (T == 0) return IFD_OK;
+  IFD_CHECK(xn && router && egu_t64 && edn_t64 && out, "null pointer");
+  IFD_CHECK(aligned(xn, 16) && aligned(router, 16) && aligned(egu_t64, 16) && aligned(edn_t64, 16) &&
+                aligned(out, 16) && (!shared || (aligned(sgu_t64, 16) && aligned(sdn_t64, 16))),
+            "tokens, router, stacks and out must be 16-byte aligned");
+  const MoeT64Layout L = moe_t64_layout(T, H, I, E, k, shared ? 1 : 0);
+  const WsView wv = ws_view(workspace, ws_bytes);
+  if (!wv.body || wv.bytes < L.total)
+    return fail(IFD_ERR_WORKSPACE, "moe_ffn_t64 needs %zu bytes of workspace, got %zu", with_header(L.total),
+                ws_bytes);
+  char* w = (char*)wv.body;
+  hipStream_t st = S(stream);
+  const int R = T * k, Rt = R + (shared ? T : 0), E1 = E + (shared_gate ? 1 : 0);
+  int* ridx = idx ? idx : (int*)(w + L.idx);
+  float* rwt = wt ? wt : (float*)(w + L.wt);
+  float* rsg = sg ? sg : (float*)(w + L.sg);
+  int* offsets = (int*)(w + L.offsets);
+  int* perm = (int*)(w + L.perm);
+  int* inv = (int*)(w + L.inv);
+  int* tiles = (int*)(w + L.tiles);
+  int* ntiles = (int*)(w + L.ntiles);
+  uint16_t* eact = (uint16_t*)(w + L.eact);
+  uint16_t* ydn = (uint16_t*)(w + L.ydn);
+  const int tr = moe_t64_tile_rows(R, E);
+  IFD_TRY(launch_router_logits((const uint16_t*)xn, (const uint16_t*)router, T, H, E1, logits_bf16, w + L.logits, st));
+  IFD_TRY(launch_moe_route(w + L.logits, logits_bf16, T, E, k, E1, norm, shared_gate, ridx, rwt, rsg, st));
+  IFD_TRY(launch_moe_dispatch(ridx, R, E, offsets, perm, inv, tiles, ntiles, w + L.disp, moe_dispatch_workspace(R, E),
+                              st, tr, shared ? T : 0, k));
+  IFD_TRY(launch_moe_gather_qmm_t64((const uint16_t*)xn, H, perm, k, tiles, ntiles, offsets, tr, egu_t64, sgu_t64, E,
+                                    2 * I, H, 1, eact, I, Rt, st));
+  IFD_TRY(launch_moe_gather_qmm_t64(eact, I, nullptr, 1, tiles, ntiles, offsets, tr, edn_t64, sdn_t64, E, H, I, 0,
+                                    ydn, H, Rt, st));
+  // the shared expert's rows follow the routed ones in token order
+  return launch_moe_combine((uint16_t*)out, ydn, rwt, shared ? ydn + (size_t)R * H : nullptr, rsg, inv, T, H, k,
+                            assign, st);
+}
+
 // ---- the dense decode MLP block -----------------------------------------------------------------------------------
 namespace {
 size_t mlp_gemm_scratch(int M, int H, int I) {

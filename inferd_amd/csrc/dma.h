@@ -20,4 +20,28 @@ __device__ __forceinline__ void wait_vm_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// s_waitcnt vmcnt(STEP * k) for a wave-uniform k in [0, KMAX]: the steady state (k = KMAX) takes one compare, the
+// tail of a pipeline one more per step it is short of it.
+template <int STEP, int KMAX>
+__device__ __forceinline__ void wait_vm_dyn(int k) {
+  if constexpr (KMAX == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    if (k >= KMAX) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(STEP * KMAX) : "memory");
+    else wait_vm_dyn<STEP, KMAX - 1>(k);
+  }
+}
+
+// s_waitcnt vmcnt(STEP * k + OFF) for a wave-uniform k in [0, KMAX]
+template <int STEP, int KMAX, int OFF>
+__device__ __forceinline__ void wait_vm_off(int k) {
+  static_assert(STEP * KMAX + OFF <= 63, "vmcnt range");
+  if constexpr (KMAX == 0) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(OFF) : "memory");
+  } else {
+    if (k >= KMAX) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(STEP * KMAX + OFF) : "memory");
+    else wait_vm_off<STEP, KMAX - 1, OFF>(k);
+  }
+}
+
 }  // namespace ifd

@@ -71,17 +71,6 @@ struct GemmSkArgs {
   int swi;  // SwiGLU mode: bands per half (N / 64); 0 otherwise
 };
 
-// vmcnt(STEP * k) for a wave-uniform k in [0, KMAX]
-template <int STEP, int KMAX>
-__device__ __forceinline__ void wait_vm_dyn(int k) {
-  if constexpr (KMAX == 0) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  } else {
-    if (k >= KMAX) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(STEP * KMAX) : "memory");
-    else wait_vm_dyn<STEP, KMAX - 1>(k);
-  }
-}
-
 // the block whose run holds unit u
 __host__ __device__ inline int sk_block_of(long u, int nblk, long U) { return (int)((u * nblk + nblk - 1) / U); }
 

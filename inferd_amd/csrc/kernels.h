@@ -99,6 +99,11 @@ int moe_tiles_max(int R, int E);
 size_t moe_dispatch_workspace(int R, int E);
 int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
                         void* ws, size_t ws_bytes, hipStream_t st);
+// The same with tile_rows-row tiles and, when shared_rows > 0, a segment for the shared expert as expert E: sorted
+// rows [R, R + shared_rows) are tokens 0, 1, ... (perm = t * kdiv), tiles after the routed ones, offsets[E + 1] =
+// R + shared_rows. offsets holds E + 2 entries then, perm R + shared_rows, tiles moe_tiles_max(R + shared_rows, E + 1).
+int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
+                        void* ws, size_t ws_bytes, hipStream_t st, int tile_rows, int shared_rows, int kdiv);
 int launch_moe_gather(const uint16_t* x, const int* perm, int div, int R, int H, uint16_t* xs, hipStream_t st);
 int launch_moe_gather_qmm(const uint16_t* A, const int* perm, int div, const int* tiles, const int* ntiles,
                           const int* offsets, int max_tiles, const uint32_t* wq, const uint16_t* s,
@@ -109,6 +114,11 @@ int launch_moe_gather_qmm_a8(const int8_t* U, const float* XS, const int* perm, 
                              hipStream_t st);
 int launch_moe_combine(uint16_t* out, const uint16_t* yd, const float* wt, const uint16_t* ys, const float* sg,
                        const int* inv, int T, int H, int k, int assign, hipStream_t st);
+// The gathered expert GEMM on T64 expert stacks (moe_t64.hip): the dispatch's tiles of tile_rows (32 or 64) rows,
+// the shared expert (wsh) as expert E, rows = sorted rows of C (ldc its row stride).
+int launch_moe_gather_qmm_t64(const uint16_t* A, int lda, const int* perm, int div, const int* tiles,
+                              const int* ntiles, const int* offsets, int tile_rows, const void* wt, const void* wsh,
+                              int E, int N, int K, int silu, uint16_t* C, int ldc, int rows, hipStream_t st);
 
 // Decode MoE for T <= 8 tokens (moe_dec.hip): router, routing + distinct-expert plan, gate/up + SwiGLU, down +
 // combine; the combine's counters are H / 128 uint32 of the workspace header.

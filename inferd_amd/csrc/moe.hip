@@ -122,9 +122,13 @@ __global__ __launch_bounds__(256) void k_disp_count(const int* __restrict__ idx,
   for (int c = tid; c < E; c += 256) bcnt[(size_t)blockIdx.x * E + c] = cnt[c];
 }
 
+// shared_rows > 0 appends a segment for the shared expert as expert E: sorted rows [R, R + shared_rows) are tokens
+// 0, 1, ... in order (perm = t * kdiv), with their own tiles after the routed ones, and offsets[E + 1] = R +
+// shared_rows.
 __global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int nchunks, int E, int R, int tile_rows,
                                                     int* __restrict__ offsets, int* __restrict__ tiles,
-                                                    int* __restrict__ ntiles) {
+                                                    int* __restrict__ ntiles, int shared_rows, int kdiv,
+                                                    int* __restrict__ perm) {
   __shared__ int part[1024], tpart[1024];
   const int e = threadIdx.x;
   int total = 0;
@@ -155,9 +159,17 @@ __global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int 
       tiles[2 * (toff + i) + 1] = off + i * tile_rows;
     }
   }
+  const int routed_tiles = tpart[1023];
+  const int nsh = (shared_rows + tile_rows - 1) / tile_rows;
+  for (int i = e; i < nsh; i += 1024) {
+    tiles[2 * (routed_tiles + i)] = E;
+    tiles[2 * (routed_tiles + i) + 1] = R + i * tile_rows;
+  }
+  for (int t = e; t < shared_rows; t += 1024) perm[R + t] = t * kdiv;
   if (e == 0) {
     offsets[E] = R;
-    ntiles[0] = tpart[1023];
+    if (shared_rows > 0) offsets[E + 1] = R + shared_rows;
+    ntiles[0] = routed_tiles + nsh;
   }
 }
 
@@ -179,7 +191,7 @@ size_t moe_dispatch_workspace(int R, int E) {
 }
 
 int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
-                        void* ws, size_t ws_bytes, hipStream_t st, int tile_rows) {
+                        void* ws, size_t ws_bytes, hipStream_t st, int tile_rows, int shared_rows, int kdiv) {
   const int nchunks = (R + kDispChunk - 1) / kDispChunk;
   if (moe_dispatch_workspace(R, E) > ws_bytes || !ws)
     return fail(IFD_ERR_WORKSPACE, "moe_dispatch needs %zu bytes of workspace", moe_dispatch_workspace(R, E));
@@ -189,7 +201,8 @@ int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, i
     hipLaunchKernelGGL(k_disp_count, dim3(nchunks), dim3(256), E * sizeof(int), st, idx, R, E, bcnt, rank);
     IFD_TRY(check_launch("moe_dispatch count"));
   }
-  hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, st, bcnt, nchunks, E, R, tile_rows, offsets, tiles, ntiles);
+  hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, st, bcnt, nchunks, E, R, tile_rows, offsets, tiles, ntiles,
+                     shared_rows, kdiv, perm);
   IFD_TRY(check_launch("moe_dispatch scan"));
   if (R > 0) {
     hipLaunchKernelGGL(k_disp_scatter, dim3(nchunks), dim3(256), 0, st, idx, R, E, bcnt, rank, perm, inv);
@@ -200,7 +213,7 @@ int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, i
 
 int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv, int* tiles, int* ntiles,
                         void* ws, size_t ws_bytes, hipStream_t st) {
-  return launch_moe_dispatch(idx, R, E, offsets, perm, inv, tiles, ntiles, ws, ws_bytes, st, 32);
+  return launch_moe_dispatch(idx, R, E, offsets, perm, inv, tiles, ntiles, ws, ws_bytes, st, 32, 0, 1);
 }
 
 // ---- gather ----------------------------------------------------------------------------------------------------

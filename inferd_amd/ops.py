@@ -382,3 +382,73 @@ def probe_mfma(int8: bool, iters: int, blocks: int, out: torch.Tensor) -> float:
     """MFMA-only loop; returns the operations it performs (FLOP for bf16, OP for int8). out: float [blocks * 256]."""
     check(lib().ifd_probe_mfma(1 if int8 else 0, iters, blocks, _p(out), _stream()))
     return float(blocks) * 4 * 8 * iters * (65536 if int8 else 32768)
+
+
+# ---- MoE on T64 expert stacks -------------------------------------------------------------------------------------
+@dataclass
+class T64Stack:
+    """E experts [E, N, K] packed expert by expert into the T64 layout (a uint8 device buffer)."""
+    wt: torch.Tensor
+    E: int
+    N: int
+    K: int
+
+
+def pack_t64_stack(W: MoeW) -> T64Stack:
+    """One-time repack of an MLX-layout expert stack into T64 tiles."""
+    nbytes = lib().ifd_t64_bytes(W.N, W.K, W.E)
+    wt = torch.empty((nbytes,), dtype=torch.uint8, device=W.wq.device)
+    check(lib().ifd_pack_t64(_p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, 0, W.E, _p(wt), _stream()))
+    return T64Stack(wt, W.E, W.N, W.K)
+
+
+def moe_dispatch_ex(idx: torch.Tensor, E: int, k: int, tile_rows: int = 32, shared_rows: int = 0):
+    """ifd_moe_dispatch_ex: returns (offsets [E + 2], perm, inv, tiles, ntiles, max_tiles, tile_rows)."""
+    R = idx.numel()
+    dev = idx.device
+    Rt = R + shared_rows
+    offsets = torch.empty((E + 2,), dtype=torch.int32, device=dev)
+    perm = torch.empty((max(Rt, 1),), dtype=torch.int32, device=dev)
+    inv = torch.empty((max(R, 1),), dtype=torch.int32, device=dev)
+    mt = lib().ifd_moe_tiles_max(Rt, E + 1)
+    tiles = torch.empty((max(mt, 1), 2), dtype=torch.int32, device=dev)
+    ntiles = torch.empty((1,), dtype=torch.int32, device=dev)
+    ws = workspace(lib().ifd_moe_dispatch_workspace(R, E), dev)
+    check(lib().ifd_moe_dispatch_ex(_p(idx), R, E, k, tile_rows, shared_rows, _p(offsets), _p(perm), _p(inv),
+                                    _p(tiles), _p(ntiles), _p(ws), ws.numel(), _stream()))
+    return offsets, perm[:Rt], inv[:R], tiles, ntiles, mt, tile_rows
+
+
+def moe_gather_qmm_t64(A: torch.Tensor, perm: Optional[torch.Tensor], div: int, disp, W: T64Stack, silu: bool,
+                       shared: Optional[T64Linear] = None) -> torch.Tensor:
+    """The gathered expert GEMM on a T64 stack (disp from moe_dispatch_ex; shared: the expert-E segment's weights)."""
+    offsets, perm_sorted, _, tiles, ntiles, _, tile_rows = disp
+    rows = perm_sorted.numel()
+    NO = W.N // 2 if silu else W.N
+    C = torch.empty((rows, NO), dtype=torch.bfloat16, device=A.device)
+    check(lib().ifd_moe_gather_qmm_t64(_p(A), A.shape[1], _p(perm), div, _p(offsets), _p(tiles), _p(ntiles), tile_rows,
+                                       _p(W.wt), _p(shared.wt) if shared is not None else None, W.E, W.N, W.K,
+                                       1 if silu else 0, _p(C), NO, rows, _stream()))
+    return C
+
+
+def moe_ffn_t64(xn: torch.Tensor, router: torch.Tensor, egu: T64Stack, edn: T64Stack, k: int,
+                shared: Optional[tuple] = None, shared_gate: bool = True, norm: bool = True,
+                logits_bf16: bool = True, out: Optional[torch.Tensor] = None, assign: bool = True):
+    """One-shot MoE FFN on T64 stacks; shared = (T64Linear gate_up [2I, H], T64Linear down [H, I]) with the routed
+    experts' I. Returns (out, idx, wt, sg)."""
+    T, H = xn.shape
+    E, I = egu.E, egu.N // 2
+    dev = xn.device
+    if out is None:
+        out = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    wt = torch.empty((T, k), dtype=torch.float32, device=dev)
+    sg = torch.empty((T,), dtype=torch.float32, device=dev)
+    ws = workspace(lib().ifd_moe_ffn_t64_workspace(T, H, I, E, k, 1 if shared is not None else 0), dev)
+    sgu, sdn = shared if shared is not None else (None, None)
+    check(lib().ifd_moe_ffn_t64(
+        _p(xn), T, H, _p(router), E, k, 1 if norm else 0, 1 if shared_gate else 0, 1 if logits_bf16 else 0,
+        _p(egu.wt), _p(edn.wt), I, _p(sgu.wt) if sgu is not None else None, _p(sdn.wt) if sdn is not None else None,
+        _p(out), 1 if assign else 0, _p(idx), _p(wt), _p(sg), _p(ws), ws.numel(), _stream()))
+    return out, idx, wt, sg

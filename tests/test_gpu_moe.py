@@ -4,6 +4,8 @@ CPU oracle, through the C ABI. Indices and permutations bit-exact; floats within
 Routing is compared on the same logits (the GPU's): router logits from two different summation orders may
 legitimately break a near-tie differently, so the end-to-end FFN check runs the oracle on the GPU's routing.
 """
+import functools
+
 import numpy as np
 import pytest
 
@@ -282,3 +284,134 @@ def test_gather_qmm_a8(silu):
         Ur, XSr = orc.a8_quant(a, 2)
         y = orc.moe_gather_w4a8(Ur, XSr, None, 1, ro, wq, s, b, H, I)
         gen.check_bf16(got, y, 2e-2, "down")
+
+
+# ---- MoE on T64 expert stacks ---------------------------------------------------------------------------------------
+@functools.lru_cache(maxsize=None)
+def _config4_stacks():
+    """BASELINE config 4's expert stacks (H = 2048, E = 512, I = 512) and a shared expert, host arrays."""
+    return (experts(512, 1024, 2048, seed=300), experts(512, 2048, 512, seed=301), experts(1, 1024, 2048, seed=302),
+            experts(1, 2048, 512, seed=303))
+
+
+def _stacks(T, E, H, I):
+    if (E, H, I) == (512, 2048, 512):
+        return _config4_stacks()
+    return (experts(E, 2 * I, H, seed=T + 1), experts(E, H, I, seed=T + 2), experts(1, 2 * I, H, seed=T + 3),
+            experts(1, H, I, seed=T + 4))
+
+
+@pytest.mark.parametrize("T,E,H,I,k,tile_rows", [
+    (16, 64, 256, 256, 4, 32),
+    (200, 32, 512, 256, 4, 64),    # ~25 rows per expert: 64-row tiles partly empty
+    (300, 16, 256, 512, 2, 64),    # ~38 rows per expert, several experts past one tile
+    (2048, 512, 2048, 512, 10, 64),  # BASELINE config 4
+    (128, 512, 2048, 512, 10, 32),
+])
+def test_gather_qmm_t64_bit_identical(T, E, H, I, k, tile_rows):
+    """The gathered GEMM on T64 stacks gives the bits of the MLX-layout one (the same bf16(s q + b) dequant and fp32
+    summation order per row) for gate/up with its SwiGLU and for down, at either tile height; ifd_moe_dispatch_ex
+    sorts the rows exactly as ifd_moe_dispatch and tiles every segment with its tile height."""
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(T + E)
+    egu, edn, _, _ = _stacks(T, E, H, I)
+    x = g.dev(gen.activations(T, H, seed=T + 5))
+    idx = g.dev(np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32))
+    d32 = ops.moe_dispatch(idx, E)
+    dex = ops.moe_dispatch_ex(idx, E, k, tile_rows)
+    torch.cuda.synchronize()
+    for a, b_ in ((d32[0], dex[0][:E + 1]), (d32[1], dex[1]), (d32[2], dex[2])):
+        assert np.array_equal(g.host(a), g.host(b_))
+    ro = g.host(dex[0])
+    nt = int(g.host(dex[4])[0])
+    want = [(e, q) for e in range(E) for q in range(ro[e], ro[e + 1], tile_rows)]
+    assert [tuple(t) for t in g.host(dex[3])[:nt].tolist()] == want
+    EGU, EDN = g.moew(*egu), g.moew(*edn)
+    TGU, TDN = ops.pack_t64_stack(EGU), ops.pack_t64_stack(EDN)
+    h_mlx = ops.moe_gather_qmm(x, d32[1], k, d32, EGU, silu=True)
+    h_t = ops.moe_gather_qmm_t64(x, dex[1], k, dex, TGU, silu=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(g.host(h_t), g.host(h_mlx)), "gate/up + SwiGLU"
+    y_mlx = ops.moe_gather_qmm(h_t, None, 1, d32, EDN, silu=False)
+    y_t = ops.moe_gather_qmm_t64(h_t, None, 1, dex, TDN, silu=False)
+    torch.cuda.synchronize()
+    assert np.array_equal(g.host(y_t), g.host(y_mlx)), "down"
+
+
+@pytest.mark.parametrize("T,tile_rows", [(37, 32), (300, 64)])
+def test_gather_qmm_t64_shared_segment(T, tile_rows):
+    """The shared expert as the dispatch's expert-E segment (every token, in token order, after the routed rows): its
+    gate/up product rows against the oracle's qmm of the tokens, the fused SwiGLU bit-identical to silu_mul of the
+    product, and the routed rows unchanged by the extra segment."""
+    g, ops = _gu(), _ops()
+    E, H, I, k = 16, 512, 256, 2
+    rng = np.random.default_rng(T)
+    egu, _, sgu, _ = _stacks(T, E, H, I)
+    xn = gen.activations(T, H, seed=T + 7)
+    x = g.dev(xn)
+    idx = g.dev(np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32))
+    TGU = ops.pack_t64_stack(g.moew(*egu))
+    SGU = ops.pack_t64(g.qlinear(sgu[0][0], sgu[1][0], sgu[2][0]))
+    dsh = ops.moe_dispatch_ex(idx, E, k, tile_rows, shared_rows=T)
+    dno = ops.moe_dispatch_ex(idx, E, k, tile_rows)
+    R = T * k
+    prod = g.host(ops.moe_gather_qmm_t64(x, dsh[1], k, dsh, TGU, silu=False, shared=SGU))
+    h = ops.moe_gather_qmm_t64(x, dsh[1], k, dsh, TGU, silu=True, shared=SGU)
+    h0 = ops.moe_gather_qmm_t64(x, dno[1], k, dno, TGU, silu=True)
+    torch.cuda.synchronize()
+    assert g.host(dsh[0])[E + 1] == R + T and np.array_equal(g.host(dsh[1])[R:], np.arange(T) * k)
+    assert np.array_equal(g.host(h), g.host(ops.silu_mul(g.dev(prod))))
+    assert np.array_equal(g.host(h)[:R], g.host(h0))
+    gen.check_bf16(prod[R:], orc.qmm(xn, sgu[0][0], sgu[1][0], sgu[2][0]), 1e-2, "shared gate/up")
+
+
+def _ffn_t64_case(T, E, H, I, k, shared_gate, seed):
+    """The one-shot FFN on T64 stacks against its stages through the C ABI (same bits), the stages against the
+    oracle on the GPU's own inputs, and the whole against the oracle's composition (shared expert in the gathered
+    GEMM's bf16 dequant arithmetic at every T)."""
+    g, ops = _gu(), _ops()
+    egu, edn, sgu, sdn = _stacks(seed, E, H, I)
+    R_ = router(E + (1 if shared_gate else 0), H, seed=seed + 4)
+    xn = gen.activations(T, H, seed=seed + 5)
+    sgu_h, sdn_h = (sgu[0][0], sgu[1][0], sgu[2][0]), (sdn[0][0], sdn[1][0], sdn[2][0])
+    xd, Rd = g.dev(xn), g.dev(R_)
+    TGU, TDN = ops.pack_t64_stack(g.moew(*egu)), ops.pack_t64_stack(g.moew(*edn))
+    SGU, SDN = ops.pack_t64(g.qlinear(*sgu_h)), ops.pack_t64(g.qlinear(*sdn_h))
+    out, idx, wt, sg = ops.moe_ffn_t64(xd, Rd, TGU, TDN, k, shared=(SGU, SDN), shared_gate=shared_gate,
+                                       logits_bf16=T >= 64)
+    # the stages
+    R = T * k
+    tile_rows = 64 if R >= 24 * E else 32
+    logits = ops.moe_router_logits(xd, Rd, out_bf16=T >= 64)
+    idx2, wt2, sg2 = ops.moe_route(logits, E, k, shared_gate=shared_gate)
+    disp = ops.moe_dispatch_ex(idx2, E, k, tile_rows, shared_rows=T)
+    eact = ops.moe_gather_qmm_t64(xd, disp[1], k, disp, TGU, silu=True, shared=SGU)
+    ydn = ops.moe_gather_qmm_t64(eact, None, 1, disp, TDN, silu=False, shared=SDN)
+    out2 = ops.moe_combine(torch.zeros_like(out), ydn[:R], wt2, ydn[R:], sg2, disp[2], k, True)
+    gu_full = ops.moe_gather_qmm_t64(xd, disp[1], k, disp, TGU, silu=False, shared=SGU)
+    torch.cuda.synchronize()
+    assert np.array_equal(g.host(out), g.host(out2)), "one-shot FFN differs from its stages"
+    assert np.array_equal(g.host(idx), g.host(idx2)) and np.array_equal(g.host(wt), g.host(wt2))
+    assert np.array_equal(g.host(eact), g.host(ops.silu_mul(gu_full))), "fused SwiGLU differs from silu_mul"
+    ri, rw, rs = orc.moe_route(g.host(logits), E, k, shared_gate=shared_gate)
+    assert np.array_equal(g.host(idx), ri)
+    ro, rp, rinv = orc.moe_dispatch(ri, E)
+    eact_h, ydn_h = g.host(eact), g.host(ydn)
+    gen.check_bf16(g.host(gu_full)[:R], orc.moe_gather_qmm(xn, rp, k, ro, *egu, 2 * I, H), 1e-2, "gate/up")
+    gen.check_bf16(g.host(gu_full)[R:], orc.qmm(xn, *sgu_h), 1e-2, "shared gate/up")
+    gen.check_bf16(ydn_h[:R], orc.moe_gather_qmm(eact_h[:R], None, 1, ro, *edn, H, I), 1e-2, "down")
+    gen.check_bf16(ydn_h[R:], orc.qmm(eact_h[R:], *sdn_h), 1e-2, "shared down")
+    comb = orc.moe_combine(np.zeros((T, H), np.uint16), ydn_h[:R], rw, ydn_h[R:], rs, rinv, k, True)
+    gen.check_bf16(g.host(out), comb, 1e-2, "combine", ref_is_bf16=True)
+    ref = orc.moe_experts(xn, ri, rw, rs, egu, edn, (sgu_h, sdn_h), I, shared_qmv=False)
+    gen.check_bf16(g.host(out), ref, 1e-2, ("end to end", T, E, H, I, k), ref_is_bf16=True, composition=True)
+
+
+@pytest.mark.parametrize("T,shared_gate", [(16, True), (128, False), (2048, False)])
+def test_moe_ffn_t64_baseline_geometry(T, shared_gate):
+    """BASELINE config 4 (H = 2048, E = 512, top-10, I = 512, shared expert) on T64 stacks at its three T."""
+    _ffn_t64_case(T, 512, 2048, 512, 10, shared_gate, seed=T)
+
+
+def test_moe_ffn_t64_small():
+    _ffn_t64_case(40, 8, 256, 256, 2, True, seed=97)
