@@ -295,19 +295,35 @@ def main():
 
             ncp = 2
             lay = [(moew(2 * I, H), moew(H, I), qlin(2 * I, H), qlin(H, I)) for _ in range(ncp)]
+            # the same experts repacked once into T64 stacks (the shared expert rides along as expert E)
+            tlay = [(ops.pack_t64_stack(egu), ops.pack_t64_stack(edn), ops.pack_t64(sgu), ops.pack_t64(sdn))
+                    for egu, edn, sgu, sdn in lay]
             router = (torch.randn((E, H), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
             moe = {}
+            e_bytes = (2 * I * H + H * I) * W_BYTES_PER_WEIGHT  # one expert's gate/up + down: 1,769,472 B
             for T in (16, 128, 2048):
                 xn = act(T, H)
                 outb = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+
+                def run_t64(i):
+                    tgu, tdn, sgu, sdn = tlay[i % ncp]
+                    ops.moe_ffn_t64(xn, router, tgu, tdn, k, shared=(sgu, sdn), shared_gate=False,
+                                    logits_bf16=T >= 64, out=outb)
 
                 def run(i):
                     egu, edn, sgu, sdn = lay[i % ncp]
                     ops.moe_ffn(xn, router, egu, edn, k, shared=(sgu, sdn), shared_gate=False,
                                 logits_bf16=T >= 64, out=outb)
 
-                ms = timed(run, 10, 3)
-                moe[f"T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3))
+                ms = timed(run_t64, 10, 3)
+                ms_mlx = timed(run, 5, 2)
+                # algorithmic bytes: the distinct experts a uniform router touches, U(T) = E (1 - (1 - k/E)^T), the
+                # shared expert, the router and the tokens in and out
+                U = E * (1.0 - (1.0 - k / E) ** T)
+                byts = (U + 1) * e_bytes + E * H * 2 + 2 * T * H * 2
+                moe[f"T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3), gbs=byts / (ms * 1e-3) / 1e9,
+                                    frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, mlx_layout_us=ms_mlx * 1e3)
+            del tlay
             # decode batches (T <= 8): the four-launch decode MoE, each distinct expert read once
             for T in (1, 2, 4, 8):
                 xn = act(T, H)
