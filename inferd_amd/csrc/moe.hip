@@ -13,39 +13,72 @@
 namespace ifd {
 
 // ---- router logits: [T][E1] = x [T][H] . W [E1][H]^T ------------------------------------------------------------
-// One wave per 32 x 32 output tile; operands straight from global memory (x and W are small and L2-resident).
-// Lane (j, h) supplies k = 32 h + 8 t .. +7 of every 64-wide K block in step t (same k assignment for both
-// operands), so each lane reads 64 contiguous bytes of its row per block.
-__global__ __launch_bounds__(256) void k_router_logits(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                       int T, int H, int E1, int out_bf16, void* out, int tiles_e) {
+// Block = 8 waves over 8 / S tiles of 32 tokens x 32 experts, the K of each tile split S ways: wave w works on tile
+// w / S and takes the 64-wide K chunks [(w % S) C / S, (w % S + 1) C / S) of the C = H / 64, issuing the loads of up
+// to four chunks before their MFMAs (x and W are small and L2-resident: a tile is bound by load latency, not
+// bytes). With S > 1 the partial tiles are summed in split order through LDS. S shrinks as the tile count grows,
+// so that small batches still spread over many waves. Lane (j, h) supplies k = 32 h + 8 t .. +7 of a chunk in
+// MFMA step t for both operands.
+constexpr int kRlWaves = 8, kRlBatch = 4;
+template <int S>
+__global__ __launch_bounds__(kRlWaves * 64) void k_router_logits(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ w, int T, int H, int E1,
+                                                                 int out_bf16, void* out, int tiles_e, int ntiles) {
+  __shared__ float red[S > 1 ? kRlWaves : 1][16][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, h = lane >> 5;
-  const int tile = blockIdx.x * 4 + wave;
+  // XCD-contiguous block order: an XCD's blocks then share token rows, which stay in its L2
+  const int blk = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = blk * (kRlWaves / S) + wave / S, part = wave % S;
+  const bool live = tile < ntiles;
   const int tt = tile / tiles_e, te = tile % tiles_e;
   const int t0 = tt * 32, e0 = te * 32;
-  if (t0 >= T) return;
-  const bool tok = t0 + j < T, eok = e0 + j < E1;
+  const bool tok = live && t0 + j < T, eok = live && e0 + j < E1;
   const uint16_t* xa = x + (size_t)(tok ? t0 + j : 0) * H + 32 * h;
   const uint16_t* wb = w + (size_t)(eok ? e0 + j : 0) * H + 32 * h;
+  const int C = H / 64, c0 = part * C / S, c1 = (part + 1) * C / S;
   f32x16 acc = zero16();
-  for (int k = 0; k < H; k += 64) {
-    u32x4 a[4], b[4];
+  for (int cb = c0; cb < c1; cb += kRlBatch) {
+    u32x4 a[kRlBatch][4], b[kRlBatch][4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      a[t] = tok ? *(const u32x4*)(xa + k + 8 * t) : u32x4{0u, 0u, 0u, 0u};
-      b[t] = eok ? *(const u32x4*)(wb + k + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+    for (int u = 0; u < kRlBatch; u++) {
+      const int k = min(cb + u, c1 - 1) * 64;  // past the range: a re-read, not used
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        a[u][t] = tok ? *(const u32x4*)(xa + k + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+        b[u][t] = eok ? *(const u32x4*)(wb + k + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+      }
     }
 #pragma unroll
-    for (int t = 0; t < 4; t++) acc = mfma_bf16(a[t], b[t], acc);
-  }
-  const int e = e0 + j;
-  if (e >= E1) return;
+    for (int u = 0; u < kRlBatch; u++)
+      if (cb + u < c1)
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int t = t0 + 8 * (r / 4) + 4 * h + (r % 4);
-    if (t >= T) continue;
-    if (out_bf16) ((uint16_t*)out)[(size_t)t * E1 + e] = f2bf(acc[r]);
-    else ((float*)out)[(size_t)t * E1 + e] = acc[r];
+        for (int t = 0; t < 4; t++) acc = mfma_bf16(a[u][t], b[u][t], acc);
+  }
+  auto store = [&](int tt_, int te_, int r, int l, float v) {
+    const int t = tt_ * 32 + 8 * (r / 4) + 4 * (l >> 5) + (r % 4), e = te_ * 32 + (l & 31);
+    if (t >= T || e >= E1) return;
+    if (out_bf16) ((uint16_t*)out)[(size_t)t * E1 + e] = f2bf(v);
+    else ((float*)out)[(size_t)t * E1 + e] = v;
+  };
+  if (S == 1) {
+    if (!live) return;
+#pragma unroll
+    for (int r = 0; r < 16; r++) store(tt, te, r, lane, acc[r]);
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; r++) red[wave][r][lane] = acc[r];
+  __syncthreads();
+  // the block's 8 / S tiles x 1024 outputs, each summed over its S parts in order
+  for (int o = threadIdx.x; o < (kRlWaves / S) * 1024; o += kRlWaves * 64) {
+    const int tl = o >> 10, r = (o >> 6) & 15, l = o & 63;
+    const int tile2 = blk * (kRlWaves / S) + tl;
+    if (tile2 >= ntiles) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < S; q++) v += red[tl * S + q][r][l];
+    store(tile2 / tiles_e, tile2 % tiles_e, r, l, v);
   }
 }
 
@@ -53,8 +86,17 @@ int launch_router_logits(const uint16_t* x, const uint16_t* w, int T, int H, int
                          hipStream_t st) {
   if (T == 0) return IFD_OK;
   const int tiles_e = (E1 + 31) / 32, tiles = (T + 31) / 32 * tiles_e;
-  hipLaunchKernelGGL(k_router_logits, dim3((tiles + 3) / 4), dim3(256), 0, st, x, w, T, H, E1, out_bf16, logits,
-                     tiles_e);
+  // K splits: at least two per tile once the tiles fill the CUs (a block then holds 4 tiles, and there are blocks
+  // for every CU), more below that
+  const int S = tiles >= 4096 ? 1 : tiles >= 256 ? 2 : tiles >= 128 ? 4 : 8;
+  const int per = kRlWaves / S;
+  const dim3 grid((tiles + per - 1) / per), block(kRlWaves * 64);
+  if (S == 1) hipLaunchKernelGGL(k_router_logits<1>, grid, block, 0, st, x, w, T, H, E1, out_bf16, logits, tiles_e, tiles);
+  else if (S == 2)
+    hipLaunchKernelGGL(k_router_logits<2>, grid, block, 0, st, x, w, T, H, E1, out_bf16, logits, tiles_e, tiles);
+  else if (S == 4)
+    hipLaunchKernelGGL(k_router_logits<4>, grid, block, 0, st, x, w, T, H, E1, out_bf16, logits, tiles_e, tiles);
+  else hipLaunchKernelGGL(k_router_logits<8>, grid, block, 0, st, x, w, T, H, E1, out_bf16, logits, tiles_e, tiles);
   return check_launch("router_logits");
 }
 
@@ -132,11 +174,18 @@ __global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int 
   __shared__ int part[1024], tpart[1024];
   const int e = threadIdx.x;
   int total = 0;
+  // exclusive prefix of the chunk counts within the expert, 16 loads in flight
   if (e < E)
-    for (int c = 0; c < nchunks; c++) {
-      const int v = bcnt[(size_t)c * E + e];
-      bcnt[(size_t)c * E + e] = total;  // exclusive prefix within the expert
-      total += v;
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+      int v[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) v[u] = c0 + u < nchunks ? bcnt[(size_t)(c0 + u) * E + e] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; u++)
+        if (c0 + u < nchunks) {
+          bcnt[(size_t)(c0 + u) * E + e] = total;
+          total += v[u];
+        }
     }
   const int nt = (total + tile_rows - 1) / tile_rows;
   part[e] = e < E ? total : 0;
@@ -152,8 +201,7 @@ __global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int 
   }
   const int off = part[e] - (e < E ? total : 0), toff = tpart[e] - (e < E ? nt : 0);
   if (e < E) {
-    offsets[e] = off;
-    for (int c = 0; c < nchunks; c++) bcnt[(size_t)c * E + e] += off;
+    offsets[e] = off;  // the scatter adds it to the chunk prefixes
     for (int i = 0; i < nt; i++) {
       tiles[2 * (toff + i)] = e;
       tiles[2 * (toff + i) + 1] = off + i * tile_rows;
@@ -174,11 +222,13 @@ __global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int 
 }
 
 __global__ __launch_bounds__(256) void k_disp_scatter(const int* __restrict__ idx, int R, int E,
-                                                      const int* __restrict__ bbase, const int* __restrict__ rank,
-                                                      int* __restrict__ perm, int* __restrict__ inv) {
+                                                      const int* __restrict__ offsets, const int* __restrict__ bbase,
+                                                      const int* __restrict__ rank, int* __restrict__ perm,
+                                                      int* __restrict__ inv) {
   const int r = blockIdx.x * kDispChunk + threadIdx.x;
   if (r >= R) return;
-  const int q = bbase[(size_t)blockIdx.x * E + min(max(idx[r], 0), E - 1)] + rank[r];
+  const int e = min(max(idx[r], 0), E - 1);
+  const int q = offsets[e] + bbase[(size_t)blockIdx.x * E + e] + rank[r];
   perm[q] = r;
   inv[r] = q;
 }
@@ -205,7 +255,7 @@ int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, i
                      shared_rows, kdiv, perm);
   IFD_TRY(check_launch("moe_dispatch scan"));
   if (R > 0) {
-    hipLaunchKernelGGL(k_disp_scatter, dim3(nchunks), dim3(256), 0, st, idx, R, E, bcnt, rank, perm, inv);
+    hipLaunchKernelGGL(k_disp_scatter, dim3(nchunks), dim3(256), 0, st, idx, R, E, offsets, bcnt, rank, perm, inv);
     IFD_TRY(check_launch("moe_dispatch scatter"));
   }
   return IFD_OK;
