@@ -148,9 +148,9 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
     const uint8_t* wst = wring + ws * kSkWBytes;
     const u32x4 codes = *(const u32x4*)(wst + wave * kT64Codes + 16 * lane);
     const uint32_t sb = *(const uint32_t*)(wst + 8 * kT64Codes + wave * 128 + 4 * j);
-    const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), s16 = sc * 0.0625f;
+    const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), sa = t64_sa(sc), sbs = t64_sb(sc);
 #pragma unroll
-    for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sc, s16, bi);
+    for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sa, sbs, bi);
   };
   // activation fragments of M tile a: MFMA step t takes k = 32 h + 8 t .. + 7 (logical column 4 h + t)
   auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) __attribute__((always_inline)) {

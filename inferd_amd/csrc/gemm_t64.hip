@@ -135,9 +135,9 @@ __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
     sc = bf2f((uint16_t)(sb & 0xFFFFu));
     const float bi = bf2f((uint16_t)(sb >> 16));
     if (DEQ) {
-      const float s16 = sc * 0.0625f;
+      const float sa = t64_sa(sc), sbs = t64_sb(sc);
 #pragma unroll
-      for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sc, s16, bi);
+      for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sa, sbs, bi);
     } else {
       bp = __builtin_fmaf(-128.f, sc, bi);
 #pragma unroll

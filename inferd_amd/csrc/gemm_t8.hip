@@ -108,9 +108,9 @@ __global__ __launch_bounds__(512, 1) void k_gemm_t8(GemmT8Args p) {
     const uint8_t* wst = wring + (step % kT8NW) * W_BYTES;
     const u32x4 codes = *(const u32x4*)(wst + wave * kT64Codes + 16 * lane);
     const uint32_t sb = *(const uint32_t*)(wst + NBB * kT64Codes + wave * 128 + 4 * j);
-    const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), s16 = sc * 0.0625f;
+    const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), sa = t64_sa(sc), sbs = t64_sb(sc);
 #pragma unroll
-    for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sc, s16, bi);
+    for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sa, sbs, bi);
   };
 
   // Pipeline: the weights of group s + 1 and the activations of group s are in LDS at step s. Per wave and step the

@@ -179,9 +179,9 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
       const int t = 8 * nb + wave;
       const u32x4 codes = *(const u32x4*)(wst + t * kT64Codes + 16 * lane);
       const uint32_t sb = *(const uint32_t*)(wst + SB_OFF + t * 128 + 4 * j);
-      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), s16 = sc * 0.0625f;
+      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), sa = t64_sa(sc), sbs = t64_sb(sc);
 #pragma unroll
-      for (int q = 0; q < 4; q++) bf[nb][q] = t64_dequant(codes[q], sc, s16, bi);
+      for (int q = 0; q < 4; q++) bf[nb][q] = t64_dequant(codes[q], sa, sbs, bi);
     }
   };
   auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) __attribute__((always_inline)) {

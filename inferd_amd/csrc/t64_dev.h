@@ -11,21 +11,24 @@ __device__ __forceinline__ u32x4 t64_off128(uint32_t w) {
   return r;
 }
 // Eight T64 codes (one word) -> bf16(s q + b) in natural k order. Code 2i sits in nibble i, code 2i + 1 in nibble
-// i + 4 (t64.h), so the low nibbles of the four bytes hold codes 0, 4, 1, 5 and the high nibbles codes 2, 6, 3, 7.
-// Two masks split the word into bytes; one byte -> fp32 conversion per code (v_cvt_f32_ubyte0..3) gives q, or 16 q for
-// the high nibbles, which take s / 16 (exact: a power-of-two scaling of a bf16); fma rounds s q + b once in fp32, as
-// the bf16(fp32(s q + b)) of the MLX loader. 22 VALU instructions per 8 codes, two of them integer ops: integer VALU
-// co-issues poorly beside MFMA, conversions and fma well. The masks go through opaque moves so that the compiler
-// selects the byte conversions instead of folding the masks into bitfield extracts.
-__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float s, float s16, float b) {
-  uint32_t lo, hi;
-  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
-  asm("v_and_b32 %0, 0xf0f0f0f0, %1" : "=v"(hi) : "v"(w));
-  const float c0 = __builtin_fmaf(s, (float)(lo & 0xFFu), b), c4 = __builtin_fmaf(s, (float)((lo >> 8) & 0xFFu), b);
-  const float c1 = __builtin_fmaf(s, (float)((lo >> 16) & 0xFFu), b), c5 = __builtin_fmaf(s, (float)(lo >> 24), b);
-  const float c2 = __builtin_fmaf(s16, (float)(hi & 0xFFu), b), c6 = __builtin_fmaf(s16, (float)((hi >> 8) & 0xFFu), b);
-  const float c3 = __builtin_fmaf(s16, (float)((hi >> 16) & 0xFFu), b), c7 = __builtin_fmaf(s16, (float)(hi >> 24), b);
-  return u32x4{pack_bf2(c0, c1), pack_bf2(c2, c3), pack_bf2(c4, c5), pack_bf2(c6, c7)};
+// i + 4 (t64.h), so each 16-bit half of the word holds four codes, the pair (2i, 2i + 1) at the same place in the
+// two halves. Masking the word (and the word shifted by 8) with 0x000F000F / 0x00F000F0 leaves two f16 subnormals
+// q 2^-24 or 16 q 2^-24 = q 2^-20 per 32 bits, which v_fma_mix_f32 widens exactly; with sa = s 2^24 and sb = s 2^20
+// (exact power-of-two scalings of a bf16) each fma computes s q exactly and rounds s q + b once in fp32, as the
+// bf16(fp32(s q + b)) of the MLX loader. 17 VALU instructions per 8 codes (5 integer, 8 fma_mix, 4 conversions).
+// The scalings are exact for |s| < 2^103; larger scales overflow (a 4-bit scale is a weight range / 15).
+__device__ __forceinline__ float h16_lo(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(p & 0xFFFFu)); }
+__device__ __forceinline__ float h16_hi(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(p >> 16)); }
+__device__ __forceinline__ u32x4 t64_dequant(uint32_t w, float sa, float sb, float b) {
+  const uint32_t p01 = w & 0x000F000Fu, p23 = w & 0x00F000F0u, w8 = w >> 8;
+  const uint32_t p45 = w8 & 0x000F000Fu, p67 = w8 & 0x00F000F0u;
+  return u32x4{pack_bf2(__builtin_fmaf(sa, h16_lo(p01), b), __builtin_fmaf(sa, h16_hi(p01), b)),
+               pack_bf2(__builtin_fmaf(sb, h16_lo(p23), b), __builtin_fmaf(sb, h16_hi(p23), b)),
+               pack_bf2(__builtin_fmaf(sa, h16_lo(p45), b), __builtin_fmaf(sa, h16_hi(p45), b)),
+               pack_bf2(__builtin_fmaf(sb, h16_lo(p67), b), __builtin_fmaf(sb, h16_hi(p67), b))};
 }
+// The two scalings of a group's bf16 scale s for t64_dequant.
+__device__ __forceinline__ float t64_sa(float s) { return s * 16777216.f; }
+__device__ __forceinline__ float t64_sb(float s) { return s * 1048576.f; }
 
 }  // namespace ifd
