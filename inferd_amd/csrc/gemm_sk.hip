@@ -12,15 +12,18 @@
 // k_sk_fixup then sums each cut tile's pieces in unit order, in parallel over all CUs, and stores it: the result
 // does not depend on timing.
 //
-// Block: 8 waves; wave w owns band w of the tile over all MT M tiles (one dequantized B fragment feeds MT MFMAs).
-// Two LDS rings filled by direct global -> LDS DMA: NA activation slabs [BM][64 bf16] (16-byte columns XOR-swizzled
-// by row pair) and NW weight stages (8 code halves + 8 (s, b) rows). Waves 0-3 issue the activation DMAs, waves 4-7
-// the weight DMAs, each with its own in-order vmcnt stream; the stream positions advance incrementally (no per-step
-// division). The dequant of step i + 1 is issued alongside the MFMAs of step i. Every DMA is issued by a whole wave
-// under wave-uniform control flow (the LDS base goes to M0). Finished tiles are staged through LDS and leave as
+// Block: 4 waves (one per SIMD); wave w owns bands 2w and 2w + 1 of the tile over all MT M tiles, so one
+// activation fragment read from LDS feeds two MFMAs and one dequantized weight fragment feeds MT. One LDS ring
+// filled by direct global -> LDS DMA; a stage holds a step's activation slab [BM][64 bf16] (16-byte columns
+// XOR-swizzled by row pair) and its weights (8 code halves + 8 (s, b) rows). Each wave issues its own share of both
+// (the activation rows 8 (MT w + q) .. + 7 and its two bands' codes; wave 0 also the (s, b) rows) as one in-order
+// vmcnt stream, the activations R - 1 steps ahead and the weights R; the stream positions advance incrementally (no
+// per-step division). Within a step the wave reads its activation fragments and the next step's codes from LDS
+// first, then runs its MFMAs with the next step's dequant scheduled between them. Every DMA is issued by a whole
+// wave under wave-uniform control flow (the LDS base goes to M0). Finished tiles are staged through LDS and leave as
 // whole rows.
 //
-// SwiGLU mode: tile t holds gate bands 4t..4t+3 (waves 0-3) and the matching up bands (waves 4-7); the staged tile
+// SwiGLU mode: tile t holds gate bands 4t..4t+3 (waves 0, 1) and the matching up bands (waves 2, 3); the staged tile
 // (or the fixup) gives h = silu(bf16(gate)) * bf16(up) (reference silu_mul, core.metal:777-787).
 #include <algorithm>
 
@@ -33,29 +36,25 @@
 
 namespace ifd {
 
-constexpr int kSkThreads = 512;
-constexpr int kSkWBytes = 8 * kT64Codes + 8 * 128;  // weight stage: 8 code halves + 8 (s, b) rows
+constexpr int kSkWaves = 4;
+constexpr int kSkThreads = 64 * kSkWaves;
+constexpr int kSkDeqValu = 2 * (4 * 17 + 8);  // VALU of a wave's dequant per step: 2 bands x (4 words, the scales)
+constexpr int kSkWBytes = 8 * kT64Codes + 8 * 128;  // weights of a stage: 8 code halves + 8 (s, b) rows
 constexpr int kSkLds = 160 * 1024;  // LDS per CU
 constexpr int kSkRow = 256 + 4;  // staged tile row stride (floats): rows h = 0, 1 of one store fall in other banks
 
-// 32-row tiles run two blocks per CU (four waves per SIMD hide the latency of their short steps); a ring of four or
-// more stages keeps the weight stream at full rate. 128-row tiles favour a deeper activation ring (16 KB slabs) over a
-// deeper weight ring (measured).
+// 32-row tiles run two blocks per CU (two waves per SIMD hide the latency of their short steps), larger tiles one.
+// A stage holds one step's activation slab and weights; the ring is as deep as LDS allows, at most 8 stages.
 __host__ __device__ constexpr int sk_bpc(int MT) { return MT == 1 ? 2 : 1; }
 __host__ __device__ constexpr int sk_abytes(int MT) { return MT * 32 * 128; }
-__host__ __device__ constexpr int sk_na(int MT) { return MT == 1 ? 4 : MT == 2 ? 5 : 6; }
-__host__ __device__ constexpr int sk_nw(int MT) {
-  return MT == 4 ? 5
-         : (kSkLds / sk_bpc(MT) - 64 - sk_na(MT) * sk_abytes(MT)) / kSkWBytes < 15
-             ? (kSkLds / sk_bpc(MT) - 64 - sk_na(MT) * sk_abytes(MT)) / kSkWBytes
-             : 15;
+__host__ __device__ constexpr int sk_stage(int MT) { return sk_abytes(MT) + kSkWBytes; }
+__host__ __device__ constexpr int sk_ring(int MT) {
+  return (kSkLds / sk_bpc(MT) - 64) / sk_stage(MT) < 8 ? (kSkLds / sk_bpc(MT) - 64) / sk_stage(MT) : 8;
 }
-__host__ __device__ constexpr size_t sk_rings(int MT) {
-  return (size_t)sk_na(MT) * sk_abytes(MT) + (size_t)sk_nw(MT) * kSkWBytes;
-}
-// the rings, and after the K loop the staged tile [32 MT][kSkRow] fp32 in the same memory
+// the ring, and after the K loop the staged tile [32 MT][kSkRow] fp32 in the same memory
 __host__ __device__ constexpr size_t sk_lds(int MT) {
-  return sk_rings(MT) > (size_t)MT * 32 * kSkRow * 4 ? sk_rings(MT) : (size_t)MT * 32 * kSkRow * 4;
+  return (size_t)sk_ring(MT) * sk_stage(MT) > (size_t)MT * 32 * kSkRow * 4 ? (size_t)sk_ring(MT) * sk_stage(MT)
+                                                                             : (size_t)MT * 32 * kSkRow * 4;
 }
 
 struct GemmSkArgs {
@@ -65,7 +64,7 @@ struct GemmSkArgs {
   int N, K;
   void* C;
   int ldc, M, mode;
-  float* part;  // partial slots [2 nblk][8 waves][MT * 16 / 4][64] float4 (MFMA fragment order)
+  float* part;  // partial slots [2 nblk][8 bands][MT * 16 / 4][64] float4 (MFMA fragment order)
   uint32_t part_bytes;
   int tiles_m, tiles_n, G, nblk;
   int swi;  // SwiGLU mode: bands per half (N / 64); 0 otherwise
@@ -76,13 +75,11 @@ __host__ __device__ inline int sk_block_of(long u, int nblk, long U) { return (i
 
 template <int MT>
 __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p) {
-  constexpr int BM = 32 * MT, NA = sk_na(MT), NW = sk_nw(MT), A_BYTES = sk_abytes(MT);
-  constexpr int NE = MT * 16;  // accumulators per lane
-  static_assert(NA >= 3 && NW >= 4 && sk_lds(MT) + 64 <= kSkLds / sk_bpc(MT), "LDS plan");
-  static_assert(3 * (NW - 2) <= 63 && MT * (NA - 2) <= 63, "vmcnt range");
+  constexpr int BM = 32 * MT, R = sk_ring(MT), A_BYTES = sk_abytes(MT), STAGE = sk_stage(MT);
+  constexpr int NE = MT * 16;  // accumulators per lane and band
+  static_assert(R >= 4 && sk_lds(MT) + 64 <= kSkLds / sk_bpc(MT), "LDS plan");
+  static_assert((R - 2) * (MT + 3) + 3 <= 63, "vmcnt range");
   extern __shared__ __align__(16) uint8_t lds[];
-  uint8_t* const aring = lds;
-  uint8_t* const wring = lds + NA * A_BYTES;
   float* const stg = (float*)lds;  // staged tile [BM][kSkRow], after the K loop
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -100,57 +97,71 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
     return min(bb, nbands - 1);
   };
 
-  // ---- DMA streams: waves 0-3 the activations, waves 4-7 the weights; (tile, group) of the next step to issue
-  int s_tile = u0 / G, s_g = u0 % G, s_i = 0, s_st = 0;
-  const uint16_t* arow[MT];  // waves 0-3: this lane's source row (and 16-byte column) of each DMA in the tile
-  const uint8_t* wsrc[3];    // waves 4-7: this lane's code sources (two bands) and (s, b) source (wave 7)
-  auto stream_tile = [&](int tile) __attribute__((always_inline)) {
-    const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
-    if (wave < 4) {
+  // ---- this wave's DMA stream. Stage s of the ring holds the activation slab of one step ([BM][64 bf16], 16-byte
+  // columns XOR-swizzled by row pair) and its weights (8 code halves, then 8 (s, b) rows). Unit j's activations and
+  // weights share stage j % R. At step i the wave issues the activations of step i + R - 1 (its MT DMAs of 8 rows)
+  // and the weights of step i + R (the code halves of its two bands; wave 0 also the (s, b) rows of all 8), each
+  // stream with its own (tile, group) position.
+  const bool has_sb = wave == 0;
+  const uint16_t* arow[MT];  // this lane's source row (and 16-byte column) of each activation DMA in the tile
+  const uint8_t* wsrc[3];    // this lane's code sources (two bands) and (s, b) source
+  auto a_tile_addr = [&](int tile) __attribute__((always_inline)) {
+    const int tm = tile % p.tiles_m;
 #pragma unroll
-      for (int q = 0; q < MT; q++) {
-        const int r = 8 * (MT * wave + q) + lane / 8;
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
-        arow[q] = p.A + (size_t)min(tm * BM + r, p.M - 1) * p.lda + 8 * c;
-      }
-    } else {
-      const int ww = wave - 4;
-      wsrc[0] = p.wt + (size_t)phys_band(tn, 2 * ww) * kT64Tile + 16 * lane;
-      wsrc[1] = p.wt + (size_t)phys_band(tn, 2 * ww + 1) * kT64Tile + 16 * lane;
-      wsrc[2] = p.wt + (size_t)phys_band(tn, lane / 8) * kT64Tile + kT64Codes + 16 * (lane & 7);
+    for (int q = 0; q < MT; q++) {
+      const int r = 8 * (MT * wave + q) + lane / 8;
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      arow[q] = p.A + (size_t)min(tm * BM + r, p.M - 1) * p.lda + 8 * c;
     }
   };
-  stream_tile(s_tile);
-  auto issue = [&]() __attribute__((always_inline)) {
-    if (wave < 4) {
-      uint8_t* st = aring + s_st * A_BYTES;
+  auto w_tile_addr = [&](int tile) __attribute__((always_inline)) {
+    const int tn = tile / p.tiles_m;
+    wsrc[0] = p.wt + (size_t)phys_band(tn, 2 * wave) * kT64Tile + 16 * lane;
+    wsrc[1] = p.wt + (size_t)phys_band(tn, 2 * wave + 1) * kT64Tile + 16 * lane;
+    wsrc[2] = p.wt + (size_t)phys_band(tn, lane / 8) * kT64Tile + kT64Codes + 16 * (lane & 7);
+  };
+  int a_tile = u0 / G, a_g = u0 % G, a_i = 0, a_st = 0;
+  int w_tile = a_tile, w_g = a_g, w_i = 0, w_st = 0;
+  a_tile_addr(a_tile);
+  w_tile_addr(w_tile);
+  auto issue_a = [&]() __attribute__((always_inline)) {
+    uint8_t* st = lds + a_st * STAGE;
 #pragma unroll
-      for (int q = 0; q < MT; q++) dma16(arow[q] + (size_t)s_g * kGroup, st + (MT * wave + q) * 1024);
-      s_st = s_st + 1 == NA ? 0 : s_st + 1;
-    } else {
-      uint8_t* st = wring + s_st * kSkWBytes;
-      const size_t off = (size_t)s_g * gstride;
-      const int ww = wave - 4;
-      dma16(wsrc[0] + off, st + (2 * ww) * kT64Codes);
-      dma16(wsrc[1] + off, st + (2 * ww + 1) * kT64Codes);
-      if (wave == 7) dma16(wsrc[2] + off, st + 8 * kT64Codes);
-      s_st = s_st + 1 == NW ? 0 : s_st + 1;
+    for (int q = 0; q < MT; q++) dma16(arow[q] + (size_t)a_g * kGroup, st + (MT * wave + q) * 1024);
+    a_st = a_st + 1 == R ? 0 : a_st + 1;
+    a_i++;
+    if (++a_g == G) {
+      a_g = 0;
+      if (a_i < n) a_tile_addr(++a_tile);
     }
-    s_i++;
-    if (++s_g == G) {
-      s_g = 0;
-      stream_tile(++s_tile);
+  };
+  auto issue_w = [&]() __attribute__((always_inline)) {
+    uint8_t* st = lds + w_st * STAGE + A_BYTES;
+    const size_t off = (size_t)w_g * gstride;
+    dma16(wsrc[0] + off, st + (2 * wave) * kT64Codes);
+    dma16(wsrc[1] + off, st + (2 * wave + 1) * kT64Codes);
+    if (has_sb) dma16(wsrc[2] + off, st + 8 * kT64Codes);
+    w_st = w_st + 1 == R ? 0 : w_st + 1;
+    w_i++;
+    if (++w_g == G) {
+      w_g = 0;
+      if (w_i < n) w_tile_addr(++w_tile);
     }
   };
 
-  // this wave's band from weight stage ws, dequantized
-  auto dequant = [&](int ws, u32x4 (&bf)[4]) __attribute__((always_inline)) {
-    const uint8_t* wst = wring + ws * kSkWBytes;
-    const u32x4 codes = *(const u32x4*)(wst + wave * kT64Codes + 16 * lane);
-    const uint32_t sb = *(const uint32_t*)(wst + 8 * kT64Codes + wave * 128 + 4 * j);
-    const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), sa = t64_sa(sc), sbs = t64_sb(sc);
+  // this wave's two bands of the weights in stage s, dequantized
+  auto dequant = [&](int s, u32x4 (&bf)[2][4]) __attribute__((always_inline)) {
+    const uint8_t* wst = lds + s * STAGE + A_BYTES;
 #pragma unroll
-    for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sa, sbs, bi);
+    for (int nb = 0; nb < 2; nb++) {
+      const int band = 2 * wave + nb;
+      const u32x4 codes = *(const u32x4*)(wst + band * kT64Codes + 16 * lane);
+      const uint32_t sb = *(const uint32_t*)(wst + 8 * kT64Codes + band * 128 + 4 * j);
+      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16));
+      const float sa = t64_sa(sc), sbs = t64_sb(sc);
+#pragma unroll
+      for (int t = 0; t < 4; t++) bf[nb][t] = t64_dequant(codes[t], sa, sbs, bi);
+    }
   };
   // activation fragments of M tile a: MFMA step t takes k = 32 h + 8 t .. + 7 (logical column 4 h + t)
   auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) __attribute__((always_inline)) {
@@ -159,53 +170,79 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
     for (int t = 0; t < 4; t++) af[t] = *(const u32x4*)(st + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
   };
 
-  f32x16 acc[MT], acc0[MT];  // acc0: the first segment, once the run crosses into a second tile
+  f32x16 acc[2][MT];
 #pragma unroll
-  for (int a = 0; a < MT; a++) acc[a] = zero16(), acc0[a] = zero16();
+  for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+    for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
 
-  // Pipeline. Waves 0-3 have issued A(0 .. i + NA - 2) at the top of step i and need A(i); waves 4-7 have issued
-  // W(0 .. i + NW - 2) and need W(i + 1) (dequantized during step i). DMAs complete in order per wave: waiting until
-  // at most the younger DMAs of this wave's own stream are outstanding leaves exactly those in flight (other
-  // outstanding operations, such as partial stores, only lengthen the wait). The stage a DMA overwrites held a step
-  // every wave finished before the barrier.
-  const int nwv = wave == 7 ? 3 : 2;  // weight DMAs per step of this wave
-  {
-    const int pre = min(wave < 4 ? NA - 1 : NW - 1, n);
-    for (int i = 0; i < pre; i++) issue();
+  // Waits. At step i the wave needs A(i) and W(i + 1), both issued at step i - R + 1 (the prologue for the first
+  // steps), W(i + 1) after A(i): it waits until at most the DMAs issued after W(i + 1) are outstanding (every
+  // operation of a wave completes in issue order; younger output stores only lengthen the wait). In the last R
+  // steps of the run fewer are in flight: wait for all.
+  constexpr int nwa = 3, nwo = 2;  // weight DMAs per step of wave 0 / of the others
+  auto wait_step = [&](int i) __attribute__((always_inline)) {
+    if (i + R > n) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (i < R - 2) {  // the prologue's lone W(R - 1) sits between
+      if (has_sb) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 3) * (MT + nwa) + nwa) : "memory");
+      else asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 3) * (MT + nwo) + nwo) : "memory");
+    } else {
+      if (has_sb) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 2) * (MT + nwa)) : "memory");
+      else asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 2) * (MT + nwo)) : "memory");
+    }
+  };
+  // prologue: A(0..R-2) and W(0..R-1) (those of the run), then W(0) for the first dequant
+  for (int jj = 0; jj < R - 1; jj++) {
+    if (a_i < n) issue_a();
+    if (w_i < n) issue_w();
   }
-  if (wave >= 4) {  // W(0) for the first dequant
-    const int y = min(NW - 2, n - 1);
-    if (nwv == 3) wait_vm_dyn<3, NW - 2>(y);
-    else wait_vm_dyn<2, NW - 2>(y);
+  if (w_i < n) issue_w();
+  if (n < R) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    if (has_sb) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 2) * (MT + nwa) + nwa) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 2) * (MT + nwo) + nwo) : "memory");
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  u32x4 bf0[4], bf1[4];
+  u32x4 bf0[2][4], bf1[2][4];
   dequant(0, bf0);
-  int ca = 0, cw = 1 % NW;  // A stage of step i, weight stage of step i + 1
+  int ca = 0, cw = 1 % R;  // stage of step i (activations) and of step i + 1 (weights to dequantize)
 
   // step i with the B fragments of step i in bc; dequantizes step i + 1 into bn
-  auto step = [&](int i, u32x4 (&bc)[4], u32x4 (&bn)[4]) __attribute__((always_inline)) {
-    if (wave < 4) {
-      wait_vm_dyn<MT, NA - 2>(min(NA - 2, n - 1 - i));
-    } else if (i + 1 < n) {
-      const int y = min(NW - 3, n - 2 - i);
-      if (nwv == 3) wait_vm_dyn<3, NW - 3>(y);
-      else wait_vm_dyn<2, NW - 3>(y);
-    }
+  auto step = [&](int i, u32x4 (&bc)[2][4], u32x4 (&bn)[2][4]) __attribute__((always_inline)) {
+    wait_step(i);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (s_i < n) issue();
-    dequant(cw, bn);  // past the run's end a stale stage, never used: one basic block with the MFMAs
-    const uint8_t* ast = aring + ca * A_BYTES;
-    u32x4 af[2][4];
-    load_a(ast, 0, af[0]);
+    if (a_i < n) issue_a();
+    if (w_i < n) issue_w();
+    // One basic block: the step's activation fragments and the next step's codes from LDS, then the MFMAs with the
+    // next step's dequant between them, so that the VALU work and the LDS latency overlap the matrix core. Past the
+    // run's end the dequant reads a stale stage, never used.
+    const uint8_t* ast = lds + ca * STAGE;
+    u32x4 af[MT][4];
 #pragma unroll
-    for (int a = 0; a < MT; a++) {
-      if (a + 1 < MT) load_a(ast, a + 1, af[(a + 1) & 1]);
+    for (int a = 0; a < MT; a++) load_a(ast, a, af[a]);
+    dequant(cw, bn);
 #pragma unroll
-      for (int t = 0; t < 4; t++) acc[a] = mfma_bf16(af[a & 1][t], bc[t], acc[a]);
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[nb][a] = mfma_bf16(af[a][t], bc[nb][t], acc[nb][a]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4 * MT + 4, 0);  // the LDS reads
+#pragma unroll
+    for (int k = 0; k < 8 * MT; k++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                    // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, (kSkDeqValu + 8 * MT - 1) / (8 * MT), 0);  // VALU between
     }
-    ca = ca + 1 == NA ? 0 : ca + 1;
-    cw = cw + 1 == NW ? 0 : cw + 1;
+    // the next step's fragments are complete in this step (else the compiler may sink the dequant past the next
+    // barrier, next to its use)
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) asm volatile("" : "+v"(bn[nb][t]));
+    ca = ca + 1 == R ? 0 : ca + 1;
+    cw = cw + 1 == R ? 0 : cw + 1;
   };
   // steps [lo, hi) with the current fragments in bf0 on entry and on exit
   auto run = [&](int lo, int hi) __attribute__((always_inline)) {
@@ -217,25 +254,30 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
     if (i < hi) {
       step(i, bf0, bf1);
 #pragma unroll
-      for (int t = 0; t < 4; t++) bf0[t] = bf1[t];
+      for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) bf0[nb][t] = bf1[nb][t];
     }
   };
 
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void*)p.part, 0, (int)p.part_bytes, 0x00020000);
   const size_t slot_floats = (size_t)8 * NE * 64;
-  auto slot_off = [&](int slot, int a, int q) __attribute__((always_inline)) {  // byte offset of this lane's float4 (a, rows 4q..4q+3) in a slot
-    return (int)((((size_t)slot * slot_floats + (size_t)wave * NE * 64) + ((size_t)(a * 4 + q) * 64 + lane) * 4) * 4);
+  // byte offset of this lane's float4 (band, M tile a, rows 4q..4q+3) in a slot
+  auto slot_off = [&](int slot, int band, int a, int q) __attribute__((always_inline)) {
+    return (int)((((size_t)slot * slot_floats + (size_t)band * NE * 64) + ((size_t)(a * 4 + q) * 64 + lane) * 4) * 4);
   };
-  auto write_slot = [&](int slot, f32x16 (&v)[MT]) __attribute__((always_inline)) {
+  auto write_slot = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
-    for (int a = 0; a < MT; a++)
+    for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const u32x4 x = {__float_as_uint(v[a][4 * q]), __float_as_uint(v[a][4 * q + 1]),
-                         __float_as_uint(v[a][4 * q + 2]), __float_as_uint(v[a][4 * q + 3])};
-        __builtin_amdgcn_raw_buffer_store_b128(x, rs, slot_off(slot, a, q), 0, 0);
-      }
+      for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const u32x4 x = {__float_as_uint(acc[nb][a][4 * q]), __float_as_uint(acc[nb][a][4 * q + 1]),
+                           __float_as_uint(acc[nb][a][4 * q + 2]), __float_as_uint(acc[nb][a][4 * q + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(x, rs, slot_off(slot, 2 * wave + nb, a, q), 0, 0);
+        }
   };
 
   const int tile_first = u0 / G, tile_last = (u1 - 1) / G;
@@ -243,53 +285,64 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
   const int n1 = min(n, (tile_first + 1) * G - u0);
   run(0, n1);
   if (two) {
+    write_slot(2 * b);  // the first tile's piece, while the run goes on
 #pragma unroll
-    for (int a = 0; a < MT; a++) acc0[a] = acc[a], acc[a] = zero16();
-    write_slot(2 * b, acc0);  // the first tile's piece, while the run goes on
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+      for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
     run(n1, n);
   }
   // every DMA and partial store has landed; LDS is free once all waves are past their reads
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  // ---- epilogue: the last segment, stored when it is a whole tile, else a piece in slot 2 b + (two ? 1 : 0)
-  const int tlo = tile_last * G;
-  if (u0 > tlo || u1 < tlo + G) {
-    write_slot(2 * b + (two ? 1 : 0), acc);
-    return;
-  }
+  // a whole tile's acc, staged through LDS and stored as rows (SwiGLU: h)
+  auto store_tile = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
-  for (int a = 0; a < MT; a++)
+    for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) stg[(a * 32 + 8 * (r / 4) + 4 * h + (r % 4)) * kSkRow + 32 * wave + j] = acc[a][r];
-  __syncthreads();
-  const int tm = tile_last % p.tiles_m, tn = tile_last / p.tiles_m;
-  if (p.swi) {
-    uint16_t* C = (uint16_t*)p.C;
-    for (int e = tid; e < BM * 32; e += kSkThreads) {
-      const int row = e >> 5, c4 = (e & 31) * 4, grow = tm * BM + row;
-      if (grow >= p.M) continue;
-      const float4 g = *(const float4*)(stg + row * kSkRow + c4);
-      const float4 u = *(const float4*)(stg + row * kSkRow + 128 + c4);
-      const uint32_t lo =
-          pack_bf2(swiglu_f(bf2f(f2bf(g.x)), bf2f(f2bf(u.x))), swiglu_f(bf2f(f2bf(g.y)), bf2f(f2bf(u.y))));
-      const uint32_t hi =
-          pack_bf2(swiglu_f(bf2f(f2bf(g.z)), bf2f(f2bf(u.z))), swiglu_f(bf2f(f2bf(g.w)), bf2f(f2bf(u.w))));
-      *(u32x2*)(C + (size_t)grow * p.ldc + tn * 128 + c4) = u32x2{lo, hi};
-    }
-    return;
-  }
-  for (int e = tid; e < BM * 64; e += kSkThreads) {
-    const int row = e >> 6, c4 = (e & 63) * 4, grow = tm * BM + row, gcol = tn * 256 + c4;
-    if (grow >= p.M || gcol >= p.N) continue;
-    const float* sv = stg + row * kSkRow + c4;
-    const size_t o = (size_t)grow * p.ldc + gcol;
-    if (gcol + 4 <= p.N && (o & 3) == 0 && p.mode != 1) {
-      if (p.mode == 2) *(float4*)((float*)p.C + o) = *(const float4*)sv;
-      else *(u32x2*)((uint16_t*)p.C + o) = u32x2{pack_bf2(sv[0], sv[1]), pack_bf2(sv[2], sv[3])};
+      for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          stg[(a * 32 + 8 * (r / 4) + 4 * h + (r % 4)) * kSkRow + 32 * (2 * wave + nb) + j] = acc[nb][a][r];
+    __syncthreads();
+    const int tm = t % p.tiles_m, tn = t / p.tiles_m;
+    if (p.swi) {
+      uint16_t* C = (uint16_t*)p.C;
+      for (int e = tid; e < BM * 32; e += kSkThreads) {
+        const int row = e >> 5, c4 = (e & 31) * 4, grow = tm * BM + row;
+        if (grow >= p.M) continue;
+        const float4 g = *(const float4*)(stg + row * kSkRow + c4);
+        const float4 u = *(const float4*)(stg + row * kSkRow + 128 + c4);
+        const uint32_t lo =
+            pack_bf2(swiglu_f(bf2f(f2bf(g.x)), bf2f(f2bf(u.x))), swiglu_f(bf2f(f2bf(g.y)), bf2f(f2bf(u.y))));
+        const uint32_t hi =
+            pack_bf2(swiglu_f(bf2f(f2bf(g.z)), bf2f(f2bf(u.z))), swiglu_f(bf2f(f2bf(g.w)), bf2f(f2bf(u.w))));
+        *(u32x2*)(C + (size_t)grow * p.ldc + tn * 128 + c4) = u32x2{lo, hi};
+      }
     } else {
-      for (int k = 0; k < 4 && gcol + k < p.N; k++) store_mode(p.C, o + k, sv[k], p.mode);
+      for (int e = tid; e < BM * 64; e += kSkThreads) {
+        const int row = e >> 6, c4 = (e & 63) * 4, grow = tm * BM + row, gcol = tn * 256 + c4;
+        if (grow >= p.M || gcol >= p.N) continue;
+        const float* sv = stg + row * kSkRow + c4;
+        const size_t o = (size_t)grow * p.ldc + gcol;
+        if (gcol + 4 <= p.N && (o & 3) == 0 && p.mode != 1) {
+          if (p.mode == 2) *(float4*)((float*)p.C + o) = *(const float4*)sv;
+          else *(u32x2*)((uint16_t*)p.C + o) = u32x2{pack_bf2(sv[0], sv[1]), pack_bf2(sv[2], sv[3])};
+        } else {
+          for (int k = 0; k < 4 && gcol + k < p.N; k++) store_mode(p.C, o + k, sv[k], p.mode);
+        }
+      }
     }
+  };
+
+  // ---- epilogue: the last segment, stored when it is a whole tile, else a piece of a cut tile
+  const int tlo = tile_last * G;
+  const bool whole = u0 <= tlo && u1 >= tlo + G;
+  if (whole) {
+    store_tile(tile_last);
+    return;
   }
+  write_slot(2 * b + (two ? 1 : 0));  // a piece of a cut tile: k_sk_fixup sums the pieces
 }
 
 // Sum of a cut tile's pieces (partial slots, in unit order) and its store. Block (tile, w, f): one wave over the

@@ -309,7 +309,7 @@ int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void
                   void* ws, size_t ws_bytes, hipStream_t st) {
   if (M == 0) return IFD_OK;
   if (K % 128) return fail(IFD_ERR_ARG, "T64 GEMM needs K %% 128 == 0 (K=%d)", K);
-  // decode batches: the stream-K kernel (every CU streams an equal share of the weights, fixup in the kernel)
+  // decode batches: the stream-K kernel (every CU streams an equal share of the weights, fixup kernel after)
   if (!use_t8(M, N) && gemm_sk_applies(M, N, K, mode))
     return launch_gemm_sk(A, lda, wt, N, K, C, ldc, M, mode, ws, ws_bytes, st);
   if (use_t8(M, N)) {

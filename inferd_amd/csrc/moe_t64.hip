@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
   constexpr int NCW = TWO ? 4 : 2;             // code DMAs per weight wave per step
   static_assert(!(SILU && WIDE), "SwiGLU pairs a gate and an up band per wave");
   static_assert(gq_lds(MT, TWO) <= 160 * 1024, "LDS plan");
-  static_assert(MT * (NA - 2) + 8 * MT <= 63 && (NCW + 1) * (NW - 3) + 8 * MT <= 63, "vmcnt range");
+  static_assert(MT * (NA - 2) + 8 * MT <= 63 && (NCW + 1) * (NW - 2) + 8 * MT <= 63, "vmcnt range");
   extern __shared__ __align__(16) uint8_t lds[];
   uint8_t* const aring = lds;
   uint8_t* const wring = lds + NA * A_BYTES;
@@ -123,20 +123,30 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
     int e, c, q0, q1;
     item_rows(item, e, c, q0, q1);
     if (wave < 4) {
+      // the wave's 8 MT row indices: all scalar loads in flight at once, then one wait
+      int v[MT][8];
+#pragma unroll
+      for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int rho = 0; rho < 8; rho++) v[i][rho] = min(q0 + 8 * (MT * wave + i) + rho, q1 - 1);
+      if (p.perm) {
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+          for (int rho = 0; rho < 8; rho++) v[i][rho] = sload(p.perm, v[i][rho]);
+        if (p.div_m)
+#pragma unroll
+          for (int i = 0; i < MT; i++)
+#pragma unroll
+            for (int rho = 0; rho < 8; rho++)
+              v[i][rho] = (int)__builtin_amdgcn_readfirstlane(__umulhi((uint32_t)v[i][rho], p.div_m));
+      }
 #pragma unroll
       for (int i = 0; i < MT; i++) {
         const int r0 = 8 * (MT * wave + i);
         int src = 0;
 #pragma unroll
-        for (int rho = 0; rho < 8; rho++) {
-          const int q = min(q0 + r0 + rho, q1 - 1);
-          int v = q;
-          if (p.perm) {
-            v = sload(p.perm, q);
-            if (p.div_m) v = (int)__builtin_amdgcn_readfirstlane(__umulhi((uint32_t)v, p.div_m));
-          }
-          src = (lane >> 3) == rho ? v : src;
-        }
+        for (int rho = 0; rho < 8; rho++) src = (lane >> 3) == rho ? v[i][rho] : src;
         const int r = r0 + (lane >> 3);
         const int c16 = (lane & 7) ^ ((r >> 1) & 7);
         arow[i] = p.A + (size_t)src * p.lda + 8 * c16;
@@ -198,26 +208,16 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
 
   // Waits. A wave waits until only younger operations than the DMA it needs are outstanding: its later DMAs and
   // the output stores (NST per item end) of the item ends it issued after that DMA. Every operation of a wave
-  // completes in issue order, so the needed DMA has landed. d1, d2: steps since the last two item ends.
+  // completes in issue order, so the needed DMA has landed. nrec: those item ends (0, 1 or 2).
   constexpr int NST = 2 * MT * (WIDE ? 2 : 1);  // output stores per item end
-  auto wait_a = [&](int k, int x) __attribute__((always_inline)) {
-    if (x == 0) wait_vm_dyn<MT, NA - 2>(k);
-    else if (x == 1) wait_vm_off<MT, NA - 2, NST>(k);
-    else wait_vm_off<MT, NA - 2, 2 * NST>(k);
-  };
-  auto wait_w = [&](int k, int x, bool first) __attribute__((always_inline)) {  // k = younger weight steps outstanding
+  auto wait_a = [&](int k, int nrec) __attribute__((always_inline)) { wait_vm_rec<MT, NA - 2, NST>(k, nrec); };
+  auto wait_w = [&](int k, int nrec, bool first) __attribute__((always_inline)) {  // k = younger weight steps
     if (first) {
       if (has_sb) wait_vm_dyn<NCW + 1, NW - 2>(k);
       else wait_vm_dyn<NCW, NW - 2>(k);
-    } else if (x == 0) {
-      if (has_sb) wait_vm_dyn<NCW + 1, NW - 3>(k);
-      else wait_vm_dyn<NCW, NW - 3>(k);
-    } else if (x == 1) {
-      if (has_sb) wait_vm_off<NCW + 1, NW - 3, NST>(k);
-      else wait_vm_off<NCW, NW - 3, NST>(k);
     } else {
-      if (has_sb) wait_vm_off<NCW + 1, NW - 3, 2 * NST>(k);
-      else wait_vm_off<NCW, NW - 3, 2 * NST>(k);
+      if (has_sb) wait_vm_rec<NCW + 1, NW - 3, NST>(k, nrec);
+      else wait_vm_rec<NCW, NW - 3, NST>(k, nrec);
     }
   };
   {
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
   // W(i + 1); the stage a DMA issued here overwrites held a step every wave finished before the barrier.
   // Item ends whose stores are younger than the DMA awaited at step i: for A(i), issued at step i - NA + 1, those
   // at the ends of steps i - NA + 1 .. i - 1; for W(i + 1), issued at step i + 2 - NW, those from step i + 2 - NW.
-  int d1 = 1 << 20, d2 = 1 << 20;
+  int d1 = 1 << 20, d2 = 1 << 20;  // steps since the last two item ends
   auto step = [&](int i, u32x4 (&bc)[NBW][4], u32x4 (&bn)[NBW][4]) __attribute__((always_inline)) {
     if (wave < 4) wait_a(min(NA - 2, n - 1 - i), (d1 < NA - 1) + (d2 < NA - 1));
     else if (i + 1 < n) wait_w(min(NW - 3, n - 2 - i), (d1 < NW - 2) + (d2 < NW - 2), false);
