@@ -279,10 +279,12 @@ size_t ifd_mlp_decode_workspace(int M, int H, int I);
 int ifd_mlp_decode(void* x, int ldx, const void* norm_w, float eps, const void* gu_t64, const void* dn_t64, int M,
                    int H, int I, void* workspace, size_t ws_bytes, void* stream);
 
-/* Decode MoE for T <= 8 tokens (reference moe_plan / moe_gu2 / moe_dn2 and their router, moe.metal:267-551; host
- * qwen35.h:1876-1908): router logits (fp32) -> routing -> the distinct experts of the step -> gate/up + SwiGLU ->
+/* Decode MoE for T <= 16 tokens (reference moe_plan / moe_gu2 / moe_dn2 and their router, moe.metal:267-551; host
+ * qwen35.h:1876-1908; beyond 8 tokens, while T k < 128, the reference's per-row expert GEMVs moe_qmv4 +
+ * moe_silu_mul + moe_combine, moe.metal:6-58, 103-187, host qwen35.h:1801-1807, 1947-1955, which compute the same
+ * per-row arithmetic): router logits (fp32) -> routing -> the distinct experts of the step -> gate/up + SwiGLU ->
  * down + combine, three launches, each distinct expert's weights read once for all tokens that picked it. Every
- * expert product uses the decode GEMV arithmetic (qmv4). The shared expert (sgu [2I][H], sdn [H][I], 4-bit, or NULL)
+ * expert product uses the decode GEMV arithmetic (qmv4), and a token's result does not depend on the others. The shared expert (sgu [2I][H], sdn [H][I], 4-bit, or NULL)
  * shares the routed experts' I. out = bf16(acc) (assign) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] d_j +
  * sg[t] d_shared. idx / wt / sg / logits ([T][E + shared_gate] fp32, the values routed on) are written if non-NULL.
  * H % 512 == 0, I % 64 == 0, E <= 512, k <= 16. Workspace: ifd_moe_decode_workspace (its header counters zeroed
@@ -294,6 +296,16 @@ int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int 
                    const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b,
                    void* out, int assign, int* idx, float* wt, float* sg, float* logits, void* workspace,
                    size_t ws_bytes, void* stream);
+/* The same from router logits the caller computed: logits_in fp32 [T][E + shared_gate] (the shared expert's gate
+ * logit last). For routers the decode kernel does not read, such as the reference's 8-bit router (moe_router8,
+ * moe.metal:553-600, routed at qwen35.h:1878-1882): ifd_gemm_w8 in mode 2 computes those logits with its qmv8
+ * arithmetic, per group s sum q x + b sum x. Same workspace as ifd_moe_decode. */
+int ifd_moe_decode_logits(const float* logits_in, const void* xn, int T, int H, int E, int k, int norm,
+                          int shared_gate, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
+                          const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I,
+                          const uint32_t* sgu_wq, const uint16_t* sgu_s, const uint16_t* sgu_b,
+                          const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b, void* out, int assign,
+                          int* idx, float* wt, float* sg, void* workspace, size_t ws_bytes, void* stream);
 
 /* ---- measurement probes (outside the operator path) ----------------------------------------------------------
  * The HBM and MFMA ceilings a benchmark reports beside the datasheet peaks, in the role of the reference's

@@ -585,9 +585,9 @@ int ifd_probe_mfma(int int8, int iters, int blocks, float* out, void* stream) {
   return launch_probe_mfma(int8, iters, blocks, out, S(stream));
 }
 
-// ---- decode MoE (T <= 8) ---------------------------------------------------------------------------------------
+// ---- decode MoE (T <= 16) ---------------------------------------------------------------------------------------
 size_t ifd_moe_decode_workspace(int T, int H, int I, int E, int k) {
-  if (T <= 0 || T > 8 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  if (T <= 0 || T > 16 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
   return with_header(mdec_layout(T, H, I, E, k).total);
 }
 
@@ -597,7 +597,7 @@ int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int 
                    const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b,
                    void* out, int assign, int* idx, float* wt, float* sg, float* logits, void* workspace,
                    size_t ws_bytes, void* stream) {
-  IFD_CHECK(T >= 0 && T <= 8, "the decode MoE takes T <= 8 tokens (T=%d): larger batches use ifd_moe_ffn", T);
+  IFD_CHECK(T >= 0 && T <= 16, "the decode MoE takes T <= 16 tokens (T=%d): larger batches use ifd_moe_ffn", T);
   IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
                 k <= 16 && k <= E,
             "bad decode MoE shape H=%d I=%d E=%d k=%d (H multiple of 512, I of 64, E <= 512, k <= 16)", H, I, E, k);
@@ -611,7 +611,31 @@ int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int 
             "tokens, router and weights must be 16-byte aligned");
   const WsView wv = ws_view(workspace, ws_bytes);
   MdecCall c{xn, router, T, H, E, k, I, norm ? 1 : 0, shared_gate ? 1 : 0, assign ? 1 : 0, egu_wq, egu_s, egu_b,
-             edn_wq, edn_s, edn_b, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, out, idx, wt, sg, logits};
+             edn_wq, edn_s, edn_b, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, out, idx, wt, sg, logits, nullptr};
+  return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
+}
+
+int ifd_moe_decode_logits(const float* logits_in, const void* xn, int T, int H, int E, int k, int norm,
+                          int shared_gate, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
+                          const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I,
+                          const uint32_t* sgu_wq, const uint16_t* sgu_s, const uint16_t* sgu_b,
+                          const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b, void* out, int assign,
+                          int* idx, float* wt, float* sg, void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(T >= 0 && T <= 16, "the decode MoE takes T <= 16 tokens (T=%d): larger batches use ifd_moe_ffn", T);
+  IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
+                k <= 16 && k <= E,
+            "bad decode MoE shape H=%d I=%d E=%d k=%d (H multiple of 512, I of 64, E <= 512, k <= 16)", H, I, E, k);
+  const bool shared = sgu_wq != nullptr;
+  IFD_CHECK(!shared || (sgu_s && sgu_b && sdn_wq && sdn_s && sdn_b), "bad shared expert");
+  IFD_CHECK(!shared_gate || shared, "a shared gate needs a shared expert");
+  if (T == 0) return IFD_OK;
+  IFD_CHECK(logits_in && xn && egu_wq && egu_s && egu_b && edn_wq && edn_s && edn_b && out, "null pointer");
+  IFD_CHECK(aligned(xn, 16) && aligned(logits_in, 4) && aligned(egu_wq, 16) && aligned(edn_wq, 16) &&
+                (!shared || (aligned(sgu_wq, 16) && aligned(sdn_wq, 16))),
+            "tokens and weights must be 16-byte aligned");
+  const WsView wv = ws_view(workspace, ws_bytes);
+  MdecCall c{xn, nullptr, T, H, E, k, I, norm ? 1 : 0, shared_gate ? 1 : 0, assign ? 1 : 0, egu_wq, egu_s, egu_b,
+             edn_wq, edn_s, edn_b, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, out, idx, wt, sg, nullptr, logits_in};
   return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
 }
 

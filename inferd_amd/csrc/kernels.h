@@ -120,7 +120,7 @@ int launch_moe_gather_qmm_t64(const uint16_t* A, int lda, const int* perm, int d
                               const int* ntiles, const int* offsets, int tile_rows, const void* wt, const void* wsh,
                               int E, int N, int K, int silu, uint16_t* C, int ldc, int rows, hipStream_t st);
 
-// Decode MoE for T <= 8 tokens (moe_dec.hip): router, routing + distinct-expert plan, gate/up + SwiGLU, down +
+// Decode MoE for T <= 16 tokens (moe_dec.hip): router, routing + distinct-expert plan, gate/up + SwiGLU, down +
 // combine; the combine's counters are H / 128 uint32 of the workspace header.
 struct MdecCall {
   const void* xn;
@@ -143,6 +143,7 @@ struct MdecCall {
   float* wt;
   float* sg;
   float* logits;
+  const float* logits_in;  // non-null: routing starts from these fp32 logits [T][E1] (router unused)
 };
 struct MdecLayout {
   size_t part, plan, act, d, idx, wt, sg, total;

@@ -1,13 +1,17 @@
-// Decode MoE for T <= 8 tokens in three launches, each distinct expert's weights read once for every token that
+// Decode MoE for T <= 16 tokens in three launches, each distinct expert's weights read once for every token that
 // picked it.
 //
 // Replaces the reference's four-launch decode MoE (engine/kernels/moe.metal:267-293 router, 326-368 moe_plan,
-// 370-488 moe_gu2, 490-551 moe_dn2; host engine/src/qwen35.h:1876-1908):
+// 370-488 moe_gu2, 490-551 moe_dn2; host engine/src/qwen35.h:1876-1908) up to 8 tokens, and its per-row expert GEMVs
+// for fewer than moe_sort_min = 128 routed rows beyond them (moe_qmv4 + moe_silu_mul + moe_qmv4 + moe_combine,
+// moe.metal:6-58, 103-111, 113-187; host qwen35.h:1801-1807, 1947-1955): the same qmv4 arithmetic per row, with each
+// distinct expert read once. Tokens are the MFMA's A rows: a lane holds rows 8 (r / 4) + 4 h + r % 4 of its RT
+// accumulators (RT = 4 up to 8 tokens, 8 up to 16).
 //  1. k_mdec_router: router logits (bf16 router [E1][H] x bf16 tokens) as K-split fp32 partials [KS][T][E1]. One
 //     32-expert tile x a K range per wave (32x32x16 bf16 MFMA, tokens in the A rows), the block's eight waves summed
 //     in wave order. The last block to finish (a counter in the workspace header) then routes: wave w sums token
 //     w's partials in split order and routes it (route_token, as k_moe_route); one thread per pick lists the
-//     distinct experts in pick order: plan = [nuniq, expert[T k], pick[T k][8]] (pick[u][t] = token t's pick index
+//     distinct experts in pick order: plan = [nuniq, expert[T k], pick[T k][16]] (pick[u][t] = token t's pick index
 //     of unique expert u, or -1).
 //  2. k_mdec_gu: one block per (32 gate/up column pairs, unique expert or the shared expert). Its four waves split K;
 //     each stages the token rows of its K range in LDS and streams the 32 gate and 32 up rows of its expert (16 B
@@ -29,7 +33,9 @@
 
 namespace ifd {
 
-constexpr int kMdecMaxT = 8, kMdecMaxK = 16, kMdecKG = 8;  // tokens, picks, groups per wave and chunk
+constexpr int kMdecMaxT = 16, kMdecMaxK = 16, kMdecKG = 8;  // tokens, picks, groups per wave and chunk
+// the MFMA output row (token) of accumulator r of a lane in half h
+__device__ __forceinline__ int mdec_row(int r, int h) { return 8 * (r / 4) + 4 * h + (r % 4); }
 constexpr int kMdecMaxKS = 4;                                 // K splits of the router
 
 struct MdecArgs {
@@ -54,7 +60,7 @@ struct MdecArgs {
   float* sg;
   float* logits;           // optional [T][E1]: the summed logits the routing used
   float* part;             // [KS][T][E1]
-  int* plan;               // [1 + T k + T k 8]
+  int* plan;               // [1 + T k + T k 16]
   uint16_t* act;           // [T][k + 1][I]
   uint16_t* d;             // [T][k + 1][H]
   uint32_t d_bytes;
@@ -75,11 +81,11 @@ __device__ __forceinline__ void load8h(const uint16_t* v, uint16_t (&o)[kMdecKG]
 // thread per pick numbers the distinct experts in pick order.
 template <int NTHR>
 __device__ __forceinline__ void mdec_plan_block(const MdecArgs& p) {
-  __shared__ int tidx[kMdecMaxT * kMdecMaxK], urank[kMdecMaxT * kMdecMaxK], firstpick[512], wcount[2];
+  __shared__ int tidx[kMdecMaxT * kMdecMaxK], urank[kMdecMaxT * kMdecMaxK], firstpick[512], wcount[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int T = p.T, k = p.k, NU = T * k;
   int* upick = p.plan + 1 + NU;
-  for (int i = tid; i < NU * 8; i += NTHR) upick[i] = -1;
+  for (int i = tid; i < NU * kMdecMaxT; i += NTHR) upick[i] = -1;
   for (int i = tid; i < p.E; i += NTHR) firstpick[i] = 0x7fffffff;
   const __amdgpu_buffer_rsrc_t rp = part_rsrc(p.part, (uint32_t)((size_t)p.KS * T * p.E1 * 4));
   for (int t = wave; t < T; t += NTHR / 64) {
@@ -126,31 +132,34 @@ __device__ __forceinline__ void mdec_plan_block(const MdecArgs& p) {
     }
   }
   __syncthreads();
-  // The distinct experts in pick order, one thread per pick q (q < T k <= 128, waves 0 and 1): its expert's first
-  // pick (an LDS atomic min), then that first pick's rank among the first picks (ballot counts): the unique slot u.
+  // The distinct experts in pick order, one thread per pick q (q < T k <= 256, waves 0-3): its expert's first pick
+  // (an LDS atomic min), then that first pick's rank among the first picks (ballot counts): the unique slot u.
+  static_assert(NTHR >= kMdecMaxT * kMdecMaxK, "one thread per pick");
   if (tid < NU) atomicMin(&firstpick[tidx[tid]], tid);
   __syncthreads();
   const int f = tid < NU ? firstpick[tidx[tid]] : 0;
   const bool first = tid < NU && f == tid;
   int rank = 0;
-  if (wave < 2) {
+  if (wave < 4) {
     const unsigned long long m = __ballot(first);
     if (lane == 0) wcount[wave] = __popcll(m);
     rank = __popcll(m & ((1ull << lane) - 1));
   }
   __syncthreads();
   if (first) {
-    const int u = rank + (wave == 1 ? wcount[0] : 0);
+    int u = rank;
+    for (int w = 0; w < wave; w++) u += wcount[w];
     urank[tid] = u;
     p.plan[1 + u] = tidx[tid];
   }
   __syncthreads();
-  if (tid < NU) upick[urank[f] * 8 + tid / k] = tid % k;
-  if (tid == 0) p.plan[0] = wcount[0] + wcount[1];
+  if (tid < NU) upick[urank[f] * kMdecMaxT + tid / k] = tid % k;
+  if (tid == 0) p.plan[0] = wcount[0] + wcount[1] + wcount[2] + wcount[3];
 }
 
+template <int RT>
 __global__ __launch_bounds__(512) void k_mdec_router(MdecArgs p) {
-  __shared__ float red[8][64][4];
+  __shared__ float red[8][64][RT];
   __shared__ unsigned s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
   const int e0 = blockIdx.x * 32, ks = blockIdx.y;
@@ -169,19 +178,19 @@ __global__ __launch_bounds__(512) void k_mdec_router(MdecArgs p) {
 #pragma unroll
     for (int t = 0; t < 4; t++) acc = mfma_bf16(a[t], b[t], acc);
   }
-  // D rows 4 h + r (r < 4) are tokens 0..7, column j is expert e0 + j; the waves' K ranges summed in wave order and
-  // written through for the block that routes
+  // D row mdec_row(r, h) (r < RT) is that token, column j is expert e0 + j; the waves' K ranges summed in wave
+  // order and written through for the block that routes
 #pragma unroll
-  for (int r = 0; r < 4; r++) red[wave][lane][r] = acc[r];
+  for (int r = 0; r < RT; r++) red[wave][lane][r] = acc[r];
   __syncthreads();
   if (wave == 0) {
     const __amdgpu_buffer_rsrc_t rp = part_rsrc(p.part, (uint32_t)((size_t)p.KS * p.T * p.E1 * 4));
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < RT; r++) {
       float v = red[0][lane][r];
 #pragma unroll
       for (int w = 1; w < 8; w++) v += red[w][lane][r];
-      const int t = 4 * h + r, e = e0 + j;
+      const int t = mdec_row(r, h), e = e0 + j;
       if (t < p.T && e < p.E1)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rp, (int)((((size_t)ks * p.T + t) * p.E1 + e) * 4),
                                               0, kSc1);
@@ -201,6 +210,9 @@ __global__ __launch_bounds__(512) void k_mdec_router(MdecArgs p) {
   if (s_last) mdec_plan_block<512>(p);
 }
 
+// Routing and the plan from logits the caller computed (p.part = those logits, one split)
+__global__ __launch_bounds__(512) void k_mdec_plan(MdecArgs p) { mdec_plan_block<512>(p); }
+
 // The slot of block row u: a distinct routed expert (u < nuniq), the shared expert (u == T k), or nothing.
 struct MdecSlot {
   int e;       // expert, or -1 for the shared expert
@@ -215,11 +227,11 @@ __device__ __forceinline__ MdecSlot mdec_slot(const MdecArgs& p, int u) {
 __device__ __forceinline__ int mdec_pick(const MdecArgs& p, int u, int t) {
   const int NU = p.T * p.k;
   if (t >= p.T) return -1;
-  return u == NU ? p.k : p.plan[1 + NU + u * 8 + t];
+  return u == NU ? p.k : p.plan[1 + NU + u * kMdecMaxT + t];
 }
 
 // Stage rows [T][ng * 64] (row t from src(t), null = zeros) into LDS As (row stride lda) and their 64-group sums into
-// Xs[g][t] (8 per group). nthr threads starting at thread `first`; every 8 consecutive chunks are one group, so the
+// Xs[g][t] (kMdecMaxT per group). nthr threads starting at thread `first`; every 8 consecutive chunks are one group, so the
 // group sum is a reduction over 8 consecutive lanes.
 template <class Src>
 __device__ __forceinline__ void mdec_stage(Src src, int T, int ng, uint16_t* As, int lda, float* Xs, int first,
@@ -240,14 +252,14 @@ __device__ __forceinline__ void mdec_stage(Src src, int T, int ng, uint16_t* As,
     sum += __shfl_xor(sum, 4, 64);
     if (ok) {
       *(u32x4*)(As + (size_t)t * lda + 8 * kc) = v;
-      if ((kc & 7) == 0) Xs[(kc >> 3) * 8 + t] = sum;
+      if ((kc & 7) == 0) Xs[(kc >> 3) * kMdecMaxT + t] = sum;
     }
   }
 }
 
 // One wave's share of a qmv4-arithmetic product: 32 weight rows (wrow: the lane's row, offset 4 h words) over ng
 // groups starting at group g0 of the row, against the staged token rows As (row j of the MFMA A operand = token j,
-// zero past T). Adds s P + (b - 128 s) X of each group into acc[r] (rows 4 h + r, r < 4).
+// zero past T). Adds s P + (b - 128 s) X of each group into acc[r] (rows mdec_row(r, h), r < RT).
 struct MdecW {
   const uint32_t* w;  // row words + 4 h
   const uint16_t* s;  // row scales
@@ -255,12 +267,22 @@ struct MdecW {
 };
 
 // ---- 3. gate/up + SwiGLU -------------------------------------------------------------------------------------------
+// LDS of k_mdec_gu for T tokens: per wave its staged rows [T][kMdecKG * 64 + 8] and group sums [kMdecKG][kMdecMaxT]
+// (then the waves' sums [4][64][2 RT])
+constexpr int kMdecGuRow = kMdecKG * 64 + 8;
+__host__ __device__ constexpr size_t mdec_gu_lds(int T, int RT) {
+  return (size_t)4 * T * kMdecGuRow * 2 + (size_t)4 * kMdecKG * kMdecMaxT * 4 + (size_t)4 * 64 * 2 * RT * 4;
+}
+
+template <int RT>
 __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
-  __shared__ __align__(16) uint16_t As[4][kMdecMaxT][kMdecKG * 64 + 8];
-  __shared__ float Xs[4][kMdecKG * 8];
-  __shared__ float red[4][64][8];
+  extern __shared__ __align__(16) uint8_t glds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
   const int u = blockIdx.y, T = p.T, I = p.I, H = p.H, G = H / kGroup, Gw = G / 4;
+  uint16_t* const As = (uint16_t*)glds + (size_t)wave * T * kMdecGuRow;
+  float* const Xs = (float*)(glds + (size_t)4 * T * kMdecGuRow * 2) + wave * kMdecKG * kMdecMaxT;
+  float* const red = (float*)(glds + (size_t)4 * T * kMdecGuRow * 2 + (size_t)4 * kMdecKG * kMdecMaxT * 4);
+  auto RED = [&](int w, int l, int r) -> float& { return red[((size_t)w * 64 + l) * 2 * RT + r]; };
   const MdecSlot sl = mdec_slot(p, u);
   if (!sl.live) return;  // block-uniform, before any barrier
   const int n0 = blockIdx.x * 32;
@@ -273,7 +295,9 @@ __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
   const MdecW Wu{wq + ru * (H / 8) + 4 * h, ws + ru * G, wb + ru * G};
   const bool aok = j < T;
 
-  float ag[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f};
+  float ag[RT], au[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) ag[r] = au[r] = 0.f;
   for (int c0 = 0; c0 < Gw; c0 += kMdecKG) {
     const int gb = wave * Gw + c0, ng = min(kMdecKG, Gw - c0);
     // every load of the chunk first (clamped re-reads past ng keep the count fixed), then the token rows
@@ -295,8 +319,8 @@ __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
       }
     }
     if (c0 > 0) __syncthreads();  // the previous chunk's reads of As are done (every wave runs the same chunks)
-    mdec_stage([&](int t) { return p.x + (size_t)t * H + (size_t)gb * 64; }, T, ng, &As[wave][0][0],
-               kMdecKG * 64 + 8, Xs[wave], wave * 64, 64);
+    mdec_stage([&](int t) { return p.x + (size_t)t * H + (size_t)gb * 64; }, T, ng, As, kMdecGuRow, Xs, wave * 64,
+               64);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kMdecKG; i++) {
@@ -304,37 +328,39 @@ __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
       f32x16 Pg = zero16(), Pu = zero16();
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        const u32x4 af = aok ? *(const u32x4*)(&As[wave][j][64 * i + GroupCodes<4>::kofs(t, h)]) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 af = aok ? *(const u32x4*)(As + (size_t)j * kMdecGuRow + 64 * i + GroupCodes<4>::kofs(t, h))
+                             : u32x4{0u, 0u, 0u, 0u};
         Pg = mfma_bf16(af, codes_bf16_off128(cg[i][t]), Pg);
         Pu = mfma_bf16(af, codes_bf16_off128(cu[i][t]), Pu);
       }
       const float sgf = bf2f(sgr[i]), bgf = __builtin_fmaf(-128.f, sgf, bf2f(bgr[i]));
       const float suf = bf2f(sur[i]), buf = __builtin_fmaf(-128.f, suf, bf2f(bur[i]));
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float X = Xs[wave][i * 8 + 4 * h + r];
+      for (int r = 0; r < RT; r++) {
+        const float X = Xs[i * kMdecMaxT + mdec_row(r, h)];
         ag[r] = __builtin_fmaf(sgf, Pg[r], __builtin_fmaf(bgf, X, ag[r]));
         au[r] = __builtin_fmaf(suf, Pu[r], __builtin_fmaf(buf, X, au[r]));
       }
     }
   }
 #pragma unroll
-  for (int r = 0; r < 4; r++) red[wave][lane][r] = ag[r], red[wave][lane][4 + r] = au[r];
+  for (int r = 0; r < RT; r++) RED(wave, lane, r) = ag[r], RED(wave, lane, RT + r) = au[r];
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int t = 4 * h + r, pk = mdec_pick(p, u, t);
+  for (int r = 0; r < RT; r++) {
+    const int t = mdec_row(r, h), pk = mdec_pick(p, u, t);
     if (pk < 0) continue;
-    const float g = red[0][lane][r] + red[1][lane][r] + red[2][lane][r] + red[3][lane][r];
-    const float v = red[0][lane][4 + r] + red[1][lane][4 + r] + red[2][lane][4 + r] + red[3][lane][4 + r];
+    const float g = RED(0, lane, r) + RED(1, lane, r) + RED(2, lane, r) + RED(3, lane, r);
+    const float v = RED(0, lane, RT + r) + RED(1, lane, RT + r) + RED(2, lane, RT + r) + RED(3, lane, RT + r);
     p.act[((size_t)t * (p.k + 1) + pk) * I + n0 + j] = f2bf(swiglu_f(bf2f(f2bf(g)), bf2f(f2bf(v))));
   }
 }
 
 // ---- 4. down + combine ---------------------------------------------------------------------------------------------
+template <int RT>
 __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
-  extern __shared__ __align__(16) uint16_t lds[];  // As [T][I + 8], then Xs [I / 64][8]
+  extern __shared__ __align__(16) uint16_t lds[];  // As [T][I + 8], then Xs [I / 64][kMdecMaxT]
   __shared__ unsigned s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
   const int u = blockIdx.y, T = p.T, I = p.I, H = p.H, Gi = I / kGroup, k = p.k;
@@ -350,7 +376,9 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   const uint16_t* wb = (sl.e < 0 ? p.sdn_b : p.edn_b) + row * Gi;
   const bool aok = j < T;
 
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float acc[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) acc[r] = 0.f;
   for (int c0 = 0; c0 < Gi; c0 += kMdecKG) {
     const int ng = min(kMdecKG, Gi - c0);
     u32x4 cw[kMdecKG];
@@ -391,14 +419,15 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
       }
       const float sf = bf2f(sr[i]), bf = __builtin_fmaf(-128.f, sf, bf2f(br[i]));
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(sf, P[r], __builtin_fmaf(bf, Xs[g * 8 + 4 * h + r], acc[r]));
+      for (int r = 0; r < RT; r++)
+        acc[r] = __builtin_fmaf(sf, P[r], __builtin_fmaf(bf, Xs[g * kMdecMaxT + mdec_row(r, h)], acc[r]));
     }
   }
   // d[t][pick][h] = bf16(result), written through for the combining block
   const __amdgpu_buffer_rsrc_t rd = part_rsrc(p.d, p.d_bytes);
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int t = 4 * h + r, pk = mdec_pick(p, u, t);
+  for (int r = 0; r < RT; r++) {
+    const int t = mdec_row(r, h), pk = mdec_pick(p, u, t);
     if (pk >= 0)
       __builtin_amdgcn_raw_buffer_store_b16(f2bf(acc[r]), rd, (int)((((size_t)t * (k + 1) + pk) * H + h0 + j) * 2), 0,
                                             kSc1);
@@ -452,7 +481,7 @@ MdecLayout mdec_layout(int T, int H, int I, int E, int k) {
   };
   const int E1 = E + 1, KS = mdec_ks(H);
   take(L.part, (size_t)KS * T * E1 * 4);
-  take(L.plan, (size_t)(1 + 9 * T * k) * 4);
+  take(L.plan, (size_t)(1 + (1 + kMdecMaxT) * T * k) * 4);
   take(L.act, (size_t)T * (k + 1) * I * 2);
   take(L.d, (size_t)T * (k + 1) * H * 2);
   take(L.idx, (size_t)T * k * 4);
@@ -461,8 +490,35 @@ MdecLayout mdec_layout(int T, int H, int I, int E, int k) {
   return L;
 }
 
+template <int RT>
+static int launch_mdec(const MdecArgs& p, const MdecCall& c, hipStream_t st) {
+  const int slots = c.T * c.k + 1;
+  if (c.logits_in) hipLaunchKernelGGL(k_mdec_plan, dim3(1), dim3(512), 0, st, p);
+  else hipLaunchKernelGGL(k_mdec_router<RT>, dim3((p.E1 + 31) / 32, p.KS), dim3(512), 0, st, p);
+  IFD_TRY(check_launch("moe_decode router"));
+  // up to 16 tokens the staged rows can take more than the default 64 KB of dynamic LDS
+  auto allow_lds = [](const void* k, size_t bytes, const char* what) -> int {
+    if (bytes <= 64 * 1024) return IFD_OK;
+    if (bytes > 150 * 1024) return fail(IFD_ERR_UNSUPPORTED, "moe_decode %s: %zu bytes of LDS", what, bytes);
+    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(IFD_ERR_LAUNCH, "moe_decode %s: %zu bytes of LDS refused", what, bytes);
+    }
+    return IFD_OK;
+  };
+  const size_t glds = mdec_gu_lds(c.T, RT);
+  IFD_TRY(allow_lds((const void*)k_mdec_gu<RT>, glds, "gate_up"));
+  hipLaunchKernelGGL(k_mdec_gu<RT>, dim3(c.I / 32, slots), dim3(256), glds, st, p);
+  IFD_TRY(check_launch("moe_decode gate_up"));
+  const size_t lds = ((size_t)c.T * (c.I + 8) + 8) * 2 + (size_t)(c.I / kGroup) * kMdecMaxT * 4;
+  IFD_TRY(allow_lds((const void*)k_mdec_dn<RT>, lds, "down"));
+  hipLaunchKernelGGL(k_mdec_dn<RT>, dim3(c.H / 128, slots), dim3(256), lds, st, p);
+  return check_launch("moe_decode down");
+}
+
 int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
   if (c.T == 0) return IFD_OK;
+  if (c.T > kMdecMaxT) return fail(IFD_ERR_UNSUPPORTED, "moe_decode takes at most %d tokens", kMdecMaxT);
   const MdecLayout L = mdec_layout(c.T, c.H, c.I, c.E, c.k);
   if (!ws || ws_bytes < L.total || !cnt)
     return fail(IFD_ERR_WORKSPACE, "moe_decode needs %zu bytes of workspace after the header, got %zu", L.total,
@@ -482,7 +538,8 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
   p.wt = c.wt ? c.wt : (float*)(w + L.wt);
   p.sg = c.sg ? c.sg : (float*)(w + L.sg);
   p.logits = c.logits;
-  p.part = (float*)(w + L.part);
+  p.part = c.logits_in ? (float*)c.logits_in : (float*)(w + L.part);
+  if (c.logits_in) p.KS = 1;
   p.plan = (int*)(w + L.plan);
   p.act = (uint16_t*)(w + L.act);
   p.d = (uint16_t*)(w + L.d);
@@ -496,14 +553,8 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
               (!shared || (aligned(c.sgu_s, 16) && aligned(c.sgu_b, 16)));
   p.sb16_dn = Gi % 8 == 0 && aligned(c.edn_s, 16) && aligned(c.edn_b, 16) &&
               (!shared || (aligned(c.sdn_s, 16) && aligned(c.sdn_b, 16)));
-  const int slots = c.T * c.k + 1;
-  hipLaunchKernelGGL(k_mdec_router, dim3((p.E1 + 31) / 32, p.KS), dim3(512), 0, st, p);
-  IFD_TRY(check_launch("moe_decode router"));
-  hipLaunchKernelGGL(k_mdec_gu, dim3(c.I / 32, slots), dim3(256), 0, st, p);
-  IFD_TRY(check_launch("moe_decode gate_up"));
-  const size_t lds = ((size_t)c.T * (c.I + 8) + 8) * 2 + (size_t)(c.I / kGroup) * 8 * 4;
-  hipLaunchKernelGGL(k_mdec_dn, dim3(c.H / 128, slots), dim3(256), lds, st, p);
-  return check_launch("moe_decode down");
+  if (c.T <= 8) return launch_mdec<4>(p, c, st);
+  return launch_mdec<8>(p, c, st);
 }
 
 }  // namespace ifd

@@ -116,10 +116,14 @@ def test_new_entry_points_reject_bad_arguments():
     assert L.ifd_a8_quant(4098, 128, 4, 128, 0, 4096, 4096, None) == E and b"aligned" in L.ifd_last_error()
     assert L.ifd_a8_quant(4096, 132, 4, 128, 0, 4096, 4096, None) == E and b"lda=132" in L.ifd_last_error()
     assert L.ifd_a8_quant(4096, 128, 4, 128, 0, 4100, 4096, None) == E and b"aligned" in L.ifd_last_error()
-    # decode MoE: at most 8 tokens, H a multiple of 512, k <= 16, no shared gate without a shared expert
-    args = [4096, 9, 2048, 4096, 512, 10, 1, 0, 4096, 4096, 4096, 4096, 4096, 4096, 512,
+    # decode MoE: at most 16 tokens, H a multiple of 512, k <= 16, no shared gate without a shared expert
+    args = [4096, 17, 2048, 4096, 512, 10, 1, 0, 4096, 4096, 4096, 4096, 4096, 4096, 512,
             None, None, None, None, None, None, 4096, 0, None, None, None, None, None, 0, None]
-    assert L.ifd_moe_decode(*args) == E and b"T <= 8" in L.ifd_last_error()
+    assert L.ifd_moe_decode(*args) == E and b"T <= 16" in L.ifd_last_error()
+    # the same checks from caller logits
+    assert L.ifd_moe_decode_logits(4096, 4096, 17, 2048, 512, 10, 1, 0, 4096, 4096, 4096, 4096, 4096, 4096, 512,
+                                   None, None, None, None, None, None, 4096, 0, None, None, None, None, 0,
+                                   None) == E and b"T <= 16" in L.ifd_last_error()
     a = list(args); a[1], a[2] = 4, 1280
     assert L.ifd_moe_decode(*a) == E and b"H multiple of 512" in L.ifd_last_error()
     a = list(args); a[1], a[5] = 4, 17
@@ -137,7 +141,7 @@ def test_new_entry_points_reject_bad_arguments():
 
 def test_new_workspace_queries():
     L = _lib.lib()
-    assert L.ifd_moe_decode_workspace(9, 2048, 512, 512, 10) == 0
+    assert L.ifd_moe_decode_workspace(17, 2048, 512, 512, 10) == 0 and L.ifd_moe_decode_workspace(16, 2048, 512, 512, 10) > 0
     w1, w8 = L.ifd_moe_decode_workspace(1, 2048, 512, 512, 10), L.ifd_moe_decode_workspace(8, 2048, 512, 512, 10)
     assert HEADER_BYTES < w1 < w8
     assert L.ifd_mlp_decode_workspace(1, 5120, 17408) > HEADER_BYTES + 5120 * 2 + 17408 * 2

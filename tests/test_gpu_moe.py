@@ -237,10 +237,59 @@ def _decode_case(T, E, H, I, k, shared, shared_gate, seed, assign=True):
     return ri
 
 
-@pytest.mark.parametrize("T", [1, 2, 5, 8])
+@pytest.mark.parametrize("T", [1, 2, 5, 8, 9, 10, 11, 12, 16])
 def test_moe_decode_baseline_geometry(T):
-    """BASELINE config 4's layer (H=2048, E=512, top-10, I=512, shared expert with its gate) at decode batch sizes."""
+    """BASELINE config 4's layer (H=2048, E=512, top-10, I=512, shared expert with its gate) at decode batch sizes,
+    and beyond 8 tokens while T k < 128 (the reference's per-row expert GEMVs, moe_qmv4, at 90..120 routed rows), up to
+    the kernel's 16."""
     _decode_case(T, 512, 2048, 512, 10, True, True, seed=120 + T)
+
+
+def test_moe_decode_rows_independent_of_batch():
+    """A token's result is the same bits whatever the other tokens of the call: 12 tokens (16-row accumulators) against
+    each token alone (8-row accumulators), as the reference's per-row arithmetic gives."""
+    g, ops = _gu(), _ops()
+    E, H, I, k, seed = 64, 1024, 256, 6, 170
+    egu, edn = experts(E, 2 * I, H, seed=seed), experts(E, H, I, seed=seed + 1)
+    sgu, sdn = experts(1, 2 * I, H, seed=seed + 2), experts(1, H, I, seed=seed + 3)
+    R = router(E + 1, H, seed=seed + 4)
+    xn = gen.activations(12, H, seed=seed + 5)
+    sh = (g.qlinear(sgu[0][0], sgu[1][0], sgu[2][0]), g.qlinear(sdn[0][0], sdn[1][0], sdn[2][0]))
+    E_gu, E_dn = g.moew(*egu), g.moew(*edn)
+    allr = g.host(ops.moe_decode(g.dev(xn), g.dev(R), E_gu, E_dn, k, shared=sh)[0])
+    for t in (0, 5, 11):
+        one = g.host(ops.moe_decode(g.dev(np.ascontiguousarray(xn[t:t + 1])), g.dev(R), E_gu, E_dn, k, shared=sh)[0])
+        assert np.array_equal(one[0], allr[t]), t
+
+
+@pytest.mark.parametrize("T", [1, 5, 12])
+def test_moe_decode_router8(T):
+    """The reference's 8-bit router (moe_router8: per group s sum q x + b sum x, fp32 logits, the shared gate as the
+    last row) through gemm_w8 mode 2, then the decode MoE from those logits (ifd_moe_decode_logits): logits against the
+    oracle's qmv8, routing bit-exact on the GPU's logits, the block against the oracle's composition."""
+    g, ops = _gu(), _ops()
+    E, H, I, k, seed = 128, 2048, 256, 8, 180 + T
+    egu, edn = experts(E, 2 * I, H, seed=seed), experts(E, H, I, seed=seed + 1)
+    sgu, sdn = experts(1, 2 * I, H, seed=seed + 2), experts(1, H, I, seed=seed + 3)
+    _, rq, rs_, rb = gen.qlinear8(E + 1, H, seed=seed + 4)
+    xn = gen.activations(T, H, seed=seed + 5)
+    x0 = gen.activations(T, H, seed=seed + 6)
+    Wr = g.qlinear(rq, rs_, rb, bits=8)
+    lg_d = ops.gemm(g.dev(xn), Wr, mode=2)
+    torch.cuda.synchronize()
+    lg = g.host(lg_d)
+    gen.check_f32(lg, orc.qmv(xn, rq, rs_, rb, bits=8), 1e-5, "router8 logits")
+    sh = (g.qlinear(sgu[0][0], sgu[1][0], sgu[2][0]), g.qlinear(sdn[0][0], sdn[1][0], sdn[2][0]))
+    out, idx, wt, sg, _ = ops.moe_decode(g.dev(xn), None, g.moew(*egu), g.moew(*edn), k, shared=sh, out=g.dev(x0),
+                                         assign=False, logits_in=lg_d)
+    torch.cuda.synchronize()
+    ri, rw, rsg = orc.moe_route(lg, E, k, shared_gate=True)
+    assert np.array_equal(g.host(idx), ri)
+    assert np.allclose(g.host(wt), rw, rtol=1e-5, atol=1e-7)
+    assert np.allclose(g.host(sg), rsg, rtol=1e-5)
+    shw = ((sgu[0][0], sgu[1][0], sgu[2][0]), (sdn[0][0], sdn[1][0], sdn[2][0]))
+    ref = orc.moe_decode(xn, ri, rw, rsg, egu, edn, shw, I, out=x0, assign=False)
+    gen.check_bf16(g.host(out), ref, 1e-2, ("router8", T), ref_is_bf16=True, composition=True)
 
 
 @pytest.mark.parametrize("assign", [True, False])
