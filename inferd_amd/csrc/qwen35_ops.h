@@ -13,6 +13,12 @@
 //  - QLinear may carry `t64`, the MI355X weight layout made once at load by ifd_pack_t64 (the role of the
 //    reference's lane4 copy `lp` / `lsb`). When present (and K % 256 == 0) gemm() runs on it.
 //  - The split-K reduce is never deferred: `defer` is accepted and has no effect.
+//  - bf16 weights (bits 16) are outside this path: gemm() reports it and exits, as for any route it lacks.
+// The W4A8 route and its fused producers follow the reference: flipped 4- and 8-bit weights for qmv_max < M <
+// w4a8_max take the int8 GEMM (w4a8_route, qwen35.h:1576; w4a8, :1323-1365), and rmsnorm_for / silu_mul_for write the next
+// GEMM's int8 rows when it takes that route (a8_ready, :1560-1561, 1982-2001, 2874-2876). encode_moe routes an 8-bit
+// router as the reference does (moe_router8 for the decode launches, the per-row qmv8 logits otherwise,
+// :1878-1882, 1930-1941).
 // Errors keep the reference's behaviour: a message on stderr and exit(1) (qwen35.h:1469, 1477), here for every
 // status the C ABI returns.
 #pragma once
@@ -121,6 +127,11 @@ struct Config {
   int router_gemm_min = 0;   // T at or above which router logits are rounded to bf16 (0 = never)
 };
 
+inline int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+
 // The model-owned state the two operators use: hidden state x [T][H] (encode_moe adds the block's output into it),
 // its normalised copy xn, routing outputs and every scratch buffer, allocated once for up to max_rows tokens
 // (the reference allocates them with the model, qwen35.h:394-407, 520-600).
@@ -135,21 +146,50 @@ struct Qwen35 {
   BufRef eact, edown_out;     // routed experts: bf16 [R][I], [R][H]
   BufRef splitk;              // gemm()'s split-K partials and the dispatch workspace
   size_t splitk_bytes = 0;
+  BufRef a8u, a8x;            // int8 rows [max_rows][a8_k] and their (sx, sx sum xq) per 64-group, fp32
+  int a8_k = 0;
+
+  // Routing thresholds of the reference (qwen35.h:1049, 1055, 1575; the same environment variables): up to
+  // qmv_max rows the decode GEMV, W4A8 for flipped 4-bit weights below w4a8_max rows; fuse_a8 0 off, 1 silu_mul_a8,
+  // 3 also rmsnorm_a8; moe_sort_min: routed rows from which the MoE sorts by expert (fewer: per-row expert
+  // products, qwen35.h:1830).
+  int qmv_max = env_int("QMV_MAX", 2), w4a8_max = env_int("W4A8_MAX", 256);
+  bool use_w4a8 = env_int("W4A8", 1) != 0;
+  int fuse_a8 = env_int("FUSE_A8", 3), moe_sort_min = env_int("MOE_SORT_MIN", 128);
+  // The next GEMM's int8 activations are already in a8u / a8x (written by rmsnorm_for or silu_mul_for).
+  bool a8_ready = false;
+  // flipped 4-bit (W4A8) or 8-bit (W8A8: the same kernel with 8-bit codes, qwen35.h:1352) weights
+  bool w4a8_route(const QLinear& W, int M) const {
+    return use_w4a8 && (W.bits == 4 || W.bits == 8) && W.flipped && !W.ldk && M > qmv_max && M < w4a8_max &&
+           W.K % 64 == 0;
+  }
 
   // shared_inter: the shared expert's intermediate size (0: none). gemm_scratch: bytes for gemm() calls made outside
-  // encode_moe (the largest ifd_gemm_w4_workspace / ifd_gemm_t64_workspace of the model's shapes).
-  Qwen35(const Config& c, int max_rows_, int shared_inter, size_t gemm_scratch) : cfg(c), max_rows(max_rows_) {
+  // encode_moe (the largest workspace query of the model's shapes over every row count). a8_k: the longest K of a
+  // W4A8 GEMM (0: the hidden size or shared_inter, whichever is larger).
+  Qwen35(const Config& c, int max_rows_, int shared_inter, size_t gemm_scratch, int a8_k_ = 0)
+      : cfg(c), max_rows(max_rows_) {
     const int H = c.hidden, E = c.experts, k = c.topk, I = c.moe_inter, R = max_rows * k;
+    a8_k = a8_k_ > 0 ? a8_k_ : std::max(H, shared_inter);
     size_t need = gemm_scratch;
     if (max_rows > 0 && E > 0) {
       need = std::max(need, ifd_moe_dispatch_workspace(R, E));
-      need = std::max(need, ifd_moe_decode_workspace(std::min(max_rows, 8), H, I, E, k));
-      if (shared_inter > 0) {
-        need = std::max(need, ifd_gemm_w4_workspace(max_rows, 2 * shared_inter, H));
-        need = std::max(need, ifd_gemm_w4_workspace(max_rows, H, shared_inter));
-        need = std::max(need, ifd_gemm_t64_workspace(max_rows, 2 * shared_inter, H));
-        need = std::max(need, ifd_gemm_t64_swiglu_workspace(max_rows, 2 * shared_inter, H));
-        need = std::max(need, ifd_gemm_t64_workspace(max_rows, H, shared_inter));
+      need = std::max(need, ifd_moe_decode_workspace(std::min(max_rows, 16), H, I, E, k));
+      // a workspace size is not monotone in the row count (each route sizes its own), so take every T a call may
+      // pass: 1 .. max_rows
+      for (int T = 1; T <= max_rows; T++) {
+        need = std::max(need, ifd_moe_dispatch_workspace(T * k, E));
+        if (T <= 16) need = std::max(need, ifd_moe_decode_workspace(T, H, I, E, k));
+        need = std::max(need, ifd_gemm_w8_workspace(T, E + 1, H));  // an 8-bit router's logits
+        if (shared_inter > 0) {
+          need = std::max(need, ifd_gemm_w4_workspace(T, 2 * shared_inter, H));
+          need = std::max(need, ifd_gemm_w4_workspace(T, H, shared_inter));
+          need = std::max(need, ifd_gemm_t64_workspace(T, 2 * shared_inter, H));
+          need = std::max(need, ifd_gemm_t64_swiglu_workspace(T, 2 * shared_inter, H));
+          need = std::max(need, ifd_gemm_t64_workspace(T, H, shared_inter));
+          need = std::max(need, ifd_qmm_w4a8_workspace(T, 2 * shared_inter, H));
+          need = std::max(need, ifd_qmm_w4a8_workspace(T, H, shared_inter));
+        }
       }
       x = alloc((size_t)max_rows * H * 2);
       xn = alloc((size_t)max_rows * H * 2);
@@ -170,6 +210,10 @@ struct Qwen35 {
       eact = alloc((size_t)R * I * 2);
       edown_out = alloc((size_t)R * H * 2);
     }
+    if (max_rows > 0 && a8_k > 0) {
+      a8u = alloc((size_t)max_rows * a8_k);
+      a8x = alloc((size_t)max_rows * (a8_k / 64) * 2 * 4);
+    }
     if (need) {
       splitk = alloc(need);
       hip_ok(hipMemset(splitk.buf, 0, need), "Qwen35");  // the workspace's leading counters start at zero
@@ -178,7 +222,8 @@ struct Qwen35 {
   }
   ~Qwen35() {
     for (void* p : {x.buf, xn.buf, rlog.buf, ridx.buf, rw.buf, rsg.buf, proj.buf, act.buf, sh_out.buf, moffs.buf,
-                    mperm.buf, minv.buf, mtiles.buf, mntiles.buf, eact.buf, edown_out.buf, splitk.buf})
+                    mperm.buf, minv.buf, mtiles.buf, mntiles.buf, eact.buf, edown_out.buf, splitk.buf, a8u.buf,
+                    a8x.buf})
       if (p) (void)hipFree(p);
   }
   Qwen35(const Qwen35&) = delete;
@@ -187,7 +232,7 @@ struct Qwen35 {
   // H [M][N/2] = SwiGLU of A . W^T for a [gate | up] linear: one fused call on T64 weights, else the reference's
   // gemm into proj + silu_mul (qwen35.h:1910-1912).
   void gemm_swiglu(Enc& e, const BufRef& A, const QLinear& W, const BufRef& H, int M) {
-    if (W.bits == 4 && W.t64 && W.K % 256 == 0 && W.N % 16 == 0) {
+    if (W.bits == 4 && W.t64 && W.K % 256 == 0 && W.N % 16 == 0 && !w4a8_route(W, M) && !a8_ready) {
       const size_t need = ifd_gemm_t64_swiglu_workspace(M, W.N, W.K);
       if (need > splitk_bytes) die("gemm_swiglu", "split-K scratch smaller than this shape needs");
       ok(ifd_gemm_t64_swiglu(A.ptr<void>(), W.K, W.t64.ptr<void>(), W.N, W.K, H.ptr<void>(), W.N / 2, M,
@@ -203,6 +248,12 @@ struct Qwen35 {
   // K), C [M][N] (row stride N).
   void gemm(Enc& e, const BufRef& A, const QLinear& W, const BufRef& C, int M, int mode, bool defer = false) {
     (void)defer;
+    if (W.ldk && a8_ready) die("gemm", "K-slice view off the qmm path");  // qwen35.h:1469
+    if (w4a8_route(W, M)) {
+      w4a8(e, A, W, C, M, mode);
+      return;
+    }
+    if (a8_ready) die("gemm", "a8_ready with a non-W4A8 GEMM");  // qwen35.h:1477
     if (W.bits == 8) {  // the reference's qmv8 / 8-bit qmm routes (qwen35.h:1520-1558)
       const size_t need = ifd_gemm_w8_workspace(M, W.N, W.K);
       if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
@@ -232,31 +283,120 @@ struct Qwen35 {
        "gemm");
   }
 
+  // The reference's W4A8 GEMM (qwen35.h:1323-1365): per-group int8 activations (a8_quant, unless a fused producer
+  // wrote them) times the flipped 4- or 8-bit codes on the integer path.
+  void w4a8(Enc& e, const BufRef& A, const QLinear& W, const BufRef& C, int M, int mode) {
+    if (M > max_rows || W.K > a8_k) die("gemm", "W4A8 rows past the int8 staging buffers (max_rows, a8_k)");
+    if (!a8_ready)
+      ok(ifd_a8_quant(A.ptr<void>(), W.K, M, W.K, 0, a8u.ptr<int8_t>(), a8x.ptr<float>(), e.stream), "gemm");
+    a8_ready = false;
+    const bool w8 = W.bits == 8;
+    const size_t need = w8 ? ifd_qmm_w8a8_workspace(M, W.N, W.K) : ifd_qmm_w4a8_workspace(M, W.N, W.K);
+    if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
+    ok((w8 ? ifd_qmm_w8a8 : ifd_qmm_w4a8)(a8u.ptr<int8_t>(), a8x.ptr<float>(), 0, W.wq.ptr<uint32_t>(),
+                                          W.s.ptr<uint16_t>(), W.b.ptr<uint16_t>(), W.N, W.K, 0,
+                                          w8 ? 0x80808080u : 0x88888888u, C.ptr<void>(), W.N, M, mode,
+                                          splitk.ptr<void>(), splitk_bytes, e.stream),
+       "gemm");
+  }
+
+  // rmsnorm of rows [rows][D] into out, fused with the W4A8 activation quantization when `next` (the GEMM that reads
+  // out) takes that route (reference rmsnorm_for, qwen35.h:1982-2001).
+  void rmsnorm_for(Enc& e, const BufRef& in, const BufRef& w, const BufRef& out, int rows, int D, const QLinear& next) {
+    if (fuse_a8 < 3 || !w4a8_route(next, rows) || D % 64 || D > a8_k || rows > max_rows) {
+      ok(ifd_rmsnorm(in.ptr<void>(), D, w.ptr<void>(), out.ptr<void>(), D, rows, D, cfg.eps, e.stream), "rmsnorm_for");
+      return;
+    }
+    ok(ifd_rmsnorm_a8(in.ptr<void>(), D, w.ptr<void>(), out.ptr<void>(), D, rows, D, cfg.eps, 0, a8u.ptr<int8_t>(),
+                      a8x.ptr<float>(), e.stream),
+       "rmsnorm_for");
+    a8_ready = true;
+  }
+
+  // h = silu_mul(gu) for the MLP's down projection `down` (gu [rows][2 I] -> act [rows][I]); when down takes the
+  // W4A8 route, its int8 rows instead (act is not written; reference qwen35.h:2868-2878).
+  void silu_mul_for(Enc& e, const BufRef& gu, const BufRef& act, int I, int rows, const QLinear& down) {
+    if (fuse_a8 && w4a8_route(down, rows) && I % 64 == 0 && I <= a8_k && rows <= max_rows) {
+      ok(ifd_silu_mul_a8(gu.ptr<void>(), I, rows, 0, a8u.ptr<int8_t>(), a8x.ptr<float>(), e.stream), "silu_mul_for");
+      a8_ready = true;
+      return;
+    }
+    ok(ifd_silu_mul(gu.ptr<void>(), act.ptr<void>(), I, rows, e.stream), "silu_mul_for");
+  }
+
+  // The MoE route encode_moe takes for T tokens: the decode launches (the reference's moe2 up to 8 tokens,
+  // qwen35.h:1823-1829, and its per-row expert products below moe_sort_min routed rows, :1947-1955: the same per-row
+  // arithmetic), else rows sorted by expert.
+  bool moe_decode_route(const Layer& ly, int T) const {
+    const int H = cfg.hidden, E = cfg.experts, k = cfg.topk, I = cfg.moe_inter;
+    const int E1 = ly.router.E * ly.router.N;
+    const bool has_shared = ly.gate_up.N > 0;
+    const bool shared_fits = !has_shared || (ly.gate_up.bits == 4 && ly.down.bits == 4 && ly.gate_up.N == 2 * I &&
+                                             ly.gate_up.K == H && ly.down.N == H && ly.down.K == I &&
+                                             !ly.gate_up.flipped && !ly.down.flipped && !ly.gate_up.ldk &&
+                                             !ly.down.ldk);
+    return (T <= 8 || (T <= 16 && T * k < moe_sort_min)) && k <= 16 && E <= 512 && H % 512 == 0 && I % 64 == 0 &&
+           E1 <= E + 1 && shared_fits;
+  }
+
   // The MoE block on the hidden state x [T][H]: xn = rmsnorm(x, post_norm); shared expert; router; top-k softmax
   // routing; dispatch by expert; gathered gate/up with SwiGLU; gathered down; x = bf16(x + bf16(weighted sum +
   // sg * shared)) (reference sorted path, qwen35.h:1909-1980).
   void encode_moe(Enc& e, const Layer& ly, int T) {
     const int H = cfg.hidden, E = cfg.experts, k = cfg.topk, I = cfg.moe_inter, R = T * k;
     if (T > max_rows) die("encode_moe", "more rows than the state was allocated for");
-    if (ly.router.bits != 16) die("encode_moe", "the router must be bf16 (bits 16)");
+    if (ly.router.bits != 16 && !(ly.router.bits == 8 && ly.router.E == 1))
+      die("encode_moe", "the router must be bf16 (bits 16) or one 8-bit matrix (bits 8)");
     if (ly.egu.bits != 4 || ly.edown.bits != 4) die("encode_moe", "routed experts must be 4-bit affine");
     if (ly.router.K != H || ly.router.E * ly.router.N < E || ly.egu.E != E || ly.egu.N != 2 * I || ly.egu.K != H ||
         ly.edown.E != E || ly.edown.N != H || ly.edown.K != I)
       die("encode_moe", "layer shapes do not match the config");
     if (T == 0) return;
     const int E1 = ly.router.E * ly.router.N;  // E, or E + 1 with the shared expert's gate row
-    ok(ifd_rmsnorm(x.ptr<void>(), H, ly.post_norm.ptr<void>(), xn.ptr<void>(), H, T, H, cfg.eps, e.stream),
-       "encode_moe");
-    // up to 8 tokens: the decode MoE (the reference's moe2 route, qwen35.h:1823-1829, 1876-1908), each distinct expert
-    // read once; it needs the shared expert (if any) unflipped 4-bit with the routed experts' intermediate size
     const bool has_shared = ly.gate_up.N > 0;
-    const bool shared_fits = !has_shared || (ly.gate_up.bits == 4 && ly.down.bits == 4 && ly.gate_up.N == 2 * I &&
-                                             ly.gate_up.K == H && ly.down.N == H && ly.down.K == I &&
-                                             !ly.gate_up.flipped && !ly.down.flipped && !ly.gate_up.ldk &&
-                                             !ly.down.ldk);
-    if (T <= 8 && k <= 16 && E <= 512 && H % 512 == 0 && I % 64 == 0 && E1 <= E + 1 && shared_fits) {
+    if (has_shared) rmsnorm_for(e, x, ly.post_norm, xn, T, H, ly.gate_up);
+    else ok(ifd_rmsnorm(x.ptr<void>(), H, ly.post_norm.ptr<void>(), xn.ptr<void>(), H, T, H, cfg.eps, e.stream), "encode_moe");
+    // An 8-bit router's logits (fp32, per group s sum q x + b sum x: the reference's moe_router8 / moe_qmv8f; bf16
+    // from router_gemm_min rows, as its quantized GEMM rounds them) come from the 8-bit GEMM.
+    const bool r8 = ly.router.bits == 8;
+    const int lbf = cfg.router_gemm_min > 0 && T >= cfg.router_gemm_min;
+    // fp32 logits keep the per-row qmv8 arithmetic for every T: the 8-bit GEMM computes it up to 32 rows, so the
+    // rows go 32 at a time (each row's logits are the same whatever the chunk)
+    auto router8_logits = [&](int bf16_out) {
+      const int step = bf16_out ? T : 32;
+      for (int r0 = 0; r0 < T; r0 += step) {
+        const int rows = std::min(step, T - r0);
+        const size_t need = ifd_gemm_w8_workspace(rows, E1, H);
+        if (need > splitk_bytes) die("encode_moe", "scratch smaller than the 8-bit router needs");
+        ok(ifd_gemm_w8(xn.at((size_t)r0 * H * 2).ptr<void>(), H, ly.router.wq.ptr<uint32_t>(),
+                       ly.router.s.ptr<uint16_t>(), ly.router.b.ptr<uint16_t>(), E1, H, 0, 0u,
+                       rlog.at((size_t)r0 * E1 * (bf16_out ? 2 : 4)).ptr<void>(), E1, rows, bf16_out ? 0 : 2,
+                       splitk.ptr<void>(), splitk_bytes, e.stream),
+           "encode_moe");
+      }
+    };
+    // the decode MoE (the reference's moe2 route up to 8 tokens, and its per-row expert products below moe_sort_min
+    // routed rows), each distinct expert read once; it needs the shared expert (if any) unflipped 4-bit with the
+    // routed experts' intermediate size
+    if (moe_decode_route(ly, T)) {
+      a8_ready = false;  // the norm's int8 rows (if it made them) are not the next GEMM's input (qwen35.h:1906)
       const size_t need = ifd_moe_decode_workspace(T, H, I, E, k);
       if (need > splitk_bytes) die("encode_moe", "scratch smaller than the decode MoE needs");
+      if (r8) {
+        router8_logits(0);
+        ok(ifd_moe_decode_logits(rlog.ptr<float>(), xn.ptr<void>(), T, H, E, k, 1, E1 > E ? 1 : 0,
+                                 ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(), ly.egu.b.ptr<uint16_t>(),
+                                 ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(), ly.edown.b.ptr<uint16_t>(), I,
+                                 has_shared ? ly.gate_up.wq.ptr<uint32_t>() : nullptr,
+                                 has_shared ? ly.gate_up.s.ptr<uint16_t>() : nullptr,
+                                 has_shared ? ly.gate_up.b.ptr<uint16_t>() : nullptr,
+                                 has_shared ? ly.down.wq.ptr<uint32_t>() : nullptr,
+                                 has_shared ? ly.down.s.ptr<uint16_t>() : nullptr,
+                                 has_shared ? ly.down.b.ptr<uint16_t>() : nullptr, x.ptr<void>(), 0, ridx.ptr<int>(),
+                                 rw.ptr<float>(), rsg.ptr<float>(), splitk.ptr<void>(), splitk_bytes, e.stream),
+           "encode_moe");
+        return;
+      }
       ok(ifd_moe_decode(xn.ptr<void>(), T, H, ly.router.wq.ptr<void>(), E, k, 1, E1 > E ? 1 : 0,
                         ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(), ly.egu.b.ptr<uint16_t>(),
                         ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(), ly.edown.b.ptr<uint16_t>(), I,
@@ -271,16 +411,20 @@ struct Qwen35 {
          "encode_moe");
       return;
     }
-    // shared expert -> sh_out
-    const bool shared = ly.gate_up.N > 0;
+    // shared expert -> sh_out (its gate/up may read the norm's int8 rows; the SwiGLU feeds the down GEMM in bf16,
+    // qwen35.h:1910-1914)
+    const bool shared = has_shared;
     if (shared) {
       gemm_swiglu(e, xn, ly.gate_up, act, T);
+      a8_ready = false;
       gemm(e, act, ly.down, sh_out, T, 0);
     }
+    a8_ready = false;
     // router
-    const int lbf = cfg.router_gemm_min > 0 && T >= cfg.router_gemm_min;
-    ok(ifd_moe_router_logits(xn.ptr<void>(), ly.router.wq.ptr<void>(), T, H, E1, lbf, rlog.ptr<void>(), e.stream),
-       "encode_moe");
+    if (r8) router8_logits(lbf);
+    else
+      ok(ifd_moe_router_logits(xn.ptr<void>(), ly.router.wq.ptr<void>(), T, H, E1, lbf, rlog.ptr<void>(), e.stream),
+         "encode_moe");
     ok(ifd_moe_route(rlog.ptr<void>(), lbf, T, E, k, E1, 1, E1 > E ? 1 : 0, ridx.ptr<int>(), rw.ptr<float>(),
                      rsg.ptr<float>(), e.stream),
        "encode_moe");

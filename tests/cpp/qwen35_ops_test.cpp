@@ -36,6 +36,10 @@ void orc_qmv(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, 
 void orc_qmm(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
              uint32_t xr, float* Y, int M, int nthreads);
 void orc_store(const float* Y, void* C, int ldc, int M, int N, int mode);
+void orc_a8_quant(const uint16_t* A, int lda, int M, int K, int per_token, int8_t* U, float* XS);
+void orc_wxa8(const int8_t* U, const float* XS, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
+              int bits, uint32_t xr, float* Y, int M, int nthreads);
+void orc_silu_mul(const uint16_t* gu, uint16_t* h, int I, int rows);
 void orc_rmsnorm(const uint16_t* x, int in_stride, const uint16_t* w, uint16_t* out, int out_stride, int rows, int D,
                  float eps);
 void orc_moe_route(const void* logits, int logits_bf16, int T, int E, int k, int stride, int norm, int shared_gate,
@@ -174,6 +178,16 @@ std::vector<uint16_t> activations(int M, int K, std::mt19937& rng) {
   return a;
 }
 
+// fp32 y of the reference's W4A8 / W8A8 route: per-group int8 activations (a8_quant) times the (unflipped) codes
+std::vector<float> ref_wxa8(const std::vector<uint16_t>& A, int M, int K, const uint32_t* wq, const uint16_t* s,
+                            const uint16_t* b, int N, int bits) {
+  std::vector<int8_t> U((size_t)M * K);
+  std::vector<float> XS((size_t)M * (K / 64) * 2), y((size_t)M * N);
+  orc_a8_quant(A.data(), K, M, K, 0, U.data(), XS.data());
+  orc_wxa8(U.data(), XS.data(), wq, s, b, N, K, bits, 0, y.data(), M, 0);
+  return y;
+}
+
 // fp32 y (before the store) of the GEMM semantics the routed kernel implements
 std::vector<float> ref_gemm(const std::vector<uint16_t>& A, const HostLinear& h, int M, bool qmv_semantics) {
   std::vector<float> y((size_t)M * h.N);
@@ -215,19 +229,65 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
     report(e2 <= 1e-3, "gemm mode 2 (fp32)", e2);
     (void)hipFree(dA.buf), (void)hipFree(dC.buf), (void)hipFree(dF.buf);
   }
-  // flipped in place: the same products
+  // flipped in place: the decode GEMV up to qmv_max rows, the W4A8 route (int8 activations) from there to w4a8_max
   {
     HostLinear hf = h;
     orc_flip(hf.wq.data(), (int64_t)hf.wq.size(), 0x88888888u);
     QLinear Wf = device_linear(hf);
     Wf.flipped = true;
-    const int M = 5;
-    const auto A = activations(M, K, rng);
-    BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
-    m.gemm(e, dA, Wf, dC, M, 0);
-    const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), ref_gemm(A, h, M, true), false);
-    report(err <= 1e-2, "gemm flipped weights", err);
-    (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+    for (int M : {2, 5, 40}) {
+      const auto A = activations(M, K, rng);
+      BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
+      m.gemm(e, dA, Wf, dC, M, 0);
+      const bool a8 = m.w4a8_route(Wf, M);
+      const auto y = a8 ? ref_wxa8(A, M, K, h.wq.data(), h.s.data(), h.b.data(), N, 4) : ref_gemm(A, h, M, true);
+      const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), y, false);
+      report(err <= 1e-2 && a8 == (M > 2), std::string("gemm flipped weights M=") + std::to_string(M) +
+                                               (a8 ? " (W4A8 route)" : ""), err);
+      (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+    }
+    // the fused producers: rmsnorm_for / silu_mul_for write the next GEMM's int8 rows (a8_ready), bit-identical to
+    // the plain producer followed by the GEMM's own quantizer (FUSE_A8 = 0)
+    const int M = 40, I = K / 2;
+    std::uniform_real_distribution<float> pw(0.5f, 2.f);
+    std::vector<uint16_t> nw((size_t)K);
+    for (auto& v : nw) v = f2bf(pw(rng));
+    const auto x = activations(M, K, rng), gu = activations(M, 2 * I, rng);
+    HostLinear hd = make_linear(N, I, rng), hdf = hd;
+    orc_flip(hdf.wq.data(), (int64_t)hdf.wq.size(), 0x88888888u);
+    QLinear Wd = device_linear(hdf);
+    Wd.flipped = true;
+    BufRef dx = upload(x), dw = upload(nw), dxn = upload(std::vector<uint16_t>((size_t)M * K));
+    BufRef dgu = upload(gu), dact = upload(std::vector<uint16_t>((size_t)M * I));
+    std::vector<uint16_t> outs[2][2];
+    for (int fuse : {3, 0}) {
+      m.fuse_a8 = fuse;
+      BufRef c1 = upload(std::vector<uint16_t>((size_t)M * N)), c2 = upload(std::vector<uint16_t>((size_t)M * N));
+      m.rmsnorm_for(e, dx, dw, dxn, M, K, Wf);
+      const bool r1 = m.a8_ready;
+      m.gemm(e, dxn, Wf, c1, M, 0);
+      m.silu_mul_for(e, dgu, dact, I, M, Wd);
+      const bool r2 = m.a8_ready;
+      m.gemm(e, dact, Wd, c2, M, 0);
+      report(r1 == (fuse >= 3) && r2 == (fuse >= 1) && !m.a8_ready,
+             "fused producers set a8_ready (FUSE_A8=" + std::to_string(fuse) + ")", 0);
+      outs[fuse ? 0 : 1][0] = download<uint16_t>(c1, (size_t)M * N);
+      outs[fuse ? 0 : 1][1] = download<uint16_t>(c2, (size_t)M * N);
+      (void)hipFree(c1.buf), (void)hipFree(c2.buf);
+    }
+    m.fuse_a8 = 3;
+    report(outs[0][0] == outs[1][0], "rmsnorm_for -> gemm (int8 rows fused) == rmsnorm -> gemm, bit for bit", 0);
+    report(outs[0][1] == outs[1][1], "silu_mul_for -> gemm (int8 rows fused) == silu_mul -> gemm, bit for bit", 0);
+    std::vector<uint16_t> xr((size_t)M * K), hr((size_t)M * I);
+    orc_rmsnorm(x.data(), K, nw.data(), xr.data(), K, M, K, m.cfg.eps);
+    orc_silu_mul(gu.data(), hr.data(), I, M);
+    double e1 = bf16_err(outs[0][0], ref_wxa8(xr, M, K, h.wq.data(), h.s.data(), h.b.data(), N, 4), false);
+    report(e1 <= 1e-2, "rmsnorm_for -> gemm (W4A8) vs the oracle", e1);
+    e1 = bf16_err(outs[0][1], ref_wxa8(hr, M, I, hd.wq.data(), hd.s.data(), hd.b.data(), N, 4), false);
+    report(e1 <= 1e-2, "silu_mul_for -> gemm (W4A8) vs the oracle", e1);
+    for (void* p : {dx.buf, dw.buf, dxn.buf, dgu.buf, dact.buf, Wd.wq.buf, Wd.s.buf, Wd.b.buf, Wf.wq.buf, Wf.s.buf,
+                    Wf.b.buf})
+      (void)hipFree(p);
   }
   // T64 copy: decode GEMV semantics up to 64 rows, prefill semantics above
   {
@@ -300,11 +360,16 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
       for (int M : {1, 33, 200}) {
         const auto A = activations(M, K, rng);
         std::vector<float> y((size_t)M * N);
-        (M <= 32 ? orc_qmv_b : orc_qmm_b)(A.data(), K, wq8.data(), s8.data(), b8.data(), N, K, 8, 0, y.data(), M, 0);
+        const bool a8 = m.w4a8_route(W8, M);  // flipped 8-bit weights below w4a8_max rows: W8A8
+        if (a8) y = ref_wxa8(A, M, K, wq8.data(), s8.data(), b8.data(), N, 8);
+        else (M <= 32 ? orc_qmv_b : orc_qmm_b)(A.data(), K, wq8.data(), s8.data(), b8.data(), N, K, 8, 0, y.data(), M, 0);
         BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
         m.gemm(e, dA, W8, dC, M, 0);
         const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), y, false);
-        report(err <= 1e-2, std::string("gemm 8-bit") + (flipped ? " flipped" : "") + " M=" + std::to_string(M), err);
+        report(err <= 1e-2 && a8 == (flipped && M > 2),
+               std::string("gemm 8-bit") + (flipped ? " flipped" : "") + " M=" + std::to_string(M) +
+                   (a8 ? " (W8A8 route)" : ""),
+               err);
         if (M == 1) {  // rows_of [128, 256) of the same layer
           QLinear Wr = rows_of(W8, 128, 128);
           BufRef dR = upload(std::vector<uint16_t>(128));
@@ -350,10 +415,37 @@ void test_encode_moe(std::mt19937& rng) {
                   0, 0, 1, sgu_t64, nullptr),
      "pack_t64");
   const QLinear sgu_mlx = ly.gate_up;
-  for (int T : {3, 8, 16, 100, -16, -100}) {
+  // an 8-bit router [E + 1, H] (the shared gate last), w = s q + b with b = -128 s
+  std::vector<uint32_t> r8wq((size_t)(E + 1) * H / 4);
+  std::vector<uint16_t> r8s((size_t)(E + 1) * H / 64), r8b(r8s.size());
+  {
+    std::vector<uint8_t> codes((size_t)(E + 1) * H);
+    std::uniform_int_distribution<int> q(0, 255);
+    for (auto& v : codes) v = (uint8_t)q(rng);
+    orc_pack_w8(codes.data(), r8wq.data(), E + 1, H);
+    std::uniform_real_distribution<float> su(0.0001f, 0.0003f);
+    for (size_t i = 0; i < r8s.size(); i++) r8s[i] = f2bf(su(rng)), r8b[i] = f2bf(-128.f * bf2f(r8s[i]));
+  }
+  const MoeW router16 = ly.router;
+  MoeW router8;
+  router8.wq = upload(r8wq), router8.s = upload(r8s), router8.b = upload(r8b);
+  router8.E = 1, router8.N = E + 1, router8.K = H, router8.bits = 8;
+  struct Case {
+    int T, max_rows;
+    bool t64, r8;
+  };
+  // the decode route up to 8 tokens and below 128 routed rows (T = 16 at top-4), the sorted route beyond; the
+  // fused T64 shared gate/up; state allocated for more rows than the call (its scratch covers every row count); the
+  // 8-bit router on both routes
+  for (const Case cs : {Case{3, 3, false, false}, Case{8, 8, false, false}, Case{16, 16, false, false},
+                        Case{100, 100, false, false}, Case{16, 16, true, false}, Case{100, 100, true, false},
+                        Case{100, 256, true, false}, Case{3, 3, false, true}, Case{12, 12, false, true},
+                        Case{40, 40, false, true}}) {
+    const int T = cs.T;
     ly.gate_up = sgu_mlx;
-    if (T < 0) ly.gate_up.t64 = BufRef(sgu_t64), T = -T;
-    Qwen35 m(c, T, Is, 0);
+    if (cs.t64) ly.gate_up.t64 = BufRef(sgu_t64);
+    ly.router = cs.r8 ? router8 : router16;
+    Qwen35 m(c, cs.max_rows, Is, 0);
     Enc e;
     const auto x0 = activations(T, H, rng);
     hip_ok(hipMemcpy(m.x.ptr<void>(), x0.data(), x0.size() * 2, hipMemcpyHostToDevice), "x");
@@ -364,7 +456,18 @@ void test_encode_moe(std::mt19937& rng) {
     const auto idx = download<int>(m.ridx, (size_t)T * k);
     const auto wt = download<float>(m.rw, (size_t)T * k);
     const auto sg = download<float>(m.rsg, (size_t)T);
-    const std::string tag = " T=" + std::to_string(T) + (ly.gate_up.t64 ? " (T64 shared gate/up)" : "");
+    const bool dec = m.moe_decode_route(ly, T);
+    const std::string tag = " T=" + std::to_string(T) + (cs.max_rows > T ? " of " + std::to_string(cs.max_rows) : "") +
+                            (ly.gate_up.t64 ? " (T64 shared gate/up)" : "") + (cs.r8 ? " (8-bit router)" : "") +
+                            (dec ? " [decode]" : " [sorted]");
+    if (cs.r8) {  // the logits against the oracle's qmv8 on the GPU's normalised rows
+      std::vector<float> yl((size_t)T * (E + 1));
+      orc_qmv_b(xn.data(), H, r8wq.data(), r8s.data(), r8b.data(), E + 1, H, 8, 0, yl.data(), T, 0);
+      double ss = 0, w = 0;
+      for (size_t i = 0; i < yl.size(); i++) ss += (double)yl[i] * yl[i], w = std::max(w, (double)std::fabs(yl[i] - logits[i]));
+      const double el = w / std::sqrt(ss / yl.size());
+      report(el <= 1e-5, "encode_moe 8-bit router logits (fp32)" + tag, el);
+    }
     // rmsnorm: within one bf16 step of the oracle
     std::vector<uint16_t> xr((size_t)T * H);
     orc_rmsnorm(x0.data(), H, post.data(), xr.data(), H, T, H, c.eps);
@@ -382,7 +485,7 @@ void test_encode_moe(std::mt19937& rng) {
     report(ri == idx && ew <= 1e-5, "encode_moe routing (indices bit-exact)" + tag, ew);
     // the block's output added into x, from the GPU's normalised rows and routing
     std::vector<uint16_t> want = x0;
-    if (T <= 8)  // the decode MoE route: the decode GEMV arithmetic for every expert product
+    if (dec)  // the decode MoE route: the decode GEMV arithmetic for every expert product
       orc_moe_decode(xn.data(), T, H, I, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
                      egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu.wq.data(), sgu.s.data(),
                      sgu.b.data(), sdn.wq.data(), sdn.s.data(), sdn.b.data(), want.data(), 0);
@@ -399,6 +502,7 @@ void test_encode_moe(std::mt19937& rng) {
            "encode_moe x += moe(xn) (end to end)" + tag, g_raw);
   }
   (void)hipFree(sgu_t64);
+  (void)hipFree(router8.wq.buf), (void)hipFree(router8.s.buf), (void)hipFree(router8.b.buf);
 }
 
 template <class T>
@@ -467,7 +571,7 @@ int main(int argc, char** argv) {
   }
   {
     Config c;
-    Qwen35 m(c, 0, 0, 64 << 20);
+    Qwen35 m(c, 256, 0, 64 << 20, 1024);  // int8 staging for the W4A8 route: up to 256 rows of K <= 1024
     Enc e;
     test_gemm(m, e, rng);
   }
