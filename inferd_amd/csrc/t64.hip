@@ -268,14 +268,18 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   }
 }
 
-// Split plan: about 6 waves per SIMD (the stream is latency-bound: more waves, more bytes in flight), whole kTB-group
-// blocks of at least two per split, at most kMaxS splits, <= ~40 KB of staged activations per block.
+// Split plan: enough waves for the bytes in flight (the stream is latency-bound): about 6 per SIMD for weights past
+// 64 MB, 2 below, where each split's fixed costs (its activation staging, partial store and the last block's reads)
+// outweigh the extra waves (measured: K = N = 5120, 10.2 -> 9.5 us; the 50 MB down, 15.5 -> 14.7 us; the 100 MB
+// gate_up is fastest at 6); whole kTB-group blocks of at least two per split, at most kMaxS splits, <= ~40 KB of
+// staged activations per block.
 struct TPlan {
   int S, gps;
 };
 static TPlan qmv_t_plan(int M, int N, int K) {
   const int G = K / kGroup, waves = 4 * ((t64_bands(N) + 3) / 4);
-  long S = (6144 + waves - 1) / waves;
+  const long target = (long)N * K / 2 <= (64l << 20) ? 2048 : 6144;
+  long S = (target + waves - 1) / waves;
   S = std::max<long>(S, ((long)M * K * 2 + 40959) / 40960);
   S = std::min<long>(S, std::max(1, G / (2 * kTB)));
   S = std::min<long>(S, kMaxS);
