@@ -20,27 +20,4 @@ __device__ __forceinline__ void wait_vm_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// The wait for a pipeline stage that has k younger stages of STEP DMAs each behind it (k wave-uniform, at most KMAX):
-// vmcnt(STEP * KMAX) in the steady state (k = KMAX), vmcnt(0) in the last steps of a stream, when fewer are in
-// flight. One compare: a chain of exact waits for every k costs the scalar unit several instructions per level on
-// every step, even when its first branch is taken. Other outstanding operations younger than the awaited DMA (output
-// stores) only make either wait longer: operations of a wave complete in issue order.
-template <int STEP, int KMAX>
-__device__ __forceinline__ void wait_vm_dyn(int k) {
-  static_assert(STEP * KMAX <= 63, "vmcnt range");
-  if (k >= KMAX) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(STEP * KMAX) : "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
-
-// The same with OFF more operations (output stores) younger than the awaited DMA for each of the nrec recent item
-// ends (0, 1 or 2) inside its window: flat compares, no chain per level.
-template <int STEP, int KMAX, int OFF>
-__device__ __forceinline__ void wait_vm_rec(int k, int nrec) {
-  static_assert(STEP * KMAX + 2 * OFF <= 63, "vmcnt range");
-  if (k < KMAX) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if (nrec == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(STEP * KMAX) : "memory");
-  else if (nrec == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(STEP * KMAX + OFF) : "memory");
-  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(STEP * KMAX + 2 * OFF) : "memory");
-}
-
 }  // namespace ifd

@@ -13,14 +13,14 @@
 // tiles. Two LDS rings filled by direct global -> LDS DMA: NA activation slabs [BM][64 bf16] (16-byte columns
 // XOR-swizzled by row pair), whose rows are gathered through perm by the DMA itself (row q of a tile is token
 // perm[q] / div, or row q of A), and NW weight stages (the item's code halves and (s, b) rows of one group). Waves
-// 0-3 issue the activation DMAs, waves 4-7 the weight DMAs, each with its own in-order vmcnt stream. Row indices
-// come from scalar loads, which do not count in vmcnt. Weights are dequantized to bf16(s q + b) (MLX's gather_qmm
-// rounding) one step ahead of their MFMAs; the k order of a lane's MFMA steps is that of k_gqmm, so the sums are
-// bit-identical to it.
+// 0-3 issue the activation DMAs, waves 4-7 the weight DMAs, each as buffer loads whose per-lane offsets are set once
+// per item and whose group offset is one scalar register, so a step issues no address arithmetic; each role's code
+// is compiled on its own, so every wait is a constant. Row indices come from scalar loads, which do not count in
+// vmcnt. Weights are dequantized to bf16(s q + b) (MLX's gather_qmm rounding) one step ahead of their MFMAs; the k
+// order of a lane's MFMA steps is that of k_gqmm, so the sums are bit-identical to it.
 //
 // At the end of an item a wave stages its bf16 outputs in its own LDS tile and writes them as 16-byte buffer
-// stores, rows past the segment at an out-of-range offset (dropped by the buffer bounds check, yet issued, so each
-// wave's count of outstanding stores is exact). The vmcnt waits count those stores among the younger operations.
+// stores, rows past the segment at an out-of-range offset (dropped by the buffer bounds check).
 #include <algorithm>
 
 #include "common.h"
@@ -37,6 +37,7 @@ constexpr int kGqThreads = 512;
 struct GqArgs {
   const uint16_t* A;
   int lda;
+  uint32_t a_bytes;  // bytes of A that a sorted row may read (buffer bound)
   const int* perm;  // null: sorted row q reads row q of A
   uint32_t div_m;   // perm[q] / div = mulhi(perm[q], div_m) (div_m = ceil(2^32 / div)); 0 when div = 1
   const int* tiles;    // [ntiles][2] = (expert, first sorted row)
@@ -67,39 +68,48 @@ __device__ __forceinline__ int sload(const int* p, int i) {
   return *((const __attribute__((address_space(4))) int*)p + __builtin_amdgcn_readfirstlane(i));
 }
 
-// WIDE (plain only): each wave owns two bands, 8 apart, so an item is 16 bands (512 columns)
-template <int MT, bool SILU, bool WIDE>
-__global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
+// One wave-wide 16-byte-per-lane DMA through a buffer resource: lane l's 16 bytes at voff(l) + soff land at
+// lds + 16 l (LDS base in M0, wave-uniform control flow only). Out-of-range lanes write zeros.
+__device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, (int)voff, (int)soff, 0, 0);
+}
+
+// The pipeline of one wave role. ROLE 0: waves 0-3, the activation DMAs (MT per step); ROLE 1 / 2: waves 4-7, the
+// weight DMAs (NCW code tiles per step, ROLE 1 also one (s, b) DMA). Each role's DMA stream has a fixed shape, so
+// every wait is a compile-time count of the DMAs younger than the one awaited:
+// - ROLE 0 needs A(i + 1) at step i (its fragments are read a step ahead), issued NA - 2 steps earlier: the
+//   MT (NA - 3) DMAs of the steps between are younger.
+// - ROLE 1 / 2 need W(i + 2) at step i (its codes are read two steps ahead), issued NW - 3 steps earlier:
+//   D (NW - 4) younger DMAs.
+// DMA loads retire from vmcnt in issue order. The output stores of an item end are not counted: a store may retire
+// before an older load, so counting it could release a wait early, while an uncounted store still in flight only
+// makes the wait longer. The streams run on past the last step (re-reading the last item) so that the steady counts
+// hold to the end; the kernel drains vmcnt before it exits.
+template <int MT, bool SILU, bool WIDE, int ROLE>
+__device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int wave, const int it0, const int it1) {
   constexpr bool TWO = SILU || WIDE;
-  constexpr int BM = 32 * MT, NBW = gq_nbw(TWO), NA = gq_na(MT, TWO), NW = gq_nw(MT, TWO);
+  constexpr int NBW = gq_nbw(TWO), NA = gq_na(MT, TWO), NW = gq_nw(MT, TWO);
   constexpr int A_BYTES = gq_abytes(MT), W_BYTES = gq_wbytes(TWO);
   constexpr int SB_OFF = NBW * 8 * kT64Codes;  // (s, b) rows of a weight stage, after its code tiles
   constexpr int NCW = TWO ? 4 : 2;             // code DMAs per weight wave per step
-  static_assert(!(SILU && WIDE), "SwiGLU pairs a gate and an up band per wave");
-  static_assert(gq_lds(MT, TWO) <= 160 * 1024, "LDS plan");
-  static_assert(MT * (NA - 2) + 8 * MT <= 63 && (NCW + 1) * (NW - 2) + 8 * MT <= 63, "vmcnt range");
-  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr bool AW = ROLE == 0;
+  constexpr int D = AW ? MT : NCW + (ROLE == 1 ? 1 : 0);  // DMAs per step
+  constexpr int NR = AW ? NA : NW;                          // the ring this role fills
+  constexpr int LAG = AW ? NA - 1 : NW - 1;                 // steps the issue runs ahead
+  constexpr int BASE = AW ? D * (NA - 3) : D * (NW - 4);  // younger than A(i + 1) / W(i + 2) at step i
+  static_assert(NA >= 3 && NW >= 4 && D * (AW ? NA - 2 : NW - 3) <= 63, "ring depth, vmcnt range");
   uint8_t* const aring = lds;
   uint8_t* const wring = lds + NA * A_BYTES;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 31, h = lane >> 5;
   uint16_t* const stg = (uint16_t*)(wring + NW * W_BYTES + wave * kGqStg);
-
-  const int b = xcd_remap(blockIdx.x, p.nblk);
-  const int nitems = sload(p.ntiles, 0) << p.nct_log2;
-  const int it0 = (int)((long)b * nitems / p.nblk), it1 = (int)((long)(b + 1) * nitems / p.nblk);
-  if (it0 >= it1) return;  // block-uniform, before any barrier
-  const int G = p.G, n = (it1 - it0) * G;
+  const int G = p.G;
   const int nbands = t64_bands(p.N);
-  const size_t gstride = (size_t)nbands * kT64Tile;
+  const uint32_t gstride = (uint32_t)nbands * kT64Tile;
   const int up0 = nbands / 2;  // first up band of a [gate | up] stack
-
-  // weight DMA roles of waves 4-7 (ww = wave - 4): SwiGLU, code tiles [4 ww, 4 ww + 4) of the stage's 16 (8 gate +
-  // 8 up bands) and the (s, b) DMA ww for ww < 2; plain, code tiles [2 ww, 2 ww + 2) of 8 and the (s, b) DMA for
-  // ww = 3
+  // weight roles: SwiGLU / wide, code tiles [4 ww, 4 ww + 4) of the stage's 16 and the (s, b) DMA ww for ww < 2;
+  // plain, code tiles [2 ww, 2 ww + 2) of 8 and the (s, b) DMA for ww = 3
   const int ww = wave - 4;
-  const bool has_sb = TWO ? ww < 2 : ww == 3;
   const int sbj = TWO ? ww : 0;
 
   // (expert, column tile, rows) of an item; a tile holds at least its first row
@@ -108,96 +118,123 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
     c = item & ((1 << p.nct_log2) - 1);
     e = min(max(sload(p.tiles, 2 * tile), 0), p.E);
     q0 = sload(p.tiles, 2 * tile + 1);
-    q1 = max(min(sload(p.offsets, e + 1), q0 + BM), q0 + 1);
+    q1 = max(min(sload(p.offsets, e + 1), q0 + 32 * MT), q0 + 1);
   };
   auto band_of = [&](int c, int ti) __attribute__((always_inline)) {  // physical band of the stage's tile ti
     const int bb = SILU ? (ti < 8 ? 8 * c + ti : up0 + 8 * c + ti - 8) : (WIDE ? 16 * c + ti : 8 * c + ti);
     return min(bb, nbands - 1);
   };
 
-  // ---- DMA streams: (item, group) of the next step to issue
-  int s_item = it0, s_g = 0, s_i = 0, s_st = 0;
-  const uint16_t* arow[MT];
-  const uint8_t* wsrc[NCW + 1];  // the code sources, then the (s, b) source
+  // ---- this role's DMA stream: (item, group) of the next issue; per-lane offsets of the item, group offset soff
+  // the source base of the stream (A, or the item's expert), as two wave-uniform halves: the buffer resource built
+  // from them stays in SGPRs
+  uint32_t base_lo = (uint32_t)(uintptr_t)p.A, base_hi = (uint32_t)((uintptr_t)p.A >> 32);
+  const uint32_t nrec = AW ? p.a_bytes : (uint32_t)p.ebytes;
+  uint32_t voff[D];
+  const uint32_t gstep = AW ? 2u * kGroup : gstride;
+  int s_item = it0, s_g = 0, s_st = 0;
+  uint32_t soff = 0;
   auto stream_item = [&](int item) __attribute__((always_inline)) {
     int e, c, q0, q1;
     item_rows(item, e, c, q0, q1);
-    if (wave < 4) {
-      // the wave's 8 MT row indices: all scalar loads in flight at once, then one wait
-      int v[MT][8];
-#pragma unroll
-      for (int i = 0; i < MT; i++)
-#pragma unroll
-        for (int rho = 0; rho < 8; rho++) v[i][rho] = min(q0 + 8 * (MT * wave + i) + rho, q1 - 1);
+    if constexpr (AW) {
+      const uint32_t rowb = 2u * (uint32_t)p.lda;
       if (p.perm) {
+        // the wave's 8 MT row indices: all scalar loads in flight at once, then one wait
+        int v[MT][8];
 #pragma unroll
         for (int i = 0; i < MT; i++)
 #pragma unroll
-          for (int rho = 0; rho < 8; rho++) v[i][rho] = sload(p.perm, v[i][rho]);
+          for (int rho = 0; rho < 8; rho++) v[i][rho] = sload(p.perm, min(q0 + 8 * (MT * wave + i) + rho, q1 - 1));
         if (p.div_m)
 #pragma unroll
           for (int i = 0; i < MT; i++)
 #pragma unroll
             for (int rho = 0; rho < 8; rho++)
               v[i][rho] = (int)__builtin_amdgcn_readfirstlane(__umulhi((uint32_t)v[i][rho], p.div_m));
-      }
 #pragma unroll
-      for (int i = 0; i < MT; i++) {
-        const int r0 = 8 * (MT * wave + i);
-        int src = 0;
+        for (int i = 0; i < MT; i++) {
+          int src = 0;
 #pragma unroll
-        for (int rho = 0; rho < 8; rho++) src = (lane >> 3) == rho ? v[i][rho] : src;
-        const int r = r0 + (lane >> 3);
-        const int c16 = (lane & 7) ^ ((r >> 1) & 7);
-        arow[i] = p.A + (size_t)src * p.lda + 8 * c16;
+          for (int rho = 0; rho < 8; rho++) src = (lane >> 3) == rho ? v[i][rho] : src;
+          const int r = 8 * (MT * wave + i) + (lane >> 3);
+          voff[i] = (uint32_t)src * rowb + 16u * (uint32_t)((lane & 7) ^ ((r >> 1) & 7));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+          const int r = 8 * (MT * wave + i) + (lane >> 3);
+          voff[i] = (uint32_t)min(q0 + r, q1 - 1) * rowb + 16u * (uint32_t)((lane & 7) ^ ((r >> 1) & 7));
+        }
       }
     } else {
       // expert E is the shared expert; without one the reads stay inside the stack
       const uint8_t* wb = e >= p.E && p.wsh ? p.wsh : p.wt + (size_t)min(e, p.E - 1) * p.ebytes;
+      base_lo = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)wb);
+      base_hi = __builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)wb >> 32));
 #pragma unroll
-      for (int i = 0; i < NCW; i++) wsrc[i] = wb + (size_t)band_of(c, NCW * ww + i) * kT64Tile + 16 * lane;
-      wsrc[NCW] = wb + (size_t)band_of(c, 8 * sbj + (lane >> 3)) * kT64Tile + kT64Codes + 16 * (lane & 7);
+      for (int i = 0; i < NCW; i++) voff[i] = (uint32_t)band_of(c, NCW * ww + i) * kT64Tile + 16u * lane;
+      if constexpr (ROLE == 1)
+        voff[NCW] = (uint32_t)band_of(c, 8 * sbj + (lane >> 3)) * kT64Tile + kT64Codes + 16u * (lane & 7);
     }
   };
   stream_item(s_item);
   auto issue = [&]() __attribute__((always_inline)) {
-    if (wave < 4) {
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(((uint64_t)base_hi << 32) | base_lo), 0, (int)nrec, 0x00020000);
+    if constexpr (AW) {
       uint8_t* st = aring + s_st * A_BYTES;
 #pragma unroll
-      for (int i = 0; i < MT; i++) dma16(arow[i] + (size_t)s_g * kGroup, st + (MT * wave + i) * 1024);
-      s_st = s_st + 1 == NA ? 0 : s_st + 1;
+      for (int i = 0; i < MT; i++) bdma16(rsrc, st + (MT * wave + i) * 1024, voff[i], soff);
     } else {
       uint8_t* st = wring + s_st * W_BYTES;
-      const size_t off = (size_t)s_g * gstride;
 #pragma unroll
-      for (int i = 0; i < NCW; i++) dma16(wsrc[i] + off, st + (NCW * ww + i) * kT64Codes);
-      if (has_sb) dma16(wsrc[NCW] + off, st + SB_OFF + sbj * 1024);
-      s_st = s_st + 1 == NW ? 0 : s_st + 1;
+      for (int i = 0; i < NCW; i++) bdma16(rsrc, st + (NCW * ww + i) * kT64Codes, voff[i], soff);
+      if constexpr (ROLE == 1) bdma16(rsrc, st + SB_OFF + sbj * 1024, voff[NCW], soff);
     }
-    s_i++;
-    if (++s_g == G) {
+    s_st = s_st + 1 == NR ? 0 : s_st + 1;
+    soff += gstep;
+    if (++s_g == G) {  // next item; past the last one the stream re-reads it
       s_g = 0;
-      if (++s_item < it1) stream_item(s_item);
+      soff = 0;
+      if (s_item + 1 < it1) s_item++;
+      stream_item(s_item);
     }
   };
 
-  // this wave's bands of weight stage ws, dequantized
-  auto dequant = [&](int ws, u32x4 (&bf)[NBW][4]) __attribute__((always_inline)) {
+  // LDS reads run one step ahead of their use: at step i the wave reads the activation fragments of step i + 1 and
+  // the weight codes of step i + 2 while its MFMAs (step i) and dequant (step i + 1) work on registers, so neither
+  // waits on LDS.
+  struct Codes {
+    u32x4 w[NBW];
+    uint32_t sb[NBW];
+  };
+  auto read_codes = [&](int ws, Codes& cd) __attribute__((always_inline)) {  // this wave's bands of weight stage ws
     const uint8_t* wst = wring + ws * W_BYTES;
 #pragma unroll
     for (int nb = 0; nb < NBW; nb++) {
       const int t = 8 * nb + wave;
-      const u32x4 codes = *(const u32x4*)(wst + t * kT64Codes + 16 * lane);
-      const uint32_t sb = *(const uint32_t*)(wst + SB_OFF + t * 128 + 4 * j);
-      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), sa = t64_sa(sc), sbs = t64_sb(sc);
-#pragma unroll
-      for (int q = 0; q < 4; q++) bf[nb][q] = t64_dequant(codes[q], sa, sbs, bi);
+      cd.w[nb] = *(const u32x4*)(wst + t * kT64Codes + 16 * lane);
+      cd.sb[nb] = *(const uint32_t*)(wst + SB_OFF + t * 128 + 4 * j);
     }
   };
-  auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) __attribute__((always_inline)) {
-    const int r = a * 32 + j;
+  auto dequant = [&](const Codes& cd, u32x4 (&bf)[NBW][4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) af[t] = *(const u32x4*)(st + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+    for (int nb = 0; nb < NBW; nb++) {
+      const float sc = bf2f((uint16_t)(cd.sb[nb] & 0xFFFFu)), bi = bf2f((uint16_t)(cd.sb[nb] >> 16));
+      const float sa = t64_sa(sc), sbs = t64_sb(sc);
+#pragma unroll
+      for (int q = 0; q < 4; q++) bf[nb][q] = t64_dequant(cd.w[nb][q], sa, sbs, bi);
+    }
+  };
+  // activation fragments of stage st: M tile a, MFMA step t takes k = 32 h + 8 t .. + 7 (logical column 4 h + t)
+  auto load_a = [&](const uint8_t* st, u32x4 (&af)[MT][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < MT; a++) {
+      const int r = a * 32 + j;
+#pragma unroll
+      for (int t = 0; t < 4; t++) af[a][t] = *(const u32x4*)(st + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+    }
   };
 
   f32x16 acc[NBW][MT];
@@ -206,58 +243,51 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
 #pragma unroll
     for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
 
-  // Waits. A wave waits until only younger operations than the DMA it needs are outstanding: its later DMAs and
-  // the output stores (NST per item end) of the item ends it issued after that DMA. Every operation of a wave
-  // completes in issue order, so the needed DMA has landed. nrec: those item ends (0, 1 or 2).
-  constexpr int NST = 2 * MT * (WIDE ? 2 : 1);  // output stores per item end
-  auto wait_a = [&](int k, int nrec) __attribute__((always_inline)) { wait_vm_rec<MT, NA - 2, NST>(k, nrec); };
-  auto wait_w = [&](int k, int nrec, bool first) __attribute__((always_inline)) {  // k = younger weight steps
-    if (first) {
-      if (has_sb) wait_vm_dyn<NCW + 1, NW - 2>(k);
-      else wait_vm_dyn<NCW, NW - 2>(k);
-    } else {
-      if (has_sb) wait_vm_rec<NCW + 1, NW - 3, NST>(k, nrec);
-      else wait_vm_rec<NCW, NW - 3, NST>(k, nrec);
-    }
-  };
-  {
-    const int pre = min(wave < 4 ? NA - 1 : NW - 1, n);
-    for (int i = 0; i < pre; i++) issue();
-  }
-  if (wave >= 4) wait_w(min(NW - 2, n - 1), 0, true);  // W(0) for the first dequant
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)p.C, 0, (int)p.c_bytes, 0x00020000);
+  // prologue: LAG steps of this role's stream; then A(0) and W(0), W(1) into registers
+  for (int i = 0; i < LAG; i++) issue();
+  if constexpr (AW) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(D * (NA - 2)) : "memory");  // A(0)
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(D * (NW - 3)) : "memory");               // W(0), W(1)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  u32x4 bf0[NBW][4], bf1[NBW][4];
-  dequant(0, bf0);
-  int ca = 0, cw = 1 % NW;
+  u32x4 bf0[NBW][4], bf1[NBW][4], af0[MT][4], af1[MT][4];
+  Codes cd0, cd1;
+  load_a(aring, af0);
+  read_codes(0, cd0);
+  dequant(cd0, bf0);
+  read_codes(1 % NW, cd0);
+  int ca1 = 1 % NA, cw2 = 2 % NW;  // stages read at step i: activations of step i + 1, codes of step i + 2
 
-  // step i with the B fragments of step i in bc; dequantizes step i + 1 into bn. Waves 0-3 need A(i), waves 4-7
-  // W(i + 1); the stage a DMA issued here overwrites held a step every wave finished before the barrier.
-  // Item ends whose stores are younger than the DMA awaited at step i: for A(i), issued at step i - NA + 1, those
-  // at the ends of steps i - NA + 1 .. i - 1; for W(i + 1), issued at step i + 2 - NW, those from step i + 2 - NW.
-  int d1 = 1 << 20, d2 = 1 << 20;  // steps since the last two item ends
-  auto step = [&](int i, u32x4 (&bc)[NBW][4], u32x4 (&bn)[NBW][4]) __attribute__((always_inline)) {
-    if (wave < 4) wait_a(min(NA - 2, n - 1 - i), (d1 < NA - 1) + (d2 < NA - 1));
-    else if (i + 1 < n) wait_w(min(NW - 3, n - 2 - i), (d1 < NW - 2) + (d2 < NW - 2), false);
-    d1++, d2++;
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (s_i < n) issue();
-    dequant(cw, bn);  // past the run's end a stale stage, never used: one basic block with the MFMAs
-    const uint8_t* ast = aring + ca * A_BYTES;
-    u32x4 af[2][4];
-    load_a(ast, 0, af[0]);
+  // Step i: B fragments bc and activation fragments afc of step i, codes cc of step i + 1 in registers; reads the
+  // activations of step i + 1 into afn and the codes of step i + 2 into cn, dequantizes cc into bn. The waits are
+  // for A(i + 1) (ROLE 0) and W(i + 2) (ROLE 1 / 2); the stage a DMA issued here overwrites was read two steps ago.
+  auto step = [&](u32x4 (&bc)[NBW][4], u32x4 (&bn)[NBW][4], u32x4 (&afc)[MT][4], u32x4 (&afn)[MT][4], Codes& cc,
+                  Codes& cn) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(BASE) : "memory");
+    issue();
+    load_a(aring + ca1 * A_BYTES, afn);
+    read_codes(cw2, cn);
+    dequant(cc, bn);  // past the run's end stale stages, never used
 #pragma unroll
-    for (int a = 0; a < MT; a++) {
-      if (a + 1 < MT) load_a(ast, a + 1, af[(a + 1) & 1]);
+    for (int a = 0; a < MT; a++)
 #pragma unroll
       for (int nb = 0; nb < NBW; nb++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[nb][a] = mfma_bf16(af[a & 1][t], bc[nb][t], acc[nb][a]);
+        for (int t = 0; t < 4; t++) acc[nb][a] = mfma_bf16(afc[a][t], bc[nb][t], acc[nb][a]);
+    // the LDS reads first, then one MFMA after each share of the dequant VALU
+    __builtin_amdgcn_sched_group_barrier(0x100, 4 * MT + 2 * NBW, 0);
+#pragma unroll
+    for (int k = 0; k < 4 * NBW * MT; k++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, (NBW * (4 * 17 + 8) + 4 * NBW * MT - 1) / (4 * NBW * MT), 0);
     }
-    ca = ca + 1 == NA ? 0 : ca + 1;
-    cw = cw + 1 == NW ? 0 : cw + 1;
+#pragma unroll
+    for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) asm volatile("" : "+v"(bn[nb][t]));
+    ca1 = ca1 + 1 == NA ? 0 : ca1 + 1;
+    cw2 = cw2 + 1 == NW ? 0 : cw2 + 1;
   };
 
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)p.C, 0, (int)p.c_bytes, 0x00020000);
   // The item's outputs, one M tile at a time: bf16 (SwiGLU: h of the bf16 gate and up sums) into this wave's LDS
   // tile [32][32], then two 16-byte stores of 16 rows x 32 columns; rows past the segment go to an offset past the
   // buffer, which the bounds check drops.
@@ -291,18 +321,35 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
       for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
   };
 
-  int i = 0;
   for (int item = it0; item < it1; item++) {
+    for (int g = 0; g < G; g += 2) {  // G is even
+      step(bf0, bf1, af0, af1, cd0, cd1);
+      step(bf1, bf0, af1, af0, cd1, cd0);
+    }
     int e, c, q0, q1;
     item_rows(item, e, c, q0, q1);
     (void)e;
-    for (int g = 0; g < G; g += 2, i += 2) {  // G is even
-      step(i, bf0, bf1);
-      step(i + 1, bf1, bf0);
-    }
     epilogue(c, q0, q1);
-    d2 = d1, d1 = 0;
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA lands in LDS after the block ends
+}
+
+// WIDE (plain only): each wave owns two bands, 8 apart, so an item is 16 bands (512 columns)
+template <int MT, bool SILU, bool WIDE>
+__global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
+  constexpr bool TWO = SILU || WIDE;
+  static_assert(!(SILU && WIDE), "SwiGLU pairs a gate and an up band per wave");
+  static_assert(gq_lds(MT, TWO) <= 160 * 1024, "LDS plan");
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = xcd_remap(blockIdx.x, p.nblk);
+  const int nitems = sload(p.ntiles, 0) << p.nct_log2;
+  const int it0 = (int)((long)b * nitems / p.nblk), it1 = (int)((long)(b + 1) * nitems / p.nblk);
+  if (it0 >= it1) return;  // block-uniform, before any barrier
+  const bool has_sb = TWO ? wave - 4 < 2 : wave == 7;
+  if (wave < 4) gq_role<MT, SILU, WIDE, 0>(p, lds, wave, it0, it1);
+  else if (has_sb) gq_role<MT, SILU, WIDE, 1>(p, lds, wave, it0, it1);
+  else gq_role<MT, SILU, WIDE, 2>(p, lds, wave, it0, it1);
 }
 
 // ---- host side
@@ -349,8 +396,12 @@ int launch_moe_gather_qmm_t64(const uint16_t* A, int lda, const int* perm, int d
   const bool wide = !silu && NO % 512 == 0;
   const int nct = NO / (wide ? 512 : 256);
   if (nct & (nct - 1)) return fail(IFD_ERR_UNSUPPORTED, "moe_gather_qmm_t64: %d column tiles (not a power of 2)", nct);
-  GqArgs a{A, lda, perm, div_m, tiles, ntiles, offsets, (const uint8_t*)wt, t64_bytes(N, K), (const uint8_t*)wsh,
-           E, N, K, K / kGroup, C, (uint32_t)cb, ldc, __builtin_ctz(nct), gq_cus()};
+  // every perm value is a routed slot below rows, so a sorted row reads one of the first (rows - 1) / div + 1 rows
+  const size_t ab = (size_t)(perm ? (rows - 1) / div + 1 : rows) * lda * sizeof(uint16_t);
+  if (ab >= ((size_t)1 << 31)) return fail(IFD_ERR_UNSUPPORTED, "moe_gather_qmm_t64: activations past 2 GiB");
+  if (t64_bytes(N, K) >= ((size_t)1 << 31)) return fail(IFD_ERR_UNSUPPORTED, "moe_gather_qmm_t64: expert past 2 GiB");
+  GqArgs a{A, lda, (uint32_t)ab, perm, div_m, tiles, ntiles, offsets, (const uint8_t*)wt, t64_bytes(N, K),
+           (const uint8_t*)wsh, E, N, K, K / kGroup, C, (uint32_t)cb, ldc, __builtin_ctz(nct), gq_cus()};
   const int MT = tile_rows / 32;
   if (silu) return MT == 2 ? launch_gq_cfg<2, true, false>(a, st) : launch_gq_cfg<1, true, false>(a, st);
   if (wide) return MT == 2 ? launch_gq_cfg<2, false, true>(a, st) : launch_gq_cfg<1, false, true>(a, st);
