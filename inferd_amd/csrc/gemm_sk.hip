@@ -61,6 +61,7 @@ struct GemmSkArgs {
   const uint16_t* A;
   int lda;
   const uint8_t* wt;
+  uint32_t w_bytes;  // bytes of the T64 weights (buffer bound)
   int N, K;
   void* C;
   int ldc, M, mode;
@@ -73,101 +74,118 @@ struct GemmSkArgs {
 // the block whose run holds unit u
 __host__ __device__ inline int sk_block_of(long u, int nblk, long U) { return (int)((u * nblk + nblk - 1) / U); }
 
-template <int MT>
-__global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p) {
+// One wave-wide 16-byte-per-lane DMA through a buffer resource: lane l's 16 bytes at voff(l) + soff land at
+// lds + 16 l (LDS base in M0, wave-uniform control flow only).
+__device__ __forceinline__ void sk_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, (int)voff, (int)soff, 0, 0);
+}
+
+// The pipeline of one wave; W0: wave 0, which also issues the (s, b) rows. Its DMA stream is a sequence of pairs
+// (A(s), W(s + 1)), s = 0, 1, ...: the prologue issues W(0) and pairs 0 .. R - 2, step i pair R - 1 + i, past the
+// run's end too (re-reading the last tile), so the waits are constants: at step i the wave reads A(i + 1)'s
+// fragments and W(i + 2)'s codes, the second of pair i + 1, which R - 3 younger pairs follow. Stage j % R holds A(j)
+// and W(j); step i overwrites A(i - 1) and W(i), both read two steps earlier.
+template <int MT, bool W0>
+__device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const int wave, const int b) {
   constexpr int BM = 32 * MT, R = sk_ring(MT), A_BYTES = sk_abytes(MT), STAGE = sk_stage(MT);
-  constexpr int NE = MT * 16;  // accumulators per lane and band
-  static_assert(R >= 4 && sk_lds(MT) + 64 <= kSkLds / sk_bpc(MT), "LDS plan");
-  static_assert((R - 2) * (MT + 3) + 3 <= 63, "vmcnt range");
-  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int NE = MT * 16;     // accumulators per lane and band
+  constexpr int NW = W0 ? 3 : 2;  // weight DMAs per pair
+  constexpr int PAIR = MT + NW;
+  static_assert(R >= 4 && (R - 2) * PAIR <= 63, "ring depth, vmcnt range");
   float* const stg = (float*)lds;  // staged tile [BM][kSkRow], after the K loop
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 31, h = lane >> 5;
 
-  const int b = xcd_remap(blockIdx.x, p.nblk);
   const int G = p.G;
   const long U = (long)p.tiles_m * p.tiles_n * G;
   const int u0 = (int)((long)b * U / p.nblk), u1 = (int)((long)(b + 1) * U / p.nblk), n = u1 - u0;
   const int nbands = t64_bands(p.N);
-  const size_t gstride = (size_t)nbands * kT64Tile;
+  const uint32_t gstride = (uint32_t)nbands * kT64Tile;
+  const int tile_first = u0 / G, tile_last = (u1 - 1) / G;
 
-  auto phys_band = [&](int tn, int lb) __attribute__((always_inline)) {  // physical band of local band lb (0..7) of column tile tn
+  auto phys_band = [&](int tn, int lb) __attribute__((always_inline)) {  // physical band of local band lb (0..7)
     const int bb = p.swi ? (lb < 4 ? 4 * tn + lb : p.swi + 4 * tn + lb - 4) : 8 * tn + lb;
     return min(bb, nbands - 1);
   };
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.A, 0, (int)((uint32_t)p.M * p.lda * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.wt, 0, (int)p.w_bytes, 0x00020000);
 
-  // ---- this wave's DMA stream. Stage s of the ring holds the activation slab of one step ([BM][64 bf16], 16-byte
-  // columns XOR-swizzled by row pair) and its weights (8 code halves, then 8 (s, b) rows). Unit j's activations and
-  // weights share stage j % R. At step i the wave issues the activations of step i + R - 1 (its MT DMAs of 8 rows)
-  // and the weights of step i + R (the code halves of its two bands; wave 0 also the (s, b) rows of all 8), each
-  // stream with its own (tile, group) position.
-  const bool has_sb = wave == 0;
-  const uint16_t* arow[MT];  // this lane's source row (and 16-byte column) of each activation DMA in the tile
-  const uint8_t* wsrc[3];    // this lane's code sources (two bands) and (s, b) source
-  auto a_tile_addr = [&](int tile) __attribute__((always_inline)) {
+  // ---- the DMA streams: per-lane offsets of the current tile, group offsets in scalar registers
+  uint32_t va[MT], vw[NW];
+  auto a_tile = [&](int tile) __attribute__((always_inline)) {
     const int tm = tile % p.tiles_m;
 #pragma unroll
     for (int q = 0; q < MT; q++) {
       const int r = 8 * (MT * wave + q) + lane / 8;
       const int c = (lane & 7) ^ ((r >> 1) & 7);
-      arow[q] = p.A + (size_t)min(tm * BM + r, p.M - 1) * p.lda + 8 * c;
+      va[q] = (uint32_t)min(tm * BM + r, p.M - 1) * (uint32_t)p.lda * 2u + 16u * c;
     }
   };
-  auto w_tile_addr = [&](int tile) __attribute__((always_inline)) {
+  auto w_tile = [&](int tile) __attribute__((always_inline)) {
     const int tn = tile / p.tiles_m;
-    wsrc[0] = p.wt + (size_t)phys_band(tn, 2 * wave) * kT64Tile + 16 * lane;
-    wsrc[1] = p.wt + (size_t)phys_band(tn, 2 * wave + 1) * kT64Tile + 16 * lane;
-    wsrc[2] = p.wt + (size_t)phys_band(tn, lane / 8) * kT64Tile + kT64Codes + 16 * (lane & 7);
+    vw[0] = (uint32_t)phys_band(tn, 2 * wave) * kT64Tile + 16u * lane;
+    vw[1] = (uint32_t)phys_band(tn, 2 * wave + 1) * kT64Tile + 16u * lane;
+    if constexpr (W0) vw[2] = (uint32_t)phys_band(tn, lane / 8) * kT64Tile + kT64Codes + 16u * (lane & 7);
   };
-  int a_tile = u0 / G, a_g = u0 % G, a_i = 0, a_st = 0;
-  int w_tile = a_tile, w_g = a_g, w_i = 0, w_st = 0;
-  a_tile_addr(a_tile);
-  w_tile_addr(w_tile);
-  auto issue_a = [&]() __attribute__((always_inline)) {
-    uint8_t* st = lds + a_st * STAGE;
+  int a_t = tile_first, a_g = u0 % G, w_t = tile_first, w_g = a_g;
+  uint32_t a_so = (uint32_t)a_g * 2u * kGroup, w_so = (uint32_t)w_g * gstride;
+  a_tile(a_t);
+  w_tile(w_t);
+  auto issue_a = [&](int stage) __attribute__((always_inline)) {
+    uint8_t* st = lds + stage * STAGE;
 #pragma unroll
-    for (int q = 0; q < MT; q++) dma16(arow[q] + (size_t)a_g * kGroup, st + (MT * wave + q) * 1024);
-    a_st = a_st + 1 == R ? 0 : a_st + 1;
-    a_i++;
-    if (++a_g == G) {
-      a_g = 0;
-      if (a_i < n) a_tile_addr(++a_tile);
+    for (int q = 0; q < MT; q++) sk_dma(ra, st + (MT * wave + q) * 1024, va[q], a_so);
+    a_so += 2u * kGroup;
+    if (++a_g == G) {  // next tile; past the run's last one the stream re-reads it
+      a_g = 0, a_so = 0;
+      if (a_t < tile_last) a_tile(++a_t);
     }
   };
-  auto issue_w = [&]() __attribute__((always_inline)) {
-    uint8_t* st = lds + w_st * STAGE + A_BYTES;
-    const size_t off = (size_t)w_g * gstride;
-    dma16(wsrc[0] + off, st + (2 * wave) * kT64Codes);
-    dma16(wsrc[1] + off, st + (2 * wave + 1) * kT64Codes);
-    if (has_sb) dma16(wsrc[2] + off, st + 8 * kT64Codes);
-    w_st = w_st + 1 == R ? 0 : w_st + 1;
-    w_i++;
+  auto issue_w = [&](int stage) __attribute__((always_inline)) {
+    uint8_t* st = lds + stage * STAGE + A_BYTES;
+    sk_dma(rw, st + (2 * wave) * kT64Codes, vw[0], w_so);
+    sk_dma(rw, st + (2 * wave + 1) * kT64Codes, vw[1], w_so);
+    if constexpr (W0) sk_dma(rw, st + 8 * kT64Codes, vw[2], w_so);
+    w_so += gstride;
     if (++w_g == G) {
-      w_g = 0;
-      if (w_i < n) w_tile_addr(++w_tile);
+      w_g = 0, w_so = 0;
+      if (w_t < tile_last) w_tile(++w_t);
     }
   };
 
-  // this wave's two bands of the weights in stage s, dequantized
-  auto dequant = [&](int s, u32x4 (&bf)[2][4]) __attribute__((always_inline)) {
+  // LDS reads one step ahead of their use
+  struct Codes {
+    u32x4 w[2];
+    uint32_t sb[2];
+  };
+  auto read_codes = [&](int s, Codes& cd) __attribute__((always_inline)) {  // this wave's two bands of stage s
     const uint8_t* wst = lds + s * STAGE + A_BYTES;
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
       const int band = 2 * wave + nb;
-      const u32x4 codes = *(const u32x4*)(wst + band * kT64Codes + 16 * lane);
-      const uint32_t sb = *(const uint32_t*)(wst + 8 * kT64Codes + band * 128 + 4 * j);
-      const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16));
-      const float sa = t64_sa(sc), sbs = t64_sb(sc);
-#pragma unroll
-      for (int t = 0; t < 4; t++) bf[nb][t] = t64_dequant(codes[t], sa, sbs, bi);
+      cd.w[nb] = *(const u32x4*)(wst + band * kT64Codes + 16 * lane);
+      cd.sb[nb] = *(const uint32_t*)(wst + 8 * kT64Codes + band * 128 + 4 * j);
     }
   };
-  // activation fragments of M tile a: MFMA step t takes k = 32 h + 8 t .. + 7 (logical column 4 h + t)
-  auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) __attribute__((always_inline)) {
-    const int r = a * 32 + j;
+  auto dequant = [&](const Codes& cd, u32x4 (&bf)[2][4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) af[t] = *(const u32x4*)(st + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+    for (int nb = 0; nb < 2; nb++) {
+      const float sc = bf2f((uint16_t)(cd.sb[nb] & 0xFFFFu)), bi = bf2f((uint16_t)(cd.sb[nb] >> 16));
+      const float sa = t64_sa(sc), sbs = t64_sb(sc);
+#pragma unroll
+      for (int t = 0; t < 4; t++) bf[nb][t] = t64_dequant(cd.w[nb][t], sa, sbs, bi);
+    }
+  };
+  // activation fragments of stage s: M tile a, MFMA step t takes k = 32 h + 8 t .. + 7 (logical column 4 h + t)
+  auto load_a = [&](int s, u32x4 (&af)[MT][4]) __attribute__((always_inline)) {
+    const uint8_t* st = lds + s * STAGE;
+#pragma unroll
+    for (int a = 0; a < MT; a++) {
+      const int r = a * 32 + j;
+#pragma unroll
+      for (int t = 0; t < 4; t++) af[a][t] = *(const u32x4*)(st + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+    }
   };
 
   f32x16 acc[2][MT];
@@ -176,87 +194,69 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
 #pragma unroll
     for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
 
-  // Waits. At step i the wave needs A(i) and W(i + 1), both issued at step i - R + 1 (the prologue for the first
-  // steps), W(i + 1) after A(i): it waits until at most the DMAs issued after W(i + 1) are outstanding (every
-  // operation of a wave completes in issue order; younger output stores only lengthen the wait). In the last R
-  // steps of the run fewer are in flight: wait for all.
-  constexpr int nwa = 3, nwo = 2;  // weight DMAs per step of wave 0 / of the others
-  auto wait_step = [&](int i) __attribute__((always_inline)) {
-    if (i + R > n) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else if (i < R - 2) {  // the prologue's lone W(R - 1) sits between
-      if (has_sb) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 3) * (MT + nwa) + nwa) : "memory");
-      else asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 3) * (MT + nwo) + nwo) : "memory");
-    } else {
-      if (has_sb) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 2) * (MT + nwa)) : "memory");
-      else asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 2) * (MT + nwo)) : "memory");
-    }
-  };
-  // prologue: A(0..R-2) and W(0..R-1) (those of the run), then W(0) for the first dequant
-  for (int jj = 0; jj < R - 1; jj++) {
-    if (a_i < n) issue_a();
-    if (w_i < n) issue_w();
+  // prologue: W(0), then pairs 0 .. R - 2; A(0) and W(0), W(1) (pair 0) are awaited before step 0
+  issue_w(0);
+  for (int s = 0; s < R - 1; s++) {
+    issue_a(s);
+    issue_w(s + 1);
   }
-  if (w_i < n) issue_w();
-  if (n < R) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  } else {
-    if (has_sb) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 2) * (MT + nwa) + nwa) : "memory");
-    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"((R - 2) * (MT + nwo) + nwo) : "memory");
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  u32x4 bf0[2][4], bf1[2][4];
-  dequant(0, bf0);
-  int ca = 0, cw = 1 % R;  // stage of step i (activations) and of step i + 1 (weights to dequantize)
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 2) * PAIR) : "memory");
+  u32x4 bf0[2][4], bf1[2][4], af0[MT][4], af1[MT][4];
+  Codes cd0, cd1;
+  load_a(0, af0);
+  read_codes(0, cd0);
+  dequant(cd0, bf0);
+  read_codes(1, cd0);
+  int s0 = 0;  // step i % R
 
-  // step i with the B fragments of step i in bc; dequantizes step i + 1 into bn
-  auto step = [&](int i, u32x4 (&bc)[2][4], u32x4 (&bn)[2][4]) __attribute__((always_inline)) {
-    wait_step(i);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (a_i < n) issue_a();
-    if (w_i < n) issue_w();
-    // One basic block: the step's activation fragments and the next step's codes from LDS, then the MFMAs with the
-    // next step's dequant between them, so that the VALU work and the LDS latency overlap the matrix core. Past the
-    // run's end the dequant reads a stale stage, never used.
-    const uint8_t* ast = lds + ca * STAGE;
-    u32x4 af[MT][4];
-#pragma unroll
-    for (int a = 0; a < MT; a++) load_a(ast, a, af[a]);
-    dequant(cw, bn);
+  // Step i: bc / afc (B and A fragments of step i) and cc (codes of step i + 1) in registers; reads afn (step i + 1)
+  // and cn (step i + 2), dequantizes cc into bn, and issues pair R - 1 + i.
+  auto step = [&](u32x4 (&bc)[2][4], u32x4 (&bn)[2][4], u32x4 (&afc)[MT][4], u32x4 (&afn)[MT][4], Codes& cc,
+                  Codes& cn) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 3) * PAIR) : "memory");
+    const int s1 = s0 + 1 == R ? 0 : s0 + 1, s2 = s1 + 1 == R ? 0 : s1 + 1, sm = s0 == 0 ? R - 1 : s0 - 1;
+    issue_a(sm);
+    issue_w(s0);
+    load_a(s1, afn);
+    read_codes(s2, cn);
+    dequant(cc, bn);  // past the run's end stale stages, never used
 #pragma unroll
     for (int a = 0; a < MT; a++)
 #pragma unroll
       for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[nb][a] = mfma_bf16(af[a][t], bc[nb][t], acc[nb][a]);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4 * MT + 4, 0);  // the LDS reads
+        for (int t = 0; t < 4; t++) acc[nb][a] = mfma_bf16(afc[a][t], bc[nb][t], acc[nb][a]);
+    // the LDS reads first, then one MFMA after each share of the dequant VALU
+    __builtin_amdgcn_sched_group_barrier(0x100, 4 * MT + 4, 0);
 #pragma unroll
     for (int k = 0; k < 8 * MT; k++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                    // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, (kSkDeqValu + 8 * MT - 1) / (8 * MT), 0);  // VALU between
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, (kSkDeqValu + 8 * MT - 1) / (8 * MT), 0);
     }
-    // the next step's fragments are complete in this step (else the compiler may sink the dequant past the next
-    // barrier, next to its use)
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
       for (int t = 0; t < 4; t++) asm volatile("" : "+v"(bn[nb][t]));
-    ca = ca + 1 == R ? 0 : ca + 1;
-    cw = cw + 1 == R ? 0 : cw + 1;
+    s0 = s1;
   };
-  // steps [lo, hi) with the current fragments in bf0 on entry and on exit
+  // steps [lo, hi) with the current fragments in bf0 / af0 / cd0 on entry and on exit
   auto run = [&](int lo, int hi) __attribute__((always_inline)) {
     int i = lo;
     for (; i + 1 < hi; i += 2) {
-      step(i, bf0, bf1);
-      step(i + 1, bf1, bf0);
+      step(bf0, bf1, af0, af1, cd0, cd1);
+      step(bf1, bf0, af1, af0, cd1, cd0);
     }
     if (i < hi) {
-      step(i, bf0, bf1);
+      step(bf0, bf1, af0, af1, cd0, cd1);
 #pragma unroll
       for (int nb = 0; nb < 2; nb++)
 #pragma unroll
         for (int t = 0; t < 4; t++) bf0[nb][t] = bf1[nb][t];
+#pragma unroll
+      for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) af0[a][t] = af1[a][t];
+      cd0 = cd1;
     }
   };
 
@@ -280,7 +280,6 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
         }
   };
 
-  const int tile_first = u0 / G, tile_last = (u1 - 1) / G;
   const bool two = tile_last != tile_first;
   const int n1 = min(n, (tile_first + 1) * G - u0);
   run(0, n1);
@@ -343,6 +342,16 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
     return;
   }
   write_slot(2 * b + (two ? 1 : 0));  // a piece of a cut tile: k_sk_fixup sums the pieces
+}
+
+template <int MT>
+__global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p) {
+  static_assert(sk_lds(MT) + 64 <= kSkLds / sk_bpc(MT), "LDS plan");
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = xcd_remap(blockIdx.x, p.nblk);
+  if (wave == 0) sk_body<MT, true>(p, lds, wave, b);
+  else sk_body<MT, false>(p, lds, wave, b);
 }
 
 // Sum of a cut tile's pieces (partial slots, in unit order) and its store. Block (tile, w, f): one wave over the
@@ -435,7 +444,7 @@ static SkPlan gemm_sk_plan(int M, int N, int K) {
 // stream-K is faster on every narrow shape measured (K = 17408: 45.9 against 47.6 us; N = K = 5120: 26.0 against
 // 31.2 us; N = 2048, K = 8192: 23.5 against 31.0 us), and both kernels compute bf16(s*q + b) there.
 bool gemm_sk_applies(int M, int N, int K, int mode) {
-  if (M <= 16 || K % kGroup) return false;
+  if (M <= 16 || K % kGroup || t64_bytes(N, K) >= ((size_t)1 << 31)) return false;
   if (mode == kModeSwiglu && N % 256) return false;
   const SkPlan pl = gemm_sk_plan(M, N, K);
   return (long)pl.tiles_m * pl.tiles_n * 3 >= cu_count() || (M > 64 && M <= 128);
@@ -470,7 +479,9 @@ int launch_gemm_sk(const uint16_t* A, int lda, const void* wt, int N, int K, voi
   if (need > ws_bytes || !ws)
     return fail(IFD_ERR_WORKSPACE, "gemm_sk needs %zu bytes of workspace, got %zu", need, ws_bytes);
   if (need >= (size_t)1 << 31) return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: partials past 2 GiB");
-  GemmSkArgs a{A, lda, (const uint8_t*)wt, N, K, C, ldc, M, mode, (float*)ws, (uint32_t)need,
+  if (t64_bytes(N, K) >= ((size_t)1 << 31) || (size_t)M * lda * 2 >= ((size_t)1 << 31))
+    return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: operands past 2 GiB");
+  GemmSkArgs a{A, lda, (const uint8_t*)wt, (uint32_t)t64_bytes(N, K), N, K, C, ldc, M, mode, (float*)ws, (uint32_t)need,
                pl.tiles_m, pl.tiles_n, pl.G, pl.nblk, mode == kModeSwiglu ? N / 64 : 0};
   if (pl.MT == 1) return launch_sk_cfg<1>(a, st);
   if (pl.MT == 2) return launch_sk_cfg<2>(a, st);

@@ -6,6 +6,7 @@
 // moe_sort (moe.metal:130-161), moe_gather (:163-170), MLX affine_gather_qmm_rhs (quantized_nax.h:1467-1681) driven by
 // schedule_row_tile (steel/utils.h:502-542), moe_silu_mul (:103-111) and moe_combine_sorted (:172-187).
 #include "common.h"
+#include "dma.h"
 #include "host.h"
 #include "kernels.h"
 #include "moe_dev.h"
@@ -82,9 +83,85 @@ __global__ __launch_bounds__(kRlWaves * 64) void k_router_logits(const uint16_t*
   }
 }
 
+// ---- router logits for large batches: LDS-staged 64-token x 128-expert tiles --------------------------------------
+// Block = 4 waves over one tile; wave w owns experts 32 w .. + 31 of the tile for all 64 tokens (two MFMA tiles).
+// K advances in 64-wide chunks through a ring of kRgR stages filled by direct global -> LDS DMA: a stage holds the
+// tile's token rows [64][64 bf16] and expert rows [128][64 bf16], 16-byte columns XOR-swizzled by row pair for
+// conflict-free fragment reads; rows past T or E1 repeat the last one. Each wave issues 2 token and 4 expert DMAs per
+// chunk. Every token row is read once per expert tile and every expert row once per token tile, from L2.
+constexpr int kRgR = 4, kRgTok = 64, kRgExp = 128;
+constexpr int kRgStage = (kRgTok + kRgExp) * 128;
+__global__ __launch_bounds__(256) void k_router_tiled(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                      int T, int H, int E1, int out_bf16, void* out) {
+  __shared__ __align__(16) uint8_t lds[kRgR * kRgStage];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 31, h = lane >> 5;
+  const int t0 = blockIdx.x * kRgTok, e0 = blockIdx.y * kRgExp;
+  const int C = H / 64;
+  // this lane's sources: token rows 16 wave + 8 i + lane / 8 (i < 2), expert rows 32 wave + 8 i + lane / 8 (i < 4)
+  const uint16_t* src[6];
+#pragma unroll
+  for (int i = 0; i < 6; i++) {
+    const bool tk = i < 2;
+    const int r = tk ? 16 * wave + 8 * i + (lane >> 3) : 32 * wave + 8 * (i - 2) + (lane >> 3);
+    const int c16 = (lane & 7) ^ ((r >> 1) & 7);
+    src[i] = tk ? x + (size_t)min(t0 + r, T - 1) * H + 8 * c16 : w + (size_t)min(e0 + r, E1 - 1) * H + 8 * c16;
+  }
+  auto issue = [&](int c, int stage) __attribute__((always_inline)) {
+    uint8_t* st = lds + stage * kRgStage;
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+      const int r0 = i < 2 ? 16 * wave + 8 * i : kRgTok + 32 * wave + 8 * (i - 2);
+      dma16(src[i] + (size_t)c * 64, st + r0 * 128);
+    }
+  };
+  for (int c = 0; c < kRgR - 1 && c < C; c++) issue(c, c);
+  f32x16 acc[2] = {zero16(), zero16()};
+  int stage = 0;
+  for (int c = 0; c < C; c++) {
+    // chunk c landed: the DMAs of the chunks issued after it are younger (6 each); near the end fewer were issued
+    if (c + kRgR - 2 < C) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(6 * (kRgR - 2)) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (c + kRgR - 1 < C) issue(c + kRgR - 1, (stage + kRgR - 1) % kRgR);  // into the stage read at chunk c - 1
+    const uint8_t* st = lds + stage * kRgStage;
+    u32x4 a[2][4], b[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+      for (int m = 0; m < 2; m++) {
+        const int r = 32 * m + j;
+        a[m][t] = *(const u32x4*)(st + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+      }
+      const int r = kRgTok + 32 * wave + j;
+      b[t] = *(const u32x4*)(st + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+      for (int m = 0; m < 2; m++) acc[m] = mfma_bf16(a[m][t], b[t], acc[m]);
+    stage = stage + 1 == kRgR ? 0 : stage + 1;
+  }
+  const int e = e0 + 32 * wave + j;
+  if (e >= E1) return;
+#pragma unroll
+  for (int m = 0; m < 2; m++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int t = t0 + 32 * m + 8 * (r / 4) + 4 * h + (r % 4);
+      if (t >= T) continue;
+      if (out_bf16) ((uint16_t*)out)[(size_t)t * E1 + e] = f2bf(acc[m][r]);
+      else ((float*)out)[(size_t)t * E1 + e] = acc[m][r];
+    }
+}
+
 int launch_router_logits(const uint16_t* x, const uint16_t* w, int T, int H, int E1, int out_bf16, void* logits,
                          hipStream_t st) {
   if (T == 0) return IFD_OK;
+  if (T >= 256) {  // enough 64 x 128 tiles to fill most CUs without a K split
+    const dim3 grid((T + kRgTok - 1) / kRgTok, (E1 + kRgExp - 1) / kRgExp);
+    hipLaunchKernelGGL(k_router_tiled, grid, dim3(256), 0, st, x, w, T, H, E1, out_bf16, logits);
+    return check_launch("router_logits");
+  }
   const int tiles_e = (E1 + 31) / 32, tiles = (T + 31) / 32 * tiles_e;
   // K splits: at least two per tile once the tiles fill the CUs (a block then holds 4 tiles, and there are blocks
   // for every CU), more below that

@@ -41,7 +41,7 @@ def router(E1, H, seed):
     return gen.f32_to_bf16((rng.standard_normal((E1, H)) * 0.02).astype(np.float32))
 
 
-@pytest.mark.parametrize("T,out_bf16", [(16, False), (128, True), (70, True)])
+@pytest.mark.parametrize("T,out_bf16", [(16, False), (128, True), (70, True), (300, False), (2048, True)])
 def test_router_logits(T, out_bf16):
     g, ops = _gu(), _ops()
     H, E1 = 2048, 513
