@@ -132,21 +132,32 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
   uint32_t a_so = (uint32_t)a_g * 2u * kGroup, w_so = (uint32_t)w_g * gstride;
   a_tile(a_t);
   w_tile(w_t);
+  // the DMAs of one pair (no branch, so that they schedule among the MFMAs), then the streams' advance
   auto issue_a = [&](int stage) __attribute__((always_inline)) {
     uint8_t* st = lds + stage * STAGE;
 #pragma unroll
     for (int q = 0; q < MT; q++) sk_dma(ra, st + (MT * wave + q) * 1024, va[q], a_so);
-    a_so += 2u * kGroup;
-    if (++a_g == G) {  // next tile; past the run's last one the stream re-reads it
-      a_g = 0, a_so = 0;
-      if (a_t < tile_last) a_tile(++a_t);
-    }
   };
   auto issue_w = [&](int stage) __attribute__((always_inline)) {
     uint8_t* st = lds + stage * STAGE + A_BYTES;
     sk_dma(rw, st + (2 * wave) * kT64Codes, vw[0], w_so);
     sk_dma(rw, st + (2 * wave + 1) * kT64Codes, vw[1], w_so);
     if constexpr (W0) sk_dma(rw, st + 8 * kT64Codes, vw[2], w_so);
+  };
+  auto advance = [&]() __attribute__((always_inline)) {
+    a_so += 2u * kGroup;
+    if (++a_g == G) {  // next tile; past the run's last one the stream re-reads it
+      a_g = 0, a_so = 0;
+      if (a_t < tile_last) a_tile(++a_t);
+    }
+    w_so += gstride;
+    if (++w_g == G) {
+      w_g = 0, w_so = 0;
+      if (w_t < tile_last) w_tile(++w_t);
+    }
+  };
+  // W(0) alone: the weight stream's advance only
+  auto advance_w = [&]() __attribute__((always_inline)) {
     w_so += gstride;
     if (++w_g == G) {
       w_g = 0, w_so = 0;
@@ -196,9 +207,11 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
 
   // prologue: W(0), then pairs 0 .. R - 2; A(0) and W(0), W(1) (pair 0) are awaited before step 0
   issue_w(0);
+  advance_w();
   for (int s = 0; s < R - 1; s++) {
     issue_a(s);
     issue_w(s + 1);
+    advance();
   }
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 2) * PAIR) : "memory");
   u32x4 bf0[2][4], bf1[2][4], af0[MT][4], af1[MT][4];
@@ -215,29 +228,56 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
                   Codes& cn) __attribute__((always_inline)) {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 3) * PAIR) : "memory");
     const int s1 = s0 + 1 == R ? 0 : s0 + 1, s2 = s1 + 1 == R ? 0 : s1 + 1, sm = s0 == 0 ? R - 1 : s0 - 1;
-    issue_a(sm);
-    issue_w(s0);
-    load_a(s1, afn);
-    read_codes(s2, cn);
-    dequant(cc, bn);  // past the run's end stale stages, never used
+    // Eight groups, each closed by a scheduling barrier: MT MFMAs of this step, one 8-code dequant of the next
+    // (17 VALU), a share of the LDS reads for the next steps and at most one DMA, so that the matrix core has work
+    // through the whole step and the wave's other instructions issue in its shadow.
+    constexpr int NDS = 4 * MT + 4, NDMA = MT + NW;
+    const uint8_t* const ast = lds + s1 * STAGE;        // activation fragments of step i + 1
+    const uint8_t* const wst = lds + s2 * STAGE + A_BYTES;  // codes of step i + 2
+    float sa[2], sbs[2], bi[2];
 #pragma unroll
-    for (int a = 0; a < MT; a++)
+    for (int nb = 0; nb < 2; nb++) {
+      const float sc = bf2f((uint16_t)(cc.sb[nb] & 0xFFFFu));
+      bi[nb] = bf2f((uint16_t)(cc.sb[nb] >> 16)), sa[nb] = t64_sa(sc), sbs[nb] = t64_sb(sc);
+    }
 #pragma unroll
-      for (int nb = 0; nb < 2; nb++)
+    for (int g = 0; g < 8; g++) {
+      if (g < NDMA) {
+        if (g < MT) sk_dma(ra, lds + sm * STAGE + (MT * wave + g) * 1024, va[g], a_so);
+        else if (g == MT) sk_dma(rw, lds + s0 * STAGE + A_BYTES + (2 * wave) * kT64Codes, vw[0], w_so);
+        else if (g == MT + 1) sk_dma(rw, lds + s0 * STAGE + A_BYTES + (2 * wave + 1) * kT64Codes, vw[1], w_so);
+        else if constexpr (W0) sk_dma(rw, lds + s0 * STAGE + A_BYTES + 8 * kT64Codes, vw[2], w_so);
+      }
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[nb][a] = mfma_bf16(afc[a][t], bc[nb][t], acc[nb][a]);
-    // the LDS reads first, then one MFMA after each share of the dequant VALU
-    __builtin_amdgcn_sched_group_barrier(0x100, 4 * MT + 4, 0);
+      for (int d = g * NDS / 8; d < (g + 1) * NDS / 8; d++) {
+        if (d < 4 * MT) {
+          const int am = d / 4, t = d % 4, r = am * 32 + j;
+          afn[am][t] = *(const u32x4*)(ast + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+        } else {
+          const int nb = (d - 4 * MT) / 2, band = 2 * wave + nb;
+          if ((d - 4 * MT) % 2 == 0) cn.w[nb] = *(const u32x4*)(wst + band * kT64Codes + 16 * lane);
+          else cn.sb[nb] = *(const uint32_t*)(wst + 8 * kT64Codes + band * 128 + 4 * j);
+        }
+      }
+      bn[g / 4][g % 4] = t64_dequant(cc.w[g / 4][g % 4], sa[g / 4], sbs[g / 4], bi[g / 4]);
 #pragma unroll
-    for (int k = 0; k < 8 * MT; k++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, (kSkDeqValu + 8 * MT - 1) / (8 * MT), 0);
+      for (int m = g * MT; m < (g + 1) * MT; m++) {
+        const int am = m / 8, nb = (m / 4) % 2, t = m % 4;
+        acc[nb][am] = mfma_bf16(afc[am][t], bc[nb][t], acc[nb][am]);
+      }
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 17 / MT + 1, 0);  // VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
       for (int t = 0; t < 4; t++) asm volatile("" : "+v"(bn[nb][t]));
     s0 = s1;
+    advance();
   };
   // steps [lo, hi) with the current fragments in bf0 / af0 / cd0 on entry and on exit
   auto run = [&](int lo, int hi) __attribute__((always_inline)) {
@@ -457,7 +497,7 @@ size_t gemm_sk_workspace(int M, int N, int K, int mode) {
 }
 
 template <int MT>
-static int launch_sk_cfg(const GemmSkArgs& a, hipStream_t st) {
+static int launch_sk_cfg(const GemmSkArgs& a, bool fixup, hipStream_t st) {
   constexpr size_t lds = sk_lds(MT);
   static bool attr = false;
   if (!attr) {
@@ -466,6 +506,7 @@ static int launch_sk_cfg(const GemmSkArgs& a, hipStream_t st) {
   }
   hipLaunchKernelGGL(k_gemm_sk<MT>, dim3(a.nblk), dim3(kSkThreads), lds, st, a);
   IFD_TRY(check_launch("gemm_sk"));
+  if (!fixup) return IFD_OK;
   hipLaunchKernelGGL(k_sk_fixup<MT>, dim3(a.tiles_m * a.tiles_n, a.swi ? 4 : 8, MT * 4), dim3(64), 0, st, a);
   return check_launch("gemm_sk fixup");
 }
@@ -481,11 +522,16 @@ int launch_gemm_sk(const uint16_t* A, int lda, const void* wt, int N, int K, voi
   if (need >= (size_t)1 << 31) return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: partials past 2 GiB");
   if (t64_bytes(N, K) >= ((size_t)1 << 31) || (size_t)M * lda * 2 >= ((size_t)1 << 31))
     return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: operands past 2 GiB");
+  // the fixup kernel runs when some tile is cut
+  const long tiles = (long)pl.tiles_m * pl.tiles_n, U = tiles * pl.G;
+  bool fixup = false;
+  for (long t = 0; t < tiles && !fixup; t++)
+    fixup = sk_block_of(t * pl.G + pl.G - 1, pl.nblk, U) != sk_block_of(t * pl.G, pl.nblk, U);
   GemmSkArgs a{A, lda, (const uint8_t*)wt, (uint32_t)t64_bytes(N, K), N, K, C, ldc, M, mode, (float*)ws, (uint32_t)need,
                pl.tiles_m, pl.tiles_n, pl.G, pl.nblk, mode == kModeSwiglu ? N / 64 : 0};
-  if (pl.MT == 1) return launch_sk_cfg<1>(a, st);
-  if (pl.MT == 2) return launch_sk_cfg<2>(a, st);
-  return launch_sk_cfg<4>(a, st);
+  if (pl.MT == 1) return launch_sk_cfg<1>(a, fixup, st);
+  if (pl.MT == 2) return launch_sk_cfg<2>(a, fixup, st);
+  return launch_sk_cfg<4>(a, fixup, st);
 }
 
 }  // namespace ifd

@@ -264,21 +264,43 @@ __device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int
                   Codes& cn) __attribute__((always_inline)) {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(BASE) : "memory");
     issue();
-    load_a(aring + ca1 * A_BYTES, afn);
-    read_codes(cw2, cn);
-    dequant(cc, bn);  // past the run's end stale stages, never used
+    // Eight groups, each closed by a scheduling barrier: 4 NBW MT / 8 MFMAs of this step, one 8-code dequant of the
+    // next (17 VALU) and a share of the LDS reads for the next steps, so that the matrix core has work through the
+    // whole step and the VALU issues in its shadow.
+    constexpr int NMF = 4 * NBW * MT, NDS = 4 * MT + 2 * NBW, NDQ = 4 * NBW;
+    const uint8_t* const ast = aring + ca1 * A_BYTES;  // activation fragments of step i + 1
+    const uint8_t* const wst = wring + cw2 * W_BYTES;  // codes of step i + 2
+    float sa[NBW], sbs[NBW], bi[NBW];
 #pragma unroll
-    for (int a = 0; a < MT; a++)
+    for (int nb = 0; nb < NBW; nb++) {
+      const float sc = bf2f((uint16_t)(cc.sb[nb] & 0xFFFFu));
+      bi[nb] = bf2f((uint16_t)(cc.sb[nb] >> 16)), sa[nb] = t64_sa(sc), sbs[nb] = t64_sb(sc);
+    }
 #pragma unroll
-      for (int nb = 0; nb < NBW; nb++)
+    for (int g = 0; g < NDQ; g++) {
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[nb][a] = mfma_bf16(afc[a][t], bc[nb][t], acc[nb][a]);
-    // the LDS reads first, then one MFMA after each share of the dequant VALU
-    __builtin_amdgcn_sched_group_barrier(0x100, 4 * MT + 2 * NBW, 0);
+      for (int d = g * NDS / NDQ; d < (g + 1) * NDS / NDQ; d++) {
+        if (d < 4 * MT) {
+          const int am = d / 4, t = d % 4, r = am * 32 + j;
+          afn[am][t] = *(const u32x4*)(ast + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+        } else {
+          const int nb = (d - 4 * MT) / 2, tt = 8 * nb + wave;
+          if ((d - 4 * MT) % 2 == 0) cn.w[nb] = *(const u32x4*)(wst + tt * kT64Codes + 16 * lane);
+          else cn.sb[nb] = *(const uint32_t*)(wst + SB_OFF + tt * 128 + 4 * j);
+        }
+      }
+      bn[g / 4][g % 4] = t64_dequant(cc.w[g / 4][g % 4], sa[g / 4], sbs[g / 4], bi[g / 4]);
 #pragma unroll
-    for (int k = 0; k < 4 * NBW * MT; k++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, (NBW * (4 * 17 + 8) + 4 * NBW * MT - 1) / (4 * NBW * MT), 0);
+      for (int m = g * NMF / NDQ; m < (g + 1) * NMF / NDQ; m++) {  // MFMA order: M tile, band, k step
+        const int am = m / (4 * NBW), nb = (m / 4) % NBW, t = m % 4;
+        acc[nb][am] = mfma_bf16(afc[am][t], bc[nb][t], acc[nb][am]);
+      }
+#pragma unroll
+      for (int m = 0; m < NMF / NDQ; m++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 17 * NDQ / NMF + 1, 0);  // VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int nb = 0; nb < NBW; nb++)
