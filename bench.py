@@ -39,8 +39,11 @@ ROW_BYTES_UNFUSED = (H_DEC + 2 * 2 * I_DEC + 2 * I_DEC + H_DEC) * 2  # + the gat
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    # The GPU's clock needs about 20-30 ms of load to settle after an idle spell (the first calls run fast, then slow
+    # while the power controller overshoots, then settle): 100 warmup steps of the headline (~26 ms) put the timed
+    # steps in the steady state that continuous serving runs in.
+    p.add_argument("--steps", type=int, default=40)
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--no-breakdown", action="store_true", help="headline workload only")
     p.add_argument("--only", default="",
@@ -81,10 +84,18 @@ def main():
             x = x * (torch.rand((M, 1), device=dev, generator=gen) * 1.5 + 0.5)
         return x.to(torch.bfloat16)
 
-    def timed(fn, n, warm):
+    def timed(fn, n, warm, settle_ms=30.0):
+        # warm calls, then more until the call has loaded the GPU for settle_ms (the clock's settling time), so that
+        # every breakdown figure is a steady-state one like the headline's
         for i in range(warm):
             fn(i)
         torch.cuda.synchronize()
+        t0, i = time.perf_counter(), warm
+        while (time.perf_counter() - t0) * 1e3 < settle_ms:
+            for _ in range(4):
+                fn(i)
+                i += 1
+            torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for i in range(n):

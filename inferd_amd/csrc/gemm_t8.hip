@@ -2,9 +2,11 @@
 // qmm rounding, quantized.h:528-535) and fp32 accumulation (reference affine_qmm_t_nax,
 // third_party/mlx/.../quantized_nax.h:938-1076, 1206-1267).
 //
-// Block: 8 waves (two per SIMD), tile 256 rows x 8 bands (256 columns); wave w owns band w over all 8 M tiles of 32
-// rows (128 fp32 accumulators per lane). Each dequantized B fragment feeds 8 MFMAs: half the dequant VALU per MFMA of
-// a 128-row tile; every wave reads the whole activation slab from LDS.
+// Block: 8 waves (two per SIMD), tile 256 rows x 8 bands (256 columns); wave w owns bands 2 (w % 4), 2 (w % 4) + 1
+// over M tiles 4 (w / 4) .. + 3 of 32 rows (128 fp32 accumulators per lane). One activation fragment read from LDS
+// feeds two MFMAs and one dequantized B fragment four: each band is dequantized by two waves, and the LDS serves
+// half the activation bytes of a one-band-per-wave layout (an MFMA reading its whole A operand from LDS would need
+// the LDS's full bandwidth).
 // K advances one 64-group per step through two LDS rings filled by direct global -> LDS DMA: kT8NS activation slabs
 // [256][64 bf16] (16-byte columns XOR-swizzled by row pair: conflict-free fragment reads) and kT8NW weight stages
 // (8 code halves, 8 (s, b) rows), one step further ahead. Per step wave w DMAs 4 KB of activations and its code tile;
@@ -21,13 +23,15 @@
 namespace ifd {
 
 constexpr int kT8NS = 3;   // activation slabs in the LDS ring
-constexpr int kT8NW = 4;   // weight stages in the LDS ring (one step further ahead)
+constexpr int kT8NW = 5;   // weight stages in the LDS ring (two steps further ahead)
 constexpr int kT8Band = 4;  // M tiles per band of the tile order
+constexpr int kT8Row = 256 + 4;  // staged half-tile row stride (floats)
 
 struct GemmT8Args {
   const uint16_t* A;
   int lda;
   const uint8_t* wt;
+  uint32_t w_bytes;  // bytes of the T64 weights (buffer bound)
   int N, K;
   void* C;
   int ldc, M, mode;
@@ -44,118 +48,220 @@ __host__ __device__ inline void t8_tile(int L, int tiles_m, int tiles_n, int& tm
   tn = within / bm;
 }
 
-__global__ __launch_bounds__(512, 1) void k_gemm_t8(GemmT8Args p) {
-  constexpr int MT = 8, BM = 256, NBB = 8;
+// One wave-wide 16-byte-per-lane DMA through a buffer resource: lane l's 16 bytes at voff(l) + soff land at
+// lds + 16 l (LDS base in M0, wave-uniform control flow only).
+__device__ __forceinline__ void t8_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, (int)voff, (int)soff, 0, 0);
+}
+
+// The pipeline of one wave; W0: wave 0, which also issues the (s, b) rows. Step s issues, right after its barrier,
+// the activations of group s + 2 and the weights of group s + 4, and waits at its barrier for the activations of s
+// (read through the step) and the weights of s + 2 (whose codes it reads for the dequant at step s + 1): both were
+// issued two steps earlier, and only the previous step's DMAs are younger. Past the split's end the streams re-read
+// its last group into stages nobody reads, so every step issues the same DMAs and every wait is a constant.
+template <bool W0>
+__device__ __forceinline__ void t8_body(const GemmT8Args& p, uint8_t* lds, const int wave, const int Lrel, int tm,
+                                        int tn) {
+  constexpr int BM = 256, NBB = 8;
   constexpr int A_BYTES = BM * 128;                     // activation slab [256][64 bf16]
   constexpr int W_BYTES = NBB * kT64Codes + NBB * 128;  // code halves [8][1024] + (s, b) rows [8][128]
-  constexpr int VPC = 4 + 1;                            // DMA instructions per wave per step (wave 0: one more)
-  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int D = 4 + 1 + (W0 ? 1 : 0);               // DMAs per step
   uint8_t* const aring = lds;                    // kT8NS slabs
   uint8_t* const wring = lds + kT8NS * A_BYTES;  // kT8NW weight stages
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 31, h = lane >> 5;
-
-  const int Lrel = xcd_remap(blockIdx.x, gridDim.x);
-  int tm, tn;
-  t8_tile(p.tile0 + Lrel, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * BM;
   const int nbands = t64_bands(p.N);
   const int G = p.K / kGroup;
   const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps), Gz = g1 - g0;
+  const uint32_t gstride = (uint32_t)nbands * kT64Tile;
 
   // activation DMA i (0..3) of this wave covers rows 8 (4 wave + i) .. + 7: lane -> row 8 (4 wave + i) + lane / 8,
   // physical 16-byte column lane % 8 holding logical column (lane % 8) ^ ((row / 2) % 8). Rows past M re-read row
   // M - 1 (their outputs are not stored).
-  const uint16_t* asrc[4];
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.A, 0, (int)((uint32_t)p.M * p.lda * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.wt, 0, (int)p.w_bytes, 0x00020000);
+  uint32_t va[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int r = 8 * (4 * wave + i) + lane / 8;
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    asrc[i] = p.A + (size_t)min(m0 + r, p.M - 1) * p.lda + 8 * c;
+    va[i] = (uint32_t)min(m0 + r, p.M - 1) * (uint32_t)p.lda * 2u + 16u * c;
   }
-  const size_t gstride = (size_t)nbands * kT64Tile;
-  const uint8_t* tb = p.wt + (size_t)min(tn * NBB + wave, nbands - 1) * kT64Tile + 16 * lane;
-  const uint8_t* sbsrc = p.wt + (size_t)min(tn * NBB + lane / 8, nbands - 1) * kT64Tile + kT64Codes + 16 * (lane & 7);
+  const uint32_t vw = (uint32_t)min(tn * NBB + wave, nbands - 1) * kT64Tile + 16u * lane;
+  const uint32_t vs = (uint32_t)min(tn * NBB + lane / 8, nbands - 1) * kT64Tile + kT64Codes + 16u * (lane & 7);
 
-  // groups past the split re-read its last group into a stage nobody reads again: every step issues the same DMAs
-  auto issue_w = [&](int step) {
-    const size_t g = (size_t)min(g0 + step, g1 - 1);
-    uint8_t* st = wring + (step % kT8NW) * W_BYTES;
-    dma16(tb + g * gstride, st + wave * kT64Codes);
-    if (wave == 0) dma16(sbsrc + g * gstride, st + NBB * kT64Codes);
-  };
-  auto issue_a = [&](int step) {
-    const size_t g = (size_t)min(g0 + step, g1 - 1);
-    uint8_t* st = aring + (step % kT8NS) * A_BYTES;
+  // the streams: group offsets of the next issue, clamped to the split's last group
+  int ga = g0, gw = g0, sa_st = 0, sw_st = 0;
+  auto issue_a = [&]() __attribute__((always_inline)) {
+    uint8_t* st = aring + sa_st * A_BYTES;
+    const uint32_t so = (uint32_t)min(ga, g1 - 1) * 2u * kGroup;
 #pragma unroll
-    for (int i = 0; i < 4; i++) dma16(asrc[i] + g * kGroup, st + (4 * wave + i) * 1024);
+    for (int i = 0; i < 4; i++) t8_dma(ra, st + (4 * wave + i) * 1024, va[i], so);
+    ga++;
+    sa_st = sa_st + 1 == kT8NS ? 0 : sa_st + 1;
+  };
+  auto issue_w = [&]() __attribute__((always_inline)) {
+    uint8_t* st = wring + sw_st * W_BYTES;
+    const uint32_t so = (uint32_t)min(gw, g1 - 1) * gstride;
+    t8_dma(rw, st + wave * kT64Codes, vw, so);
+    if constexpr (W0) t8_dma(rw, st + NBB * kT64Codes, vs, so);
+    gw++;
+    sw_st = sw_st + 1 == kT8NW ? 0 : sw_st + 1;
   };
 
-  f32x16 acc[MT];
+  // compute roles: wave w owns bands 2 bp, 2 bp + 1 (bp = w % 4) over M tiles 4 mh .. 4 mh + 3 (mh = w / 4), so one
+  // activation fragment read from LDS feeds two MFMAs
+  const int mh = wave >> 2, bp = wave & 3;
+  f32x16 acc[2][4];
 #pragma unroll
-  for (int a = 0; a < MT; a++) acc[a] = zero16();
-
-  // activation fragments of M tile a: MFMA step t takes k = 32 h + 8 t .. + 7 (logical column 4 h + t)
-  auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) {
-    const int r = a * 32 + j;
+  for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+    for (int a = 0; a < 4; a++) acc[nb][a] = zero16();
+  struct Codes {
+    u32x4 w[2];
+    uint32_t sb[2];
+  };
+  auto read_codes = [&](int ws, Codes& cd) __attribute__((always_inline)) {  // the wave's two bands of stage ws
+    const uint8_t* wst = wring + ws * W_BYTES;
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const int band = 2 * bp + nb;
+      cd.w[nb] = *(const u32x4*)(wst + band * kT64Codes + 16 * lane);
+      cd.sb[nb] = *(const uint32_t*)(wst + NBB * kT64Codes + band * 128 + 4 * j);
+    }
+  };
+  auto dequant = [&](const Codes& cd, u32x4 (&bf)[2][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const float sc = bf2f((uint16_t)(cd.sb[nb] & 0xFFFFu)), bi = bf2f((uint16_t)(cd.sb[nb] >> 16));
+      const float sa = t64_sa(sc), sbs = t64_sb(sc);
+#pragma unroll
+      for (int t = 0; t < 4; t++) bf[nb][t] = t64_dequant(cd.w[nb][t], sa, sbs, bi);
+    }
+  };
+  // activation fragments of the wave's M tile a: MFMA step t takes k = 32 h + 8 t .. + 7 (logical column 4 h + t)
+  auto load_a = [&](const uint8_t* st, int a, u32x4 (&af)[4]) __attribute__((always_inline)) {
+    const int r = (4 * mh + a) * 32 + j;
 #pragma unroll
     for (int t = 0; t < 4; t++) af[t] = *(const u32x4*)(st + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
   };
 
-  // the wave's band of group `step`, dequantized from its weight stage (one fragment set feeds the 8 M tiles)
-  auto dequant = [&](int step, u32x4 (&bf)[4]) {
-    const uint8_t* wst = wring + (step % kT8NW) * W_BYTES;
-    const u32x4 codes = *(const u32x4*)(wst + wave * kT64Codes + 16 * lane);
-    const uint32_t sb = *(const uint32_t*)(wst + NBB * kT64Codes + wave * 128 + 4 * j);
-    const float sc = bf2f((uint16_t)(sb & 0xFFFFu)), bi = bf2f((uint16_t)(sb >> 16)), sa = t64_sa(sc), sbs = t64_sb(sc);
-#pragma unroll
-    for (int t = 0; t < 4; t++) bf[t] = t64_dequant(codes[t], sa, sbs, bi);
-  };
+  // prologue: A(0), A(1) and W(0) .. W(3); then W(0) dequantized and W(1)'s codes read before step 0
+  for (int s = 0; s < 2; s++) {
+    issue_a();
+    issue_w();
+  }
+  issue_w();
+  issue_w();
+  // W(1) landed: the younger DMAs are W(2), W(3)
+  if constexpr (W0) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  u32x4 bf0[2][4], bf1[2][4];
+  Codes cc;
+  read_codes(0, cc);
+  dequant(cc, bf0);
+  read_codes(1, cc);
+  int ca = 0, cw2 = 2;  // stages: activations of step s, weights of step s + 2
 
-  // Pipeline: the weights of group s + 1 and the activations of group s are in LDS at step s. Per wave and step the
-  // DMAs are [activations of s + 2, weights of s + 3]: waiting for all but the last step's DMAs leaves exactly those
-  // in flight. The weight stage overwritten at step s (kT8NW = 4) held group s - 1, read at step s - 1; the slab
-  // overwritten (kT8NS = 3) held group s - 1 too. Step s: the wave dequantizes its band of group s, then runs the
-  // 32 MFMAs with activation fragments read one M tile ahead.
-  issue_w(0);
-  issue_a(0);
-  issue_w(1);
-  issue_a(1);
-  issue_w(2);
-  for (int s = 0; s < Gz; s++) {
-    if (wave == 0) wait_vm_barrier<VPC + 1>();
-    else wait_vm_barrier<VPC>();
-    issue_a(s + 2);
-    issue_w(s + 3);
-    u32x4 bf[4];
-    dequant(s, bf);
-    const uint8_t* ast = aring + (s % kT8NS) * A_BYTES;
+  // Step s: bc (B fragments of s) and cc (codes of s + 1) in registers; dequantizes cc into bn, then reads the codes
+  // of s + 2 into cc (the next barrier waits for them). Four groups, one per M tile, each closed by a scheduling
+  // barrier: the tile's eight MFMAs (two bands), the next tile's activation fragments and a quarter of the dequant.
+  auto step = [&](u32x4 (&bc)[2][4], u32x4 (&bn)[2][4]) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(D) : "memory");
+    issue_a();
+    issue_w();
+    const uint8_t* ast = aring + ca * A_BYTES;
+    float sa[2], sbs[2], bi[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const float sc = bf2f((uint16_t)(cc.sb[nb] & 0xFFFFu));
+      bi[nb] = bf2f((uint16_t)(cc.sb[nb] >> 16)), sa[nb] = t64_sa(sc), sbs[nb] = t64_sb(sc);
+    }
     u32x4 af[2][4];
     load_a(ast, 0, af[0]);
 #pragma unroll
-    for (int a = 0; a < MT; a++) {
-      if (a + 1 < MT) load_a(ast, a + 1, af[(a + 1) & 1]);
+    for (int a = 0; a < 4; a++) {
+      if (a + 1 < 4) load_a(ast, a + 1, af[(a + 1) & 1]);
 #pragma unroll
-      for (int t = 0; t < 4; t++) acc[a] = mfma_bf16(af[a & 1][t], bf[t], acc[a]);
+      for (int k = 0; k < 2; k++) {
+        const int d = 2 * a + k;  // dequant word d: band d / 4, word d % 4
+        bn[d / 4][d % 4] = t64_dequant(cc.w[d / 4][d % 4], sa[d / 4], sbs[d / 4], bi[d / 4]);
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[nb][a] = mfma_bf16(af[a & 1][t], bc[nb][t], acc[nb][a]);
+#pragma unroll
+      for (int m = 0; m < 8; m++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if (m < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) asm volatile("" : "+v"(bn[nb][t]));
+    read_codes(cw2, cc);
+    ca = ca + 1 == kT8NS ? 0 : ca + 1;
+    cw2 = cw2 + 1 == kT8NW ? 0 : cw2 + 1;
+  };
+  int s = 0;
+  for (; s + 1 < Gz; s += 2) {
+    step(bf0, bf1);
+    step(bf1, bf0);
   }
-  wait_vm_barrier<0>();
+  if (s < Gz) step(bf0, bf1);
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
+  // The tile leaves through LDS (free after the K loop) in two halves of 128 rows: the four waves holding a half
+  // stage it as fp32 [128][kT8Row], then all waves store whole rows, 4 columns per access (a split tail: its compact
+  // fp32 partials).
   const bool split = gridDim.y > 1;
-  const int col = (tn * NBB + wave) * 32 + j;
-  if (col >= p.N) return;
+  float* const stg = (float*)lds;
 #pragma unroll
-  for (int a = 0; a < MT; a++)
+  for (int hf = 0; hf < 2; hf++) {
+    if (mh == hf)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = m0 + a * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-      if (row >= p.M) continue;
-      if (split)
-        p.part[(((size_t)blockIdx.y * p.ntail + Lrel) * BM + (row - m0)) * 256 + (col - tn * 256)] = acc[a][r];
-      else
-        store_mode(p.C, (size_t)row * p.ldc + col, acc[a][r], p.mode);
+      for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            stg[(a * 32 + 8 * (r / 4) + 4 * h + (r % 4)) * kT8Row + (2 * bp + nb) * 32 + j] = acc[nb][a][r];
+    __syncthreads();
+    for (int e = tid; e < 128 * 64; e += 512) {
+      const int row = e >> 6, c4 = (e & 63) * 4, lrow = 128 * hf + row, grow = m0 + lrow, gcol = tn * 256 + c4;
+      if (grow >= p.M || gcol >= p.N) continue;
+      const float4 v = *(const float4*)(stg + row * kT8Row + c4);
+      if (split) {
+        *(float4*)(p.part + (((size_t)blockIdx.y * p.ntail + Lrel) * BM + lrow) * 256 + c4) = v;
+        continue;
+      }
+      const size_t o = (size_t)grow * p.ldc + gcol;
+      if (gcol + 4 <= p.N && (o & 3) == 0 && p.mode != 1) {
+        if (p.mode == 2) *(float4*)((float*)p.C + o) = v;
+        else *(u32x2*)((uint16_t*)p.C + o) = u32x2{pack_bf2(v.x, v.y), pack_bf2(v.z, v.w)};
+      } else {
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        for (int k = 0; k < 4 && gcol + k < p.N; k++) store_mode(p.C, o + k, vv[k], p.mode);
+      }
     }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(512, 1) void k_gemm_t8(GemmT8Args p) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int Lrel = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  t8_tile(p.tile0 + Lrel, p.tiles_m, p.tiles_n, tm, tn);
+  if (wave == 0) t8_body<true>(p, lds, wave, Lrel, tm, tn);
+  else t8_body<false>(p, lds, wave, Lrel, tm, tn);
 }
 
 // C (mode) = the split sum of the compact tail partials, 4 columns per thread, in split order.
@@ -212,7 +318,8 @@ int launch_gemm_t8(const uint16_t* A, int lda, const void* wt, int N, int K, voi
   const size_t need = gemm_t8_workspace(M, N, K);
   if (need > ws_bytes || (need && !ws))
     return fail(IFD_ERR_WORKSPACE, "gemm_t8 needs %zu bytes of workspace, got %zu", need, ws_bytes);
-  constexpr size_t lds = (size_t)kT8NS * 256 * 128 + (size_t)kT8NW * (8 * kT64Codes + 8 * 128);
+  constexpr size_t ring = (size_t)kT8NS * 256 * 128 + (size_t)kT8NW * (8 * kT64Codes + 8 * 128);
+  constexpr size_t lds = ring > (size_t)128 * kT8Row * 4 ? ring : (size_t)128 * kT8Row * 4;  // ring, then half a tile
   static bool attr = false;
   if (!attr) {
     hipFuncSetAttribute((const void*)k_gemm_t8, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -220,12 +327,15 @@ int launch_gemm_t8(const uint16_t* A, int lda, const void* wt, int N, int K, voi
   }
   const int tiles_m = (M + 255) / 256, tiles_n = (t64_bands(N) + 7) / 8;
   const int G = K / kGroup;
-  GemmT8Args p{A, lda, (const uint8_t*)wt, N, K, C, ldc, M, mode, (float*)ws, G, tiles_m, tiles_n, 0, 0};
+  if (t64_bytes(N, K) >= ((size_t)1 << 31) || (size_t)M * lda * 2 >= ((size_t)1 << 31))
+    return fail(IFD_ERR_UNSUPPORTED, "gemm_t8: operands past 2 GiB");
+  const uint32_t wb = (uint32_t)t64_bytes(N, K);
+  GemmT8Args p{A, lda, (const uint8_t*)wt, wb, N, K, C, ldc, M, mode, (float*)ws, G, tiles_m, tiles_n, 0, 0};
   hipLaunchKernelGGL(k_gemm_t8, dim3(pl.full, 1), dim3(512), lds, st, p);
   IFD_TRY(check_launch("gemm_t8"));
   if (!pl.St) return IFD_OK;
   const int ntail = pl.tiles - pl.full;
-  GemmT8Args q{A, lda, (const uint8_t*)wt, N, K, C, ldc, M, mode, (float*)ws, pl.gpt, tiles_m, tiles_n, pl.full,
+  GemmT8Args q{A, lda, (const uint8_t*)wt, wb, N, K, C, ldc, M, mode, (float*)ws, pl.gpt, tiles_m, tiles_n, pl.full,
                ntail};
   hipLaunchKernelGGL(k_gemm_t8, dim3(ntail, pl.St), dim3(512), lds, st, q);
   IFD_TRY(check_launch("gemm_t8 tail"));
