@@ -82,7 +82,7 @@ __device__ __forceinline__ void sk_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint
 
 // The pipeline of one wave; W0: wave 0, which also issues the (s, b) rows. Its DMA stream is a sequence of pairs
 // (A(s), W(s + 1)), s = 0, 1, ...: the prologue issues W(0) and pairs 0 .. R - 2, step i pair R - 1 + i, past the
-// run's end too (re-reading the last tile), so the waits are constants: at step i the wave reads A(i + 1)'s
+// run's end too (re-reading its last unit), so the waits are constants: at step i the wave reads A(i + 1)'s
 // fragments and W(i + 2)'s codes, the second of pair i + 1, which R - 3 younger pairs follow. Stage j % R holds A(j)
 // and W(j); step i overwrites A(i - 1) and W(i), both read two steps earlier.
 template <int MT, bool W0>
@@ -144,25 +144,29 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
     sk_dma(rw, st + (2 * wave + 1) * kT64Codes, vw[1], w_so);
     if constexpr (W0) sk_dma(rw, st + 8 * kT64Codes, vw[2], w_so);
   };
-  auto advance = [&]() __attribute__((always_inline)) {
+  // Past the run's last unit a stream stays on it: the extra DMAs re-read that unit (L2 hits), never new bytes.
+  int a_left = n - 1, w_left = n - 1;  // advances left before a stream reaches the run's last unit
+  auto advance_a = [&]() __attribute__((always_inline)) {
+    if (a_left <= 0) return;
+    a_left--;
     a_so += 2u * kGroup;
-    if (++a_g == G) {  // next tile; past the run's last one the stream re-reads it
+    if (++a_g == G) {  // next tile
       a_g = 0, a_so = 0;
-      if (a_t < tile_last) a_tile(++a_t);
-    }
-    w_so += gstride;
-    if (++w_g == G) {
-      w_g = 0, w_so = 0;
-      if (w_t < tile_last) w_tile(++w_t);
+      a_tile(++a_t);
     }
   };
-  // W(0) alone: the weight stream's advance only
   auto advance_w = [&]() __attribute__((always_inline)) {
+    if (w_left <= 0) return;
+    w_left--;
     w_so += gstride;
     if (++w_g == G) {
       w_g = 0, w_so = 0;
-      if (w_t < tile_last) w_tile(++w_t);
+      w_tile(++w_t);
     }
+  };
+  auto advance = [&]() __attribute__((always_inline)) {
+    advance_a();
+    advance_w();
   };
 
   // LDS reads one step ahead of their use

@@ -83,8 +83,8 @@ __device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, void* lds, uint
 //   D (NW - 4) younger DMAs.
 // DMA loads retire from vmcnt in issue order. The output stores of an item end are not counted: a store may retire
 // before an older load, so counting it could release a wait early, while an uncounted store still in flight only
-// makes the wait longer. The streams run on past the last step (re-reading the last item) so that the steady counts
-// hold to the end; the kernel drains vmcnt before it exits.
+// makes the wait longer. The streams run on past the last step (re-reading it) so that the steady counts hold to the
+// end; the kernel drains vmcnt before it exits.
 template <int MT, bool SILU, bool WIDE, int ROLE>
 __device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int wave, const int it0, const int it1) {
   constexpr bool TWO = SILU || WIDE;
@@ -132,7 +132,7 @@ __device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int
   const uint32_t nrec = AW ? p.a_bytes : (uint32_t)p.ebytes;
   uint32_t voff[D];
   const uint32_t gstep = AW ? 2u * kGroup : gstride;
-  int s_item = it0, s_g = 0, s_st = 0;
+  int s_item = it0, s_g = 0, s_st = 0, s_left = (it1 - it0) * G - 1;
   uint32_t soff = 0;
   auto stream_item = [&](int item) __attribute__((always_inline)) {
     int e, c, q0, q1;
@@ -193,12 +193,13 @@ __device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int
       if constexpr (ROLE == 1) bdma16(rsrc, st + SB_OFF + sbj * 1024, voff[NCW], soff);
     }
     s_st = s_st + 1 == NR ? 0 : s_st + 1;
+    if (s_left <= 0) return;  // past the run's last step: re-read it (L2 hits), never new bytes
+    s_left--;
     soff += gstep;
-    if (++s_g == G) {  // next item; past the last one the stream re-reads it
+    if (++s_g == G) {  // next item
       s_g = 0;
       soff = 0;
-      if (s_item + 1 < it1) s_item++;
-      stream_item(s_item);
+      stream_item(++s_item);
     }
   };
 
