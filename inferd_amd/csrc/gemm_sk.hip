@@ -69,6 +69,12 @@ struct GemmSkArgs {
   uint32_t part_bytes;
   int tiles_m, tiles_n, G, nblk;
   int swi;  // SwiGLU mode: bands per half (N / 64); 0 otherwise
+  // k_sk_fixup only: the stream-K tiles are tiles tile0 .. tile0 + ntiles - 1 of the tile order, and each output row
+  // is scaled by rs[row * rs_stride] before its store (rs null: no scale)
+  int tile0, ntiles;
+  const float* rs;
+  int rs_stride;
+  int sparse;  // more blocks than units: some runs are empty
 };
 
 // the block whose run holds unit u
@@ -400,43 +406,59 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
 
 // Sum of a cut tile's pieces (partial slots, in unit order) and its store. Block (tile, w, f): one wave over the
 // float4 fragment f = (a, q) of column band w of the tile (SwiGLU: gate band w with up band w + 4, giving h), the
-// loads of up to kFixBatch pieces in flight at once; whole tiles were stored by k_gemm_sk.
+// loads of up to kFixBatch pieces in flight at once; whole tiles were stored by the GEMM kernel. blockIdx.x is the
+// tile's index among the stream-K tiles (units [tile G, tile G + G) of their U = ntiles G).
 constexpr int kFixBatch = 8;
 template <int MT>
 __global__ __launch_bounds__(64) void k_sk_fixup(GemmSkArgs p) {
   constexpr int BM = 32 * MT, NE = MT * 16;
   const int tile = blockIdx.x, w = blockIdx.y, a = blockIdx.z / 4, q = blockIdx.z % 4;
   const int lane = threadIdx.x, j = lane & 31, h = lane >> 5;
-  const int G = p.G;
-  const long U = (long)p.tiles_m * p.tiles_n * G;
-  const long tlo = (long)tile * G;
-  const int bf = sk_block_of(tlo, p.nblk, U), bl = sk_block_of(tlo + G - 1, p.nblk, U);
+  // run boundaries in 32-bit arithmetic (the host keeps U nblk below 2^32): block bb's run starts at unit
+  // bb U / nblk, and unit u lies in the run of block (u nblk + nblk - 1) / U
+  const uint32_t G = (uint32_t)p.G, U = (uint32_t)p.ntiles * G, nb = (uint32_t)p.nblk;
+  const uint32_t tlo = (uint32_t)tile * G;
+  const int bf = (int)((tlo * nb + nb - 1) / U), bl = (int)(((tlo + G - 1) * nb + nb - 1) / U);
   if (bf == bl) return;
+  // Block bf holds the tile's first unit: the tile is its second segment (slot 2 bf + 1) when its run starts
+  // before the tile, else its first (slot 2 bf). Every later block's run starts inside the tile, which is its first
+  // segment (slot 2 bb). With more blocks than units (sparse) some of those runs are empty and hold no piece.
+  const uint32_t lo_f = (uint32_t)bf * U / nb;
   const float4* part = (const float4*)p.part;
-  auto sum = [&](int wv) __attribute__((always_inline)) {
-    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int b0 = bf; b0 <= bl; b0 += kFixBatch) {
-      float4 x[kFixBatch];
+  const int w1 = p.swi ? w + 4 : w;  // SwiGLU: the up band's pieces, loaded beside the gate band's
+  float4 t0 = make_float4(0.f, 0.f, 0.f, 0.f), t1 = t0;
+  for (int b0 = bf; b0 <= bl; b0 += kFixBatch) {
+    float4 x0[kFixBatch], x1[kFixBatch];
+    bool has[kFixBatch];
 #pragma unroll
-      for (int k = 0; k < kFixBatch; k++) {
-        const int bb = b0 + k;
-        if (bb <= bl) {
-          const int slot = 2 * bb + ((long)bb * U / p.nblk < tlo ? 1 : 0);
-          x[k] = part[(((size_t)slot * 8 + wv) * NE / 4 + a * 4 + q) * 64 + lane];
-        }
+    for (int k = 0; k < kFixBatch; k++) {
+      const int bb = b0 + k;
+      has[k] = bb <= bl;
+      if (has[k] && p.sparse && bb > bf) has[k] = (uint32_t)(bb + 1) * U / nb > (uint32_t)bb * U / nb;
+      if (has[k]) {
+        const int slot = 2 * bb + (bb == bf && lo_f < tlo ? 1 : 0);
+        x0[k] = part[(((size_t)slot * 8 + w) * NE / 4 + a * 4 + q) * 64 + lane];
+        if (p.swi) x1[k] = part[(((size_t)slot * 8 + w1) * NE / 4 + a * 4 + q) * 64 + lane];
       }
-#pragma unroll
-      for (int k = 0; k < kFixBatch; k++)
-        if (b0 + k <= bl) t.x += x[k].x, t.y += x[k].y, t.z += x[k].z, t.w += x[k].w;
     }
-    return t;
-  };
-  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
-  const float4 v = sum(w);
-  const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < kFixBatch; k++)
+      if (has[k]) {
+        t0.x += x0[k].x, t0.y += x0[k].y, t0.z += x0[k].z, t0.w += x0[k].w;
+        if (p.swi) t1.x += x1[k].x, t1.y += x1[k].y, t1.z += x1[k].z, t1.w += x1[k].w;
+      }
+  }
+  const int tm = (p.tile0 + tile) % p.tiles_m, tn = (p.tile0 + tile) / p.tiles_m;
+  const float4 v = t0;
+  float vv[4] = {v.x, v.y, v.z, v.w};
   const int row0 = tm * BM + a * 32 + 8 * q + 4 * h;
+  if (p.rs) {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      if (row0 + e < p.M) vv[e] *= p.rs[(size_t)(row0 + e) * p.rs_stride];
+  }
   if (p.swi) {
-    const float4 u4 = sum(w + 4);
+    const float4 u4 = t1;
     const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
     const int col = (4 * tn + w) * 32 + j;
 #pragma unroll
@@ -453,16 +475,6 @@ __global__ __launch_bounds__(64) void k_sk_fixup(GemmSkArgs p) {
 }
 
 // ---- host side
-
-static int cu_count() {
-  static int n = 0;
-  if (!n) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-  }
-  return n;
-}
 
 struct SkPlan {
   int MT, tiles_m, tiles_n, G, nblk;
@@ -491,6 +503,7 @@ bool gemm_sk_applies(int M, int N, int K, int mode) {
   if (M <= 16 || K % kGroup || t64_bytes(N, K) >= ((size_t)1 << 31)) return false;
   if (mode == kModeSwiglu && N % 256) return false;
   const SkPlan pl = gemm_sk_plan(M, N, K);
+  if (((uint64_t)pl.tiles_m * pl.tiles_n * pl.G + 1) * (pl.nblk + 1) >= ((uint64_t)1 << 32)) return false;  // fixup
   return (long)pl.tiles_m * pl.tiles_n * 3 >= cu_count() || (M > 64 && M <= 128);
 }
 
@@ -511,8 +524,19 @@ static int launch_sk_cfg(const GemmSkArgs& a, bool fixup, hipStream_t st) {
   hipLaunchKernelGGL(k_gemm_sk<MT>, dim3(a.nblk), dim3(kSkThreads), lds, st, a);
   IFD_TRY(check_launch("gemm_sk"));
   if (!fixup) return IFD_OK;
-  hipLaunchKernelGGL(k_sk_fixup<MT>, dim3(a.tiles_m * a.tiles_n, a.swi ? 4 : 8, MT * 4), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(k_sk_fixup<MT>, dim3(a.ntiles, a.swi ? 4 : 8, MT * 4), dim3(64), 0, st, a);
   return check_launch("gemm_sk fixup");
+}
+
+int launch_sk_fixup_rows(const float* part, int tiles_m, int tiles_n, int tile0, int ntiles, int G, int nblk, void* C,
+                         int ldc, int M, int N, int mode, const float* rs, int rs_stride, hipStream_t st) {
+  GemmSkArgs a{};
+  a.part = (float*)part;
+  a.tiles_m = tiles_m, a.tiles_n = tiles_n, a.tile0 = tile0, a.ntiles = ntiles, a.G = G, a.nblk = nblk;
+  a.C = C, a.ldc = ldc, a.M = M, a.N = N, a.mode = mode, a.rs = rs, a.rs_stride = rs_stride;
+  a.sparse = (long)ntiles * G < nblk;
+  hipLaunchKernelGGL(k_sk_fixup<4>, dim3(ntiles, 8, 16), dim3(64), 0, st, a);
+  return check_launch("sk fixup");
 }
 
 int launch_gemm_sk(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
@@ -532,7 +556,7 @@ int launch_gemm_sk(const uint16_t* A, int lda, const void* wt, int N, int K, voi
   for (long t = 0; t < tiles && !fixup; t++)
     fixup = sk_block_of(t * pl.G + pl.G - 1, pl.nblk, U) != sk_block_of(t * pl.G, pl.nblk, U);
   GemmSkArgs a{A, lda, (const uint8_t*)wt, (uint32_t)t64_bytes(N, K), N, K, C, ldc, M, mode, (float*)ws, (uint32_t)need,
-               pl.tiles_m, pl.tiles_n, pl.G, pl.nblk, mode == kModeSwiglu ? N / 64 : 0};
+               pl.tiles_m, pl.tiles_n, pl.G, pl.nblk, mode == kModeSwiglu ? N / 64 : 0, 0, (int)tiles, nullptr, 0, 0};
   if (pl.MT == 1) return launch_sk_cfg<1>(a, fixup, st);
   if (pl.MT == 2) return launch_sk_cfg<2>(a, fixup, st);
   return launch_sk_cfg<4>(a, fixup, st);

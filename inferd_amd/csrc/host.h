@@ -28,6 +28,16 @@ inline int check_launch(const char* what) {
 }
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+// compute units of the current device (256 on MI355X), read once
+inline int cu_count() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  }
+  return n;
+}
 
 #define IFD_CHECK(cond, ...)                      \
   do {                                            \

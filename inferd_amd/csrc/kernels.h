@@ -82,6 +82,10 @@ bool gemm_sk_applies(int M, int N, int K, int mode);
 size_t gemm_sk_workspace(int M, int N, int K, int mode);
 int launch_gemm_sk(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                    void* ws, size_t ws_bytes, hipStream_t st);
+// The fixup of a 128-row-tile stream-K split (gemm_sk.hip): sums the pieces of the cut tiles among the stream-K
+// tiles tile0 .. tile0 + ntiles - 1, scales row m by rs[m rs_stride] (rs null: no scale) and stores them.
+int launch_sk_fixup_rows(const float* part, int tiles_m, int tiles_n, int tile0, int ntiles, int G, int nblk, void* C,
+                         int ldc, int M, int N, int mode, const float* rs, int rs_stride, hipStream_t st);
 // W4A8 on T64 weights, per-token int8 activations (U [M][K], XS [M][G][2] from a8_quant).
 size_t w4a8_t_workspace(int M, int N, int K);
 int launch_w4a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M, int mode,

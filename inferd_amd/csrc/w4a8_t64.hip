@@ -311,11 +311,6 @@ static size_t wa_part_bytes(const WaPlan& pl, int M, int N) {
   return 0;
 }
 
-size_t w4a8_t_workspace(int M, int N, int K) {
-  const WaPlan pl = w4a8_t_plan(M, N, K);
-  return xprep_bytes(M, K) + wa_part_bytes(pl, M, N);
-}
-
 // C (mode) = the split sum of the compact tail partials, 4 columns per thread, in split order.
 __global__ __launch_bounds__(256) void k_wa_tail_reduce(const float* __restrict__ part, int St, int ntail, int tile0,
                                                          int tiles_m, int tiles_n, int BM, int M, int N, void* C,
@@ -336,6 +331,356 @@ __global__ __launch_bounds__(256) void k_wa_tail_reduce(const float* __restrict_
   for (int k = 0; k < 4 && col + k < N; k++) store_mode(C, (size_t)row * ldc + col + k, vv[k], mode);
 }
 
+// ---- W4A8 stream-K for M > 64: 128-row tiles, every CU an equal share of the (tile, group) units ----------------
+//
+// Work is the set of units (tile, 64-group), tile = 128 rows x 8 bands (256 columns). With T tiles over nblk blocks
+// (one per CU), the first q nblk = (T / nblk) nblk tiles are whole-tile work: block b takes tiles b q .. b q + q - 1.
+// The other nsk = T % nblk tiles are split stream-K: block b takes their units [b U / nblk, (b + 1) U / nblk),
+// U = nsk G, first. A run is that share (at most two segments, each a piece of its tile unless it covers the whole
+// tile) followed by the block's whole tiles, streamed as one sequence of steps. Pieces go to the block's two
+// partial slots (unscaled fp32 sums in MFMA fragment order); k_sk_fixup sums each cut tile's pieces in unit order,
+// applies the row scale sx and stores the tile.
+//
+// Block: 8 waves, two per SIMD; wave w owns band w over the 4 M tiles. Per step, for M tile a: two
+// v_mfma_i32_32x32x32_i8 give the group's exact P, acc += s float(P) (two VALU per accumulator, the floor of a
+// per-group-scaled integer product), and the bias term b X_g enters acc through one bf16 MFMA whose only non-zero
+// k entries are X_g = hi + lo (two exact bf16 parts) against (b, b). So the group's whole contribution
+// s P + b X is added per step and a segment can end at any group.
+// One LDS ring of kWsR stages filled by direct global -> LDS DMA; a stage holds a group's int8 activation slab
+// [128][64] (16-byte columns XOR-swizzled by row quad), the 8 bands' code halves, their (s, b) rows and the X pairs
+// of the 128 rows in 16-byte slots (from k_w4a8_xprep_t). Every wave issues its slab rows and its band's codes;
+// wave 0 also the (s, b) rows and the first 64 rows' X pairs, wave 1 the other 64 rows' X pairs. They are buffer
+// loads with a scalar group offset; each role's code is compiled on its own, so every wait is a constant. The stream
+// keeps issuing past the run's last unit (re-reading it) so that the count holds to the last step.
+constexpr int kWsR = 8;
+constexpr int kWsA = 128 * 64;
+constexpr int kWsC = 8 * kT64Codes;
+constexpr int kWsSB = 1024;
+constexpr int kWsX = 2048;
+constexpr int kWsStage = kWsA + kWsC + kWsSB + kWsX;
+constexpr int kWsRow = 256 + 4;  // staged tile row stride (floats)
+constexpr size_t kWsLds = (size_t)kWsR * kWsStage > (size_t)128 * kWsRow * 4 ? (size_t)kWsR * kWsStage
+                                                                               : (size_t)128 * kWsRow * 4;
+static_assert(kWsLds <= 160 * 1024, "LDS plan");
+
+struct W4A8SkArgs {
+  const int8_t* U;       // [M][K]
+  const float* XS;       // [M][G][2]
+  const u32x4* Xt;       // [G][Mx]: (X pair (bf16 hi | bf16 lo << 16), 0, 0, 0), rows past M zero
+  int Mx;
+  const uint8_t* wt;
+  uint32_t w_bytes, u_bytes, x_bytes;
+  int N, K;
+  void* C;
+  int ldc, M, mode;
+  float* part;
+  uint32_t part_bytes;
+  int tiles_m, tiles_n, G, nblk;
+  int q, tile0, nsk;  // whole tiles per block; the stream-K tiles tile0 .. tile0 + nsk - 1
+};
+
+// X_g of (row, group) as an exact bf16 pair: hi = 256 floor(X / 256), lo = X - hi; Xt[g][m] = (pair, 0, 0, 0), zero
+// for m >= M. The pair sits in a 16-byte slot that the kernel reads as a whole MFMA operand.
+__global__ __launch_bounds__(256) void k_w4a8_xprep_t(const float* __restrict__ XS, int M, int G, int Mx,
+                                                      u32x4* __restrict__ Xt) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)G * Mx) return;
+  const int g = (int)(i / Mx), m = (int)(i % Mx);
+  uint32_t v = 0;
+  if (m < M) {
+    const float x = rintf(XS[((size_t)m * G + g) * 2 + 1] / XS[((size_t)m * G + g) * 2]);
+    const float hi = floorf(x * (1.f / 256.f)) * 256.f;
+    v = (uint32_t)f2bf(hi) | (uint32_t)f2bf(x - hi) << 16;
+  }
+  Xt[i] = u32x4{v, 0u, 0u, 0u};
+}
+
+__device__ __forceinline__ void ws_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, (int)voff, (int)soff, 0, 0);
+}
+
+// ROLE 0: wave 0 (also the (s, b) rows and X pairs of rows 0-63), 1: wave 1 (X pairs of rows 64-127), 2: waves 2-7.
+template <int ROLE>
+__device__ __forceinline__ void ws_body(const W4A8SkArgs& p, uint8_t* lds, const int wave, const int b) {
+  constexpr int R = kWsR, D = ROLE == 0 ? 4 : ROLE == 1 ? 3 : 2;
+  static_assert(R >= 4 && (R - 2) * D <= 63, "ring depth, vmcnt range");
+  float* const stg = (float*)lds;  // staged tile [128][kWsRow], after the K loop
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int j = lane & 31, h = lane >> 5;
+  const int G = p.G;
+  const long Usk = (long)p.nsk * G;
+  const int ur0 = (int)((long)b * Usk / p.nblk), ur1 = (int)((long)(b + 1) * Usk / p.nblk);
+  const int nr = ur1 - ur0, n = nr + p.q * G;
+  const int nbands = t64_bands(p.N);
+  const uint32_t gstride = (uint32_t)nbands * kT64Tile;
+
+  // unit i of the run -> (tile, group)
+  auto unit = [&](int i, int& tile, int& g) __attribute__((always_inline)) {
+    if (i < nr) {
+      tile = p.tile0 + (ur0 + i) / G, g = (ur0 + i) % G;
+    } else {
+      tile = b * p.q + (i - nr) / G, g = (i - nr) % G;
+    }
+  };
+
+  const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc((void*)p.U, 0, (int)p.u_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.wt, 0, (int)p.w_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.Xt, 0, (int)p.x_bytes, 0x00020000);
+
+  // ---- the DMA stream: per-lane offsets of the current tile, the group in a scalar
+  uint32_t va, vw, v3 = 0, vx = 0;
+  auto set_tile = [&](int tile) __attribute__((always_inline)) {
+    const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+    const int r = 16 * wave + lane / 4;  // slab row of this lane's 16 bytes
+    va = (uint32_t)min(tm * 128 + r, p.M - 1) * (uint32_t)p.K + 16u * ((lane & 3) ^ ((r >> 2) & 3));
+    vw = (uint32_t)min(8 * tn + wave, nbands - 1) * kT64Tile + 16u * lane;
+    if constexpr (ROLE == 0) v3 = (uint32_t)min(8 * tn + lane / 8, nbands - 1) * kT64Tile + kT64Codes + 16u * (lane & 7);
+    vx = (uint32_t)(tm * 128 + 64 * ROLE) * 16u + 16u * lane;
+  };
+  int s_i = 0, s_tile, s_g;
+  unit(0, s_tile, s_g);
+  set_tile(s_tile);
+  auto issue = [&](int slot) __attribute__((always_inline)) {
+    uint8_t* st = lds + slot * kWsStage;
+    ws_dma(ru, st + wave * 1024, va, (uint32_t)s_g * 64u);
+    ws_dma(rw, st + kWsA + wave * 1024, vw, (uint32_t)s_g * gstride);
+    if constexpr (ROLE == 0) ws_dma(rw, st + kWsA + kWsC, v3, (uint32_t)s_g * gstride);
+    if constexpr (ROLE < 2) ws_dma(rx, st + kWsA + kWsC + kWsSB + ROLE * 1024, vx, (uint32_t)s_g * (uint32_t)p.Mx * 16u);
+  };
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (s_i >= n - 1) return;  // past the run's last unit the stream re-reads it
+    s_i++;
+    if (++s_g == G || s_i == nr) {
+      unit(s_i, s_tile, s_g);
+      set_tile(s_tile);
+    }
+  };
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int a = 0; a < 4; a++) acc[a] = zero16();
+
+  // The operands of one step, read from its stage one step ahead of their use.
+  struct Ops {
+    u32x4 a[4][2];   // activation fragments of the 4 M tiles (k = 32 h + 16 s2 + 0..15 at index s2)
+    u32x4 bq[2];     // the band's B fragments (words 2 s2, 2 s2 + 1 of the lane's codes)
+    float sc;        // the column's scale
+    uint32_t bb;     // (b, b) for the lanes h = 0, else 0
+    u32x4 xv[4];     // (the X pair of row a 32 + j, 0, 0, 0)
+  };
+  auto read_a = [&](const uint8_t* st, int a, Ops& o) __attribute__((always_inline)) {
+    const int r = a * 32 + j;
+    o.a[a][0] = *(const u32x4*)(st + r * 64 + 16 * ((2 * h) ^ ((r >> 2) & 3)));
+    o.a[a][1] = *(const u32x4*)(st + r * 64 + 16 * ((2 * h + 1) ^ ((r >> 2) & 3)));
+    o.xv[a] = *(const u32x4*)(st + kWsA + kWsC + kWsSB + 16 * r);
+  };
+  auto finish = [&](const u32x4 codes, const uint32_t sb, Ops& o) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++) {
+      uint32_t d[4];
+      t64_bytes(codes[2 * s2], d[0], d[1]);
+      t64_bytes(codes[2 * s2 + 1], d[2], d[3]);
+      o.bq[s2] = u32x4{d[0], d[1], d[2], d[3]};
+    }
+    o.sc = bf2f((uint16_t)(sb & 0xFFFFu));
+    o.bb = h ? 0u : ((sb >> 16) | (sb & 0xFFFF0000u));
+  };
+  auto read_all = [&](int slot, Ops& o) __attribute__((always_inline)) {
+    const uint8_t* st = lds + slot * kWsStage;
+    const u32x4 codes = *(const u32x4*)(st + kWsA + wave * 1024 + 16 * lane);
+    const uint32_t sb = *(const uint32_t*)(st + kWsA + kWsC + wave * 128 + 4 * j);
+#pragma unroll
+    for (int a = 0; a < 4; a++) read_a(st, a, o);
+    finish(codes, sb, o);
+  };
+
+  // Step i: cu holds step i's operands. Waits for stage i + 1 (R - 3 younger stages in flight), issues stage
+  // i + R - 1 into the stage read at step i - 1, then per M tile a: the two i8 MFMAs of P, the bias MFMA (X_hi b +
+  // X_lo b at k = 0, 1), step i + 1's fragments of tile a, and the epilogue of tile a - 1 (P double-buffered).
+  auto step = [&](int i, Ops& cu, Ops& nx) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 3) * D) : "memory");
+    const int slot = i % R;
+    issue(slot == 0 ? R - 1 : slot - 1);
+    advance();
+    const uint8_t* st = lds + (slot + 1 == R ? 0 : slot + 1) * kWsStage;
+    const u32x4 codes = *(const u32x4*)(st + kWsA + wave * 1024 + 16 * lane);
+    const uint32_t sb = *(const uint32_t*)(st + kWsA + kWsC + wave * 128 + 4 * j);
+    const u32x4 xb = {cu.bb, 0u, 0u, 0u};
+    i32x16 P[2];
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+      P[a & 1] = mfma_i8(cu.a[a][0], cu.bq[0], izero16());
+      P[a & 1] = mfma_i8(cu.a[a][1], cu.bq[1], P[a & 1]);
+      acc[a] = mfma_bf16(cu.xv[a], xb, acc[a]);
+      read_a(st, a, nx);
+      if (a > 0) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[a - 1][e] = __builtin_fmaf(cu.sc, (float)P[(a - 1) & 1][e], acc[a - 1][e]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc[3][e] = __builtin_fmaf(cu.sc, (float)P[1][e], acc[3][e]);
+    finish(codes, sb, nx);
+  };
+
+  // prologue: stages 0 .. R - 2 issued, stage 0 read
+#pragma unroll
+  for (int k = 0; k < R - 1; k++) {
+    issue(k);
+    advance();
+  }
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((R - 2) * D) : "memory");
+  Ops o0, o1;
+  read_all(0, o0);
+
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.part, 0, (int)p.part_bytes, 0x00020000);
+  auto write_slot = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+      for (int qq = 0; qq < 4; qq++) {
+        const u32x4 x = {__float_as_uint(acc[a][4 * qq]), __float_as_uint(acc[a][4 * qq + 1]),
+                         __float_as_uint(acc[a][4 * qq + 2]), __float_as_uint(acc[a][4 * qq + 3])};
+        const int off = (((slot * 8 + wave) * 16 + a * 4 + qq) * 64 + lane) * 16;
+        __builtin_amdgcn_raw_buffer_store_b128(x, rs, off, 0, 0);
+      }
+  };
+  // a whole tile in the middle of the run: its rows scaled and stored from the fragments
+  auto store_direct = [&](int tile) __attribute__((always_inline)) {
+    const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+    const int col = (8 * tn + wave) * 32 + j;
+    if (col >= p.N) return;
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int row = tm * 128 + a * 32 + 8 * (e / 4) + 4 * h + (e % 4);
+        if (row < p.M) store_mode(p.C, (size_t)row * p.ldc + col, p.XS[(size_t)row * G * 2] * acc[a][e], p.mode);
+      }
+  };
+
+  // segments: the stream-K share (pieces, unless a segment covers its whole tile), then the whole tiles
+  int i = 0, piece = 0, tile = 0;
+  bool whole = false;
+  for (;;) {
+    int g;
+    unit(i, tile, g);
+    const int len = i < nr ? min(G - g, nr - i) : G;
+    int k = i;
+    for (; k + 1 < i + len; k += 2) {
+      step(k, o0, o1);
+      step(k + 1, o1, o0);
+    }
+    if (k < i + len) {
+      step(k, o0, o1);
+      o0 = o1;
+    }
+    i += len;
+    whole = len == G;
+    if (i >= n) break;
+    if (whole) {
+      store_direct(tile);
+    } else {
+      write_slot(2 * b + piece);
+      piece++;
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) acc[a] = zero16();
+  }
+  // every DMA (the stream ran on past the end) and piece store has landed; LDS is free once all waves are here
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (!whole) {
+    write_slot(2 * b + piece);
+    return;
+  }
+  // the last whole tile, staged through LDS and stored as rows
+#pragma unroll
+  for (int a = 0; a < 4; a++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) stg[(a * 32 + 8 * (e / 4) + 4 * h + (e % 4)) * kWsRow + 32 * wave + j] = acc[a][e];
+  __syncthreads();
+  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+  for (int e = tid; e < 128 * 64; e += 512) {
+    const int row = e >> 6, c4 = (e & 63) * 4, grow = tm * 128 + row, gcol = tn * 256 + c4;
+    if (grow >= p.M || gcol >= p.N) continue;
+    const float sx = p.XS[(size_t)grow * G * 2];
+    const float4 v4 = *(const float4*)(stg + row * kWsRow + c4);
+    const float sv[4] = {sx * v4.x, sx * v4.y, sx * v4.z, sx * v4.w};
+    const size_t o = (size_t)grow * p.ldc + gcol;
+    if (gcol + 4 <= p.N && (o & 3) == 0 && p.mode != 1) {
+      if (p.mode == 2) *(float4*)((float*)p.C + o) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+      else *(u32x2*)((uint16_t*)p.C + o) = u32x2{pack_bf2(sv[0], sv[1]), pack_bf2(sv[2], sv[3])};
+    } else {
+      for (int k = 0; k < 4 && gcol + k < p.N; k++) store_mode(p.C, o + k, sv[k], p.mode);
+    }
+  }
+}
+
+__global__ __launch_bounds__(512, 1) void k_w4a8_sk(W4A8SkArgs p) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = xcd_remap(blockIdx.x, p.nblk);
+  if (wave == 0) ws_body<0>(p, lds, wave, b);
+  else if (wave == 1) ws_body<1>(p, lds, wave, b);
+  else ws_body<2>(p, lds, wave, b);
+}
+
+// Stream-K plan: q whole tiles per block, the last T % nblk tiles split over the blocks
+struct WsPlan {
+  int tiles_m, tiles_n, G, nblk, q, tile0, nsk, Mx;
+};
+static WsPlan w4a8_sk_plan(int M, int N, int K) {
+  WsPlan pl{};
+  pl.tiles_m = (M + 127) / 128;
+  pl.tiles_n = (t64_bands(N) + 7) / 8;
+  pl.G = K / kGroup;
+  pl.Mx = pl.tiles_m * 128;
+  const int tiles = pl.tiles_m * pl.tiles_n, cus = cu_count();
+  pl.q = tiles / cus;
+  pl.nsk = tiles - pl.q * cus;
+  pl.tile0 = pl.q * cus;
+  // with no whole tiles, never more blocks than units
+  pl.nblk = pl.q ? cus : std::min(cus, pl.nsk * pl.G);
+  return pl;
+}
+static bool w4a8_sk_applies(int M) { return M > 64; }
+static size_t ws_xt_bytes(const WsPlan& pl) { return align_up((size_t)pl.G * pl.Mx * 16, 256); }
+static size_t ws_part_bytes(const WsPlan& pl) { return pl.nsk ? (size_t)2 * pl.nblk * 8 * 16 * 64 * 16 : 0; }
+
+static int launch_w4a8_sk(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M,
+                          int mode, void* ws, hipStream_t st) {
+  const WsPlan pl = w4a8_sk_plan(M, N, K);
+  if (t64_bytes(N, K) >= ((size_t)1 << 31) || (size_t)M * K >= ((size_t)1 << 31) ||
+      ws_xt_bytes(pl) >= ((size_t)1 << 31) || ws_part_bytes(pl) >= ((size_t)1 << 31) ||
+      ((uint64_t)pl.nsk * pl.G + 1) * (pl.nblk + 1) >= ((uint64_t)1 << 32))
+    return fail(IFD_ERR_UNSUPPORTED, "w4a8_t64: operands past 2 GiB");
+  u32x4* Xt = (u32x4*)ws;
+  float* part = (float*)((char*)ws + ws_xt_bytes(pl));
+  const size_t nx = (size_t)pl.G * pl.Mx;
+  hipLaunchKernelGGL(k_w4a8_xprep_t, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, st, XS, M, pl.G, pl.Mx, Xt);
+  IFD_TRY(check_launch("w4a8_xprep_t"));
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)k_w4a8_sk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWsLds);
+    attr = true;
+  }
+  W4A8SkArgs a{U, XS, Xt, pl.Mx, (const uint8_t*)wt, (uint32_t)t64_bytes(N, K), (uint32_t)((size_t)M * K),
+               (uint32_t)(nx * 16), N, K, C, ldc, M, mode, part, (uint32_t)ws_part_bytes(pl), pl.tiles_m, pl.tiles_n,
+               pl.G, pl.nblk, pl.q, pl.tile0, pl.nsk};
+  hipLaunchKernelGGL(k_w4a8_sk, dim3(pl.nblk), dim3(512), kWsLds, st, a);
+  IFD_TRY(check_launch("w4a8_sk"));
+  if (!pl.nsk) return IFD_OK;
+  // the fixup runs when some stream-K tile is cut between blocks
+  const long U2 = (long)pl.nsk * pl.G;
+  bool cut = false;
+  for (long t = 0; t < pl.nsk && !cut; t++)
+    cut = (t * pl.G * pl.nblk + pl.nblk - 1) / U2 != ((t * pl.G + pl.G - 1) * pl.nblk + pl.nblk - 1) / U2;
+  if (!cut) return IFD_OK;
+  return launch_sk_fixup_rows(part, pl.tiles_m, pl.tiles_n, pl.tile0, pl.nsk, pl.G, pl.nblk, C, ldc, M, N, mode, XS,
+                              2 * pl.G, st);
+}
+
 template <int MT>
 static int launch_w4a8_t_cfg(const W4A8TArgs& p, int blocks, int S, hipStream_t st) {
   constexpr int NB = 2;
@@ -353,14 +698,24 @@ static int launch_w4a8_t_cfg(const W4A8TArgs& p, int blocks, int S, hipStream_t 
   return check_launch("w4a8_t64");
 }
 
+size_t w4a8_t_workspace(int M, int N, int K) {
+  if (w4a8_sk_applies(M)) {
+    const WsPlan pl = w4a8_sk_plan(M, N, K);
+    return ws_xt_bytes(pl) + ws_part_bytes(pl);
+  }
+  const WaPlan pl = w4a8_t_plan(M, N, K);
+  return xprep_bytes(M, K) + wa_part_bytes(pl, M, N);
+}
+
 int launch_w4a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   void* ws, size_t ws_bytes, hipStream_t st) {
   if (M == 0) return IFD_OK;
   if (K % 128) return fail(IFD_ERR_ARG, "T64 W4A8 needs K %% 128 == 0 (K=%d)", K);
-  const WaPlan pl = w4a8_t_plan(M, N, K);
   const size_t need = w4a8_t_workspace(M, N, K);
   if (need > ws_bytes || !ws)
     return fail(IFD_ERR_WORKSPACE, "w4a8_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
+  if (w4a8_sk_applies(M)) return launch_w4a8_sk(U, XS, wt, N, K, C, ldc, M, mode, ws, st);
+  const WaPlan pl = w4a8_t_plan(M, N, K);
   const int G = K / kGroup, Gx = (G + 15) / 16 * 16 + 16;
   uint16_t* Xhl = (uint16_t*)ws;
   float* part = (float*)((char*)ws + xprep_bytes(M, K));

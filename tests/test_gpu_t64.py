@@ -357,8 +357,9 @@ def test_gemm_t64_w4a8_config3_sampled():
 
 
 def test_gemm_t64_w4a8_tail_split():
-    """A tile count just past a whole round (9 x 30 = 270 tiles): the last 14 tiles run K-split in a second launch
-    with compact partials; sampled rows against the oracle, all three store modes."""
+    """A tile count just past a whole round (9 x 30 = 270 tiles): one whole tile per block, the last 14 tiles split
+    stream-K over all blocks (16 pieces each, summed by the fixup); sampled rows against the oracle, all three store
+    modes."""
     from inferd_amd._lib import lib
     g, ops = _gu(), _ops()
     M, N, K = 1152, 7680, 1024
@@ -375,6 +376,27 @@ def test_gemm_t64_w4a8_tail_split():
         out = g.host(ops.gemm_t64_w4a8(U, XS, T, g.dev(C0) if mode == 1 else None, mode=mode))[rows]
         ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
         gen.check_out(out, ref, 2e-2, mode, fp32=mode == 2)
+
+
+@pytest.mark.parametrize("M,N,K", [(2560, 6656, 512), (2048, 4096, 256), (1280, 5120, 256)])
+def test_gemm_t64_w4a8_stream_k_plans(M, N, K):
+    """The W4A8 stream-K plans past M = 64, sampled rows against the oracle in all three store modes:
+    20 x 26 = 520 tiles (two whole tiles per block, the first stored in the middle of the run, then 8 stream-K tiles);
+    16 x 16 = 256 tiles (one whole tile per block, no pieces, no fixup); 10 x 20 = 200 tiles of four groups
+    (stream-K only: runs of three or four units, some of them a whole tile)."""
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear(N, K, seed=M + 90)
+    A = gen.activations(M, K, seed=M + 91)
+    U, XS = ops.a8_quant(g.dev(A), True)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    rows = np.unique(np.concatenate([np.linspace(0, M - 1, 24).astype(int), [127, 128, M - 1]]))
+    Ur, XSr = orc.a8_quant(A[rows], True)
+    Y = orc.w4a8(Ur, XSr, wq, s, b)
+    C0 = gen.activations(M, N, seed=M + 92)
+    for mode in (0, 1, 2):
+        out = g.host(ops.gemm_t64_w4a8(U, XS, T, g.dev(C0) if mode == 1 else None, mode=mode))[rows]
+        ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
+        gen.check_out(out, ref, 2e-2, (M, N, K, mode), fp32=mode == 2)
 
 
 def test_gemm_t64_prefill_tiles_with_tail():
