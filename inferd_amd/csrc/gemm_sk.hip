@@ -404,16 +404,16 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p
   else sk_body<MT, false>(p, lds, wave, b);
 }
 
-// Sum of a cut tile's pieces (partial slots, in unit order) and its store. Block (tile, w, f): one wave over the
-// float4 fragment f = (a, q) of column band w of the tile (SwiGLU: gate band w with up band w + 4, giving h), the
+// Sum of a cut tile's pieces (partial slots, in unit order) and its store. Block (tile, w, a), wave q: the float4
+// fragment (a, q) of column band w of the tile (SwiGLU: gate band w with up band w + 4, giving h), the
 // loads of up to kFixBatch pieces in flight at once; whole tiles were stored by the GEMM kernel. blockIdx.x is the
 // tile's index among the stream-K tiles (units [tile G, tile G + G) of their U = ntiles G).
 constexpr int kFixBatch = 8;
 template <int MT>
-__global__ __launch_bounds__(64) void k_sk_fixup(GemmSkArgs p) {
+__global__ __launch_bounds__(256) void k_sk_fixup(GemmSkArgs p) {
   constexpr int BM = 32 * MT, NE = MT * 16;
-  const int tile = blockIdx.x, w = blockIdx.y, a = blockIdx.z / 4, q = blockIdx.z % 4;
-  const int lane = threadIdx.x, j = lane & 31, h = lane >> 5;
+  const int tile = blockIdx.x, w = blockIdx.y, a = blockIdx.z, q = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
   // run boundaries in 32-bit arithmetic (the host keeps U nblk below 2^32): block bb's run starts at unit
   // bb U / nblk, and unit u lies in the run of block (u nblk + nblk - 1) / U
   const uint32_t G = (uint32_t)p.G, U = (uint32_t)p.ntiles * G, nb = (uint32_t)p.nblk;
@@ -524,7 +524,7 @@ static int launch_sk_cfg(const GemmSkArgs& a, bool fixup, hipStream_t st) {
   hipLaunchKernelGGL(k_gemm_sk<MT>, dim3(a.nblk), dim3(kSkThreads), lds, st, a);
   IFD_TRY(check_launch("gemm_sk"));
   if (!fixup) return IFD_OK;
-  hipLaunchKernelGGL(k_sk_fixup<MT>, dim3(a.ntiles, a.swi ? 4 : 8, MT * 4), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(k_sk_fixup<MT>, dim3(a.ntiles, a.swi ? 4 : 8, MT), dim3(256), 0, st, a);
   return check_launch("gemm_sk fixup");
 }
 
@@ -535,7 +535,7 @@ int launch_sk_fixup_rows(const float* part, int tiles_m, int tiles_n, int tile0,
   a.tiles_m = tiles_m, a.tiles_n = tiles_n, a.tile0 = tile0, a.ntiles = ntiles, a.G = G, a.nblk = nblk;
   a.C = C, a.ldc = ldc, a.M = M, a.N = N, a.mode = mode, a.rs = rs, a.rs_stride = rs_stride;
   a.sparse = (long)ntiles * G < nblk;
-  hipLaunchKernelGGL(k_sk_fixup<4>, dim3(ntiles, 8, 16), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(k_sk_fixup<4>, dim3(ntiles, 8, 4), dim3(256), 0, st, a);
   return check_launch("sk fixup");
 }
 
