@@ -331,31 +331,32 @@ __global__ __launch_bounds__(256) void k_wa_tail_reduce(const float* __restrict_
   for (int k = 0; k < 4 && col + k < N; k++) store_mode(C, (size_t)row * ldc + col + k, vv[k], mode);
 }
 
-// ---- W4A8 stream-K for M > 64: 128-row tiles, every CU an equal share of the (tile, group) units ----------------
+// ---- W4A8 stream-K for M > 64: 128-row tiles, every CU an equal share of the (tile, group pair) units -----------
 //
-// Work is the set of units (tile, 64-group), tile = 128 rows x 8 bands (256 columns). With T tiles over nblk blocks
-// (one per CU), the first q nblk = (T / nblk) nblk tiles are whole-tile work: block b takes tiles b q .. b q + q - 1.
-// The other nsk = T % nblk tiles are split stream-K: block b takes their units [b U / nblk, (b + 1) U / nblk),
-// U = nsk G, first. A run is that share (at most two segments, each a piece of its tile unless it covers the whole
-// tile) followed by the block's whole tiles, streamed as one sequence of steps. Pieces go to the block's two
-// partial slots (unscaled fp32 sums in MFMA fragment order); k_sk_fixup sums each cut tile's pieces in unit order,
-// applies the row scale sx and stores the tile.
+// Work is the set of units (tile, pair of 64-groups), tile = 128 rows x 8 bands (256 columns). With T tiles over
+// nblk blocks (one per CU), the first q nblk = (T / nblk) nblk tiles are whole-tile work: block b takes tiles
+// b q .. b q + q - 1. The other nsk = T % nblk tiles are split stream-K: block b takes their units
+// [b U / nblk, (b + 1) U / nblk), U = nsk G2, first. A run is that share (at most two segments, each a piece of its
+// tile unless it covers the whole tile) followed by the block's whole tiles, streamed as one sequence of steps.
+// Pieces go to the block's two partial slots (unscaled fp32 sums in MFMA fragment order); k_sk_fixup sums each cut
+// tile's pieces in unit order, applies the row scale sx and stores the tile.
 //
-// Block: 8 waves, two per SIMD; wave w owns band w over the 4 M tiles. Per step, for M tile a: two
-// v_mfma_i32_32x32x32_i8 give the group's exact P, acc += s float(P) (two VALU per accumulator, the floor of a
-// per-group-scaled integer product), and the bias term b X_g enters acc through one bf16 MFMA whose only non-zero
-// k entries are X_g = hi + lo (two exact bf16 parts) against (b, b). So the group's whole contribution
-// s P + b X is added per step and a segment can end at any group.
-// One LDS ring of kWsR stages filled by direct global -> LDS DMA; a stage holds a group's int8 activation slab
-// [128][64] (16-byte columns XOR-swizzled by row quad), the 8 bands' code halves, their (s, b) rows and the X pairs
-// of the 128 rows in 16-byte slots (from k_w4a8_xprep_t). Every wave issues its slab rows and its band's codes;
-// wave 0 also the (s, b) rows and the first 64 rows' X pairs, wave 1 the other 64 rows' X pairs. They are buffer
-// loads with a scalar group offset; each role's code is compiled on its own, so every wait is a constant. The stream
-// keeps issuing past the run's last unit (re-reading it) so that the count holds to the last step.
-constexpr int kWsR = 8;
-constexpr int kWsA = 128 * 64;
-constexpr int kWsC = 8 * kT64Codes;
-constexpr int kWsSB = 1024;
+// Block: 8 waves, two per SIMD; wave w owns band w over the 4 M tiles. A step is one group pair; per M tile a: for
+// each group, two v_mfma_i32_32x32x32_i8 give its exact P and acc += s float(P) (two VALU per accumulator, the floor
+// of a per-group-scaled integer product); the bias terms b X_g of both groups enter acc through one bf16 MFMA whose
+// only non-zero k entries are X_g = hi + lo (two exact bf16 parts) of the two groups against their (b, b). So a
+// pair's whole contribution is added at its step and a segment can end at any pair.
+// One LDS ring of kWsR stages filled by direct global -> LDS DMA; a stage holds a pair's int8 activation slab
+// [128][2 x 64] (16-byte columns XOR-swizzled by row pair), the 8 bands' code halves and (s, b) rows of both groups
+// and the 128 rows' X pairs of both groups in 16-byte slots (from k_w4a8_xprep_t). Every wave issues its 16 slab rows
+// and its band's two code halves; waves 0 and 1 also the (s, b) rows of one group each, waves 2 and 3 the X pairs of
+// 64 rows each. They are buffer loads with a scalar pair offset; each role's code is compiled on its own, so every
+// wait is a constant. The stream keeps issuing past the run's last unit (re-reading it) so that the count holds to
+// the last step. One barrier per pair of groups.
+constexpr int kWsR = 4;
+constexpr int kWsA = 128 * 128;
+constexpr int kWsC = 2 * 8 * kT64Codes;
+constexpr int kWsSB = 2 * 1024;
 constexpr int kWsX = 2048;
 constexpr int kWsStage = kWsA + kWsC + kWsSB + kWsX;
 constexpr int kWsRow = 256 + 4;  // staged tile row stride (floats)
@@ -364,9 +365,9 @@ constexpr size_t kWsLds = (size_t)kWsR * kWsStage > (size_t)128 * kWsRow * 4 ? (
 static_assert(kWsLds <= 160 * 1024, "LDS plan");
 
 struct W4A8SkArgs {
-  const int8_t* U;       // [M][K]
-  const float* XS;       // [M][G][2]
-  const u32x4* Xt;       // [G][Mx]: (X pair (bf16 hi | bf16 lo << 16), 0, 0, 0), rows past M zero
+  const int8_t* U;     // [M][K]
+  const float* XS;     // [M][G][2]
+  const u32x4* Xt;     // [G / 2][Mx]: (X pair of group 2 p, X pair of group 2 p + 1, 0, 0), rows past M zero
   int Mx;
   const uint8_t* wt;
   uint32_t w_bytes, u_bytes, x_bytes;
@@ -375,51 +376,57 @@ struct W4A8SkArgs {
   int ldc, M, mode;
   float* part;
   uint32_t part_bytes;
-  int tiles_m, tiles_n, G, nblk;
-  int q, tile0, nsk;  // whole tiles per block; the stream-K tiles tile0 .. tile0 + nsk - 1
+  int tiles_m, tiles_n, G2, nblk;  // G2: group pairs per tile (the units)
+  int q, tile0, nsk;               // whole tiles per block; the stream-K tiles tile0 .. tile0 + nsk - 1
 };
 
-// X_g of (row, group) as an exact bf16 pair: hi = 256 floor(X / 256), lo = X - hi; Xt[g][m] = (pair, 0, 0, 0), zero
-// for m >= M. The pair sits in a 16-byte slot that the kernel reads as a whole MFMA operand.
+// X_g of (row, group) as an exact bf16 pair (bf16 hi | bf16 lo << 16): hi = 256 floor(X / 256), lo = X - hi.
+// Xt[p][m] = (pair of group 2 p, pair of group 2 p + 1, 0, 0), zero for m >= M: a 16-byte slot that the kernel reads
+// as a whole MFMA operand.
 __global__ __launch_bounds__(256) void k_w4a8_xprep_t(const float* __restrict__ XS, int M, int G, int Mx,
                                                       u32x4* __restrict__ Xt) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (size_t)G * Mx) return;
-  const int g = (int)(i / Mx), m = (int)(i % Mx);
-  uint32_t v = 0;
+  if (i >= (size_t)(G / 2) * Mx) return;
+  const int pr = (int)(i / Mx), m = (int)(i % Mx);
+  uint32_t v[2] = {0u, 0u};
   if (m < M) {
-    const float x = rintf(XS[((size_t)m * G + g) * 2 + 1] / XS[((size_t)m * G + g) * 2]);
-    const float hi = floorf(x * (1.f / 256.f)) * 256.f;
-    v = (uint32_t)f2bf(hi) | (uint32_t)f2bf(x - hi) << 16;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const int g = 2 * pr + e;
+      const float x = rintf(XS[((size_t)m * G + g) * 2 + 1] / XS[((size_t)m * G + g) * 2]);
+      const float hi = floorf(x * (1.f / 256.f)) * 256.f;
+      v[e] = (uint32_t)f2bf(hi) | (uint32_t)f2bf(x - hi) << 16;
+    }
   }
-  Xt[i] = u32x4{v, 0u, 0u, 0u};
+  Xt[i] = u32x4{v[0], v[1], 0u, 0u};
 }
 
 __device__ __forceinline__ void ws_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, (int)voff, (int)soff, 0, 0);
 }
 
-// ROLE 0: wave 0 (also the (s, b) rows and X pairs of rows 0-63), 1: wave 1 (X pairs of rows 64-127), 2: waves 2-7.
+// ROLE 0: waves 0-3 (also the (s, b) rows of group 2 p + wave for waves 0, 1; the X pairs of rows 64 (wave - 2) ..
+// + 63 for waves 2, 3), ROLE 1: waves 4-7.
 template <int ROLE>
 __device__ __forceinline__ void ws_body(const W4A8SkArgs& p, uint8_t* lds, const int wave, const int b) {
-  constexpr int R = kWsR, D = ROLE == 0 ? 4 : ROLE == 1 ? 3 : 2;
+  constexpr int R = kWsR, D = ROLE == 0 ? 5 : 4;
   static_assert(R >= 4 && (R - 2) * D <= 63, "ring depth, vmcnt range");
   float* const stg = (float*)lds;  // staged tile [128][kWsRow], after the K loop
   const int tid = threadIdx.x, lane = tid & 63;
   const int j = lane & 31, h = lane >> 5;
-  const int G = p.G;
-  const long Usk = (long)p.nsk * G;
+  const int G2 = p.G2, G = 2 * G2;
+  const long Usk = (long)p.nsk * G2;
   const int ur0 = (int)((long)b * Usk / p.nblk), ur1 = (int)((long)(b + 1) * Usk / p.nblk);
-  const int nr = ur1 - ur0, n = nr + p.q * G;
+  const int nr = ur1 - ur0, n = nr + p.q * G2;
   const int nbands = t64_bands(p.N);
   const uint32_t gstride = (uint32_t)nbands * kT64Tile;
 
-  // unit i of the run -> (tile, group)
+  // unit i of the run -> (tile, pair)
   auto unit = [&](int i, int& tile, int& g) __attribute__((always_inline)) {
     if (i < nr) {
-      tile = p.tile0 + (ur0 + i) / G, g = (ur0 + i) % G;
+      tile = p.tile0 + (ur0 + i) / G2, g = (ur0 + i) % G2;
     } else {
-      tile = b * p.q + (i - nr) / G, g = (i - nr) % G;
+      tile = b * p.q + (i - nr) / G2, g = (i - nr) % G2;
     }
   };
 
@@ -427,30 +434,40 @@ __device__ __forceinline__ void ws_body(const W4A8SkArgs& p, uint8_t* lds, const
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.wt, 0, (int)p.w_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.Xt, 0, (int)p.x_bytes, 0x00020000);
 
-  // ---- the DMA stream: per-lane offsets of the current tile, the group in a scalar
-  uint32_t va, vw, v3 = 0, vx = 0;
+  // ---- the DMA stream: per-lane offsets of the current tile, the pair in a scalar
+  uint32_t va[2], vw, v3 = 0;
   auto set_tile = [&](int tile) __attribute__((always_inline)) {
     const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
-    const int r = 16 * wave + lane / 4;  // slab row of this lane's 16 bytes
-    va = (uint32_t)min(tm * 128 + r, p.M - 1) * (uint32_t)p.K + 16u * ((lane & 3) ^ ((r >> 2) & 3));
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+      const int r = 16 * wave + 8 * d + lane / 8;  // slab row of this lane's 16 bytes
+      va[d] = (uint32_t)min(tm * 128 + r, p.M - 1) * (uint32_t)p.K + 16u * ((lane & 7) ^ ((r >> 1) & 7));
+    }
     vw = (uint32_t)min(8 * tn + wave, nbands - 1) * kT64Tile + 16u * lane;
-    if constexpr (ROLE == 0) v3 = (uint32_t)min(8 * tn + lane / 8, nbands - 1) * kT64Tile + kT64Codes + 16u * (lane & 7);
-    vx = (uint32_t)(tm * 128 + 64 * ROLE) * 16u + 16u * lane;
+    if constexpr (ROLE == 0) {
+      if (wave < 2) v3 = (uint32_t)min(8 * tn + lane / 8, nbands - 1) * kT64Tile + kT64Codes + 16u * (lane & 7);
+      else v3 = (uint32_t)(tm * 128 + 64 * (wave - 2) + lane) * 16u;
+    }
   };
   int s_i = 0, s_tile, s_g;
   unit(0, s_tile, s_g);
   set_tile(s_tile);
   auto issue = [&](int slot) __attribute__((always_inline)) {
     uint8_t* st = lds + slot * kWsStage;
-    ws_dma(ru, st + wave * 1024, va, (uint32_t)s_g * 64u);
-    ws_dma(rw, st + kWsA + wave * 1024, vw, (uint32_t)s_g * gstride);
-    if constexpr (ROLE == 0) ws_dma(rw, st + kWsA + kWsC, v3, (uint32_t)s_g * gstride);
-    if constexpr (ROLE < 2) ws_dma(rx, st + kWsA + kWsC + kWsSB + ROLE * 1024, vx, (uint32_t)s_g * (uint32_t)p.Mx * 16u);
+#pragma unroll
+    for (int d = 0; d < 2; d++) ws_dma(ru, st + (2 * wave + d) * 1024, va[d], (uint32_t)s_g * 128u);
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+      ws_dma(rw, st + kWsA + (8 * g + wave) * kT64Codes, vw, (uint32_t)(2 * s_g + g) * gstride);
+    if constexpr (ROLE == 0) {
+      if (wave < 2) ws_dma(rw, st + kWsA + kWsC + wave * 1024, v3, (uint32_t)(2 * s_g + wave) * gstride);
+      else ws_dma(rx, st + kWsA + kWsC + kWsSB + (wave - 2) * 1024, v3, (uint32_t)s_g * (uint32_t)p.Mx * 16u);
+    }
   };
   auto advance = [&]() __attribute__((always_inline)) {
     if (s_i >= n - 1) return;  // past the run's last unit the stream re-reads it
     s_i++;
-    if (++s_g == G || s_i == nr) {
+    if (++s_g == G2 || s_i == nr) {
       unit(s_i, s_tile, s_g);
       set_tile(s_tile);
     }
@@ -460,78 +477,92 @@ __device__ __forceinline__ void ws_body(const W4A8SkArgs& p, uint8_t* lds, const
 #pragma unroll
   for (int a = 0; a < 4; a++) acc[a] = zero16();
 
-  // The operands of one step, read from its stage one step ahead of their use.
-  struct Ops {
-    u32x4 a[4][2];   // activation fragments of the 4 M tiles (k = 32 h + 16 s2 + 0..15 at index s2)
-    u32x4 bq[2];     // the band's B fragments (words 2 s2, 2 s2 + 1 of the lane's codes)
-    float sc;        // the column's scale
-    uint32_t bb;     // (b, b) for the lanes h = 0, else 0
-    u32x4 xv[4];     // (the X pair of row a 32 + j, 0, 0, 0)
-  };
-  auto read_a = [&](const uint8_t* st, int a, Ops& o) __attribute__((always_inline)) {
+  // activation fragments of tile a, group g, MFMA step s2 (k = 32 h + 16 s2 + 0..15 of the group) and the X slot
+  auto read_a = [&](const uint8_t* st, int a, u32x4 (&af)[2][2], u32x4& xv) __attribute__((always_inline)) {
     const int r = a * 32 + j;
-    o.a[a][0] = *(const u32x4*)(st + r * 64 + 16 * ((2 * h) ^ ((r >> 2) & 3)));
-    o.a[a][1] = *(const u32x4*)(st + r * 64 + 16 * ((2 * h + 1) ^ ((r >> 2) & 3)));
-    o.xv[a] = *(const u32x4*)(st + kWsA + kWsC + kWsSB + 16 * r);
-  };
-  auto finish = [&](const u32x4 codes, const uint32_t sb, Ops& o) __attribute__((always_inline)) {
 #pragma unroll
-    for (int s2 = 0; s2 < 2; s2++) {
-      uint32_t d[4];
-      t64_bytes(codes[2 * s2], d[0], d[1]);
-      t64_bytes(codes[2 * s2 + 1], d[2], d[3]);
-      o.bq[s2] = u32x4{d[0], d[1], d[2], d[3]};
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++) af[g][s2] = *(const u32x4*)(st + r * 128 + 16 * ((4 * g + 2 * h + s2) ^ ((r >> 1) & 7)));
+    xv = *(const u32x4*)(st + kWsA + kWsC + kWsSB + 16 * r);
+  };
+  struct Codes {
+    u32x4 w[2];
+    uint32_t sb[2];
+  };
+  auto read_codes = [&](const uint8_t* st, Codes& cd) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      cd.w[g] = *(const u32x4*)(st + kWsA + (8 * g + wave) * kT64Codes + 16 * lane);
+      cd.sb[g] = *(const uint32_t*)(st + kWsA + kWsC + g * 1024 + wave * 128 + 4 * j);
     }
-    o.sc = bf2f((uint16_t)(sb & 0xFFFFu));
-    o.bb = h ? 0u : ((sb >> 16) | (sb & 0xFFFF0000u));
-  };
-  auto read_all = [&](int slot, Ops& o) __attribute__((always_inline)) {
-    const uint8_t* st = lds + slot * kWsStage;
-    const u32x4 codes = *(const u32x4*)(st + kWsA + wave * 1024 + 16 * lane);
-    const uint32_t sb = *(const uint32_t*)(st + kWsA + kWsC + wave * 128 + 4 * j);
-#pragma unroll
-    for (int a = 0; a < 4; a++) read_a(st, a, o);
-    finish(codes, sb, o);
   };
 
-  // Step i: cu holds step i's operands. Waits for stage i + 1 (R - 3 younger stages in flight), issues stage
-  // i + R - 1 into the stage read at step i - 1, then per M tile a: the two i8 MFMAs of P, the bias MFMA (X_hi b +
-  // X_lo b at k = 0, 1), step i + 1's fragments of tile a, and the epilogue of tile a - 1 (P double-buffered).
-  auto step = [&](int i, Ops& cu, Ops& nx) __attribute__((always_inline)) {
+  // Step i: on entry A[0] / X[0] hold tile 0's operands of step i and cd its codes. Waits for stage i + 1 (R - 3
+  // younger stages in flight), issues stage i + R - 1 into the stage read at step i - 1, then per M tile a: the four
+  // i8 MFMAs of the pair's P, the bias MFMA, tile a + 1's operands (for a = 3: tile 0 of step i + 1) and the epilogue
+  // of tile a - 1 (P double-buffered); last, step i + 1's codes.
+  u32x4 A[2][2][2], X[2];
+  Codes cd;
+  auto step = [&](int i) __attribute__((always_inline)) {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 3) * D) : "memory");
     const int slot = i % R;
     issue(slot == 0 ? R - 1 : slot - 1);
     advance();
-    const uint8_t* st = lds + (slot + 1 == R ? 0 : slot + 1) * kWsStage;
-    const u32x4 codes = *(const u32x4*)(st + kWsA + wave * 1024 + 16 * lane);
-    const uint32_t sb = *(const uint32_t*)(st + kWsA + kWsC + wave * 128 + 4 * j);
-    const u32x4 xb = {cu.bb, 0u, 0u, 0u};
-    i32x16 P[2];
+    const uint8_t* st = lds + slot * kWsStage;
+    const uint8_t* stn = lds + (slot + 1 == R ? 0 : slot + 1) * kWsStage;
+    u32x4 bq[2][2];
+    float sc[2];
+    uint32_t bb[2];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++) {
+        uint32_t d[4];
+        t64_bytes(cd.w[g][2 * s2], d[0], d[1]);
+        t64_bytes(cd.w[g][2 * s2 + 1], d[2], d[3]);
+        bq[g][s2] = u32x4{d[0], d[1], d[2], d[3]};
+      }
+      sc[g] = bf2f((uint16_t)(cd.sb[g] & 0xFFFFu));
+      bb[g] = h ? 0u : ((cd.sb[g] >> 16) | (cd.sb[g] & 0xFFFF0000u));
+    }
+    const u32x4 xb = {bb[0], bb[1], 0u, 0u};
+    i32x16 P[2][2];
 #pragma unroll
     for (int a = 0; a < 4; a++) {
-      P[a & 1] = mfma_i8(cu.a[a][0], cu.bq[0], izero16());
-      P[a & 1] = mfma_i8(cu.a[a][1], cu.bq[1], P[a & 1]);
-      acc[a] = mfma_bf16(cu.xv[a], xb, acc[a]);
-      read_a(st, a, nx);
+      const int c = a & 1;
+#pragma unroll
+      for (int g = 0; g < 2; g++) {
+        P[c][g] = mfma_i8(A[c][g][0], bq[g][0], izero16());
+        P[c][g] = mfma_i8(A[c][g][1], bq[g][1], P[c][g]);
+      }
+      acc[a] = mfma_bf16(X[c], xb, acc[a]);
+      read_a(a < 3 ? st : stn, (a + 1) & 3, A[c ^ 1], X[c ^ 1]);
       if (a > 0) {
 #pragma unroll
-        for (int e = 0; e < 16; e++) acc[a - 1][e] = __builtin_fmaf(cu.sc, (float)P[(a - 1) & 1][e], acc[a - 1][e]);
+        for (int e = 0; e < 16; e++) {
+          acc[a - 1][e] = __builtin_fmaf(sc[0], (float)P[c ^ 1][0][e], acc[a - 1][e]);
+          acc[a - 1][e] = __builtin_fmaf(sc[1], (float)P[c ^ 1][1][e], acc[a - 1][e]);
+        }
       }
     }
 #pragma unroll
-    for (int e = 0; e < 16; e++) acc[3][e] = __builtin_fmaf(cu.sc, (float)P[1][e], acc[3][e]);
-    finish(codes, sb, nx);
+    for (int e = 0; e < 16; e++) {
+      acc[3][e] = __builtin_fmaf(sc[0], (float)P[1][0][e], acc[3][e]);
+      acc[3][e] = __builtin_fmaf(sc[1], (float)P[1][1][e], acc[3][e]);
+    }
+    read_codes(stn, cd);
   };
 
-  // prologue: stages 0 .. R - 2 issued, stage 0 read
+  // prologue: stages 0 .. R - 2 issued, stage 0's first operands read
 #pragma unroll
   for (int k = 0; k < R - 1; k++) {
     issue(k);
     advance();
   }
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((R - 2) * D) : "memory");
-  Ops o0, o1;
-  read_all(0, o0);
+  read_a(lds, 0, A[0], X[0]);
+  read_codes(lds, cd);
 
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void*)p.part, 0, (int)p.part_bytes, 0x00020000);
@@ -566,18 +597,10 @@ __device__ __forceinline__ void ws_body(const W4A8SkArgs& p, uint8_t* lds, const
   for (;;) {
     int g;
     unit(i, tile, g);
-    const int len = i < nr ? min(G - g, nr - i) : G;
-    int k = i;
-    for (; k + 1 < i + len; k += 2) {
-      step(k, o0, o1);
-      step(k + 1, o1, o0);
-    }
-    if (k < i + len) {
-      step(k, o0, o1);
-      o0 = o1;
-    }
+    const int len = i < nr ? min(G2 - g, nr - i) : G2;
+    for (int k = i; k < i + len; k++) step(k);
     i += len;
-    whole = len == G;
+    whole = len == G2;
     if (i >= n) break;
     if (whole) {
       store_direct(tile);
@@ -621,31 +644,30 @@ __global__ __launch_bounds__(512, 1) void k_w4a8_sk(W4A8SkArgs p) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = xcd_remap(blockIdx.x, p.nblk);
-  if (wave == 0) ws_body<0>(p, lds, wave, b);
-  else if (wave == 1) ws_body<1>(p, lds, wave, b);
-  else ws_body<2>(p, lds, wave, b);
+  if (wave < 4) ws_body<0>(p, lds, wave, b);
+  else ws_body<1>(p, lds, wave, b);
 }
 
-// Stream-K plan: q whole tiles per block, the last T % nblk tiles split over the blocks
+// Stream-K plan: q whole tiles per block, the last T % nblk tiles split over the blocks (units: group pairs)
 struct WsPlan {
-  int tiles_m, tiles_n, G, nblk, q, tile0, nsk, Mx;
+  int tiles_m, tiles_n, G2, nblk, q, tile0, nsk, Mx;
 };
 static WsPlan w4a8_sk_plan(int M, int N, int K) {
   WsPlan pl{};
   pl.tiles_m = (M + 127) / 128;
   pl.tiles_n = (t64_bands(N) + 7) / 8;
-  pl.G = K / kGroup;
+  pl.G2 = K / (2 * kGroup);
   pl.Mx = pl.tiles_m * 128;
   const int tiles = pl.tiles_m * pl.tiles_n, cus = cu_count();
   pl.q = tiles / cus;
   pl.nsk = tiles - pl.q * cus;
   pl.tile0 = pl.q * cus;
   // with no whole tiles, never more blocks than units
-  pl.nblk = pl.q ? cus : std::min(cus, pl.nsk * pl.G);
+  pl.nblk = pl.q ? cus : std::min(cus, pl.nsk * pl.G2);
   return pl;
 }
 static bool w4a8_sk_applies(int M) { return M > 64; }
-static size_t ws_xt_bytes(const WsPlan& pl) { return align_up((size_t)pl.G * pl.Mx * 16, 256); }
+static size_t ws_xt_bytes(const WsPlan& pl) { return align_up((size_t)pl.G2 * pl.Mx * 16, 256); }
 static size_t ws_part_bytes(const WsPlan& pl) { return pl.nsk ? (size_t)2 * pl.nblk * 8 * 16 * 64 * 16 : 0; }
 
 static int launch_w4a8_sk(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M,
@@ -653,12 +675,13 @@ static int launch_w4a8_sk(const int8_t* U, const float* XS, const void* wt, int 
   const WsPlan pl = w4a8_sk_plan(M, N, K);
   if (t64_bytes(N, K) >= ((size_t)1 << 31) || (size_t)M * K >= ((size_t)1 << 31) ||
       ws_xt_bytes(pl) >= ((size_t)1 << 31) || ws_part_bytes(pl) >= ((size_t)1 << 31) ||
-      ((uint64_t)pl.nsk * pl.G + 1) * (pl.nblk + 1) >= ((uint64_t)1 << 32))
+      ((uint64_t)pl.nsk * pl.G2 + 1) * (pl.nblk + 1) >= ((uint64_t)1 << 32))
     return fail(IFD_ERR_UNSUPPORTED, "w4a8_t64: operands past 2 GiB");
   u32x4* Xt = (u32x4*)ws;
   float* part = (float*)((char*)ws + ws_xt_bytes(pl));
-  const size_t nx = (size_t)pl.G * pl.Mx;
-  hipLaunchKernelGGL(k_w4a8_xprep_t, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, st, XS, M, pl.G, pl.Mx, Xt);
+  const size_t nx = (size_t)pl.G2 * pl.Mx;
+  hipLaunchKernelGGL(k_w4a8_xprep_t, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, st, XS, M, 2 * pl.G2, pl.Mx,
+                     Xt);
   IFD_TRY(check_launch("w4a8_xprep_t"));
   static bool attr = false;
   if (!attr) {
@@ -667,18 +690,18 @@ static int launch_w4a8_sk(const int8_t* U, const float* XS, const void* wt, int 
   }
   W4A8SkArgs a{U, XS, Xt, pl.Mx, (const uint8_t*)wt, (uint32_t)t64_bytes(N, K), (uint32_t)((size_t)M * K),
                (uint32_t)(nx * 16), N, K, C, ldc, M, mode, part, (uint32_t)ws_part_bytes(pl), pl.tiles_m, pl.tiles_n,
-               pl.G, pl.nblk, pl.q, pl.tile0, pl.nsk};
+               pl.G2, pl.nblk, pl.q, pl.tile0, pl.nsk};
   hipLaunchKernelGGL(k_w4a8_sk, dim3(pl.nblk), dim3(512), kWsLds, st, a);
   IFD_TRY(check_launch("w4a8_sk"));
   if (!pl.nsk) return IFD_OK;
   // the fixup runs when some stream-K tile is cut between blocks
-  const long U2 = (long)pl.nsk * pl.G;
+  const long U2 = (long)pl.nsk * pl.G2;
   bool cut = false;
   for (long t = 0; t < pl.nsk && !cut; t++)
-    cut = (t * pl.G * pl.nblk + pl.nblk - 1) / U2 != ((t * pl.G + pl.G - 1) * pl.nblk + pl.nblk - 1) / U2;
+    cut = (t * pl.G2 * pl.nblk + pl.nblk - 1) / U2 != ((t * pl.G2 + pl.G2 - 1) * pl.nblk + pl.nblk - 1) / U2;
   if (!cut) return IFD_OK;
-  return launch_sk_fixup_rows(part, pl.tiles_m, pl.tiles_n, pl.tile0, pl.nsk, pl.G, pl.nblk, C, ldc, M, N, mode, XS,
-                              2 * pl.G, st);
+  return launch_sk_fixup_rows(part, pl.tiles_m, pl.tiles_n, pl.tile0, pl.nsk, pl.G2, pl.nblk, C, ldc, M, N, mode, XS,
+                              4 * pl.G2, st);
 }
 
 template <int MT>
