@@ -325,10 +325,12 @@ def test_gemm_t64_swiglu_strided_output():
     assert np.all(gen.bf16_to_f32(out[:, N // 2:]) == -1.0)
 
 
-@pytest.mark.parametrize("M,N,K", [(37, 200, 512), (128, 384, 1024), (300, 256, 5120), (64, 512, 17408)])
+@pytest.mark.parametrize("M,N,K", [(37, 200, 512), (128, 384, 1024), (300, 256, 5120), (64, 512, 17408),
+                                   (200, 640, 17408)])
 def test_gemm_t64_w4a8(M, N, K):
     """W4A8 on T64 weights (int8 MFMA, per-token activations) against the oracle's w4a8_gemm semantics, all store
-    modes; K = 17408 splits K (bias part per split, fp32 partials)."""
+    modes. M <= 64 runs the K-split kernel (K = 17408: the bias part per split, fp32 partials); M > 64 the stream-K
+    kernel (200 x 640 x 17408: 2 x 3 tiles of 136 group pairs, every tile cut into about 40 pieces)."""
     g, ops = _gu(), _ops()
     codes, wq, s, b = gen.qlinear(N, K, seed=M + 7)
     A = gen.activations(M, K, seed=M + 8)
