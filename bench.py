@@ -280,6 +280,11 @@ def main():
             op = 2.0 * 2048 * 5120 * 5120
             w8["w8a8_M2048"] = dict(us=ms * 1e3, tops=op / (ms * 1e-3) / 1e12,
                                     frac_int8=op / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS)
+            T8 = [ops.pack_t64x8(W8[i % ncp]) for i in range(4)]
+            ms = timed(lambda i: ops.gemm_t64x8_w8a8(U8, XS8, T8[i % 4], C8), 20, 3)
+            w8["w8a8_t64x8_M2048"] = dict(us=ms * 1e3, tops=op / (ms * 1e-3) / 1e12,
+                                          frac_int8=op / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS)
+            del T8
             breakdown["w8_5120x5120"] = dict(w8, copies=ncp)
             del W8
             # the decode MLP's gate_up shape (N = 34816, K = 5120): long enough to stream at bandwidth

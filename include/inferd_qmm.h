@@ -184,6 +184,21 @@ size_t ifd_gemm_t64_w4a8_workspace(int M, int N, int K);
 int ifd_gemm_t64_w4a8(const int8_t* U, const float* XS, int per_token, const void* wt, int N, int K, void* C, int ldc,
                       int M, int mode, void* workspace, size_t ws_bytes, void* stream);
 
+/* ---- T64x8: the T64 arrangement for 8-bit weights (no counterpart in the reference, as T64) ---------------------
+ * 2176-byte tiles per 64-group and 32-column band: the codes as int8 q - 128 in v_mfma_i32_32x32x32_i8 B-fragment
+ * order + the (s, b) pairs; group-major. Same size as the MLX 8-bit source (1.0625 B per weight). xr: the source's
+ * flip mask (0, or 0x80808080 for a flipped 8-bit layer). */
+size_t ifd_t64x8_bytes(int N, int K);
+int ifd_pack_t64x8(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr,
+                   void* out, void* stream);
+/* W8A8 on T64x8 weights (per-token activations from ifd_a8_quant with per_token = 1): replaces ifd_qmm_w8a8 for
+ * packed weights, the same sum C (mode) = sx[m] * sum_g [ s P_g + (b + 128 s) X_g ], P_g = sum (q - 128) xq (exact
+ * int32), as w4a8_gemm with BITS = 8 (w4a8.metal:43-98, :57). K % 64 == 0. per_token = 0 returns
+ * IFD_ERR_UNSUPPORTED. */
+size_t ifd_gemm_t64x8_w8a8_workspace(int M, int N, int K);
+int ifd_gemm_t64x8_w8a8(const int8_t* U, const float* XS, int per_token, const void* wt, int N, int K, void* C,
+                        int ldc, int M, int mode, void* workspace, size_t ws_bytes, void* stream);
+
 /* ---- MoE (reference encode_moe sorted path, qwen35.h:1869-1980; kernels moe.metal:60-187) -------------------- */
 
 /* Router logits [T][E1] = x [T][H] . W [E1][H]^T, bf16 operands, fp32 accumulation; out_bf16 = 1 rounds to bf16

@@ -15,8 +15,8 @@ OUT = os.path.join(HERE, "libinferd_amd.so")
 OBJ = os.path.join(HERE, "_build")
 
 SOURCES = ["qmv.hip", "qmm.hip", "w4a8.hip", "moe.hip", "t64.hip", "gemm_t64.hip", "gemm_sk.hip", "gemm_t8.hip",
-           "w4a8_t64.hip", "fused.hip", "moe_dec.hip", "moe_t64.hip", "capi.hip", "workspace.hip", "probe.hip",
-           "noalloc.hip"]
+           "w4a8_t64.hip", "w8a8_t64.hip", "fused.hip", "moe_dec.hip", "moe_t64.hip", "capi.hip", "workspace.hip",
+           "probe.hip", "noalloc.hip"]
 
 # Packed-fp32 VALU forms are kept out of every code object; hipcc's host pass warns that it does not know the
 # feature, which is harmless.

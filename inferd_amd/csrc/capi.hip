@@ -266,6 +266,39 @@ int ifd_gemm_t64_w4a8(const int8_t* U, const float* XS, int per_token, const voi
   return launch_w4a8_t(U, XS, wt, N, K, C, ldc, M, mode, w.body, w.bytes, S(stream));
 }
 
+// ---- T64x8 layout (8-bit weights) --------------------------------------------------------------------------------
+size_t ifd_t64x8_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 64) return 0;
+  return t64x8_bytes(N, K);
+}
+
+int ifd_pack_t64x8(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr,
+                   void* out, void* stream) {
+  IFD_CHECK(N > 0 && K > 0 && K % 64 == 0, "bad shape N=%d K=%d", N, K);
+  IFD_CHECK(ldk == 0 || (ldk >= K && ldk % 64 == 0), "ldk=%d must be 0 or a multiple of 64 >= K", ldk);
+  IFD_CHECK(xr == 0u || xr == 0x80808080u, "xr=0x%x must be 0 or 0x80808080", xr);
+  IFD_CHECK(wq && s && b && out && aligned(out, 16), "null or misaligned pointer");
+  return launch_pack_t64x8(wq, s, b, N, K, ldk ? ldk : K, xr, out, S(stream));
+}
+
+size_t ifd_gemm_t64x8_w8a8_workspace(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  return with_header(w8a8_t_workspace(M, N, K));
+}
+
+int ifd_gemm_t64x8_w8a8(const int8_t* U, const float* XS, int per_token, const void* wt, int N, int K, void* C,
+                        int ldc, int M, int mode, void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(M >= 0 && N > 0 && K > 0 && K % 64 == 0, "bad shape M=%d N=%d K=%d (K multiple of 64)", M, N, K);
+  IFD_CHECK(mode >= 0 && mode <= 2, "mode=%d must be 0, 1 or 2", mode);
+  IFD_CHECK(ldc >= N, "bad stride ldc=%d", ldc);
+  if (!per_token) return fail(IFD_ERR_UNSUPPORTED, "T64x8 W8A8 takes per-token activations (per_token = 1)");
+  if (M == 0) return IFD_OK;
+  IFD_CHECK(U && XS && wt && C && aligned(U, 16) && aligned(wt, 16), "null or misaligned pointer");
+  IFD_CHECK(!workspace || aligned(workspace, 16), "workspace must be 16-byte aligned");
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_w8a8_t(U, XS, wt, N, K, C, ldc, M, mode, w.body, w.bytes, S(stream));
+}
+
 int ifd_moe_router_logits(const void* x, const void* w, int T, int H, int E1, int out_bf16, void* logits,
                           void* stream) {
   IFD_CHECK(T >= 0 && H > 0 && H % 64 == 0 && E1 > 0, "bad shape T=%d H=%d E1=%d (H multiple of 64)", T, H, E1);

@@ -37,4 +37,17 @@ __host__ __device__ inline uint32_t t64_word(uint32_t w) {
   return o;
 }
 
+// ---- T64x8: the same arrangement for an MLX affine 8-bit group-64 linear (wq uint32 [N][K/4]) -------------------
+//
+//   tile(g, b) = 2176 bytes at ((g * nb) + b) * 2176 (group-major, as above)
+//     bytes [0, 2048): [s2 = 0, 1][64 lanes][16 bytes]. Lane l = j + 32 h (row 32 b + j) holds, at s2 * 1024 + 16 l,
+//                      the codes of k = 64 g + 32 h + 16 s2 + 0..15 in natural order, each stored as the int8
+//                      q - 128 (the byte q ^ 0x80): exactly the lane's B fragment of v_mfma_i32_32x32x32_i8 step s2.
+//     bytes [2048, 2176): 32 dwords, dword j = s | (b << 16) (bf16 bits) of row 32 b + j.
+// 1.0625 B per weight, the size of the MLX layout.
+constexpr int kT64x8Tile = 2176;
+constexpr int kT64x8Codes = 2048;
+
+__host__ __device__ inline size_t t64x8_bytes(int N, int K) { return (size_t)(K / 64) * t64_bands(N) * kT64x8Tile; }
+
 }  // namespace ifd

@@ -70,6 +70,8 @@ class T64Linear:
 
 def pack_t64(W: "QLinear") -> T64Linear:
     """One-time repack of an MLX-layout linear into the T64 layout (undoes a flip)."""
+    if W.bits != 4:
+        raise ValueError("pack_t64 takes 4-bit layers; 8-bit layers go to pack_t64x8")
     nbytes = lib().ifd_t64_bytes(W.N, W.K, 1)
     wt = torch.empty((nbytes,), dtype=torch.uint8, device=W.wq.device)
     check(lib().ifd_pack_t64(_p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, W.xr, 1, _p(wt), _stream()))
@@ -112,6 +114,38 @@ def gemm_t64_w4a8(U: torch.Tensor, XS: torch.Tensor, W: T64Linear, C: Optional[t
     ws = workspace(need, U.device) if need else None
     check(lib().ifd_gemm_t64_w4a8(_p(U), _p(XS), 1, _p(W.wt), W.N, W.K, _p(C), C.shape[1], M, mode, _p(ws),
                                   ws.numel() if ws is not None else 0, _stream()))
+    return C
+
+
+@dataclass
+class T64x8Linear:
+    """An 8-bit linear [N, K] repacked into the T64x8 layout (inferd_amd/csrc/t64.h): a uint8 device buffer."""
+    wt: torch.Tensor
+    N: int
+    K: int
+
+
+def pack_t64x8(W: QLinear) -> T64x8Linear:
+    """One-time repack of an MLX-layout 8-bit linear into the T64x8 layout (undoes a flip)."""
+    if W.bits != 8:
+        raise ValueError("pack_t64x8 takes 8-bit layers")
+    nbytes = lib().ifd_t64x8_bytes(W.N, W.K)
+    wt = torch.empty((nbytes,), dtype=torch.uint8, device=W.wq.device)
+    check(lib().ifd_pack_t64x8(_p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, W.xr, _p(wt), _stream()))
+    return T64x8Linear(wt, W.N, W.K)
+
+
+def gemm_t64x8_w8a8(U: torch.Tensor, XS: torch.Tensor, W: T64x8Linear, C: Optional[torch.Tensor] = None,
+                    mode: int = 0) -> torch.Tensor:
+    """C (mode) = W8A8 product of per-token int8 activations (ops.a8_quant(A, True)) with T64x8 weights."""
+    M, K = U.shape
+    assert K == W.K and U.dtype == torch.int8 and U.is_contiguous()
+    if C is None:
+        C = torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=U.device)
+    need = lib().ifd_gemm_t64x8_w8a8_workspace(M, W.N, W.K)
+    ws = workspace(need, U.device) if need else None
+    check(lib().ifd_gemm_t64x8_w8a8(_p(U), _p(XS), 1, _p(W.wt), W.N, W.K, _p(C), C.shape[1], M, mode, _p(ws),
+                                    ws.numel() if ws is not None else 0, _stream()))
     return C
 
 

@@ -202,3 +202,23 @@ def pack_t64(codes: np.ndarray, s: np.ndarray, b: np.ndarray) -> np.ndarray:
     out[:, :, :1024] = w.reshape(G, nb, 256).view(np.uint8).reshape(G, nb, 1024)
     out[:, :, 1024:] = np.ascontiguousarray(sb).view(np.uint8).reshape(G, nb, 128)
     return out.reshape(-1)
+
+
+def pack_t64x8(codes: np.ndarray, s: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """numpy restatement of the T64x8 layout (inferd_amd/csrc/t64.h) from unflipped 8-bit codes [N, K]: uint8 bytes.
+    Tile (g, band): [s2][lane = 32 h + j][16 bytes] of q ^ 0x80 for k = 64 g + 32 h + 16 s2 + 0..15, then the
+    32 (s, b) dwords."""
+    N, K = codes.shape
+    G, nb = K // 64, (N + 31) // 32
+    cp = np.full((nb * 32, K), 0x80, np.uint8)
+    cp[:N] = codes
+    sp = np.zeros((nb * 32, G), np.uint16)
+    bp = np.zeros((nb * 32, G), np.uint16)
+    sp[:N], bp[:N] = s, b
+    c = (cp ^ np.uint8(0x80)).reshape(nb, 32, G, 2, 2, 16)  # band, j, g, h, s2, byte
+    frag = np.ascontiguousarray(c.transpose(2, 0, 4, 3, 1, 5))  # g, band, s2, h, j, byte
+    sb = (sp.astype(np.uint32) | (bp.astype(np.uint32) << np.uint32(16))).reshape(nb, 32, G).transpose(2, 0, 1)
+    out = np.zeros((G, nb, 2176), np.uint8)
+    out[:, :, :2048] = frag.reshape(G, nb, 2048)
+    out[:, :, 2048:] = np.ascontiguousarray(sb).view(np.uint8).reshape(G, nb, 128)
+    return out.reshape(-1)

@@ -101,6 +101,18 @@ def test_t64_w4a8_refuses_per_group_activations():
     assert rc == _lib.IFD_ERR_UNSUPPORTED and b"per-token" in L.ifd_last_error()
 
 
+def test_t64x8_refuses_bad_arguments():
+    """The 8-bit T64x8 entry points: per-group activation scales, K % 64, the 4-bit flip mask and its size query."""
+    L = _lib.lib()
+    rc = L.ifd_gemm_t64x8_w8a8(4096, 4096, 0, 4096, 256, 256, 4096, 256, 4, 0, None, 0, None)
+    assert rc == _lib.IFD_ERR_UNSUPPORTED and b"per-token" in L.ifd_last_error()
+    assert L.ifd_gemm_t64x8_w8a8(4096, 4096, 1, 4096, 256, 96, 4096, 256, 4, 0, None, 0, None) == _lib.IFD_ERR_ARG
+    assert L.ifd_pack_t64x8(4096, 4096, 4096, 64, 128, 0, 0x88888888, 4096, None) == _lib.IFD_ERR_ARG
+    assert b"0x80808080" in L.ifd_last_error()
+    assert L.ifd_t64x8_bytes(64, 96) == 0 and L.ifd_t64x8_bytes(200, 128) == 2 * 7 * 2176
+    assert L.ifd_gemm_t64x8_w8a8_workspace(2048, 5120, 5120) > HEADER_BYTES
+
+
 def test_new_entry_points_reject_bad_arguments():
     """8-bit GEMM / W8A8, the decode MoE, the MLP block and the int8 gathered GEMM return IFD_ERR_ARG with a reason
     before any GPU work."""

@@ -1,0 +1,101 @@
+"""GPU parity of the T64x8 path (8-bit weights repacked into MFMA fragment order, inferd_amd/csrc/t64.h) through
+the C ABI: ifd_pack_t64x8 bit-exact against the numpy restatement of the layout, and ifd_gemm_t64x8_w8a8 against the
+oracle's w4a8_gemm with BITS = 8 (engine/kernels/w4a8.metal:43-98, the offset 128 at :57), 2e-2 RMS as every W8A8
+path. The shapes cover one cut tile, tiles cut into many pieces, runs of one unit, empty runs (fewer units than
+CUs), ragged N and whole-tile work beside the stream-K share (the BASELINE config 3 shape, sampled rows)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import gen
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+FLIP8 = 0x80808080
+
+
+def _gu():
+    from tests import gpu_util
+    return gpu_util
+
+
+def _ops():
+    from inferd_amd import ops
+    return ops
+
+
+@pytest.mark.parametrize("N,K", [(200, 512), (64, 64), (1024, 2048)])
+@pytest.mark.parametrize("flipped", [False, True])
+def test_pack_t64x8_bit_exact(N, K, flipped):
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear8(N, K, seed=N + K, bias="free")
+    W = g.qlinear(wq ^ np.uint32(FLIP8) if flipped else wq, s, b, flipped, bits=8)
+    T = ops.pack_t64x8(W)
+    torch.cuda.synchronize()
+    assert T.wt.numel() == gen.pack_t64x8(codes, s, b).size
+    assert np.array_equal(g.host(T.wt), gen.pack_t64x8(codes, s, b))
+
+
+@pytest.mark.parametrize("M,N,K", [(37, 200, 512), (128, 384, 1024), (300, 256, 5120), (1, 32, 64),
+                                   (200, 640, 17408), (129, 1000, 256), (300, 22016, 256)])
+def test_gemm_t64x8_w8a8(M, N, K):
+    """All store modes, independent biases (b' = b + 128 s far from 0). 37 x 200 x 512: one tile cut over 8 blocks;
+    300 x 256 x 5120: 3 tiles, 240 units on 240 blocks (runs of one unit); 1 x 32 x 64: one unit on one block;
+    200 x 640 x 17408: 6 tiles of 272 groups, each cut into about 43 pieces; 129 x 1000 x 256: a ragged last band
+    and a second M tile of one row; 300 x 22016 x 256: 258 tiles on 256 CUs, one whole tile per block and 2 tiles of
+    4 groups split over 8 blocks (the other runs empty)."""
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear8(N, K, seed=M + 40, bias="free")
+    A = gen.activations(M, K, seed=M + 41)
+    U, XS = orc.a8_quant(A, True)
+    T = ops.pack_t64x8(g.qlinear(wq, s, b, bits=8))
+    Y = orc.w4a8(U, XS, wq, s, b, bits=8)
+    C0 = gen.activations(M, N, seed=M + 42)
+    for mode in (0, 1, 2):
+        C = g.dev(C0) if mode == 1 else None
+        out = g.host(ops.gemm_t64x8_w8a8(g.dev(U), g.dev(XS), T, C, mode=mode))
+        gen.check_out(out, Y + gen.bf16_to_f32(C0) if mode == 1 else Y, 2e-2, (M, N, K, mode), fp32=mode == 2)
+
+
+def test_gemm_t64x8_w8a8_flipped_minus128():
+    """A flipped source layer (the reference's load-time w_flip with the 8-bit mask) packs to the same tiles, and
+    b = -128 s (b' = 0) gives the same product as the MLX-layout W8A8 GEMM."""
+    g, ops = _gu(), _ops()
+    M, N, K = 96, 512, 2048
+    codes, wq, s, b = gen.qlinear8(N, K, seed=77)
+    A = gen.activations(M, K, seed=78)
+    U, XS = orc.a8_quant(A, True)
+    Y = orc.w4a8(U, XS, wq, s, b, bits=8)
+    Wf = g.qlinear(wq ^ np.uint32(FLIP8), s, b, True, bits=8)
+    out = g.host(ops.gemm_t64x8_w8a8(g.dev(U), g.dev(XS), ops.pack_t64x8(Wf)))
+    gen.check_out(out, Y, 2e-2, (M, N, K, "flipped"))
+    mlx = g.host(ops.qmm_w4a8(g.dev(U), g.dev(XS), True, Wf))
+    gen.check_out(out, gen.bf16_to_f32(mlx), 2e-2, (M, N, K, "vs MLX-layout W8A8"))
+
+
+def test_gemm_t64x8_w8a8_config3_sampled():
+    """The BASELINE config 3 shape in 8 bits (M=2048, K=N=5120, per-token int8): 320 tiles on 256 CUs, so one whole
+    tile per block plus 64 tiles split stream-K. The oracle on 16 sampled rows; a row-sum property on all rows."""
+    g, ops = _gu(), _ops()
+    M, N, K = 2048, 5120, 5120
+    codes, wq, s, b = gen.qlinear8(N, K, seed=80, bias="free")
+    A = gen.activations(M, K, seed=81)
+    U, XS = ops.a8_quant(g.dev(A), True)
+    out = g.host(ops.gemm_t64x8_w8a8(U, XS, ops.pack_t64x8(g.qlinear(wq, s, b, bits=8)), mode=2))
+    rows = np.linspace(0, M - 1, 16).astype(int)
+    Uh, XSh = g.host(U), g.host(XS)
+    Y = orc.w4a8(Uh[rows], XSh[rows], wq, s, b, bits=8)
+    gen.check_out(out[rows], Y, 2e-2, ("config3 rows",), fp32=True)
+    # every row: sum over n of y[m][n] = sx sum_g (P_g . sum_n s + X_g . sum_n b') is linear in the weights, so the
+    # product with the column sums of the dequantized weights (fp64 on the host) must match the row sums
+    G = K // 64
+    q = codes.astype(np.float64).reshape(N, G, 64)
+    Wd = q * gen.bf16_to_f32(s).astype(np.float64)[..., None] + gen.bf16_to_f32(b).astype(np.float64)[..., None]
+    wsum = Wd.reshape(N, K).sum(0)
+    xq = Uh.astype(np.float64) * np.repeat(XSh[:, :, 0].astype(np.float64), 64, axis=1)
+    ref = xq @ wsum
+    got = out.astype(np.float64).sum(1)
+    err = np.sqrt(np.mean((got - ref) ** 2)) / np.sqrt(np.mean(ref ** 2))
+    assert err < 1e-3, err
+
