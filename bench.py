@@ -299,6 +299,16 @@ def main():
                 byts = nbg + M * (5120 + 34816) * 2
                 wg[f"M{M}"] = dict(us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9,
                                    frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+            # the same layers repacked as T64x8, on the stream-K bf16 GEMM
+            Tg = [ops.pack_t64x8(w) for w in Wg]
+            for M in (32, 128):
+                Ag = act(M, 5120)
+                Cg = torch.empty((M, 34816), dtype=torch.bfloat16, device=dev)
+                ms = timed(lambda i: ops.gemm_t64x8(Ag, Tg[i % ncg], Cg), 40, 5)
+                byts = nbg + M * (5120 + 34816) * 2
+                wg[f"t64x8_M{M}"] = dict(us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9,
+                                         frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+            del Tg
             breakdown["w8_34816x5120"] = dict(wg, copies=ncg)
             del Wg
         # ---- config 4: MoE FFN H=2048, E=512, top-10, I=512, + shared expert ----------------------------------

@@ -191,6 +191,12 @@ int ifd_gemm_t64_w4a8(const int8_t* U, const float* XS, int per_token, const voi
 size_t ifd_t64x8_bytes(int N, int K);
 int ifd_pack_t64x8(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr,
                    void* out, void* stream);
+/* C (mode) = A . W^T with W in T64x8 layout (K % 64 == 0), every weight dequantized to bf16(s q + b) with fp32
+ * accumulation: MLX's 8-bit qmm (quantized.h:528-535, the reference's affine_qmm_t at BITS = 8) on a stream-K
+ * bf16 MFMA kernel, for every M (meant for M > 16: decode rows go to ifd_gemm_w8's qmv arithmetic). */
+size_t ifd_gemm_t64x8_workspace(int M, int N, int K);
+int ifd_gemm_t64x8(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                   void* workspace, size_t ws_bytes, void* stream);
 /* W8A8 on T64x8 weights (per-token activations from ifd_a8_quant with per_token = 1): replaces ifd_qmm_w8a8 for
  * packed weights, the same sum C (mode) = sx[m] * sum_g [ s P_g + (b + 128 s) X_g ], P_g = sum (q - 128) xq (exact
  * int32), as w4a8_gemm with BITS = 8 (w4a8.metal:43-98, :57). K % 64 == 0. per_token = 0 returns

@@ -55,6 +55,8 @@ SIGNATURES = {
     "ifd_gemm_t64_w4a8": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_t64x8_bytes": (_sz, [_i, _i]),
     "ifd_pack_t64x8": (_i, [_vp, _vp, _vp, _i, _i, _i, _u32, _vp, _vp]),
+    "ifd_gemm_t64x8_workspace": (_sz, [_i, _i, _i]),
+    "ifd_gemm_t64x8": (_i, [_vp, _i, _vp, _i, _i, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_gemm_t64x8_w8a8_workspace": (_sz, [_i, _i, _i]),
     "ifd_gemm_t64x8_w8a8": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_moe_router_logits": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp]),

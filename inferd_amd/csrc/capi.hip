@@ -281,6 +281,23 @@ int ifd_pack_t64x8(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int
   return launch_pack_t64x8(wq, s, b, N, K, ldk ? ldk : K, xr, out, S(stream));
 }
 
+size_t ifd_gemm_t64x8_workspace(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  return with_header(gemm_sk8_workspace(M, N, K));
+}
+
+int ifd_gemm_t64x8(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                   void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(M >= 0 && N > 0 && K > 0 && K % 64 == 0, "bad shape M=%d N=%d K=%d (K multiple of 64)", M, N, K);
+  IFD_CHECK(mode >= 0 && mode <= 2, "mode=%d must be 0, 1 or 2", mode);
+  IFD_CHECK(lda >= K && lda % 8 == 0 && ldc >= N, "bad strides lda=%d ldc=%d", lda, ldc);
+  if (M == 0) return IFD_OK;
+  IFD_CHECK(A && wt && C && aligned(A, 16) && aligned(wt, 16), "null or misaligned pointer");
+  IFD_CHECK(!workspace || aligned(workspace, 16), "workspace must be 16-byte aligned");
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_gemm_sk8((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, w.body, w.bytes, S(stream));
+}
+
 size_t ifd_gemm_t64x8_w8a8_workspace(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
   return with_header(w8a8_t_workspace(M, N, K));

@@ -38,23 +38,31 @@ namespace ifd {
 
 constexpr int kSkWaves = 4;
 constexpr int kSkThreads = 64 * kSkWaves;
-constexpr int kSkDeqValu = 2 * (4 * 17 + 8);  // VALU of a wave's dequant per step: 2 bands x (4 words, the scales)
-constexpr int kSkWBytes = 8 * kT64Codes + 8 * 128;  // weights of a stage: 8 code halves + 8 (s, b) rows
 constexpr int kSkLds = 160 * 1024;  // LDS per CU
 constexpr int kSkRow = 256 + 4;  // staged tile row stride (floats): rows h = 0, 1 of one store fall in other banks
 
-// 32-row tiles run two blocks per CU (two waves per SIMD hide the latency of their short steps), larger tiles one.
-// A stage holds one step's activation slab and weights; the ring is as deep as LDS allows, at most 8 stages.
-__host__ __device__ constexpr int sk_bpc(int MT) { return MT == 1 ? 2 : 1; }
+// BITS = 4: T64 weights; BITS = 8: T64x8 weights (t64.h), whose code tiles are twice as large (two 1 KB halves per
+// band and group, each one DMA) and are dequantized from the stored q - 128 bytes.
+__host__ __device__ constexpr int sk_codes(int BITS) { return BITS == 8 ? kT64x8Codes : kT64Codes; }
+__host__ __device__ constexpr int sk_tileb(int BITS) { return BITS == 8 ? kT64x8Tile : kT64Tile; }
+// weights of a stage: 8 bands' codes + 8 (s, b) rows
+__host__ __device__ constexpr int sk_wbytes(int BITS) { return 8 * sk_codes(BITS) + 8 * 128; }
+
+// 4-bit 32-row tiles run two blocks per CU (two waves per SIMD hide the latency of their short steps), other tiles
+// one (an 8-bit stage is too large for two rings of four). A stage holds one step's activation slab and weights; the
+// ring is as deep as LDS allows, at most 8 stages.
+__host__ __device__ constexpr int sk_bpc(int MT, int BITS) { return MT == 1 && BITS == 4 ? 2 : 1; }
 __host__ __device__ constexpr int sk_abytes(int MT) { return MT * 32 * 128; }
-__host__ __device__ constexpr int sk_stage(int MT) { return sk_abytes(MT) + kSkWBytes; }
-__host__ __device__ constexpr int sk_ring(int MT) {
-  return (kSkLds / sk_bpc(MT) - 64) / sk_stage(MT) < 8 ? (kSkLds / sk_bpc(MT) - 64) / sk_stage(MT) : 8;
+__host__ __device__ constexpr int sk_stage(int MT, int BITS) { return sk_abytes(MT) + sk_wbytes(BITS); }
+__host__ __device__ constexpr int sk_ring(int MT, int BITS) {
+  return (kSkLds / sk_bpc(MT, BITS) - 64) / sk_stage(MT, BITS) < 8 ? (kSkLds / sk_bpc(MT, BITS) - 64) / sk_stage(MT, BITS)
+                                                                   : 8;
 }
 // the ring, and after the K loop the staged tile [32 MT][kSkRow] fp32 in the same memory
-__host__ __device__ constexpr size_t sk_lds(int MT) {
-  return (size_t)sk_ring(MT) * sk_stage(MT) > (size_t)MT * 32 * kSkRow * 4 ? (size_t)sk_ring(MT) * sk_stage(MT)
-                                                                             : (size_t)MT * 32 * kSkRow * 4;
+__host__ __device__ constexpr size_t sk_lds(int MT, int BITS) {
+  return (size_t)sk_ring(MT, BITS) * sk_stage(MT, BITS) > (size_t)MT * 32 * kSkRow * 4
+             ? (size_t)sk_ring(MT, BITS) * sk_stage(MT, BITS)
+             : (size_t)MT * 32 * kSkRow * 4;
 }
 
 struct GemmSkArgs {
@@ -91,11 +99,14 @@ __device__ __forceinline__ void sk_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint
 // run's end too (re-reading its last unit), so the waits are constants: at step i the wave reads A(i + 1)'s
 // fragments and W(i + 2)'s codes, the second of pair i + 1, which R - 3 younger pairs follow. Stage j % R holds A(j)
 // and W(j); step i overwrites A(i - 1) and W(i), both read two steps earlier.
-template <int MT, bool W0>
+template <int MT, int BITS, bool W0>
 __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const int wave, const int b) {
-  constexpr int BM = 32 * MT, R = sk_ring(MT), A_BYTES = sk_abytes(MT), STAGE = sk_stage(MT);
-  constexpr int NE = MT * 16;     // accumulators per lane and band
-  constexpr int NW = W0 ? 3 : 2;  // weight DMAs per pair
+  constexpr int BM = 32 * MT, R = sk_ring(MT, BITS), A_BYTES = sk_abytes(MT), STAGE = sk_stage(MT, BITS);
+  constexpr int CODES = sk_codes(BITS), TILEB = sk_tileb(BITS);
+  constexpr int NE = MT * 16;              // accumulators per lane and band
+  constexpr int NH = BITS / 4;             // 1 KB code DMAs per band
+  constexpr int NWC = 2 * NH;              // code DMAs per pair (two bands)
+  constexpr int NW = NWC + (W0 ? 1 : 0);   // weight DMAs per pair
   constexpr int PAIR = MT + NW;
   static_assert(R >= 4 && (R - 2) * PAIR <= 63, "ring depth, vmcnt range");
   float* const stg = (float*)lds;  // staged tile [BM][kSkRow], after the K loop
@@ -106,7 +117,7 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
   const long U = (long)p.tiles_m * p.tiles_n * G;
   const int u0 = (int)((long)b * U / p.nblk), u1 = (int)((long)(b + 1) * U / p.nblk), n = u1 - u0;
   const int nbands = t64_bands(p.N);
-  const uint32_t gstride = (uint32_t)nbands * kT64Tile;
+  const uint32_t gstride = (uint32_t)nbands * TILEB;
   const int tile_first = u0 / G, tile_last = (u1 - 1) / G;
 
   auto phys_band = [&](int tn, int lb) __attribute__((always_inline)) {  // physical band of local band lb (0..7)
@@ -128,12 +139,16 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
       va[q] = (uint32_t)min(tm * BM + r, p.M - 1) * (uint32_t)p.lda * 2u + 16u * c;
     }
   };
+  // weight DMA k < NWC: half k % NH of band 2 wave + k / NH; k = NWC (wave 0): the 8 (s, b) rows
   auto w_tile = [&](int tile) __attribute__((always_inline)) {
     const int tn = tile / p.tiles_m;
-    vw[0] = (uint32_t)phys_band(tn, 2 * wave) * kT64Tile + 16u * lane;
-    vw[1] = (uint32_t)phys_band(tn, 2 * wave + 1) * kT64Tile + 16u * lane;
-    if constexpr (W0) vw[2] = (uint32_t)phys_band(tn, lane / 8) * kT64Tile + kT64Codes + 16u * (lane & 7);
+#pragma unroll
+    for (int k = 0; k < NWC; k++)
+      vw[k] = (uint32_t)phys_band(tn, 2 * wave + k / NH) * TILEB + 1024u * (k % NH) + 16u * lane;
+    if constexpr (W0) vw[NWC] = (uint32_t)phys_band(tn, lane / 8) * TILEB + CODES + 16u * (lane & 7);
   };
+  // LDS offset of code DMA k from the wave's first band
+  auto w_dst = [](int k) { return (k / NH) * CODES + (k % NH) * 1024; };
   int a_t = tile_first, a_g = u0 % G, w_t = tile_first, w_g = a_g;
   uint32_t a_so = (uint32_t)a_g * 2u * kGroup, w_so = (uint32_t)w_g * gstride;
   a_tile(a_t);
@@ -145,10 +160,10 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
     for (int q = 0; q < MT; q++) sk_dma(ra, st + (MT * wave + q) * 1024, va[q], a_so);
   };
   auto issue_w = [&](int stage) __attribute__((always_inline)) {
-    uint8_t* st = lds + stage * STAGE + A_BYTES;
-    sk_dma(rw, st + (2 * wave) * kT64Codes, vw[0], w_so);
-    sk_dma(rw, st + (2 * wave + 1) * kT64Codes, vw[1], w_so);
-    if constexpr (W0) sk_dma(rw, st + 8 * kT64Codes, vw[2], w_so);
+    uint8_t* st = lds + stage * STAGE + A_BYTES + (2 * wave) * CODES;
+#pragma unroll
+    for (int k = 0; k < NWC; k++) sk_dma(rw, st + w_dst(k), vw[k], w_so);
+    if constexpr (W0) sk_dma(rw, lds + stage * STAGE + A_BYTES + 8 * CODES, vw[NWC], w_so);
   };
   // Past the run's last unit a stream stays on it: the extra DMAs re-read that unit (L2 hits), never new bytes.
   int a_left = n - 1, w_left = n - 1;  // advances left before a stream reaches the run's last unit
@@ -177,7 +192,7 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
 
   // LDS reads one step ahead of their use
   struct Codes {
-    u32x4 w[2];
+    u32x4 w[2][NH];
     uint32_t sb[2];
   };
   auto read_codes = [&](int s, Codes& cd) __attribute__((always_inline)) {  // this wave's two bands of stage s
@@ -185,17 +200,35 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
       const int band = 2 * wave + nb;
-      cd.w[nb] = *(const u32x4*)(wst + band * kT64Codes + 16 * lane);
-      cd.sb[nb] = *(const uint32_t*)(wst + 8 * kT64Codes + band * 128 + 4 * j);
+#pragma unroll
+      for (int hh = 0; hh < NH; hh++) cd.w[nb][hh] = *(const u32x4*)(wst + band * CODES + hh * 1024 + 16 * lane);
+      cd.sb[nb] = *(const uint32_t*)(wst + 8 * CODES + band * 128 + 4 * j);
     }
+  };
+  // MFMA step t's B fragment of band nb: column j, k = 32 h + 8 t .. + 7 dequantized to bf16(s q + b). sa, sbs: the
+  // scalings of s for t64_dequant (4 bits); 8 bits: sa = s, and q = stored byte ^ 0x80.
+  auto deq_step = [&](const Codes& cd, int nb, int t, float sa, float sbs, float bi) __attribute__((always_inline)) {
+    if constexpr (BITS == 4) {
+      return t64_dequant(cd.w[nb][0][t], sa, sbs, bi);
+    } else {
+      (void)sbs;
+      return dequant8x8_bf16(cd.w[nb][t / 2][2 * (t % 2)] ^ 0x80808080u, cd.w[nb][t / 2][2 * (t % 2) + 1] ^ 0x80808080u,
+                             sa, bi);
+    }
+  };
+  auto scales = [&](uint32_t sbw, float& sa, float& sbs, float& bi) __attribute__((always_inline)) {
+    const float sc = bf2f((uint16_t)(sbw & 0xFFFFu));
+    bi = bf2f((uint16_t)(sbw >> 16));
+    sa = BITS == 4 ? t64_sa(sc) : sc;
+    sbs = BITS == 4 ? t64_sb(sc) : 0.f;
   };
   auto dequant = [&](const Codes& cd, u32x4 (&bf)[2][4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
-      const float sc = bf2f((uint16_t)(cd.sb[nb] & 0xFFFFu)), bi = bf2f((uint16_t)(cd.sb[nb] >> 16));
-      const float sa = t64_sa(sc), sbs = t64_sb(sc);
+      float sa, sbs, bi;
+      scales(cd.sb[nb], sa, sbs, bi);
 #pragma unroll
-      for (int t = 0; t < 4; t++) bf[nb][t] = t64_dequant(cd.w[nb][t], sa, sbs, bi);
+      for (int t = 0; t < 4; t++) bf[nb][t] = deq_step(cd, nb, t, sa, sbs, bi);
     }
   };
   // activation fragments of stage s: M tile a, MFMA step t takes k = 32 h + 8 t .. + 7 (logical column 4 h + t)
@@ -239,24 +272,26 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 3) * PAIR) : "memory");
     const int s1 = s0 + 1 == R ? 0 : s0 + 1, s2 = s1 + 1 == R ? 0 : s1 + 1, sm = s0 == 0 ? R - 1 : s0 - 1;
     // Eight groups, each closed by a scheduling barrier: MT MFMAs of this step, one 8-code dequant of the next
-    // (17 VALU), a share of the LDS reads for the next steps and at most one DMA, so that the matrix core has work
-    // through the whole step and the wave's other instructions issue in its shadow.
-    constexpr int NDS = 4 * MT + 4, NDMA = MT + NW;
+    // (17 VALU for 4 bits, 22 for 8), a share of the LDS reads for the next steps and of the pair's DMAs, so that the
+    // matrix core has work through the whole step and the wave's other instructions issue in its shadow.
+    constexpr int NDS = 4 * MT + 2 * (NH + 1), NDMA = MT + NW, DEQ = BITS == 4 ? 17 : 22;
     const uint8_t* const ast = lds + s1 * STAGE;        // activation fragments of step i + 1
     const uint8_t* const wst = lds + s2 * STAGE + A_BYTES;  // codes of step i + 2
     float sa[2], sbs[2], bi[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-      const float sc = bf2f((uint16_t)(cc.sb[nb] & 0xFFFFu));
-      bi[nb] = bf2f((uint16_t)(cc.sb[nb] >> 16)), sa[nb] = t64_sa(sc), sbs[nb] = t64_sb(sc);
-    }
+    for (int nb = 0; nb < 2; nb++) scales(cc.sb[nb], sa[nb], sbs[nb], bi[nb]);
+    auto issue_one = [&](int d) __attribute__((always_inline)) {  // DMA d of the pair: A rows, then the weights
+      if (d < MT) sk_dma(ra, lds + sm * STAGE + (MT * wave + d) * 1024, va[d], a_so);
+      else if (d - MT < NWC) sk_dma(rw, lds + s0 * STAGE + A_BYTES + (2 * wave) * CODES + w_dst(d - MT), vw[d - MT], w_so);
+      else sk_dma(rw, lds + s0 * STAGE + A_BYTES + 8 * CODES, vw[NWC], w_so);
+    };
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-      if (g < NDMA) {
-        if (g < MT) sk_dma(ra, lds + sm * STAGE + (MT * wave + g) * 1024, va[g], a_so);
-        else if (g == MT) sk_dma(rw, lds + s0 * STAGE + A_BYTES + (2 * wave) * kT64Codes, vw[0], w_so);
-        else if (g == MT + 1) sk_dma(rw, lds + s0 * STAGE + A_BYTES + (2 * wave + 1) * kT64Codes, vw[1], w_so);
-        else if constexpr (W0) sk_dma(rw, lds + s0 * STAGE + A_BYTES + 8 * kT64Codes, vw[2], w_so);
+      if constexpr (NDMA <= 8) {
+        if (g < NDMA) issue_one(g);
+      } else {
+#pragma unroll
+        for (int d = g * NDMA / 8; d < (g + 1) * NDMA / 8; d++) issue_one(d);
       }
 #pragma unroll
       for (int d = g * NDS / 8; d < (g + 1) * NDS / 8; d++) {
@@ -264,12 +299,12 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
           const int am = d / 4, t = d % 4, r = am * 32 + j;
           afn[am][t] = *(const u32x4*)(ast + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
         } else {
-          const int nb = (d - 4 * MT) / 2, band = 2 * wave + nb;
-          if ((d - 4 * MT) % 2 == 0) cn.w[nb] = *(const u32x4*)(wst + band * kT64Codes + 16 * lane);
-          else cn.sb[nb] = *(const uint32_t*)(wst + 8 * kT64Codes + band * 128 + 4 * j);
+          const int nb = (d - 4 * MT) / (NH + 1), e = (d - 4 * MT) % (NH + 1), band = 2 * wave + nb;
+          if (e < NH) cn.w[nb][e] = *(const u32x4*)(wst + band * CODES + e * 1024 + 16 * lane);
+          else cn.sb[nb] = *(const uint32_t*)(wst + 8 * CODES + band * 128 + 4 * j);
         }
       }
-      bn[g / 4][g % 4] = t64_dequant(cc.w[g / 4][g % 4], sa[g / 4], sbs[g / 4], bi[g / 4]);
+      bn[g / 4][g % 4] = deq_step(cc, g / 4, g % 4, sa[g / 4], sbs[g / 4], bi[g / 4]);
 #pragma unroll
       for (int m = g * MT; m < (g + 1) * MT; m++) {
         const int am = m / 8, nb = (m / 4) % 2, t = m % 4;
@@ -278,7 +313,7 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
 #pragma unroll
       for (int m = 0; m < MT; m++) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 17 / MT + 1, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, DEQ / MT + 1, 0);  // VALU
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -394,14 +429,14 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
   write_slot(2 * b + (two ? 1 : 0));  // a piece of a cut tile: k_sk_fixup sums the pieces
 }
 
-template <int MT>
-__global__ __launch_bounds__(kSkThreads, sk_bpc(MT)) void k_gemm_sk(GemmSkArgs p) {
-  static_assert(sk_lds(MT) + 64 <= kSkLds / sk_bpc(MT), "LDS plan");
+template <int MT, int BITS>
+__global__ __launch_bounds__(kSkThreads, sk_bpc(MT, BITS)) void k_gemm_sk(GemmSkArgs p) {
+  static_assert(sk_lds(MT, BITS) + 64 <= kSkLds / sk_bpc(MT, BITS), "LDS plan");
   extern __shared__ __align__(16) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = xcd_remap(blockIdx.x, p.nblk);
-  if (wave == 0) sk_body<MT, true>(p, lds, wave, b);
-  else sk_body<MT, false>(p, lds, wave, b);
+  if (wave == 0) sk_body<MT, BITS, true>(p, lds, wave, b);
+  else sk_body<MT, BITS, false>(p, lds, wave, b);
 }
 
 // Sum of a cut tile's pieces (partial slots, in unit order) and its store. Block (tile, w, a), wave q: the float4
@@ -479,10 +514,10 @@ __global__ __launch_bounds__(256) void k_sk_fixup(GemmSkArgs p) {
 struct SkPlan {
   int MT, tiles_m, tiles_n, G, nblk;
 };
-static SkPlan gemm_sk_plan(int M, int N, int K) {
+static SkPlan gemm_sk_plan(int M, int N, int K, int bits = 4) {
   SkPlan pl{};
   pl.MT = M <= 32 ? 1 : M <= 64 ? 2 : 4;
-  const int bpc = pl.MT == 1 ? 2 : 1;  // sk_bpc
+  const int bpc = pl.MT == 1 && bits == 4 ? 2 : 1;  // sk_bpc
   pl.tiles_m = (M + 32 * pl.MT - 1) / (32 * pl.MT);
   pl.tiles_n = (t64_bands(N) + 7) / 8;
   pl.G = K / kGroup;
@@ -507,21 +542,24 @@ bool gemm_sk_applies(int M, int N, int K, int mode) {
   return (long)pl.tiles_m * pl.tiles_n * 3 >= cu_count() || (M > 64 && M <= 128);
 }
 
+static size_t sk_part_bytes(const SkPlan& pl) { return (size_t)2 * pl.nblk * 8 * (16 * pl.MT) * 64 * sizeof(float); }
+
 size_t gemm_sk_workspace(int M, int N, int K, int mode) {
   (void)mode;
-  const SkPlan pl = gemm_sk_plan(M, N, K);
-  return (size_t)2 * pl.nblk * 8 * (16 * pl.MT) * 64 * sizeof(float);
+  return sk_part_bytes(gemm_sk_plan(M, N, K));
 }
 
-template <int MT>
+size_t gemm_sk8_workspace(int M, int N, int K) { return sk_part_bytes(gemm_sk_plan(M, N, K, 8)); }
+
+template <int MT, int BITS>
 static int launch_sk_cfg(const GemmSkArgs& a, bool fixup, hipStream_t st) {
-  constexpr size_t lds = sk_lds(MT);
+  constexpr size_t lds = sk_lds(MT, BITS);
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)k_gemm_sk<MT>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    (void)hipFuncSetAttribute((const void*)k_gemm_sk<MT, BITS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr = true;
   }
-  hipLaunchKernelGGL(k_gemm_sk<MT>, dim3(a.nblk), dim3(kSkThreads), lds, st, a);
+  hipLaunchKernelGGL((k_gemm_sk<MT, BITS>), dim3(a.nblk), dim3(kSkThreads), lds, st, a);
   IFD_TRY(check_launch("gemm_sk"));
   if (!fixup) return IFD_OK;
   hipLaunchKernelGGL(k_sk_fixup<MT>, dim3(a.ntiles, a.swi ? 4 : 8, MT), dim3(256), 0, st, a);
@@ -539,27 +577,43 @@ int launch_sk_fixup_rows(const float* part, int tiles_m, int tiles_n, int tile0,
   return check_launch("sk fixup");
 }
 
-int launch_gemm_sk(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
-                   void* ws, size_t ws_bytes, hipStream_t st) {
-  if (M == 0) return IFD_OK;
-  if (!gemm_sk_applies(M, N, K, mode)) return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: shape M=%d N=%d K=%d", M, N, K);
-  const SkPlan pl = gemm_sk_plan(M, N, K);
-  const size_t need = gemm_sk_workspace(M, N, K, mode);
+template <int BITS>
+static int launch_sk_bits(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                          void* ws, size_t ws_bytes, hipStream_t st) {
+  const SkPlan pl = gemm_sk_plan(M, N, K, BITS);
+  const size_t need = sk_part_bytes(pl), wbytes = BITS == 8 ? t64x8_bytes(N, K) : t64_bytes(N, K);
   if (need > ws_bytes || !ws)
     return fail(IFD_ERR_WORKSPACE, "gemm_sk needs %zu bytes of workspace, got %zu", need, ws_bytes);
   if (need >= (size_t)1 << 31) return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: partials past 2 GiB");
-  if (t64_bytes(N, K) >= ((size_t)1 << 31) || (size_t)M * lda * 2 >= ((size_t)1 << 31))
+  if (wbytes >= ((size_t)1 << 31) || (size_t)M * lda * 2 >= ((size_t)1 << 31))
     return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: operands past 2 GiB");
+  if (((uint64_t)pl.tiles_m * pl.tiles_n * pl.G + 1) * (pl.nblk + 1) >= ((uint64_t)1 << 32))
+    return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: too many units");
   // the fixup kernel runs when some tile is cut
   const long tiles = (long)pl.tiles_m * pl.tiles_n, U = tiles * pl.G;
   bool fixup = false;
   for (long t = 0; t < tiles && !fixup; t++)
     fixup = sk_block_of(t * pl.G + pl.G - 1, pl.nblk, U) != sk_block_of(t * pl.G, pl.nblk, U);
-  GemmSkArgs a{A, lda, (const uint8_t*)wt, (uint32_t)t64_bytes(N, K), N, K, C, ldc, M, mode, (float*)ws, (uint32_t)need,
+  GemmSkArgs a{A, lda, (const uint8_t*)wt, (uint32_t)wbytes, N, K, C, ldc, M, mode, (float*)ws, (uint32_t)need,
                pl.tiles_m, pl.tiles_n, pl.G, pl.nblk, mode == kModeSwiglu ? N / 64 : 0, 0, (int)tiles, nullptr, 0, 0};
-  if (pl.MT == 1) return launch_sk_cfg<1>(a, fixup, st);
-  if (pl.MT == 2) return launch_sk_cfg<2>(a, fixup, st);
-  return launch_sk_cfg<4>(a, fixup, st);
+  if (pl.MT == 1) return launch_sk_cfg<1, BITS>(a, fixup, st);
+  if (pl.MT == 2) return launch_sk_cfg<2, BITS>(a, fixup, st);
+  return launch_sk_cfg<4, BITS>(a, fixup, st);
+}
+
+int launch_gemm_sk(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                   void* ws, size_t ws_bytes, hipStream_t st) {
+  if (M == 0) return IFD_OK;
+  if (!gemm_sk_applies(M, N, K, mode)) return fail(IFD_ERR_UNSUPPORTED, "gemm_sk: shape M=%d N=%d K=%d", M, N, K);
+  return launch_sk_bits<4>(A, lda, wt, N, K, C, ldc, M, mode, ws, ws_bytes, st);
+}
+
+int launch_gemm_sk8(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                    void* ws, size_t ws_bytes, hipStream_t st) {
+  if (M == 0) return IFD_OK;
+  if (K % kGroup || (mode == kModeSwiglu && N % 256))
+    return fail(IFD_ERR_UNSUPPORTED, "gemm_sk8: shape N=%d K=%d", N, K);
+  return launch_sk_bits<8>(A, lda, wt, N, K, C, ldc, M, mode, ws, ws_bytes, st);
 }
 
 }  // namespace ifd

@@ -90,6 +90,10 @@ int launch_sk_fixup_rows(const float* part, int tiles_m, int tiles_n, int tile0,
 size_t w4a8_t_workspace(int M, int N, int K);
 int launch_w4a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   void* ws, size_t ws_bytes, hipStream_t st);
+// The same stream-K GEMM on T64x8 weights (8-bit codes, dequantized to bf16(s q + b)); any M >= 1.
+size_t gemm_sk8_workspace(int M, int N, int K);
+int launch_gemm_sk8(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                    void* ws, size_t ws_bytes, hipStream_t st);
 // T64x8 (t64.h): the repack of an MLX 8-bit linear, and W8A8 on it with per-token int8 activations.
 int launch_pack_t64x8(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr,
                       void* out, hipStream_t st);

@@ -135,6 +135,19 @@ def pack_t64x8(W: QLinear) -> T64x8Linear:
     return T64x8Linear(wt, W.N, W.K)
 
 
+def gemm_t64x8(A: torch.Tensor, W: T64x8Linear, C: Optional[torch.Tensor] = None, mode: int = 0) -> torch.Tensor:
+    """C (mode) = A . W^T for T64x8 (8-bit) weights, bf16(s q + b) dequant."""
+    M, K = A.shape
+    assert K == W.K and A.dtype == torch.bfloat16 and A.is_contiguous()
+    if C is None:
+        C = torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=A.device)
+    need = lib().ifd_gemm_t64x8_workspace(M, W.N, W.K)
+    ws = workspace(need, A.device) if need else None
+    check(lib().ifd_gemm_t64x8(_p(A), K, _p(W.wt), W.N, W.K, _p(C), C.shape[1], M, mode, _p(ws),
+                               ws.numel() if ws is not None else 0, _stream()))
+    return C
+
+
 def gemm_t64x8_w8a8(U: torch.Tensor, XS: torch.Tensor, W: T64x8Linear, C: Optional[torch.Tensor] = None,
                     mode: int = 0) -> torch.Tensor:
     """C (mode) = W8A8 product of per-token int8 activations (ops.a8_quant(A, True)) with T64x8 weights."""

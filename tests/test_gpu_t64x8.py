@@ -99,3 +99,35 @@ def test_gemm_t64x8_w8a8_config3_sampled():
     err = np.sqrt(np.mean((got - ref) ** 2)) / np.sqrt(np.mean(ref ** 2))
     assert err < 1e-3, err
 
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 200, 512), (32, 1024, 2048), (33, 384, 1024), (64, 640, 17408),
+                                   (100, 256, 5120), (128, 5120, 1024), (300, 1000, 256), (1, 64, 64)])
+def test_gemm_t64x8_bf16(M, N, K):
+    """The stream-K bf16 GEMM on T64x8 weights against MLX's 8-bit qmm semantics (bf16(s q + b) dequant, fp32 sums),
+    1e-2 RMS, all store modes: 32-, 64- and 128-row tiles, tiles cut into many pieces (K = 17408), ragged N and M."""
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear8(N, K, seed=M + 50, bias="free")
+    A = gen.activations(M, K, seed=M + 51)
+    T = ops.pack_t64x8(g.qlinear(wq, s, b, bits=8))
+    Y = orc.qmm(A, wq, s, b, bits=8)
+    C0 = gen.activations(M, N, seed=M + 52)
+    for mode in (0, 1, 2):
+        C = g.dev(C0) if mode == 1 else None
+        out = g.host(ops.gemm_t64x8(g.dev(A), T, C, mode=mode))
+        gen.check_out(out, Y + gen.bf16_to_f32(C0) if mode == 1 else Y, 1e-2, (M, N, K, mode), fp32=mode == 2)
+
+
+def test_gemm_t64x8_bf16_matches_mlx_layout():
+    """At M = 128 on the decode MLP's gate_up shape (N = 34816, K = 5120) the T64x8 GEMM and the MLX-layout 8-bit
+    GEMM (ifd_gemm_w8, the same dequant rounding) agree; the oracle on 8 sampled rows."""
+    g, ops = _gu(), _ops()
+    M, N, K = 128, 34816, 5120
+    codes, wq, s, b = gen.qlinear8(N, K, seed=90)
+    A = gen.activations(M, K, seed=91)
+    W = g.qlinear(wq, s, b, bits=8)
+    out = g.host(ops.gemm_t64x8(g.dev(A), ops.pack_t64x8(W), mode=2))
+    ref = g.host(ops.gemm(g.dev(A), W, mode=2))
+    gen.check_out(out, ref, 1e-3, ("vs MLX layout",), fp32=True)
+    rows = np.linspace(0, M - 1, 8).astype(int)
+    gen.check_out(out[rows], orc.qmm(A[rows], wq, s, b, bits=8), 1e-2, ("rows",), fp32=True)
