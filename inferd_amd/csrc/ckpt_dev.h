@@ -46,7 +46,8 @@ inline void upload(Gpu& g, void* dst, const void* src, size_t bytes) {
 }  // namespace detail
 
 // A host linear on the device: [wq | s | b] in one buffer (bits 16: the bf16 rows), plus the T64 copy when t64 and the
-// shape allows it (4-bit, K % 256 == 0). The upload is synchronous with respect to the host arrays.
+// shape allows it (4-bit with K % 256 == 0: T64; 8-bit: T64x8). The upload is synchronous with respect to the host
+// arrays.
 inline QLinear upload_qlinear(Gpu& g, const HostQLinear& h, bool t64 = true) {
   QLinear q;
   q.N = h.N, q.K = h.K, q.bits = h.bits;
@@ -64,6 +65,12 @@ inline QLinear upload_qlinear(Gpu& g, const HostQLinear& h, bool t64 = true) {
     if (t64 && h.bits == 4 && h.K % 256 == 0) {
       void* t = g.alloc(ifd_t64_bytes(h.N, h.K, 1));
       ok(ifd_pack_t64(q.wq.ptr<uint32_t>(), q.s.ptr<uint16_t>(), q.b.ptr<uint16_t>(), h.N, h.K, 0, 0u, 1, t, g.stream),
+         "load");
+      q.t64 = BufRef(t);
+    }
+    if (t64 && h.bits == 8 && h.K % 64 == 0) {
+      void* t = g.alloc(ifd_t64x8_bytes(h.N, h.K));
+      ok(ifd_pack_t64x8(q.wq.ptr<uint32_t>(), q.s.ptr<uint16_t>(), q.b.ptr<uint16_t>(), h.N, h.K, 0, 0u, t, g.stream),
          "load");
       q.t64 = BufRef(t);
     }

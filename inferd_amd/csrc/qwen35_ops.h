@@ -73,7 +73,7 @@ struct Enc {
 // K-slice).
 struct QLinear {
   BufRef wq, s, b;
-  BufRef t64;            // optional T64 copy (ifd_pack_t64), read by gemm() when present
+  BufRef t64;            // optional T64 copy (ifd_pack_t64; 8 bits: T64x8, ifd_pack_t64x8), read by gemm() when present
   int ldk = 0;           // a K-slice view: the full matrix's row length; 0 = K
   bool flipped = false;  // codes stored q ^ 8 (4 bits) or q ^ 0x80 (8 bits) (ifd_flip_w4); readers flip back
   int N = 0, K = 0, bits = 4;
@@ -93,7 +93,7 @@ inline QLinear rows_of(const QLinear& q, int lo, int n) {
 }
 
 // Input columns [k0, k0 + kn) (multiples of 64). The T64 copy is group-major, so a K-slice of it is the tiles from
-// group k0 / 64 on: kept when k0 and kn are multiples of 256 (whole T64 GEMM chunks).
+// group k0 / 64 on: kept when k0 and kn are multiples of 256 (whole T64 GEMM chunks; any 64-group for T64x8).
 inline QLinear kslice_of(const QLinear& q, int k0, int kn) {
   QLinear r = q;
   r.ldk = q.ldk ? q.ldk : q.K;
@@ -101,8 +101,9 @@ inline QLinear kslice_of(const QLinear& q, int k0, int kn) {
   r.wq = q.wq.at((size_t)k0 * q.bits / 8);
   r.s = q.s.at((size_t)k0 / 64 * 2);
   r.b = q.b.at((size_t)k0 / 64 * 2);
-  if (q.t64 && k0 % 256 == 0 && kn % 256 == 0)
-    r.t64 = q.t64.at((size_t)(k0 / 64) * ((q.N + 31) / 32) * 1152);
+  const int kq = q.bits == 8 ? 64 : 256, tile = q.bits == 8 ? 2176 : 1152;
+  if (q.t64 && k0 % kq == 0 && kn % kq == 0)
+    r.t64 = q.t64.at((size_t)(k0 / 64) * ((q.N + 31) / 32) * tile);
   else
     r.t64 = BufRef();
   return r;
@@ -255,6 +256,14 @@ struct Qwen35 {
     }
     if (a8_ready) die("gemm", "a8_ready with a non-W4A8 GEMM");  // qwen35.h:1477
     if (W.bits == 8) {  // the reference's qmv8 / 8-bit qmm routes (qwen35.h:1520-1558)
+      if (W.t64 && M > 32) {  // the qmm route's rounding, on the T64x8 copy
+        const size_t need = ifd_gemm_t64x8_workspace(M, W.N, W.K);
+        if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
+        ok(ifd_gemm_t64x8(A.ptr<void>(), W.K, W.t64.ptr<void>(), W.N, W.K, C.ptr<void>(), W.N, M, mode,
+                          splitk.ptr<void>(), splitk_bytes, e.stream),
+           "gemm");
+        return;
+      }
       const size_t need = ifd_gemm_w8_workspace(M, W.N, W.K);
       if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
       ok(ifd_gemm_w8(A.ptr<void>(), W.K, W.wq.ptr<uint32_t>(), W.s.ptr<uint16_t>(), W.b.ptr<uint16_t>(), W.N, W.K,

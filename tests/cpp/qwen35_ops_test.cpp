@@ -383,6 +383,45 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
       }
       (void)hipFree(W8.wq.buf), (void)hipFree(W8.s.buf), (void)hipFree(W8.b.buf);
     }
+    // a T64x8 copy: the 8-bit qmm route above 32 rows runs on it (same rounding), whole and as a K-slice
+    QLinear W8;
+    W8.wq = upload(wq8), W8.s = upload(s8), W8.b = upload(b8);
+    W8.N = N, W8.K = K, W8.bits = 8;
+    void* t = nullptr;
+    hip_ok(hipMalloc(&t, ifd_t64x8_bytes(N, K)), "t64x8");
+    ok(ifd_pack_t64x8(W8.wq.ptr<uint32_t>(), W8.s.ptr<uint16_t>(), W8.b.ptr<uint16_t>(), N, K, 0, 0, t, e.stream),
+       "pack_t64x8");
+    W8.t64 = BufRef(t);
+    for (int M : {33, 200}) {
+      const auto A = activations(M, K, rng);
+      std::vector<float> y((size_t)M * N);
+      orc_qmm_b(A.data(), K, wq8.data(), s8.data(), b8.data(), N, K, 8, 0, y.data(), M, 0);
+      BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
+      m.gemm(e, dA, W8, dC, M, 0);
+      const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), y, false);
+      report(err <= 1e-2, "gemm 8-bit T64x8 M=" + std::to_string(M), err);
+      (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+    }
+    {
+      const int M = 40, k0 = 192, kn = 320;
+      QLinear Ws = kslice_of(W8, k0, kn);
+      const auto A = activations(M, kn, rng);
+      std::vector<uint32_t> ws((size_t)N * kn / 4);
+      std::vector<uint16_t> ss((size_t)N * kn / 64), bs(ss.size());
+      for (int n = 0; n < N; n++) {
+        memcpy(&ws[(size_t)n * kn / 4], &wq8[(size_t)n * K / 4 + k0 / 4], kn);
+        memcpy(&ss[(size_t)n * kn / 64], &s8[(size_t)n * K / 64 + k0 / 64], kn / 32);
+        memcpy(&bs[(size_t)n * kn / 64], &b8[(size_t)n * K / 64 + k0 / 64], kn / 32);
+      }
+      std::vector<float> y((size_t)M * N);
+      orc_qmm_b(A.data(), kn, ws.data(), ss.data(), bs.data(), N, kn, 8, 0, y.data(), M, 0);
+      BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)M * N));
+      m.gemm(e, dA, Ws, dC, M, 0);
+      const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), y, false);
+      report(err <= 1e-2 && (bool)Ws.t64, "gemm 8-bit kslice_of (T64x8)", err);
+      (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+    }
+    (void)hipFree(t), (void)hipFree(W8.wq.buf), (void)hipFree(W8.s.buf), (void)hipFree(W8.b.buf);
   }
 }
 
@@ -536,9 +575,9 @@ void test_load(const std::string& dir, std::mt19937& rng) {
   }
   const HostQLinear h8 = load_qlinear_bf16(ck, {"x.weight"}, 8);
   const QLinear W8 = load_qlinear_bf16_q8(g, ck, {"x.weight"}, 8);
-  report(W8.bits == 8 && !W8.t64 && same_as_device(h8.wq, W8.wq) && same_as_device(h8.s, W8.s) &&
+  report(W8.bits == 8 && (bool)W8.t64 && same_as_device(h8.wq, W8.wq) && same_as_device(h8.s, W8.s) &&
              same_as_device(h8.b, W8.b),
-         "load_qlinear_bf16_q8 upload (8-bit, no T64 copy)", 0);
+         "load_qlinear_bf16_q8 upload (8-bit, T64x8 packed)", 0);
   const HostQLinear h16 = load_qlinear(ck, {"x"});
   const QLinear W16 = load_qlinear(g, ck, {"x"});
   report(W16.bits == 16 && same_as_device(h16.w16, W16.wq), "load_qlinear bf16 passthrough upload", 0);
