@@ -301,7 +301,7 @@ def main():
                                    frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
             # the same layers repacked as T64x8, on the stream-K bf16 GEMM
             Tg = [ops.pack_t64x8(w) for w in Wg]
-            for M in (32, 128):
+            for M in (1, 8, 32, 128):
                 Ag = act(M, 5120)
                 Cg = torch.empty((M, 34816), dtype=torch.bfloat16, device=dev)
                 ms = timed(lambda i: ops.gemm_t64x8(Ag, Tg[i % ncg], Cg), 40, 5)

@@ -191,9 +191,10 @@ int ifd_gemm_t64_w4a8(const int8_t* U, const float* XS, int per_token, const voi
 size_t ifd_t64x8_bytes(int N, int K);
 int ifd_pack_t64x8(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr,
                    void* out, void* stream);
-/* C (mode) = A . W^T with W in T64x8 layout (K % 64 == 0), every weight dequantized to bf16(s q + b) with fp32
- * accumulation: MLX's 8-bit qmm (quantized.h:528-535, the reference's affine_qmm_t at BITS = 8) on a stream-K
- * bf16 MFMA kernel, for every M (meant for M > 16: decode rows go to ifd_gemm_w8's qmv arithmetic). */
+/* C (mode) = A . W^T with W in T64x8 layout (K % 64 == 0). M <= 16 with K % 128 == 0: the reference's qmv8
+ * arithmetic (core.metal:175-248: per group s * sum q x + b * sum x in fp32) on the T64 decode GEMV; otherwise every
+ * weight dequantized to bf16(s q + b) with fp32 accumulation, MLX's 8-bit qmm (quantized.h:528-535, the reference's
+ * affine_qmm_t at BITS = 8), on the stream-K bf16 MFMA kernel. */
 size_t ifd_gemm_t64x8_workspace(int M, int N, int K);
 int ifd_gemm_t64x8(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                    void* workspace, size_t ws_bytes, void* stream);

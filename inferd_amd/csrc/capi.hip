@@ -281,9 +281,12 @@ int ifd_pack_t64x8(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int
   return launch_pack_t64x8(wq, s, b, N, K, ldk ? ldk : K, xr, out, S(stream));
 }
 
+// the T64x8 decode GEMV serves M <= 16 when K % 128 == 0, the stream-K GEMM the rest
+static bool t64x8_qmv(int M, int K) { return M <= 16 && K % 128 == 0; }
+
 size_t ifd_gemm_t64x8_workspace(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  return with_header(gemm_sk8_workspace(M, N, K));
+  return with_header(t64x8_qmv(M, K) ? qmv_t_workspace(M, N, K, 0, 8) : gemm_sk8_workspace(M, N, K));
 }
 
 int ifd_gemm_t64x8(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
@@ -295,6 +298,8 @@ int ifd_gemm_t64x8(const void* A, int lda, const void* wt, int N, int K, void* C
   IFD_CHECK(A && wt && C && aligned(A, 16) && aligned(wt, 16), "null or misaligned pointer");
   IFD_CHECK(!workspace || aligned(workspace, 16), "workspace must be 16-byte aligned");
   const WsView w = ws_view(workspace, ws_bytes);
+  if (t64x8_qmv(M, K))
+    return launch_qmv_t8((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, w.cnt, w.body, w.bytes, S(stream));
   return launch_gemm_sk8((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, w.body, w.bytes, S(stream));
 }
 

@@ -68,7 +68,7 @@ int launch_epilogue(const void* ws, int S, int M, int N, void* C, int ldc, int m
 // T64 layout (t64.h).
 int launch_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int ldk, uint32_t xr,
                     int E, void* out, hipStream_t st);
-size_t qmv_t_workspace(int M, int N, int K, int mode);
+size_t qmv_t_workspace(int M, int N, int K, int mode, int bits = 4);
 size_t gemm_t_workspace(int M, int N, int K, int mode);
 // 256-row-tile prefill GEMM on T64 weights (modes 0-2); gemm_t routes prefill shapes to it.
 size_t gemm_t8_workspace(int M, int N, int K);
@@ -90,6 +90,10 @@ int launch_sk_fixup_rows(const float* part, int tiles_m, int tiles_n, int tile0,
 size_t w4a8_t_workspace(int M, int N, int K);
 int launch_w4a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   void* ws, size_t ws_bytes, hipStream_t st);
+// The decode GEMV on T64x8 weights (M <= 16, K % 128 == 0; the qmv8 arithmetic s sum q x + b sum x); its workspace
+// is qmv_t_workspace(M, N, K, mode, 8).
+int launch_qmv_t8(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                  unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st);
 // The same stream-K GEMM on T64x8 weights (8-bit codes, dequantized to bf16(s q + b)); any M >= 1.
 size_t gemm_sk8_workspace(int M, int N, int K);
 int launch_gemm_sk8(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,

@@ -84,8 +84,11 @@ __device__ __forceinline__ u32x4 t64_bf16_off128(uint32_t w) {
 }
 
 
-template <int RACT>
+// BITS = 8: T64x8 tiles (two 1 KB code halves per lane group; the exact q as bf16 and the bias b, the reference's
+// qmv8 arithmetic s * sum q x + b * sum x, core.metal:175-248).
+template <int RACT, int BITS>
 __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
+  constexpr int NH = BITS / 4, TILEB = BITS == 8 ? kT64x8Tile : kT64Tile, CODES = BITS == 8 ? kT64x8Codes : kT64Codes;
   extern __shared__ __align__(16) uint16_t lds[];
   __shared__ unsigned s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -100,18 +103,19 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   // stream starts one memory latency earlier
   const int band = blockIdx.x * 4 + wave;
   const bool live = band < nb;
-  const uint8_t* tcol = p.wt + (size_t)(live ? band : 0) * kT64Tile;  // + g * nb * kT64Tile
-  const size_t gstride = (size_t)nb * kT64Tile;
+  const uint8_t* tcol = p.wt + (size_t)(live ? band : 0) * TILEB;  // + g * nb * TILEB
+  const size_t gstride = (size_t)nb * TILEB;
   struct Blk {
-    u32x4 w[kTB];
+    u32x4 w[kTB][NH];
     uint32_t sb[kTB];
   };
   auto load_blk = [&](Blk& B, int g) {
 #pragma unroll
     for (int i = 0; i < kTB; i++) {
       const uint8_t* t = tcol + (size_t)(g + i) * gstride;
-      B.w[i] = *(const u32x4*)(t + 16 * lane);
-      B.sb[i] = *(const uint32_t*)(t + kT64Codes + 4 * j);
+#pragma unroll
+      for (int hh = 0; hh < NH; hh++) B.w[i][hh] = *(const u32x4*)(t + 1024 * hh + 16 * lane);
+      B.sb[i] = *(const uint32_t*)(t + CODES + 4 * j);
     }
   };
   Blk b0, b1;
@@ -167,10 +171,16 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
       if (RACT > 4) x1 = *(const float4*)(Xs + gl * 16 + 8 + 4 * h);
       f32x16 P = zero16();
 #pragma unroll
-      for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], t64_bf16_off128(B.w[i][t]), P);
+      for (int t = 0; t < 4; t++) {
+        // MFMA step t: codes of k = 32 h + 8 t .. + 7 as exact bf16, 128 + q (4 bits) or q (8 bits: byte ^ 0x80)
+        const u32x4 bq = BITS == 4 ? t64_bf16_off128(B.w[i][0][t])
+                                   : codes8_bf16(B.w[i][t / 2 % NH][2 * (t % 2)] ^ 0x80808080u,
+                                                 B.w[i][t / 2 % NH][2 * (t % 2) + 1] ^ 0x80808080u);
+        P = mfma_bf16(af[t], bq, P);
+      }
       const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       const float sc = bf2f((uint16_t)(B.sb[i] & 0xFFFFu)), bi = bf2f((uint16_t)(B.sb[i] >> 16));
-      const float bp = __builtin_fmaf(-128.f, sc, bi);
+      const float bp = BITS == 4 ? __builtin_fmaf(-128.f, sc, bi) : bi;
 #pragma unroll
       for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[r]));
     }
@@ -276,9 +286,9 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
 struct TPlan {
   int S, gps;
 };
-static TPlan qmv_t_plan(int M, int N, int K) {
+static TPlan qmv_t_plan(int M, int N, int K, int bits = 4) {
   const int G = K / kGroup, waves = 4 * ((t64_bands(N) + 3) / 4);
-  const long target = (long)N * K / 2 <= (64l << 20) ? 2048 : 6144;
+  const long target = (long)N * K / 8 * bits <= (64l << 20) ? 2048 : 6144;
   long S = (target + waves - 1) / waves;
   S = std::max<long>(S, ((long)M * K * 2 + 40959) / 40960);
   S = std::min<long>(S, std::max(1, G / (2 * kTB)));
@@ -296,17 +306,18 @@ static bool qmv_t_fixup(int N, int mode, int S) {
   return mode != kModeSwiglu || (N % 256 == 0);
 }
 
-size_t qmv_t_workspace(int M, int N, int K, int mode) {
+size_t qmv_t_workspace(int M, int N, int K, int mode, int bits) {
   if (M > 16) return 0;
-  return epilogue_ws_bytes(qmv_t_plan(M, N, K).S, M, N, mode);
+  return epilogue_ws_bytes(qmv_t_plan(M, N, K, bits).S, M, N, mode);
 }
 
-int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
-                 unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
+template <int BITS>
+static int launch_qmv_t_bits(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M,
+                             int mode, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
   if (M == 0) return IFD_OK;
   if (M > 16) return fail(IFD_ERR_UNSUPPORTED, "T64 decode kernel takes M <= 16");
   if (K % (kGroup * kTB)) return fail(IFD_ERR_ARG, "T64 decode needs K %% %d == 0 (K=%d)", kGroup * kTB, K);
-  const TPlan pl = qmv_t_plan(M, N, K);
+  const TPlan pl = qmv_t_plan(M, N, K, BITS);
   const size_t need = epilogue_ws_bytes(pl.S, M, N, mode);
   if (need > ws_bytes || (need && !ws))
     return fail(IFD_ERR_WORKSPACE, "qmv_t64 needs %zu bytes of workspace, got %zu", need, ws_bytes);
@@ -331,11 +342,21 @@ int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void*
   const size_t lds = ((size_t)M * (Kz + 8) * 2 + 15) / 16 * 16 + (size_t)pl.gps * 16 * sizeof(float);
   if (lds > 64 * 1024) return fail(IFD_ERR_UNSUPPORTED, "qmv_t64: %zu bytes of LDS needed", lds);
   dim3 grid((t64_bands(N) + 3) / 4, pl.S), block(256);
-  if (M <= 8) hipLaunchKernelGGL(k_qmv_t<4>, grid, block, lds, st, p);
-  else hipLaunchKernelGGL(k_qmv_t<8>, grid, block, lds, st, p);
+  if (M <= 8) hipLaunchKernelGGL((k_qmv_t<4, BITS>), grid, block, lds, st, p);
+  else hipLaunchKernelGGL((k_qmv_t<8, BITS>), grid, block, lds, st, p);
   IFD_TRY(check_launch("qmv_t64"));
   if (fix) return IFD_OK;
   return launch_epilogue(ws, pl.S, M, N, C, ldc, mode, st);
+}
+
+int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                 unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
+  return launch_qmv_t_bits<4>(A, lda, wt, N, K, C, ldc, M, mode, cnt, ws, ws_bytes, st);
+}
+
+int launch_qmv_t8(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
+                  unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
+  return launch_qmv_t_bits<8>(A, lda, wt, N, K, C, ldc, M, mode, cnt, ws, ws_bytes, st);
 }
 
 }  // namespace ifd

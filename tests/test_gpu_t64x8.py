@@ -131,3 +131,21 @@ def test_gemm_t64x8_bf16_matches_mlx_layout():
     gen.check_out(out, ref, 1e-3, ("vs MLX layout",), fp32=True)
     rows = np.linspace(0, M - 1, 8).astype(int)
     gen.check_out(out[rows], orc.qmm(A[rows], wq, s, b, bits=8), 1e-2, ("rows",), fp32=True)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 200, 512), (8, 5120, 5120), (16, 384, 17408), (5, 1000, 2048),
+                                   (1, 34816, 5120)])
+def test_gemm_t64x8_decode(M, N, K):
+    """M <= 16 (K % 128 == 0) runs the T64 decode GEMV on T64x8 tiles: the reference's qmv8 arithmetic (per group
+    s * sum q x + b * sum x, fp32), 1e-2 RMS against the oracle's qmv, all store modes; K split with the in-kernel
+    fixup on the long shapes (the workspace header is checked back at zero after every GPU test)."""
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear8(N, K, seed=M + 60, bias="free")
+    A = gen.activations(M, K, seed=M + 61)
+    T = ops.pack_t64x8(g.qlinear(wq, s, b, bits=8))
+    Y = orc.qmv(A, wq, s, b, bits=8)
+    C0 = gen.activations(M, N, seed=M + 62)
+    for mode in (0, 1, 2):
+        C = g.dev(C0) if mode == 1 else None
+        out = g.host(ops.gemm_t64x8(g.dev(A), T, C, mode=mode))
+        gen.check_out(out, Y + gen.bf16_to_f32(C0) if mode == 1 else Y, 1e-2, (M, N, K, mode), fp32=mode == 2)
