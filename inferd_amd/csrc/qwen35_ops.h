@@ -256,8 +256,9 @@ struct Qwen35 {
     }
     if (a8_ready) die("gemm", "a8_ready with a non-W4A8 GEMM");  // qwen35.h:1477
     if (W.bits == 8) {  // the reference's qmv8 / 8-bit qmm routes (qwen35.h:1520-1558)
-      // on the T64x8 copy: the qmv8 arithmetic up to 16 rows, the qmm route's rounding above 32
-      if (W.t64 && (M > 32 || (M <= 16 && W.K % 128 == 0))) {
+      // On the T64x8 copy: the qmv8 arithmetic up to 16 rows, the 8-bit qmm rounding above, which is the
+      // reference's route past qmv_max (= 2 by default, qwen35.h:1049, 1525-1558).
+      if (W.t64) {
         const size_t need = ifd_gemm_t64x8_workspace(M, W.N, W.K);
         if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
         ok(ifd_gemm_t64x8(A.ptr<void>(), W.K, W.t64.ptr<void>(), W.N, W.K, C.ptr<void>(), W.N, M, mode,

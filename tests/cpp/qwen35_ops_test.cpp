@@ -383,8 +383,8 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
       }
       (void)hipFree(W8.wq.buf), (void)hipFree(W8.s.buf), (void)hipFree(W8.b.buf);
     }
-    // a T64x8 copy: the 8-bit routes up to 16 rows (qmv8 arithmetic) and above 32 (qmm rounding) run on it, whole
-    // and as a K-slice
+    // a T64x8 copy: every 8-bit route runs on it, qmv8 arithmetic up to 16 rows and qmm rounding above, whole and
+    // as a K-slice
     QLinear W8;
     W8.wq = upload(wq8), W8.s = upload(s8), W8.b = upload(b8);
     W8.N = N, W8.K = K, W8.bits = 8;
@@ -393,7 +393,7 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
     ok(ifd_pack_t64x8(W8.wq.ptr<uint32_t>(), W8.s.ptr<uint16_t>(), W8.b.ptr<uint16_t>(), N, K, 0, 0, t, e.stream),
        "pack_t64x8");
     W8.t64 = BufRef(t);
-    for (int M : {1, 16, 33, 200}) {
+    for (int M : {1, 16, 24, 33, 200}) {
       const auto A = activations(M, K, rng);
       std::vector<float> y((size_t)M * N);
       (M <= 16 ? orc_qmv_b : orc_qmm_b)(A.data(), K, wq8.data(), s8.data(), b8.data(), N, K, 8, 0, y.data(), M, 0);
