@@ -190,6 +190,8 @@ struct Qwen35 {
           need = std::max(need, ifd_gemm_t64_workspace(T, H, shared_inter));
           need = std::max(need, ifd_qmm_w4a8_workspace(T, 2 * shared_inter, H));
           need = std::max(need, ifd_qmm_w4a8_workspace(T, H, shared_inter));
+          need = std::max(need, ifd_gemm_t64x8_workspace(T, 2 * shared_inter, H));  // an 8-bit shared expert
+          need = std::max(need, ifd_gemm_t64x8_workspace(T, H, shared_inter));
         }
       }
       x = alloc((size_t)max_rows * H * 2);
