@@ -142,7 +142,9 @@ size_t ifd_gemm_t64_workspace(int M, int N, int K);
 int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                  void* workspace, size_t ws_bytes, void* stream);
 /* Gate/up projection with its SwiGLU: W (T64) holds [gate (N/2) | up (N/2)] rows and H [M][N/2] (row stride ldh)
- * receives silu_mul of the bf16 product, bit-identical to ifd_gemm_t64 (mode 0) followed by ifd_silu_mul. Replaces
+ * receives silu_mul of the bf16 product: bit-identical to ifd_gemm_t64 (mode 0) followed by ifd_silu_mul for
+ * M <= 16 and on the prefill tiles; on the stream-K rows between, the fused tiles cut K at other places than the
+ * plain GEMM's, so a gate or up sum may differ from it by one bf16 step before the SwiGLU. Replaces
  * the reference's gemm + silu_mul pair (qwen35.h:1910-1912, shared expert; qwen35.h:2868-2878, dense MLP) with one
  * call that never stores the [M][N] product when K is split (the SwiGLU runs in the split-K reduction).
  * N % 16 == 0, ldh % 8 == 0, A, H and the workspace 16-byte aligned. */
