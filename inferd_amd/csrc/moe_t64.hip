@@ -415,8 +415,10 @@ int launch_moe_gather_qmm_t64(const uint16_t* A, int lda, const int* perm, int d
   if (div < 1 || div > 64) return fail(IFD_ERR_ARG, "moe_gather_qmm_t64: div=%d must be in [1, 64]", div);
   // perm[q] / div as a multiply-high: exact for perm values below 2^32 / div (2^26 at div = 64)
   const uint32_t div_m = div == 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + div - 1) / div);
-  // plain products with output columns in whole 512-column tiles take the wide form (two bands per wave)
-  const bool wide = !silu && NO % 512 == 0;
+  // plain products with output columns in whole 512-column tiles take the wide form (two bands per wave) on 64-row
+  // tiles; 32-row tiles (few rows per expert) keep 256-column items, twice as many, which spread more evenly over
+  // the CUs (config 4 at T = 128: 238 against 244 us, same box)
+  const bool wide = !silu && NO % 512 == 0 && tile_rows == 64;
   const int nct = NO / (wide ? 512 : 256);
   if (nct & (nct - 1)) return fail(IFD_ERR_UNSUPPORTED, "moe_gather_qmm_t64: %d column tiles (not a power of 2)", nct);
   // every perm value is a routed slot below rows, so a sorted row reads one of the first (rows - 1) / div + 1 rows
