@@ -149,3 +149,50 @@ def test_gemm_t64x8_decode(M, N, K):
         C = g.dev(C0) if mode == 1 else None
         out = g.host(ops.gemm_t64x8(g.dev(A), T, C, mode=mode))
         gen.check_out(out, Y + gen.bf16_to_f32(C0) if mode == 1 else Y, 1e-2, (M, N, K, mode), fp32=mode == 2)
+
+
+def test_t64x8_strides_through_the_c_abi():
+    """The stride arguments of the T64x8 entry points, through the C ABI: ifd_pack_t64x8 from a K-slice view of a
+    wider MLX matrix (ldk = 2 K, columns [K, 2 K)) packs the same bytes as the sliced matrix, and both GEMMs store
+    rows ldc > N apart without touching the gap."""
+    g, ops = _gu(), _ops()
+    from inferd_amd._lib import lib
+    N, K = 320, 1024
+    codes, wq, s, b = gen.qlinear8(N, 2 * K, seed=120, bias="free")
+    W2 = g.qlinear(wq, s, b, bits=8)  # [N][2K]
+    T = torch.empty((lib().ifd_t64x8_bytes(N, K),), dtype=torch.uint8, device="cuda")
+    # the view's first element is column K: wq words K / 4, scales K / 64
+    wq_v = W2.wq.view(-1)[K // 4:]
+    s_v, b_v = W2.s.view(-1)[K // 64:], W2.b.view(-1)[K // 64:]
+    assert lib().ifd_pack_t64x8(ops._p(wq_v), ops._p(s_v), ops._p(b_v), N, K, 2 * K, 0, ops._p(T), ops._stream()) == 0
+    torch.cuda.synchronize()
+    cs, ss, bs = codes[:, K:], s[:, K // 64:], b[:, K // 64:]
+    assert np.array_equal(g.host(T), gen.pack_t64x8(np.ascontiguousarray(cs), np.ascontiguousarray(ss),
+                                                     np.ascontiguousarray(bs)))
+    wq_s = np.ascontiguousarray(wq[:, K // 4:])
+    ldc = N + 40
+    for M, w8a8 in ((5, False), (40, False), (150, False), (150, True)):
+        A = gen.activations(M, K, seed=M + 121)
+        C = torch.full((M, ldc), 7.0, dtype=torch.float32, device="cuda")
+        if w8a8:
+            U, XS = orc.a8_quant(A, True)
+            Y = orc.w4a8(U, XS, wq_s, np.ascontiguousarray(ss), np.ascontiguousarray(bs), bits=8)
+            need = lib().ifd_gemm_t64x8_w8a8_workspace(M, N, K)
+            ws = ops.workspace(need, C.device)
+            dU, dXS = g.dev(U), g.dev(XS)  # held until the kernel has run (a freed block is reused at once)
+            rc = lib().ifd_gemm_t64x8_w8a8(ops._p(dU), ops._p(dXS), 1, ops._p(T), N, K, ops._p(C), ldc, M, 2,
+                                           ops._p(ws), ws.numel(), ops._stream())
+            torch.cuda.synchronize()
+        else:
+            fn = orc.qmv if M <= 16 else orc.qmm
+            Y = fn(A, wq_s, np.ascontiguousarray(ss), np.ascontiguousarray(bs), bits=8)
+            need = lib().ifd_gemm_t64x8_workspace(M, N, K)
+            ws = ops.workspace(need, C.device) if need else None
+            dA = g.dev(A)
+            rc = lib().ifd_gemm_t64x8(ops._p(dA), K, ops._p(T), N, K, ops._p(C), ldc, M, 2, ops._p(ws),
+                                      ws.numel() if ws is not None else 0, ops._stream())
+            torch.cuda.synchronize()
+        assert rc == 0, lib().ifd_last_error()
+        out = g.host(C)
+        gen.check_out(out[:, :N], Y, 2e-2 if w8a8 else 1e-2, (M, N, K, "ldc", w8a8), fp32=True)
+        assert np.all(out[:, N:] == 7.0), "a store landed in the row gap"
