@@ -25,6 +25,9 @@
 //
 // SwiGLU mode: tile t holds gate bands 4t..4t+3 (waves 0, 1) and the matching up bands (waves 2, 3); the staged tile
 // (or the fixup) gives h = silu(bf16(gate)) * bf16(up) (reference silu_mul, core.metal:777-787).
+//
+// The same kernel serves T64x8 (8-bit) weights with BITS = 8: a band's codes are two 1 KB halves per group (two DMAs
+// instead of one), dequantized from the stored q - 128 bytes to bf16(s q + b), MLX's 8-bit qmm rounding.
 #include <algorithm>
 
 #include "common.h"

@@ -1,4 +1,5 @@
-// T64-layout kernels: the repack from the reference layout and the decode GEMV on T64 weights.
+// T64-layout kernels: the repack from the reference layout and the decode GEMV on T64 weights (and, with BITS = 8,
+// on T64x8 weights).
 //
 // The decode kernel computes what the reference's qmv4 computes (engine/kernels/core.metal:85-171): per 64-group
 // s * sum q x + b * sum x in fp32, here with the products on bf16 MFMA (codes enter as exact bf16 (128 + q)) and the
