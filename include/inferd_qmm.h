@@ -330,6 +330,22 @@ int ifd_moe_decode_logits(const float* logits_in, const void* xn, int T, int H, 
                           const uint32_t* sgu_wq, const uint16_t* sgu_s, const uint16_t* sgu_b,
                           const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b, void* out, int assign,
                           int* idx, float* wt, float* sg, void* workspace, size_t ws_bytes, void* stream);
+/* ifd_moe_decode and ifd_moe_decode_logits with the shared expert's width: shared_bits 4, or 8 for an MLX 8-bit
+ * shared expert (wq uint32 [2I][H/4] and [H][I/4]), which runs the qmv8 arithmetic (per group s sum q x + b sum x)
+ * beside the 4-bit routed experts: the reference's moe_gu2_4_8 / moe_dn2_4_8 (moe.metal:465-476, 544-547). */
+int ifd_moe_decode_ex(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
+                      const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
+                      const uint16_t* edn_s, const uint16_t* edn_b, int I, const uint32_t* sgu_wq,
+                      const uint16_t* sgu_s, const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s,
+                      const uint16_t* sdn_b, int shared_bits, void* out, int assign, int* idx, float* wt, float* sg,
+                      float* logits, void* workspace, size_t ws_bytes, void* stream);
+int ifd_moe_decode_logits_ex(const float* logits_in, const void* xn, int T, int H, int E, int k, int norm,
+                             int shared_gate, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
+                             const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I,
+                             const uint32_t* sgu_wq, const uint16_t* sgu_s, const uint16_t* sgu_b,
+                             const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b, int shared_bits,
+                             void* out, int assign, int* idx, float* wt, float* sg, void* workspace, size_t ws_bytes,
+                             void* stream);
 
 /* ---- measurement probes (outside the operator path) ----------------------------------------------------------
  * The HBM and MFMA ceilings a benchmark reports beside the datasheet peaks, in the role of the reference's

@@ -86,6 +86,14 @@ SIGNATURES = {
                                    _vp, _vp, _vp, _vp, _vp, _vp, _i,
                                    _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ifd_moe_decode_ex": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i,
+                               _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                               _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                               _vp, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ifd_moe_decode_logits_ex": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i,
+                                      _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                                      _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                                      _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ifd_moe_ffn_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
     "ifd_moe_ffn": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i, _i,
                          _vp, _vp, _vp, _vp, _vp, _vp, _i,

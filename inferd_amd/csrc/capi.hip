@@ -646,12 +646,13 @@ size_t ifd_moe_decode_workspace(int T, int H, int I, int E, int k) {
   return with_header(mdec_layout(T, H, I, E, k).total);
 }
 
-int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
-                   const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
-                   const uint16_t* edn_s, const uint16_t* edn_b, int I, const uint32_t* sgu_wq, const uint16_t* sgu_s,
-                   const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b,
-                   void* out, int assign, int* idx, float* wt, float* sg, float* logits, void* workspace,
-                   size_t ws_bytes, void* stream) {
+int ifd_moe_decode_ex(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
+                      const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
+                      const uint16_t* edn_s, const uint16_t* edn_b, int I, const uint32_t* sgu_wq,
+                      const uint16_t* sgu_s, const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s,
+                      const uint16_t* sdn_b, int shared_bits, void* out, int assign, int* idx, float* wt, float* sg,
+                      float* logits, void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(shared_bits == 4 || shared_bits == 8, "shared_bits=%d must be 4 or 8", shared_bits);
   IFD_CHECK(T >= 0 && T <= 16, "the decode MoE takes T <= 16 tokens (T=%d): larger batches use ifd_moe_ffn", T);
   IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
                 k <= 16 && k <= E,
@@ -666,16 +667,30 @@ int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int 
             "tokens, router and weights must be 16-byte aligned");
   const WsView wv = ws_view(workspace, ws_bytes);
   MdecCall c{xn, router, T, H, E, k, I, norm ? 1 : 0, shared_gate ? 1 : 0, assign ? 1 : 0, egu_wq, egu_s, egu_b,
-             edn_wq, edn_s, edn_b, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, out, idx, wt, sg, logits, nullptr};
+             edn_wq, edn_s, edn_b, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, out, idx, wt, sg, logits, nullptr,
+             shared_bits};
   return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
 }
 
-int ifd_moe_decode_logits(const float* logits_in, const void* xn, int T, int H, int E, int k, int norm,
-                          int shared_gate, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
-                          const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I,
-                          const uint32_t* sgu_wq, const uint16_t* sgu_s, const uint16_t* sgu_b,
-                          const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b, void* out, int assign,
-                          int* idx, float* wt, float* sg, void* workspace, size_t ws_bytes, void* stream) {
+int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
+                   const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
+                   const uint16_t* edn_s, const uint16_t* edn_b, int I, const uint32_t* sgu_wq, const uint16_t* sgu_s,
+                   const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b,
+                   void* out, int assign, int* idx, float* wt, float* sg, float* logits, void* workspace,
+                   size_t ws_bytes, void* stream) {
+  return ifd_moe_decode_ex(xn, T, H, router, E, k, norm, shared_gate, egu_wq, egu_s, egu_b, edn_wq, edn_s, edn_b, I,
+                           sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, 4, out, assign, idx, wt, sg, logits, workspace,
+                           ws_bytes, stream);
+}
+
+int ifd_moe_decode_logits_ex(const float* logits_in, const void* xn, int T, int H, int E, int k, int norm,
+                             int shared_gate, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
+                             const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I,
+                             const uint32_t* sgu_wq, const uint16_t* sgu_s, const uint16_t* sgu_b,
+                             const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b, int shared_bits,
+                             void* out, int assign, int* idx, float* wt, float* sg, void* workspace, size_t ws_bytes,
+                             void* stream) {
+  IFD_CHECK(shared_bits == 4 || shared_bits == 8, "shared_bits=%d must be 4 or 8", shared_bits);
   IFD_CHECK(T >= 0 && T <= 16, "the decode MoE takes T <= 16 tokens (T=%d): larger batches use ifd_moe_ffn", T);
   IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
                 k <= 16 && k <= E,
@@ -690,8 +705,20 @@ int ifd_moe_decode_logits(const float* logits_in, const void* xn, int T, int H, 
             "tokens and weights must be 16-byte aligned");
   const WsView wv = ws_view(workspace, ws_bytes);
   MdecCall c{xn, nullptr, T, H, E, k, I, norm ? 1 : 0, shared_gate ? 1 : 0, assign ? 1 : 0, egu_wq, egu_s, egu_b,
-             edn_wq, edn_s, edn_b, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, out, idx, wt, sg, nullptr, logits_in};
+             edn_wq, edn_s, edn_b, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, out, idx, wt, sg, nullptr, logits_in,
+             shared_bits};
   return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
+}
+
+int ifd_moe_decode_logits(const float* logits_in, const void* xn, int T, int H, int E, int k, int norm,
+                          int shared_gate, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
+                          const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I,
+                          const uint32_t* sgu_wq, const uint16_t* sgu_s, const uint16_t* sgu_b,
+                          const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b, void* out, int assign,
+                          int* idx, float* wt, float* sg, void* workspace, size_t ws_bytes, void* stream) {
+  return ifd_moe_decode_logits_ex(logits_in, xn, T, H, E, k, norm, shared_gate, egu_wq, egu_s, egu_b, edn_wq, edn_s,
+                                  edn_b, I, sgu_wq, sgu_s, sgu_b, sdn_wq, sdn_s, sdn_b, 4, out, assign, idx, wt, sg,
+                                  workspace, ws_bytes, stream);
 }
 
 }  // extern "C"

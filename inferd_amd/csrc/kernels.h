@@ -162,6 +162,7 @@ struct MdecCall {
   float* sg;
   float* logits;
   const float* logits_in;  // non-null: routing starts from these fp32 logits [T][E1] (router unused)
+  int sh_bits = 4;         // the shared expert's width, 4 or 8
 };
 struct MdecLayout {
   size_t part, plan, act, d, idx, wt, sg, total;

@@ -25,6 +25,7 @@
 //     out[t][h] = bf16(acc) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] d[t][j][h] + sg[t] d[t][k][h], in j order.
 // Every sum runs in a fixed order, so results do not depend on block timing.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "host.h"
@@ -66,6 +67,7 @@ struct MdecArgs {
   uint32_t d_bytes;
   unsigned* cnt;           // H / 128 counters, zero between calls
   int sb16_gu, sb16_dn;    // a wave's 8 scales (biases) of a row are one aligned 16 B load
+  int sh_bits;             // the shared expert's width: 4, or 8 (the reference's moe_gu2_4_8 / moe_dn2_4_8)
 };
 
 // The 8 bf16 values at v (16-byte aligned) as 8 raw halves.
@@ -274,7 +276,9 @@ __host__ __device__ constexpr size_t mdec_gu_lds(int T, int RT) {
   return (size_t)4 * T * kMdecGuRow * 2 + (size_t)4 * kMdecKG * kMdecMaxT * 4 + (size_t)4 * 64 * 2 * RT * 4;
 }
 
-template <int RT>
+// SB: the shared expert's width (8: the reference's moe_gu2_4_8, a kernel of its own, so that the 4-bit form keeps its
+// registers)
+template <int RT, int SB>
 __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
   extern __shared__ __align__(16) uint8_t glds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
@@ -291,29 +295,36 @@ __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
   const uint16_t* ws = sl.e < 0 ? p.sgu_s : p.egu_s;
   const uint16_t* wb = sl.e < 0 ? p.sgu_b : p.egu_b;
   const size_t rg = rows0 + n0 + j, ru = rg + I;
-  const MdecW Wg{wq + rg * (H / 8) + 4 * h, ws + rg * G, wb + rg * G};
-  const MdecW Wu{wq + ru * (H / 8) + 4 * h, ws + ru * G, wb + ru * G};
   const bool aok = j < T;
 
   float ag[RT], au[RT];
 #pragma unroll
   for (int r = 0; r < RT; r++) ag[r] = au[r] = 0.f;
-  for (int c0 = 0; c0 < Gw; c0 += kMdecKG) {
-    const int gb = wave * Gw + c0, ng = min(kMdecKG, Gw - c0);
+  // the product for codes of B bits (4: the routed experts and a 4-bit shared expert; 8: an 8-bit shared expert,
+  // the qmv8 arithmetic s P + b X)
+  auto run = [&](auto bits_c) __attribute__((always_inline)) {
+  constexpr int B = decltype(bits_c)::value;
+  // groups per chunk: 8-bit chunks hold half the groups, so that the code registers are those of a 4-bit chunk
+  constexpr int KG = B == 8 ? kMdecKG / 2 : kMdecKG;
+  const size_t wpr = (size_t)H * B / 32;  // words per row
+  const MdecW Wg{wq + rg * wpr + 4 * h, ws + rg * G, wb + rg * G};
+  const MdecW Wu{wq + ru * wpr + 4 * h, ws + ru * G, wb + ru * G};
+  for (int c0 = 0; c0 < Gw; c0 += KG) {
+    const int gb = wave * Gw + c0, ng = min(KG, Gw - c0);
     // every load of the chunk first (clamped re-reads past ng keep the count fixed), then the token rows
-    u32x4 cg[kMdecKG], cu[kMdecKG];
+    GroupCodes<B> cg[KG], cu[KG];
     uint16_t sgr[kMdecKG], bgr[kMdecKG], sur[kMdecKG], bur[kMdecKG];
 #pragma unroll
-    for (int i = 0; i < kMdecKG; i++) {
+    for (int i = 0; i < KG; i++) {
       const int g = gb + min(i, ng - 1);
-      cg[i] = *(const u32x4*)(Wg.w + (size_t)g * 8);
-      cu[i] = *(const u32x4*)(Wu.w + (size_t)g * 8);
+      cg[i].load(Wg.w, g);
+      cu[i].load(Wu.w, g);
     }
-    if (p.sb16_gu) {  // whole chunks of 8 groups at 16-byte aligned offsets (block-uniform)
+    if (B == 4 && p.sb16_gu) {  // whole chunks of 8 groups at 16-byte aligned offsets (block-uniform)
       load8h(Wg.s + gb, sgr), load8h(Wg.b + gb, bgr), load8h(Wu.s + gb, sur), load8h(Wu.b + gb, bur);
     } else {
 #pragma unroll
-      for (int i = 0; i < kMdecKG; i++) {
+      for (int i = 0; i < KG; i++) {
         const int g = gb + min(i, ng - 1);
         sgr[i] = Wg.s[g], bgr[i] = Wg.b[g], sur[i] = Wu.s[g], bur[i] = Wu.b[g];
       }
@@ -323,18 +334,18 @@ __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
                64);
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kMdecKG; i++) {
+    for (int i = 0; i < KG; i++) {
       if (i >= ng) break;
       f32x16 Pg = zero16(), Pu = zero16();
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        const u32x4 af = aok ? *(const u32x4*)(As + (size_t)j * kMdecGuRow + 64 * i + GroupCodes<4>::kofs(t, h))
+        const u32x4 af = aok ? *(const u32x4*)(As + (size_t)j * kMdecGuRow + 64 * i + GroupCodes<B>::kofs(t, h))
                              : u32x4{0u, 0u, 0u, 0u};
-        Pg = mfma_bf16(af, codes_bf16_off128(cg[i][t]), Pg);
-        Pu = mfma_bf16(af, codes_bf16_off128(cu[i][t]), Pu);
+        Pg = mfma_bf16(af, cg[i].step_affine(t, 0u), Pg);
+        Pu = mfma_bf16(af, cu[i].step_affine(t, 0u), Pu);
       }
-      const float sgf = bf2f(sgr[i]), bgf = __builtin_fmaf(-128.f, sgf, bf2f(bgr[i]));
-      const float suf = bf2f(sur[i]), buf = __builtin_fmaf(-128.f, suf, bf2f(bur[i]));
+      const float sgf = bf2f(sgr[i]), bgf = affine_bias<B>(sgf, bf2f(bgr[i]));
+      const float suf = bf2f(sur[i]), buf = affine_bias<B>(suf, bf2f(bur[i]));
 #pragma unroll
       for (int r = 0; r < RT; r++) {
         const float X = Xs[i * kMdecMaxT + mdec_row(r, h)];
@@ -342,6 +353,13 @@ __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
         au[r] = __builtin_fmaf(suf, Pu[r], __builtin_fmaf(buf, X, au[r]));
       }
     }
+  }
+  };
+  if constexpr (SB == 8) {
+    if (sl.e < 0) run(std::integral_constant<int, 8>{});  // block-uniform
+    else run(std::integral_constant<int, 4>{});
+  } else {
+    run(std::integral_constant<int, 4>{});
   }
 #pragma unroll
   for (int r = 0; r < RT; r++) RED(wave, lane, r) = ag[r], RED(wave, lane, RT + r) = au[r];
@@ -358,7 +376,7 @@ __global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
 }
 
 // ---- 4. down + combine ---------------------------------------------------------------------------------------------
-template <int RT>
+template <int RT, int SB>
 __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   extern __shared__ __align__(16) uint16_t lds[];  // As [T][I + 8], then Xs [I / 64][kMdecMaxT]
   __shared__ unsigned s_last;
@@ -371,7 +389,6 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   float* Xs = (float*)(lds + (size_t)T * lda + 8);  // 16-byte aligned: T lda + 8 is a multiple of 8
   const int h0 = blockIdx.x * 128 + wave * 32;
   const size_t row = (sl.e < 0 ? 0 : (size_t)sl.e * H) + h0 + j;
-  const uint32_t* wq = (sl.e < 0 ? p.sdn_wq : p.edn_wq) + row * (I / 8) + 4 * h;
   const uint16_t* ws = (sl.e < 0 ? p.sdn_s : p.edn_s) + row * Gi;
   const uint16_t* wb = (sl.e < 0 ? p.sdn_b : p.edn_b) + row * Gi;
   const bool aok = j < T;
@@ -379,20 +396,25 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   float acc[RT];
 #pragma unroll
   for (int r = 0; r < RT; r++) acc[r] = 0.f;
-  for (int c0 = 0; c0 < Gi; c0 += kMdecKG) {
-    const int ng = min(kMdecKG, Gi - c0);
-    u32x4 cw[kMdecKG];
+  // codes of B bits, as in k_mdec_gu
+  auto run = [&](auto bits_c) __attribute__((always_inline)) {
+  constexpr int B = decltype(bits_c)::value;
+  constexpr int KG = B == 8 ? kMdecKG / 2 : kMdecKG;  // as in k_mdec_gu
+  const uint32_t* wq = (sl.e < 0 ? p.sdn_wq : p.edn_wq) + row * ((size_t)I * B / 32) + 4 * h;
+  for (int c0 = 0; c0 < Gi; c0 += KG) {
+    const int ng = min(KG, Gi - c0);
+    GroupCodes<B> cw[KG];
     uint16_t sr[kMdecKG], br[kMdecKG];
 #pragma unroll
-    for (int i = 0; i < kMdecKG; i++) {
+    for (int i = 0; i < KG; i++) {
       const int g = c0 + min(i, ng - 1);
-      cw[i] = *(const u32x4*)(wq + (size_t)g * 8);
+      cw[i].load(wq, g);
     }
-    if (p.sb16_dn) {
+    if (B == 4 && p.sb16_dn) {
       load8h(ws + c0, sr), load8h(wb + c0, br);
     } else {
 #pragma unroll
-      for (int i = 0; i < kMdecKG; i++) {
+      for (int i = 0; i < KG; i++) {
         const int g = c0 + min(i, ng - 1);
         sr[i] = ws[g], br[i] = wb[g];
       }
@@ -407,21 +429,28 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
       __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < kMdecKG; i++) {
+    for (int i = 0; i < KG; i++) {
       if (i >= ng) break;
       const int g = c0 + i;
       f32x16 P = zero16();
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        const u32x4 af = aok ? *(const u32x4*)(As + (size_t)j * lda + 64 * g + GroupCodes<4>::kofs(t, h))
+        const u32x4 af = aok ? *(const u32x4*)(As + (size_t)j * lda + 64 * g + GroupCodes<B>::kofs(t, h))
                              : u32x4{0u, 0u, 0u, 0u};
-        P = mfma_bf16(af, codes_bf16_off128(cw[i][t]), P);
+        P = mfma_bf16(af, cw[i].step_affine(t, 0u), P);
       }
-      const float sf = bf2f(sr[i]), bf = __builtin_fmaf(-128.f, sf, bf2f(br[i]));
+      const float sf = bf2f(sr[i]), bf = affine_bias<B>(sf, bf2f(br[i]));
 #pragma unroll
       for (int r = 0; r < RT; r++)
         acc[r] = __builtin_fmaf(sf, P[r], __builtin_fmaf(bf, Xs[g * kMdecMaxT + mdec_row(r, h)], acc[r]));
     }
+  }
+  };
+  if constexpr (SB == 8) {
+    if (sl.e < 0) run(std::integral_constant<int, 8>{});  // block-uniform
+    else run(std::integral_constant<int, 4>{});
+  } else {
+    run(std::integral_constant<int, 4>{});
   }
   // d[t][pick][h] = bf16(result), written through for the combining block
   const __amdgpu_buffer_rsrc_t rd = part_rsrc(p.d, p.d_bytes);
@@ -507,12 +536,16 @@ static int launch_mdec(const MdecArgs& p, const MdecCall& c, hipStream_t st) {
     return IFD_OK;
   };
   const size_t glds = mdec_gu_lds(c.T, RT);
-  IFD_TRY(allow_lds((const void*)k_mdec_gu<RT>, glds, "gate_up"));
-  hipLaunchKernelGGL(k_mdec_gu<RT>, dim3(c.I / 32, slots), dim3(256), glds, st, p);
+  const void* gu = p.sh_bits == 8 ? (const void*)k_mdec_gu<RT, 8> : (const void*)k_mdec_gu<RT, 4>;
+  IFD_TRY(allow_lds(gu, glds, "gate_up"));
+  if (p.sh_bits == 8) hipLaunchKernelGGL((k_mdec_gu<RT, 8>), dim3(c.I / 32, slots), dim3(256), glds, st, p);
+  else hipLaunchKernelGGL((k_mdec_gu<RT, 4>), dim3(c.I / 32, slots), dim3(256), glds, st, p);
   IFD_TRY(check_launch("moe_decode gate_up"));
   const size_t lds = ((size_t)c.T * (c.I + 8) + 8) * 2 + (size_t)(c.I / kGroup) * kMdecMaxT * 4;
-  IFD_TRY(allow_lds((const void*)k_mdec_dn<RT>, lds, "down"));
-  hipLaunchKernelGGL(k_mdec_dn<RT>, dim3(c.H / 128, slots), dim3(256), lds, st, p);
+  const void* dn = p.sh_bits == 8 ? (const void*)k_mdec_dn<RT, 8> : (const void*)k_mdec_dn<RT, 4>;
+  IFD_TRY(allow_lds(dn, lds, "down"));
+  if (p.sh_bits == 8) hipLaunchKernelGGL((k_mdec_dn<RT, 8>), dim3(c.H / 128, slots), dim3(256), lds, st, p);
+  else hipLaunchKernelGGL((k_mdec_dn<RT, 4>), dim3(c.H / 128, slots), dim3(256), lds, st, p);
   return check_launch("moe_decode down");
 }
 
@@ -533,6 +566,7 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
   p.edn_wq = c.edn_wq, p.edn_s = c.edn_s, p.edn_b = c.edn_b;
   p.sgu_wq = c.sgu_wq, p.sgu_s = c.sgu_s, p.sgu_b = c.sgu_b;
   p.sdn_wq = c.sdn_wq, p.sdn_s = c.sdn_s, p.sdn_b = c.sdn_b;
+  p.sh_bits = c.sh_bits;
   p.out = (uint16_t*)c.out;
   p.idx = c.idx ? c.idx : (int*)(w + L.idx);
   p.wt = c.wt ? c.wt : (float*)(w + L.wt);

@@ -344,7 +344,9 @@ struct Qwen35 {
     const int H = cfg.hidden, E = cfg.experts, k = cfg.topk, I = cfg.moe_inter;
     const int E1 = ly.router.E * ly.router.N;
     const bool has_shared = ly.gate_up.N > 0;
-    const bool shared_fits = !has_shared || (ly.gate_up.bits == 4 && ly.down.bits == 4 && ly.gate_up.N == 2 * I &&
+    // a 4- or 8-bit shared expert (moe_gu2_4_4 / moe_gu2_4_8, moe.metal:465-487)
+    const bool shared_fits = !has_shared || ((ly.gate_up.bits == 4 || ly.gate_up.bits == 8) &&
+                                             ly.down.bits == ly.gate_up.bits && ly.gate_up.N == 2 * I &&
                                              ly.gate_up.K == H && ly.down.N == H && ly.down.K == I &&
                                              !ly.gate_up.flipped && !ly.down.flipped && !ly.gate_up.ldk &&
                                              !ly.down.ldk);
@@ -395,9 +397,10 @@ struct Qwen35 {
       a8_ready = false;  // the norm's int8 rows (if it made them) are not the next GEMM's input (qwen35.h:1906)
       const size_t need = ifd_moe_decode_workspace(T, H, I, E, k);
       if (need > splitk_bytes) die("encode_moe", "scratch smaller than the decode MoE needs");
+      const int sbits = has_shared ? ly.gate_up.bits : 4;
       if (r8) {
         router8_logits(0);
-        ok(ifd_moe_decode_logits(rlog.ptr<float>(), xn.ptr<void>(), T, H, E, k, 1, E1 > E ? 1 : 0,
+        ok(ifd_moe_decode_logits_ex(rlog.ptr<float>(), xn.ptr<void>(), T, H, E, k, 1, E1 > E ? 1 : 0,
                                  ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(), ly.egu.b.ptr<uint16_t>(),
                                  ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(), ly.edown.b.ptr<uint16_t>(), I,
                                  has_shared ? ly.gate_up.wq.ptr<uint32_t>() : nullptr,
@@ -405,12 +408,13 @@ struct Qwen35 {
                                  has_shared ? ly.gate_up.b.ptr<uint16_t>() : nullptr,
                                  has_shared ? ly.down.wq.ptr<uint32_t>() : nullptr,
                                  has_shared ? ly.down.s.ptr<uint16_t>() : nullptr,
-                                 has_shared ? ly.down.b.ptr<uint16_t>() : nullptr, x.ptr<void>(), 0, ridx.ptr<int>(),
-                                 rw.ptr<float>(), rsg.ptr<float>(), splitk.ptr<void>(), splitk_bytes, e.stream),
+                                 has_shared ? ly.down.b.ptr<uint16_t>() : nullptr, sbits, x.ptr<void>(), 0,
+                                 ridx.ptr<int>(), rw.ptr<float>(), rsg.ptr<float>(), splitk.ptr<void>(), splitk_bytes,
+                                 e.stream),
            "encode_moe");
         return;
       }
-      ok(ifd_moe_decode(xn.ptr<void>(), T, H, ly.router.wq.ptr<void>(), E, k, 1, E1 > E ? 1 : 0,
+      ok(ifd_moe_decode_ex(xn.ptr<void>(), T, H, ly.router.wq.ptr<void>(), E, k, 1, E1 > E ? 1 : 0,
                         ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(), ly.egu.b.ptr<uint16_t>(),
                         ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(), ly.edown.b.ptr<uint16_t>(), I,
                         has_shared ? ly.gate_up.wq.ptr<uint32_t>() : nullptr,
@@ -418,7 +422,7 @@ struct Qwen35 {
                         has_shared ? ly.gate_up.b.ptr<uint16_t>() : nullptr,
                         has_shared ? ly.down.wq.ptr<uint32_t>() : nullptr,
                         has_shared ? ly.down.s.ptr<uint16_t>() : nullptr,
-                        has_shared ? ly.down.b.ptr<uint16_t>() : nullptr, x.ptr<void>(), 0, ridx.ptr<int>(),
+                        has_shared ? ly.down.b.ptr<uint16_t>() : nullptr, sbits, x.ptr<void>(), 0, ridx.ptr<int>(),
                         rw.ptr<float>(), rsg.ptr<float>(), rlog.ptr<float>(), splitk.ptr<void>(), splitk_bytes,
                         e.stream),
          "encode_moe");

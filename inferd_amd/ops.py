@@ -376,8 +376,8 @@ def moe_decode(xn: torch.Tensor, router: Optional[torch.Tensor], egu: MoeW, edn:
                out: Optional[torch.Tensor] = None, assign: bool = True, logits_in: Optional[torch.Tensor] = None):
     """Decode MoE for T <= 16 tokens (reference moe_plan / moe_gu2 / moe_dn2, and its per-row expert GEMVs below 128
     routed rows): each distinct expert read once. shared = (QLinear gate_up [2I, H], QLinear down [H, I]) with the
-    routed experts' I. With logits_in (fp32 [T, E + shared_gate], e.g. an 8-bit router through gemm_w8 mode 2) the
-    router is not read (ifd_moe_decode_logits).
+    routed experts' I, 4- or 8-bit (ifd_moe_decode_ex with the layers' width). With logits_in (fp32 [T, E +
+    shared_gate], e.g. an 8-bit router through gemm_w8 mode 2) the router is not read (ifd_moe_decode_logits_ex).
 
     Returns (out, idx, wt, sg, logits)."""
     T, H = xn.shape
@@ -391,21 +391,23 @@ def moe_decode(xn: torch.Tensor, router: Optional[torch.Tensor], egu: MoeW, edn:
     logits = torch.empty((T, E + (1 if shared_gate else 0)), dtype=torch.float32, device=dev)
     ws = workspace(lib().ifd_moe_decode_workspace(T, H, I, E, k), dev)
     sgu, sdn = shared if shared is not None else (None, None)
+    sbits = sgu.bits if sgu is not None else 4
+    assert sdn is None or sdn.bits == sbits
     if logits_in is not None:
         assert logits_in.dtype == torch.float32 and logits_in.is_contiguous()
         assert logits_in.shape == (T, E + (1 if shared_gate else 0))
-        check(lib().ifd_moe_decode_logits(
+        check(lib().ifd_moe_decode_logits_ex(
             _p(logits_in), _p(xn), T, H, E, k, 1 if norm else 0, 1 if shared_gate else 0,
             _p(egu.wq), _p(egu.s), _p(egu.b), _p(edn.wq), _p(edn.s), _p(edn.b), I,
             _p(sgu.wq) if sgu else None, _p(sgu.s) if sgu else None, _p(sgu.b) if sgu else None,
-            _p(sdn.wq) if sdn else None, _p(sdn.s) if sdn else None, _p(sdn.b) if sdn else None,
+            _p(sdn.wq) if sdn else None, _p(sdn.s) if sdn else None, _p(sdn.b) if sdn else None, sbits,
             _p(out), 1 if assign else 0, _p(idx), _p(wt), _p(sg), _p(ws), ws.numel(), _stream()))
         return out, idx, wt, sg, logits_in
-    check(lib().ifd_moe_decode(
+    check(lib().ifd_moe_decode_ex(
         _p(xn), T, H, _p(router), E, k, 1 if norm else 0, 1 if shared_gate else 0,
         _p(egu.wq), _p(egu.s), _p(egu.b), _p(edn.wq), _p(edn.s), _p(edn.b), I,
         _p(sgu.wq) if sgu else None, _p(sgu.s) if sgu else None, _p(sgu.b) if sgu else None,
-        _p(sdn.wq) if sdn else None, _p(sdn.s) if sdn else None, _p(sdn.b) if sdn else None,
+        _p(sdn.wq) if sdn else None, _p(sdn.s) if sdn else None, _p(sdn.b) if sdn else None, sbits,
         _p(out), 1 if assign else 0, _p(idx), _p(wt), _p(sg), _p(logits), _p(ws), ws.numel(), _stream()))
     return out, idx, wt, sg, logits
 

@@ -60,6 +60,9 @@ def lib():
         L.orc_moe_decode.argtypes = [_u16p, _i, _i, _i, _i, _i32p, _f32p, _f32p,
                                      _u32p, _u16p, _u16p, _u32p, _u16p, _u16p,
                                      _vp, _vp, _vp, _vp, _vp, _vp, _u16p, _i]
+        L.orc_moe_decode_b.argtypes = [_u16p, _i, _i, _i, _i, _i32p, _f32p, _f32p,
+                                       _u32p, _u16p, _u16p, _u32p, _u16p, _u16p,
+                                       _vp, _vp, _vp, _vp, _vp, _vp, _i, _u16p, _i]
         L.orc_store.argtypes = [_f32p, _vp, _i, _i, _i, _i]
         L.orc_a8_quant.argtypes = [_u16p, _i, _i, _i, _i, _i8p, _f32p]
         L.orc_w4a8.argtypes = [_i8p, _f32p, _u32p, _u16p, _u16p, _i, _i, _u, _f32p, _i, _i]
@@ -407,10 +410,12 @@ def quantize_affine(w_bf16, bits: int):
     return pack_affine(codes, bits), sb, bb, codes
 
 
-def moe_decode(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: bool = True) -> np.ndarray:
+def moe_decode(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: bool = True,
+               shared_bits: int = 4) -> np.ndarray:
     """Decode MoE for T <= 8 tokens (engine/kernels/moe.metal:326-551): per token and pick the decode GEMV arithmetic
     for gate/up and down, SwiGLU, bf16 expert outputs, weighted combine (plus sg * the shared expert).
-    egu / edn: (wq, s, b) stacks [E, 2I, H/8] and [E, H, I/8]; shared = ((gu), (dn)) or None."""
+    egu / edn: (wq, s, b) stacks [E, 2I, H/8] and [E, H, I/8]; shared = ((gu), (dn)) or None, of shared_bits 4 or 8
+    (moe_gu2_4_8 / moe_dn2_4_8, moe.metal:465-476, 544-547: the qmv8 dot)."""
     xn = _c(xn, np.uint16)
     T, H = xn.shape
     idx = _c(idx, np.int32)
@@ -429,10 +434,10 @@ def moe_decode(xn, idx, wt, sg, egu, edn, shared, I: int, out=None, assign: bool
               p(sdb, np.uint16)]
     else:
         sh = [None] * 6
-    lib().orc_moe_decode(xn, T, H, I, k, idx, _c(wt, np.float32), _c(sg, np.float32),
-                         _c(egu[0], np.uint32), _c(egu[1], np.uint16), _c(egu[2], np.uint16),
-                         _c(edn[0], np.uint32), _c(edn[1], np.uint16), _c(edn[2], np.uint16), *sh, o,
-                         1 if assign else 0)
+    lib().orc_moe_decode_b(xn, T, H, I, k, idx, _c(wt, np.float32), _c(sg, np.float32),
+                           _c(egu[0], np.uint32), _c(egu[1], np.uint16), _c(egu[2], np.uint16),
+                           _c(edn[0], np.uint32), _c(edn[1], np.uint16), _c(edn[2], np.uint16), *sh, shared_bits, o,
+                           1 if assign else 0)
     return o
 
 

@@ -501,21 +501,24 @@ void orc_moe_experts(const uint16_t* xn, int T, int H, int I, int E, int k, cons
 //   g, u = qmv(x_t, [gate | up]_e); a = bf16(float(bf16(silu(bf16 g))) * bf16 u); d_j = bf16(qmv(a, down_e));
 //   acc = sum_{j < k} wt[t][j] d_j + sg[t] d_k in fp32 (j order); out = bf16(acc) (assign) or bf16(x + bf16(acc)).
 // Deduplicating the experts across tokens (moe_plan) changes which weights are read once, not these values.
-void orc_moe_decode(const uint16_t* xn, int T, int H, int I, int k, const int* idx, const float* wt, const float* sg,
-                    const uint32_t* gu_wq, const uint16_t* gu_s, const uint16_t* gu_b, const uint32_t* dn_wq,
-                    const uint16_t* dn_s, const uint16_t* dn_b, const uint32_t* sh_gu_wq, const uint16_t* sh_gu_s,
-                    const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq, const uint16_t* sh_dn_s, const uint16_t* sh_dn_b,
-                    uint16_t* out, int assign) {
+// sh_bits: the shared expert's width, 4 or 8 (the reference's moe_gu2_4_8 / moe_dn2_4_8, moe.metal:465-476, 544-547:
+// the same arithmetic with the qmv8 dot, core.metal:175-248)
+void orc_moe_decode_b(const uint16_t* xn, int T, int H, int I, int k, const int* idx, const float* wt, const float* sg,
+                      const uint32_t* gu_wq, const uint16_t* gu_s, const uint16_t* gu_b, const uint32_t* dn_wq,
+                      const uint16_t* dn_s, const uint16_t* dn_b, const uint32_t* sh_gu_wq, const uint16_t* sh_gu_s,
+                      const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq, const uint16_t* sh_dn_s,
+                      const uint16_t* sh_dn_b, int sh_bits, uint16_t* out, int assign) {
   const size_t gw = (size_t)2 * I * (H / 8), gs = (size_t)2 * I * (H / 64), dw = (size_t)H * (I / 8),
                ds = (size_t)H * (I / 64);
   std::vector<float> y(2 * I), yd(H);
   std::vector<uint16_t> gu(2 * I), act(I);
   auto expert = [&](const uint16_t* x, const uint32_t* gwq, const uint16_t* gsc, const uint16_t* gbi,
-                    const uint32_t* dwq, const uint16_t* dsc, const uint16_t* dbi, std::vector<uint16_t>& d) {
-    orc_qmv(x, H, gwq, gsc, gbi, 2 * I, H, 0, y.data(), 1, 1);
+                    const uint32_t* dwq, const uint16_t* dsc, const uint16_t* dbi, std::vector<uint16_t>& d,
+                    int bits) {
+    orc_qmv_b(x, H, gwq, gsc, gbi, 2 * I, H, bits, 0, y.data(), 1, 1);
     for (int i = 0; i < 2 * I; i++) gu[i] = f2bf(y[i]);
     orc_silu_mul(gu.data(), act.data(), I, 1);
-    orc_qmv(act.data(), I, dwq, dsc, dbi, H, I, 0, yd.data(), 1, 1);
+    orc_qmv_b(act.data(), I, dwq, dsc, dbi, H, I, bits, 0, yd.data(), 1, 1);
     d.resize(H);
     for (int h = 0; h < H; h++) d[h] = f2bf(yd[h]);
   };
@@ -524,9 +527,9 @@ void orc_moe_decode(const uint16_t* xn, int T, int H, int I, int k, const int* i
     const uint16_t* x = xn + (size_t)t * H;
     for (int j = 0; j < k; j++) {
       const size_t e = (size_t)idx[t * k + j];
-      expert(x, gu_wq + e * gw, gu_s + e * gs, gu_b + e * gs, dn_wq + e * dw, dn_s + e * ds, dn_b + e * ds, dj[j]);
+      expert(x, gu_wq + e * gw, gu_s + e * gs, gu_b + e * gs, dn_wq + e * dw, dn_s + e * ds, dn_b + e * ds, dj[j], 4);
     }
-    if (sh_gu_wq) expert(x, sh_gu_wq, sh_gu_s, sh_gu_b, sh_dn_wq, sh_dn_s, sh_dn_b, dj[k]);
+    if (sh_gu_wq) expert(x, sh_gu_wq, sh_gu_s, sh_gu_b, sh_dn_wq, sh_dn_s, sh_dn_b, dj[k], sh_bits);
     for (int h = 0; h < H; h++) {
       float acc = 0.f;
       for (int j = 0; j < k; j++) acc += wt[t * k + j] * bf2f(dj[j][h]);
@@ -535,6 +538,14 @@ void orc_moe_decode(const uint16_t* xn, int T, int H, int I, int k, const int* i
       *o = assign ? f2bf(acc) : f2bf(bf2f(*o) + bfround(acc));
     }
   }
+}
+void orc_moe_decode(const uint16_t* xn, int T, int H, int I, int k, const int* idx, const float* wt, const float* sg,
+                    const uint32_t* gu_wq, const uint16_t* gu_s, const uint16_t* gu_b, const uint32_t* dn_wq,
+                    const uint16_t* dn_s, const uint16_t* dn_b, const uint32_t* sh_gu_wq, const uint16_t* sh_gu_s,
+                    const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq, const uint16_t* sh_dn_s, const uint16_t* sh_dn_b,
+                    uint16_t* out, int assign) {
+  orc_moe_decode_b(xn, T, H, I, k, idx, wt, sg, gu_wq, gu_s, gu_b, dn_wq, dn_s, dn_b, sh_gu_wq, sh_gu_s, sh_gu_b,
+                   sh_dn_wq, sh_dn_s, sh_dn_b, 4, out, assign);
 }
 
 }  // extern "C"

@@ -26,6 +26,11 @@ void orc_moe_decode(const uint16_t* xn, int T, int H, int I, int k, const int* i
                     const uint16_t* dn_s, const uint16_t* dn_b, const uint32_t* sh_gu_wq, const uint16_t* sh_gu_s,
                     const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq, const uint16_t* sh_dn_s, const uint16_t* sh_dn_b,
                     uint16_t* out, int assign);
+void orc_moe_decode_b(const uint16_t* xn, int T, int H, int I, int k, const int* idx, const float* wt, const float* sg,
+                      const uint32_t* gu_wq, const uint16_t* gu_s, const uint16_t* gu_b, const uint32_t* dn_wq,
+                      const uint16_t* dn_s, const uint16_t* dn_b, const uint32_t* sh_gu_wq, const uint16_t* sh_gu_s,
+                      const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq, const uint16_t* sh_dn_s,
+                      const uint16_t* sh_dn_b, int sh_bits, uint16_t* out, int assign);
 void orc_qmv_b(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
                int bits, uint32_t xr, float* Y, int M, int nthreads);
 void orc_qmm_b(const uint16_t* A, int lda, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K,
@@ -466,13 +471,29 @@ void test_encode_moe(std::mt19937& rng) {
     std::uniform_real_distribution<float> su(0.0001f, 0.0003f);
     for (size_t i = 0; i < r8s.size(); i++) r8s[i] = f2bf(su(rng)), r8b[i] = f2bf(-128.f * bf2f(r8s[i]));
   }
+  // an 8-bit shared expert (the reference's moe_gu2_4_8 / moe_dn2_4_8), taken on the decode route
+  auto make_linear8 = [&](int N, int K) {
+    HostLinear h{N, K, std::vector<uint32_t>((size_t)N * K / 4), std::vector<uint16_t>((size_t)N * K / 64), {}};
+    std::vector<uint8_t> codes((size_t)N * K);
+    std::uniform_int_distribution<int> q(0, 255);
+    for (auto& v : codes) v = (uint8_t)q(rng);
+    orc_pack_w8(codes.data(), h.wq.data(), N, K);
+    std::uniform_real_distribution<float> su(0.0003f, 0.0012f), bu(-0.1f, 0.1f);
+    h.b.resize(h.s.size());
+    for (size_t i = 0; i < h.s.size(); i++) h.s[i] = f2bf(su(rng)), h.b[i] = f2bf(bu(rng));
+    return h;
+  };
+  const HostLinear sgu8 = make_linear8(2 * Is, H), sdn8 = make_linear8(H, Is);
+  QLinear sgu8_d = device_linear(sgu8), sdn8_d = device_linear(sdn8);
+  sgu8_d.bits = 8, sdn8_d.bits = 8;
+  const QLinear sdn_mlx = ly.down;
   const MoeW router16 = ly.router;
   MoeW router8;
   router8.wq = upload(r8wq), router8.s = upload(r8s), router8.b = upload(r8b);
   router8.E = 1, router8.N = E + 1, router8.K = H, router8.bits = 8;
   struct Case {
     int T, max_rows;
-    bool t64, r8;
+    bool t64, r8, s8 = false;
   };
   // the decode route up to 8 tokens and below 128 routed rows (T = 16 at top-4), the sorted route beyond; the
   // fused T64 shared gate/up; state allocated for more rows than the call (its scratch covers every row count); the
@@ -480,9 +501,10 @@ void test_encode_moe(std::mt19937& rng) {
   for (const Case cs : {Case{3, 3, false, false}, Case{8, 8, false, false}, Case{16, 16, false, false},
                         Case{100, 100, false, false}, Case{16, 16, true, false}, Case{100, 100, true, false},
                         Case{100, 256, true, false}, Case{3, 3, false, true}, Case{12, 12, false, true},
-                        Case{40, 40, false, true}}) {
+                        Case{40, 40, false, true}, Case{3, 3, false, false, true}, Case{8, 8, false, true, true}}) {
     const int T = cs.T;
-    ly.gate_up = sgu_mlx;
+    ly.gate_up = cs.s8 ? sgu8_d : sgu_mlx;
+    ly.down = cs.s8 ? sdn8_d : sdn_mlx;
     if (cs.t64) ly.gate_up.t64 = BufRef(sgu_t64);
     ly.router = cs.r8 ? router8 : router16;
     Qwen35 m(c, cs.max_rows, Is, 0);
@@ -499,6 +521,7 @@ void test_encode_moe(std::mt19937& rng) {
     const bool dec = m.moe_decode_route(ly, T);
     const std::string tag = " T=" + std::to_string(T) + (cs.max_rows > T ? " of " + std::to_string(cs.max_rows) : "") +
                             (ly.gate_up.t64 ? " (T64 shared gate/up)" : "") + (cs.r8 ? " (8-bit router)" : "") +
+                            (cs.s8 ? " (8-bit shared expert)" : "") +
                             (dec ? " [decode]" : " [sorted]");
     if (cs.r8) {  // the logits against the oracle's qmv8 on the GPU's normalised rows
       std::vector<float> yl((size_t)T * (E + 1));
@@ -525,7 +548,12 @@ void test_encode_moe(std::mt19937& rng) {
     report(ri == idx && ew <= 1e-5, "encode_moe routing (indices bit-exact)" + tag, ew);
     // the block's output added into x, from the GPU's normalised rows and routing
     std::vector<uint16_t> want = x0;
-    if (dec)  // the decode MoE route: the decode GEMV arithmetic for every expert product
+    if (cs.s8) {  // on the decode route only
+      report(dec, "encode_moe takes the decode route with an 8-bit shared expert" + tag, 0);
+      orc_moe_decode_b(xn.data(), T, H, I, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
+                       egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu8.wq.data(), sgu8.s.data(),
+                       sgu8.b.data(), sdn8.wq.data(), sdn8.s.data(), sdn8.b.data(), 8, want.data(), 0);
+    } else if (dec)  // the decode MoE route: the decode GEMV arithmetic for every expert product
       orc_moe_decode(xn.data(), T, H, I, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
                      egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu.wq.data(), sgu.s.data(),
                      sgu.b.data(), sdn.wq.data(), sdn.s.data(), sdn.b.data(), want.data(), 0);
@@ -543,6 +571,8 @@ void test_encode_moe(std::mt19937& rng) {
   }
   (void)hipFree(sgu_t64);
   (void)hipFree(router8.wq.buf), (void)hipFree(router8.s.buf), (void)hipFree(router8.b.buf);
+  for (void* q : {sgu8_d.wq.buf, sgu8_d.s.buf, sgu8_d.b.buf, sdn8_d.wq.buf, sdn8_d.s.buf, sdn8_d.b.buf})
+    (void)hipFree(q);
 }
 
 template <class T>

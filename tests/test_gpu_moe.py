@@ -245,6 +245,30 @@ def test_moe_decode_baseline_geometry(T):
     _decode_case(T, 512, 2048, 512, 10, True, True, seed=120 + T)
 
 
+@pytest.mark.parametrize("T", [1, 4, 8, 12, 16])
+def test_moe_decode_8bit_shared_expert(T):
+    """An 8-bit shared expert beside the 4-bit routed experts (the reference's moe_gu2_4_8 / moe_dn2_4_8,
+    moe.metal:465-476, 544-547): its slot runs the qmv8 arithmetic. Config 4's layer geometry; the oracle's decode MoE
+    with the same width, 1e-2 RMS."""
+    g, ops = _gu(), _ops()
+    E, H, I, k, seed = 512, 2048, 512, 10, 210 + T
+    egu, edn = experts(E, 2 * I, H, seed=seed), experts(E, H, I, seed=seed + 1)
+    _, gq, gs, gb = gen.qlinear8(2 * I, H, seed=seed + 2, bias="free")
+    _, dq, ds, db = gen.qlinear8(H, I, seed=seed + 3, bias="free")
+    R = router(E + 1, H, seed=seed + 4)
+    xn = gen.activations(T, H, seed=seed + 5)
+    x0 = gen.activations(T, H, seed=seed + 6)
+    sh = (g.qlinear(gq, gs, gb, bits=8), g.qlinear(dq, ds, db, bits=8))
+    out, idx, wt, sg, logits = ops.moe_decode(g.dev(xn), g.dev(R), g.moew(*egu), g.moew(*edn), k, shared=sh,
+                                              out=g.dev(x0), assign=False)
+    torch.cuda.synchronize()
+    ri, rw, rs = orc.moe_route(g.host(logits), E, k, shared_gate=True)
+    assert np.array_equal(g.host(idx), ri)
+    ref = orc.moe_decode(xn, ri, rw, rs, egu, edn, ((gq, gs, gb), (dq, ds, db)), I, out=x0, assign=False,
+                         shared_bits=8)
+    gen.check_bf16(g.host(out), ref, 1e-2, (T, "8-bit shared"), ref_is_bf16=True, composition=True)
+
+
 def test_moe_decode_rows_independent_of_batch():
     """A token's result is the same bits whatever the other tokens of the call: 12 tokens (16-row accumulators) against
     each token alone (8-row accumulators), as the reference's per-row arithmetic gives."""

@@ -526,6 +526,27 @@ def test_moe_decode_composition():
     ref2 = ref - sg[:, None] * np.stack([mlp(sgu, sdn, x[t:t + 1])[0] for t in range(T)])
     got2 = gen.bf16_to_f32(no_sh).astype(np.float64)
     assert np.sqrt(np.mean((got2 - ref2) ** 2) / np.mean(ref2 ** 2)) < 1e-2
+    # an 8-bit shared expert (moe_gu2_4_8 / moe_dn2_4_8): the shared term is that expert's MLP in float64
+    sgu8, sdn8 = gen.qlinear8(2 * I, H, seed=702, bias="free"), gen.qlinear8(H, I, seed=703, bias="free")
+
+    def deq8(q):
+        codes, _, sc, bi = q
+        N, K = codes.shape
+        return (codes.astype(np.float64).reshape(N, K // 64, 64) * gen.bf16_to_f32(sc).astype(np.float64)[..., None]
+                + gen.bf16_to_f32(bi).astype(np.float64)[..., None]).reshape(N, K)
+
+    def mlp8(xr):
+        h = xr @ deq8(sgu8).T
+        a = h[:, :I] / (1 + np.exp(-h[:, :I])) * h[:, I:]
+        return a @ deq8(sdn8).T
+
+    out8 = orc.moe_decode(xn, idx, wt, sg, args[0], args[1], ((sgu8[1], sgu8[2], sgu8[3]), (sdn8[1], sdn8[2], sdn8[3])),
+                          I, shared_bits=8)
+    ref8 = ref2 + sg[:, None] * np.stack([mlp8(x[t:t + 1])[0] for t in range(T)])
+    got8 = gen.bf16_to_f32(out8).astype(np.float64)
+    assert np.sqrt(np.mean((got8 - ref8) ** 2) / np.mean(ref8 ** 2)) < 1e-2
+    # the 8-bit shared expert's term is not the 4-bit one read as 8-bit (a wrong width would be an O(1) error)
+    assert np.sqrt(np.mean((got8 - ref) ** 2) / np.mean(ref ** 2)) > 1e-1
 
 
 def test_qa8_quant_form():
