@@ -55,8 +55,8 @@ def parse():
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU design is in DESIGN.md",
-              file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): it measures one GPU's share of the "
+              "path, and no multi-GPU run is built", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
