@@ -101,6 +101,18 @@ def test_t64_w4a8_refuses_per_group_activations():
     assert rc == _lib.IFD_ERR_UNSUPPORTED and b"per-token" in L.ifd_last_error()
 
 
+def test_moe_decode_ex_refuses_other_shared_widths():
+    """The decode MoE takes a 4- or 8-bit shared expert (moe_gu2_4_4 / moe_gu2_4_8) and refuses any other width
+    before any GPU work."""
+    L = _lib.lib()
+    args = [4096, 4, 2048, 4096, 512, 10, 1, 1, 4096, 4096, 4096, 4096, 4096, 4096, 512,
+            4096, 4096, 4096, 4096, 4096, 4096, 6, 4096, 0, None, None, None, None, None, 0, None]
+    assert L.ifd_moe_decode_ex(*args) == _lib.IFD_ERR_ARG and b"shared_bits=6" in L.ifd_last_error()
+    la = [4096, 4096, 4, 2048, 512, 10, 1, 1, 4096, 4096, 4096, 4096, 4096, 4096, 512,
+          4096, 4096, 4096, 4096, 4096, 4096, 3, 4096, 0, None, None, None, None, 0, None]
+    assert L.ifd_moe_decode_logits_ex(*la) == _lib.IFD_ERR_ARG and b"shared_bits=3" in L.ifd_last_error()
+
+
 def test_t64x8_refuses_bad_arguments():
     """The 8-bit T64x8 entry points: per-group activation scales, K % 64, the 4-bit flip mask and its size query."""
     L = _lib.lib()
