@@ -242,6 +242,11 @@ int ifd_moe_gather(const void* x, const int* perm, int div, int R, int H, void* 
 int ifd_moe_gather_qmm(const void* A, const int* perm, int div, const int* offsets, const int* tiles,
                        const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int E,
                        int N, int K, int silu, void* C, int R, void* stream);
+/* The same for 4- or 8-bit expert stacks (bits; 8: wq uint32 [E][N][K/4]), the reference's gqmm at W.bits = 8
+ * (mlx_gqmm_b8, qwen35.h:1835; MLX gather_qmm, quantized_nax.h:1467-1681): bf16(s q + b) dequant, fp32 sums. */
+int ifd_moe_gather_qmm_ex(const void* A, const int* perm, int div, const int* offsets, const int* tiles,
+                          const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                          int E, int N, int K, int bits, int silu, void* C, int R, void* stream);
 
 /* The gathered expert GEMM on int8 activations (reference qa8g_gemm, qa8.metal:212-397; host qa8g,
  * qwen35.h:1847-1868): U int8 [rows][K] and XS [rows][K/64][2] from ifd_a8_quant with per-group scales (per_token 0

@@ -66,6 +66,7 @@ SIGNATURES = {
     "ifd_moe_dispatch": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ifd_moe_gather": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     "ifd_moe_gather_qmm": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
+    "ifd_moe_gather_qmm_ex": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i, _vp]),
     "ifd_moe_gather_qmm_a8": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i,
                                    _vp]),
     "ifd_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),

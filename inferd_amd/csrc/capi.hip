@@ -353,16 +353,24 @@ int ifd_moe_gather(const void* x, const int* perm, int div, int R, int H, void* 
   return launch_moe_gather((const uint16_t*)x, perm, div, R, H, (uint16_t*)xs, S(stream));
 }
 
-int ifd_moe_gather_qmm(const void* A, const int* perm, int div, const int* offsets, const int* tiles,
-                       const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int E,
-                       int N, int K, int silu, void* C, int R, void* stream) {
+int ifd_moe_gather_qmm_ex(const void* A, const int* perm, int div, const int* offsets, const int* tiles,
+                          const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                          int E, int N, int K, int bits, int silu, void* C, int R, void* stream) {
+  IFD_CHECK(bits == 4 || bits == 8, "bits=%d must be 4 or 8", bits);
   IFD_CHECK(R >= 0 && E > 0 && N > 0 && K > 0 && K % 64 == 0 && div > 0, "bad shape E=%d N=%d K=%d", E, N, K);
   IFD_CHECK(!silu || N % 2 == 0, "silu needs an even N (gate | up)");
   IFD_CHECK(max_tiles >= 0, "bad max_tiles");
   IFD_CHECK(R == 0 || (A && offsets && tiles && ntiles && wq && s && b && C), "null pointer");
   IFD_CHECK(R == 0 || (aligned(A, 16) && aligned(wq, 16)), "A and wq must be 16-byte aligned");
   return launch_moe_gather_qmm((const uint16_t*)A, perm, div, tiles, ntiles, offsets, max_tiles, wq, s, b, N, K,
-                               silu ? 1 : 0, (uint16_t*)C, R, S(stream));
+                               silu ? 1 : 0, (uint16_t*)C, R, S(stream), bits);
+}
+
+int ifd_moe_gather_qmm(const void* A, const int* perm, int div, const int* offsets, const int* tiles,
+                       const int* ntiles, int max_tiles, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int E,
+                       int N, int K, int silu, void* C, int R, void* stream) {
+  return ifd_moe_gather_qmm_ex(A, perm, div, offsets, tiles, ntiles, max_tiles, wq, s, b, E, N, K, 4, silu, C, R,
+                               stream);
 }
 
 int ifd_moe_gather_qmm_a8(const int8_t* U, const float* XS, const int* perm, int div, const int* offsets,

@@ -125,7 +125,8 @@ int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, i
 int launch_moe_gather(const uint16_t* x, const int* perm, int div, int R, int H, uint16_t* xs, hipStream_t st);
 int launch_moe_gather_qmm(const uint16_t* A, const int* perm, int div, const int* tiles, const int* ntiles,
                           const int* offsets, int max_tiles, const uint32_t* wq, const uint16_t* s,
-                          const uint16_t* b, int N, int K, int silu, uint16_t* C, int R, hipStream_t st);
+                          const uint16_t* b, int N, int K, int silu, uint16_t* C, int R, hipStream_t st,
+                          int bits = 4);
 int launch_moe_gather_qmm_a8(const int8_t* U, const float* XS, const int* perm, int div, const int* tiles,
                              const int* ntiles, const int* offsets, int max_tiles, const uint32_t* wq,
                              const uint16_t* s, const uint16_t* b, int N, int K, int silu, uint16_t* C, int R,

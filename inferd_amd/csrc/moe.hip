@@ -366,7 +366,9 @@ int launch_moe_gather(const uint16_t* x, const int* perm, int div, int R, int H,
 // rows, read through perm (row q of the tile is token perm[q] / div) or directly (perm == null).
 // SILU: the wave also runs the matching up-projection column (n + N/2) and stores
 // bf16(float(bf16(g sigmoid g)) * u) of the bf16-rounded products, as moe_silu_mul does on gqmm's bf16 output.
-template <bool SILU>
+// BITS: 4, or 8 for MLX 8-bit expert stacks (the reference's gqmm at W.bits = 8, mlx_gqmm_b8; two 16-byte code
+// pieces per lane and group, in GroupCodes' k order).
+template <bool SILU, int BITS>
 __global__ __launch_bounds__(256) void k_gqmm(const uint16_t* __restrict__ A, const int* __restrict__ perm, int div,
                                               const int* __restrict__ tiles, const int* __restrict__ ntiles,
                                               const uint32_t* __restrict__ wq, const uint16_t* __restrict__ s,
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(256) void k_gqmm(const uint16_t* __restrict__ A, co
   const int n0 = cb * 128 + wave * 32;
   if (n0 >= NO) return;
   const int n = min(n0 + j, NO - 1);
-  const int G = K / kGroup, ldw = K / 8;
+  const int G = K / kGroup, ldw = K * BITS / 32;
   const size_t erow = (size_t)e * N;
   const uint32_t* wrow = wq + (erow + n) * ldw + 4 * h;
   const uint16_t* srow = s + (erow + n) * G;
@@ -392,26 +394,27 @@ __global__ __launch_bounds__(256) void k_gqmm(const uint16_t* __restrict__ A, co
   const int q = q0 + j;
   const bool aok = q < q1;
   const int arow_i = aok ? (perm ? perm[q] / div : q) : 0;
-  const uint16_t* arow = A + (size_t)arow_i * K + 32 * h;
+  const uint16_t* arow = A + (size_t)arow_i * K;
 
   f32x16 acc = zero16(), acc2 = zero16();
   for (int g = 0; g < G; g++) {
-    const u32x4 wv = *(const u32x4*)(wrow + (size_t)g * 8);
+    GroupCodes<BITS> wv, wv2;
+    wv.load(wrow, g);
     const float sc = bf2f(srow[g]), bi = bf2f(brow[g]);
-    u32x4 wv2;
     float sc2 = 0.f, bi2 = 0.f;
     if (SILU) {
-      wv2 = *(const u32x4*)(wrow2 + (size_t)g * 8);
+      wv2.load(wrow2, g);
       sc2 = bf2f(srow2[g]);
       bi2 = bf2f(brow2[g]);
     }
     u32x4 af[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) af[t] = aok ? *(const u32x4*)(arow + (size_t)g * 64 + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+    for (int t = 0; t < 4; t++)
+      af[t] = aok ? *(const u32x4*)(arow + (size_t)g * 64 + GroupCodes<BITS>::kofs(t, h)) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-      acc = mfma_bf16(af[t], dequant8_bf16(wv[t], sc, bi), acc);
-      if (SILU) acc2 = mfma_bf16(af[t], dequant8_bf16(wv2[t], sc2, bi2), acc2);
+      acc = mfma_bf16(af[t], wv.step_dequant(t, 0u, sc, bi), acc);
+      if (SILU) acc2 = mfma_bf16(af[t], wv2.step_dequant(t, 0u, sc2, bi2), acc2);
     }
   }
   const int col = n0 + j;
@@ -431,15 +434,22 @@ __global__ __launch_bounds__(256) void k_gqmm(const uint16_t* __restrict__ A, co
 
 int launch_moe_gather_qmm(const uint16_t* A, const int* perm, int div, const int* tiles, const int* ntiles,
                               const int* offsets, int max_tiles, const uint32_t* wq, const uint16_t* s,
-                              const uint16_t* b, int N, int K, int silu, uint16_t* C, int R, hipStream_t st) {
+                              const uint16_t* b, int N, int K, int silu, uint16_t* C, int R, hipStream_t st, int bits) {
   if (R == 0 || max_tiles == 0) return IFD_OK;
   const int NO = silu ? N / 2 : N, ncb = (NO + 127) / 128;
   dim3 grid((unsigned)(max_tiles * ncb)), block(256);
-  if (silu)
-    hipLaunchKernelGGL(k_gqmm<true>, grid, block, 0, st, A, perm, div, tiles, ntiles, wq, s, b, N, K, offsets, C, ncb);
-  else
-    hipLaunchKernelGGL(k_gqmm<false>, grid, block, 0, st, A, perm, div, tiles, ntiles, wq, s, b, N, K, offsets, C,
+  if (silu && bits == 8)
+    hipLaunchKernelGGL((k_gqmm<true, 8>), grid, block, 0, st, A, perm, div, tiles, ntiles, wq, s, b, N, K, offsets, C,
                        ncb);
+  else if (silu)
+    hipLaunchKernelGGL((k_gqmm<true, 4>), grid, block, 0, st, A, perm, div, tiles, ntiles, wq, s, b, N, K, offsets, C,
+                       ncb);
+  else if (bits == 8)
+    hipLaunchKernelGGL((k_gqmm<false, 8>), grid, block, 0, st, A, perm, div, tiles, ntiles, wq, s, b, N, K, offsets,
+                       C, ncb);
+  else
+    hipLaunchKernelGGL((k_gqmm<false, 4>), grid, block, 0, st, A, perm, div, tiles, ntiles, wq, s, b, N, K, offsets,
+                       C, ncb);
   return check_launch("moe_gather_qmm");
 }
 

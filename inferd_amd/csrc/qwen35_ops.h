@@ -350,8 +350,9 @@ struct Qwen35 {
                                              ly.gate_up.K == H && ly.down.N == H && ly.down.K == I &&
                                              !ly.gate_up.flipped && !ly.down.flipped && !ly.gate_up.ldk &&
                                              !ly.down.ldk);
+    // 4-bit routed experts (moe_gu2 / moe_dn2 are built for EB = 4 only, moe.metal:465-548)
     return (T <= 8 || (T <= 16 && T * k < moe_sort_min)) && k <= 16 && E <= 512 && H % 512 == 0 && I % 64 == 0 &&
-           E1 <= E + 1 && shared_fits;
+           E1 <= E + 1 && shared_fits && ly.egu.bits == 4 && ly.edown.bits == 4;
   }
 
   // The MoE block on the hidden state x [T][H]: xn = rmsnorm(x, post_norm); shared expert; router; top-k softmax
@@ -362,7 +363,8 @@ struct Qwen35 {
     if (T > max_rows) die("encode_moe", "more rows than the state was allocated for");
     if (ly.router.bits != 16 && !(ly.router.bits == 8 && ly.router.E == 1))
       die("encode_moe", "the router must be bf16 (bits 16) or one 8-bit matrix (bits 8)");
-    if (ly.egu.bits != 4 || ly.edown.bits != 4) die("encode_moe", "routed experts must be 4-bit affine");
+    if ((ly.egu.bits != 4 && ly.egu.bits != 8) || (ly.edown.bits != 4 && ly.edown.bits != 8))
+      die("encode_moe", "routed experts must be 4- or 8-bit affine");
     if (ly.router.K != H || ly.router.E * ly.router.N < E || ly.egu.E != E || ly.egu.N != 2 * I || ly.egu.K != H ||
         ly.edown.E != E || ly.edown.N != H || ly.edown.K != I)
       die("encode_moe", "layer shapes do not match the config");
@@ -450,13 +452,14 @@ struct Qwen35 {
                         mntiles.ptr<int>(), splitk.ptr<void>(), splitk_bytes, e.stream),
        "encode_moe");
     const int mt = ifd_moe_tiles_max(R, E);
-    ok(ifd_moe_gather_qmm(xn.ptr<void>(), mperm.ptr<int>(), k, moffs.ptr<int>(), mtiles.ptr<int>(), mntiles.ptr<int>(),
-                          mt, ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(), ly.egu.b.ptr<uint16_t>(), E, 2 * I,
-                          H, 1, eact.ptr<void>(), R, e.stream),
+    // 4- or 8-bit stacks (the reference's gqmm at W.bits, qwen35.h:1835)
+    ok(ifd_moe_gather_qmm_ex(xn.ptr<void>(), mperm.ptr<int>(), k, moffs.ptr<int>(), mtiles.ptr<int>(),
+                             mntiles.ptr<int>(), mt, ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(),
+                             ly.egu.b.ptr<uint16_t>(), E, 2 * I, H, ly.egu.bits, 1, eact.ptr<void>(), R, e.stream),
        "encode_moe");
-    ok(ifd_moe_gather_qmm(eact.ptr<void>(), nullptr, 1, moffs.ptr<int>(), mtiles.ptr<int>(), mntiles.ptr<int>(), mt,
-                          ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(), ly.edown.b.ptr<uint16_t>(), E, H, I,
-                          0, edown_out.ptr<void>(), R, e.stream),
+    ok(ifd_moe_gather_qmm_ex(eact.ptr<void>(), nullptr, 1, moffs.ptr<int>(), mtiles.ptr<int>(), mntiles.ptr<int>(), mt,
+                             ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(), ly.edown.b.ptr<uint16_t>(), E, H,
+                             I, ly.edown.bits, 0, edown_out.ptr<void>(), R, e.stream),
        "encode_moe");
     ok(ifd_moe_combine(x.ptr<void>(), edown_out.ptr<void>(), rw.ptr<float>(), shared ? sh_out.ptr<void>() : nullptr,
                        rsg.ptr<float>(), minv.ptr<int>(), T, H, k, 0, e.stream),

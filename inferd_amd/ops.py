@@ -164,13 +164,15 @@ def gemm_t64x8_w8a8(U: torch.Tensor, XS: torch.Tensor, W: T64x8Linear, C: Option
 
 @dataclass
 class MoeW:
-    """Stacked experts [E, N, K] in the same affine layout (engine/src/moe.h:8-11)."""
+    """Stacked experts [E, N, K] in the same affine layout (engine/src/moe.h:8-11), 4-bit (wq [E, N, K/8]) or 8-bit
+    (wq [E, N, K/4]; moe_gather_qmm only)."""
     wq: torch.Tensor
     s: torch.Tensor
     b: torch.Tensor
     E: int
     N: int
     K: int
+    bits: int = 4
 
 
 # ---- dense ----------------------------------------------------------------------------------------------------------
@@ -319,8 +321,8 @@ def moe_gather_qmm(A: torch.Tensor, perm: Optional[torch.Tensor], div: int, disp
     R = perm_sorted.numel()
     NO = W.N // 2 if silu else W.N
     C = torch.empty((R, NO), dtype=torch.bfloat16, device=A.device)
-    check(lib().ifd_moe_gather_qmm(_p(A), _p(perm), div, _p(offsets), _p(tiles), _p(ntiles), mt, _p(W.wq), _p(W.s),
-                                   _p(W.b), W.E, W.N, W.K, 1 if silu else 0, _p(C), R, _stream()))
+    check(lib().ifd_moe_gather_qmm_ex(_p(A), _p(perm), div, _p(offsets), _p(tiles), _p(ntiles), mt, _p(W.wq),
+                                      _p(W.s), _p(W.b), W.E, W.N, W.K, W.bits, 1 if silu else 0, _p(C), R, _stream()))
     return C
 
 
@@ -457,6 +459,8 @@ class T64Stack:
 
 def pack_t64_stack(W: MoeW) -> T64Stack:
     """One-time repack of an MLX-layout expert stack into T64 tiles."""
+    if W.bits != 4:
+        raise ValueError("pack_t64_stack takes 4-bit expert stacks")
     nbytes = lib().ifd_t64_bytes(W.N, W.K, W.E)
     wt = torch.empty((nbytes,), dtype=torch.uint8, device=W.wq.device)
     check(lib().ifd_pack_t64(_p(W.wq), _p(W.s), _p(W.b), W.N, W.K, 0, 0, W.E, _p(wt), _stream()))

@@ -112,6 +112,35 @@ def test_gather_qmm(T, E, silu):
     gen.check_bf16(got, ref, 1e-2, (T, E, silu))
 
 
+@pytest.mark.parametrize("silu", [False, True])
+def test_gather_qmm_8bit(silu):
+    """8-bit expert stacks on the gathered GEMM (the reference's gqmm at W.bits = 8, mlx_gqmm_b8): each expert's
+    sorted rows against the oracle's 8-bit qmm (bf16(s q + b) dequant, fp32 sums), 1e-2 RMS; the fused SwiGLU
+    bit-identical to silu_mul of that product."""
+    g, ops = _gu(), _ops()
+    from inferd_amd.ops import MoeW
+    rng = np.random.default_rng(77)
+    T, E, H, I, k = 40, 16, 512, 128, 4
+    N, K = (2 * I, H) if silu else (H, H)
+    layers = [gen.qlinear8(N, K, seed=300 + e, bias="free") for e in range(E)]
+    wq = np.stack([q[1] for q in layers]); s = np.stack([q[2] for q in layers]); b = np.stack([q[3] for q in layers])
+    W = MoeW(g.dev(wq), g.dev(s), g.dev(b), E, N, K, bits=8)
+    x = gen.activations(T, K, seed=78)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    disp = ops.moe_dispatch(g.dev(idx), E)
+    ro, rp, ri = orc.moe_dispatch(idx, E)
+    prod = ops.moe_gather_qmm(g.dev(x), disp[1], k, disp, W, silu=False)
+    if silu:
+        got = g.host(ops.moe_gather_qmm(g.dev(x), disp[1], k, disp, W, silu=True))
+        assert np.array_equal(got, g.host(ops.silu_mul(prod)))
+    ref = np.zeros((T * k, N), np.float32)
+    for e in range(E):
+        q0, q1 = int(ro[e]), int(ro[e + 1])
+        if q1 > q0:
+            ref[q0:q1] = orc.qmm(np.ascontiguousarray(x[rp[q0:q1] // k]), wq[e], s[e], b[e], bits=8)
+    gen.check_bf16(g.host(prod), ref, 1e-2, ("8-bit stacks", silu))
+
+
 def test_combine():
     g, ops = _gu(), _ops()
     rng = np.random.default_rng(6)
