@@ -102,8 +102,8 @@ def test_t64_w4a8_refuses_per_group_activations():
 
 
 def test_moe_decode_ex_refuses_other_shared_widths():
-    """The decode MoE takes a 4- or 8-bit shared expert (moe_gu2_4_4 / moe_gu2_4_8) and refuses any other width
-    before any GPU work."""
+    """The decode MoE takes a 4- or 8-bit shared expert (moe_gu2_4_4 / moe_gu2_4_8), the gathered GEMM 4- or 8-bit
+    stacks; any other width is refused before any GPU work."""
     L = _lib.lib()
     args = [4096, 4, 2048, 4096, 512, 10, 1, 1, 4096, 4096, 4096, 4096, 4096, 4096, 512,
             4096, 4096, 4096, 4096, 4096, 4096, 6, 4096, 0, None, None, None, None, None, 0, None]
@@ -111,6 +111,9 @@ def test_moe_decode_ex_refuses_other_shared_widths():
     la = [4096, 4096, 4, 2048, 512, 10, 1, 1, 4096, 4096, 4096, 4096, 4096, 4096, 512,
           4096, 4096, 4096, 4096, 4096, 4096, 3, 4096, 0, None, None, None, None, 0, None]
     assert L.ifd_moe_decode_logits_ex(*la) == _lib.IFD_ERR_ARG and b"shared_bits=3" in L.ifd_last_error()
+    # the gathered expert GEMM: 4- or 8-bit stacks
+    assert L.ifd_moe_gather_qmm_ex(4096, None, 1, 4096, 4096, 4096, 4, 4096, 4096, 4096, 8, 256, 256, 2, 0, 4096, 32,
+                                   None) == _lib.IFD_ERR_ARG and b"bits=2" in L.ifd_last_error()
 
 
 def test_t64x8_refuses_bad_arguments():
