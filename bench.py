@@ -414,7 +414,7 @@ def main():
     }
     # HBM bytes per call of a bench call, from the FETCH_SIZE / WRITE_SIZE counter runs of the same workload scaled by
     # a plain 256 MiB device copy (profiles/traffic_decode_mlp.md); calls not measured report null
-    measured_traffic = {"gate_up_swiglu_M128": 217857334}
+    measured_traffic = {"gate_up_swiglu_M128": 217737206}
 
     def roofline(d):
         # the bound is the larger of the call's two floors: its algorithmic bytes at HBM peak, its flops at dense
