@@ -281,6 +281,10 @@ int ifd_moe_ffn(const void* xn, int T, int H, const void* router, int E, int k, 
  * ifd_moe_tiles_max(R + shared_rows, E + 1) pairs; workspace ifd_moe_dispatch_workspace(R, E). */
 int ifd_moe_dispatch_ex(const int* idx, int R, int E, int k, int tile_rows, int shared_rows, int* offsets, int* perm,
                         int* inv, int* tiles, int* ntiles, void* workspace, size_t ws_bytes, void* stream);
+/* The tile height ifd_moe_ffn_t64 dispatches R routed rows over E experts with (64 once an expert holds about 24 rows
+ * on average, else 32): the schedule a caller composing ifd_moe_dispatch_ex and ifd_moe_gather_qmm_t64 itself uses
+ * to get the one-shot call's tiles. */
+int ifd_moe_t64_tile_rows(int R, int E);
 /* The gathered expert GEMM of ifd_moe_gather_qmm on T64 stacks (the same bits: bf16(s q + b) dequant, fp32 sums in
  * the same order): wt = E experts [E][N][K] packed by ifd_pack_t64, wt_shared (may be NULL) the shared expert [N][K]
  * taking the dispatch's expert-E segment; tiles / ntiles / offsets / tile_rows from ifd_moe_dispatch_ex; rows = the

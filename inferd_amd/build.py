@@ -12,6 +12,9 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libinferd_amd.so")
+# the operator-level MoE timer bench.py runs (Qwen35::encode_moe over this library)
+MOE_BENCH_SRC = os.path.join(HERE, "csrc", "encode_moe_bench.cpp")
+MOE_BENCH = os.path.join(HERE, "encode_moe_bench")
 OBJ = os.path.join(HERE, "_build")
 
 SOURCES = ["qmv.hip", "qmm.hip", "w4a8.hip", "moe.hip", "t64.hip", "gemm_t64.hip", "gemm_sk.hip", "gemm_t8.hip",
@@ -56,8 +59,15 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, OUT)
+    cmd = [_hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-Wall",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-I", os.path.join(os.path.dirname(HERE), "include"), "-I", CSRC, MOE_BENCH_SRC, "-o", MOE_BENCH,
+           "-L", HERE, "-linferd_amd", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"encode_moe_bench failed to build:\n{r.stdout}\n{r.stderr}")
     if verbose:
-        print(f"built {OUT}")
+        print(f"built {OUT} and {MOE_BENCH}")
     return OUT
 
 

@@ -515,6 +515,11 @@ int ifd_moe_gather_qmm_t64(const void* A, int lda, const int* perm, int div, con
 namespace {
 // rows per tile of the T64 gathered GEMM: 64-row tiles once an expert holds about 24 routed rows on average
 int moe_t64_tile_rows(int R, int E) { return R >= 24 * E ? 64 : 32; }
+}  // namespace
+
+int ifd_moe_t64_tile_rows(int R, int E) { return moe_t64_tile_rows(std::max(R, 0), std::max(E, 1)); }
+
+namespace {
 struct MoeT64Layout {
   size_t logits, idx, wt, sg, offsets, perm, inv, tiles, ntiles, disp, eact, ydn, total;
 };

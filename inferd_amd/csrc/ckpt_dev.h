@@ -79,7 +79,9 @@ inline QLinear upload_qlinear(Gpu& g, const HostQLinear& h, bool t64 = true) {
   return q;
 }
 
-inline MoeW upload_moe(Gpu& g, const HostMoeW& h) {
+// A host expert stack on the device: [wq | s | b] in one buffer, plus the E experts' T64 copy (ifd_pack_t64 with E)
+// when t64 and the stack is 4-bit with K and N multiples of 256, which encode_moe's sorted route then reads.
+inline MoeW upload_moe(Gpu& g, const HostMoeW& h, bool t64 = true) {
   MoeW m;
   m.E = h.E, m.N = h.N, m.K = h.K, m.bits = h.bits;
   const size_t wb = h.wq.size() * 4, sb = h.s.size() * 2;
@@ -88,6 +90,12 @@ inline MoeW upload_moe(Gpu& g, const HostMoeW& h) {
   detail::upload(g, m.wq.ptr<void>(), h.wq.data(), wb);
   detail::upload(g, m.s.ptr<void>(), h.s.data(), sb);
   detail::upload(g, m.b.ptr<void>(), h.b.data(), sb);
+  if (t64 && h.bits == 4 && h.K % 256 == 0 && h.N % 256 == 0) {
+    void* t = g.alloc(ifd_t64_bytes(h.N, h.K, h.E));
+    ok(ifd_pack_t64(m.wq.ptr<uint32_t>(), m.s.ptr<uint16_t>(), m.b.ptr<uint16_t>(), h.N, h.K, 0, 0u, h.E, t, g.stream),
+       "load");
+    m.t64 = BufRef(t);
+  }
   hip_ok(hipStreamSynchronize(g.stream), "load");
   return m;
 }
@@ -103,8 +111,8 @@ inline QLinear load_qlinear_bf16_q8(Gpu& g, const Checkpoint& ck, const std::vec
                         t64);
 }
 // reference load_moe (moe.h:14-87): stacked expert matrices fused along N per expert, groups expanded to 64.
-inline MoeW load_moe(Gpu& g, const Checkpoint& ck, const std::vector<std::string>& prefixes) {
-  return upload_moe(g, detail::or_exit("load_moe", [&] { return load_moe(ck, prefixes); }));
+inline MoeW load_moe(Gpu& g, const Checkpoint& ck, const std::vector<std::string>& prefixes, bool t64 = true) {
+  return upload_moe(g, detail::or_exit("load_moe", [&] { return load_moe(ck, prefixes); }), t64);
 }
 
 }  // namespace inferd

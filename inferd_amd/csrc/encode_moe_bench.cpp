@@ -1,0 +1,158 @@
+// encode_moe_bench — times the drop-in operator Qwen35::encode_moe (qwen35_ops.h; reference engine/src/qwen35.h:1869)
+// at BASELINE config 4's geometry: hidden 2048, 512 experts, top-10 softmax routing renormalised over the picks, one
+// always-on shared expert (no gate row: its weight is 1), SwiGLU experts of width 512, 4-bit group-64 affine weights
+// (q ~ U{0..15}, s ~ U(0.005, 0.02) rounded to bf16, b = -8 s), a bf16 N(0, 0.02) router. The layer is held the way
+// the device loader leaves it: the MLX-layout stacks plus their T64 copies (ckpt_dev.h upload_moe / upload_qlinear),
+// so the sorted route runs the T64 gathered GEMMs with the shared expert as expert E; `--mlx` drops the copies and
+// times the MLX-layout route instead. Two weight copies alternate (1.85 GB, over 3x the 256 MB Infinity Cache).
+//
+//   encode_moe_bench [--mlx] T...    one JSON line: {"T16": {"us": ..., "tok_s": ...}, ...}
+//
+// Timing: HIP events on the operator's stream around `iters` calls after warm calls that keep the GPU loaded for
+// 30 ms (its clock settles in that time). The hidden state x is updated in place by each call, as in a model.
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "qwen35_ops.h"
+
+using namespace inferd;
+
+namespace {
+
+uint64_t g_state = 0x9E3779B97F4A7C15ull;
+uint64_t next64() {  // splitmix64
+  uint64_t z = (g_state += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+float uni() { return (float)((next64() >> 40) * (1.0 / 16777216.0)); }
+float gauss() {  // sum of four uniforms, variance-normalised: enough for timing inputs
+  return (uni() + uni() + uni() + uni() - 2.f) * 1.7320508f;
+}
+uint16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+float bf2f(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+void* dalloc(size_t bytes) {
+  void* p = nullptr;
+  hip_ok(hipMalloc(&p, bytes), "bench alloc");
+  return p;
+}
+
+// one [wq | s | b] buffer of `rows` rows of K inputs (4-bit), filled with the config's distribution
+struct Affine {
+  BufRef wq, s, b;
+};
+Affine make_affine(size_t rows, int K) {
+  const size_t nw = rows * K / 8, ng = rows * K / 64;
+  char* buf = (char*)dalloc(nw * 4 + 2 * ng * 2);
+  std::vector<uint32_t> w(nw);
+  for (auto& v : w) v = (uint32_t)next64();
+  std::vector<uint16_t> s(ng), b(ng);
+  for (size_t i = 0; i < ng; i++) s[i] = f2bf(0.005f + 0.015f * uni()), b[i] = f2bf(-8.f * bf2f(s[i]));
+  hip_ok(hipMemcpy(buf, w.data(), nw * 4, hipMemcpyHostToDevice), "bench upload");
+  hip_ok(hipMemcpy(buf + nw * 4, s.data(), ng * 2, hipMemcpyHostToDevice), "bench upload");
+  hip_ok(hipMemcpy(buf + nw * 4 + ng * 2, b.data(), ng * 2, hipMemcpyHostToDevice), "bench upload");
+  return Affine{BufRef(buf, 0), BufRef(buf, nw * 4), BufRef(buf, nw * 4 + ng * 2)};
+}
+BufRef pack(const Affine& a, int N, int K, int E) {
+  void* t = dalloc(ifd_t64_bytes(N, K, E));
+  ok(ifd_pack_t64(a.wq.ptr<uint32_t>(), a.s.ptr<uint16_t>(), a.b.ptr<uint16_t>(), N, K, 0, 0u, E, t, nullptr),
+     "pack_t64");
+  return BufRef(t);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  bool mlx = false;
+  std::vector<int> Ts;
+  for (int i = 1; i < argc; i++) {
+    if (std::string(argv[i]) == "--mlx") mlx = true;
+    else Ts.push_back(atoi(argv[i]));
+  }
+  if (Ts.empty()) Ts = {16, 128, 2048};
+  const int H = 2048, E = 512, k = 10, I = 512, ncp = 2;
+  int Tmax = 0;
+  for (int T : Ts) Tmax = std::max(Tmax, T);
+  Config c;
+  c.hidden = H, c.experts = E, c.topk = k, c.moe_inter = I, c.eps = 1e-6f;
+  c.router_gemm_min = 64;  // bf16 router logits from 64 rows (qwen35.h:1919-1929)
+
+  std::vector<Layer> layers(ncp);
+  std::vector<uint16_t> router((size_t)E * H), post(H);
+  for (auto& v : router) v = f2bf(0.02f * gauss());
+  for (auto& v : post) v = f2bf(1.f);
+  BufRef drouter(dalloc(router.size() * 2)), dpost(dalloc(post.size() * 2));
+  hip_ok(hipMemcpy(drouter.buf, router.data(), router.size() * 2, hipMemcpyHostToDevice), "bench upload");
+  hip_ok(hipMemcpy(dpost.buf, post.data(), post.size() * 2, hipMemcpyHostToDevice), "bench upload");
+  for (auto& ly : layers) {
+    ly.post_norm = dpost;
+    ly.router.wq = drouter;
+    ly.router.E = 1, ly.router.N = E, ly.router.K = H, ly.router.bits = 16;
+    const Affine gu = make_affine((size_t)E * 2 * I, H), dn = make_affine((size_t)E * H, I);
+    ly.egu.wq = gu.wq, ly.egu.s = gu.s, ly.egu.b = gu.b, ly.egu.E = E, ly.egu.N = 2 * I, ly.egu.K = H, ly.egu.bits = 4;
+    ly.edown.wq = dn.wq, ly.edown.s = dn.s, ly.edown.b = dn.b, ly.edown.E = E, ly.edown.N = H, ly.edown.K = I,
+    ly.edown.bits = 4;
+    const Affine sgu = make_affine(2 * I, H), sdn = make_affine(H, I);
+    ly.gate_up.wq = sgu.wq, ly.gate_up.s = sgu.s, ly.gate_up.b = sgu.b, ly.gate_up.N = 2 * I, ly.gate_up.K = H;
+    ly.down.wq = sdn.wq, ly.down.s = sdn.s, ly.down.b = sdn.b, ly.down.N = H, ly.down.K = I;
+    if (!mlx) {
+      ly.egu.t64 = pack(gu, 2 * I, H, E), ly.edown.t64 = pack(dn, H, I, E);
+      ly.gate_up.t64 = pack(sgu, 2 * I, H, 1), ly.down.t64 = pack(sdn, H, I, 1);
+    }
+  }
+  hip_ok(hipDeviceSynchronize(), "bench setup");
+
+  Qwen35 m(c, Tmax, I, 0);
+  hipStream_t st;
+  hip_ok(hipStreamCreate(&st), "bench stream");
+  Enc e{st};
+  std::vector<uint16_t> x0((size_t)Tmax * H);
+  for (auto& v : x0) v = f2bf(gauss());
+  hipEvent_t e0, e1;
+  hip_ok(hipEventCreate(&e0), "event");
+  hip_ok(hipEventCreate(&e1), "event");
+  std::string out = "{";
+  for (size_t ti = 0; ti < Ts.size(); ti++) {
+    const int T = Ts[ti];
+    hip_ok(hipMemcpy(m.x.ptr<void>(), x0.data(), (size_t)T * H * 2, hipMemcpyHostToDevice), "bench x");
+    int i = 0;
+    for (; i < 3; i++) m.encode_moe(e, layers[i % ncp], T);
+    hip_ok(hipStreamSynchronize(st), "bench warm");
+    const auto t0 = std::chrono::steady_clock::now();
+    while (std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() < 30.0) {
+      for (int r = 0; r < 4; r++, i++) m.encode_moe(e, layers[i % ncp], T);
+      hip_ok(hipStreamSynchronize(st), "bench warm");
+    }
+    const int iters = 20;
+    hip_ok(hipEventRecord(e0, st), "event");
+    for (int r = 0; r < iters; r++, i++) m.encode_moe(e, layers[i % ncp], T);
+    hip_ok(hipEventRecord(e1, st), "event");
+    hip_ok(hipEventSynchronize(e1), "event");
+    float ms = 0;
+    hip_ok(hipEventElapsedTime(&ms, e0, e1), "event");
+    const double us = ms * 1e3 / iters;
+    char buf[160];
+    snprintf(buf, sizeof buf, "%s\"T%d\": {\"us\": %.2f, \"tok_s\": %.1f, \"decode_route\": %s, \"t64_route\": %s}",
+             ti ? ", " : "", T, us, T / (us * 1e-6), m.moe_decode_route(layers[0], T) ? "true" : "false",
+             m.moe_t64_route(layers[0]) && !m.moe_decode_route(layers[0], T) ? "true" : "false");
+    out += buf;
+  }
+  out += "}";
+  printf("%s\n", out.c_str());
+  return 0;
+}

@@ -109,9 +109,12 @@ inline QLinear kslice_of(const QLinear& q, int k0, int kn) {
   return r;
 }
 
-// A stacked affine matrix [E, N, K] (bits 4), or a bf16 matrix (bits 16: wq holds [E * N][K] bf16).
+// A stacked affine matrix [E, N, K] (bits 4 or 8), or a bf16 matrix (bits 16: wq holds [E * N][K] bf16). A 4-bit stack
+// may carry `t64`, its E experts packed by ifd_pack_t64 (the MI355X layout, made once at load); encode_moe's sorted
+// route reads it when both expert stacks have one.
 struct MoeW {
   BufRef wq, s, b;
+  BufRef t64;
   int E = 0, N = 0, K = 0, bits = 0;
 };
 
@@ -143,8 +146,8 @@ struct Qwen35 {
   BufRef rlog;                // router logits fp32 [max_rows][E + 1] (bf16 when rounded)
   BufRef ridx, rw, rsg;       // int [T][k], float [T][k], float [T]
   BufRef proj, act, sh_out;   // shared expert: bf16 [T][2 Is], [T][Is], [T][H]
-  BufRef moffs, mperm, minv, mtiles, mntiles;  // dispatch
-  BufRef eact, edown_out;     // routed experts: bf16 [R][I], [R][H]
+  BufRef moffs, mperm, minv, mtiles, mntiles;  // dispatch (room for the shared expert as expert E: E + 2 offsets, R + T rows)
+  BufRef eact, edown_out;     // routed experts (and the shared expert's rows after them): bf16 [R + T][I], [R + T][H]
   BufRef splitk;              // gemm()'s split-K partials and the dispatch workspace
   size_t splitk_bytes = 0;
   BufRef a8u, a8x;            // int8 rows [max_rows][a8_k] and their (sx, sx sum xq) per 64-group, fp32
@@ -205,13 +208,14 @@ struct Qwen35 {
         act = alloc((size_t)max_rows * shared_inter * 2);
         sh_out = alloc((size_t)max_rows * H * 2);
       }
-      moffs = alloc((size_t)(E + 1) * 4);
-      mperm = alloc((size_t)R * 4);
+      const int Rt = R + max_rows;  // the T64 route appends the shared expert's rows as expert E
+      moffs = alloc((size_t)(E + 2) * 4);
+      mperm = alloc((size_t)Rt * 4);
       minv = alloc((size_t)R * 4);
-      mtiles = alloc((size_t)ifd_moe_tiles_max(R, E) * 2 * 4);
+      mtiles = alloc((size_t)std::max(ifd_moe_tiles_max(R, E), ifd_moe_tiles_max(Rt, E + 1)) * 2 * 4);
       mntiles = alloc(4);
-      eact = alloc((size_t)R * I * 2);
-      edown_out = alloc((size_t)R * H * 2);
+      eact = alloc((size_t)Rt * I * 2);
+      edown_out = alloc((size_t)Rt * H * 2);
     }
     if (max_rows > 0 && a8_k > 0) {
       a8u = alloc((size_t)max_rows * a8_k);
@@ -355,6 +359,23 @@ struct Qwen35 {
            E1 <= E + 1 && shared_fits && ly.egu.bits == 4 && ly.edown.bits == 4;
   }
 
+  // The sorted route on the experts' T64 stacks (ifd_moe_gather_qmm_t64: the same bf16(s q + b) dequant and fp32 sums
+  // as the MLX-layout gathered GEMM): both stacks 4-bit with T64 copies, H and I multiples of 256.
+  bool moe_t64_route(const Layer& ly) const {
+    return ly.egu.t64 && ly.edown.t64 && ly.egu.bits == 4 && ly.edown.bits == 4 && cfg.hidden % 256 == 0 &&
+           cfg.moe_inter % 256 == 0;
+  }
+  // On that route the shared expert runs as expert E of the same two launches when it is a 4-bit linear pair of the
+  // routed experts' width with T64 copies that gemm() would also run in bf16 (not the W4A8 route): its rows get the
+  // qmm rounding gemm() gives them past qmv_max rows (qwen35.h:1525-1558, 1909-1914).
+  bool shared_as_expert(const Layer& ly, int T) const {
+    const int H = cfg.hidden, I = cfg.moe_inter;
+    const QLinear &gu = ly.gate_up, &dn = ly.down;
+    return moe_t64_route(ly) && gu.N > 0 && gu.bits == 4 && dn.bits == 4 && gu.t64 && dn.t64 && gu.N == 2 * I &&
+           gu.K == H && dn.N == H && dn.K == I && !gu.ldk && !dn.ldk && T > qmv_max && !w4a8_route(gu, T) &&
+           !w4a8_route(dn, T);
+  }
+
   // The MoE block on the hidden state x [T][H]: xn = rmsnorm(x, post_norm); shared expert; router; top-k softmax
   // routing; dispatch by expert; gathered gate/up with SwiGLU; gathered down; x = bf16(x + bf16(weighted sum +
   // sg * shared)) (reference sorted path, qwen35.h:1909-1980).
@@ -431,8 +452,9 @@ struct Qwen35 {
       return;
     }
     // shared expert -> sh_out (its gate/up may read the norm's int8 rows; the SwiGLU feeds the down GEMM in bf16,
-    // qwen35.h:1910-1914)
-    const bool shared = has_shared;
+    // qwen35.h:1910-1914), unless it runs as expert E of the T64 launches
+    const bool t64 = moe_t64_route(ly), fold = shared_as_expert(ly, T);
+    const bool shared = has_shared && !fold;
     if (shared) {
       gemm_swiglu(e, xn, ly.gate_up, act, T);
       a8_ready = false;
@@ -447,6 +469,30 @@ struct Qwen35 {
     ok(ifd_moe_route(rlog.ptr<void>(), lbf, T, E, k, E1, 1, E1 > E ? 1 : 0, ridx.ptr<int>(), rw.ptr<float>(),
                      rsg.ptr<float>(), e.stream),
        "encode_moe");
+    if (t64) {
+      // routed experts on their T64 stacks, rows sorted by expert in tiles of tr rows; with `fold`, tokens 0..T-1
+      // follow as expert E's segment (the shared expert) and its output rows R..R+T-1 are the combine's ys
+      const int tr = ifd_moe_t64_tile_rows(R, E), Rt = R + (fold ? T : 0);
+      ok(ifd_moe_dispatch_ex(ridx.ptr<int>(), R, E, k, tr, fold ? T : 0, moffs.ptr<int>(), mperm.ptr<int>(),
+                             minv.ptr<int>(), mtiles.ptr<int>(), mntiles.ptr<int>(), splitk.ptr<void>(), splitk_bytes,
+                             e.stream),
+         "encode_moe");
+      ok(ifd_moe_gather_qmm_t64(xn.ptr<void>(), H, mperm.ptr<int>(), k, moffs.ptr<int>(), mtiles.ptr<int>(),
+                                mntiles.ptr<int>(), tr, ly.egu.t64.ptr<void>(),
+                                fold ? ly.gate_up.t64.ptr<void>() : nullptr, E, 2 * I, H, 1, eact.ptr<void>(), I, Rt,
+                                e.stream),
+         "encode_moe");
+      ok(ifd_moe_gather_qmm_t64(eact.ptr<void>(), I, nullptr, 1, moffs.ptr<int>(), mtiles.ptr<int>(),
+                                mntiles.ptr<int>(), tr, ly.edown.t64.ptr<void>(),
+                                fold ? ly.down.t64.ptr<void>() : nullptr, E, H, I, 0, edown_out.ptr<void>(), H, Rt,
+                                e.stream),
+         "encode_moe");
+      const void* ys = fold ? edown_out.at((size_t)R * H * 2).ptr<void>() : shared ? sh_out.ptr<void>() : nullptr;
+      ok(ifd_moe_combine(x.ptr<void>(), edown_out.ptr<void>(), rw.ptr<float>(), ys, rsg.ptr<float>(), minv.ptr<int>(),
+                         T, H, k, 0, e.stream),
+         "encode_moe");
+      return;
+    }
     // routed experts, rows sorted by expert
     ok(ifd_moe_dispatch(ridx.ptr<int>(), R, E, moffs.ptr<int>(), mperm.ptr<int>(), minv.ptr<int>(), mtiles.ptr<int>(),
                         mntiles.ptr<int>(), splitk.ptr<void>(), splitk_bytes, e.stream),

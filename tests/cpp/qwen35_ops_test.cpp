@@ -6,6 +6,8 @@
 //   qwen35_ops_test --bad-bits  gemm() on a 16-bit QLinear: must print its error and exit(1) (no GPU needed)
 //   qwen35_ops_test --ckpt DIR  the device loaders (ckpt_dev.h) on a checkpoint written by tests/test_shim.py:
 //                               uploads bit-identical to the host loader, and gemm() on the loaded layer
+//   qwen35_ops_test --moe-c4 T  encode_moe on T64 expert stacks at BASELINE config 4's geometry (H 2048, 512 experts,
+//                               top-10, I 512, a shared expert) for T tokens
 //
 // Tolerances are BASELINE's: max |err| <= 1e-2 RMS(ref) after the output's own bf16 rounding; routing indices
 // bit-exact.
@@ -55,6 +57,8 @@ void orc_moe_experts(const uint16_t* xn, int T, int H, int I, int E, int k, cons
                      const uint16_t* sh_gu_s, const uint16_t* sh_gu_b, const uint32_t* sh_dn_wq,
                      const uint16_t* sh_dn_s, const uint16_t* sh_dn_b, int shared_qmv, uint16_t* out, int assign,
                      int nthreads);
+void orc_moe_combine(uint16_t* x, const uint16_t* yd, const float* wt, const uint16_t* ys, const float* sg,
+                     const int* inv, int T, int H, int k, int assign);
 }
 
 using namespace inferd;
@@ -156,6 +160,20 @@ HostLinear make_linear(int N, int K, std::mt19937& rng) {
   for (auto& c : codes) c = (uint8_t)q(rng);
   h.wq.resize((size_t)N * K / 8);
   orc_pack_w4(codes.data(), h.wq.data(), N, K);
+  std::uniform_real_distribution<float> su(0.005f, 0.02f);
+  h.s.resize((size_t)N * K / 64);
+  h.b.resize(h.s.size());
+  for (size_t i = 0; i < h.s.size(); i++) {
+    h.s[i] = f2bf(su(rng));
+    h.b[i] = f2bf(-8.f * bf2f(h.s[i]));
+  }
+  return h;
+}
+
+// As make_linear, with the codes taken from random 32-bit words (every nibble uniform on 0..15): for the large stacks
+HostLinear make_linear_words(int N, int K, std::mt19937& rng) {
+  HostLinear h{N, K, std::vector<uint32_t>((size_t)N * K / 8), {}, {}};
+  for (auto& w : h.wq) w = (uint32_t)rng();
   std::uniform_real_distribution<float> su(0.005f, 0.02f);
   h.s.resize((size_t)N * K / 64);
   h.b.resize(h.s.size());
@@ -575,6 +593,216 @@ void test_encode_moe(std::mt19937& rng) {
     (void)hipFree(q);
 }
 
+// A MoE layer at one geometry, with both the MLX-layout stacks and their T64 copies on the device.
+struct MoeGeo {
+  int H, E, k, I;
+};
+struct MoeLayer {
+  MoeGeo g;
+  HostLinear egu, edn, sgu, sdn;
+  std::vector<uint16_t> router, post;
+  Layer ly;                      // MLX buffers + T64 stacks; the shared expert with its T64 copies
+  void* t64[4] = {};             // egu, edn, sgu, sdn T64 copies
+  MoeLayer(const MoeGeo& geo, std::mt19937& rng) : g(geo) {
+    const int H = g.H, E = g.E, I = g.I;
+    egu = make_linear_words(E * 2 * I, H, rng), edn = make_linear_words(E * H, I, rng);
+    sgu = make_linear_words(2 * I, H, rng), sdn = make_linear_words(H, I, rng);
+    std::normal_distribution<float> nr(0.f, 0.02f);
+    router.resize((size_t)(E + 1) * H), post.resize(H);
+    for (auto& v : router) v = f2bf(nr(rng));
+    std::uniform_real_distribution<float> pw(0.5f, 2.f);
+    for (auto& v : post) v = f2bf(pw(rng));
+    ly.post_norm = upload(post);
+    ly.router.wq = upload(router);
+    ly.router.E = 1, ly.router.N = E + 1, ly.router.K = H, ly.router.bits = 16;
+    const QLinear gq = device_linear(egu), dq = device_linear(edn);
+    ly.egu.wq = gq.wq, ly.egu.s = gq.s, ly.egu.b = gq.b, ly.egu.E = E, ly.egu.N = 2 * I, ly.egu.K = H, ly.egu.bits = 4;
+    ly.edown.wq = dq.wq, ly.edown.s = dq.s, ly.edown.b = dq.b, ly.edown.E = E, ly.edown.N = H, ly.edown.K = I,
+    ly.edown.bits = 4;
+    ly.gate_up = device_linear(sgu), ly.down = device_linear(sdn);
+    const QLinear* src[4] = {&gq, &dq, &ly.gate_up, &ly.down};
+    const int NN[4] = {2 * I, H, 2 * I, H}, KK[4] = {H, I, H, I}, EE[4] = {E, E, 1, 1};
+    for (int i = 0; i < 4; i++) {
+      hip_ok(hipMalloc(&t64[i], ifd_t64_bytes(NN[i], KK[i], EE[i])), "t64");
+      ok(ifd_pack_t64(src[i]->wq.ptr<uint32_t>(), src[i]->s.ptr<uint16_t>(), src[i]->b.ptr<uint16_t>(), NN[i], KK[i], 0,
+                      0u, EE[i], t64[i], nullptr),
+         "pack_t64");
+    }
+    ly.egu.t64 = BufRef(t64[0]), ly.edown.t64 = BufRef(t64[1]);
+    ly.gate_up.t64 = BufRef(t64[2]), ly.down.t64 = BufRef(t64[3]);
+    hip_ok(hipDeviceSynchronize(), "pack_t64");
+  }
+  ~MoeLayer() {
+    for (void* p : {ly.post_norm.buf, ly.router.wq.buf, ly.egu.wq.buf, ly.egu.s.buf, ly.egu.b.buf, ly.edown.wq.buf,
+                    ly.edown.s.buf, ly.edown.b.buf, ly.gate_up.wq.buf, ly.gate_up.s.buf, ly.gate_up.b.buf,
+                    ly.down.wq.buf, ly.down.s.buf, ly.down.b.buf, t64[0], t64[1], t64[2], t64[3]})
+      if (p) (void)hipFree(p);
+  }
+};
+
+// encode_moe on the sorted route over T64 expert stacks. shared: 0 no shared expert; 1 the shared expert with T64
+// copies (expert E of the gathered launches); 2 the shared expert without T64 copies (gemm() on the MLX layout, then
+// the T64 launches for the routed experts). Checks: rmsnorm within one bf16 step; routing indices bit-exact
+// on the GPU's own logits; x += MoE(xn) against the oracle's composition on the GPU's normalised rows and routing, for
+// `check` tokens spread over the batch (every token when check >= T; each token's output depends on its own row only).
+void run_moe_t64(MoeLayer& L, int T, int max_rows, int shared, int check, int nthreads, std::mt19937& rng) {
+  const MoeGeo g = L.g;
+  const int H = g.H, E = g.E, k = g.k, I = g.I;
+  Config c;
+  c.hidden = H, c.experts = E, c.topk = k, c.moe_inter = I, c.eps = 1e-6f;
+  Layer ly = L.ly;
+  if (shared == 0) ly.gate_up = QLinear(), ly.down = QLinear(), ly.router.N = E;
+  if (shared == 2) ly.gate_up.t64 = BufRef(), ly.down.t64 = BufRef();
+  Qwen35 m(c, max_rows, shared ? I : 0, 0);
+  Enc e;
+  const auto x0 = activations(T, H, rng);
+  hip_ok(hipMemcpy(m.x.ptr<void>(), x0.data(), x0.size() * 2, hipMemcpyHostToDevice), "x");
+  m.encode_moe(e, ly, T);
+  const auto x1 = download<uint16_t>(m.x, (size_t)T * H);
+  const auto xn = download<uint16_t>(m.xn, (size_t)T * H);
+  const int E1 = shared ? E + 1 : E;
+  const auto logits = download<float>(m.rlog, (size_t)T * E1);
+  const auto idx = download<int>(m.ridx, (size_t)T * k);
+  const auto wt = download<float>(m.rw, (size_t)T * k);
+  const auto sg = download<float>(m.rsg, (size_t)T);
+  const bool dec = m.moe_decode_route(ly, T), t64 = m.moe_t64_route(ly), fold = m.shared_as_expert(ly, T);
+  const std::string tag = " T=" + std::to_string(T) + " H=" + std::to_string(H) + " E=" + std::to_string(E) +
+                          " k=" + std::to_string(k) + " I=" + std::to_string(I) +
+                          (shared == 0 ? " (no shared expert)" : fold ? " (shared = expert E)" : " (shared via gemm)") +
+                          (dec ? " [decode]" : t64 ? " [sorted, T64]" : " [sorted, MLX]");
+  report(!dec && t64 && fold == (shared == 1), "encode_moe takes the T64 sorted route" + tag, 0);
+  // rmsnorm: within one bf16 step of the oracle (the sum of squares runs in another order)
+  std::vector<uint16_t> xr((size_t)T * H);
+  orc_rmsnorm(x0.data(), H, L.post.data(), xr.data(), H, T, H, c.eps);
+  std::vector<float> xrf(xr.size());
+  for (size_t i = 0; i < xr.size(); i++) xrf[i] = bf2f(xr[i]);
+  const double en = bf16_err(xn, xrf, true);
+  report(en == 0.0, "encode_moe rmsnorm" + tag, en);
+  std::vector<int> ri((size_t)T * k);
+  std::vector<float> rwt((size_t)T * k), rsg((size_t)T);
+  orc_moe_route(logits.data(), 0, T, E, k, E1, 1, shared ? 1 : 0, ri.data(), rwt.data(), rsg.data());
+  double ew = 0;
+  for (size_t i = 0; i < rwt.size(); i++) ew = std::max(ew, (double)std::fabs(rwt[i] - wt[i]));
+  for (int t = 0; t < T && shared; t++) ew = std::max(ew, (double)std::fabs(rsg[t] - sg[t]));
+  report(ri == idx && ew <= 1e-5, "encode_moe routing (indices bit-exact)" + tag, ew);
+  // the checked tokens: all, or `check` spread evenly
+  std::vector<int> tok;
+  for (int i = 0; i < std::min(T, check); i++) tok.push_back(check >= T ? i : (int)((long)i * T / check));
+  const int C = (int)tok.size();
+  std::vector<uint16_t> xs((size_t)C * H), want((size_t)C * H), got((size_t)C * H);
+  std::vector<int> si((size_t)C * k);
+  std::vector<float> sw((size_t)C * k), ss((size_t)C);
+  for (int i = 0; i < C; i++) {
+    const int t = tok[i];
+    memcpy(&xs[(size_t)i * H], &xn[(size_t)t * H], H * 2);
+    memcpy(&want[(size_t)i * H], &x0[(size_t)t * H], H * 2);
+    memcpy(&got[(size_t)i * H], &x1[(size_t)t * H], H * 2);
+    for (int j = 0; j < k; j++) si[(size_t)i * k + j] = idx[(size_t)t * k + j], sw[(size_t)i * k + j] = wt[(size_t)t * k + j];
+    ss[i] = sg[t];
+  }
+  // the shared expert as expert E gets the gathered GEMM's qmm rounding; through gemm() on the MLX layout, the decode
+  // GEMV arithmetic up to 32 rows (ifd_gemm_w4) and qmm's above
+  const int shared_qmv = shared == 2 && T <= 32 ? 1 : 0;
+  orc_moe_experts(xs.data(), C, H, I, E, k, si.data(), sw.data(), ss.data(), L.egu.wq.data(), L.egu.s.data(),
+                  L.egu.b.data(), L.edn.wq.data(), L.edn.s.data(), L.edn.b.data(),
+                  shared ? L.sgu.wq.data() : nullptr, L.sgu.s.data(), L.sgu.b.data(), L.sdn.wq.data(), L.sdn.s.data(),
+                  L.sdn.b.data(), shared_qmv, want.data(), 0, nthreads);
+  std::vector<float> wf(want.size());
+  for (size_t i = 0; i < want.size(); i++) wf[i] = bf2f(want[i]);
+  // a chain of bf16 stages on both sides, compared end to end (the stages are checked one by one at the bar in
+  // tests/test_gpu_moe.py)
+  (void)bf16_err(got, wf, true);
+  report(g_rel_rms <= 1e-2 && g_raw <= 5e-2 && g_ulp1 <= 0.05,
+         "encode_moe x += moe(xn) on " + std::to_string(C) + " tokens (end to end)" + tag, g_raw);
+}
+
+void test_encode_moe_t64(std::mt19937& rng) {
+  MoeLayer L(MoeGeo{512, 32, 4, 256}, rng);
+  // 32-row tiles (R < 24 E) and 64-row tiles (T = 300: R = 1200), the shared expert folded in, through gemm(), or
+  // absent; state allocated for more rows than the call
+  run_moe_t64(L, 40, 40, 1, 1 << 30, 0, rng);
+  run_moe_t64(L, 40, 100, 2, 1 << 30, 0, rng);
+  run_moe_t64(L, 300, 300, 1, 1 << 30, 0, rng);
+  run_moe_t64(L, 300, 300, 2, 1 << 30, 0, rng);
+  run_moe_t64(L, 64, 64, 0, 1 << 30, 0, rng);
+}
+
+// encode_moe with 8-bit routed experts on the sorted route (MLX-layout stacks, the reference's mlx_gqmm_b8 through
+// gqmm at W.bits, qwen35.h:1835): x += MoE(xn) against the composition of the oracle's 8-bit qmm per routed row
+// (gathered GEMM = each row's own expert product), SwiGLU, the shared expert's 4-bit qmm and the weighted combine.
+void test_encode_moe_8bit_sorted(std::mt19937& rng) {
+  const int H = 512, E = 16, k = 4, I = 128, T = 40, R = T * k;
+  Config c;
+  c.hidden = H, c.experts = E, c.topk = k, c.moe_inter = I, c.eps = 1e-6f;
+  auto make8 = [&](int N, int K) {
+    HostLinear h{N, K, std::vector<uint32_t>((size_t)N * K / 4), std::vector<uint16_t>((size_t)N * K / 64), {}};
+    for (auto& w : h.wq) w = (uint32_t)rng();
+    std::uniform_real_distribution<float> su(0.0003f, 0.0012f);
+    h.b.resize(h.s.size());
+    for (size_t i = 0; i < h.s.size(); i++) h.s[i] = f2bf(su(rng)), h.b[i] = f2bf(-128.f * bf2f(h.s[i]));
+    return h;
+  };
+  const HostLinear egu = make8(E * 2 * I, H), edn = make8(E * H, I);
+  const HostLinear sgu = make_linear(2 * I, H, rng), sdn = make_linear(H, I, rng);
+  std::normal_distribution<float> nr(0.f, 0.02f);
+  std::vector<uint16_t> router((size_t)(E + 1) * H), post((size_t)H);
+  for (auto& v : router) v = f2bf(nr(rng));
+  for (auto& v : post) v = f2bf(1.f);
+  Layer ly;
+  ly.post_norm = upload(post);
+  ly.router.wq = upload(router);
+  ly.router.E = 1, ly.router.N = E + 1, ly.router.K = H, ly.router.bits = 16;
+  const QLinear gq = device_linear(egu), dq = device_linear(edn);
+  ly.egu.wq = gq.wq, ly.egu.s = gq.s, ly.egu.b = gq.b, ly.egu.E = E, ly.egu.N = 2 * I, ly.egu.K = H, ly.egu.bits = 8;
+  ly.edown.wq = dq.wq, ly.edown.s = dq.s, ly.edown.b = dq.b, ly.edown.E = E, ly.edown.N = H, ly.edown.K = I,
+  ly.edown.bits = 8;
+  ly.gate_up = device_linear(sgu), ly.down = device_linear(sdn);
+  Qwen35 m(c, T, I, 0);
+  Enc e;
+  const auto x0 = activations(T, H, rng);
+  hip_ok(hipMemcpy(m.x.ptr<void>(), x0.data(), x0.size() * 2, hipMemcpyHostToDevice), "x");
+  m.encode_moe(e, ly, T);
+  const auto x1 = download<uint16_t>(m.x, (size_t)T * H);
+  const auto xn = download<uint16_t>(m.xn, (size_t)T * H);
+  const auto idx = download<int>(m.ridx, (size_t)R);
+  const auto wt = download<float>(m.rw, (size_t)R);
+  const auto sg = download<float>(m.rsg, (size_t)T);
+  const std::string tag = " T=40 E=16 k=4 (8-bit routed experts)";
+  report(!m.moe_decode_route(ly, T) && !m.moe_t64_route(ly), "encode_moe takes the MLX sorted route" + tag, 0);
+  // routed rows r = t k + j in row order: yd[r] = bf16(qmm8(act_r, down_e)), act_r = silu_mul(bf16(qmm8(xn_t, gu_e)))
+  std::vector<uint16_t> yd((size_t)R * H), gu(2 * I), act(I);
+  std::vector<float> y1(2 * I), y2(H);
+  for (int r = 0; r < R; r++) {
+    const int ex = idx[r], t = r / k;
+    orc_qmm_b(&xn[(size_t)t * H], H, &egu.wq[(size_t)ex * 2 * I * H / 4], &egu.s[(size_t)ex * 2 * I * H / 64],
+              &egu.b[(size_t)ex * 2 * I * H / 64], 2 * I, H, 8, 0, y1.data(), 1, 0);
+    for (int i = 0; i < 2 * I; i++) gu[i] = f2bf(y1[i]);
+    orc_silu_mul(gu.data(), act.data(), I, 1);
+    orc_qmm_b(act.data(), I, &edn.wq[(size_t)ex * H * I / 4], &edn.s[(size_t)ex * H * I / 64],
+              &edn.b[(size_t)ex * H * I / 64], H, I, 8, 0, y2.data(), 1, 0);
+    for (int h = 0; h < H; h++) yd[(size_t)r * H + h] = f2bf(y2[h]);
+  }
+  // the shared expert through gemm() on the MLX layout: the decode GEMV arithmetic up to 32 rows, qmm's above
+  std::vector<float> ys1((size_t)T * 2 * I), ys2((size_t)T * H);
+  std::vector<uint16_t> sgu_o((size_t)T * 2 * I), sact((size_t)T * I), ys((size_t)T * H);
+  (T <= 32 ? orc_qmv : orc_qmm)(xn.data(), H, sgu.wq.data(), sgu.s.data(), sgu.b.data(), 2 * I, H, 0, ys1.data(), T, 0);
+  for (size_t i = 0; i < ys1.size(); i++) sgu_o[i] = f2bf(ys1[i]);
+  orc_silu_mul(sgu_o.data(), sact.data(), I, T);
+  (T <= 32 ? orc_qmv : orc_qmm)(sact.data(), I, sdn.wq.data(), sdn.s.data(), sdn.b.data(), H, I, 0, ys2.data(), T, 0);
+  for (size_t i = 0; i < ys2.size(); i++) ys[i] = f2bf(ys2[i]);
+  std::vector<int> inv(R);
+  for (int r = 0; r < R; r++) inv[r] = r;
+  std::vector<uint16_t> want = x0;
+  orc_moe_combine(want.data(), yd.data(), wt.data(), ys.data(), sg.data(), inv.data(), T, H, k, 0);
+  std::vector<float> wf(want.size());
+  for (size_t i = 0; i < want.size(); i++) wf[i] = bf2f(want[i]);
+  (void)bf16_err(x1, wf, true);
+  report(g_rel_rms <= 1e-2 && g_raw <= 5e-2 && g_ulp1 <= 0.05, "encode_moe x += moe(xn) (end to end)" + tag, g_raw);
+  for (void* p : {ly.post_norm.buf, ly.router.wq.buf, gq.wq.buf, gq.s.buf, gq.b.buf, dq.wq.buf, dq.s.buf, dq.b.buf,
+                  ly.gate_up.wq.buf, ly.gate_up.s.buf, ly.gate_up.b.buf, ly.down.wq.buf, ly.down.s.buf, ly.down.b.buf})
+    (void)hipFree(p);
+}
+
 template <class T>
 bool same_as_device(const std::vector<T>& host, const BufRef& d) {
   return host.empty() || download<T>(d, host.size()) == host;
@@ -634,6 +862,15 @@ int main(int argc, char** argv) {
     return 0;
   }
   std::mt19937 rng(20251201);
+  if (argc > 2 && std::string(argv[1]) == "--moe-c4") {
+    // H 2048, 512 experts, top-10, I 512, the shared expert; the oracle on up to 96 tokens spread
+    // over the batch, on 16 threads
+    const int T = atoi(argv[2]);
+    MoeLayer L(MoeGeo{2048, 512, 10, 512}, rng);
+    run_moe_t64(L, T, T, 1, 96, 16, rng);
+    printf(failures ? "%d FAILED\n" : "ALL OK\n", failures);
+    return failures ? 1 : 0;
+  }
   if (argc > 2 && std::string(argv[1]) == "--ckpt") {
     test_load(argv[2], rng);
     printf(failures ? "%d FAILED\n" : "ALL OK\n", failures);
@@ -646,6 +883,8 @@ int main(int argc, char** argv) {
     test_gemm(m, e, rng);
   }
   test_encode_moe(rng);
+  test_encode_moe_t64(rng);
+  test_encode_moe_8bit_sorted(rng);
   printf(failures ? "%d FAILED\n" : "ALL OK\n", failures);
   return failures ? 1 : 0;
 }
