@@ -201,6 +201,26 @@ def main():
             ms_b = timed(lambda i: ops.mlp_decode(Xb[M], nw, 1e-6, *layers[i % ncp]), args.steps * 2, 3)
             mlp_block[f"M{M}"] = dict(us=ms_b * 1e3, gbs=(w_bytes + M * (4 * H_DEC + 2 * I_DEC) * 2) / (ms_b * 1e-3) / 1e9)
         out["mlp_block"] = mlp_block
+        # the reference's default decode route for flipped weights (qwen35.h:1576): per-(row, 64-group) int8
+        # activations, W4A8 gate_up, silu_mul_a8 (the next GEMM's int8 rows, core.metal:789-814), W4A8 down, both
+        # GEMMs on the T64 copies (int8 rows as exact bf16 integers through the affine T64 kernels); bytes as value's
+        # plus the gate/up product written and read (229,376 B per row: no SwiGLU epilogue on this route)
+        w4a8_route = {}
+        GUb = {M: torch.empty((M, 2 * I_DEC), dtype=torch.bfloat16, device=dev) for M in Ms}
+
+        def w4a8_mlp(M, c):
+            gu, dn = layers[c % ncp]
+            U, XS = ops.a8_quant(A[M], False)
+            ops.gemm_t64_w4a8(U, XS, gu, GUb[M], per_token=False)
+            Uh, XSh = ops.silu_mul_a8(GUb[M], False)
+            ops.gemm_t64_w4a8(Uh, XSh, dn, Y[M], per_token=False)
+
+        for M in Ms:
+            if M < 3:
+                continue  # the reference takes the decode GEMV up to qmv_max = 2 rows
+            ms_w = timed(lambda i: w4a8_mlp(M, i), args.steps, 3)
+            w4a8_route[f"M{M}"] = dict(us=ms_w * 1e3, gbs=(w_bytes + M * ROW_BYTES_UNFUSED) / (ms_w * 1e-3) / 1e9)
+        out["w4a8_route"] = w4a8_route
         dom = max(calls, key=lambda k: calls[k][0])
         ms_d, b_d, f_d = calls[dom]
         achieved = b_d / (ms_d * 1e-3) / 1e9
@@ -460,6 +480,7 @@ def main():
             "value_unfused_count": round(h["value_unfused_count"], 1),
             "per_M": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in out["per_M"].items()},
             "mlp_block": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in out["mlp_block"].items()},
+            "w4a8_route": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in out["w4a8_route"].items()},
         })
     if cpu:
         line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()}

@@ -248,9 +248,27 @@ int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, 
   return launch_gemm_t((const uint16_t*)A, lda, wt, N, K, C, ldc, M, mode, w.body, w.bytes, S(stream));
 }
 
+// Per-group activations: [Ab = bf16(U) | sxT | the GEMM's own workspace] in the body.
+namespace {
+struct W4a8gLayout {
+  size_t ab, sxt, gemm, total;
+  int Mp;
+};
+W4a8gLayout w4a8g_layout(int M, int N, int K, int mode) {
+  W4a8gLayout L{};
+  L.Mp = w4a8g_mp(M);
+  L.ab = 0;
+  L.sxt = align_up((size_t)M * K * 2, 256);
+  L.gemm = L.sxt + align_up((size_t)(K / 64) * L.Mp * 4, 256);
+  L.total = L.gemm + (M <= 16 ? qmv_t_workspace(M, N, K, mode) : gemm_t_a8_workspace(M, N, K, mode));
+  return L;
+}
+}  // namespace
+
 size_t ifd_gemm_t64_w4a8_workspace(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
-  return with_header(w4a8_t_workspace(M, N, K));
+  // either form of the activations: per token, or per group (modes 0 and 1 size alike, mode 2 no larger)
+  return with_header(std::max(w4a8_t_workspace(M, N, K), w4a8g_layout(M, N, K, 0).total));
 }
 
 int ifd_gemm_t64_w4a8(const int8_t* U, const float* XS, int per_token, const void* wt, int N, int K, void* C, int ldc,
@@ -258,12 +276,25 @@ int ifd_gemm_t64_w4a8(const int8_t* U, const float* XS, int per_token, const voi
   IFD_CHECK(M >= 0 && N > 0 && K > 0 && K % 256 == 0, "bad shape M=%d N=%d K=%d (K multiple of 256)", M, N, K);
   IFD_CHECK(mode >= 0 && mode <= 2, "mode=%d must be 0, 1 or 2", mode);
   IFD_CHECK(ldc >= N, "bad stride ldc=%d", ldc);
-  if (!per_token) return fail(IFD_ERR_UNSUPPORTED, "T64 W4A8 takes per-token activations (per_token = 1)");
+  IFD_CHECK(per_token == 0 || per_token == 1, "per_token=%d must be 0 (per 64-group) or 1 (per row)", per_token);
   if (M == 0) return IFD_OK;
   IFD_CHECK(U && XS && wt && C && aligned(U, 16) && aligned(wt, 16), "null or misaligned pointer");
   IFD_CHECK(!workspace || aligned(workspace, 16), "workspace must be 16-byte aligned");
   const WsView w = ws_view(workspace, ws_bytes);
-  return launch_w4a8_t(U, XS, wt, N, K, C, ldc, M, mode, w.body, w.bytes, S(stream));
+  if (per_token) return launch_w4a8_t(U, XS, wt, N, K, C, ldc, M, mode, w.body, w.bytes, S(stream));
+  // per (row, 64-group) scales: xq as bf16 integers through the affine T64 kernels
+  const W4a8gLayout L = w4a8g_layout(M, N, K, mode);
+  if (!w.body || w.bytes < L.total)
+    return fail(IFD_ERR_WORKSPACE, "gemm_t64_w4a8 needs %zu bytes of workspace, got %zu", with_header(L.total),
+                ws_bytes);
+  char* b = (char*)w.body;
+  uint16_t* Ab = (uint16_t*)(b + L.ab);
+  float* sxT = (float*)(b + L.sxt);
+  hipStream_t st = S(stream);
+  IFD_TRY(launch_w4a8g_prep(U, XS, M, K, Ab, sxT, L.Mp, st));
+  if (M <= 16)
+    return launch_qmv_t_a8(Ab, XS, wt, N, K, C, ldc, M, mode, w.cnt, b + L.gemm, w.bytes - L.gemm, st);
+  return launch_gemm_t_a8(Ab, sxT, L.Mp, wt, N, K, C, ldc, M, mode, b + L.gemm, w.bytes - L.gemm, st);
 }
 
 // ---- T64x8 layout (8-bit weights) --------------------------------------------------------------------------------

@@ -23,6 +23,11 @@
 //    arithmetic (engine/kernels/core.metal:85-171).
 //  DEQ = true: codes are dequantized in registers to bf16(s q + b) (MLX qmm rounding, quantized.h:528-535) and
 //    accumulate over K; one dequant feeds MT MFMA tiles: the cheaper choice from 4 M tiles up.
+//  A8 (with DEQ = false): the reference's W4A8 GEMM with per-(row, 64-group) int8 activations (w4a8.metal:24-98):
+//    A holds the int8 codes xq as exact bf16 integers, so the MFMAs give P = sum (128 + q) xq and X = sum xq exactly
+//    (every partial sum is an integer below 2^24), and per group acc += sx (s P + (b - 128 s) X) with sx the row's
+//    scale for that group, = sx s sum q xq + sx b sum xq: the reference's S sx P + B (sx sum xq). The stage also
+//    holds the chunk's sx for the tile's rows (from a transposed copy sxT [G][Mp]), DMAd by waves 2 and 3.
 #include <algorithm>
 
 #include "common.h"
@@ -44,26 +49,32 @@ struct GemmTArgs {
   float* part;
   int gps;
   int tiles_m, tiles_n;
+  const float* sxT;  // A8: the activation scales transposed, [G][Mp] (rows past M zero)
+  int Mp;
 };
 
 constexpr int kGtBand = 4;  // M tiles per band of the tile order
 constexpr int kGtThreads = 512;
 
-// bytes of one pipeline stage, and the stages that fit in 160 KB of LDS
-__host__ __device__ constexpr int gt_stage_bytes(int MT, int NB) { return MT * 32 * 256 + 2 * 4 * NB * kT64Codes + 2 * 1024; }
-__host__ __device__ constexpr int gt_stages(int MT, int NB) {
-  return 160 * 1024 / gt_stage_bytes(MT, NB) < 6 ? 160 * 1024 / gt_stage_bytes(MT, NB) : 6;
+// bytes of one pipeline stage, and the stages that fit in 160 KB of LDS; A8 adds [2 groups][256 rows] sx
+__host__ __device__ constexpr int gt_stage_bytes(int MT, int NB, bool A8 = false) {
+  return MT * 32 * 256 + 2 * 4 * NB * kT64Codes + 2 * 1024 + (A8 ? 2 * 1024 : 0);
+}
+__host__ __device__ constexpr int gt_stages(int MT, int NB, bool A8 = false) {
+  return 160 * 1024 / gt_stage_bytes(MT, NB, A8) < 6 ? 160 * 1024 / gt_stage_bytes(MT, NB, A8) : 6;
 }
 
-template <int MT, int NB, bool DEQ>
+template <int MT, int NB, bool DEQ, bool A8 = false>
 __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
-  constexpr int NS = gt_stages(MT, NB);
+  constexpr int NS = gt_stages(MT, NB, A8);
   static_assert(NB >= 1 && NB <= 2, "one (s, b) DMA covers a group's NBB <= 8 tiles");
+  static_assert(!(A8 && DEQ), "the W4A8 form is the affine arithmetic");
   constexpr int BM = 32 * MT, NBB = 4 * NB;
   constexpr int A_BYTES = BM * 256;             // [BM][128 bf16]
   constexpr int C_BYTES = 2 * NBB * kT64Codes;  // [2 groups][NBB bands][1024]
-  constexpr int ST = A_BYTES + C_BYTES + 2 * 1024;  // + [2 groups][1 KB] (s, b)
-  static_assert(ST == gt_stage_bytes(MT, NB) && NS >= 3, "stage layout");
+  constexpr int SX_OFF = A_BYTES + C_BYTES + 2 * 1024;  // A8: [2 groups][256] sx
+  constexpr int ST = SX_OFF + (A8 ? 2 * 1024 : 0);  // + [2 groups][1 KB] (s, b)
+  static_assert(ST == gt_stage_bytes(MT, NB, A8) && NS >= 3, "stage layout");
   constexpr int VPC = MT + NB;                  // DMA instructions per wave per chunk (waves 0, 1: one more)
   constexpr int NE = MT * NB * 16;              // accumulators per lane
   extern __shared__ __align__(16) uint8_t lds[];
@@ -106,6 +117,8 @@ __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
   const uint8_t* sbsrc = p.wt +
                          (size_t)min(tn * NBB + (lane % (8 * NBB)) / 8, nbands - 1) * kT64Tile + kT64Codes +
                          16 * (lane & 7) + (size_t)(wave & 1) * gstride;
+  // A8: waves 2 and 3 DMA the sx of rows m0 .. m0 + 255 for group (wave - 2) of the chunk (sxT is padded past them)
+  const float* sxsrc = A8 ? p.sxT + (size_t)(wave & 1) * p.Mp + m0 + 4 * lane : nullptr;
 
   auto issue = [&](int chunk, int stage) {
     const size_t g = (size_t)min(g0 + 2 * chunk, lastg);
@@ -116,6 +129,9 @@ __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
     for (int b = 0; b < NB; b++)
       dma16(tb[b] + g * gstride, st + A_BYTES + (kq * NBB + wq * NB + b) * kT64Codes);
     if (wave < 2) dma16(sbsrc + g * gstride, st + A_BYTES + C_BYTES + wave * 1024);
+    if constexpr (A8) {
+      if (wave >= 2 && wave < 4) dma16(sxsrc + g * (size_t)p.Mp, st + SX_OFF + (wave - 2) * 1024);
+    }
   };
 
   f32x16 acc[MT][NB];
@@ -188,14 +204,28 @@ __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
         f32x16 X = zero16();
 #pragma unroll
         for (int t = 0; t < 4; t++) X = mfma_bf16(af[t], ones, X);
+        // A8: the sx of this lane's 16 rows (a 32 + 8 q + 4 h + 0..3) for group kq
+        float sxv[16];
+        if constexpr (A8) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const u32x4 v = *(const u32x4*)(st + SX_OFF + kq * 1024 + (a * 32 + 8 * q + 4 * h) * 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) sxv[4 * q + e] = __uint_as_float(v[e]);
+          }
+        }
 #pragma unroll
         for (int b = 0; b < NB; b++) {
           f32x16 P = zero16();
 #pragma unroll
           for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], bfr[b][t], P);
 #pragma unroll
-          for (int r2 = 0; r2 < 16; r2++)
-            acc[a][b][r2] = __builtin_fmaf(sc[b], P[r2], __builtin_fmaf(bp[b], X[r2], acc[a][b][r2]));
+          for (int r2 = 0; r2 < 16; r2++) {
+            if constexpr (A8)
+              acc[a][b][r2] = __builtin_fmaf(sxv[r2], __builtin_fmaf(sc[b], P[r2], bp[b] * X[r2]), acc[a][b][r2]);
+            else
+              acc[a][b][r2] = __builtin_fmaf(sc[b], P[r2], __builtin_fmaf(bp[b], X[r2], acc[a][b][r2]));
+          }
         }
       }
     }
@@ -208,7 +238,7 @@ __global__ __launch_bounds__(kGtThreads, 1) void k_gemm_t(GemmTArgs p) {
 #pragma unroll
   for (int s = 0; s < NS - 1; s++) issue(s, s);
   for (int c = 0; c < nch; c++) {
-    if (wave < 2) wait_vm_barrier<(VPC + 1) * (NS - 2)>();
+    if (wave < (A8 ? 4 : 2)) wait_vm_barrier<(VPC + 1) * (NS - 2)>();
     else wait_vm_barrier<VPC * (NS - 2)>();
     issue(c + NS - 1, (c + NS - 1) % NS);
     compute(c % NS);
@@ -258,11 +288,13 @@ struct GtPlan {
   int MT, NB, S, gps;
   bool deq;
 };
-static GtPlan gemm_t_plan(int M, int N, int K) {
+// Mrows: the rows the tiles cover (M, or more when the tile height is chosen for fewer rows)
+static GtPlan gemm_t_plan(int M, int N, int K, int Mrows = 0) {
   GtPlan pl{};
   pl.MT = M <= 32 ? 1 : M <= 64 ? 2 : 4;
   pl.NB = 2;
   pl.deq = pl.MT == 4;
+  if (Mrows > M) M = Mrows;
   const int G = K / kGroup;
   const long tiles = (long)((M + 32 * pl.MT - 1) / (32 * pl.MT)) * ((t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB));
   const long smax = std::max(1L, std::min<long>(G / 8, (64L << 20) / ((long)M * N * 4)));
@@ -291,18 +323,45 @@ size_t gemm_t_workspace(int M, int N, int K, int mode) {
   return epilogue_ws_bytes(gemm_t_plan(M, N, K).S, M, N, mode);
 }
 
-template <int MT, int NB, bool DEQ>
+template <int MT, int NB, bool DEQ, bool A8 = false>
 static int launch_gemm_t_cfg(const GemmTArgs& p, int S, hipStream_t st) {
-  const size_t pipe = (size_t)gt_stages(MT, NB) * gt_stage_bytes(MT, NB);
+  const size_t pipe = (size_t)gt_stages(MT, NB, A8) * gt_stage_bytes(MT, NB, A8);
   const size_t red = (size_t)4 * MT * NB * 16 * 64 * sizeof(float);  // quad 1's sums, after the K loop
   const size_t lds = std::max(pipe, red);
   static bool attr = false;
   if (!attr) {
-    hipFuncSetAttribute((const void*)k_gemm_t<MT, NB, DEQ>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)k_gemm_t<MT, NB, DEQ, A8>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)lds);
     attr = true;
   }
-  hipLaunchKernelGGL((k_gemm_t<MT, NB, DEQ>), dim3(p.tiles_m * p.tiles_n, S), dim3(kGtThreads), lds, st, p);
+  hipLaunchKernelGGL((k_gemm_t<MT, NB, DEQ, A8>), dim3(p.tiles_m * p.tiles_n, S), dim3(kGtThreads), lds, st, p);
   return check_launch("gemm_t64");
+}
+
+// W4A8 with per-(row, 64-group) scales on T64 weights past the decode GEMV's rows: Ab = the int8 rows as bf16
+// integers [M][K], sxT = their scales transposed [G][Mp] (Mp >= 128 tiles + 256, zero past M); the affine pipeline
+// for every tile height. Workspace: the K-split partials (epilogue_ws_bytes of the plan).
+// 64-row tiles at most: the affine form has no dequant to share across M tiles, and four tiles' accumulators with
+// their row scales spill registers
+static GtPlan gemm_t_a8_plan(int M, int N, int K) { return gemm_t_plan(std::min(M, 64), N, K, M); }
+size_t gemm_t_a8_workspace(int M, int N, int K, int mode) {
+  return epilogue_ws_bytes(gemm_t_a8_plan(M, N, K).S, M, N, mode);
+}
+int launch_gemm_t_a8(const uint16_t* Ab, const float* sxT, int Mp, const void* wt, int N, int K, void* C, int ldc,
+                     int M, int mode, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (M == 0) return IFD_OK;
+  if (K % 128) return fail(IFD_ERR_ARG, "T64 W4A8 needs K %% 128 == 0 (K=%d)", K);
+  if (mode == kModeSwiglu) return fail(IFD_ERR_UNSUPPORTED, "T64 W4A8: no SwiGLU mode");
+  const GtPlan pl = gemm_t_a8_plan(M, N, K);
+  const size_t need = epilogue_ws_bytes(pl.S, M, N, mode);
+  if (need > ws_bytes || (need && !ws))
+    return fail(IFD_ERR_WORKSPACE, "gemm_t64_w4a8 needs %zu bytes of workspace, got %zu", need, ws_bytes);
+  GemmTArgs p{Ab, K, (const uint8_t*)wt, N, K, C, ldc, M, mode, (float*)ws, pl.gps,
+              (M + 32 * pl.MT - 1) / (32 * pl.MT), (t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB), sxT, Mp};
+  const int rc = pl.MT == 1 ? launch_gemm_t_cfg<1, 2, false, true>(p, pl.S, st)
+                            : launch_gemm_t_cfg<2, 2, false, true>(p, pl.S, st);
+  IFD_TRY(rc);
+  return launch_epilogue(ws, pl.S, M, N, C, ldc, mode, st);
 }
 
 int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
@@ -329,7 +388,7 @@ int launch_gemm_t(const uint16_t* A, int lda, const void* wt, int N, int K, void
   // the SwiGLU mode without a split stores the bf16 product into the workspace for silu_mul
   const bool via_ws = mode == kModeSwiglu && pl.S == 1;
   GemmTArgs p{A, lda, (const uint8_t*)wt, N, K, via_ws ? ws : C, via_ws ? N : ldc, M, via_ws ? 0 : mode, (float*)ws,
-              pl.gps, (M + 32 * pl.MT - 1) / (32 * pl.MT), (t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB)};
+              pl.gps, (M + 32 * pl.MT - 1) / (32 * pl.MT), (t64_bands(N) + 4 * pl.NB - 1) / (4 * pl.NB), nullptr, 0};
   int rc;
   if (pl.MT == 1) rc = launch_gemm_t_cfg<1, 2, false>(p, pl.S, st);
   else if (pl.MT == 2) rc = launch_gemm_t_cfg<2, 2, false>(p, pl.S, st);

@@ -107,6 +107,16 @@ int launch_w8a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K
 // cnt: kWsCounters zeroed counters (the workspace header) for the in-kernel split-K fixup; null -> a reduction kernel
 int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                  unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st);
+// W4A8 with per-(row, 64-group) int8 activations on T64 weights, in the affine bf16-MFMA form (xq as exact bf16
+// integers): the prep writes Ab = bf16(U) [M][K] and sxT = sx transposed [G][Mp] (zero past M); M <= 16 runs the
+// decode GEMV (qmv_t_workspace(M, N, K, mode)), more rows the affine k_gemm_t (gemm_t_a8_workspace).
+int w4a8g_mp(int M);
+int launch_w4a8g_prep(const int8_t* U, const float* XS, int M, int K, uint16_t* Ab, float* sxT, int Mp, hipStream_t st);
+int launch_qmv_t_a8(const uint16_t* Ab, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M,
+                    int mode, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st);
+size_t gemm_t_a8_workspace(int M, int N, int K, int mode);
+int launch_gemm_t_a8(const uint16_t* Ab, const float* sxT, int Mp, const void* wt, int N, int K, void* C, int ldc,
+                     int M, int mode, void* ws, size_t ws_bytes, hipStream_t st);
 
 // MoE.
 int launch_router_logits(const uint16_t* x, const uint16_t* w, int T, int H, int E1, int out_bf16, void* logits,

@@ -193,6 +193,8 @@ struct Qwen35 {
           need = std::max(need, ifd_gemm_t64_workspace(T, H, shared_inter));
           need = std::max(need, ifd_qmm_w4a8_workspace(T, 2 * shared_inter, H));
           need = std::max(need, ifd_qmm_w4a8_workspace(T, H, shared_inter));
+          need = std::max(need, ifd_gemm_t64_w4a8_workspace(T, 2 * shared_inter, H));
+          need = std::max(need, ifd_gemm_t64_w4a8_workspace(T, H, shared_inter));
           need = std::max(need, ifd_gemm_t64x8_workspace(T, 2 * shared_inter, H));  // an 8-bit shared expert
           need = std::max(need, ifd_gemm_t64x8_workspace(T, H, shared_inter));
         }
@@ -301,12 +303,21 @@ struct Qwen35 {
   }
 
   // The reference's W4A8 GEMM (qwen35.h:1323-1365): per-group int8 activations (a8_quant, unless a fused producer
-  // wrote them) times the flipped 4- or 8-bit codes on the integer path.
+  // wrote them) times the flipped 4- or 8-bit codes on the integer path. A 4-bit layer's T64 copy (always the
+  // unflipped codes) runs it on the T64 kernels with the same per-group scales.
   void w4a8(Enc& e, const BufRef& A, const QLinear& W, const BufRef& C, int M, int mode) {
     if (M > max_rows || W.K > a8_k) die("gemm", "W4A8 rows past the int8 staging buffers (max_rows, a8_k)");
     if (!a8_ready)
       ok(ifd_a8_quant(A.ptr<void>(), W.K, M, W.K, 0, a8u.ptr<int8_t>(), a8x.ptr<float>(), e.stream), "gemm");
     a8_ready = false;
+    if (W.bits == 4 && W.t64 && W.K % 256 == 0) {
+      const size_t need = ifd_gemm_t64_w4a8_workspace(M, W.N, W.K);
+      if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
+      ok(ifd_gemm_t64_w4a8(a8u.ptr<int8_t>(), a8x.ptr<float>(), 0, W.t64.ptr<void>(), W.N, W.K, C.ptr<void>(), W.N, M,
+                           mode, splitk.ptr<void>(), splitk_bytes, e.stream),
+         "gemm");
+      return;
+    }
     const bool w8 = W.bits == 8;
     const size_t need = w8 ? ifd_qmm_w8a8_workspace(M, W.N, W.K) : ifd_qmm_w4a8_workspace(M, W.N, W.K);
     if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");

@@ -68,6 +68,7 @@ struct QmvTArgs {
   unsigned* cnt;  // null: partials only, a reduction kernel follows
   int sw_half;    // SwiGLU fixup: number of gate column tiles (0: plain store mode)
   int gps;
+  const float* XS;  // A8: the rows' (sx, sx sum xq) per 64-group [M][K / 64][2] (A holds xq as bf16 integers)
 };
 
 constexpr int kTB = 2;     // groups per pipeline block
@@ -87,7 +88,10 @@ __device__ __forceinline__ u32x4 t64_bf16_off128(uint32_t w) {
 
 // BITS = 8: T64x8 tiles (two 1 KB code halves per lane group; the exact q as bf16 and the bias b, the reference's
 // qmv8 arithmetic s * sum q x + b * sum x, core.metal:175-248).
-template <int RACT, int BITS>
+// A8: the reference's W4A8 GEMM with per-(row, 64-group) int8 activations (w4a8.metal:24-98): A holds xq as exact
+// bf16 integers, so P and the group sums X are exact integers, and per group acc += sx (s P + (b - 128 s) X), the
+// row's group scale sx staged beside X.
+template <int RACT, int BITS, bool A8 = false>
 __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   constexpr int NH = BITS / 4, TILEB = BITS == 8 ? kT64x8Tile : kT64Tile, CODES = BITS == 8 ? kT64x8Codes : kT64Codes;
   extern __shared__ __align__(16) uint16_t lds[];
@@ -99,6 +103,7 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   const int Kz = Gz * kGroup, ldA = Kz + 8, M = p.M;
   uint16_t* As = lds;
   float* Xs = (float*)((char*)lds + ((size_t)M * ldA * 2 + 15) / 16 * 16);  // [Gz][16]
+  float* Ss = Xs + (size_t)Gz * 16;                                          // A8: [Gz][16] sx
 
   // this wave's band; its first block of tiles is requested before the activations are staged, so the weight
   // stream starts one memory latency earlier
@@ -151,8 +156,11 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
       }
     }
   }
-  for (int i = tid; i < Gz * 16; i += 256)
-    if ((i & 15) >= M) Xs[i] = 0.f;
+  for (int i = tid; i < Gz * 16; i += 256) {
+    const int m = i & 15, gl = i >> 4;
+    if (m >= M) Xs[i] = 0.f;
+    if constexpr (A8) Ss[i] = m < M ? p.XS[((size_t)m * G + g0 + gl) * 2] : 0.f;
+  }
   __syncthreads();
 
   const bool aok = j < M;
@@ -182,8 +190,17 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
       const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       const float sc = bf2f((uint16_t)(B.sb[i] & 0xFFFFu)), bi = bf2f((uint16_t)(B.sb[i] >> 16));
       const float bp = BITS == 4 ? __builtin_fmaf(-128.f, sc, bi) : bi;
+      if constexpr (A8) {
+        const float4 s0 = *(const float4*)(Ss + gl * 16 + 4 * h);
+        float4 s1 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (RACT > 4) s1 = *(const float4*)(Ss + gl * 16 + 8 + 4 * h);
+        const float ss[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-      for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[r]));
+        for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(ss[r], __builtin_fmaf(sc, P[r], bp * xs[r]), acc[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < RACT; r++) acc[r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[r]));
+      }
     }
   };
   if (live) {  // waves past the last band skip the stream but take part in the fixup's barriers
@@ -312,9 +329,10 @@ size_t qmv_t_workspace(int M, int N, int K, int mode, int bits) {
   return epilogue_ws_bytes(qmv_t_plan(M, N, K, bits).S, M, N, mode);
 }
 
-template <int BITS>
+template <int BITS, bool A8 = false>
 static int launch_qmv_t_bits(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M,
-                             int mode, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
+                             int mode, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st,
+                             const float* XS = nullptr) {
   if (M == 0) return IFD_OK;
   if (M > 16) return fail(IFD_ERR_UNSUPPORTED, "T64 decode kernel takes M <= 16");
   if (K % (kGroup * kTB)) return fail(IFD_ERR_ARG, "T64 decode needs K %% %d == 0 (K=%d)", kGroup * kTB, K);
@@ -338,13 +356,15 @@ static int launch_qmv_t_bits(const uint16_t* A, int lda, const void* wt, int N, 
              (uint32_t)(pl.S > 1 ? need : 0),
              fix ? cnt : nullptr,
              fix && mode == kModeSwiglu ? (t64_bands(N) + 3) / 4 / 2 : 0,
-             pl.gps};
+             pl.gps,
+             XS};
   const int Kz = pl.gps * kGroup;
-  const size_t lds = ((size_t)M * (Kz + 8) * 2 + 15) / 16 * 16 + (size_t)pl.gps * 16 * sizeof(float);
+  const size_t lds =
+      ((size_t)M * (Kz + 8) * 2 + 15) / 16 * 16 + (size_t)pl.gps * 16 * sizeof(float) * (A8 ? 2 : 1);
   if (lds > 64 * 1024) return fail(IFD_ERR_UNSUPPORTED, "qmv_t64: %zu bytes of LDS needed", lds);
   dim3 grid((t64_bands(N) + 3) / 4, pl.S), block(256);
-  if (M <= 8) hipLaunchKernelGGL((k_qmv_t<4, BITS>), grid, block, lds, st, p);
-  else hipLaunchKernelGGL((k_qmv_t<8, BITS>), grid, block, lds, st, p);
+  if (M <= 8) hipLaunchKernelGGL((k_qmv_t<4, BITS, A8>), grid, block, lds, st, p);
+  else hipLaunchKernelGGL((k_qmv_t<8, BITS, A8>), grid, block, lds, st, p);
   IFD_TRY(check_launch("qmv_t64"));
   if (fix) return IFD_OK;
   return launch_epilogue(ws, pl.S, M, N, C, ldc, mode, st);
@@ -358,6 +378,14 @@ int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void*
 int launch_qmv_t8(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                   unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
   return launch_qmv_t_bits<8>(A, lda, wt, N, K, C, ldc, M, mode, cnt, ws, ws_bytes, st);
+}
+
+// The W4A8 form of the decode GEMV (per-group int8 activations): Ab = xq as bf16 integers [M][K], XS their
+// (sx, sx sum xq) per group.
+int launch_qmv_t_a8(const uint16_t* Ab, const float* XS, const void* wt, int N, int K, void* C, int ldc, int M,
+                    int mode, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (mode == kModeSwiglu) return fail(IFD_ERR_UNSUPPORTED, "T64 W4A8: no SwiGLU mode");
+  return launch_qmv_t_bits<4, true>(Ab, K, wt, N, K, C, ldc, M, mode, cnt, ws, ws_bytes, st, XS);
 }
 
 }  // namespace ifd

@@ -47,6 +47,40 @@ __global__ __launch_bounds__(256) void k_w4a8_xprep(const float* __restrict__ XS
   Xhl[(size_t)M * Gx + i] = f2bf(lo);
 }
 
+// The per-group W4A8 form's operands: Ab = U as exact bf16 integers [M][K] (8 per thread) and sxT[g][m] = sx of
+// (row m, group g) = XS[m][g][0], zero for m in [M, Mp).
+__global__ __launch_bounds__(256) void k_w4a8g_prep(const int8_t* __restrict__ U, const float* __restrict__ XS, int M,
+                                                    int K, uint16_t* __restrict__ Ab, float* __restrict__ sxT,
+                                                    int Mp) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, n8 = (size_t)M * K / 8;
+  if (i < n8) {
+    const u32x2 q = *(const u32x2*)(U + 8 * i);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t w = q[e / 2] >> (16 * (e % 2));
+      const float lo = (float)(int8_t)(w & 0xFFu), hi = (float)(int8_t)((w >> 8) & 0xFFu);
+      o[e] = (uint32_t)f2bf(lo) | (uint32_t)f2bf(hi) << 16;  // integers |x| <= 128: exact in bf16
+    }
+    *(u32x4*)(Ab + 8 * i) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+  const int G = K / kGroup;
+  if (i < (size_t)G * Mp) {
+    const int g = (int)(i / Mp), m = (int)(i % Mp);
+    sxT[i] = m < M ? XS[((size_t)m * G + g) * 2] : 0.f;
+  }
+}
+
+int w4a8g_mp(int M) { return (M + 127) / 128 * 128 + 256; }
+
+int launch_w4a8g_prep(const int8_t* U, const float* XS, int M, int K, uint16_t* Ab, float* sxT, int Mp,
+                      hipStream_t st) {
+  const size_t n = std::max((size_t)M * K / 8, (size_t)(K / kGroup) * Mp);
+  if (n == 0) return IFD_OK;
+  hipLaunchKernelGGL(k_w4a8g_prep, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, U, XS, M, K, Ab, sxT, Mp);
+  return check_launch("w4a8g prep");
+}
+
 struct W4A8TArgs {
   const int8_t* U;    // [M][K] int8, row stride K
   const float* XS;    // [M][G][2]: sx = XS[m][0][0] (per token)

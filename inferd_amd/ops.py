@@ -104,16 +104,18 @@ def gemm_t64_swiglu(A: torch.Tensor, W: T64Linear, out: Optional[torch.Tensor] =
 
 
 def gemm_t64_w4a8(U: torch.Tensor, XS: torch.Tensor, W: T64Linear, C: Optional[torch.Tensor] = None,
-                  mode: int = 0) -> torch.Tensor:
-    """C (mode) = W4A8 product of per-token int8 activations (ops.a8_quant(A, True)) with T64 weights."""
+                  mode: int = 0, per_token: bool = True) -> torch.Tensor:
+    """C (mode) = W4A8 product of int8 activations with T64 weights: per-token (ops.a8_quant(A, True)) on the int8
+    MFMA kernels, or per 64-group (ops.a8_quant(A, False), the reference's default W4A8 route) on the affine T64
+    kernels."""
     M, K = U.shape
     assert K == W.K and U.dtype == torch.int8 and U.is_contiguous()
     if C is None:
         C = torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=U.device)
     need = lib().ifd_gemm_t64_w4a8_workspace(M, W.N, W.K)
     ws = workspace(need, U.device) if need else None
-    check(lib().ifd_gemm_t64_w4a8(_p(U), _p(XS), 1, _p(W.wt), W.N, W.K, _p(C), C.shape[1], M, mode, _p(ws),
-                                  ws.numel() if ws is not None else 0, _stream()))
+    check(lib().ifd_gemm_t64_w4a8(_p(U), _p(XS), 1 if per_token else 0, _p(W.wt), W.N, W.K, _p(C), C.shape[1], M,
+                                  mode, _p(ws), ws.numel() if ws is not None else 0, _stream()))
     return C
 
 

@@ -308,8 +308,47 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
     report(e1 <= 1e-2, "rmsnorm_for -> gemm (W4A8) vs the oracle", e1);
     e1 = bf16_err(outs[0][1], ref_wxa8(hr, M, I, hd.wq.data(), hd.s.data(), hd.b.data(), N, 4), false);
     report(e1 <= 1e-2, "silu_mul_for -> gemm (W4A8) vs the oracle", e1);
+    // the same flipped layers with their T64 copies (the unflipped codes, as the loader packs them): the W4A8 route
+    // then runs on T64 (the decode GEMV up to 16 rows, the affine K-split kernel above) with the same per-group
+    // int8 activations, for plain and fused producers
+    void* tf = nullptr;
+    void* td = nullptr;
+    hip_ok(hipMalloc(&tf, ifd_t64_bytes(N, K, 1)), "t64");
+    hip_ok(hipMalloc(&td, ifd_t64_bytes(N, I, 1)), "t64");
+    ok(ifd_pack_t64(Wf.wq.ptr<uint32_t>(), Wf.s.ptr<uint16_t>(), Wf.b.ptr<uint16_t>(), N, K, 0, 0x88888888u, 1, tf,
+                    e.stream),
+       "pack_t64");
+    ok(ifd_pack_t64(Wd.wq.ptr<uint32_t>(), Wd.s.ptr<uint16_t>(), Wd.b.ptr<uint16_t>(), N, I, 0, 0x88888888u, 1, td,
+                    e.stream),
+       "pack_t64");
+    Wf.t64 = BufRef(tf), Wd.t64 = BufRef(td);
+    for (int Mt : {3, 16, 17, 40, 100, 200}) {
+      const auto A = activations(Mt, K, rng);
+      BufRef dA = upload(A), dC = upload(std::vector<uint16_t>((size_t)Mt * N));
+      m.gemm(e, dA, Wf, dC, Mt, 0);
+      const double err =
+          bf16_err(download<uint16_t>(dC, (size_t)Mt * N), ref_wxa8(A, Mt, K, h.wq.data(), h.s.data(), h.b.data(), N, 4),
+                   false);
+      report(err <= 1e-2 && m.w4a8_route(Wf, Mt), "gemm flipped weights, T64 copy, M=" + std::to_string(Mt) +
+                                                      " (W4A8 route on T64)", err);
+      (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+    }
+    {
+      BufRef c1 = upload(std::vector<uint16_t>((size_t)M * N)), c2 = upload(std::vector<uint16_t>((size_t)M * N));
+      m.rmsnorm_for(e, dx, dw, dxn, M, K, Wf);
+      m.gemm(e, dxn, Wf, c1, M, 0);
+      m.silu_mul_for(e, dgu, dact, I, M, Wd);
+      m.gemm(e, dact, Wd, c2, M, 0);
+      double e3 = bf16_err(download<uint16_t>(c1, (size_t)M * N),
+                           ref_wxa8(xr, M, K, h.wq.data(), h.s.data(), h.b.data(), N, 4), false);
+      report(e3 <= 1e-2, "rmsnorm_for -> gemm (W4A8 on T64) vs the oracle", e3);
+      e3 = bf16_err(download<uint16_t>(c2, (size_t)M * N),
+                    ref_wxa8(hr, M, I, hd.wq.data(), hd.s.data(), hd.b.data(), N, 4), false);
+      report(e3 <= 1e-2, "silu_mul_for -> gemm (W4A8 on T64) vs the oracle", e3);
+      (void)hipFree(c1.buf), (void)hipFree(c2.buf);
+    }
     for (void* p : {dx.buf, dw.buf, dxn.buf, dgu.buf, dact.buf, Wd.wq.buf, Wd.s.buf, Wd.b.buf, Wf.wq.buf, Wf.s.buf,
-                    Wf.b.buf})
+                    Wf.b.buf, tf, td})
       (void)hipFree(p);
   }
   // T64 copy: decode GEMV semantics up to 64 rows, prefill semantics above

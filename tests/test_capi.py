@@ -95,10 +95,15 @@ def test_workspace_queries():
     assert rc == _lib.IFD_ERR_WORKSPACE
 
 
-def test_t64_w4a8_refuses_per_group_activations():
+def test_t64_w4a8_argument_checks():
+    """Per-group activations (per_token = 0) need the workspace the size query reports (its int8-to-bf16 staging and
+    transposed scales); any per_token other than 0 or 1 is refused. Both before any GPU work."""
     L = _lib.lib()
     rc = L.ifd_gemm_t64_w4a8(4096, 4096, 0, 4096, 256, 256, 4096, 256, 4, 0, None, 0, None)
-    assert rc == _lib.IFD_ERR_UNSUPPORTED and b"per-token" in L.ifd_last_error()
+    assert rc == _lib.IFD_ERR_WORKSPACE and b"workspace" in L.ifd_last_error()
+    assert L.ifd_gemm_t64_w4a8_workspace(4, 256, 256) > 4096 + 4 * 256 * 2
+    rc = L.ifd_gemm_t64_w4a8(4096, 4096, 3, 4096, 256, 256, 4096, 256, 4, 0, None, 0, None)
+    assert rc == _lib.IFD_ERR_ARG and b"per_token=3" in L.ifd_last_error()
 
 
 def test_moe_decode_ex_refuses_other_shared_widths():

@@ -344,6 +344,44 @@ def test_gemm_t64_w4a8(M, N, K):
         gen.check_out(out, Y + gen.bf16_to_f32(C0) if mode == 1 else Y, 2e-2, (M, N, K, mode), fp32=mode == 2)
 
 
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 32, 33, 64, 65, 128, 255])
+@pytest.mark.parametrize("N,K", [(384, 1024), (320, 17408)])
+def test_gemm_t64_w4a8_per_group(M, N, K):
+    """The reference's default W4A8 route (per-(row, 64-group) int8 activations, w4a8.metal:24-98) on T64 weights:
+    the decode GEMV up to 16 rows, the affine K-split kernel above (xq as bf16 integers, every group scaled by its
+    row's sx), against the oracle's w4a8 on the same int8 inputs in all store modes. Both sides compute the same
+    exact integer products, so the bars are the output rounding's: 1e-2 net for bf16, 1e-4 for fp32."""
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear(N, K, seed=M + 17, bias="free")
+    A = gen.activations(M, K, seed=M + 18)
+    U, XS = orc.a8_quant(A, False)
+    T = ops.pack_t64(g.qlinear(wq, s, b))
+    Y = orc.w4a8(U, XS, wq, s, b)
+    C0 = gen.activations(M, N, seed=M + 19)
+    for mode in (0, 1, 2):
+        C = g.dev(C0) if mode == 1 else None
+        out = g.host(ops.gemm_t64_w4a8(g.dev(U), g.dev(XS), T, C, mode=mode, per_token=False))
+        ref = Y + gen.bf16_to_f32(C0) if mode == 1 else Y
+        gen.check_out(out, ref, 1e-4 if mode == 2 else 1e-2, (M, N, K, mode, "per group"), fp32=mode == 2)
+
+
+@pytest.mark.parametrize("M", [8, 32, 128])
+@pytest.mark.parametrize("N,K", [(34816, 5120), (5120, 17408)])
+def test_gemm_t64_w4a8_per_group_config1(M, N, K):
+    """Per-group W4A8 on T64 at config 1's shapes (gate_up, down), the GPU's own quantization bit-exact against the
+    oracle's; 768 sampled columns against the oracle's w4a8."""
+    g, ops = _gu(), _ops()
+    codes, wq, s, b = gen.qlinear(N, K, seed=M + N)
+    A = gen.activations(M, K, seed=M + 3)
+    U, XS = ops.a8_quant(g.dev(A), False)
+    Uh, XSh = orc.a8_quant(A, False)
+    assert np.array_equal(g.host(U), Uh) and np.array_equal(g.host(XS), XSh)
+    out = g.host(ops.gemm_t64_w4a8(U, XS, ops.pack_t64(g.qlinear(wq, s, b)), per_token=False))
+    cols = np.linspace(0, N - 1, 768).astype(int)
+    Y = orc.w4a8(Uh, XSh, wq[cols], s[cols], b[cols])
+    gen.check_bf16(out[:, cols], Y, 1e-2, (M, N, K, "per group, sampled columns"))
+
+
 def test_gemm_t64_w4a8_config3_sampled():
     """BASELINE config 3 (M=2048, K=N=5120, per-token int8) on T64 weights; oracle on 16 sampled rows."""
     g, ops = _gu(), _ops()
