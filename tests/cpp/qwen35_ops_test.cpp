@@ -484,6 +484,37 @@ void test_gemm(Qwen35& m, Enc& e, std::mt19937& rng) {
       report(err <= 1e-2 && (bool)Ws.t64, "gemm 8-bit kslice_of (T64x8)", err);
       (void)hipFree(dA.buf), (void)hipFree(dC.buf);
     }
+    // the same 8-bit layer with and without its T64x8 copy: both routes keep the qmv8 arithmetic up to 16 rows (the
+    // MLX layout up to 32), so at M = 3 and 16 they differ by fp32 summation order at most; at M = 24 the T64x8 route
+    // has the qmm rounding (every weight rounded to bf16(s q + b)) and the MLX route still the qmv8 arithmetic.
+    // Differences in bf16 steps of the larger of the two values. Budget: M <= 16, no element more than one step
+    // apart; M = 24, RMS(difference) <= 5e-3 RMS and max |difference| <= 2e-2 RMS (two roundings of the same sum,
+    // each within BASELINE's 1e-2 of it).
+    {
+      QLinear Wm = W8;
+      Wm.t64 = BufRef();
+      for (int M : {3, 16, 24}) {
+        const auto A = activations(M, K, rng);
+        BufRef dA = upload(A), c1 = upload(std::vector<uint16_t>((size_t)M * N)),
+               c2 = upload(std::vector<uint16_t>((size_t)M * N));
+        m.gemm(e, dA, W8, c1, M, 0);
+        m.gemm(e, dA, Wm, c2, M, 0);
+        const auto o1 = download<uint16_t>(c1, (size_t)M * N), o2 = download<uint16_t>(c2, (size_t)M * N);
+        double ss = 0, sd = 0, worst = 0, maxst = 0;
+        for (size_t i = 0; i < o1.size(); i++) {
+          const double a = bf2f(o1[i]), bb = bf2f(o2[i]), d = std::fabs(a - bb), big = std::max(std::fabs(a), std::fabs(bb));
+          ss += bb * bb, sd += d * d;
+          worst = std::max(worst, d);
+          if (d > 0) maxst = std::max(maxst, d / std::ldexp(1.0, std::ilogb(big) - 7));
+        }
+        const double rms = std::sqrt(ss / o1.size()), rd = std::sqrt(sd / o1.size()) / rms;
+        const bool pass = M <= 16 ? maxst <= 1.0 : rd <= 5e-3 && worst <= 2e-2 * rms;
+        printf("     8-bit T64x8 vs MLX layout M=%d: max steps %.1f, RMS(diff)/RMS %.2e, max|diff|/RMS %.2e\n", M,
+               maxst, rd, worst / rms);
+        report(pass, "gemm 8-bit, T64x8 copy vs MLX layout M=" + std::to_string(M), worst / rms);
+        (void)hipFree(dA.buf), (void)hipFree(c1.buf), (void)hipFree(c2.buf);
+      }
+    }
     (void)hipFree(t), (void)hipFree(W8.wq.buf), (void)hipFree(W8.s.buf), (void)hipFree(W8.b.buf);
   }
 }

@@ -143,7 +143,7 @@ def test_w4a8(M, N, K, per_token):
         W = g.qlinear(wq ^ np.uint32(0x88888888) if flipped else wq, s, b, flipped)
         out = g.host(ops.qmm_w4a8(g.dev(U), g.dev(XS), per_token, W, mode=mode))
         Y = orc.w4a8(U, XS, wq, s, b)
-        gen.check_out(out, Y, 2e-2, (M, N, K, per_token, flipped), fp32=mode == 2)
+        gen.check_out(out, Y, 1e-4 if mode == 2 else 1e-2, (M, N, K, per_token, flipped), fp32=mode == 2)
 
 
 def test_w4a8_config3_sampled():

@@ -341,7 +341,9 @@ def test_gemm_t64_w4a8(M, N, K):
     for mode in (0, 1, 2):
         C = g.dev(C0) if mode == 1 else None
         out = g.host(ops.gemm_t64_w4a8(g.dev(U), g.dev(XS), T, C, mode=mode))
-        gen.check_out(out, Y + gen.bf16_to_f32(C0) if mode == 1 else Y, 2e-2, (M, N, K, mode), fp32=mode == 2)
+        # the same int8 inputs on both sides: the bars are the output rounding's (bf16 1e-2 net, fp32 1e-4)
+        gen.check_out(out, Y + gen.bf16_to_f32(C0) if mode == 1 else Y, 1e-4 if mode == 2 else 1e-2,
+                      (M, N, K, mode), fp32=mode == 2)
 
 
 @pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 32, 33, 64, 65, 128, 255])
@@ -415,7 +417,7 @@ def test_gemm_t64_w4a8_tail_split():
     for mode in (0, 1, 2):
         out = g.host(ops.gemm_t64_w4a8(U, XS, T, g.dev(C0) if mode == 1 else None, mode=mode))[rows]
         ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
-        gen.check_out(out, ref, 2e-2, mode, fp32=mode == 2)
+        gen.check_out(out, ref, 1e-4 if mode == 2 else 1e-2, mode, fp32=mode == 2)
 
 
 @pytest.mark.parametrize("M,N,K", [(2560, 6656, 512), (2048, 4096, 256), (1280, 5120, 256)])
@@ -436,7 +438,7 @@ def test_gemm_t64_w4a8_stream_k_plans(M, N, K):
     for mode in (0, 1, 2):
         out = g.host(ops.gemm_t64_w4a8(U, XS, T, g.dev(C0) if mode == 1 else None, mode=mode))[rows]
         ref = Y + gen.bf16_to_f32(C0[rows]) if mode == 1 else Y
-        gen.check_out(out, ref, 2e-2, (M, N, K, mode), fp32=mode == 2)
+        gen.check_out(out, ref, 1e-4 if mode == 2 else 1e-2, (M, N, K, mode), fp32=mode == 2)
 
 
 def test_gemm_t64_prefill_tiles_with_tail():

@@ -88,7 +88,7 @@ def test_w8a8(M, N, K, per_token):
     for flipped, mode in ((False, 0), (True, 2), (True, 0)):
         W = g.qlinear(wq ^ np.uint32(FLIP8) if flipped else wq, s, b, flipped, bits=8)
         out = g.host(ops.qmm_w4a8(g.dev(U), g.dev(XS), per_token, W, mode=mode))
-        gen.check_out(out, Y, 2e-2, (M, N, K, per_token, flipped, mode), fp32=mode == 2)
+        gen.check_out(out, Y, 1e-4 if mode == 2 else 1e-2, (M, N, K, per_token, flipped, mode), fp32=mode == 2)
 
 
 def test_flip_8bit_in_place():
