@@ -8,8 +8,10 @@
 //
 //   encode_moe_bench [--mlx] T...    one JSON line: {"T16": {"us": ..., "tok_s": ...}, ...}
 //
-// Timing: HIP events on the operator's stream around `iters` calls after warm calls that keep the GPU loaded for
-// 30 ms (its clock settles in that time). The hidden state x is updated in place by each call, as in a model.
+// Timing: HIP events on the operator's stream around each of `iters` calls, after warm calls that keep the GPU loaded
+// for 30 ms (its clock settles in that time). Every call starts from the same hidden state: encode_moe adds its
+// output into x, and a drifting x would concentrate the routing on a few experts; the device-to-device copy that
+// restores x sits between the event pairs, outside the timed intervals.
 #include <chrono>
 #include <cstdio>
 #include <cstring>
@@ -123,28 +125,40 @@ int main(int argc, char** argv) {
   Enc e{st};
   std::vector<uint16_t> x0((size_t)Tmax * H);
   for (auto& v : x0) v = f2bf(gauss());
-  hipEvent_t e0, e1;
-  hip_ok(hipEventCreate(&e0), "event");
-  hip_ok(hipEventCreate(&e1), "event");
+  constexpr int iters = 20;
+  std::vector<hipEvent_t> ev(2 * iters);
+  for (auto& v : ev) hip_ok(hipEventCreate(&v), "event");
+  void* xsave = dalloc((size_t)Tmax * H * 2);
+  hip_ok(hipMemcpy(xsave, x0.data(), x0.size() * 2, hipMemcpyHostToDevice), "bench x");
   std::string out = "{";
   for (size_t ti = 0; ti < Ts.size(); ti++) {
     const int T = Ts[ti];
-    hip_ok(hipMemcpy(m.x.ptr<void>(), x0.data(), (size_t)T * H * 2, hipMemcpyHostToDevice), "bench x");
+    const size_t xb = (size_t)T * H * 2;
+    auto call = [&](int i) {
+      hip_ok(hipMemcpyAsync(m.x.ptr<void>(), xsave, xb, hipMemcpyDeviceToDevice, st), "bench x");
+      m.encode_moe(e, layers[i % ncp], T);
+    };
     int i = 0;
-    for (; i < 3; i++) m.encode_moe(e, layers[i % ncp], T);
+    for (; i < 3; i++) call(i);
     hip_ok(hipStreamSynchronize(st), "bench warm");
     const auto t0 = std::chrono::steady_clock::now();
     while (std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() < 30.0) {
-      for (int r = 0; r < 4; r++, i++) m.encode_moe(e, layers[i % ncp], T);
+      for (int r = 0; r < 4; r++, i++) call(i);
       hip_ok(hipStreamSynchronize(st), "bench warm");
     }
-    const int iters = 20;
-    hip_ok(hipEventRecord(e0, st), "event");
-    for (int r = 0; r < iters; r++, i++) m.encode_moe(e, layers[i % ncp], T);
-    hip_ok(hipEventRecord(e1, st), "event");
-    hip_ok(hipEventSynchronize(e1), "event");
-    float ms = 0;
-    hip_ok(hipEventElapsedTime(&ms, e0, e1), "event");
+    for (int r = 0; r < iters; r++, i++) {
+      hip_ok(hipMemcpyAsync(m.x.ptr<void>(), xsave, xb, hipMemcpyDeviceToDevice, st), "bench x");
+      hip_ok(hipEventRecord(ev[2 * r], st), "event");
+      m.encode_moe(e, layers[i % ncp], T);
+      hip_ok(hipEventRecord(ev[2 * r + 1], st), "event");
+    }
+    hip_ok(hipStreamSynchronize(st), "event");
+    double ms = 0;
+    for (int r = 0; r < iters; r++) {
+      float t = 0;
+      hip_ok(hipEventElapsedTime(&t, ev[2 * r], ev[2 * r + 1]), "event");
+      ms += t;
+    }
     const double us = ms * 1e3 / iters;
     char buf[160];
     snprintf(buf, sizeof buf, "%s\"T%d\": {\"us\": %.2f, \"tok_s\": %.1f, \"decode_route\": %s, \"t64_route\": %s}",

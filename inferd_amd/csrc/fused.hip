@@ -2,9 +2,10 @@
 // int8 activations, and a deferred split-K residual reduce runs inside the next norm. Each is bit-identical to its
 // unfused sequence of this library's kernels (k_splitk_reduce, k_rmsnorm, k_silu_mul, k_a8_quant).
 //
-// One block of 256 threads per row. Thread t takes elements t + 256 k (as k_rmsnorm), so wave w of pass k covers the
-// 64 consecutive elements of group 4 k + w: the per-group amax and code sums of the W4A8 quantization stay inside one
-// wave, and no thread reads an element another thread wrote.
+// One block of 256 threads per row (per 2048-column chunk of a row for the per-group silu_mul_a8). Thread t takes
+// elements t + 256 k (as k_rmsnorm), so wave w of pass k covers the 64 consecutive elements of group 4 k + w: the
+// per-group amax and code sums of the W4A8 quantization stay inside one wave, and no thread reads an element another
+// thread wrote.
 #include "common.h"
 #include "host.h"
 #include "kernels.h"
@@ -94,15 +95,19 @@ __global__ __launch_bounds__(256) void k_rmsnorm_a8(const uint16_t* __restrict__
 }
 
 // silu_mul (k_silu_mul; reference core.metal:777-787) quantized without writing h (reference silu_mul_a8,
-// core.metal:789-814, per group there). gu rows [gate (I) | up (I)], ldgu apart.
+// core.metal:789-814, per group there). gu rows [gate (I) | up (I)], ldgu apart. Per group, block (row, c) takes
+// columns [c kSmChunk, (c + 1) kSmChunk): the groups are independent, so a row spreads over blocks; per token the
+// row's amax needs the whole row in one block (gridDim.y = 1).
+constexpr int kSmChunk = 256 * 8;
 template <bool PT>
 __global__ __launch_bounds__(256) void k_silu_mul_a8(const uint16_t* __restrict__ gu, int ldgu, int I,
                                                      int8_t* __restrict__ U, float* __restrict__ XS) {
   __shared__ float red[4];
   const size_t row = blockIdx.x;
-  const uint16_t* g = gu + row * ldgu;
+  const int c0 = PT ? 0 : (int)blockIdx.y * kSmChunk, n = PT ? I : min(kSmChunk, I - c0);
+  const uint16_t* g = gu + row * ldgu + c0;
   auto value = [&](int i) { return bf2f(f2bf(swiglu_f(bf2f(g[i]), bf2f(g[I + i])))); };
-  quant_row<PT>(value, I, red, U + row * I, XS + row * (I / kGroup) * 2);
+  quant_row<PT>(value, n, red, U + row * I + c0, XS + (row * (I / kGroup) + c0 / kGroup) * 2);
 }
 
 // A deferred split-K residual reduce inside the next rmsnorm (reference splitk_res_norm, core.metal:539-595):
@@ -171,7 +176,9 @@ int launch_silu_mul_a8(const uint16_t* gu, int ldgu, int I, int rows, int per_to
                        hipStream_t st) {
   if (rows == 0) return IFD_OK;
   if (per_token) hipLaunchKernelGGL(k_silu_mul_a8<true>, dim3(rows), dim3(256), 0, st, gu, ldgu, I, U, XS);
-  else hipLaunchKernelGGL(k_silu_mul_a8<false>, dim3(rows), dim3(256), 0, st, gu, ldgu, I, U, XS);
+  else
+    hipLaunchKernelGGL(k_silu_mul_a8<false>, dim3(rows, (I + kSmChunk - 1) / kSmChunk), dim3(256), 0, st, gu, ldgu, I,
+                       U, XS);
   return check_launch("silu_mul_a8");
 }
 

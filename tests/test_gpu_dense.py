@@ -196,13 +196,15 @@ def test_rmsnorm_a8(R, D, per_token):
     assert np.all(gen.bf16_steps(y, orc.rmsnorm(x, w, 1e-6)) <= 1)
 
 
+@pytest.mark.parametrize("I", [17408, 1088])
 @pytest.mark.parametrize("per_token", [False, True])
-def test_silu_mul_a8(per_token):
-    """silu_mul_a8 gives the bits of ifd_silu_mul then ifd_a8_quant, and the oracle's a8_quant of that product."""
+def test_silu_mul_a8(per_token, I):
+    """silu_mul_a8 gives the bits of ifd_silu_mul then ifd_a8_quant, and the oracle's a8_quant of that product. Per
+    group a row spreads over 2048-column blocks: I = 17408 ends in a half block, I = 1088 is less than one."""
     g, ops = _gu(), _ops()
     rng = np.random.default_rng(95)
-    gu = gen.f32_to_bf16((rng.standard_normal((9, 2 * 17408)) * 3).astype(np.float32))
-    gu[2, 17408:] = 0  # up = 0: a zero row
+    gu = gen.f32_to_bf16((rng.standard_normal((9, 2 * I)) * 3).astype(np.float32))
+    gu[2, I:] = 0  # up = 0: a zero row
     gd = g.dev(gu)
     U, XS = ops.silu_mul_a8(gd, per_token)
     h = ops.silu_mul(gd)
