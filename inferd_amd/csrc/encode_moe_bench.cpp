@@ -6,7 +6,11 @@
 // so the sorted route runs the T64 gathered GEMMs with the shared expert as expert E; `--mlx` drops the copies and
 // times the MLX-layout route instead. Two weight copies alternate (1.85 GB, over 3x the 256 MB Infinity Cache).
 //
-//   encode_moe_bench [--mlx] T...    one JSON line: {"T16": {"us": ..., "tok_s": ...}, ...}
+//   encode_moe_bench [--mlx] [--graph] T...    one JSON line: {"T16": {"us": ..., "tok_s": ...}, ...}
+//
+// --graph: each weight copy's encode_moe call is captured once in a HIP graph and the timed calls replay it (the
+// operator issues no allocation, memset or synchronisation, so the call is capturable): the GPU time of the
+// operator without the host's per-launch cost.
 //
 // Timing: HIP events on the operator's stream around each of `iters` calls, after warm calls that keep the GPU loaded
 // for 30 ms (its clock settles in that time). Every call starts from the same hidden state: encode_moe adds its
@@ -15,6 +19,7 @@
 #include <chrono>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -80,10 +85,11 @@ BufRef pack(const Affine& a, int N, int K, int E) {
 }  // namespace
 
 int main(int argc, char** argv) {
-  bool mlx = false;
+  bool mlx = false, graph = false;
   std::vector<int> Ts;
   for (int i = 1; i < argc; i++) {
     if (std::string(argv[i]) == "--mlx") mlx = true;
+    else if (std::string(argv[i]) == "--graph") graph = true;
     else Ts.push_back(atoi(argv[i]));
   }
   if (Ts.empty()) Ts = {16, 128, 2048};
@@ -134,9 +140,29 @@ int main(int argc, char** argv) {
   for (size_t ti = 0; ti < Ts.size(); ti++) {
     const int T = Ts[ti];
     const size_t xb = (size_t)T * H * 2;
+    std::function<void(int)> moe_fn;
     auto call = [&](int i) {
       hip_ok(hipMemcpyAsync(m.x.ptr<void>(), xsave, xb, hipMemcpyDeviceToDevice, st), "bench x");
-      m.encode_moe(e, layers[i % ncp], T);
+      moe_fn(i);
+    };
+    // with --graph: one captured encode_moe per weight copy, replayed by moe_fn
+    std::vector<hipGraphExec_t> gx;
+    if (graph) {
+      for (int c = 0; c < ncp; c++) {
+        m.encode_moe(e, layers[c], T);  // first calls outside capture (one-time kernel attributes)
+        hip_ok(hipStreamSynchronize(st), "bench warm");
+        hipGraph_t g;
+        hip_ok(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal), "capture");
+        m.encode_moe(e, layers[c], T);
+        hip_ok(hipStreamEndCapture(st, &g), "capture");
+        hipGraphExec_t x;
+        hip_ok(hipGraphInstantiate(&x, g, nullptr, nullptr, 0), "instantiate");
+        gx.push_back(x);
+      }
+    }
+    moe_fn = [&](int i) {
+      if (graph) hip_ok(hipGraphLaunch(gx[i % ncp], st), "replay");
+      else m.encode_moe(e, layers[i % ncp], T);
     };
     int i = 0;
     for (; i < 3; i++) call(i);
@@ -149,7 +175,7 @@ int main(int argc, char** argv) {
     for (int r = 0; r < iters; r++, i++) {
       hip_ok(hipMemcpyAsync(m.x.ptr<void>(), xsave, xb, hipMemcpyDeviceToDevice, st), "bench x");
       hip_ok(hipEventRecord(ev[2 * r], st), "event");
-      m.encode_moe(e, layers[i % ncp], T);
+      moe_fn(i);
       hip_ok(hipEventRecord(ev[2 * r + 1], st), "event");
     }
     hip_ok(hipStreamSynchronize(st), "event");
@@ -160,6 +186,7 @@ int main(int argc, char** argv) {
       ms += t;
     }
     const double us = ms * 1e3 / iters;
+    for (auto x : gx) hip_ok(hipGraphExecDestroy(x), "graph");
     char buf[160];
     snprintf(buf, sizeof buf, "%s\"T%d\": {\"us\": %.2f, \"tok_s\": %.1f, \"decode_route\": %s, \"t64_route\": %s}",
              ti ? ", " : "", T, us, T / (us * 1e-6), m.moe_decode_route(layers[0], T) ? "true" : "false",

@@ -146,7 +146,8 @@ struct Qwen35 {
   BufRef rlog;                // router logits fp32 [max_rows][E + 1] (bf16 when rounded)
   BufRef ridx, rw, rsg;       // int [T][k], float [T][k], float [T]
   BufRef proj, act, sh_out;   // shared expert: bf16 [T][2 Is], [T][Is], [T][H]
-  BufRef moffs, mperm, minv, mtiles, mntiles;  // dispatch (room for the shared expert as expert E: E + 2 offsets, R + T rows)
+  BufRef moffs, mperm, minv, mtiles, mntiles;  // dispatch (room for the shared expert as expert E: E + 2 offsets,
+                                               // R + T rows)
   BufRef eact, edown_out;     // routed experts (and the shared expert's rows after them): bf16 [R + T][I], [R + T][H]
   BufRef splitk;              // gemm()'s split-K partials and the dispatch workspace
   size_t splitk_bytes = 0;
