@@ -16,12 +16,13 @@
 // activation fragment read from LDS feeds two MFMAs and one dequantized weight fragment feeds MT. One LDS ring
 // filled by direct global -> LDS DMA; a stage holds a step's activation slab [BM][64 bf16] (16-byte columns
 // XOR-swizzled by row pair) and its weights (8 code halves + 8 (s, b) rows). Each wave issues its own share of both
-// (the activation rows 8 (MT w + q) .. + 7 and its two bands' codes; wave 0 also the (s, b) rows) as one in-order
-// vmcnt stream, the activations R - 1 steps ahead and the weights R; the stream positions advance incrementally (no
-// per-step division). Within a step the wave reads its activation fragments and the next step's codes from LDS
-// first, then runs its MFMAs with the next step's dequant scheduled between them. Every DMA is issued by a whole
-// wave under wave-uniform control flow (the LDS base goes to M0). Finished tiles are staged through LDS and leave as
-// whole rows.
+// (the activation rows 8 (MT w + q) .. + 7, its two bands' codes and their two (s, b) rows) as one in-order vmcnt
+// stream, R units ahead; the stream positions advance by scalar adds, with a branch only at a tile boundary or the
+// run's end. All waves run the same code. The step loop is unrolled over the ring, so stages, LDS addresses and
+// fragment registers are compile-time constants and a step issues little beyond its MFMAs, dequant, LDS reads and
+// DMAs (one wave per SIMD issues about one instruction every 4 cycles, so the count sets the step time). Every DMA
+// is issued by a whole wave under wave-uniform control flow (the LDS base goes to M0). Finished tiles are staged
+// through LDS and leave as whole rows.
 //
 // SwiGLU mode: tile t holds gate bands 4t..4t+3 (waves 0, 1) and the matching up bands (waves 2, 3); the staged tile
 // (or the fixup) gives h = silu(bf16(gate)) * bf16(up) (reference silu_mul, core.metal:777-787).
@@ -29,6 +30,7 @@
 // The same kernel serves T64x8 (8-bit) weights with BITS = 8: a band's codes are two 1 KB halves per group (two DMAs
 // instead of one), dequantized from the stored q - 128 bytes to bf16(s q + b), MLX's 8-bit qmm rounding.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "dma.h"
@@ -91,27 +93,46 @@ struct GemmSkArgs {
 // the block whose run holds unit u
 __host__ __device__ inline int sk_block_of(long u, int nblk, long U) { return (int)((u * nblk + nblk - 1) / U); }
 
-// One wave-wide 16-byte-per-lane DMA through a buffer resource: lane l's 16 bytes at voff(l) + soff land at
-// lds + 16 l (LDS base in M0, wave-uniform control flow only).
+// Wave-wide DMAs through a buffer resource: lane l's 16 (4) bytes at voff(l) + soff land at lds + 16 l (4 l) (LDS
+// base in M0, wave-uniform control flow only).
 __device__ __forceinline__ void sk_dma(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, (int)voff, (int)soff, 0, 0);
 }
+__device__ __forceinline__ void sk_dma4(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 4, (int)voff, (int)soff, 0, 0);
+}
 
-// The pipeline of one wave; W0: wave 0, which also issues the (s, b) rows. Its DMA stream is a sequence of pairs
-// (A(s), W(s + 1)), s = 0, 1, ...: the prologue issues W(0) and pairs 0 .. R - 2, step i pair R - 1 + i, past the
-// run's end too (re-reading its last unit), so the waits are constants: at step i the wave reads A(i + 1)'s
-// fragments and W(i + 2)'s codes, the second of pair i + 1, which R - 3 younger pairs follow. Stage j % R holds A(j)
-// and W(j); step i overwrites A(i - 1) and W(i), both read two steps earlier.
-template <int MT, int BITS, bool W0>
+template <int K>
+using sk_ic = std::integral_constant<int, K>;
+// f(sk_ic<K>{}) for K = 0 .. N - 1, unrolled at compile time
+template <int K, int N, class F>
+__device__ __forceinline__ void sk_static_for(F&& f) {
+  if constexpr (K < N) {
+    f(sk_ic<K>{});
+    sk_static_for<K + 1, N>(f);
+  }
+}
+
+// The pipeline of one wave. A wave issues a step's data as one pair of DMAs per unit: A(j), its 8 MT activation rows
+// (8 (MT w + q) .. + 7, q < MT), and W(j), the codes of its two bands and their two (s, b) rows (one 4-byte-per-lane
+// DMA). Pair j lands in stage j % R. The prologue issues pairs 0 .. R - 1 and step i pair i + R, past the run's end
+// too (re-reading its last unit, L2 hits), so the waits are constants: at step i the wave reads A(i + 1)'s fragments
+// and W(i + 2)'s codes, so it waits for pair i + 2, behind which R - 3 younger pairs are in flight. Step i refills
+// stage i % R, whose A(i) was last read at step i - 1 and W(i) at step i - 2, both before the barrier that opens step
+// i. The loop is unrolled over the ring (twice for an odd depth), so that every stage, LDS address and fragment
+// register set is a compile-time constant; a run enters it at its phase (Duff's device). A step issues about 220
+// instructions for its 8 MT MFMAs, which a single wave per SIMD issues one every ~4 cycles: the stream's bookkeeping
+// is a few scalar adds and one countdown per step.
+template <int MT, int BITS>
 __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const int wave, const int b) {
   constexpr int BM = 32 * MT, R = sk_ring(MT, BITS), A_BYTES = sk_abytes(MT), STAGE = sk_stage(MT, BITS);
   constexpr int CODES = sk_codes(BITS), TILEB = sk_tileb(BITS);
-  constexpr int NE = MT * 16;              // accumulators per lane and band
-  constexpr int NH = BITS / 4;             // 1 KB code DMAs per band
-  constexpr int NWC = 2 * NH;              // code DMAs per pair (two bands)
-  constexpr int NW = NWC + (W0 ? 1 : 0);   // weight DMAs per pair
-  constexpr int PAIR = MT + NW;
-  static_assert(R >= 4 && (R - 2) * PAIR <= 63, "ring depth, vmcnt range");
+  constexpr int NE = MT * 16;             // accumulators per lane and band
+  constexpr int NH = BITS / 4;            // 1 KB code DMAs per band
+  constexpr int NWC = 2 * NH;             // code DMAs per pair (two bands)
+  constexpr int PAIR = MT + NWC + 1;      // DMAs per pair: activation rows, codes, the (s, b) rows
+  constexpr int UNR = R % 2 ? 2 * R : R;  // steps per unrolled body
+  static_assert(R >= 4 && (R - 2) * PAIR <= 63 && UNR <= 16, "ring depth, vmcnt range, unroll");
   float* const stg = (float*)lds;  // staged tile [BM][kSkRow], after the K loop
   const int tid = threadIdx.x, lane = tid & 63;
   const int j = lane & 31, h = lane >> 5;
@@ -131,66 +152,52 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
       __builtin_amdgcn_make_buffer_rsrc((void*)p.A, 0, (int)((uint32_t)p.M * p.lda * 2u), 0x00020000);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.wt, 0, (int)p.w_bytes, 0x00020000);
 
-  // ---- the DMA streams: per-lane offsets of the current tile, group offsets in scalar registers
-  uint32_t va[MT], vw[NW];
-  auto a_tile = [&](int tile) __attribute__((always_inline)) {
-    const int tm = tile % p.tiles_m;
+  // ---- the DMA stream: per-lane offsets of the current tile, the unit's group offsets in scalar registers
+  uint32_t va[MT], vw[NWC], vs;
+  auto set_tile = [&](int tile) __attribute__((always_inline)) {
+    const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
 #pragma unroll
     for (int q = 0; q < MT; q++) {
       const int r = 8 * (MT * wave + q) + lane / 8;
       const int c = (lane & 7) ^ ((r >> 1) & 7);
       va[q] = (uint32_t)min(tm * BM + r, p.M - 1) * (uint32_t)p.lda * 2u + 16u * c;
     }
-  };
-  // weight DMA k < NWC: half k % NH of band 2 wave + k / NH; k = NWC (wave 0): the 8 (s, b) rows
-  auto w_tile = [&](int tile) __attribute__((always_inline)) {
-    const int tn = tile / p.tiles_m;
 #pragma unroll
     for (int k = 0; k < NWC; k++)
       vw[k] = (uint32_t)phys_band(tn, 2 * wave + k / NH) * TILEB + 1024u * (k % NH) + 16u * lane;
-    if constexpr (W0) vw[NWC] = (uint32_t)phys_band(tn, lane / 8) * TILEB + CODES + 16u * (lane & 7);
+    vs = (uint32_t)phys_band(tn, 2 * wave + h) * TILEB + CODES + 4u * j;  // lane l: band 2 w + l / 32, column l % 32
   };
-  // LDS offset of code DMA k from the wave's first band
-  auto w_dst = [](int k) { return (k / NH) * CODES + (k % NH) * 1024; };
-  int a_t = tile_first, a_g = u0 % G, w_t = tile_first, w_g = a_g;
-  uint32_t a_so = (uint32_t)a_g * 2u * kGroup, w_so = (uint32_t)w_g * gstride;
-  a_tile(a_t);
-  w_tile(w_t);
-  // the DMAs of one pair (no branch, so that they schedule among the MFMAs), then the streams' advance
-  auto issue_a = [&](int stage) __attribute__((always_inline)) {
-    uint8_t* st = lds + stage * STAGE;
-#pragma unroll
-    for (int q = 0; q < MT; q++) sk_dma(ra, st + (MT * wave + q) * 1024, va[q], a_so);
-  };
-  auto issue_w = [&](int stage) __attribute__((always_inline)) {
-    uint8_t* st = lds + stage * STAGE + A_BYTES + (2 * wave) * CODES;
-#pragma unroll
-    for (int k = 0; k < NWC; k++) sk_dma(rw, st + w_dst(k), vw[k], w_so);
-    if constexpr (W0) sk_dma(rw, lds + stage * STAGE + A_BYTES + 8 * CODES, vw[NWC], w_so);
-  };
-  // Past the run's last unit a stream stays on it: the extra DMAs re-read that unit (L2 hits), never new bytes.
-  int a_left = n - 1, w_left = n - 1;  // advances left before a stream reaches the run's last unit
-  auto advance_a = [&]() __attribute__((always_inline)) {
-    if (a_left <= 0) return;
-    a_left--;
-    a_so += 2u * kGroup;
-    if (++a_g == G) {  // next tile
-      a_g = 0, a_so = 0;
-      a_tile(++a_t);
-    }
-  };
-  auto advance_w = [&]() __attribute__((always_inline)) {
-    if (w_left <= 0) return;
-    w_left--;
-    w_so += gstride;
-    if (++w_g == G) {
-      w_g = 0, w_so = 0;
-      w_tile(++w_t);
-    }
-  };
+  // The stream walks units u0 .. u1 - 1 and then stays on u1 - 1. `left` counts the advances to its next event (a
+  // tile boundary or the run's last unit); only then does it branch.
+  int s_tile = tile_first, to_switch = G - u0 % G, to_end = n - 1;
+  uint32_t a_so = (uint32_t)(u0 % G) * 2u * kGroup, w_so = (uint32_t)(u0 % G) * gstride;
+  uint32_t a_inc = 2u * kGroup, w_inc = gstride;
+  int seg = min(to_switch, to_end), left;
+  if (to_end == 0) a_inc = 0, w_inc = 0, seg = 1 << 30;
+  left = seg;
+  set_tile(s_tile);
   auto advance = [&]() __attribute__((always_inline)) {
-    advance_a();
-    advance_w();
+    a_so += a_inc;
+    w_so += w_inc;
+    if (--left == 0) {
+      to_switch -= seg;
+      to_end -= seg;
+      if (to_switch == 0) {  // the next unit opens the next tile
+        set_tile(++s_tile);
+        a_so = 0, w_so = 0, to_switch = G;
+      }
+      if (to_end == 0) a_inc = 0, w_inc = 0, seg = 1 << 30;  // on the run's last unit: stay
+      else seg = min(to_switch, to_end);
+      left = seg;
+    }
+  };
+  // DMA d of the pair bound for stage s: activation rows (d < MT), code halves, then the (s, b) rows
+  auto issue_one = [&](int s, int d) __attribute__((always_inline)) {
+    uint8_t* st = lds + s * STAGE;
+    if (d < MT) sk_dma(ra, st + (MT * wave + d) * 1024, va[d], a_so);
+    else if (d - MT < NWC)
+      sk_dma(rw, st + A_BYTES + (2 * wave + (d - MT) / NH) * CODES + ((d - MT) % NH) * 1024, vw[d - MT], w_so);
+    else sk_dma4(rw, st + A_BYTES + 8 * CODES + 2 * wave * 128, vs, w_so);
   };
 
   // LDS reads one step ahead of their use
@@ -251,67 +258,57 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
 #pragma unroll
     for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
 
-  // prologue: W(0), then pairs 0 .. R - 2; A(0) and W(0), W(1) (pair 0) are awaited before step 0
-  issue_w(0);
-  advance_w();
-  for (int s = 0; s < R - 1; s++) {
-    issue_a(s);
-    issue_w(s + 1);
+  // Fragment sets by step parity: entering step i, set i % 2 holds A(i)'s fragments, W(i) dequantized and W(i + 1)'s
+  // codes; the step fills the other set with A(i + 1), W(i + 1) dequantized and W(i + 2)'s codes.
+  u32x4 af[2][MT][4], bf[2][2][4];
+  Codes cd[2];
+
+  // prologue: pairs 0 .. R - 1; A(0) and W(0), W(1) (pairs 0, 1) are awaited before step 0
+#pragma unroll
+  for (int s = 0; s < R; s++) {
+#pragma unroll
+    for (int d = 0; d < PAIR; d++) issue_one(s, d);
     advance();
   }
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 2) * PAIR) : "memory");
-  u32x4 bf0[2][4], bf1[2][4], af0[MT][4], af1[MT][4];
-  Codes cd0, cd1;
-  load_a(0, af0);
-  read_codes(0, cd0);
-  dequant(cd0, bf0);
-  read_codes(1, cd0);
-  int s0 = 0;  // step i % R
+  load_a(0, af[0]);
+  read_codes(0, cd[0]);
+  dequant(cd[0], bf[0]);
+  read_codes(1, cd[0]);
 
-  // Step i: bc / afc (B and A fragments of step i) and cc (codes of step i + 1) in registers; reads afn (step i + 1)
-  // and cn (step i + 2), dequantizes cc into bn, and issues pair R - 1 + i.
-  auto step = [&](u32x4 (&bc)[2][4], u32x4 (&bn)[2][4], u32x4 (&afc)[MT][4], u32x4 (&afn)[MT][4], Codes& cc,
-                  Codes& cn) __attribute__((always_inline)) {
+  // Step i = K (mod UNR): eight groups, each closed by a scheduling barrier: MT MFMAs of this step (consecutive ones
+  // on different accumulators), one 8-code dequant of the next, a share of the LDS reads for the next steps and of
+  // the pair's DMAs, so that the matrix core has work through the whole step and the wave's other instructions issue
+  // in its shadow.
+  auto step = [&](auto KC) __attribute__((always_inline)) {
+    constexpr int K = decltype(KC)::value, S = K % R, P = K % 2, S1 = (S + 1) % R, S2 = (S + 2) % R;
+    constexpr int NDS = 4 * MT + 2 * (NH + 1), DEQ = BITS == 4 ? 17 : 22;
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((R - 3) * PAIR) : "memory");
-    const int s1 = s0 + 1 == R ? 0 : s0 + 1, s2 = s1 + 1 == R ? 0 : s1 + 1, sm = s0 == 0 ? R - 1 : s0 - 1;
-    // Eight groups, each closed by a scheduling barrier: MT MFMAs of this step, one 8-code dequant of the next
-    // (17 VALU for 4 bits, 22 for 8), a share of the LDS reads for the next steps and of the pair's DMAs, so that the
-    // matrix core has work through the whole step and the wave's other instructions issue in its shadow.
-    constexpr int NDS = 4 * MT + 2 * (NH + 1), NDMA = MT + NW, DEQ = BITS == 4 ? 17 : 22;
-    const uint8_t* const ast = lds + s1 * STAGE;        // activation fragments of step i + 1
-    const uint8_t* const wst = lds + s2 * STAGE + A_BYTES;  // codes of step i + 2
+    const uint8_t* const ast = lds + S1 * STAGE;           // activation fragments of step i + 1
+    const uint8_t* const wst = lds + S2 * STAGE + A_BYTES;  // codes of step i + 2
     float sa[2], sbs[2], bi[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) scales(cc.sb[nb], sa[nb], sbs[nb], bi[nb]);
-    auto issue_one = [&](int d) __attribute__((always_inline)) {  // DMA d of the pair: A rows, then the weights
-      if (d < MT) sk_dma(ra, lds + sm * STAGE + (MT * wave + d) * 1024, va[d], a_so);
-      else if (d - MT < NWC) sk_dma(rw, lds + s0 * STAGE + A_BYTES + (2 * wave) * CODES + w_dst(d - MT), vw[d - MT], w_so);
-      else sk_dma(rw, lds + s0 * STAGE + A_BYTES + 8 * CODES, vw[NWC], w_so);
-    };
+    for (int nb = 0; nb < 2; nb++) scales(cd[P].sb[nb], sa[nb], sbs[nb], bi[nb]);
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-      if constexpr (NDMA <= 8) {
-        if (g < NDMA) issue_one(g);
-      } else {
 #pragma unroll
-        for (int d = g * NDMA / 8; d < (g + 1) * NDMA / 8; d++) issue_one(d);
-      }
+      for (int d = g * PAIR / 8; d < (g + 1) * PAIR / 8; d++) issue_one(S, d);
 #pragma unroll
       for (int d = g * NDS / 8; d < (g + 1) * NDS / 8; d++) {
         if (d < 4 * MT) {
           const int am = d / 4, t = d % 4, r = am * 32 + j;
-          afn[am][t] = *(const u32x4*)(ast + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
+          af[P ^ 1][am][t] = *(const u32x4*)(ast + r * 128 + 16 * ((4 * h + t) ^ ((r >> 1) & 7)));
         } else {
           const int nb = (d - 4 * MT) / (NH + 1), e = (d - 4 * MT) % (NH + 1), band = 2 * wave + nb;
-          if (e < NH) cn.w[nb][e] = *(const u32x4*)(wst + band * CODES + e * 1024 + 16 * lane);
-          else cn.sb[nb] = *(const uint32_t*)(wst + 8 * CODES + band * 128 + 4 * j);
+          if (e < NH) cd[P ^ 1].w[nb][e] = *(const u32x4*)(wst + band * CODES + e * 1024 + 16 * lane);
+          else cd[P ^ 1].sb[nb] = *(const uint32_t*)(wst + 8 * CODES + band * 128 + 4 * j);
         }
       }
-      bn[g / 4][g % 4] = deq_step(cc, g / 4, g % 4, sa[g / 4], sbs[g / 4], bi[g / 4]);
+      bf[P ^ 1][g / 4][g % 4] = deq_step(cd[P], g / 4, g % 4, sa[g / 4], sbs[g / 4], bi[g / 4]);
 #pragma unroll
       for (int m = g * MT; m < (g + 1) * MT; m++) {
-        const int am = m / 8, nb = (m / 4) % 2, t = m % 4;
-        acc[nb][am] = mfma_bf16(afc[am][t], bc[nb][t], acc[nb][am]);
+        const int am = m % MT, nb = (m / MT) % 2, t = m / (2 * MT);
+        acc[nb][am] = mfma_bf16(af[P][am][t], bf[P][nb][t], acc[nb][am]);
       }
 #pragma unroll
       for (int m = 0; m < MT; m++) {
@@ -323,31 +320,9 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-      for (int t = 0; t < 4; t++) asm volatile("" : "+v"(bn[nb][t]));
-    s0 = s1;
+      for (int t = 0; t < 4; t++) asm volatile("" : "+v"(bf[P ^ 1][nb][t]));
     advance();
   };
-  // steps [lo, hi) with the current fragments in bf0 / af0 / cd0 on entry and on exit
-  auto run = [&](int lo, int hi) __attribute__((always_inline)) {
-    int i = lo;
-    for (; i + 1 < hi; i += 2) {
-      step(bf0, bf1, af0, af1, cd0, cd1);
-      step(bf1, bf0, af1, af0, cd1, cd0);
-    }
-    if (i < hi) {
-      step(bf0, bf1, af0, af1, cd0, cd1);
-#pragma unroll
-      for (int nb = 0; nb < 2; nb++)
-#pragma unroll
-        for (int t = 0; t < 4; t++) bf0[nb][t] = bf1[nb][t];
-#pragma unroll
-      for (int a = 0; a < MT; a++)
-#pragma unroll
-        for (int t = 0; t < 4; t++) af0[a][t] = af1[a][t];
-      cd0 = cd1;
-    }
-  };
-
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc((void*)p.part, 0, (int)p.part_bytes, 0x00020000);
   const size_t slot_floats = (size_t)8 * NE * 64;
@@ -368,29 +343,51 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
         }
   };
 
+  // Steps [lo, hi): the unrolled body starts at phase 0, and its first pass skips the steps before lo (one unsigned
+  // compare per step).
+  auto run = [&](int lo, int hi) __attribute__((always_inline)) {
+    int i = lo - lo % UNR;
+    const uint32_t len = (uint32_t)(hi - lo);
+    while (i < hi) {
+      sk_static_for<0, UNR>([&](auto KC) __attribute__((always_inline)) {
+        if ((uint32_t)(i - lo) < len) step(KC);
+        i++;
+      });
+    }
+  };
+  // the run's one or two segments: the first segment's piece is written as soon as it ends, while the run goes on
   const bool two = tile_last != tile_first;
   const int n1 = min(n, (tile_first + 1) * G - u0);
-  run(0, n1);
-  if (two) {
-    write_slot(2 * b);  // the first tile's piece, while the run goes on
+  int lo = 0, hi = n1;
+#pragma clang loop unroll(disable)
+  for (int sgi = 0; sgi < 2; sgi++) {
+    run(lo, hi);
+    if (sgi == 1 || !two) break;
+    write_slot(2 * b);
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
       for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
-    run(n1, n);
+    lo = n1, hi = n;
   }
   // every DMA and partial store has landed; LDS is free once all waves are past their reads
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  // a whole tile's acc, staged through LDS and stored as rows (SwiGLU: h)
-  auto store_tile = [&](int t) __attribute__((always_inline)) {
+  // A tile is staged through LDS ([BM][kSkRow] fp32) and leaves as rows (SwiGLU: h). Lane (wave, j, h) stages
+  // acc[nb][a][r] at row a 32 + 8 (r / 4) + 4 h + r % 4, column 32 (2 wave + nb) + j, which are also the entries of its
+  // float4s in a piece slot. The caller has passed a barrier since the staging area was last read.
+  auto stg_at = [&](int nb, int a, int r) __attribute__((always_inline)) {
+    return stg + (a * 32 + 8 * (r / 4) + 4 * h + (r % 4)) * kSkRow + 32 * (2 * wave + nb) + j;
+  };
+  auto stage_tile = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
       for (int a = 0; a < MT; a++)
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-          stg[(a * 32 + 8 * (r / 4) + 4 * h + (r % 4)) * kSkRow + 32 * (2 * wave + nb) + j] = acc[nb][a][r];
+        for (int r = 0; r < 16; r++) *stg_at(nb, a, r) = acc[nb][a][r];
+  };
+  auto emit_tile = [&](int t) __attribute__((always_inline)) {
     __syncthreads();
     const int tm = t % p.tiles_m, tn = t / p.tiles_m;
     if (p.swi) {
@@ -421,6 +418,10 @@ __device__ __forceinline__ void sk_body(const GemmSkArgs& p, uint8_t* lds, const
       }
     }
   };
+  auto store_tile = [&](int t) __attribute__((always_inline)) {
+    stage_tile();
+    emit_tile(t);
+  };
 
   // ---- epilogue: the last segment, stored when it is a whole tile, else a piece of a cut tile
   const int tlo = tile_last * G;
@@ -438,8 +439,7 @@ __global__ __launch_bounds__(kSkThreads, sk_bpc(MT, BITS)) void k_gemm_sk(GemmSk
   extern __shared__ __align__(16) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = xcd_remap(blockIdx.x, p.nblk);
-  if (wave == 0) sk_body<MT, BITS, true>(p, lds, wave, b);
-  else sk_body<MT, BITS, false>(p, lds, wave, b);
+  sk_body<MT, BITS>(p, lds, wave, b);
 }
 
 // Sum of a cut tile's pieces (partial slots, in unit order) and its store. Block (tile, w, a), wave q: the float4
