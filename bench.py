@@ -26,6 +26,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+SETTLE_MS = 30.0  # minimum warmup load before a timed region (see --warmup)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 INT8_PEAK_TOPS = 5000.0
@@ -41,8 +42,8 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     # The GPU's clock needs about 20-30 ms of load to settle after an idle spell (the first calls run fast, then slow
-    # while the power controller overshoots, then settle): 100 warmup steps of the headline (~26 ms) put the timed
-    # steps in the steady state that continuous serving runs in.
+    # while the power controller overshoots, then settle): the warmup runs at least --warmup steps and at least
+    # kSettleMs of load, so the timed steps run in the steady state that continuous serving runs in.
     p.add_argument("--steps", type=int, default=40)
     p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
@@ -165,9 +166,15 @@ def main():
             for j, M in enumerate(Ms):
                 mlp(M, i * len(Ms) + j)
 
-        for i in range(args.warmup):
-            step(i)
-        torch.cuda.synchronize()
+        # at least args.warmup untimed steps, and at least SETTLE_MS of them (in batches of 8, so that the GPU stays
+        # loaded between the host's checks)
+        t0, i = time.perf_counter(), 0
+        while i < args.warmup or (time.perf_counter() - t0) * 1e3 < SETTLE_MS:
+            for _ in range(8 if i >= args.warmup else args.warmup):
+                step(i)
+                i += 1
+            torch.cuda.synchronize()
+        warm_steps = i
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for i in range(args.steps):
@@ -224,7 +231,7 @@ def main():
         dom = max(calls, key=lambda k: calls[k][0])
         ms_d, b_d, f_d = calls[dom]
         achieved = b_d / (ms_d * 1e-3) / 1e9
-        out["headline"] = dict(ms_step=ms_step, value=value, step_bytes=step_bytes, copies=ncp,
+        out["headline"] = dict(ms_step=ms_step, value=value, step_bytes=step_bytes, copies=ncp, warmup_run=warm_steps,
                                value_unfused_count=step_bytes_unfused / (ms_step * 1e-3) / 1e9)
         out["dominant"] = dict(name=dom, ms=ms_d, bytes=b_d, flops=f_d, gbs=achieved,
                                tflops=f_d / (ms_d * 1e-3) / 1e12)
@@ -450,8 +457,8 @@ def main():
         "data": "synthetic (seeded 4-bit affine weights, bf16 N(0,1) activations)",
     }
     # HBM bytes per call of a bench call, from the FETCH_SIZE / WRITE_SIZE counter runs of the same workload scaled by
-    # a plain 256 MiB device copy (profiles/traffic_decode_mlp.md); calls not measured report null
-    measured_traffic = {"gate_up_swiglu_M128": 217737206}
+    # a plain 256 MiB device copy (profiles/traffic_c1_c0_c4.md); calls not measured report null
+    measured_traffic = {"gate_up_swiglu_M128": 216816249}
 
     def roofline(d):
         # the bound is the larger of the call's two floors: its algorithmic bytes at HBM peak, its flops at dense
@@ -473,6 +480,7 @@ def main():
         line.update({
             "value": round(h["value"], 1),
             "ms_per_step": round(h["ms_step"], 4),
+            "warmup_steps_run": h["warmup_run"],
             "config": {"workload": "decode MLP (BASELINE config 1): M in {1,8,32,128}, gate_up 5120->34816, "
                                    "SwiGLU, down 17408->5120, 4-bit g64 weights in the T64 layout",
                        "weight_copies": h["copies"]},
