@@ -259,6 +259,25 @@ def main():
             breakdown["c0_qmv_M1"] = dict(us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9,
                                           frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, copies=ncp)
             del Ws
+            # four such linears sharing the input (a layer's q/k/v/o-sized projections) in one launch
+            # (ifd_gemm_t64_multi), against four single launches of the same weights
+            nl = 4
+            nsets = copies_for(nl * nb)
+            sets = [[ops.pack_t64(qlin(5120, 5120)) for _ in range(nl)] for _ in range(nsets)]
+            Cm = [torch.empty((1, 5120), dtype=torch.bfloat16, device=dev) for _ in range(nl)]
+            mcalls = [ops.gemm_t64_multi_call(A0, S, Cm) for S in sets]
+            ms_m = timed(lambda i: mcalls[i % nsets](), 200, 20)
+
+            def singles(i):
+                for W, C in zip(sets[i % nsets], Cm):
+                    ops.gemm_t64(A0, W, C)
+
+            ms_s = timed(singles, 100, 10)
+            breakdown["c0_multi4_M1"] = dict(us=ms_m * 1e3, us_per_linear=ms_m * 1e3 / nl,
+                                             gbs=nl * byts / (ms_m * 1e-3) / 1e9,
+                                             frac_hbm=nl * byts / (ms_m * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                             singles_us_per_linear=ms_s * 1e3 / nl, copies=nsets)
+            del sets, mcalls
         # ---- config 2: prefill qmm M=4096, K=5120, N=17408 ----------------------------------------------------
         if args.only in ("", "c2"):
             W2 = [ops.pack_t64(qlin(17408, 5120)) for _ in range(2)]

@@ -141,13 +141,6 @@ size_t ifd_gemm_t64_workspace(int M, int N, int K);
 /* C (mode) = A . W^T with W in T64 layout (K % 256 == 0). */
 int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                  void* workspace, size_t ws_bytes, void* stream);
-/* Gate/up projection with its SwiGLU: W (T64) holds [gate (N/2) | up (N/2)] rows and H [M][N/2] (row stride ldh)
- * receives silu_mul of the bf16 product: bit-identical to ifd_gemm_t64 (mode 0) followed by ifd_silu_mul for
- * M <= 16 and on the prefill tiles; on the stream-K rows between, the fused tiles cut K at other places than the
- * plain GEMM's, so a gate or up sum may differ from it by one bf16 step before the SwiGLU. Replaces
- * the reference's gemm + silu_mul pair (qwen35.h:1910-1912, shared expert; qwen35.h:2868-2878, dense MLP) with one
- * call that never stores the [M][N] product when K is split (the SwiGLU runs in the split-K reduction).
- * N % 16 == 0, ldh % 8 == 0, A, H and the workspace 16-byte aligned. */
 /* ifd_gemm_t64 without a caller workspace. No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
  * workspace is a static device array of IFD_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; requests
@@ -157,9 +150,27 @@ int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, 
 #define IFD_NOALLOC_SCRATCH_BYTES ((size_t)68 << 20)
 int ifd_gemm_t64_noalloc(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                          void* stream);
+/* Gate/up projection with its SwiGLU: W (T64) holds [gate (N/2) | up (N/2)] rows and H [M][N/2] (row stride ldh)
+ * receives silu_mul of the bf16 product: bit-identical to ifd_gemm_t64 (mode 0) followed by ifd_silu_mul for
+ * M <= 16 and on the prefill tiles; on the stream-K rows between, the fused tiles cut K at other places than the
+ * plain GEMM's, so a gate or up sum may differ from it by one bf16 step before the SwiGLU. Replaces
+ * the reference's gemm + silu_mul pair (qwen35.h:1910-1912, shared expert; qwen35.h:2868-2878, dense MLP) with one
+ * call that never stores the [M][N] product when K is split (the SwiGLU runs in the split-K reduction).
+ * N % 16 == 0, ldh % 8 == 0, A, H and the workspace 16-byte aligned. */
 size_t ifd_gemm_t64_swiglu_workspace(int M, int N, int K);
 int ifd_gemm_t64_swiglu(const void* A, int lda, const void* wt, int N, int K, void* H, int ldh, int M,
                         void* workspace, size_t ws_bytes, void* stream);
+/* Several T64 linears that share one input, in one launch: C_l (mode 0-2) = A . W_l^T for l < n (1 <= n <= 8),
+ * W_l [Ns[l]][K] packed by ifd_pack_t64, C_l with leading dimension ldcs[l]; M <= 16 (the decode GEMV), K % 256 == 0.
+ * No counterpart in the reference, which issues one gemm() per linear (e.g. in_proj then iproj on the same xn,
+ * engine/src/qwen35.h:2577-2581): this is that set as one launch, the decode GEMV over the linears' concatenated
+ * bands with one K split for all of them. It amortises the per-launch cost (about 2.5 us back to back) that bounds a
+ * small decode linear (5120 x 5120 at M = 1). Same qmv arithmetic as ifd_gemm_t64 at these rows; the K split (and so
+ * the fp32 summation order) is planned for the concatenated width. The workspace's counter header is required when
+ * the launch splits K. */
+size_t ifd_gemm_t64_multi_workspace(int M, int n, const int* Ns, int K);
+int ifd_gemm_t64_multi(const void* A, int lda, int n, const void* const* wts, const int* Ns, int K, void* const* Cs,
+                       const int* ldcs, int M, int mode, void* workspace, size_t ws_bytes, void* stream);
 
 /* ---- W4A8 (reference a8_quant + w4a8_gemm, w4a8.metal:24-98; host w4a8, qwen35.h:1323-1366) ------------------ */
 

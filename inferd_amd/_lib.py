@@ -49,6 +49,8 @@ SIGNATURES = {
     "ifd_gemm_t64_workspace": (_sz, [_i, _i, _i]),
     "ifd_gemm_t64": (_i, [_vp, _i, _vp, _i, _i, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "ifd_gemm_t64_noalloc": (_i, [_vp, _i, _vp, _i, _i, _vp, _i, _i, _i, _vp]),
+    "ifd_gemm_t64_multi_workspace": (_sz, [_i, _i, _vp, _i]),
+    "ifd_gemm_t64_multi": (_i, [_vp, _i, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _vp, _sz, _vp]),
     "ifd_gemm_t64_swiglu_workspace": (_sz, [_i, _i, _i]),
     "ifd_gemm_t64_swiglu": (_i, [_vp, _i, _vp, _i, _i, _vp, _i, _i, _vp, _sz, _vp]),
     "ifd_gemm_t64_w4a8_workspace": (_sz, [_i, _i, _i]),

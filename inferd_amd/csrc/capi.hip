@@ -234,6 +234,31 @@ int ifd_gemm_t64_swiglu(const void* A, int lda, const void* wt, int N, int K, vo
   return launch_gemm_t((const uint16_t*)A, lda, wt, N, K, H, ldh, M, kModeSwiglu, w.body, w.bytes, S(stream));
 }
 
+size_t ifd_gemm_t64_multi_workspace(int M, int n, const int* Ns, int K) {
+  if (M <= 0 || M > 16 || n < 1 || n > 8 || !Ns || K <= 0 || K % 256) return 0;
+  for (int l = 0; l < n; l++)
+    if (Ns[l] <= 0) return 0;
+  return with_header(qmv_t_multi_workspace(M, n, Ns, K));
+}
+
+int ifd_gemm_t64_multi(const void* A, int lda, int n, const void* const* wts, const int* Ns, int K, void* const* Cs,
+                       const int* ldcs, int M, int mode, void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(n >= 1 && n <= 8 && wts && Ns && Cs && ldcs, "n=%d linears (1 to 8) with their arrays", n);
+  IFD_CHECK(M >= 0 && M <= 16 && K > 0 && K % 256 == 0, "bad shape M=%d K=%d (M <= 16, K multiple of 256)", M, K);
+  IFD_CHECK(mode >= 0 && mode <= 2, "mode=%d must be 0, 1 or 2", mode);
+  IFD_CHECK(lda >= K && lda % 8 == 0, "bad stride lda=%d", lda);
+  for (int l = 0; l < n; l++) {
+    IFD_CHECK(Ns[l] > 0 && ldcs[l] >= Ns[l], "linear %d: N=%d ldc=%d", l, Ns[l], ldcs[l]);
+    IFD_CHECK(wts[l] && Cs[l] && aligned(wts[l], 16), "linear %d: null or misaligned pointer", l);
+  }
+  if (M == 0) return IFD_OK;
+  IFD_CHECK(A && aligned(A, 16), "null or misaligned pointer");
+  IFD_CHECK(!workspace || aligned(workspace, 16), "workspace must be 16-byte aligned");
+  const WsView w = ws_view(workspace, ws_bytes);
+  return launch_qmv_t_multi((const uint16_t*)A, lda, n, wts, Ns, K, Cs, ldcs, M, mode, w.cnt, w.body, w.bytes,
+                            S(stream));
+}
+
 int ifd_gemm_t64(const void* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                  void* workspace, size_t ws_bytes, void* stream) {
   IFD_CHECK(M >= 0 && N > 0 && K > 0 && K % 256 == 0, "bad shape M=%d N=%d K=%d (K multiple of 256)", M, N, K);

@@ -107,6 +107,11 @@ int launch_w8a8_t(const int8_t* U, const float* XS, const void* wt, int N, int K
 // cnt: kWsCounters zeroed counters (the workspace header) for the in-kernel split-K fixup; null -> a reduction kernel
 int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,
                  unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st);
+// n linears sharing A and K in one decode-GEMV launch (ifd_gemm_t64_multi)
+size_t qmv_t_multi_workspace(int M, int n, const int* Ns, int K);
+int launch_qmv_t_multi(const uint16_t* A, int lda, int n, const void* const* wts, const int* Ns, int K,
+                       void* const* Cs, const int* ldcs, int M, int mode, unsigned* cnt, void* ws, size_t ws_bytes,
+                       hipStream_t st);
 // W4A8 with per-(row, 64-group) int8 activations on T64 weights, in the affine bf16-MFMA form (xq as exact bf16
 // integers): the prep writes Ab = bf16(U) [M][K] and sxT = sx transposed [G][Mp] (zero past M); M <= 16 runs the
 // decode GEMV (qmv_t_workspace(M, N, K, mode)), more rows the affine k_gemm_t (gemm_t_a8_workspace).

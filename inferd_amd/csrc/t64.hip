@@ -56,6 +56,19 @@ int launch_pack_t64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, in
 // last block to finish a 128-column tile sums its S partials in split order and stores the result (SwiGLU mode:
 // gate tile t and up tile t + sw_half share one counter, and the last of their 2 S blocks writes h), so no
 // reduction kernel follows. The sums are those of k_splitk_reduce / k_splitk_swiglu, bit for bit.
+// MULTI: several linears that share A and K in one launch. Linear l owns the global bands band0[l] ..
+// band0[l + 1] - 1, each linear's count rounded up to whole blocks of 4, so a block never spans two linears. The
+// split partials and the fixup's counters run over the global columns (N = 32 band0[n]); the stores go to each
+// linear's own output.
+constexpr int kQmvMulti = 8;
+struct QmvTMulti {
+  int n;
+  int band0[kQmvMulti + 1];
+  const uint8_t* wt[kQmvMulti];
+  void* C[kQmvMulti];
+  int ldc[kQmvMulti], N[kQmvMulti];
+};
+
 struct QmvTArgs {
   const uint16_t* A;
   int lda;
@@ -69,6 +82,7 @@ struct QmvTArgs {
   int sw_half;    // SwiGLU fixup: number of gate column tiles (0: plain store mode)
   int gps;
   const float* XS;  // A8: the rows' (sx, sx sum xq) per 64-group [M][K / 64][2] (A holds xq as bf16 integers)
+  QmvTMulti mt;     // MULTI only
 };
 
 constexpr int kTB = 2;     // groups per pipeline block
@@ -91,14 +105,23 @@ __device__ __forceinline__ u32x4 t64_bf16_off128(uint32_t w) {
 // A8: the reference's W4A8 GEMM with per-(row, 64-group) int8 activations (w4a8.metal:24-98): A holds xq as exact
 // bf16 integers, so P and the group sums X are exact integers, and per group acc += sx (s P + (b - 128 s) X), the
 // row's group scale sx staged beside X.
-template <int RACT, int BITS, bool A8 = false>
+template <int RACT, int BITS, bool A8 = false, bool MULTI = false>
 __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   constexpr int NH = BITS / 4, TILEB = BITS == 8 ? kT64x8Tile : kT64Tile, CODES = BITS == 8 ? kT64x8Codes : kT64Codes;
   extern __shared__ __align__(16) uint16_t lds[];
   __shared__ unsigned s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
-  const int G = p.K / kGroup, nb = t64_bands(p.N);
+  // this block's linear (MULTI): its weights, output and column count; gb0 its first global band
+  const uint8_t* wbase = p.wt;
+  void* Cl = p.C;
+  int ldcl = p.ldc, Nl = p.N, gb0 = 0;
+  if constexpr (MULTI) {
+    int lin = 0;
+    for (int l = 1; l < p.mt.n; l++) lin += (int)blockIdx.x * 4 >= p.mt.band0[l];
+    wbase = p.mt.wt[lin], Cl = p.mt.C[lin], ldcl = p.mt.ldc[lin], Nl = p.mt.N[lin], gb0 = p.mt.band0[lin];
+  }
+  const int G = p.K / kGroup, nb = t64_bands(Nl);
   const int g0 = blockIdx.y * p.gps, g1 = min(G, g0 + p.gps), Gz = g1 - g0;
   const int Kz = Gz * kGroup, ldA = Kz + 8, M = p.M;
   uint16_t* As = lds;
@@ -107,9 +130,9 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
 
   // this wave's band; its first block of tiles is requested before the activations are staged, so the weight
   // stream starts one memory latency earlier
-  const int band = blockIdx.x * 4 + wave;
+  const int band = blockIdx.x * 4 + wave - gb0;  // the linear's band
   const bool live = band < nb;
-  const uint8_t* tcol = p.wt + (size_t)(live ? band : 0) * TILEB;  // + g * nb * TILEB
+  const uint8_t* tcol = wbase + (size_t)(live ? band : 0) * TILEB;  // + g * nb * TILEB
   const size_t gstride = (size_t)nb * TILEB;
   struct Blk {
     u32x4 w[kTB][NH];
@@ -214,26 +237,26 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
       if (g + 2 * kTB >= g1) break;
     }
   }
-  const int col = band * 32 + j;
+  const int col = band * 32 + j, gcol = (gb0 + band) * 32 + j;  // the linear's column, the global column
   if (gridDim.y == 1) {
-    if (!live || col >= p.N) return;
+    if (!live || col >= Nl) return;
 #pragma unroll
     for (int r = 0; r < RACT; r++) {
       const int row = 8 * (r / 4) + 4 * h + (r % 4);
-      if (row < M) store_mode(p.C, (size_t)row * p.ldc + col, acc[r], p.mode);
+      if (row < M) store_mode(Cl, (size_t)row * ldcl + col, acc[r], p.mode);
     }
     return;
   }
 
   // ---- K split: partials, then (with counters) the fixup by the tile's last block
   const __amdgpu_buffer_rsrc_t rs = part_rsrc(p.part, p.part_bytes);
-  if (live && col < p.N) {
+  if (live && col < Nl) {
 #pragma unroll
     for (int r = 0; r < RACT; r++) {
       const int row = 8 * (r / 4) + 4 * h + (r % 4);
       if (row < M)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[r]),  rs,
-                                              (int)((((size_t)blockIdx.y * M + row) * p.N + col) * 4), 0, kSc1);
+                                              (int)((((size_t)blockIdx.y * M + row) * p.N + gcol) * 4), 0, kSc1);
     }
   }
   if (!p.cnt) return;
@@ -276,14 +299,14 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
   for (int e = tid; e < M * 32; e += 256) {
     const int row = e >> 5, c4 = (e & 31) * 4;
     if (!p.sw_half) {
-      const int c = (int)blockIdx.x * 128 + c4;
-      if (c >= p.N) continue;
+      const int c = (int)blockIdx.x * 128 + c4, cl = c - 32 * gb0;  // global, and the linear's column
+      if (cl >= Nl) continue;
       const float4 v = sum4((size_t)row * p.N + c);
-      const size_t o = (size_t)row * p.ldc + c;
-      store_mode(p.C, o, v.x, p.mode);
-      store_mode(p.C, o + 1, v.y, p.mode);
-      store_mode(p.C, o + 2, v.z, p.mode);
-      store_mode(p.C, o + 3, v.w, p.mode);
+      const size_t o = (size_t)row * ldcl + cl;
+      store_mode(Cl, o, v.x, p.mode);
+      store_mode(Cl, o + 1, v.y, p.mode);
+      store_mode(Cl, o + 2, v.z, p.mode);
+      store_mode(Cl, o + 3, v.w, p.mode);
     } else {
       const int I = p.N / 2, c = tile * 128 + c4;
       const float4 g = sum4((size_t)row * p.N + c), u = sum4((size_t)row * p.N + I + c);
@@ -357,7 +380,8 @@ static int launch_qmv_t_bits(const uint16_t* A, int lda, const void* wt, int N, 
              fix ? cnt : nullptr,
              fix && mode == kModeSwiglu ? (t64_bands(N) + 3) / 4 / 2 : 0,
              pl.gps,
-             XS};
+             XS,
+             {}};
   const int Kz = pl.gps * kGroup;
   const size_t lds =
       ((size_t)M * (Kz + 8) * 2 + 15) / 16 * 16 + (size_t)pl.gps * 16 * sizeof(float) * (A8 ? 2 : 1);
@@ -368,6 +392,47 @@ static int launch_qmv_t_bits(const uint16_t* A, int lda, const void* wt, int N, 
   IFD_TRY(check_launch("qmv_t64"));
   if (fix) return IFD_OK;
   return launch_epilogue(ws, pl.S, M, N, C, ldc, mode, st);
+}
+
+// Several linears sharing A and K (M <= 16, modes 0-2): the decode GEMV over their concatenated bands in one launch.
+// Its K split is planned for the concatenated width and summed in-kernel (counters required when it splits).
+size_t qmv_t_multi_workspace(int M, int n, const int* Ns, int K) {
+  int bands = 0;
+  for (int l = 0; l < n; l++) bands += (t64_bands(Ns[l]) + 3) / 4 * 4;
+  return qmv_t_workspace(M, 32 * bands, K, 0);
+}
+int launch_qmv_t_multi(const uint16_t* A, int lda, int n, const void* const* wts, const int* Ns, int K,
+                       void* const* Cs, const int* ldcs, int M, int mode, unsigned* cnt, void* ws, size_t ws_bytes,
+                       hipStream_t st) {
+  if (M == 0) return IFD_OK;
+  if (M > 16) return fail(IFD_ERR_UNSUPPORTED, "T64 multi-linear GEMV takes M <= 16");
+  if (n < 1 || n > kQmvMulti) return fail(IFD_ERR_ARG, "T64 multi-linear GEMV: n=%d linears (1 to %d)", n, kQmvMulti);
+  if (K % (kGroup * kTB)) return fail(IFD_ERR_ARG, "T64 decode needs K %% %d == 0 (K=%d)", kGroup * kTB, K);
+  if (mode == kModeSwiglu) return fail(IFD_ERR_UNSUPPORTED, "T64 multi-linear GEMV: modes 0-2");
+  QmvTMulti mt{};
+  mt.n = n;
+  int bands = 0;
+  for (int l = 0; l < n; l++) {
+    mt.band0[l] = bands;
+    mt.wt[l] = (const uint8_t*)wts[l], mt.C[l] = Cs[l], mt.ldc[l] = ldcs[l], mt.N[l] = Ns[l];
+    bands += (t64_bands(Ns[l]) + 3) / 4 * 4;
+  }
+  mt.band0[n] = bands;
+  const int Ntot = 32 * bands;
+  const TPlan pl = qmv_t_plan(M, Ntot, K);
+  const size_t need = epilogue_ws_bytes(pl.S, M, Ntot, mode);
+  if (need > ws_bytes || (need && !ws))
+    return fail(IFD_ERR_WORKSPACE, "qmv_t64 multi needs %zu bytes of workspace, got %zu", need, ws_bytes);
+  if (pl.S > 1 && !(cnt && qmv_t_fixup(Ntot, mode, pl.S)))
+    return fail(IFD_ERR_WORKSPACE, "qmv_t64 multi: a split launch needs the workspace's counter header");
+  QmvTArgs p{A, lda, nullptr, Ntot, K, nullptr, 0, M, mode, (float*)ws, (uint32_t)(pl.S > 1 ? need : 0),
+             pl.S > 1 ? cnt : nullptr, 0, pl.gps, nullptr, mt};
+  const size_t lds = ((size_t)M * (pl.gps * kGroup + 8) * 2 + 15) / 16 * 16 + (size_t)pl.gps * 16 * sizeof(float);
+  if (lds > 64 * 1024) return fail(IFD_ERR_UNSUPPORTED, "qmv_t64 multi: %zu bytes of LDS needed", lds);
+  dim3 grid(bands / 4, pl.S), block(256);
+  if (M <= 8) hipLaunchKernelGGL((k_qmv_t<4, 4, false, true>), grid, block, lds, st, p);
+  else hipLaunchKernelGGL((k_qmv_t<8, 4, false, true>), grid, block, lds, st, p);
+  return check_launch("qmv_t64 multi");
 }
 
 int launch_qmv_t(const uint16_t* A, int lda, const void* wt, int N, int K, void* C, int ldc, int M, int mode,

@@ -9,6 +9,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Optional
 
+import ctypes
+
 import torch
 
 from ._lib import check, lib
@@ -89,6 +91,40 @@ def gemm_t64(A: torch.Tensor, W: T64Linear, C: Optional[torch.Tensor] = None, mo
     check(lib().ifd_gemm_t64(_p(A), K, _p(W.wt), W.N, W.K, _p(C), C.shape[1], M, mode, _p(ws),
                              ws.numel() if ws is not None else 0, _stream()))
     return C
+
+
+def gemm_t64_multi_call(A: torch.Tensor, Ws: list, outs: list, mode: int = 0):
+    """A prepared gemm_t64_multi: the pointer arrays and the workspace are built once, and the returned function
+    launches C_l (mode) = A . W_l^T with one library call (it keeps A, Ws, outs and the workspace alive)."""
+    M, K = A.shape
+    n = len(Ws)
+    assert A.dtype == torch.bfloat16 and A.is_contiguous() and 1 <= n <= 8 and len(outs) == n
+    assert all(W.K == K for W in Ws)
+    Ns = (ctypes.c_int * n)(*[W.N for W in Ws])
+    wts = (ctypes.c_void_p * n)(*[W.wt.data_ptr() for W in Ws])
+    Cs = (ctypes.c_void_p * n)(*[C.data_ptr() for C in outs])
+    ldcs = (ctypes.c_int * n)(*[C.stride(0) for C in outs])
+    need = lib().ifd_gemm_t64_multi_workspace(M, n, Ns, K)
+    ws = workspace(need, A.device) if need else None
+    args = (_p(A), K, n, wts, Ns, K, Cs, ldcs, M, mode, _p(ws), ws.numel() if ws is not None else 0)
+    keep = (A, Ws, outs, ws)
+
+    def call() -> None:
+        assert keep
+        check(lib().ifd_gemm_t64_multi(*args, _stream()))
+
+    return call
+
+
+def gemm_t64_multi(A: torch.Tensor, Ws: list, outs: Optional[list] = None, mode: int = 0) -> list:
+    """C_l (mode) = A . W_l^T for 1 to 8 T64 linears that share A and K (M <= 16), in one launch; mode 1 adds into
+    the given outputs, mode 2 writes fp32."""
+    M = A.shape[0]
+    if outs is None:
+        outs = [torch.empty((M, W.N), dtype=torch.float32 if mode == 2 else torch.bfloat16, device=A.device)
+                for W in Ws]
+    gemm_t64_multi_call(A, Ws, outs, mode)()
+    return outs
 
 
 def gemm_t64_swiglu(A: torch.Tensor, W: T64Linear, out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -178,3 +178,32 @@ def test_new_workspace_queries():
     assert HEADER_BYTES < w1 < w8
     assert L.ifd_mlp_decode_workspace(1, 5120, 17408) > HEADER_BYTES + 5120 * 2 + 17408 * 2
     assert L.ifd_gemm_w8_workspace(1, 5120, 5120) == L.ifd_gemm_w4_workspace(1, 5120, 5120)
+
+
+def test_multi_linear_gemv_checks():
+    """The multi-linear decode GEMV: 1 to 8 linears, M <= 16, K a multiple of 256, ldc >= N per linear, and a K split
+    needs the workspace (with its counter header) the size query reports. All before any GPU work."""
+    L = _lib.lib()
+    E = _lib.IFD_ERR_ARG
+
+    def arrs(Ns, ldcs=None):
+        n = len(Ns)
+        return ((ctypes.c_void_p * n)(*[4096] * n), (ctypes.c_int * n)(*Ns), (ctypes.c_void_p * n)(*[4096] * n),
+                (ctypes.c_int * n)(*(ldcs or Ns)))
+
+    Ns = [5120, 1024, 1024, 5120]
+    wts, ns, cs, ldcs = arrs(Ns)
+    need = L.ifd_gemm_t64_multi_workspace(1, 4, ns, 5120)
+    assert need > HEADER_BYTES and (need - HEADER_BYTES) % (4 * 32 * 4) == 0
+    assert L.ifd_gemm_t64_multi_workspace(17, 4, ns, 5120) == 0
+    assert L.ifd_gemm_t64_multi_workspace(1, 9, (ctypes.c_int * 9)(*[128] * 9), 5120) == 0
+    assert L.ifd_gemm_t64_multi_workspace(1, 4, ns, 5000) == 0
+    call = lambda n=4, M=1, K=5120, mode=0, a=(wts, ns, cs, ldcs), ws=4096, wsb=0: L.ifd_gemm_t64_multi(
+        4096, K, n, a[0], a[1], K, a[2], a[3], M, mode, ws, wsb, None)
+    assert call(n=0) == E and call(n=9) == E and b"1 to 8" in L.ifd_last_error()
+    assert call(M=17) == E and call(K=5000) == E
+    assert call(mode=3) == E and b"mode=3" in L.ifd_last_error()
+    assert call(a=arrs(Ns, [5120, 1000, 1024, 5120])) == E and b"linear 1" in L.ifd_last_error()
+    assert call() == _lib.IFD_ERR_WORKSPACE
+    assert call(ws=None, wsb=need) == _lib.IFD_ERR_WORKSPACE
+    assert call(M=0) == _lib.IFD_OK

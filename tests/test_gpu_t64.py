@@ -221,6 +221,66 @@ def test_split_k_is_deterministic():
         gen.check_bf16(outs[0][rows], Y, 1e-2, (M, N, K))
 
 
+def _multi_linears(Ns, K, seed):
+    g, ops = _gu(), _ops()
+    ws = [gen.qlinear(N, K, seed=seed + i)[1:] for i, N in enumerate(Ns)]
+    return ws, [ops.pack_t64(g.qlinear(*w)) for w in ws]
+
+
+@pytest.mark.parametrize("M", [1, 8, 9, 16])
+def test_gemm_t64_multi_matches_oracle(M):
+    """Several linears sharing A in one decode launch (the attention projections' q/k/v/o widths, a 200-wide tail and
+    a 96-wide one that pads its block with dead bands): each output against the oracle, over a K split planned for
+    their concatenated width (in-kernel fixup)."""
+    import ctypes
+    from inferd_amd._lib import lib
+    g, ops = _gu(), _ops()
+    Ns, K = [5120, 1024, 200, 4096, 96], 5120
+    assert lib().ifd_gemm_t64_multi_workspace(M, len(Ns), (ctypes.c_int * len(Ns))(*Ns), K) > 0
+    ws, Ts = _multi_linears(Ns, K, 40 + M)
+    A = gen.activations(M, K, seed=M + 41)
+    outs = [g.host(o) for o in ops.gemm_t64_multi(g.dev(A), Ts)]
+    for (wq, s, b), out, N in zip(ws, outs, Ns):
+        assert out.shape == (M, N)
+        gen.check_bf16(out, orc.qmv(A, wq, s, b), 1e-2, (M, N, K))
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_gemm_t64_multi_modes(mode):
+    """Residual add (mode 1) and fp32 out (mode 2) into strided views of wider buffers, eight linears (the most one
+    launch takes) with no K split (K = 512) and with one (K = 8192)."""
+    g, ops = _gu(), _ops()
+    M = 5
+    for K, Ns in [(512, [128, 256, 32, 640, 128, 96, 384, 128]), (8192, [512, 1536, 256])]:
+        ws, Ts = _multi_linears(Ns, K, 60 + K)
+        A = gen.activations(M, K, seed=K)
+        C0 = [gen.activations(M, N, seed=N + i) for i, N in enumerate(Ns)]
+        dt = torch.float32 if mode == 2 else torch.bfloat16
+        wide = [torch.zeros((M, N + 40), dtype=dt, device="cuda") for N in Ns]
+        if mode == 1:
+            for w, c in zip(wide, C0):
+                w[:, : c.shape[1]] = g.dev(c)
+        ops.gemm_t64_multi(g.dev(A), Ts, outs=[w[:, :N] for w, N in zip(wide, Ns)], mode=mode)
+        for (wq, s, b), w, c, N in zip(ws, wide, C0, Ns):
+            got = g.host(w)
+            Y = orc.qmv(A, wq, s, b)
+            gen.check_out(got[:, :N], Y if mode == 2 else Y + gen.bf16_to_f32(c), 1e-2, (mode, K, N), fp32=mode == 2)
+            assert not got[:, N:].any(), "stores past a linear's N"
+
+
+def test_gemm_t64_multi_repeats_and_matches_single_calls():
+    """The fixup's counters return to zero: repeated launches give identical bits, and each output stays within the
+    bar of the single-linear call (their K splits differ, so the sums' order does too)."""
+    g, ops = _gu(), _ops()
+    Ns, K, M = [5120, 5120, 5120, 5120], 5120, 1
+    _, Ts = _multi_linears(Ns, K, 90)
+    A = g.dev(gen.activations(M, K, seed=91))
+    runs = [[g.host(o) for o in ops.gemm_t64_multi(A, Ts)] for _ in range(3)]
+    assert all(np.array_equal(a, b) for r in runs[1:] for a, b in zip(runs[0], r))
+    for T, out in zip(Ts, runs[0]):
+        gen.check_bf16(out, gen.bf16_to_f32(g.host(ops.gemm_t64(A, T))), 1e-2, "multi vs single")
+
+
 @pytest.mark.parametrize("M,N,K,mode", [
     (32, 34816, 5120, 1),   # decode gate_up, 32-row tiles two blocks per CU: ~5 pieces per tile
     (64, 23040, 1024, 2),   # 90 tiles (the fewest stream-K takes), runs of ~6 groups: ~4 pieces per tile
