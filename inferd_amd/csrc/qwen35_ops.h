@@ -168,6 +168,23 @@ struct Qwen35 {
     return use_w4a8 && (W.bits == 4 || W.bits == 8) && W.flipped && !W.ldk && M > qmv_max && M < w4a8_max &&
            W.K % 64 == 0;
   }
+  // QA8 (qwen35.h:1164-1206, 1847-1868): steps of at least qa8_min rows run on per-(row, 64-group) int8 activations
+  // from the qa8 quantizer (xq = clamp(rint(x 127 / amax), -127, 127), ifd_a8_quant form 2) times the 4-bit codes:
+  // the dense GEMMs, and (moe_qa8, from moe_qa8_min tokens) the sorted MoE's gathered expert GEMMs. The reference
+  // turns it on by itself only on GPUs with neural accelerators (qa8_auto, :1084-1092) and leaves it off on the
+  // others, as this build does unless QA8=1 (the same variables as the reference): then the results take the
+  // arithmetic of such a run. The MoE's int8 rows need staging the constructor allocates only when QA8 is on.
+  int qa8_on = env_int("QA8", 0), qa8_min = env_int("QA8_MIN", 256);
+  int moe_qa8 = env_int("MOE_QA8", 1), moe_qa8_min = env_int("MOE_QA8_MIN", 9);
+  BufRef q8u, q8x;  // the MoE's int8 rows [max_rows k][max(H, I)] and their (sx, sx sum xq) per 64-group
+  bool qa8_route(const QLinear& W, int M) const {
+    return qa8_on > 0 && W.bits == 4 && !W.ldk && W.K % 256 == 0 && W.N % 32 == 0 && M >= qa8_min && M <= max_rows &&
+           !a8_ready && W.K <= a8_k;
+  }
+  bool qa8g_route(const Layer& ly, int T) const {
+    return moe_qa8 && qa8_on > 0 && T >= moe_qa8_min && ly.egu.bits == 4 && ly.edown.bits == 4 &&
+           cfg.hidden % 256 == 0 && cfg.moe_inter % 256 == 0 && cfg.experts <= 1024;
+  }
 
   // shared_inter: the shared expert's intermediate size (0: none). gemm_scratch: bytes for gemm() calls made outside
   // encode_moe (the largest workspace query of the model's shapes over every row count). a8_k: the longest K of a
@@ -224,6 +241,11 @@ struct Qwen35 {
       a8u = alloc((size_t)max_rows * a8_k);
       a8x = alloc((size_t)max_rows * (a8_k / 64) * 2 * 4);
     }
+    if (qa8_on > 0 && max_rows > 0 && E > 0) {
+      const size_t rows = (size_t)max_rows * k, w = std::max(H, I);
+      q8u = alloc(rows * w);
+      q8x = alloc(rows * (w / 64) * 2 * 4);
+    }
     if (need) {
       splitk = alloc(need);
       hip_ok(hipMemset(splitk.buf, 0, need), "Qwen35");  // the workspace's leading counters start at zero
@@ -233,7 +255,7 @@ struct Qwen35 {
   ~Qwen35() {
     for (void* p : {x.buf, xn.buf, rlog.buf, ridx.buf, rw.buf, rsg.buf, proj.buf, act.buf, sh_out.buf, moffs.buf,
                     mperm.buf, minv.buf, mtiles.buf, mntiles.buf, eact.buf, edown_out.buf, splitk.buf, a8u.buf,
-                    a8x.buf})
+                    a8x.buf, q8u.buf, q8x.buf})
       if (p) (void)hipFree(p);
   }
   Qwen35(const Qwen35&) = delete;
@@ -242,7 +264,8 @@ struct Qwen35 {
   // H [M][N/2] = SwiGLU of A . W^T for a [gate | up] linear: one fused call on T64 weights, else the reference's
   // gemm into proj + silu_mul (qwen35.h:1910-1912).
   void gemm_swiglu(Enc& e, const BufRef& A, const QLinear& W, const BufRef& H, int M) {
-    if (W.bits == 4 && W.t64 && W.K % 256 == 0 && W.N % 16 == 0 && !w4a8_route(W, M) && !a8_ready) {
+    if (W.bits == 4 && W.t64 && W.K % 256 == 0 && W.N % 16 == 0 && !w4a8_route(W, M) && !qa8_route(W, M) &&
+        !a8_ready) {
       const size_t need = ifd_gemm_t64_swiglu_workspace(M, W.N, W.K);
       if (need > splitk_bytes) die("gemm_swiglu", "split-K scratch smaller than this shape needs");
       ok(ifd_gemm_t64_swiglu(A.ptr<void>(), W.K, W.t64.ptr<void>(), W.N, W.K, H.ptr<void>(), W.N / 2, M,
@@ -259,6 +282,10 @@ struct Qwen35 {
   void gemm(Enc& e, const BufRef& A, const QLinear& W, const BufRef& C, int M, int mode, bool defer = false) {
     (void)defer;
     if (W.ldk && a8_ready) die("gemm", "K-slice view off the qmm path");  // qwen35.h:1469
+    if (qa8_route(W, M)) {  // qwen35.h:1472
+      qa8(e, A, W, C, M, mode);
+      return;
+    }
     if (w4a8_route(W, M)) {
       w4a8(e, A, W, C, M, mode);
       return;
@@ -329,6 +356,27 @@ struct Qwen35 {
        "gemm");
   }
 
+  // The reference's QA8 GEMM (qwen35.h:1187-1206): the rows' qa8 int8 form, then per group y += s sx P + b (sx sum xq)
+  // on the 4-bit codes (unflipped: a flipped layer's MLX codes are read through xr; its T64 copy holds them
+  // unflipped), on the T64 kernels when the layer has its copy.
+  void qa8(Enc& e, const BufRef& A, const QLinear& W, const BufRef& C, int M, int mode) {
+    ok(ifd_a8_quant(A.ptr<void>(), W.K, M, W.K, 2, a8u.ptr<int8_t>(), a8x.ptr<float>(), e.stream), "gemm");
+    if (W.t64) {
+      const size_t need = ifd_gemm_t64_w4a8_workspace(M, W.N, W.K);
+      if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
+      ok(ifd_gemm_t64_w4a8(a8u.ptr<int8_t>(), a8x.ptr<float>(), 0, W.t64.ptr<void>(), W.N, W.K, C.ptr<void>(), W.N, M,
+                           mode, splitk.ptr<void>(), splitk_bytes, e.stream),
+         "gemm");
+      return;
+    }
+    const size_t need = ifd_qmm_w4a8_workspace(M, W.N, W.K);
+    if (need > splitk_bytes) die("gemm", "split-K scratch smaller than this shape needs");
+    ok(ifd_qmm_w4a8(a8u.ptr<int8_t>(), a8x.ptr<float>(), 0, W.wq.ptr<uint32_t>(), W.s.ptr<uint16_t>(),
+                    W.b.ptr<uint16_t>(), W.N, W.K, 0, W.flipped ? 0x88888888u : 0u, C.ptr<void>(), W.N, M, mode,
+                    splitk.ptr<void>(), splitk_bytes, e.stream),
+       "gemm");
+  }
+
   // rmsnorm of rows [rows][D] into out, fused with the W4A8 activation quantization when `next` (the GEMM that reads
   // out) takes that route (reference rmsnorm_for, qwen35.h:1982-2001).
   void rmsnorm_for(Enc& e, const BufRef& in, const BufRef& w, const BufRef& out, int rows, int D, const QLinear& next) {
@@ -385,7 +433,7 @@ struct Qwen35 {
     const QLinear &gu = ly.gate_up, &dn = ly.down;
     return moe_t64_route(ly) && gu.N > 0 && gu.bits == 4 && dn.bits == 4 && gu.t64 && dn.t64 && gu.N == 2 * I &&
            gu.K == H && dn.N == H && dn.K == I && !gu.ldk && !dn.ldk && T > qmv_max && !w4a8_route(gu, T) &&
-           !w4a8_route(dn, T);
+           !w4a8_route(dn, T) && !qa8_route(gu, T) && !qa8_route(dn, T);
   }
 
   // The MoE block on the hidden state x [T][H]: xn = rmsnorm(x, post_norm); shared expert; router; top-k softmax
@@ -465,7 +513,9 @@ struct Qwen35 {
     }
     // shared expert -> sh_out (its gate/up may read the norm's int8 rows; the SwiGLU feeds the down GEMM in bf16,
     // qwen35.h:1910-1914), unless it runs as expert E of the T64 launches
-    const bool t64 = moe_t64_route(ly), fold = shared_as_expert(ly, T);
+    const bool q8 = qa8g_route(ly, T);
+    if (q8 && !q8u.buf) die("encode_moe", "the MoE's QA8 route needs its int8 staging: construct with QA8=1");
+    const bool t64 = !q8 && moe_t64_route(ly), fold = !q8 && shared_as_expert(ly, T);
     const bool shared = has_shared && !fold;
     if (shared) {
       gemm_swiglu(e, xn, ly.gate_up, act, T);
@@ -510,6 +560,25 @@ struct Qwen35 {
                         mntiles.ptr<int>(), splitk.ptr<void>(), splitk_bytes, e.stream),
        "encode_moe");
     const int mt = ifd_moe_tiles_max(R, E);
+    if (q8) {
+      // QA8's gathered GEMMs (qa8g, qwen35.h:1960-1966): the token rows' int8 form read through perm for gate/up
+      // (SwiGLU fused: silu_mul of the bf16 product, as moe_silu_mul), then the sorted SwiGLU rows' int8 form for down
+      ok(ifd_a8_quant(xn.ptr<void>(), H, T, H, 2, q8u.ptr<int8_t>(), q8x.ptr<float>(), e.stream), "encode_moe");
+      ok(ifd_moe_gather_qmm_a8(q8u.ptr<int8_t>(), q8x.ptr<float>(), mperm.ptr<int>(), k, moffs.ptr<int>(),
+                               mtiles.ptr<int>(), mntiles.ptr<int>(), mt, ly.egu.wq.ptr<uint32_t>(),
+                               ly.egu.s.ptr<uint16_t>(), ly.egu.b.ptr<uint16_t>(), E, 2 * I, H, 1, eact.ptr<void>(), R,
+                               e.stream),
+         "encode_moe");
+      ok(ifd_a8_quant(eact.ptr<void>(), I, R, I, 2, q8u.ptr<int8_t>(), q8x.ptr<float>(), e.stream), "encode_moe");
+      ok(ifd_moe_gather_qmm_a8(q8u.ptr<int8_t>(), q8x.ptr<float>(), nullptr, 1, moffs.ptr<int>(), mtiles.ptr<int>(),
+                               mntiles.ptr<int>(), mt, ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(),
+                               ly.edown.b.ptr<uint16_t>(), E, H, I, 0, edown_out.ptr<void>(), R, e.stream),
+         "encode_moe");
+      ok(ifd_moe_combine(x.ptr<void>(), edown_out.ptr<void>(), rw.ptr<float>(), shared ? sh_out.ptr<void>() : nullptr,
+                         rsg.ptr<float>(), minv.ptr<int>(), T, H, k, 0, e.stream),
+         "encode_moe");
+      return;
+    }
     // 4- or 8-bit stacks (the reference's gqmm at W.bits, qwen35.h:1835)
     ok(ifd_moe_gather_qmm_ex(xn.ptr<void>(), mperm.ptr<int>(), k, moffs.ptr<int>(), mtiles.ptr<int>(),
                              mntiles.ptr<int>(), mt, ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(),

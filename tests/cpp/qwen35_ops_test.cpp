@@ -59,6 +59,10 @@ void orc_moe_experts(const uint16_t* xn, int T, int H, int I, int E, int k, cons
                      int nthreads);
 void orc_moe_combine(uint16_t* x, const uint16_t* yd, const float* wt, const uint16_t* ys, const float* sg,
                      const int* inv, int T, int H, int k, int assign);
+void orc_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, int* inv);
+void orc_moe_gather_w4a8(const int8_t* U, const float* XS, const int* perm, int div, const int* offsets,
+                         const uint32_t* wq, const uint16_t* s, const uint16_t* b, int E, int N, int K, float* Y,
+                         int nthreads);
 }
 
 using namespace inferd;
@@ -202,11 +206,12 @@ std::vector<uint16_t> activations(int M, int K, std::mt19937& rng) {
 }
 
 // fp32 y of the reference's W4A8 / W8A8 route: per-group int8 activations (a8_quant) times the (unflipped) codes
+// form: the activation quantizer (0: a8_quant, the W4A8 route's; 2: qa8_quant, the QA8 route's)
 std::vector<float> ref_wxa8(const std::vector<uint16_t>& A, int M, int K, const uint32_t* wq, const uint16_t* s,
-                            const uint16_t* b, int N, int bits) {
+                            const uint16_t* b, int N, int bits, int form = 0) {
   std::vector<int8_t> U((size_t)M * K);
   std::vector<float> XS((size_t)M * (K / 64) * 2), y((size_t)M * N);
-  orc_a8_quant(A.data(), K, M, K, 0, U.data(), XS.data());
+  orc_a8_quant(A.data(), K, M, K, form, U.data(), XS.data());
   orc_wxa8(U.data(), XS.data(), wq, s, b, N, K, bits, 0, y.data(), M, 0);
   return y;
 }
@@ -797,6 +802,132 @@ void test_encode_moe_t64(std::mt19937& rng) {
   run_moe_t64(L, 64, 64, 0, 1 << 30, 0, rng);
 }
 
+// The QA8 routes (QA8=1): gemm() of at least qa8_min rows on the qa8 int8 rows (MLX layout, unflipped and flipped, and
+// the T64 copy; modes 0-2), one row fewer on the plain route; and encode_moe's sorted path on the gathered int8
+// GEMMs, against the oracle's composition of the qa8 quantizer, the per-group integer products, SwiGLU and the
+// combine (the shared expert through gemm_swiglu / gemm(): qmm below qa8_min rows, QA8 from there, where the T64
+// copy's fused SwiGLU call gives way to gemm() + silu_mul).
+void test_qa8(std::mt19937& rng) {
+  setenv("QA8", "1", 1);
+  {
+    Config c;
+    Qwen35 m(c, 300, 0, 64 << 20, 1024);
+    Enc e;
+    const int N = 384, K = 1024;
+    const HostLinear h = make_linear(N, K, rng);
+    HostLinear hf = h;
+    orc_flip(hf.wq.data(), (int64_t)hf.wq.size(), 0x88888888u);
+    QLinear W = device_linear(h), Wf = device_linear(hf), Wt = W;
+    Wf.flipped = true;
+    void* t = nullptr;
+    hip_ok(hipMalloc(&t, ifd_t64_bytes(N, K, 1)), "t64");
+    ok(ifd_pack_t64(W.wq.ptr<uint32_t>(), W.s.ptr<uint16_t>(), W.b.ptr<uint16_t>(), N, K, 0, 0, 1, t, e.stream),
+       "pack_t64");
+    Wt.t64 = BufRef(t);
+    struct Case {
+      const QLinear* W;
+      const char* name;
+      int M, mode;
+    };
+    for (const Case cs : {Case{&W, "MLX layout", 255, 0}, Case{&W, "MLX layout", 256, 0}, Case{&W, "MLX layout", 300, 0},
+                          Case{&Wf, "MLX layout, flipped", 300, 0}, Case{&Wt, "T64", 255, 0}, Case{&Wt, "T64", 300, 0},
+                          Case{&Wt, "T64", 300, 1}, Case{&Wt, "T64", 300, 2}}) {
+      const int M = cs.M;
+      const auto A = activations(M, K, rng);
+      const auto C0 = activations(M, N, rng);
+      const bool q8 = m.qa8_route(*cs.W, M);
+      BufRef dA = upload(A), dC = cs.mode == 2 ? upload(std::vector<float>((size_t)M * N)) : upload(C0);
+      m.gemm(e, dA, *cs.W, dC, M, cs.mode);
+      // the plain route at 255 rows: qmm on the MLX layout; T64's stream-K or prefill tiles (qmm) at these shapes
+      auto y = q8 ? ref_wxa8(A, M, K, h.wq.data(), h.s.data(), h.b.data(), N, 4, 2) : ref_gemm(A, h, M, false);
+      const std::string tag = std::string("gemm ") + cs.name + " M=" + std::to_string(M) + " mode " +
+                              std::to_string(cs.mode) + (q8 ? " (QA8 route)" : " (plain route)");
+      if (cs.mode == 2) {
+        const auto f = download<float>(dC, (size_t)M * N);
+        double ss = 0, w = 0;
+        for (size_t i = 0; i < y.size(); i++) ss += (double)y[i] * y[i], w = std::max(w, (double)std::fabs(f[i] - y[i]));
+        const double err = w / std::sqrt(ss / y.size());
+        report(err <= 1e-4 && q8 == (M >= 256), tag, err);
+      } else {
+        if (cs.mode == 1)
+          for (size_t i = 0; i < y.size(); i++) y[i] += bf2f(C0[i]);
+        const double err = bf16_err(download<uint16_t>(dC, (size_t)M * N), y, false);
+        report(err <= 1e-2 && q8 == (M >= 256), tag, err);
+      }
+      (void)hipFree(dA.buf), (void)hipFree(dC.buf);
+    }
+    for (void* p : {W.wq.buf, W.s.buf, W.b.buf, Wf.wq.buf, Wf.s.buf, Wf.b.buf, t}) (void)hipFree(p);
+  }
+  // encode_moe: T = 40 with the shared expert on the MLX layout (qmm); T = 300 with its T64 copies (QA8 from 256
+  // rows); T = 64 without one. The routed experts take the int8 gathered GEMMs whatever copies the stacks have.
+  MoeLayer L(MoeGeo{512, 32, 4, 256}, rng);
+  const int H = 512, E = 32, k = 4, I = 256;
+  for (const int cs : {0, 1, 2}) {
+    const int T = cs == 0 ? 40 : cs == 1 ? 300 : 64, R = T * k;
+    const bool has_shared = cs != 2;
+    Config c;
+    c.hidden = H, c.experts = E, c.topk = k, c.moe_inter = I, c.eps = 1e-6f;
+    Layer ly = L.ly;
+    if (!has_shared) ly.gate_up = QLinear(), ly.down = QLinear(), ly.router.N = E;
+    if (cs == 0) ly.gate_up.t64 = BufRef(), ly.down.t64 = BufRef();
+    Qwen35 m(c, T, has_shared ? I : 0, 0);
+    Enc e;
+    const auto x0 = activations(T, H, rng);
+    hip_ok(hipMemcpy(m.x.ptr<void>(), x0.data(), x0.size() * 2, hipMemcpyHostToDevice), "x");
+    m.encode_moe(e, ly, T);
+    const auto x1 = download<uint16_t>(m.x, (size_t)T * H);
+    const auto xn = download<uint16_t>(m.xn, (size_t)T * H);
+    const auto idx = download<int>(m.ridx, (size_t)T * k);
+    const auto wt = download<float>(m.rw, (size_t)T * k);
+    const auto sg = download<float>(m.rsg, (size_t)T);
+    const std::string tag = " T=" + std::to_string(T) +
+                            (has_shared ? (ly.gate_up.t64 ? " (shared expert, T64 copies)" : " (shared expert, MLX)")
+                                        : " (no shared expert)");
+    report(m.qa8g_route(ly, T) && !m.moe_decode_route(ly, T), "encode_moe takes the QA8 sorted route" + tag, 0);
+    // shared expert: gemm() on xn, silu_mul, gemm() (QA8 from qa8_min rows, else qmm)
+    std::vector<uint16_t> ys;
+    if (has_shared) {
+      const bool q8 = T >= m.qa8_min;
+      auto dense = [&](const std::vector<uint16_t>& a, const HostLinear& w, int N, int K) {
+        std::vector<float> y((size_t)T * N);
+        if (q8) y = ref_wxa8(a, T, K, w.wq.data(), w.s.data(), w.b.data(), N, 4, 2);
+        else orc_qmm(a.data(), K, w.wq.data(), w.s.data(), w.b.data(), N, K, 0, y.data(), T, 0);
+        std::vector<uint16_t> o(y.size());
+        for (size_t i = 0; i < y.size(); i++) o[i] = f2bf(y[i]);
+        return o;
+      };
+      const auto gu = dense(xn, L.sgu, 2 * I, H);
+      std::vector<uint16_t> act((size_t)T * I);
+      orc_silu_mul(gu.data(), act.data(), I, T);
+      ys = dense(act, L.sdn, H, I);
+    }
+    // routed experts: the token rows' qa8 form through perm; SwiGLU of the bf16 product; its rows' qa8 form
+    std::vector<int> off(E + 1), perm(R), inv(R);
+    orc_moe_dispatch(idx.data(), R, E, off.data(), perm.data(), inv.data());
+    std::vector<int8_t> U((size_t)R * std::max(H, I));
+    std::vector<float> XS((size_t)R * (std::max(H, I) / 64) * 2), y1((size_t)R * 2 * I), y2((size_t)R * H);
+    orc_a8_quant(xn.data(), H, T, H, 2, U.data(), XS.data());
+    orc_moe_gather_w4a8(U.data(), XS.data(), perm.data(), k, off.data(), L.egu.wq.data(), L.egu.s.data(),
+                        L.egu.b.data(), E, 2 * I, H, y1.data(), 0);
+    std::vector<uint16_t> egu(y1.size()), eact((size_t)R * I), edn(y2.size());
+    for (size_t i = 0; i < y1.size(); i++) egu[i] = f2bf(y1[i]);
+    orc_silu_mul(egu.data(), eact.data(), I, R);
+    orc_a8_quant(eact.data(), I, R, I, 2, U.data(), XS.data());
+    orc_moe_gather_w4a8(U.data(), XS.data(), nullptr, 1, off.data(), L.edn.wq.data(), L.edn.s.data(), L.edn.b.data(),
+                        E, H, I, y2.data(), 0);
+    for (size_t i = 0; i < y2.size(); i++) edn[i] = f2bf(y2[i]);
+    std::vector<uint16_t> want = x0;
+    orc_moe_combine(want.data(), edn.data(), wt.data(), has_shared ? ys.data() : nullptr, sg.data(), inv.data(), T, H,
+                    k, 0);
+    std::vector<float> wf(want.size());
+    for (size_t i = 0; i < want.size(); i++) wf[i] = bf2f(want[i]);
+    (void)bf16_err(x1, wf, true);
+    report(g_rel_rms <= 1e-2 && g_raw <= 5e-2 && g_ulp1 <= 0.05, "encode_moe x += moe(xn) (QA8, end to end)" + tag,
+           g_raw);
+  }
+  unsetenv("QA8");
+}
+
 // encode_moe with 8-bit routed experts on the sorted route (MLX-layout stacks, the reference's mlx_gqmm_b8 through
 // gqmm at W.bits, qwen35.h:1835): x += MoE(xn) against the composition of the oracle's 8-bit qmm per routed row
 // (gathered GEMM = each row's own expert product), SwiGLU, the shared expert's 4-bit qmm and the weighted combine.
@@ -955,6 +1086,7 @@ int main(int argc, char** argv) {
   test_encode_moe(rng);
   test_encode_moe_t64(rng);
   test_encode_moe_8bit_sorted(rng);
+  test_qa8(rng);
   printf(failures ? "%d FAILED\n" : "ALL OK\n", failures);
   return failures ? 1 : 0;
 }
