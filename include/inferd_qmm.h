@@ -367,6 +367,21 @@ int ifd_moe_decode_logits_ex(const float* logits_in, const void* xn, int T, int 
                              void* out, int assign, int* idx, float* wt, float* sg, void* workspace, size_t ws_bytes,
                              void* stream);
 
+/* The reference's per-row expert products below moe_sort_min routed rows when the four-launch route does not apply
+ * (moe_qmv4 on the gate/up and down stacks, moe_silu_mul, moe_combine: moe.metal:6-58, 103-111, 115-128; host
+ * qwen35.h:1947-1955), on the caller's routing: idx / wt [T][k] and sg [T] from ifd_moe_route, and the shared expert's
+ * output rows ys [T][H] (bf16; NULL: none) that the caller computed as the reference does, through gemm()
+ * (qwen35.h:1909-1914). The decode MoE's kernels with the router and routing left out: each distinct expert's weights
+ * read once per 16 tokens, the decode GEMV arithmetic (qmv4) for every routed product, SwiGLU of the bf16 gate and up,
+ * then out = bf16(acc) (assign) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] d_j + sg[t] ys[t] in fp32 (pick
+ * order, shared last). Any T: 16 tokens per launch group, each token's result depends on its own row only. idx values
+ * must lie in [0, E). Shapes as ifd_moe_decode. Workspace: ifd_moe_rows_workspace. */
+size_t ifd_moe_rows_workspace(int T, int H, int I, int E, int k);
+int ifd_moe_rows(const void* xn, int T, int H, int E, int k, const int* idx, const float* wt, const float* sg,
+                 const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
+                 const uint16_t* edn_s, const uint16_t* edn_b, int I, const void* ys, void* out, int assign,
+                 void* workspace, size_t ws_bytes, void* stream);
+
 /* ---- measurement probes (outside the operator path) ----------------------------------------------------------
  * The HBM and MFMA ceilings a benchmark reports beside the datasheet peaks, in the role of the reference's
  * micro-benchmarks (bw_read, micro/kernels.metal:8-16; fma_rate, micro/fma_rate.mm).

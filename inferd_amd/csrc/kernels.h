@@ -179,6 +179,8 @@ struct MdecCall {
   float* logits;
   const float* logits_in;  // non-null: routing starts from these fp32 logits [T][E1] (router unused)
   int sh_bits = 4;         // the shared expert's width, 4 or 8
+  int routed = 0;          // idx / wt / sg hold the caller's routing (router and logits unused); any T
+  const void* ys = nullptr;  // with routed: the shared expert's output rows [T][H] (bf16) for the combine, or null
 };
 struct MdecLayout {
   size_t part, plan, act, d, idx, wt, sg, total;

@@ -68,6 +68,8 @@ struct MdecArgs {
   unsigned* cnt;           // H / 128 counters, zero between calls
   int sb16_gu, sb16_dn;    // a wave's 8 scales (biases) of a row are one aligned 16 B load
   int sh_bits;             // the shared expert's width: 4, or 8 (the reference's moe_gu2_4_8 / moe_dn2_4_8)
+  int routed;              // idx / wt / sg hold the caller's routing (no router, no routing here)
+  const uint16_t* ys;      // with routed: the shared expert's output rows [T][H] for the combine, or null
 };
 
 // The 8 bf16 values at v (16-byte aligned) as 8 raw halves.
@@ -91,6 +93,11 @@ __device__ __forceinline__ void mdec_plan_block(const MdecArgs& p) {
   for (int i = tid; i < p.E; i += NTHR) firstpick[i] = 0x7fffffff;
   const __amdgpu_buffer_rsrc_t rp = part_rsrc(p.part, (uint32_t)((size_t)p.KS * T * p.E1 * 4));
   for (int t = wave; t < T; t += NTHR / 64) {
+    if (p.routed) {  // the caller's routing
+      if (lane == 0)
+        for (int jj = 0; jj < k; jj++) tidx[t * k + jj] = p.idx[t * k + jj];
+      continue;
+    }
     // token t's logits: every load issued before the first add
     float part[kMdecMaxKS][9];
 #pragma unroll
@@ -473,7 +480,7 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   __syncthreads();
   if (!s_last) return;
   // the chunk's combine: every (token, column) of its 128 columns
-  const int nj = k + (p.sgu_wq ? 1 : 0);
+  const int nj = k + (p.sgu_wq || p.ys ? 1 : 0);
   for (int i = tid; i < T * 128; i += 256) {
     const int t = i >> 7, hc = blockIdx.x * 128 + (i & 127);
     // every slot's value and weight requested before the first is used, then summed in slot order
@@ -482,7 +489,9 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
 #pragma unroll
     for (int jj = 0; jj <= kMdecMaxK; jj++)
       if (jj < nj) {
-        dv[jj] = __builtin_amdgcn_raw_buffer_load_b16(rd, (int)((((size_t)t * (k + 1) + jj) * H + hc) * 2), 0, kSc1);
+        dv[jj] = jj == k && p.ys ? p.ys[(size_t)t * H + hc]
+                                 : __builtin_amdgcn_raw_buffer_load_b16(
+                                       rd, (int)((((size_t)t * (k + 1) + jj) * H + hc) * 2), 0, kSc1);
         wv[jj] = jj < k ? p.wt[t * k + jj] : p.sg[t];
       }
     float a = 0.f;
@@ -522,7 +531,7 @@ MdecLayout mdec_layout(int T, int H, int I, int E, int k) {
 template <int RT>
 static int launch_mdec(const MdecArgs& p, const MdecCall& c, hipStream_t st) {
   const int slots = c.T * c.k + 1;
-  if (c.logits_in) hipLaunchKernelGGL(k_mdec_plan, dim3(1), dim3(512), 0, st, p);
+  if (c.logits_in || c.routed) hipLaunchKernelGGL(k_mdec_plan, dim3(1), dim3(512), 0, st, p);
   else hipLaunchKernelGGL(k_mdec_router<RT>, dim3((p.E1 + 31) / 32, p.KS), dim3(512), 0, st, p);
   IFD_TRY(check_launch("moe_decode router"));
   // up to 16 tokens the staged rows can take more than the default 64 KB of dynamic LDS
@@ -551,6 +560,20 @@ static int launch_mdec(const MdecArgs& p, const MdecCall& c, hipStream_t st) {
 
 int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
   if (c.T == 0) return IFD_OK;
+  if (c.routed && c.T > kMdecMaxT) {
+    // the caller's routing: every token's result depends on its own row only, so the launches take 16 tokens at a
+    // time on the one workspace (stream-ordered)
+    for (int t0 = 0; t0 < c.T; t0 += kMdecMaxT) {
+      MdecCall cc = c;
+      cc.T = std::min(kMdecMaxT, c.T - t0);
+      cc.xn = (const uint16_t*)c.xn + (size_t)t0 * c.H;
+      cc.out = (uint16_t*)c.out + (size_t)t0 * c.H;
+      cc.idx = c.idx + (size_t)t0 * c.k, cc.wt = c.wt + (size_t)t0 * c.k, cc.sg = c.sg ? c.sg + t0 : nullptr;
+      cc.ys = c.ys ? (const uint16_t*)c.ys + (size_t)t0 * c.H : nullptr;
+      IFD_TRY(launch_moe_decode(cc, cnt, ws, ws_bytes, st));
+    }
+    return IFD_OK;
+  }
   if (c.T > kMdecMaxT) return fail(IFD_ERR_UNSUPPORTED, "moe_decode takes at most %d tokens", kMdecMaxT);
   const MdecLayout L = mdec_layout(c.T, c.H, c.I, c.E, c.k);
   if (!ws || ws_bytes < L.total || !cnt)
@@ -567,6 +590,7 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
   p.sgu_wq = c.sgu_wq, p.sgu_s = c.sgu_s, p.sgu_b = c.sgu_b;
   p.sdn_wq = c.sdn_wq, p.sdn_s = c.sdn_s, p.sdn_b = c.sdn_b;
   p.sh_bits = c.sh_bits;
+  p.routed = c.routed, p.ys = (const uint16_t*)c.ys;
   p.out = (uint16_t*)c.out;
   p.idx = c.idx ? c.idx : (int*)(w + L.idx);
   p.wt = c.wt ? c.wt : (float*)(w + L.wt);

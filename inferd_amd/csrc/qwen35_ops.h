@@ -401,9 +401,12 @@ struct Qwen35 {
     ok(ifd_silu_mul(gu.ptr<void>(), act.ptr<void>(), I, rows, e.stream), "silu_mul_for");
   }
 
-  // The MoE route encode_moe takes for T tokens: the decode launches (the reference's moe2 up to 8 tokens,
-  // qwen35.h:1823-1829, and its per-row expert products below moe_sort_min routed rows, :1947-1955: the same per-row
-  // arithmetic), else rows sorted by expert.
+  // The MoE routes encode_moe takes for T tokens (qwen35.h:1876, 1947, 1956): the four decode launches (the
+  // reference's moe2, :1823-1829: up to min(MOE_V2, 8) tokens with an 8-bit router; here also up to qmv_max tokens
+  // with any router, where the per-row route computes the same values: its shared expert goes through gemm()'s
+  // decode GEMV at those rows); below moe_sort_min routed rows otherwise the per-row expert products
+  // (moe_rows_route); else rows sorted by expert.
+  int moe_v2 = env_int("MOE_V2", 8);
   bool moe_decode_route(const Layer& ly, int T) const {
     const int H = cfg.hidden, E = cfg.experts, k = cfg.topk, I = cfg.moe_inter;
     const int E1 = ly.router.E * ly.router.N;
@@ -415,8 +418,16 @@ struct Qwen35 {
                                              !ly.gate_up.flipped && !ly.down.flipped && !ly.gate_up.ldk &&
                                              !ly.down.ldk);
     // 4-bit routed experts (moe_gu2 / moe_dn2 are built for EB = 4 only, moe.metal:465-548)
-    return (T <= 8 || (T <= 16 && T * k < moe_sort_min)) && k <= 16 && E <= 512 && H % 512 == 0 && I % 64 == 0 &&
-           E1 <= E + 1 && shared_fits && ly.egu.bits == 4 && ly.edown.bits == 4;
+    return (T <= qmv_max || (T <= std::min(moe_v2, 8) && ly.router.bits == 8)) && k <= 16 && E <= 512 &&
+           H % 512 == 0 && I % 64 == 0 && E1 <= E + 1 && shared_fits && ly.egu.bits == 4 && ly.edown.bits == 4;
+  }
+  // The reference's per-row expert products (moe_qmv4 + moe_silu_mul + moe_combine, qwen35.h:1947-1955) on
+  // ifd_moe_rows, with the shared expert through gemm() (:1909-1914): any T below moe_sort_min routed rows that the
+  // decode launches do not take, 4-bit routed experts of the decode kernels' shapes.
+  bool moe_rows_route(const Layer& ly, int T) const {
+    const int H = cfg.hidden, E = cfg.experts, k = cfg.topk, I = cfg.moe_inter;
+    return !moe_decode_route(ly, T) && T * k < moe_sort_min && k <= 16 && E <= 512 && H % 512 == 0 && I % 64 == 0 &&
+           ly.egu.bits == 4 && ly.edown.bits == 4;
   }
 
   // The sorted route on the experts' T64 stacks (ifd_moe_gather_qmm_t64: the same bf16(s q + b) dequant and fp32 sums
@@ -513,9 +524,9 @@ struct Qwen35 {
     }
     // shared expert -> sh_out (its gate/up may read the norm's int8 rows; the SwiGLU feeds the down GEMM in bf16,
     // qwen35.h:1910-1914), unless it runs as expert E of the T64 launches
-    const bool q8 = qa8g_route(ly, T);
+    const bool rows = moe_rows_route(ly, T), q8 = !rows && qa8g_route(ly, T);
     if (q8 && !q8u.buf) die("encode_moe", "the MoE's QA8 route needs its int8 staging: construct with QA8=1");
-    const bool t64 = !q8 && moe_t64_route(ly), fold = !q8 && shared_as_expert(ly, T);
+    const bool t64 = !rows && !q8 && moe_t64_route(ly), fold = t64 && shared_as_expert(ly, T);
     const bool shared = has_shared && !fold;
     if (shared) {
       gemm_swiglu(e, xn, ly.gate_up, act, T);
@@ -531,6 +542,17 @@ struct Qwen35 {
     ok(ifd_moe_route(rlog.ptr<void>(), lbf, T, E, k, E1, 1, E1 > E ? 1 : 0, ridx.ptr<int>(), rw.ptr<float>(),
                      rsg.ptr<float>(), e.stream),
        "encode_moe");
+    if (rows) {  // a few routed rows: one decode-GEMV product per (token, expert) row, the shared rows in the combine
+      const size_t need = ifd_moe_rows_workspace(T, H, I, E, k);
+      if (need > splitk_bytes) die("encode_moe", "scratch smaller than the per-row MoE needs");
+      ok(ifd_moe_rows(xn.ptr<void>(), T, H, E, k, ridx.ptr<int>(), rw.ptr<float>(), rsg.ptr<float>(),
+                      ly.egu.wq.ptr<uint32_t>(), ly.egu.s.ptr<uint16_t>(), ly.egu.b.ptr<uint16_t>(),
+                      ly.edown.wq.ptr<uint32_t>(), ly.edown.s.ptr<uint16_t>(), ly.edown.b.ptr<uint16_t>(), I,
+                      shared ? sh_out.ptr<void>() : nullptr, x.ptr<void>(), 0, splitk.ptr<void>(), splitk_bytes,
+                      e.stream),
+         "encode_moe");
+      return;
+    }
     if (t64) {
       // routed experts on their T64 stacks, rows sorted by expert in tiles of tr rows; with `fold`, tokens 0..T-1
       // follow as expert E's segment (the shared expert) and its output rows R..R+T-1 are the combine's ys

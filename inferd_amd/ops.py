@@ -411,6 +411,26 @@ def moe_ffn(xn: torch.Tensor, router: torch.Tensor, egu: MoeW, edn: MoeW, k: int
     return out, idx, wt, sg
 
 
+def moe_rows(xn: torch.Tensor, idx: torch.Tensor, wt: torch.Tensor, sg: Optional[torch.Tensor], egu: MoeW,
+             edn: MoeW, ys: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+             assign: bool = True) -> torch.Tensor:
+    """The per-row expert products on the caller's routing (ifd_moe_rows; reference moe_qmv4 + moe_silu_mul +
+    moe_combine below 128 routed rows): idx int32 / wt fp32 [T, k], sg fp32 [T] and the shared expert's output rows
+    ys bf16 [T, H] (or None). Any T. out = bf16(acc) (assign) or out += bf16(acc)."""
+    T, H = xn.shape
+    k = idx.shape[1]
+    E, I = egu.E, egu.N // 2
+    assert idx.dtype == torch.int32 and wt.dtype == torch.float32 and idx.is_contiguous() and wt.is_contiguous()
+    assert ys is None or (ys.dtype == torch.bfloat16 and ys.shape == (T, H) and ys.is_contiguous() and sg is not None)
+    if out is None:
+        out = torch.zeros((T, H), dtype=torch.bfloat16, device=xn.device)
+    ws = workspace(lib().ifd_moe_rows_workspace(T, H, I, E, k), xn.device)
+    check(lib().ifd_moe_rows(_p(xn), T, H, E, k, _p(idx), _p(wt), _p(sg), _p(egu.wq), _p(egu.s), _p(egu.b),
+                             _p(edn.wq), _p(edn.s), _p(edn.b), I, _p(ys), _p(out), 1 if assign else 0, _p(ws),
+                             ws.numel(), _stream()))
+    return out
+
+
 def moe_decode(xn: torch.Tensor, router: Optional[torch.Tensor], egu: MoeW, edn: MoeW, k: int,
                shared: Optional[tuple] = None, shared_gate: bool = True, norm: bool = True,
                out: Optional[torch.Tensor] = None, assign: bool = True, logits_in: Optional[torch.Tensor] = None):

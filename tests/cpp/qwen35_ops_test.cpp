@@ -588,10 +588,11 @@ void test_encode_moe(std::mt19937& rng) {
     int T, max_rows;
     bool t64, r8, s8 = false;
   };
-  // the decode route up to 8 tokens and below 128 routed rows (T = 16 at top-4), the sorted route beyond; the
-  // fused T64 shared gate/up; state allocated for more rows than the call (its scratch covers every row count); the
-  // 8-bit router on both routes
-  for (const Case cs : {Case{3, 3, false, false}, Case{8, 8, false, false}, Case{16, 16, false, false},
+  // the decode route (up to qmv_max tokens; up to 8 with the 8-bit router), the per-row route below 128 routed rows
+  // (T <= 31 at top-4, 16 tokens per launch group), the sorted route beyond; the fused T64 shared gate/up; state
+  // allocated for more rows than the call (its scratch covers every row count); the 8-bit router on all three
+  for (const Case cs : {Case{1, 1, false, false}, Case{24, 24, false, false}, Case{31, 40, false, true},
+                        Case{3, 3, false, false}, Case{8, 8, false, false}, Case{16, 16, false, false},
                         Case{100, 100, false, false}, Case{16, 16, true, false}, Case{100, 100, true, false},
                         Case{100, 256, true, false}, Case{3, 3, false, true}, Case{12, 12, false, true},
                         Case{40, 40, false, true}, Case{3, 3, false, false, true}, Case{8, 8, false, true, true}}) {
@@ -611,11 +612,15 @@ void test_encode_moe(std::mt19937& rng) {
     const auto idx = download<int>(m.ridx, (size_t)T * k);
     const auto wt = download<float>(m.rw, (size_t)T * k);
     const auto sg = download<float>(m.rsg, (size_t)T);
-    const bool dec = m.moe_decode_route(ly, T);
+    const bool dec = m.moe_decode_route(ly, T), rows = m.moe_rows_route(ly, T);
     const std::string tag = " T=" + std::to_string(T) + (cs.max_rows > T ? " of " + std::to_string(cs.max_rows) : "") +
                             (ly.gate_up.t64 ? " (T64 shared gate/up)" : "") + (cs.r8 ? " (8-bit router)" : "") +
                             (cs.s8 ? " (8-bit shared expert)" : "") +
-                            (dec ? " [decode]" : " [sorted]");
+                            (dec ? " [decode]" : rows ? " [per-row]" : " [sorted]");
+    // the reference's routes: moe2 up to 8 tokens with an 8-bit router (and here up to qmv_max tokens with any),
+    // the per-row products below 128 routed rows, the sorted path from there
+    report(dec == (T <= m.qmv_max || (T <= 8 && cs.r8)) && rows == (!dec && T * k < 128),
+           "encode_moe route" + tag, 0);
     if (cs.r8) {  // the logits against the oracle's qmv8 on the GPU's normalised rows
       std::vector<float> yl((size_t)T * (E + 1));
       orc_qmv_b(xn.data(), H, r8wq.data(), r8s.data(), r8b.data(), E + 1, H, 8, 0, yl.data(), T, 0);
@@ -641,12 +646,14 @@ void test_encode_moe(std::mt19937& rng) {
     report(ri == idx && ew <= 1e-5, "encode_moe routing (indices bit-exact)" + tag, ew);
     // the block's output added into x, from the GPU's normalised rows and routing
     std::vector<uint16_t> want = x0;
-    if (cs.s8) {  // on the decode route only
-      report(dec, "encode_moe takes the decode route with an 8-bit shared expert" + tag, 0);
+    // the per-row route's shared expert goes through gemm(): the decode GEMV arithmetic at these rows (up to 32 on
+    // the MLX layout, 16 on T64), as on the decode route
+    if (cs.s8) {  // the decode or the per-row route
+      report(dec || rows, "encode_moe takes the decode or per-row route with an 8-bit shared expert" + tag, 0);
       orc_moe_decode_b(xn.data(), T, H, I, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
                        egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu8.wq.data(), sgu8.s.data(),
                        sgu8.b.data(), sdn8.wq.data(), sdn8.s.data(), sdn8.b.data(), 8, want.data(), 0);
-    } else if (dec)  // the decode MoE route: the decode GEMV arithmetic for every expert product
+    } else if (dec || rows)  // the decode GEMV arithmetic for every expert product
       orc_moe_decode(xn.data(), T, H, I, k, ri.data(), rwt.data(), rsg.data(), egu.wq.data(), egu.s.data(),
                      egu.b.data(), edn.wq.data(), edn.s.data(), edn.b.data(), sgu.wq.data(), sgu.s.data(),
                      sgu.b.data(), sdn.wq.data(), sdn.s.data(), sdn.b.data(), want.data(), 0);

@@ -274,6 +274,47 @@ def test_moe_decode_baseline_geometry(T):
     _decode_case(T, 512, 2048, 512, 10, True, True, seed=120 + T)
 
 
+@pytest.mark.parametrize("T,k,shared", [(3, 10, True), (12, 10, True), (17, 4, True), (31, 4, True), (40, 2, False),
+                                          (100, 1, True)])
+def test_moe_rows(T, k, shared):
+    """The per-row expert products on the caller's routing (reference moe_qmv4 + moe_silu_mul + moe_combine, the route
+    below 128 routed rows where the four-launch path does not apply), with the shared expert's rows given: 16 tokens
+    per launch group, so T = 17 .. 100 cross group edges. Against the oracle's per-token decode arithmetic (the
+    routed products in qmv4 form) with the same shared rows, assign and residual."""
+    g, ops = _gu(), _ops()
+    E, H, I, seed = 64, 1024, 256, 400 + T
+    egu, edn = experts(E, 2 * I, H, seed=seed), experts(E, H, I, seed=seed + 1)
+    rng = np.random.default_rng(seed)
+    xn = gen.activations(T, H, seed=seed + 2)
+    x0 = gen.activations(T, H, seed=seed + 3)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    wt = rng.random((T, k)).astype(np.float32)
+    wt /= wt.sum(axis=1, keepdims=True)
+    sg = rng.random(T).astype(np.float32) if shared else np.ones(T, np.float32)
+    ys = gen.activations(T, H, seed=seed + 4) if shared else None
+    W1, W2 = g.moew(*egu), g.moew(*edn)
+    d = np.empty((T * k, H), np.uint16)
+    for t in range(T):
+        for j in range(k):
+            e = idx[t, j]
+            gu = gen.f32_to_bf16(orc.qmv(xn[t:t + 1], egu[0][e], egu[1][e], egu[2][e]))
+            a = orc.silu_mul(gu)
+            d[t * k + j] = gen.f32_to_bf16(orc.qmv(a, edn[0][e], edn[1][e], edn[2][e]))[0]
+    ident = np.arange(T * k, dtype=np.int32)
+    ref_rows = {asg: orc.moe_combine(x0, d, wt, ys, sg, ident, k, asg) for asg in (True, False)}
+    for assign in (True, False):
+        out = ops.moe_rows(g.dev(xn), g.dev(idx), g.dev(wt), g.dev(sg), W1, W2, g.dev(ys) if shared else None,
+                           out=g.dev(x0), assign=assign)
+        again = ops.moe_rows(g.dev(xn), g.dev(idx), g.dev(wt), g.dev(sg), W1, W2, g.dev(ys) if shared else None,
+                             out=g.dev(x0), assign=assign)
+        torch.cuda.synchronize()
+        assert np.array_equal(g.host(out), g.host(again))
+        # the oracle: each routed row (t, j) in the decode arithmetic, bf16 d_j, then the weighted combine with the
+        # given shared rows (moe.metal:115-128), rows in (t, j) order
+        gen.check_bf16(g.host(out), ref_rows[assign], 1e-2, (T, k, shared, assign), ref_is_bf16=True,
+                       composition=True)
+
+
 @pytest.mark.parametrize("T", [1, 4, 8, 12, 16])
 def test_moe_decode_8bit_shared_expert(T):
     """An 8-bit shared expert beside the 4-bit routed experts (the reference's moe_gu2_4_8 / moe_dn2_4_8,
