@@ -484,9 +484,8 @@ struct Qwen35 {
            "encode_moe");
       }
     };
-    // the decode MoE (the reference's moe2 route up to 8 tokens, and its per-row expert products below moe_sort_min
-    // routed rows), each distinct expert read once; it needs the shared expert (if any) unflipped 4-bit with the
-    // routed experts' intermediate size
+    // the decode MoE (the reference's moe2 route), each distinct expert read once; it needs the shared expert (if
+    // any) unflipped, 4- or 8-bit, with the routed experts' intermediate size
     if (moe_decode_route(ly, T)) {
       a8_ready = false;  // the norm's int8 rows (if it made them) are not the next GEMM's input (qwen35.h:1906)
       const size_t need = ifd_moe_decode_workspace(T, H, I, E, k);
