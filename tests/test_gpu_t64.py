@@ -279,6 +279,11 @@ def test_gemm_t64_multi_repeats_and_matches_single_calls():
     assert all(np.array_equal(a, b) for r in runs[1:] for a, b in zip(runs[0], r))
     for T, out in zip(Ts, runs[0]):
         gen.check_bf16(out, gen.bf16_to_f32(g.host(ops.gemm_t64(A, T))), 1e-2, "multi vs single")
+    # one linear whose width is whole 128-column blocks: the same plan and sums as the single call, bit for bit
+    for M in (1, 7, 16):
+        Am = g.dev(gen.activations(M, K, seed=92 + M))
+        one = g.host(ops.gemm_t64_multi(Am, Ts[:1])[0])
+        assert np.array_equal(one, g.host(ops.gemm_t64(Am, Ts[0]))), M
 
 
 @pytest.mark.parametrize("M,N,K,mode", [
