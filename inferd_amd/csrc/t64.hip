@@ -303,10 +303,11 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
       if (cl >= Nl) continue;
       const float4 v = sum4((size_t)row * p.N + c);
       const size_t o = (size_t)row * ldcl + cl;
+      // a linear of the multi-linear launch may end inside the quad (its N need not be a multiple of 4)
       store_mode(Cl, o, v.x, p.mode);
-      store_mode(Cl, o + 1, v.y, p.mode);
-      store_mode(Cl, o + 2, v.z, p.mode);
-      store_mode(Cl, o + 3, v.w, p.mode);
+      if (cl + 1 < Nl) store_mode(Cl, o + 1, v.y, p.mode);
+      if (cl + 2 < Nl) store_mode(Cl, o + 2, v.z, p.mode);
+      if (cl + 3 < Nl) store_mode(Cl, o + 3, v.w, p.mode);
     } else {
       const int I = p.N / 2, c = tile * 128 + c4;
       const float4 g = sum4((size_t)row * p.N + c), u = sum4((size_t)row * p.N + I + c);

@@ -229,13 +229,13 @@ def _multi_linears(Ns, K, seed):
 
 @pytest.mark.parametrize("M", [1, 8, 9, 16])
 def test_gemm_t64_multi_matches_oracle(M):
-    """Several linears sharing A in one decode launch (the attention projections' q/k/v/o widths, a 200-wide tail and
-    a 96-wide one that pads its block with dead bands): each output against the oracle, over a K split planned for
-    their concatenated width (in-kernel fixup)."""
+    """Several linears sharing A in one decode launch (the attention projections' q/k/v/o widths, and 198- and
+    97-wide ones that end inside a band and a 4-column quad, padding their blocks with dead bands): each output
+    against the oracle, over a K split planned for their concatenated width (in-kernel fixup)."""
     import ctypes
     from inferd_amd._lib import lib
     g, ops = _gu(), _ops()
-    Ns, K = [5120, 1024, 200, 4096, 96], 5120
+    Ns, K = [5120, 1024, 198, 4096, 97], 5120
     assert lib().ifd_gemm_t64_multi_workspace(M, len(Ns), (ctypes.c_int * len(Ns))(*Ns), K) > 0
     ws, Ts = _multi_linears(Ns, K, 40 + M)
     A = gen.activations(M, K, seed=M + 41)
