@@ -374,8 +374,9 @@ int ifd_moe_decode_logits_ex(const float* logits_in, const void* xn, int T, int 
  * (qwen35.h:1909-1914). The decode MoE's kernels with the router and routing left out: each distinct expert's weights
  * read once per 16 tokens, the decode GEMV arithmetic (qmv4) for every routed product, SwiGLU of the bf16 gate and up,
  * then out = bf16(acc) (assign) or bf16(out + bf16(acc)), acc = sum_j wt[t][j] d_j + sg[t] ys[t] in fp32 (pick
- * order, shared last). Any T: 16 tokens per launch group, each token's result depends on its own row only. idx values
- * must lie in [0, E). Shapes as ifd_moe_decode. Workspace: ifd_moe_rows_workspace. */
+ * order, shared last). Any T: 16 tokens per launch group, each token's result depends on its own row only. A row of
+ * idx holds k distinct experts in [0, E), as ifd_moe_route writes it. Shapes as ifd_moe_decode. Workspace:
+ * ifd_moe_rows_workspace. */
 size_t ifd_moe_rows_workspace(int T, int H, int I, int E, int k);
 int ifd_moe_rows(const void* xn, int T, int H, int E, int k, const int* idx, const float* wt, const float* sg,
                  const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
