@@ -207,3 +207,21 @@ def test_multi_linear_gemv_checks():
     assert call() == _lib.IFD_ERR_WORKSPACE
     assert call(ws=None, wsb=need) == _lib.IFD_ERR_WORKSPACE
     assert call(M=0) == _lib.IFD_OK
+
+
+def test_moe_rows_checks():
+    """The per-row MoE on the caller's routing: the decode kernels' shapes (H multiple of 512, I of 64, E <= 512,
+    k <= 16), the routing arrays, and the shared rows' gate weights; any T, with one workspace size from 16 tokens
+    up. All before any GPU work."""
+    L = _lib.lib()
+    E = _lib.IFD_ERR_ARG
+    assert L.ifd_moe_rows_workspace(16, 2048, 512, 512, 10) == L.ifd_moe_decode_workspace(16, 2048, 512, 512, 10) > 0
+    assert L.ifd_moe_rows_workspace(300, 2048, 512, 512, 10) == L.ifd_moe_rows_workspace(16, 2048, 512, 512, 10)
+    call = lambda T=20, H=2048, Ex=512, k=10, idx=4096, sg=4096, I=512, ys=4096: L.ifd_moe_rows(
+        4096, T, H, Ex, k, idx, 4096, sg, 4096, 4096, 4096, 4096, 4096, 4096, I, ys, 4096, 0, 4096, 0, None)
+    assert call(H=1280) == E and b"H multiple of 512" in L.ifd_last_error()
+    assert call(Ex=513) == E and call(k=17) == E and call(I=100) == E
+    assert call(idx=None) == E and b"null" in L.ifd_last_error()
+    assert call(sg=None) == E and b"gate weights" in L.ifd_last_error()
+    assert call(T=0) == _lib.IFD_OK
+    assert call() == _lib.IFD_ERR_WORKSPACE  # no workspace past the header
