@@ -143,8 +143,9 @@ __global__ __launch_bounds__(256, 2) void k_qmv_t(QmvTArgs p) {
     for (int i = 0; i < kTB; i++) {
       const uint8_t* t = tcol + (size_t)(g + i) * gstride;
 #pragma unroll
-      for (int hh = 0; hh < NH; hh++) B.w[i][hh] = *(const u32x4*)(t + 1024 * hh + 16 * lane);
-      B.sb[i] = *(const uint32_t*)(t + CODES + 4 * j);
+      // streamed once: non-temporal loads (measured 2-3% faster on the gate_up and down shapes at M = 1)
+      for (int hh = 0; hh < NH; hh++) B.w[i][hh] = __builtin_nontemporal_load((const u32x4*)(t + 1024 * hh + 16 * lane));
+      B.sb[i] = __builtin_nontemporal_load((const uint32_t*)(t + CODES + 4 * j));
     }
   };
   Blk b0, b1;
