@@ -266,6 +266,7 @@ __device__ __forceinline__ int wave_min_i(int v) {
 // kernel: stores write through to memory, loads do not hit a stale line of the local L2. Plain loads batch, unlike
 // atomic loads, which the compiler orders one after another.
 constexpr int kSc1 = 16;  // cache-policy operand: SC1
+constexpr int kNt = 2;    // cache-policy operand: NT (non-temporal)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const void* part, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, (int)bytes, 0x00020000);
 }
