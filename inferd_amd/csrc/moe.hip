@@ -241,32 +241,17 @@ __global__ __launch_bounds__(256) void k_disp_count(const int* __restrict__ idx,
   for (int c = tid; c < E; c += 256) bcnt[(size_t)blockIdx.x * E + c] = cnt[c];
 }
 
-// shared_rows > 0 appends a segment for the shared expert as expert E: sorted rows [R, R + shared_rows) are tokens
-// 0, 1, ... in order (perm = t * kdiv), with their own tiles after the routed ones, and offsets[E + 1] = R +
-// shared_rows.
-__global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int nchunks, int E, int R, int tile_rows,
-                                                    int* __restrict__ offsets, int* __restrict__ tiles,
-                                                    int* __restrict__ ntiles, int shared_rows, int kdiv,
-                                                    int* __restrict__ perm) {
-  __shared__ int part[1024], tpart[1024];
+// The expert offsets and the tile schedule from each expert's row count `total` (thread e < 1024 holds expert e's;
+// zero past E), by the whole block of 1024 threads; returns expert e's offset. shared_rows > 0 appends a segment for
+// the shared expert as expert E: sorted rows [R, R + shared_rows) are tokens 0, 1, ... in order (perm = t * kdiv),
+// with their own tiles after the routed ones, and offsets[E + 1] = R + shared_rows.
+__device__ __forceinline__ int disp_schedule(int total, int E, int R, int tile_rows, int* __restrict__ offsets,
+                                             int* __restrict__ tiles, int* __restrict__ ntiles, int shared_rows,
+                                             int kdiv, int* __restrict__ perm, int* part, int* tpart) {
   const int e = threadIdx.x;
-  int total = 0;
-  // exclusive prefix of the chunk counts within the expert, 16 loads in flight
-  if (e < E)
-    for (int c0 = 0; c0 < nchunks; c0 += 16) {
-      int v[16];
-#pragma unroll
-      for (int u = 0; u < 16; u++) v[u] = c0 + u < nchunks ? bcnt[(size_t)(c0 + u) * E + e] : 0;
-#pragma unroll
-      for (int u = 0; u < 16; u++)
-        if (c0 + u < nchunks) {
-          bcnt[(size_t)(c0 + u) * E + e] = total;
-          total += v[u];
-        }
-    }
   const int nt = (total + tile_rows - 1) / tile_rows;
-  part[e] = e < E ? total : 0;
-  tpart[e] = e < E ? nt : 0;
+  part[e] = total;
+  tpart[e] = nt;
   __syncthreads();
   // inclusive Hillis-Steele scans over 1024 entries
   for (int o = 1; o < 1024; o <<= 1) {
@@ -276,9 +261,9 @@ __global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int 
     tpart[e] += b;
     __syncthreads();
   }
-  const int off = part[e] - (e < E ? total : 0), toff = tpart[e] - (e < E ? nt : 0);
+  const int off = part[e] - total, toff = tpart[e] - nt;
   if (e < E) {
-    offsets[e] = off;  // the scatter adds it to the chunk prefixes
+    offsets[e] = off;
     for (int i = 0; i < nt; i++) {
       tiles[2 * (toff + i)] = e;
       tiles[2 * (toff + i) + 1] = off + i * tile_rows;
@@ -295,6 +280,62 @@ __global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int 
     offsets[E] = R;
     if (shared_rows > 0) offsets[E + 1] = R + shared_rows;
     ntiles[0] = routed_tiles + nsh;
+  }
+  return off;
+}
+
+// Pass 2: per expert, the exclusive prefix of the chunk counts (written back over them), then the schedule.
+__global__ __launch_bounds__(1024) void k_disp_scan(int* __restrict__ bcnt, int nchunks, int E, int R, int tile_rows,
+                                                    int* __restrict__ offsets, int* __restrict__ tiles,
+                                                    int* __restrict__ ntiles, int shared_rows, int kdiv,
+                                                    int* __restrict__ perm) {
+  __shared__ int part[1024], tpart[1024];
+  const int e = threadIdx.x;
+  int total = 0;
+  // 16 loads in flight
+  if (e < E)
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+      int v[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) v[u] = c0 + u < nchunks ? bcnt[(size_t)(c0 + u) * E + e] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; u++)
+        if (c0 + u < nchunks) {
+          bcnt[(size_t)(c0 + u) * E + e] = total;
+          total += v[u];
+        }
+    }
+  (void)disp_schedule(total, E, R, tile_rows, offsets, tiles, ntiles, shared_rows, kdiv, perm, part, tpart);
+}
+
+// The three passes in one block for at most one chunk of rows (R <= kDispChunk): the chunk's ranks and counts, the
+// schedule (the chunk prefix is 0), then perm / inv, with every intermediate in LDS. Same results as the three
+// passes, in one launch instead of three.
+__global__ __launch_bounds__(1024) void k_disp_small(const int* __restrict__ idx, int R, int E, int tile_rows,
+                                                     int* __restrict__ offsets, int* __restrict__ perm,
+                                                     int* __restrict__ inv, int* __restrict__ tiles,
+                                                     int* __restrict__ ntiles, int shared_rows, int kdiv) {
+  __shared__ int ex[kDispChunk], cnt[1024], part[1024], tpart[1024];
+  const int tid = threadIdx.x;
+  cnt[tid] = 0;
+  // expert ids are clamped to [0, E) as in the chunk pass
+  const int er = tid < R ? min(max(idx[tid], 0), E - 1) : -1;
+  if (tid < kDispChunk) ex[tid] = er;
+  __syncthreads();
+  int rk = 0;
+  if (er >= 0) {
+    for (int i = 0; i < tid; i++) rk += ex[i] == er;
+    atomicAdd(&cnt[er], 1);
+  }
+  __syncthreads();
+  const int total = tid < E ? cnt[tid] : 0;
+  const int off = disp_schedule(total, E, R, tile_rows, offsets, tiles, ntiles, shared_rows, kdiv, perm, part, tpart);
+  cnt[tid] = off;  // each thread rewrites only its own entry, read above by itself alone
+  __syncthreads();
+  if (er >= 0) {
+    const int q = cnt[er] + rk;
+    perm[q] = tid;
+    inv[tid] = q;
   }
 }
 
@@ -322,6 +363,11 @@ int launch_moe_dispatch(const int* idx, int R, int E, int* offsets, int* perm, i
   const int nchunks = (R + kDispChunk - 1) / kDispChunk;
   if (moe_dispatch_workspace(R, E) > ws_bytes || !ws)
     return fail(IFD_ERR_WORKSPACE, "moe_dispatch needs %zu bytes of workspace", moe_dispatch_workspace(R, E));
+  if (R <= kDispChunk) {  // one chunk: the single-block form
+    hipLaunchKernelGGL(k_disp_small, dim3(1), dim3(1024), 0, st, idx, R, E, tile_rows, offsets, perm, inv, tiles, ntiles,
+                       shared_rows, kdiv);
+    return check_launch("moe_dispatch");
+  }
   int* bcnt = (int*)ws;
   int* rank = (int*)((char*)ws + align_up((size_t)nchunks * E * sizeof(int), 256));
   if (R > 0) {
