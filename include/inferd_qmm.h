@@ -296,18 +296,26 @@ int ifd_moe_dispatch_ex(const int* idx, int R, int E, int k, int tile_rows, int 
  * on average, else 32): the schedule a caller composing ifd_moe_dispatch_ex and ifd_moe_gather_qmm_t64 itself uses
  * to get the one-shot call's tiles. */
 int ifd_moe_t64_tile_rows(int R, int E);
-/* The gathered expert GEMM of ifd_moe_gather_qmm on T64 stacks (the same bits: bf16(s q + b) dequant, fp32 sums in
- * the same order): wt = E experts [E][N][K] packed by ifd_pack_t64, wt_shared (may be NULL) the shared expert [N][K]
- * taking the dispatch's expert-E segment; tiles / ntiles / offsets / tile_rows from ifd_moe_dispatch_ex; rows = the
- * sorted rows of C (ldc its row stride). silu: the stack holds [gate (N/2) | up (N/2)] and C receives the SwiGLU
- * [rows][N/2]. Output columns in whole 256-column tiles (N % 256 == 0, with silu N / 2 % 256 == 0), K % 128 == 0. */
+/* The gathered expert GEMM of ifd_moe_gather_qmm on T64 stacks (bf16(s q + b) dequant, fp32 sums): wt = E experts
+ * [E][N][K] packed by ifd_pack_t64, wt_shared (may be NULL) the shared expert [N][K] taking the dispatch's expert-E
+ * segment; tiles / ntiles / offsets / tile_rows from ifd_moe_dispatch_ex; rows = the sorted rows of C (ldc its row
+ * stride). silu: the stack holds [gate (N/2) | up (N/2)] and C receives the SwiGLU [rows][N/2]. Output columns in
+ * whole 256-column tiles (N % 256 == 0, with silu N / 2 % 256 == 0), K % 128 == 0.
+ * workspace NULL: each GPU block takes whole (row tile, 256-column tile) items, and the sums are those of
+ * ifd_moe_gather_qmm bit for bit. With a workspace (ifd_moe_gather_qmm_t64_workspace(tile_rows) bytes, counter header
+ * zeroed once): the balanced schedule, every block an equal share of the items' 64-group pairs, which takes no
+ * longer whatever the item count; an item split between blocks sums the fp32 sums of its K ranges in K order
+ * (deterministic, within fp32 rounding of the unsplit sum). No counterpart in the reference, whose gather_qmm has no
+ * work split of its own. */
+size_t ifd_moe_gather_qmm_t64_workspace(int tile_rows);
 int ifd_moe_gather_qmm_t64(const void* A, int lda, const int* perm, int div, const int* offsets, const int* tiles,
                            const int* ntiles, int tile_rows, const void* wt, const void* wt_shared, int E, int N, int K,
-                           int silu, void* C, int ldc, int rows, void* stream);
+                           int silu, void* C, int ldc, int rows, void* workspace, size_t ws_bytes, void* stream);
 /* One-shot MoE FFN on T64 stacks (reference encode_moe after rmsnorm_for, qwen35.h:1909-1980): router -> route ->
  * dispatch with the shared expert (sgu_t64 [2 I][H], sdn_t64 [H][I], the routed experts' I, or NULL) as expert E ->
- * gathered gate/up + SwiGLU -> gathered down -> combine; the same arithmetic as ifd_moe_ffn. H and I multiples of
- * 256. Workspace: ifd_moe_ffn_t64_workspace (shared: 1 with a shared expert). */
+ * gathered gate/up + SwiGLU -> gathered down (both on the balanced schedule of ifd_moe_gather_qmm_t64) -> combine;
+ * the arithmetic of ifd_moe_ffn. H and I multiples of 256. Workspace: ifd_moe_ffn_t64_workspace (shared: 1 with a
+ * shared expert). */
 size_t ifd_moe_ffn_t64_workspace(int T, int H, int I, int E, int k, int shared);
 int ifd_moe_ffn_t64(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
                     int logits_bf16, const void* egu_t64, const void* edn_t64, int I, const void* sgu_t64,

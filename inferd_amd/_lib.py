@@ -74,8 +74,9 @@ SIGNATURES = {
     "ifd_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "ifd_moe_dispatch_ex": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ifd_moe_t64_tile_rows": (_i, [_i, _i]),
+    "ifd_moe_gather_qmm_t64_workspace": (_sz, [_i]),
     "ifd_moe_gather_qmm_t64": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp, _i, _i,
-                                    _vp]),
+                                    _vp, _sz, _vp]),
     "ifd_moe_ffn_t64_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
     "ifd_moe_ffn_t64": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp,
                              _vp, _sz, _vp]),

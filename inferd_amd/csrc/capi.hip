@@ -555,17 +555,33 @@ int ifd_moe_dispatch_ex(const int* idx, int R, int E, int k, int tile_rows, int 
                              shared_rows, k);
 }
 
+size_t ifd_moe_gather_qmm_t64_workspace(int tile_rows) {
+  if (tile_rows != 32 && tile_rows != 64) return 0;
+  return with_header(moe_gather_t64_part_bytes(tile_rows));
+}
+
 int ifd_moe_gather_qmm_t64(const void* A, int lda, const int* perm, int div, const int* offsets, const int* tiles,
                            const int* ntiles, int tile_rows, const void* wt, const void* wt_shared, int E, int N, int K,
-                           int silu, void* C, int ldc, int rows, void* stream) {
+                           int silu, void* C, int ldc, int rows, void* workspace, size_t ws_bytes, void* stream) {
   IFD_CHECK(rows >= 0 && E > 0 && N > 0 && K > 0 && div > 0, "bad shape E=%d N=%d K=%d rows=%d", E, N, K, rows);
   IFD_CHECK(lda >= K && lda % 8 == 0 && ldc >= (silu ? N / 2 : N) && ldc % 8 == 0, "bad strides lda=%d ldc=%d", lda,
             ldc);
   IFD_CHECK(rows == 0 || (A && offsets && tiles && ntiles && wt && C), "null pointer");
   IFD_CHECK(rows == 0 || (aligned(A, 16) && aligned(wt, 16) && aligned(C, 16) && (!wt_shared || aligned(wt_shared, 16))),
             "A, C and the stacks must be 16-byte aligned");
+  float* part = nullptr;
+  size_t part_bytes = 0;
+  unsigned* cnt = nullptr;
+  if (workspace) {  // the balanced schedule
+    const WsView w = ws_view(workspace, ws_bytes);
+    if (ws_bytes < ifd_moe_gather_qmm_t64_workspace(tile_rows) || !aligned(workspace, 16))
+      return fail(IFD_ERR_WORKSPACE, "moe_gather_qmm_t64 needs %zu bytes of 16-byte aligned workspace, got %zu",
+                  ifd_moe_gather_qmm_t64_workspace(tile_rows), ws_bytes);
+    part = (float*)w.body, part_bytes = w.bytes, cnt = w.cnt;
+  }
   return launch_moe_gather_qmm_t64((const uint16_t*)A, lda, perm, div, tiles, ntiles, offsets, tile_rows, wt,
-                                   wt_shared, E, N, K, silu ? 1 : 0, (uint16_t*)C, ldc, rows, S(stream));
+                                   wt_shared, E, N, K, silu ? 1 : 0, (uint16_t*)C, ldc, rows, part, part_bytes, cnt,
+                                   S(stream));
 }
 
 namespace {
@@ -577,7 +593,7 @@ int ifd_moe_t64_tile_rows(int R, int E) { return moe_t64_tile_rows(std::max(R, 0
 
 namespace {
 struct MoeT64Layout {
-  size_t logits, idx, wt, sg, offsets, perm, inv, tiles, ntiles, disp, eact, ydn, total;
+  size_t logits, idx, wt, sg, offsets, perm, inv, tiles, ntiles, disp, eact, ydn, part, total;
 };
 MoeT64Layout moe_t64_layout(int T, int H, int I, int E, int k, int shared) {
   MoeT64Layout L{};
@@ -600,6 +616,7 @@ MoeT64Layout moe_t64_layout(int T, int H, int I, int E, int k, int shared) {
   L.disp = take(moe_dispatch_workspace(R, E));
   L.eact = take((size_t)Rt * I * 2);
   L.ydn = take((size_t)Rt * H * 2);
+  L.part = take(moe_gather_t64_part_bytes(moe_t64_tile_rows(R, E)));
   L.total = o;
   return L;
 }
@@ -648,10 +665,13 @@ int ifd_moe_ffn_t64(const void* xn, int T, int H, const void* router, int E, int
   IFD_TRY(launch_moe_route(w + L.logits, logits_bf16, T, E, k, E1, norm, shared_gate, ridx, rwt, rsg, st));
   IFD_TRY(launch_moe_dispatch(ridx, R, E, offsets, perm, inv, tiles, ntiles, w + L.disp, moe_dispatch_workspace(R, E),
                               st, tr, shared ? T : 0, k));
+  // the balanced schedule: the pieces in the workspace, the counters in its header
+  float* part = (float*)(w + L.part);
+  const size_t pb = moe_gather_t64_part_bytes(tr);
   IFD_TRY(launch_moe_gather_qmm_t64((const uint16_t*)xn, H, perm, k, tiles, ntiles, offsets, tr, egu_t64, sgu_t64, E,
-                                    2 * I, H, 1, eact, I, Rt, st));
+                                    2 * I, H, 1, eact, I, Rt, part, pb, wv.cnt, st));
   IFD_TRY(launch_moe_gather_qmm_t64(eact, I, nullptr, 1, tiles, ntiles, offsets, tr, edn_t64, sdn_t64, E, H, I, 0,
-                                    ydn, H, Rt, st));
+                                    ydn, H, Rt, part, pb, wv.cnt, st));
   // the shared expert's rows follow the routed ones in token order
   return launch_moe_combine((uint16_t*)out, ydn, rwt, shared ? ydn + (size_t)R * H : nullptr, rsg, inv, T, H, k,
                             assign, st);

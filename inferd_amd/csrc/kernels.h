@@ -149,10 +149,15 @@ int launch_moe_gather_qmm_a8(const int8_t* U, const float* XS, const int* perm, 
 int launch_moe_combine(uint16_t* out, const uint16_t* yd, const float* wt, const uint16_t* ys, const float* sg,
                        const int* inv, int T, int H, int k, int assign, hipStream_t st);
 // The gathered expert GEMM on T64 expert stacks (moe_t64.hip): the dispatch's tiles of tile_rows (32 or 64) rows,
-// the shared expert (wsh) as expert E, rows = sorted rows of C (ldc its row stride).
+// the shared expert (wsh) as expert E, rows = sorted rows of C (ldc its row stride). part (at least
+// moe_gather_t64_part_bytes(tile_rows) bytes) and cnt (the workspace's zeroed counter header): the balanced schedule,
+// whose cut items sum their K ranges' pieces in K order; part null: whole items per block (the same bits as
+// launch_moe_gather_qmm).
+size_t moe_gather_t64_part_bytes(int tile_rows);
 int launch_moe_gather_qmm_t64(const uint16_t* A, int lda, const int* perm, int div, const int* tiles,
                               const int* ntiles, const int* offsets, int tile_rows, const void* wt, const void* wsh,
-                              int E, int N, int K, int silu, uint16_t* C, int ldc, int rows, hipStream_t st);
+                              int E, int N, int K, int silu, uint16_t* C, int ldc, int rows, float* part,
+                              size_t part_bytes, unsigned* cnt, hipStream_t st);
 
 // Decode MoE for T <= 16 tokens (moe_dec.hip): router, routing + distinct-expert plan, gate/up + SwiGLU, down +
 // combine; the combine's counters are H / 128 uint32 of the workspace header.

@@ -6,8 +6,14 @@
 // Work items are (row tile, column tile) pairs: a row tile is up to BM = 32 MT sorted rows of one expert (the
 // dispatch's tile schedule), a column tile 8 bands (256 output columns; with SwiGLU 8 gate bands and the matching 8
 // up bands, 256 h columns). Items are numbered row tile-major, so an expert's column tiles are neighbours and share
-// its activation rows in L2. The grid is one block per CU; block b streams items [b n / nblk, (b + 1) n / nblk) as one
-// continuous sequence of (item, 64-group) steps, so the DMA pipeline runs across item boundaries without draining.
+// its activation rows in L2. The grid is one block per CU; a block streams a contiguous run of (item, group pair)
+// units as one continuous sequence of (item, 64-group) steps, so the DMA pipeline runs across item boundaries without
+// draining. Without a piece buffer a run is whole items, [b n / nblk, (b + 1) n / nblk). With one (the balanced
+// schedule) block b takes units [b U / nblk, (b + 1) U / nblk) of the U = n G / 2: every CU streams the same bytes
+// whatever n, and an item cut by a run boundary leaves each contributor's fp32 sums (its rows only) in a piece slot,
+// written through to memory. The contributors count themselves in a counter of the workspace header once their run
+// is done; the last one sums the item's pieces in unit order and stores the item as a whole item ends. A cut item's
+// sum is therefore the sum of its K ranges' sums, in K order, and does not depend on timing.
 //
 // Block: 8 waves; wave w owns band w of the column tile (with SwiGLU, its gate band and its up band) over all MT M
 // tiles. Two LDS rings filled by direct global -> LDS DMA: NA activation slabs [BM][64 bf16] (16-byte columns
@@ -22,6 +28,7 @@
 // At the end of an item a wave stages its bf16 outputs in its own LDS tile and writes them as 16-byte buffer
 // stores, rows past the segment at an out-of-range offset (dropped by the buffer bounds check).
 #include <algorithm>
+#include <cmath>
 
 #include "common.h"
 #include "dma.h"
@@ -50,7 +57,17 @@ struct GqArgs {
   uint16_t* C;
   uint32_t c_bytes;
   int ldc, nct_log2, nblk;
+  float* part;         // balanced schedule: piece slots [2 nblk][8 waves][NBW][MT][4][64] float4; null: whole items
+  uint32_t part_bytes;
+  unsigned* cnt;       // [nblk] counters of the cut items (zero between calls), by the block holding the first unit
 };
+
+// The balanced schedule runs when whole-item runs would make the longest run at least this many (item, group pair)
+// units longer than the even share (config 4: gate/up at T = 16 and 2048, 14.5 and 11.8 units; not down, nor gate/up
+// at T = 128, 2-5 units, where the cut items' sums cost more than they save).
+constexpr int kGqMinLoss = 8;
+// the block whose run of units holds unit u (runs [b U / nblk, (b + 1) U / nblk))
+__device__ __forceinline__ int gq_block_of(long u, int nblk, long U) { return (int)((u * nblk + nblk - 1) / U); }
 
 // bands per wave: two with SwiGLU (its gate and up band) or in the wide plain form (two 8-band column groups)
 __host__ __device__ constexpr int gq_nbw(bool two) { return two ? 2 : 1; }
@@ -59,9 +76,12 @@ __host__ __device__ constexpr int gq_wbytes(bool two) { return gq_nbw(two) * (8 
 constexpr int kGqStg = 32 * 64;  // a wave's staged output: one M tile [32][32] bf16
 __host__ __device__ constexpr int gq_na(int MT, bool two) { return two ? 4 : (MT == 2 ? 6 : 8); }
 __host__ __device__ constexpr int gq_nw(int MT, bool two) { return two ? (MT == 2 ? 6 : 7) : (MT == 2 ? 10 : 12); }
+// the rings, the waves' output tiles and one word for the cut items' arrival flag
 __host__ __device__ constexpr size_t gq_lds(int MT, bool two) {
-  return (size_t)gq_na(MT, two) * gq_abytes(MT) + (size_t)gq_nw(MT, two) * gq_wbytes(two) + 8 * kGqStg;
+  return (size_t)gq_na(MT, two) * gq_abytes(MT) + (size_t)gq_nw(MT, two) * gq_wbytes(two) + 8 * kGqStg + 16;
 }
+// bytes of one piece slot at 32 MT-row tiles (two bands per wave at most)
+__host__ __device__ constexpr size_t gq_slot_bytes(int MT) { return (size_t)8 * 2 * MT * 4 * 64 * 16; }
 
 // A scalar (SMEM) load of a wave-uniform element: it counts in lgkmcnt, not in vmcnt.
 __device__ __forceinline__ int sload(const int* p, int i) {
@@ -90,8 +110,10 @@ __device__ __forceinline__ void bdma16_nt(__amdgpu_buffer_rsrc_t r, void* lds, u
 // before an older load, so counting it could release a wait early, while an uncounted store still in flight only
 // makes the wait longer. The streams run on past the last step (re-reading it) so that the steady counts hold to the
 // end; the kernel drains vmcnt before it exits.
-template <int MT, bool SILU, bool WIDE, int ROLE>
-__device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int wave, const int it0, const int it1) {
+// BAL: the balanced schedule's run (cut items possible); otherwise whole items only, compiled without the pieces
+template <int MT, bool SILU, bool WIDE, int ROLE, bool BAL>
+__device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int wave, const int b, const int nitems,
+                                        const int u0, const int u1) {
   constexpr bool TWO = SILU || WIDE;
   constexpr int NBW = gq_nbw(TWO), NA = gq_na(MT, TWO), NW = gq_nw(MT, TWO);
   constexpr int A_BYTES = gq_abytes(MT), W_BYTES = gq_wbytes(TWO);
@@ -108,7 +130,7 @@ __device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int
   const int tid = threadIdx.x, lane = tid & 63;
   const int j = lane & 31, h = lane >> 5;
   uint16_t* const stg = (uint16_t*)(wring + NW * W_BYTES + wave * kGqStg);
-  const int G = p.G;
+  const int G = p.G, G2 = G / 2;
   const int nbands = t64_bands(p.N);
   const uint32_t gstride = (uint32_t)nbands * kT64Tile;
   const int up0 = nbands / 2;  // first up band of a [gate | up] stack
@@ -137,8 +159,8 @@ __device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int
   const uint32_t nrec = AW ? p.a_bytes : (uint32_t)p.ebytes;
   uint32_t voff[D];
   const uint32_t gstep = AW ? 2u * kGroup : gstride;
-  int s_item = it0, s_g = 0, s_st = 0, s_left = (it1 - it0) * G - 1;
-  uint32_t soff = 0;
+  int s_item = u0 / G2, s_g = 2 * (u0 - s_item * G2), s_st = 0, s_left = 2 * (u1 - u0) - 1;
+  uint32_t soff = (uint32_t)s_g * gstep;
   auto stream_item = [&](int item) __attribute__((always_inline)) {
     int e, c, q0, q1;
     item_rows(item, e, c, q0, q1);
@@ -349,21 +371,165 @@ __device__ __forceinline__ void gq_role(const GqArgs& p, uint8_t* lds, const int
       for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
   };
 
-  for (int item = it0; item < it1; item++) {
-    for (int g = 0; g < G; g += 2) {  // G is even
+  if constexpr (!BAL) {
+    for (int item = u0 / G2; item < u1 / G2; item++) {
+      for (int g = 0; g < G; g += 2) {  // G is even
+        step(bf0, bf1, af0, af1, cd0, cd1);
+        step(bf1, bf0, af1, af0, cd1, cd0);
+      }
+      int e, c, q0, q1;
+      item_rows(item, e, c, q0, q1);
+      (void)e;
+      epilogue(c, q0, q1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA lands in LDS after the block ends
+    return;
+  }
+  // a cut item's piece: this wave's sums of the item's rows (fragment rows past them are never read), written through
+  // to memory; float4 k of a lane holds rows 8 k + 4 h .. + 3 of its M tile
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void*)p.part, 0, (int)p.part_bytes, 0x00020000);
+  auto piece_off = [&](int slot, int nb, int a, int k4) __attribute__((always_inline)) {
+    return (int)((((((size_t)slot * 8 + wave) * NBW + nb) * MT + a) * 4 + k4) * 64 + lane) * 16;
+  };
+  auto store_piece = [&](int slot, int nrows) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+      for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int k4 = 0; k4 < 4; k4++) {
+          if (a * 32 + 8 * k4 + 4 * h >= nrows) continue;
+          const u32x4 v = {__float_as_uint(acc[nb][a][4 * k4]), __float_as_uint(acc[nb][a][4 * k4 + 1]),
+                           __float_as_uint(acc[nb][a][4 * k4 + 2]), __float_as_uint(acc[nb][a][4 * k4 + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(v, rp, piece_off(slot, nb, a, k4), 0, kSc1);
+        }
+  };
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+      for (int a = 0; a < MT; a++) acc[nb][a] = zero16();
+  };
+
+  // the run: segments of items; a whole item is stored at its end, a cut one leaves a piece (slot 2 b for the run's
+  // first segment, 2 b + 1 for its last)
+  const long U = (long)nitems * G2;
+  int u = u0, ncut = 0, cut0 = 0, cut1 = 0;
+  bool seeded = false;  // acc still holds the run's last segment, the first piece of its cut item (its sum's seed)
+  while (u < u1) {
+    const int item = u / G2, ga = u - item * G2, gb = min(G2, u1 - item * G2);
+    for (int g = ga; g < gb; g++) {  // a unit is two groups
       step(bf0, bf1, af0, af1, cd0, cd1);
       step(bf1, bf0, af1, af0, cd1, cd0);
     }
     int e, c, q0, q1;
     item_rows(item, e, c, q0, q1);
     (void)e;
-    epilogue(c, q0, q1);
+    if (ga == 0 && gb == G2) {
+      epilogue(c, q0, q1);
+    } else {
+      store_piece(2 * b + (u == u0 ? 0 : 1), q1 - q0);
+      if (ncut == 0) cut0 = item;
+      else cut1 = item;
+      ncut++;
+      // the item's first piece is this block's when the item starts in this run, which leaves it the run's last
+      // segment: keep the sums for the item's total
+      seeded = item * G2 + gb == u1 && gq_block_of((long)item * G2, p.nblk, U) == b;
+      if (!seeded) zero_acc();
+    }
+    u = item * G2 + gb;
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA lands in LDS after the block ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA lands in LDS after this; the pieces are in memory
+  if (ncut == 0) return;
+  // arrivals at the cut items, one counter round trip for both: the last contributor of an item sums its pieces in
+  // unit order and stores it
+  unsigned* const s_last = (unsigned*)(wring + NW * W_BYTES + 8 * kGqStg);
+  auto contributors = [&](int item, int& bf, int& bl) __attribute__((always_inline)) {
+    const long us = (long)item * G2;
+    bf = gq_block_of(us, p.nblk, U), bl = gq_block_of(us + G2 - 1, p.nblk, U);
+    int n = 0;
+    for (int bb = bf; bb <= bl; bb++) n += (long)(bb + 1) * U / p.nblk > (long)bb * U / p.nblk;
+    return n;
+  };
+  __syncthreads();  // every wave's pieces are complete
+  if (threadIdx.x == 0) {
+    unsigned old[2];
+#pragma unroll
+    for (int ci = 0; ci < 2; ci++)
+      if (ci < ncut) {
+        int bf, bl;
+        (void)contributors(ci == 0 ? cut0 : cut1, bf, bl);
+        old[ci] = __hip_atomic_fetch_add(p.cnt + bf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+    for (int ci = 0; ci < 2; ci++)
+      if (ci < ncut) {
+        int bf, bl;
+        const bool last = old[ci] + 1 == (unsigned)contributors(ci == 0 ? cut0 : cut1, bf, bl);
+        if (last) __hip_atomic_store(p.cnt + bf, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+        s_last[ci] = last;
+      }
+  }
+  __syncthreads();
+  const bool last0 = s_last[0] != 0, last1 = ncut > 1 && s_last[1] != 0;
+  // the run's last cut first, while acc may still hold its seed
+  for (int r = ncut - 1; r >= 0; r--) {
+    const bool seed = seeded && r == ncut - 1;
+    if (!(r == 0 ? last0 : last1)) {
+      if (seed) zero_acc();
+      continue;
+    }
+    const int item = r == 0 ? cut0 : cut1;
+    int bf, bl;
+    (void)contributors(item, bf, bl);
+    const long lo_f = (long)bf * U / p.nblk, us = (long)item * G2;
+    int e, c, q0, q1;
+    item_rows(item, e, c, q0, q1);
+    (void)e;
+    const int nrows = q1 - q0;
+    // the pieces in unit order (the seed, when held, is the first), a batch of contributors' loads in flight
+    constexpr int FB = MT == 2 ? 2 : 4;
+    for (int b0 = seed ? bf + 1 : bf; b0 <= bl; b0 += FB) {
+      u32x4 v[FB][NBW][MT][4];
+#pragma unroll
+      for (int z = 0; z < FB; z++) {
+        const int bb = b0 + z;
+        const bool has = bb <= bl && (long)(bb + 1) * U / p.nblk > (long)bb * U / p.nblk;
+        const int slot = bb == bf && lo_f < us ? 2 * bf + 1 : 2 * bb;
+#pragma unroll
+        for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+          for (int a = 0; a < MT; a++)
+#pragma unroll
+            for (int k4 = 0; k4 < 4; k4++)
+              v[z][nb][a][k4] = has && a * 32 + 8 * k4 + 4 * h < nrows
+                                    ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                    rp, piece_off(slot, nb, a, k4), 0, kSc1))
+                                    : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int z = 0; z < FB; z++) {
+        const int bb = b0 + z;
+        if (bb > bl || (long)(bb + 1) * U / p.nblk <= (long)bb * U / p.nblk) continue;  // no piece
+#pragma unroll
+        for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+          for (int a = 0; a < MT; a++)
+#pragma unroll
+            for (int k4 = 0; k4 < 4; k4++)
+#pragma unroll
+              for (int x = 0; x < 4; x++) acc[nb][a][4 * k4 + x] += __uint_as_float(v[z][nb][a][k4][x]);
+      }
+    }
+    epilogue(c, q0, q1);  // stores the item and zeroes acc
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // WIDE (plain only): each wave owns two bands, 8 apart, so an item is 16 bands (512 columns)
-template <int MT, bool SILU, bool WIDE>
+// BALK: compiled with the balanced schedule (launched when a piece buffer is given and a whole-item run can fall
+// kGqMinLoss units behind, K >= 128 kGqMinLoss); otherwise whole items only
+template <int MT, bool SILU, bool WIDE, bool BALK>
 __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
   constexpr bool TWO = SILU || WIDE;
   static_assert(!(SILU && WIDE), "SwiGLU pairs a gate and an up band per wave");
@@ -372,12 +538,29 @@ __global__ __launch_bounds__(kGqThreads, 1) void k_gqmm_t(GqArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = xcd_remap(blockIdx.x, p.nblk);
   const int nitems = sload(p.ntiles, 0) << p.nct_log2;
-  const int it0 = (int)((long)b * nitems / p.nblk), it1 = (int)((long)(b + 1) * nitems / p.nblk);
-  if (it0 >= it1) return;  // block-uniform, before any barrier
+  const int G2 = p.G / 2;
+  int u0, u1;  // this block's run of (item, group pair) units
+  // the balanced schedule where whole-item runs would leave the longest at least kGqMinLoss units past the even
+  // share (the fixed cost of the cut items' sums is a few steps); the same decision in every block
+  const int per = (nitems + p.nblk - 1) / p.nblk;
+  const bool bal = BALK && p.part && (long)per * G2 * p.nblk - (long)nitems * G2 >= (long)kGqMinLoss * p.nblk;
+  if (bal) {
+    const long U = (long)nitems * G2;
+    u0 = (int)((long)b * U / p.nblk), u1 = (int)((long)(b + 1) * U / p.nblk);
+  } else {
+    u0 = (int)((long)b * nitems / p.nblk) * G2, u1 = (int)((long)(b + 1) * nitems / p.nblk) * G2;
+  }
+  if (u0 >= u1) return;  // block-uniform, before any barrier
   const bool has_sb = TWO ? wave - 4 < 2 : wave == 7;
-  if (wave < 4) gq_role<MT, SILU, WIDE, 0>(p, lds, wave, it0, it1);
-  else if (has_sb) gq_role<MT, SILU, WIDE, 1>(p, lds, wave, it0, it1);
-  else gq_role<MT, SILU, WIDE, 2>(p, lds, wave, it0, it1);
+  if (BALK && bal) {
+    if (wave < 4) gq_role<MT, SILU, WIDE, 0, BALK>(p, lds, wave, b, nitems, u0, u1);
+    else if (has_sb) gq_role<MT, SILU, WIDE, 1, BALK>(p, lds, wave, b, nitems, u0, u1);
+    else gq_role<MT, SILU, WIDE, 2, BALK>(p, lds, wave, b, nitems, u0, u1);
+  } else {
+    if (wave < 4) gq_role<MT, SILU, WIDE, 0, false>(p, lds, wave, b, nitems, u0, u1);
+    else if (has_sb) gq_role<MT, SILU, WIDE, 1, false>(p, lds, wave, b, nitems, u0, u1);
+    else gq_role<MT, SILU, WIDE, 2, false>(p, lds, wave, b, nitems, u0, u1);
+  }
 }
 
 // ---- host side
@@ -392,22 +575,51 @@ static int gq_cus() {
   return n;
 }
 
-template <int MT, bool SILU, bool WIDE>
-static int launch_gq_cfg(const GqArgs& a, hipStream_t st) {
+template <int MT, bool SILU, bool WIDE, bool BALK>
+static int launch_gq_kernel(const GqArgs& a, hipStream_t st) {
   constexpr size_t lds = gq_lds(MT, SILU || WIDE);
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)k_gqmm_t<MT, SILU, WIDE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds);
+    (void)hipFuncSetAttribute((const void*)k_gqmm_t<MT, SILU, WIDE, BALK>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr = true;
   }
-  hipLaunchKernelGGL((k_gqmm_t<MT, SILU, WIDE>), dim3(a.nblk), dim3(kGqThreads), lds, st, a);
+  hipLaunchKernelGGL((k_gqmm_t<MT, SILU, WIDE, BALK>), dim3(a.nblk), dim3(kGqThreads), lds, st, a);
   return check_launch("moe_gather_qmm_t64");
 }
+// The units by which the longest whole-item run is expected to exceed the even share, for `rows` sorted rows spread
+// uniformly over E experts (Poisson rows per expert, one tile per tile_rows of an expert's rows), nct column tiles
+// and G2 group pairs per item, on nblk blocks. The kernel decides on the dispatch's actual item count; this estimate
+// only picks which compiled form to launch.
+static double gq_expected_loss(int rows, int E, int tile_rows, int nct, int G2, int nblk) {
+  const double lam = (double)rows / E;
+  double tiles = 0.0, pr = std::exp(-lam);  // P(x) for x = 0, 1, ...
+  const int xmax = (int)(lam + 12.0 * std::sqrt(lam) + 30.0);
+  for (int x = 0; x <= xmax; x++) {
+    tiles += pr * ((x + tile_rows - 1) / tile_rows);
+    pr *= lam / (x + 1);
+  }
+  const double n = tiles * E * nct;
+  return std::ceil(n / nblk) * G2 - n * G2 / nblk;
+}
+
+template <int MT, bool SILU, bool WIDE>
+static int launch_gq_cfg(const GqArgs& a, int rows, hipStream_t st) {
+  // the form compiled with the balanced schedule where the kernel is expected to take it (its whole-item path runs
+  // slower there than in the form compiled without it); with fewer than kGqMinLoss group pairs per item no
+  // whole-item run falls that far behind the even share
+  if (a.part && a.G / 2 >= kGqMinLoss &&
+      gq_expected_loss(rows, a.E + (a.wsh ? 1 : 0), 32 * MT, 1 << a.nct_log2, a.G / 2, a.nblk) >= kGqMinLoss - 2)
+    return launch_gq_kernel<MT, SILU, WIDE, true>(a, st);
+  return launch_gq_kernel<MT, SILU, WIDE, false>(a, st);
+}
+
+size_t moe_gather_t64_part_bytes(int tile_rows) { return 2 * (size_t)gq_cus() * gq_slot_bytes(tile_rows / 32); }
 
 int launch_moe_gather_qmm_t64(const uint16_t* A, int lda, const int* perm, int div, const int* tiles,
                               const int* ntiles, const int* offsets, int tile_rows, const void* wt, const void* wsh,
-                              int E, int N, int K, int silu, uint16_t* C, int ldc, int rows, hipStream_t st) {
+                              int E, int N, int K, int silu, uint16_t* C, int ldc, int rows, float* part,
+                              size_t part_bytes, unsigned* cnt, hipStream_t st) {
   if (rows == 0) return IFD_OK;
   if (tile_rows != 32 && tile_rows != 64)
     return fail(IFD_ERR_ARG, "moe_gather_qmm_t64: tile_rows=%d must be 32 or 64", tile_rows);
@@ -430,12 +642,18 @@ int launch_moe_gather_qmm_t64(const uint16_t* A, int lda, const int* perm, int d
   const size_t ab = (size_t)(perm ? (rows - 1) / div + 1 : rows) * lda * sizeof(uint16_t);
   if (ab >= ((size_t)1 << 31)) return fail(IFD_ERR_UNSUPPORTED, "moe_gather_qmm_t64: activations past 2 GiB");
   if (t64_bytes(N, K) >= ((size_t)1 << 31)) return fail(IFD_ERR_UNSUPPORTED, "moe_gather_qmm_t64: expert past 2 GiB");
+  if (part) {  // the balanced schedule: a piece slot pair per block, a header counter per block
+    if (!cnt || part_bytes < moe_gather_t64_part_bytes(tile_rows) || gq_cus() > kWsCounters)
+      return fail(IFD_ERR_WORKSPACE, "moe_gather_qmm_t64: %zu bytes of pieces and the counter header needed",
+                  moe_gather_t64_part_bytes(tile_rows));
+  }
   GqArgs a{A, lda, (uint32_t)ab, perm, div_m, tiles, ntiles, offsets, (const uint8_t*)wt, t64_bytes(N, K),
-           (const uint8_t*)wsh, E, N, K, K / kGroup, C, (uint32_t)cb, ldc, __builtin_ctz(nct), gq_cus()};
+           (const uint8_t*)wsh, E, N, K, K / kGroup, C, (uint32_t)cb, ldc, __builtin_ctz(nct), gq_cus(),
+           part, (uint32_t)(part ? moe_gather_t64_part_bytes(tile_rows) : 0), cnt};
   const int MT = tile_rows / 32;
-  if (silu) return MT == 2 ? launch_gq_cfg<2, true, false>(a, st) : launch_gq_cfg<1, true, false>(a, st);
-  if (wide) return MT == 2 ? launch_gq_cfg<2, false, true>(a, st) : launch_gq_cfg<1, false, true>(a, st);
-  return MT == 2 ? launch_gq_cfg<2, false, false>(a, st) : launch_gq_cfg<1, false, false>(a, st);
+  if (silu) return MT == 2 ? launch_gq_cfg<2, true, false>(a, rows, st) : launch_gq_cfg<1, true, false>(a, rows, st);
+  if (wide) return MT == 2 ? launch_gq_cfg<2, false, true>(a, rows, st) : launch_gq_cfg<1, false, true>(a, rows, st);
+  return MT == 2 ? launch_gq_cfg<2, false, false>(a, rows, st) : launch_gq_cfg<1, false, false>(a, rows, st);
 }
 
 }  // namespace ifd

@@ -197,6 +197,7 @@ struct Qwen35 {
     if (max_rows > 0 && E > 0) {
       need = std::max(need, ifd_moe_dispatch_workspace(R, E));
       need = std::max(need, ifd_moe_decode_workspace(std::min(max_rows, 16), H, I, E, k));
+      need = std::max(need, ifd_moe_gather_qmm_t64_workspace(64));  // the balanced schedule's pieces (either height)
       // a workspace size is not monotone in the row count (each route sizes its own), so take every T a call may
       // pass: 1 .. max_rows
       for (int T = 1; T <= max_rows; T++) {
@@ -560,15 +561,16 @@ struct Qwen35 {
                              minv.ptr<int>(), mtiles.ptr<int>(), mntiles.ptr<int>(), splitk.ptr<void>(), splitk_bytes,
                              e.stream),
          "encode_moe");
+      // both products on the balanced schedule, their pieces in the scratch (its counter header kept zero)
       ok(ifd_moe_gather_qmm_t64(xn.ptr<void>(), H, mperm.ptr<int>(), k, moffs.ptr<int>(), mtiles.ptr<int>(),
                                 mntiles.ptr<int>(), tr, ly.egu.t64.ptr<void>(),
                                 fold ? ly.gate_up.t64.ptr<void>() : nullptr, E, 2 * I, H, 1, eact.ptr<void>(), I, Rt,
-                                e.stream),
+                                splitk.ptr<void>(), splitk_bytes, e.stream),
          "encode_moe");
       ok(ifd_moe_gather_qmm_t64(eact.ptr<void>(), I, nullptr, 1, moffs.ptr<int>(), mtiles.ptr<int>(),
                                 mntiles.ptr<int>(), tr, ly.edown.t64.ptr<void>(),
                                 fold ? ly.down.t64.ptr<void>() : nullptr, E, H, I, 0, edown_out.ptr<void>(), H, Rt,
-                                e.stream),
+                                splitk.ptr<void>(), splitk_bytes, e.stream),
          "encode_moe");
       const void* ys = fold ? edown_out.at((size_t)R * H * 2).ptr<void>() : shared ? sh_out.ptr<void>() : nullptr;
       ok(ifd_moe_combine(x.ptr<void>(), edown_out.ptr<void>(), rw.ptr<float>(), ys, rsg.ptr<float>(), minv.ptr<int>(),

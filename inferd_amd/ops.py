@@ -543,15 +543,18 @@ def moe_dispatch_ex(idx: torch.Tensor, E: int, k: int, tile_rows: int = 32, shar
 
 
 def moe_gather_qmm_t64(A: torch.Tensor, perm: Optional[torch.Tensor], div: int, disp, W: T64Stack, silu: bool,
-                       shared: Optional[T64Linear] = None) -> torch.Tensor:
-    """The gathered expert GEMM on a T64 stack (disp from moe_dispatch_ex; shared: the expert-E segment's weights)."""
+                       shared: Optional[T64Linear] = None, balanced: bool = False) -> torch.Tensor:
+    """The gathered expert GEMM on a T64 stack (disp from moe_dispatch_ex; shared: the expert-E segment's weights).
+    balanced: the balanced schedule (a workspace), else whole items per block (the bits of moe_gather_qmm)."""
     offsets, perm_sorted, _, tiles, ntiles, _, tile_rows = disp
     rows = perm_sorted.numel()
     NO = W.N // 2 if silu else W.N
     C = torch.empty((rows, NO), dtype=torch.bfloat16, device=A.device)
+    ws = workspace(lib().ifd_moe_gather_qmm_t64_workspace(tile_rows), A.device) if balanced else None
     check(lib().ifd_moe_gather_qmm_t64(_p(A), A.shape[1], _p(perm), div, _p(offsets), _p(tiles), _p(ntiles), tile_rows,
                                        _p(W.wt), _p(shared.wt) if shared is not None else None, W.E, W.N, W.K,
-                                       1 if silu else 0, _p(C), NO, rows, _stream()))
+                                       1 if silu else 0, _p(C), NO, rows, _p(ws) if ws is not None else None,
+                                       ws.numel() if ws is not None else 0, _stream()))
     return C
 
 

@@ -483,6 +483,76 @@ def test_gather_qmm_t64_bit_identical(T, E, H, I, k, tile_rows):
     assert np.array_equal(g.host(y_t), g.host(y_mlx)), "down"
 
 
+def _cut_items(nitems, G2, P, min_loss=8):
+    """The items the balanced schedule cuts. It runs when whole-item runs would make the longest run at least
+    min_loss (item, group pair) units longer than the even share; then block b runs units [b U / P, (b + 1) U / P) of
+    the U = nitems G2, and an item is cut when its first and last units lie in different runs."""
+    per = -(-nitems // P)
+    if per * G2 * P - nitems * G2 < min_loss * P:
+        return set()
+    U = nitems * G2
+    block_of = lambda u: (u * P + P - 1) // U  # noqa: E731
+    return {it for it in range(nitems) if block_of(it * G2) != block_of(it * G2 + G2 - 1)}
+
+
+def _check_balanced(g, Cb, Cw, disp, tile_rows, width, K, what):
+    """Uncut items bit-identical to the whole-item schedule; cut items (their K ranges summed in K order) within
+    fp32 summation-order rounding, i.e. a few bf16 steps at most. Returns the number of cut items."""
+    offsets, tiles, nt = g.host(disp[0]), g.host(disp[3]), int(g.host(disp[4])[0])
+    nct = Cw.shape[1] // width
+    P = torch.cuda.get_device_properties(0).multi_processor_count
+    cut = _cut_items(nt * nct, K // 128, P)
+    b, w = gen.bf16_to_f32(g.host(Cb)), gen.bf16_to_f32(g.host(Cw))
+    for it in range(nt * nct):
+        e, q0 = tiles[it // nct]
+        q1 = min(int(offsets[e + 1]), q0 + tile_rows)
+        c0 = (it % nct) * width
+        bb, ww = b[q0:q1, c0:c0 + width], w[q0:q1, c0:c0 + width]
+        if it not in cut:
+            assert np.array_equal(bb, ww), f"{what}: uncut item {it} differs"
+        else:
+            bound = 2.0 ** -5 * np.abs(ww) + 1e-6 * max(np.abs(w).max(), 1e-30)
+            assert (np.abs(bb - ww) <= bound).all(), f"{what}: cut item {it} beyond summation-order rounding"
+    return len(cut)
+
+
+@pytest.mark.parametrize("T,E,H,I,k,tile_rows,shared,gu_cut", [
+    (2, 16, 2048, 256, 2, 32, True, True),   # fewer units than blocks: empty runs, items cut into one-unit pieces
+    (16, 64, 256, 256, 4, 32, True, False),  # 2 units per item: whole items always
+    (300, 16, 256, 512, 2, 64, False, False),
+    (16, 512, 2048, 512, 10, 32, True, True),    # BASELINE config 4 geometry: ~280 gate/up items on 256 blocks
+    (128, 512, 2048, 512, 10, 32, True, False),  # ~950 items: whole-item runs within 5 units of the even share
+    (2048, 512, 2048, 512, 10, 64, True, True),  # ~1090 items: 5 per block against 4.26
+])
+def test_gather_qmm_t64_balanced(T, E, H, I, k, tile_rows, shared, gu_cut):
+    """The balanced schedule (a workspace: every block an equal share of the (item, group pair) units, cut items
+    summed from their pieces by the last contributor) against the whole-item schedule on the same dispatch, for
+    gate/up + SwiGLU and for down (the wide form on 64-row tiles): bit-identical on uncut items, within summation-order
+    rounding on cut ones, and the same bits on a second call (the counters reset themselves). gu_cut: the schedule
+    cuts gate/up items here (the kernel takes it only where whole-item runs lose at least 8 units)."""
+    g, ops = _gu(), _ops()
+    rng = np.random.default_rng(T + E + 1)
+    egu, edn, sgu, sdn = _stacks(T, E, H, I)
+    x = g.dev(gen.activations(T, H, seed=T + 6))
+    idx = g.dev(np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32))
+    disp = ops.moe_dispatch_ex(idx, E, k, tile_rows, shared_rows=T if shared else 0)
+    TGU, TDN = ops.pack_t64_stack(g.moew(*egu)), ops.pack_t64_stack(g.moew(*edn))
+    SGU = ops.pack_t64(g.qlinear(sgu[0][0], sgu[1][0], sgu[2][0])) if shared else None
+    SDN = ops.pack_t64(g.qlinear(sdn[0][0], sdn[1][0], sdn[2][0])) if shared else None
+    hw = ops.moe_gather_qmm_t64(x, disp[1], k, disp, TGU, silu=True, shared=SGU)
+    hb = ops.moe_gather_qmm_t64(x, disp[1], k, disp, TGU, silu=True, shared=SGU, balanced=True)
+    hb2 = ops.moe_gather_qmm_t64(x, disp[1], k, disp, TGU, silu=True, shared=SGU, balanced=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(g.host(hb), g.host(hb2)), "gate/up: a second call differs"
+    ncut = _check_balanced(g, hb, hw, disp, tile_rows, 256, H, "gate/up + SwiGLU")
+    assert (ncut > 0) == gu_cut, f"gate/up: {ncut} items cut"
+    wide = H % 512 == 0 and tile_rows == 64
+    yw = ops.moe_gather_qmm_t64(hw, None, 1, disp, TDN, silu=False, shared=SDN)
+    yb = ops.moe_gather_qmm_t64(hw, None, 1, disp, TDN, silu=False, shared=SDN, balanced=True)
+    torch.cuda.synchronize()
+    _check_balanced(g, yb, yw, disp, tile_rows, 512 if wide else 256, I, "down")
+
+
 @pytest.mark.parametrize("T,tile_rows", [(37, 32), (300, 64)])
 def test_gather_qmm_t64_shared_segment(T, tile_rows):
     """The shared expert as the dispatch's expert-E segment (every token, in token order, after the routed rows): its
@@ -530,14 +600,17 @@ def _ffn_t64_case(T, E, H, I, k, shared_gate, seed):
     logits = ops.moe_router_logits(xd, Rd, out_bf16=T >= 64)
     idx2, wt2, sg2 = ops.moe_route(logits, E, k, shared_gate=shared_gate)
     disp = ops.moe_dispatch_ex(idx2, E, k, tile_rows, shared_rows=T)
-    eact = ops.moe_gather_qmm_t64(xd, disp[1], k, disp, TGU, silu=True, shared=SGU)
-    ydn = ops.moe_gather_qmm_t64(eact, None, 1, disp, TDN, silu=False, shared=SDN)
+    # the one-shot call runs both products on the balanced schedule
+    eact = ops.moe_gather_qmm_t64(xd, disp[1], k, disp, TGU, silu=True, shared=SGU, balanced=True)
+    ydn = ops.moe_gather_qmm_t64(eact, None, 1, disp, TDN, silu=False, shared=SDN, balanced=True)
     out2 = ops.moe_combine(torch.zeros_like(out), ydn[:R], wt2, ydn[R:], sg2, disp[2], k, True)
+    # the product itself and its fused SwiGLU on whole items (no cut sums: the same bits either way)
     gu_full = ops.moe_gather_qmm_t64(xd, disp[1], k, disp, TGU, silu=False, shared=SGU)
+    eact_w = ops.moe_gather_qmm_t64(xd, disp[1], k, disp, TGU, silu=True, shared=SGU)
     torch.cuda.synchronize()
     assert np.array_equal(g.host(out), g.host(out2)), "one-shot FFN differs from its stages"
     assert np.array_equal(g.host(idx), g.host(idx2)) and np.array_equal(g.host(wt), g.host(wt2))
-    assert np.array_equal(g.host(eact), g.host(ops.silu_mul(gu_full))), "fused SwiGLU differs from silu_mul"
+    assert np.array_equal(g.host(eact_w), g.host(ops.silu_mul(gu_full))), "fused SwiGLU differs from silu_mul"
     ri, rw, rs = orc.moe_route(g.host(logits), E, k, shared_gate=shared_gate)
     assert np.array_equal(g.host(idx), ri)
     ro, rp, rinv = orc.moe_dispatch(ri, E)
