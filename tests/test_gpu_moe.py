@@ -143,10 +143,13 @@ def test_gather_qmm_8bit(silu):
     gen.check_bf16(g.host(prod), ref, 1e-2, ("8-bit stacks", silu))
 
 
-def test_combine():
+@pytest.mark.parametrize("k,T", [(10, 50), (1, 50), (16, 50), (20, 50), (10, 2100)])
+def test_combine(k, T):
+    """Up to 16 picks on at most 512 blocks a thread loads every pick's row before summing; past 16 picks (k = 20) or
+    on more blocks (T = 2100 tokens of 512 columns: 525 blocks) it loops."""
     g, ops = _gu(), _ops()
-    rng = np.random.default_rng(6)
-    T, H, k = 50, 512, 10
+    rng = np.random.default_rng(6 + k)
+    H = 512
     yd = gen.f32_to_bf16(rng.standard_normal((T * k, H)).astype(np.float32))
     ys = gen.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
     wt = rng.uniform(0, 1, (T, k)).astype(np.float32)
