@@ -38,6 +38,7 @@ constexpr int kMdecMaxT = 16, kMdecMaxK = 16, kMdecKG = 8;  // tokens, picks, gr
 // the MFMA output row (token) of accumulator r of a lane in half h
 __device__ __forceinline__ int mdec_row(int r, int h) { return 8 * (r / 4) + 4 * h + (r % 4); }
 constexpr int kMdecMaxKS = 4;                                 // K splits of the router
+constexpr int kMdecCmbB = 12;  // slots whose 16-byte loads a combining thread has in flight at once
 
 struct MdecArgs {
   const uint16_t* x;       // normalised tokens [T][H]
@@ -70,6 +71,7 @@ struct MdecArgs {
   int sh_bits;             // the shared expert's width: 4, or 8 (the reference's moe_gu2_4_8 / moe_dn2_4_8)
   int routed;              // idx / wt / sg hold the caller's routing (no router, no routing here)
   const uint16_t* ys;      // with routed: the shared expert's output rows [T][H] for the combine, or null
+  int out16;               // out and ys 16-byte aligned: the combine loads and stores 8 columns at a time
 };
 
 // The 8 bf16 values at v (16-byte aligned) as 8 raw halves.
@@ -285,8 +287,9 @@ __host__ __device__ constexpr size_t mdec_gu_lds(int T, int RT) {
 
 // SB: the shared expert's width (8: the reference's moe_gu2_4_8, a kernel of its own, so that the 4-bit form keeps its
 // registers)
+// three waves per SIMD up to 8 tokens (three blocks of 8 staged rows fit the LDS), two beyond
 template <int RT, int SB>
-__global__ __launch_bounds__(256) void k_mdec_gu(MdecArgs p) {
+__global__ __launch_bounds__(256, RT == 4 ? 3 : 2) void k_mdec_gu(MdecArgs p) {
   extern __shared__ __align__(16) uint8_t glds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
   const int u = blockIdx.y, T = p.T, I = p.I, H = p.H, G = H / kGroup, Gw = G / 4;
@@ -481,6 +484,52 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   if (!s_last) return;
   // the chunk's combine: every (token, column) of its 128 columns
   const int nj = k + (p.sgu_wq || p.ys ? 1 : 0);
+  if (p.out16) {
+    // eight columns per thread (16-byte loads and stores; out and ys 16-byte aligned), kMdecCmbB slots' loads in
+    // flight at once, summed in slot order
+    for (int i = tid; i < T * 16; i += 256) {
+      const int t = i >> 4, hc = blockIdx.x * 128 + (i & 15) * 8;
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) a[e] = 0.f;
+      for (int j0 = 0; j0 < nj; j0 += kMdecCmbB) {
+        u32x4 dv[kMdecCmbB];
+        float wv[kMdecCmbB];
+#pragma unroll
+        for (int z = 0; z < kMdecCmbB; z++) {
+          const int jj = j0 + z;
+          if (jj < nj) {
+            dv[z] = jj == k && p.ys ? *(const u32x4*)(p.ys + (size_t)t * H + hc)
+                                    : __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                    rd, (int)((((size_t)t * (k + 1) + jj) * H + hc) * 2),
+                                                                    0, kSc1));
+            wv[z] = jj < k ? p.wt[t * k + jj] : p.sg[t];
+          }
+        }
+#pragma unroll
+        for (int z = 0; z < kMdecCmbB; z++)
+          if (j0 + z < nj)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+              a[e] = __builtin_fmaf(wv[z], bf2f((uint16_t)(dv[z][e / 2] >> (16 * (e & 1)))), a[e]);
+      }
+      u32x4* o = (u32x4*)(p.out + (size_t)t * H + hc);
+      const u32x4 ov = p.assign ? u32x4{0u, 0u, 0u, 0u} : *o;
+      u32x4 res;
+#pragma unroll
+      for (int e2 = 0; e2 < 4; e2++) {
+        float v[2];
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+          const int e = 2 * e2 + f;
+          v[f] = p.assign ? a[e] : bf2f((uint16_t)(ov[e2] >> (16 * f))) + bf2f(f2bf(a[e]));
+        }
+        res[e2] = pack_bf2(v[0], v[1]);
+      }
+      *o = res;
+    }
+    return;
+  }
   for (int i = tid; i < T * 128; i += 256) {
     const int t = i >> 7, hc = blockIdx.x * 128 + (i & 127);
     // every slot's value and weight requested before the first is used, then summed in slot order
@@ -591,6 +640,7 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
   p.sdn_wq = c.sdn_wq, p.sdn_s = c.sdn_s, p.sdn_b = c.sdn_b;
   p.sh_bits = c.sh_bits;
   p.routed = c.routed, p.ys = (const uint16_t*)c.ys;
+  p.out16 = ((uintptr_t)c.out % 16 == 0 && (uintptr_t)c.ys % 16 == 0) ? 1 : 0;
   p.out = (uint16_t*)c.out;
   p.idx = c.idx ? c.idx : (int*)(w + L.idx);
   p.wt = c.wt ? c.wt : (float*)(w + L.wt);

@@ -398,6 +398,29 @@ def test_moe_decode_shared_experts_across_tokens(assign):
     assert len(np.unique(ri)) < ri.size
 
 
+@pytest.mark.parametrize("T", [1, 5, 16])
+def test_moe_decode_out_alignment(T):
+    """The combine stores 8 columns at a time into a 16-byte aligned out, else one at a time: the same bits either
+    way (residual add, shared expert)."""
+    g, ops = _gu(), _ops()
+    E, H, I, k = 32, 512, 128, 4
+    egu, edn = g.moew(*experts(E, 2 * I, H, seed=170)), g.moew(*experts(E, H, I, seed=171))
+    sgu, sdn = experts(1, 2 * I, H, seed=172), experts(1, H, I, seed=173)
+    sh = (g.qlinear(sgu[0][0], sgu[1][0], sgu[2][0]), g.qlinear(sdn[0][0], sdn[1][0], sdn[2][0]))
+    xn = g.dev(gen.activations(T, H, seed=174))
+    Rd = g.dev(router(E + 1, H, seed=175))
+    x0 = g.dev(gen.activations(T, H, seed=176))
+    a16 = x0.clone()
+    big = torch.empty((T * H + 8,), dtype=torch.bfloat16, device=x0.device)
+    a2 = big[1:1 + T * H].view(T, H)  # 2 bytes past a 16-byte boundary
+    a2.copy_(x0)
+    ops.moe_decode(xn, Rd, egu, edn, k, shared=sh, out=a16, assign=False)
+    ops.moe_decode(xn, Rd, egu, edn, k, shared=sh, out=a2, assign=False)
+    torch.cuda.synchronize()
+    assert np.array_equal(g.host(a16), g.host(a2.contiguous()))
+    assert not np.array_equal(g.host(a16), g.host(x0))
+
+
 def test_moe_decode_no_shared_expert_long_k():
     """No shared expert; I = 1152 (two K chunks of 8 groups in the down kernel), H = 4608 (gate/up chunks too), k = 16."""
     _decode_case(3, 64, 4608, 1152, 16, False, False, seed=150)
