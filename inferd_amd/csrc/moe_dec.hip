@@ -39,6 +39,7 @@ constexpr int kMdecMaxT = 16, kMdecMaxK = 16, kMdecKG = 8;  // tokens, picks, gr
 __device__ __forceinline__ int mdec_row(int r, int h) { return 8 * (r / 4) + 4 * h + (r % 4); }
 constexpr int kMdecMaxKS = 4;                                 // K splits of the router
 constexpr int kMdecCmbB = 12;  // slots whose 16-byte loads a combining thread has in flight at once
+constexpr int kMdecStageU = 4;  // token-row chunks a staging thread loads before using any
 
 struct MdecArgs {
   const uint16_t* x;       // normalised tokens [T][H]
@@ -244,26 +245,35 @@ __device__ __forceinline__ int mdec_pick(const MdecArgs& p, int u, int t) {
 // Stage rows [T][ng * 64] (row t from src(t), null = zeros) into LDS As (row stride lda) and their 64-group sums into
 // Xs[g][t] (kMdecMaxT per group). nthr threads starting at thread `first`; every 8 consecutive chunks are one group, so the
 // group sum is a reduction over 8 consecutive lanes.
-template <class Src>
+// U chunks per thread are loaded before any is used (one memory latency per U passes, not per pass).
+template <int U, class Src>
 __device__ __forceinline__ void mdec_stage(Src src, int T, int ng, uint16_t* As, int lda, float* Xs, int first,
                                            int nthr) {
   const int cpr = ng * 8, total = T * cpr, me = (int)threadIdx.x - first;
-  for (int c0 = 0; c0 < total; c0 += nthr) {
-    const int c = c0 + me;
-    const bool ok = c < total;
-    const int t = ok ? c / cpr : 0, kc = ok ? c % cpr : 0;
-    const uint16_t* s = ok ? src(t) : nullptr;
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (s) v = *(const u32x4*)(s + 8 * kc);
-    float sum = 0.f;
+  for (int c0 = 0; c0 < total; c0 += U * nthr) {
+    u32x4 v[U];
 #pragma unroll
-    for (int e = 0; e < 4; e++) sum += bf2f((uint16_t)(v[e] & 0xFFFFu)) + bf2f((uint16_t)(v[e] >> 16));
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
-    if (ok) {
-      *(u32x4*)(As + (size_t)t * lda + 8 * kc) = v;
-      if ((kc & 7) == 0) Xs[(kc >> 3) * kMdecMaxT + t] = sum;
+    for (int q = 0; q < U; q++) {
+      const int c = c0 + q * nthr + me;
+      const bool ok = c < total;
+      const uint16_t* s = ok ? src(c / cpr) : nullptr;
+      v[q] = s ? *(const u32x4*)(s + 8 * (c % cpr)) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < U; q++) {
+      const int c = c0 + q * nthr + me;
+      const bool ok = c < total;
+      const int t = ok ? c / cpr : 0, kc = ok ? c % cpr : 0;
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) sum += bf2f((uint16_t)(v[q][e] & 0xFFFFu)) + bf2f((uint16_t)(v[q][e] >> 16));
+      sum += __shfl_xor(sum, 1, 64);
+      sum += __shfl_xor(sum, 2, 64);
+      sum += __shfl_xor(sum, 4, 64);
+      if (ok) {
+        *(u32x4*)(As + (size_t)t * lda + 8 * kc) = v[q];
+        if ((kc & 7) == 0) Xs[(kc >> 3) * kMdecMaxT + t] = sum;
+      }
     }
   }
 }
@@ -340,8 +350,8 @@ __global__ __launch_bounds__(256, RT == 4 ? 3 : 2) void k_mdec_gu(MdecArgs p) {
       }
     }
     if (c0 > 0) __syncthreads();  // the previous chunk's reads of As are done (every wave runs the same chunks)
-    mdec_stage([&](int t) { return p.x + (size_t)t * H + (size_t)gb * 64; }, T, ng, As, kMdecGuRow, Xs, wave * 64,
-               64);
+    mdec_stage<kMdecStageU>([&](int t) { return p.x + (size_t)t * H + (size_t)gb * 64; }, T, ng, As, kMdecGuRow, Xs,
+                            wave * 64, 64);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < KG; i++) {
@@ -430,7 +440,7 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
       }
     }
     if (c0 == 0) {  // the activation rows of the tokens that picked this slot (zero rows for the others)
-      mdec_stage(
+      mdec_stage<2>(  // T / 4 passes of 256 threads at most: two in flight
           [&](int t) -> const uint16_t* {
             const int pk = mdec_pick(p, u, t);
             return pk < 0 ? nullptr : p.act + ((size_t)t * (k + 1) + pk) * I;
