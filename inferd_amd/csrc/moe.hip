@@ -190,16 +190,12 @@ __global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ logi
   float v[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) v[i] = i * 64 + (int)(threadIdx.x & 63) < E ? L(i * 64 + (threadIdx.x & 63)) : 0.f;
-  int who[16];
-  float p[16];
+  int who;
+  float p;
   route_token(v, E, k, norm, who, p);
-  if ((threadIdx.x & 63) == 0) {
-    for (int jj = 0; jj < k; jj++) {
-      idx[(size_t)t * k + jj] = who[jj];
-      wt[(size_t)t * k + jj] = p[jj];
-    }
-    sg[t] = shared_gate ? 1.f / (1.f + expf(-L(E))) : 1.f;
-  }
+  const int l = threadIdx.x & 63;
+  if (l < k) idx[(size_t)t * k + l] = who, wt[(size_t)t * k + l] = p;
+  if (l == 0) sg[t] = shared_gate ? 1.f / (1.f + expf(-L(E))) : 1.f;
 }
 
 int launch_moe_route(const void* logits, int logits_bf16, int T, int E, int k, int stride, int norm, int shared_gate,

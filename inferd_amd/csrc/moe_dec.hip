@@ -131,17 +131,11 @@ __device__ __forceinline__ void mdec_plan_block(const MdecArgs& p) {
     float r[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) r[i] = v[i];
-    int who[16];
-    float pw[16];
+    int who;
+    float pw;
     route_token(r, p.E, k, p.norm, who, pw);
-    if (lane == 0) {
-      for (int jj = 0; jj < k; jj++) {
-        tidx[t * k + jj] = who[jj];
-        p.idx[t * k + jj] = who[jj];
-        p.wt[t * k + jj] = pw[jj];
-      }
-      p.sg[t] = p.shared_gate ? 1.f / (1.f + expf(-gate)) : 1.f;
-    }
+    if (lane < k) tidx[t * k + lane] = who, p.idx[t * k + lane] = who, p.wt[t * k + lane] = pw;
+    if (lane == 0) p.sg[t] = p.shared_gate ? 1.f / (1.f + expf(-gate)) : 1.f;
   }
   __syncthreads();
   // The distinct experts in pick order, one thread per pick q (q < T k <= 256, waves 0-3): its expert's first pick

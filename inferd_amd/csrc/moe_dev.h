@@ -7,9 +7,13 @@
 
 namespace ifd {
 
-// v[i]: logit i * 64 + lane of the token (lanes past E: anything). On return lane 0 holds the picks: who[j], p[j]
-// (j < k <= 16).
-__device__ __forceinline__ void route_token(float (&v)[8], int E, int k, int norm, int (&who)[16], float (&p)[16]) {
+// v[i]: logit i * 64 + lane of the token (lanes past E: anything). On return lane j < k <= 16 holds pick j: its
+// expert who and weight p.
+// Each round takes the largest remaining value: its lowest index comes from a ballot when one lane holds it (a tie
+// within the lane goes to the lower i by the strict compare), and from a min-reduction over the tied lanes'
+// indices when several do. The weights are divided after the rounds, pick j in lane j, all in one instruction: the
+// same quotients m / sum, and their total in pick order, as a division per round.
+__device__ __forceinline__ void route_token(float (&v)[8], int E, int k, int norm, int& who, float& p) {
   const int lane = threadIdx.x & 63;
   float mx = -INFINITY;
 #pragma unroll
@@ -27,7 +31,8 @@ __device__ __forceinline__ void route_token(float (&v)[8], int E, int k, int nor
     v[i] = ok ? ex : -2.f;  // padding never wins a pick (picks need v > -1)
   }
   sum = dpp_sum_f(sum);
-  float tot = 0.f;
+  float m_l = 0.f;
+  int w_l = 0;
   for (int jj = 0; jj < k; jj++) {
     float best = -1.f;
     int bi = 0x7fffffff;
@@ -35,18 +40,21 @@ __device__ __forceinline__ void route_token(float (&v)[8], int E, int k, int nor
     for (int i = 0; i < 8; i++)
       if (v[i] > best) best = v[i], bi = i * 64 + lane;  // strict >: lowest index of this lane wins a tie
     const float m = dpp_max_f(best);
-    const int w = dpp_min_i(best == m ? bi : 0x7fffffff);
+    const unsigned long long hit = __ballot(best == m);
+    const int w = __popcll(hit) == 1 ? __builtin_amdgcn_readlane(bi, __ffsll((long long)hit) - 1)
+                                     : dpp_min_i(best == m ? bi : 0x7fffffff);
     if ((w & 63) == lane) {
 #pragma unroll
       for (int i = 0; i < 8; i++)
         if (i == w / 64) v[i] = -1.f;
     }
-    p[jj] = m / sum;
-    who[jj] = w;
-    tot += m / sum;
+    if (lane == jj) m_l = m, w_l = w;
   }
-  if (norm)
-    for (int jj = 0; jj < k; jj++) p[jj] = p[jj] / tot;
+  p = m_l / sum;
+  float tot = 0.f;
+  for (int jj = 0; jj < k; jj++) tot += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), jj));
+  if (norm) p = p / tot;
+  who = w_l;
 }
 
 }  // namespace ifd
