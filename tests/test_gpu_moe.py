@@ -68,10 +68,11 @@ def test_route_bit_exact(bf, shared_gate):
     assert np.allclose(g.host(sg), rs, rtol=1e-5)
 
 
-@pytest.mark.parametrize("T,E", [(16, 512), (128, 512), (2048, 512), (1, 8), (37, 64), (25, 512), (26, 512)])
+@pytest.mark.parametrize("T,E", [(16, 512), (128, 512), (2048, 512), (1, 8), (37, 64), (25, 512), (26, 512),
+                                 (409, 512), (410, 512)])
 def test_dispatch_bit_exact(T, E):
     """Up to 256 routed rows (T = 1, 16, 25 here) the three passes run as one block; T = 26 (260 rows) is the first
-    count past it."""
+    count past it. T = 409 / 410: 16 chunks of 256 rows, the last one full and partial."""
     g, ops = _gu(), _ops()
     rng = np.random.default_rng(T)
     k = min(10, E)
