@@ -396,7 +396,6 @@ def main():
                 byts = (U + 1) * e_bytes + E * H * 2 + 2 * T * H * 2
                 moe[f"T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3), gbs=byts / (ms * 1e-3) / 1e9,
                                     frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, mlx_layout_us=ms_mlx * 1e3)
-            del tlay
             # the drop-in operator itself: Qwen35::encode_moe (rmsnorm, router, routing, the sorted route on the
             # loader's T64 copies with the shared expert as expert E, combine into x), timed by its own C++ program
             # over this library; and the same operator on the MLX-layout stacks alone
@@ -413,19 +412,29 @@ def main():
                     byts = (U + 1) * e_bytes + E * H * 2 + 2 * T * H * 2
                     op[f"T{T}"]["frac_hbm"] = byts / (op[f"T{T}"]["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
                 moe[key] = op
-            # decode batches (T <= 8): the four-launch decode MoE, each distinct expert read once
+            # decode batches (T <= 8): the four-launch decode MoE, each distinct expert read once, streaming the
+            # T64 stacks (what encode_moe runs when the loader made them) and the MLX-layout stacks
             for T in (1, 2, 4, 8):
                 xn = act(T, H)
                 outb = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+
+                def run_dec_t64(i):
+                    tgu, tdn, sgu, sdn = tlay[i % ncp]
+                    ops.moe_decode_t64(xn, router, tgu, tdn, k, shared=(sgu, sdn), shared_gate=False, out=outb)
 
                 def run_dec(i):
                     egu, edn, sgu, sdn = lay[i % ncp]
                     ops.moe_decode(xn, router, egu, edn, k, shared=(sgu, sdn), shared_gate=False, out=outb)
 
-                ms = timed(run_dec, 50, 5)
-                moe[f"decode_T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3))
+                ms = timed(run_dec_t64, 50, 5)
+                ms_mlx = timed(run_dec, 50, 5)
+                U = E * (1.0 - (1.0 - k / E) ** T)
+                byts = (U + 1) * e_bytes + E * H * 2 + 2 * T * H * 2
+                moe[f"decode_T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3),
+                                           frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                           mlx_layout_us=ms_mlx * 1e3)
             breakdown["c4_moe"] = moe
-            del lay
+            del lay, tlay
 
     if breakdown:
         out["breakdown"] = breakdown

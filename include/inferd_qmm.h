@@ -348,6 +348,17 @@ int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int 
                    const uint16_t* sgu_b, const uint32_t* sdn_wq, const uint16_t* sdn_s, const uint16_t* sdn_b,
                    void* out, int assign, int* idx, float* wt, float* sg, float* logits, void* workspace,
                    size_t ws_bytes, void* stream);
+/* The decode MoE of ifd_moe_decode on T64 stacks (the layout ifd_pack_t64 writes, the device loader's default copy):
+ * egu_t64 = E experts [E][2I][H], edn_t64 = [E][H][I], the shared expert's T64 copies sgu_t64 [2I][H] / sdn_t64
+ * [H][I] (4-bit) or NULL. Up to 8 tokens (the reference's moe2 range). The router is either `router` (bf16 [E1][H],
+ * as ifd_moe_decode) or the caller's fp32 logits `logits_in` [T][E1] (as ifd_moe_decode_logits_ex): exactly one is
+ * non-NULL. The same per-row qmv4 arithmetic (fp32 sums in another order); each wave streams one 32-column band's
+ * 1152-byte tiles, and gate/up splits K over blocks. Workspace: ifd_moe_decode_t64_workspace. */
+size_t ifd_moe_decode_t64_workspace(int T, int H, int I, int E, int k);
+int ifd_moe_decode_t64(const void* xn, int T, int H, const void* router, const float* logits_in, int E, int k,
+                       int norm, int shared_gate, const void* egu_t64, const void* edn_t64, int I, const void* sgu_t64,
+                       const void* sdn_t64, void* out, int assign, int* idx, float* wt, float* sg, float* logits,
+                       void* workspace, size_t ws_bytes, void* stream);
 /* The same from router logits the caller computed: logits_in fp32 [T][E + shared_gate] (the shared expert's gate
  * logit last). For routers the decode kernel does not read, such as the reference's 8-bit router (moe_router8,
  * moe.metal:553-600, routed at qwen35.h:1878-1882): ifd_gemm_w8 in mode 2 computes those logits with its qmv8

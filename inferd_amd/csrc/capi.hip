@@ -761,6 +761,36 @@ int ifd_moe_decode_ex(const void* xn, int T, int H, const void* router, int E, i
   return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
 }
 
+size_t ifd_moe_decode_t64_workspace(int T, int H, int I, int E, int k) {
+  if (T <= 0 || T > 8 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  return with_header(mdec_layout(T, H, I, E, k, true).total);
+}
+
+int ifd_moe_decode_t64(const void* xn, int T, int H, const void* router, const float* logits_in, int E, int k,
+                       int norm, int shared_gate, const void* egu_t64, const void* edn_t64, int I, const void* sgu_t64,
+                       const void* sdn_t64, void* out, int assign, int* idx, float* wt, float* sg, float* logits,
+                       void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(T >= 0 && T <= 8, "the decode MoE on T64 stacks takes T <= 8 tokens (T=%d)", T);
+  IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
+                k <= 16 && k <= E,
+            "bad decode MoE shape H=%d I=%d E=%d k=%d (H multiple of 512, I of 64, E <= 512, k <= 16)", H, I, E, k);
+  const bool shared = sgu_t64 != nullptr;
+  IFD_CHECK(shared == (sdn_t64 != nullptr), "the shared expert needs both stacks");
+  IFD_CHECK(!shared_gate || shared, "a shared gate needs a shared expert");
+  IFD_CHECK((router == nullptr) != (logits_in == nullptr), "exactly one of router and logits_in");
+  if (T == 0) return IFD_OK;
+  IFD_CHECK(xn && egu_t64 && edn_t64 && out, "null pointer");
+  IFD_CHECK(aligned(xn, 16) && (!router || aligned(router, 16)) && (!logits_in || aligned(logits_in, 4)) &&
+                aligned(egu_t64, 16) && aligned(edn_t64, 16) && (!shared || (aligned(sgu_t64, 16) && aligned(sdn_t64, 16))),
+            "tokens, router and stacks must be 16-byte aligned");
+  const WsView wv = ws_view(workspace, ws_bytes);
+  MdecCall c{xn, router, T, H, E, k, I, norm ? 1 : 0, shared_gate ? 1 : 0, assign ? 1 : 0, nullptr, nullptr, nullptr,
+             nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, out, idx, wt, sg, logits,
+             logits_in, 4};
+  c.egu_t64 = egu_t64, c.edn_t64 = edn_t64, c.sgu_t64 = sgu_t64, c.sdn_t64 = sdn_t64;
+  return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
+}
+
 int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int k, int norm, int shared_gate,
                    const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
                    const uint16_t* edn_s, const uint16_t* edn_b, int I, const uint32_t* sgu_wq, const uint16_t* sgu_s,

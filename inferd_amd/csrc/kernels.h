@@ -186,11 +186,18 @@ struct MdecCall {
   int sh_bits = 4;         // the shared expert's width, 4 or 8
   int routed = 0;          // idx / wt / sg hold the caller's routing (router and logits unused); any T
   const void* ys = nullptr;  // with routed: the shared expert's output rows [T][H] (bf16) for the combine, or null
+  // the T64 path (T <= 8, not routed): the stacks packed by ifd_pack_t64 (egu [E][2I][H], edn [E][H][I]) and the
+  // shared expert's T64 copies (4-bit) or null; the MLX-layout pointers are then unused
+  const void* egu_t64 = nullptr;
+  const void* edn_t64 = nullptr;
+  const void* sgu_t64 = nullptr;
+  const void* sdn_t64 = nullptr;
 };
 struct MdecLayout {
-  size_t part, plan, act, d, idx, wt, sg, total;
+  size_t part, plan, act, d, idx, wt, sg, gpart, total;
+  int gS, gps;  // the T64 path's gate/up K split
 };
-MdecLayout mdec_layout(int T, int H, int I, int E, int k);
+MdecLayout mdec_layout(int T, int H, int I, int E, int k, bool t64 = false);
 int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st);
 
 }  // namespace ifd

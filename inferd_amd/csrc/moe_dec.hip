@@ -31,6 +31,8 @@
 #include "host.h"
 #include "kernels.h"
 #include "moe_dev.h"
+#include "t64.h"
+#include "t64_dev.h"
 
 namespace ifd {
 
@@ -73,6 +75,17 @@ struct MdecArgs {
   int routed;              // idx / wt / sg hold the caller's routing (no router, no routing here)
   const uint16_t* ys;      // with routed: the shared expert's output rows [T][H] for the combine, or null
   int out16;               // out and ys 16-byte aligned: the combine loads and stores 8 columns at a time
+  int has_sh;              // a shared expert (either layout)
+  // the T64 path (T <= 8): routed experts packed by ifd_pack_t64 with E (expert e at e gu_eb, e dn_eb bytes), the
+  // shared expert's T64 copies or null; the gate/up K split (gS splits of gps groups) and its partials
+  const uint8_t* egu_t;
+  const uint8_t* edn_t;
+  const uint8_t* sgu_t;
+  const uint8_t* sdn_t;
+  size_t gu_eb, dn_eb;
+  float* gpart;
+  uint32_t gpart_bytes;
+  int gS, gps;
 };
 
 // The 8 bf16 values at v (16-byte aligned) as 8 raw halves.
@@ -226,7 +239,7 @@ struct MdecSlot {
 };
 __device__ __forceinline__ MdecSlot mdec_slot(const MdecArgs& p, int u) {
   const int NU = p.T * p.k;
-  if (u == NU) return MdecSlot{-1, p.sgu_wq != nullptr};
+  if (u == NU) return MdecSlot{-1, p.has_sh != 0};
   return MdecSlot{u < p.plan[0] ? p.plan[1 + u] : 0, u < p.plan[0]};
 }
 // token t's pick index of slot u (k for the shared expert), or -1
@@ -389,6 +402,80 @@ __global__ __launch_bounds__(256, RT == 4 ? 3 : 2) void k_mdec_gu(MdecArgs p) {
   }
 }
 
+// The combine of 128-column chunk blockIdx.x, by the last down block of that chunk: out[t][h] = bf16(acc) or
+// bf16(out + bf16(acc)), acc = sum_j wt[t][j] d[t][j][h] + sg[t] d[t][k][h] in slot order (rd: d, written through).
+template <int CB = kMdecCmbB, int CW = 128>
+__device__ __forceinline__ void mdec_combine(const MdecArgs& p, __amdgpu_buffer_rsrc_t rd) {
+  const int tid = threadIdx.x, T = p.T, H = p.H, k = p.k;
+  const int nj = k + (p.has_sh || p.ys ? 1 : 0);
+  if (p.out16) {
+    // eight columns per thread (16-byte loads and stores; out and ys 16-byte aligned), CB slots' loads in
+    // flight at once, summed in slot order
+    for (int i = tid; i < T * (CW / 8); i += 256) {
+      const int t = i / (CW / 8), hc = blockIdx.x * CW + (i % (CW / 8)) * 8;
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) a[e] = 0.f;
+      for (int j0 = 0; j0 < nj; j0 += CB) {
+        u32x4 dv[CB];
+        float wv[CB];
+#pragma unroll
+        for (int z = 0; z < CB; z++) {
+          const int jj = j0 + z;
+          if (jj < nj) {
+            dv[z] = jj == k && p.ys ? *(const u32x4*)(p.ys + (size_t)t * H + hc)
+                                    : __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                    rd, (int)((((size_t)t * (k + 1) + jj) * H + hc) * 2),
+                                                                    0, kSc1));
+            wv[z] = jj < k ? p.wt[t * k + jj] : p.sg[t];
+          }
+        }
+#pragma unroll
+        for (int z = 0; z < CB; z++)
+          if (j0 + z < nj)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+              a[e] = __builtin_fmaf(wv[z], bf2f((uint16_t)(dv[z][e / 2] >> (16 * (e & 1)))), a[e]);
+      }
+      u32x4* o = (u32x4*)(p.out + (size_t)t * H + hc);
+      const u32x4 ov = p.assign ? u32x4{0u, 0u, 0u, 0u} : *o;
+      u32x4 res;
+#pragma unroll
+      for (int e2 = 0; e2 < 4; e2++) {
+        float v[2];
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+          const int e = 2 * e2 + f;
+          v[f] = p.assign ? a[e] : bf2f((uint16_t)(ov[e2] >> (16 * f))) + bf2f(f2bf(a[e]));
+        }
+        res[e2] = pack_bf2(v[0], v[1]);
+      }
+      *o = res;
+    }
+    return;
+  }
+  for (int i = tid; i < T * CW; i += 256) {
+    const int t = i / CW, hc = blockIdx.x * CW + (i % CW);
+    // every slot's value and weight requested before the first is used, then summed in slot order
+    uint16_t dv[kMdecMaxK + 1];
+    float wv[kMdecMaxK + 1];
+#pragma unroll
+    for (int jj = 0; jj <= kMdecMaxK; jj++)
+      if (jj < nj) {
+        dv[jj] = jj == k && p.ys ? p.ys[(size_t)t * H + hc]
+                                 : __builtin_amdgcn_raw_buffer_load_b16(
+                                       rd, (int)((((size_t)t * (k + 1) + jj) * H + hc) * 2), 0, kSc1);
+        wv[jj] = jj < k ? p.wt[t * k + jj] : p.sg[t];
+      }
+    float a = 0.f;
+#pragma unroll
+    for (int jj = 0; jj <= kMdecMaxK; jj++)
+      if (jj < nj) a = __builtin_fmaf(wv[jj], bf2f(dv[jj]), a);
+    uint16_t* o = p.out + (size_t)t * H + hc;
+    *o = p.assign ? f2bf(a) : f2bf(bf2f(*o) + bf2f(f2bf(a)));
+  }
+}
+
 // ---- 4. down + combine ---------------------------------------------------------------------------------------------
 template <int RT, int SB>
 __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
@@ -478,7 +565,7 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    const unsigned arrivals = (unsigned)p.plan[0] + (p.sgu_wq ? 1u : 0u);
+    const unsigned arrivals = (unsigned)p.plan[0] + (p.has_sh ? 1u : 0u);
     const unsigned old = __hip_atomic_fetch_add(p.cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = old + 1 == arrivals;
     if (last) __hip_atomic_store(p.cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -486,74 +573,205 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   }
   __syncthreads();
   if (!s_last) return;
-  // the chunk's combine: every (token, column) of its 128 columns
-  const int nj = k + (p.sgu_wq || p.ys ? 1 : 0);
-  if (p.out16) {
-    // eight columns per thread (16-byte loads and stores; out and ys 16-byte aligned), kMdecCmbB slots' loads in
-    // flight at once, summed in slot order
-    for (int i = tid; i < T * 16; i += 256) {
-      const int t = i >> 4, hc = blockIdx.x * 128 + (i & 15) * 8;
-      float a[8];
+  mdec_combine(p, rd);
+}
+
+// ---- the T64 path (T <= 8 tokens): expert stacks in the T64 layout, each wave streaming one band --------------------
+// A wave streams its band's 1152-byte (group, band) tiles, 16 bytes per lane of one tile per group, in ping-pong
+// blocks of kMdtTB groups with the next block requested before the current one is used (non-temporal loads: each
+// tile is read once). The arithmetic is the qmv4 arithmetic of the MLX-layout kernels: codes as exact bf16 128 + q,
+// P = sum x (128 + q) by bf16 MFMA, s P + (b - 128 s) X per group with the group sums X of the staged token rows.
+constexpr int kMdtTB = 2;
+struct MdtBlk {
+  u32x4 w[kMdtTB];
+  uint32_t sb[kMdtTB];
+};
+// Stage rows [T][ng 64] of this slot's tokens (row t from src(t), zeros for null) into As (row stride lda) and their
+// 64-group sums into Xs[g][16] (rows past T zero), by the block's 256 threads.
+template <class Src>
+__device__ __forceinline__ void mdt_stage(Src src, int T, int ng, uint16_t* As, int lda, float* Xs) {
+  mdec_stage<kMdecStageU>(src, T, ng, As, lda, Xs, 0, 256);
+  for (int i = threadIdx.x; i < ng * kMdecMaxT; i += 256)
+    if ((i & (kMdecMaxT - 1)) >= T) Xs[i] = 0.f;
+}
+// One wave's product over groups [g0, g1) of NB bands, streamed as one sequence band by band (with NB > 1, g1 - g0
+// is a multiple of kMdtTB, so that a ping-pong block never spans two bands): tcol = the first band's first tile,
+// bstride = bytes
+// between the bands, gstride = bytes between groups; As / Xs staged from group g0 on. acc[b][r]: token row
+// mdec_row(r, h), column j of band b.
+template <int NB>
+__device__ __forceinline__ void mdt_band(const uint8_t* tcol, size_t bstride, size_t gstride, int g0, int g1,
+                                         const uint16_t* As, int lda, const float* Xs, int T, f32x16 (&acc)[NB]) {
+  const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+  const bool aok = j < T;
+  const uint16_t* arow = As + (size_t)(aok ? j : 0) * lda + 32 * h;
+  const int ng = g1 - g0, n = NB * ng;  // steps: (band, group) band-major
+  auto load_blk = [&](MdtBlk& B, int s) __attribute__((always_inline)) {
 #pragma unroll
-      for (int e = 0; e < 8; e++) a[e] = 0.f;
-      for (int j0 = 0; j0 < nj; j0 += kMdecCmbB) {
-        u32x4 dv[kMdecCmbB];
-        float wv[kMdecCmbB];
-#pragma unroll
-        for (int z = 0; z < kMdecCmbB; z++) {
-          const int jj = j0 + z;
-          if (jj < nj) {
-            dv[z] = jj == k && p.ys ? *(const u32x4*)(p.ys + (size_t)t * H + hc)
-                                    : __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                    rd, (int)((((size_t)t * (k + 1) + jj) * H + hc) * 2),
-                                                                    0, kSc1));
-            wv[z] = jj < k ? p.wt[t * k + jj] : p.sg[t];
-          }
-        }
-#pragma unroll
-        for (int z = 0; z < kMdecCmbB; z++)
-          if (j0 + z < nj)
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-              a[e] = __builtin_fmaf(wv[z], bf2f((uint16_t)(dv[z][e / 2] >> (16 * (e & 1)))), a[e]);
-      }
-      u32x4* o = (u32x4*)(p.out + (size_t)t * H + hc);
-      const u32x4 ov = p.assign ? u32x4{0u, 0u, 0u, 0u} : *o;
-      u32x4 res;
-#pragma unroll
-      for (int e2 = 0; e2 < 4; e2++) {
-        float v[2];
-#pragma unroll
-        for (int f = 0; f < 2; f++) {
-          const int e = 2 * e2 + f;
-          v[f] = p.assign ? a[e] : bf2f((uint16_t)(ov[e2] >> (16 * f))) + bf2f(f2bf(a[e]));
-        }
-        res[e2] = pack_bf2(v[0], v[1]);
-      }
-      *o = res;
+    for (int i = 0; i < kMdtTB; i++) {
+      const int q = min(s + i, n - 1), b = q / ng;
+      const uint8_t* t = tcol + (size_t)b * bstride + (size_t)(g0 + q - b * ng) * gstride;
+      B.w[i] = __builtin_nontemporal_load((const u32x4*)(t + 16 * lane));
+      B.sb[i] = __builtin_nontemporal_load((const uint32_t*)(t + kT64Codes + 4 * j));
     }
-    return;
-  }
-  for (int i = tid; i < T * 128; i += 256) {
-    const int t = i >> 7, hc = blockIdx.x * 128 + (i & 127);
-    // every slot's value and weight requested before the first is used, then summed in slot order
-    uint16_t dv[kMdecMaxK + 1];
-    float wv[kMdecMaxK + 1];
+  };
+  auto compute_blk = [&](const MdtBlk& B, int s) __attribute__((always_inline)) {
+    const int b = NB == 1 ? 0 : s / ng;  // the block's band
 #pragma unroll
-    for (int jj = 0; jj <= kMdecMaxK; jj++)
-      if (jj < nj) {
-        dv[jj] = jj == k && p.ys ? p.ys[(size_t)t * H + hc]
-                                 : __builtin_amdgcn_raw_buffer_load_b16(
-                                       rd, (int)((((size_t)t * (k + 1) + jj) * H + hc) * 2), 0, kSc1);
-        wv[jj] = jj < k ? p.wt[t * k + jj] : p.sg[t];
-      }
-    float a = 0.f;
+    for (int i = 0; i < kMdtTB; i++) {
+      if (s + i >= n) break;
+      const int gl = s + i - b * ng;
+      u32x4 af[4];
 #pragma unroll
-    for (int jj = 0; jj <= kMdecMaxK; jj++)
-      if (jj < nj) a = __builtin_fmaf(wv[jj], bf2f(dv[jj]), a);
-    uint16_t* o = p.out + (size_t)t * H + hc;
-    *o = p.assign ? f2bf(a) : f2bf(bf2f(*o) + bf2f(f2bf(a)));
+      for (int t = 0; t < 4; t++) af[t] = aok ? *(const u32x4*)(arow + (size_t)gl * 64 + 8 * t) : u32x4{0u, 0u, 0u, 0u};
+      const float4 x0 = *(const float4*)(Xs + gl * kMdecMaxT + 4 * h);
+      f32x16 P = zero16();
+#pragma unroll
+      for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], t64_off128(B.w[i][t]), P);
+      const float xs[4] = {x0.x, x0.y, x0.z, x0.w};
+      const float sc = bf2f((uint16_t)(B.sb[i] & 0xFFFFu)), bi = bf2f((uint16_t)(B.sb[i] >> 16));
+      const float bp = __builtin_fmaf(-128.f, sc, bi);
+#pragma unroll
+      for (int bb = 0; bb < NB; bb++)
+        if (bb == b)
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[bb][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[bb][r]));
+    }
+  };
+  MdtBlk b0, b1;
+  load_blk(b0, 0);
+  for (int s = 0;; s += 2 * kMdtTB) {
+    load_blk(b1, min(s + kMdtTB, n - 1));
+    compute_blk(b0, s);
+    if (s + kMdtTB >= n) break;
+    load_blk(b0, min(s + 2 * kMdtTB, n - 1));
+    compute_blk(b1, s + kMdtTB);
+    if (s + 2 * kMdtTB >= n) break;
   }
+}
+
+// Gate/up + SwiGLU: block = (64 h columns c, slot u, K split z). Waves 0, 1 stream gate bands 2c, 2c + 1 of the
+// slot's expert, waves 2, 3 the matching up bands I / 32 + 2c, + 1, over groups [z gps, (z + 1) gps). With one split
+// the block pairs gate and up through LDS and writes h; with several each block writes its fp32 sums (write-through)
+// and the last of a (slot, c)'s splits (a counter in the workspace header) sums them in split order and writes h.
+__global__ __launch_bounds__(256) void k_mdt_gu(MdecArgs p) {
+  extern __shared__ __align__(16) uint16_t lds[];
+  __shared__ float red[4][64][4];
+  __shared__ unsigned s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
+  const int c = blockIdx.x, u = blockIdx.y, z = blockIdx.z, T = p.T, H = p.H, I = p.I, nct = I / 64;
+  const MdecSlot sl = mdec_slot(p, u);
+  if (!sl.live) return;  // block-uniform, before any barrier
+  const int G = H / kGroup, g0 = z * p.gps, g1 = min(G, g0 + p.gps), ng = g1 - g0, lda = ng * 64 + 8;
+  uint16_t* As = lds;
+  float* Xs = (float*)(lds + (size_t)T * lda + 8);  // 16-byte aligned: T lda + 8 is a multiple of 8
+  mdt_stage([&](int t) { return p.x + (size_t)t * H + (size_t)g0 * 64; }, T, ng, As, lda, Xs);
+  __syncthreads();
+  const uint8_t* stack = sl.e < 0 ? p.sgu_t : p.egu_t + (size_t)sl.e * p.gu_eb;
+  const int band = wave < 2 ? 2 * c + wave : I / 32 + 2 * c + wave - 2, nb = 2 * I / 32;
+  f32x16 accs[1] = {zero16()};
+  mdt_band<1>(stack + (size_t)band * kT64Tile, 0, (size_t)nb * kT64Tile, g0, g1, As, lda, Xs, T, accs);
+  f32x16& acc = accs[0];
+  if (p.gS > 1) {  // this split's sums, then the (slot, c) tile's last split sums them all
+    const __amdgpu_buffer_rsrc_t rg = part_rsrc(p.gpart, p.gpart_bytes);
+    const int slot = (u * nct + c) * p.gS + z;
+    const u32x4 v = {__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]), __float_as_uint(acc[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(v, rg, (int)((((size_t)slot * 4 + wave) * 64 + lane) * 16), 0, kSc1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      unsigned* ctr = p.cnt + u * nct + c;
+      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old + 1 == (unsigned)p.gS;
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int z0 = 0; z0 < p.gS; z0 += 4) {  // four splits' loads in flight, summed in split order
+      u32x4 w[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (z0 + q < p.gS)
+          w[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rg, (int)(((((size_t)(u * nct + c) * p.gS + z0 + q) * 4 + wave) * 64 +
+                                                          lane) * 16), 0, kSc1));
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (z0 + q < p.gS)
+#pragma unroll
+          for (int r = 0; r < 4; r++) a[r] += __uint_as_float(w[q][r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] = a[r];
+  }
+  // gate (waves 0, 1) with up (waves 2, 3): h = silu(bf16(gate)) bf16(up) for the tokens that picked the slot
+#pragma unroll
+  for (int r = 0; r < 4; r++) red[wave][lane][r] = acc[r];
+  __syncthreads();
+  if (wave >= 2) return;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int t = mdec_row(r, h), pk = mdec_pick(p, u, t);
+    if (pk < 0) continue;
+    const float g = red[wave][lane][r], v = red[wave + 2][lane][r];
+    p.act[((size_t)t * (p.k + 1) + pk) * I + 64 * c + 32 * wave + j] = f2bf(swiglu_f(bf2f(f2bf(g)), bf2f(f2bf(v))));
+  }
+}
+
+// Down + combine: block = (128 NB output columns, slot u); wave w streams bands NB (4 x + w) .. + NB - 1
+// of the slot's down rows over all I / 64 groups against the act rows of the tokens that picked it (the staging and
+// the block's fixed costs shared by more weight bytes), d[t][pick][h] = bf16(result) written through; the last block
+// of a chunk (a counter in the workspace header) combines its columns, as k_mdec_dn.
+template <int NB>
+__global__ __launch_bounds__(256) void k_mdt_dn(MdecArgs p) {
+  extern __shared__ __align__(16) uint16_t lds[];
+  __shared__ unsigned s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
+  const int u = blockIdx.y, T = p.T, I = p.I, H = p.H, Gi = I / kGroup, k = p.k;
+  const MdecSlot sl = mdec_slot(p, u);
+  if (!sl.live) return;  // block-uniform, before any barrier
+  const int lda = I + 8;
+  uint16_t* As = lds;
+  float* Xs = (float*)(lds + (size_t)T * lda + 8);
+  mdt_stage(
+      [&](int t) -> const uint16_t* {
+        const int pk = mdec_pick(p, u, t);
+        return pk < 0 ? nullptr : p.act + ((size_t)t * (k + 1) + pk) * I;
+      },
+      T, Gi, As, lda, Xs);
+  __syncthreads();
+  const uint8_t* stack = sl.e < 0 ? p.sdn_t : p.edn_t + (size_t)sl.e * p.dn_eb;
+  const int band = (blockIdx.x * 4 + wave) * NB, nb = H / 32;
+  f32x16 acc[NB];
+#pragma unroll
+  for (int bb = 0; bb < NB; bb++) acc[bb] = zero16();
+  mdt_band<NB>(stack + (size_t)band * kT64Tile, kT64Tile, (size_t)nb * kT64Tile, 0, Gi, As, lda, Xs, T, acc);
+  const __amdgpu_buffer_rsrc_t rd = part_rsrc(p.d, p.d_bytes);
+#pragma unroll
+  for (int bb = 0; bb < NB; bb++) {
+    const int h0 = (band + bb) * 32;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int t = mdec_row(r, h), pk = mdec_pick(p, u, t);
+      if (pk >= 0)
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(acc[bb][r]), rd,
+                                              (int)((((size_t)t * (k + 1) + pk) * H + h0 + j) * 2), 0, kSc1);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned arrivals = (unsigned)p.plan[0] + (p.has_sh ? 1u : 0u);
+    const unsigned old = __hip_atomic_fetch_add(p.cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1 == arrivals;
+    if (last) __hip_atomic_store(p.cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  mdec_combine<4, 128 * NB>(p, rd);  // a small batch: fewer registers, more of this kernel's waves in flight
 }
 
 // ---- host ------------------------------------------------------------------------------------------------------------
@@ -564,7 +782,18 @@ static int mdec_ks(int H) {
   return 0;
 }
 
-MdecLayout mdec_layout(int T, int H, int I, int E, int k) {
+// The T64 path's gate/up K split: about 6 waves per SIMD over the T k + 1 slots (most of them live), whole blocks of
+// kMdtTB groups and at least two per split, and a counter per (slot, 64-column tile) below the router's.
+static void mdt_split(int T, int H, int I, int k, int& S, int& gps) {
+  const int slots = T * k + 1, nct = I / 64, G = H / kGroup;
+  S = (int)std::min<long>((6144l + (long)slots * nct * 4 - 1) / ((long)slots * nct * 4), G / (2 * kMdtTB));
+  if (S < 1 || (long)slots * nct > kWsCounters - 2) S = 1;
+  gps = (G + S - 1) / S;
+  gps = (gps + kMdtTB - 1) / kMdtTB * kMdtTB;
+  S = (G + gps - 1) / gps;
+}
+
+MdecLayout mdec_layout(int T, int H, int I, int E, int k, bool t64) {
   MdecLayout L{};
   auto take = [&](size_t& off, size_t bytes) {
     off = L.total;
@@ -578,6 +807,11 @@ MdecLayout mdec_layout(int T, int H, int I, int E, int k) {
   take(L.idx, (size_t)T * k * 4);
   take(L.wt, (size_t)T * k * 4);
   take(L.sg, (size_t)T * 4);
+  L.gS = 1, L.gps = H / kGroup;
+  if (t64) {
+    mdt_split(T, H, I, k, L.gS, L.gps);
+    take(L.gpart, L.gS > 1 ? (size_t)(T * k + 1) * (I / 64) * L.gS * 4 * 64 * 16 : 0);
+  }
   return L;
 }
 
@@ -597,6 +831,24 @@ static int launch_mdec(const MdecArgs& p, const MdecCall& c, hipStream_t st) {
     }
     return IFD_OK;
   };
+  if (p.egu_t) {  // the T64 path (RT = 4: up to 8 tokens)
+    const size_t glds = ((size_t)c.T * (p.gps * 64 + 8) + 8) * 2 + (size_t)p.gps * kMdecMaxT * 4;
+    IFD_TRY(allow_lds((const void*)k_mdt_gu, glds, "gate_up"));
+    hipLaunchKernelGGL(k_mdt_gu, dim3(c.I / 64, slots, p.gS), dim3(256), glds, st, p);
+    IFD_TRY(check_launch("moe_decode gate_up"));
+    const size_t dlds = ((size_t)c.T * (c.I + 8) + 8) * 2 + (size_t)(c.I / kGroup) * kMdecMaxT * 4;
+    // two bands per wave when one per wave would give more than four blocks per CU (config 4 at T = 8: 61.3 against
+    // 66.1 us for the whole decode; at T <= 4 one band per wave keeps more blocks in flight: T = 1 / 2 / 4 32.9 /
+    // 37.1 / 46.6 against 36.0 / 39.9 / 47.6 us) and a band's groups fill whole ping-pong blocks
+    if ((long)slots * (c.H / 128) > 4l * cu_count() && (c.I / kGroup) % kMdtTB == 0) {
+      IFD_TRY(allow_lds((const void*)k_mdt_dn<2>, dlds, "down"));
+      hipLaunchKernelGGL(k_mdt_dn<2>, dim3(c.H / 256, slots), dim3(256), dlds, st, p);
+    } else {
+      IFD_TRY(allow_lds((const void*)k_mdt_dn<1>, dlds, "down"));
+      hipLaunchKernelGGL(k_mdt_dn<1>, dim3(c.H / 128, slots), dim3(256), dlds, st, p);
+    }
+    return check_launch("moe_decode down");
+  }
   const size_t glds = mdec_gu_lds(c.T, RT);
   const void* gu = p.sh_bits == 8 ? (const void*)k_mdec_gu<RT, 8> : (const void*)k_mdec_gu<RT, 4>;
   IFD_TRY(allow_lds(gu, glds, "gate_up"));
@@ -628,7 +880,10 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
     return IFD_OK;
   }
   if (c.T > kMdecMaxT) return fail(IFD_ERR_UNSUPPORTED, "moe_decode takes at most %d tokens", kMdecMaxT);
-  const MdecLayout L = mdec_layout(c.T, c.H, c.I, c.E, c.k);
+  const bool t64 = c.egu_t64 != nullptr;
+  if (t64 && (c.T > 8 || c.routed || c.sh_bits != 4 || (c.sgu_t64 == nullptr) != (c.sdn_t64 == nullptr)))
+    return fail(IFD_ERR_UNSUPPORTED, "moe_decode on T64 stacks: up to 8 tokens, router in, 4-bit shared expert");
+  const MdecLayout L = mdec_layout(c.T, c.H, c.I, c.E, c.k, t64);
   if (!ws || ws_bytes < L.total || !cnt)
     return fail(IFD_ERR_WORKSPACE, "moe_decode needs %zu bytes of workspace after the header, got %zu", L.total,
                 ws_bytes);
@@ -643,6 +898,7 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
   p.sgu_wq = c.sgu_wq, p.sgu_s = c.sgu_s, p.sgu_b = c.sgu_b;
   p.sdn_wq = c.sdn_wq, p.sdn_s = c.sdn_s, p.sdn_b = c.sdn_b;
   p.sh_bits = c.sh_bits;
+  p.has_sh = c.sgu_wq || c.sgu_t64 ? 1 : 0;
   p.routed = c.routed, p.ys = (const uint16_t*)c.ys;
   p.out16 = ((uintptr_t)c.out % 16 == 0 && (uintptr_t)c.ys % 16 == 0) ? 1 : 0;
   p.out = (uint16_t*)c.out;
@@ -657,6 +913,14 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
   p.d = (uint16_t*)(w + L.d);
   p.d_bytes = (uint32_t)((size_t)c.T * (c.k + 1) * c.H * 2);
   p.cnt = cnt;
+  if (t64) {
+    p.egu_t = (const uint8_t*)c.egu_t64, p.edn_t = (const uint8_t*)c.edn_t64;
+    p.sgu_t = (const uint8_t*)c.sgu_t64, p.sdn_t = (const uint8_t*)c.sdn_t64;
+    p.gu_eb = t64_bytes(2 * c.I, c.H), p.dn_eb = t64_bytes(c.H, c.I);
+    p.gS = L.gS, p.gps = L.gps;
+    p.gpart = (float*)(w + L.gpart);
+    p.gpart_bytes = (uint32_t)((size_t)(c.T * c.k + 1) * (c.I / 64) * L.gS * 4 * 64 * 16);
+  }
   // vector scale / bias loads: every chunk holds 8 groups (the wave's group count a multiple of 8) and rows start
   // 16-byte aligned
   const bool shared = c.sgu_wq != nullptr;

@@ -203,6 +203,7 @@ struct Qwen35 {
       for (int T = 1; T <= max_rows; T++) {
         need = std::max(need, ifd_moe_dispatch_workspace(T * k, E));
         if (T <= 16) need = std::max(need, ifd_moe_decode_workspace(T, H, I, E, k));
+        if (T <= 8) need = std::max(need, ifd_moe_decode_t64_workspace(T, H, I, E, k));
         need = std::max(need, ifd_gemm_w8_workspace(T, E + 1, H));  // an 8-bit router's logits
         if (shared_inter > 0) {
           need = std::max(need, ifd_gemm_w4_workspace(T, 2 * shared_inter, H));
@@ -433,6 +434,13 @@ struct Qwen35 {
 
   // The sorted route on the experts' T64 stacks (ifd_moe_gather_qmm_t64: the same bf16(s q + b) dequant and fp32 sums
   // as the MLX-layout gathered GEMM): both stacks 4-bit with T64 copies, H and I multiples of 256.
+  // On the decode route, the T64 copies of the routed experts (and of a 4-bit shared expert, if any) are streamed
+  // in place of the MLX-layout stacks, up to 8 tokens: the same per-row qmv4 arithmetic
+  bool moe_decode_t64(const Layer& ly, int T) const {
+    const bool has_shared = ly.gate_up.N > 0;
+    return moe_decode_route(ly, T) && T <= 8 && ly.egu.t64 && ly.edown.t64 &&
+           (!has_shared || (ly.gate_up.bits == 4 && ly.gate_up.t64 && ly.down.t64));
+  }
   bool moe_t64_route(const Layer& ly) const {
     return ly.egu.t64 && ly.edown.t64 && ly.egu.bits == 4 && ly.edown.bits == 4 && cfg.hidden % 256 == 0 &&
            cfg.moe_inter % 256 == 0;
@@ -492,6 +500,19 @@ struct Qwen35 {
       const size_t need = ifd_moe_decode_workspace(T, H, I, E, k);
       if (need > splitk_bytes) die("encode_moe", "scratch smaller than the decode MoE needs");
       const int sbits = has_shared ? ly.gate_up.bits : 4;
+      if (moe_decode_t64(ly, T)) {
+        if (ifd_moe_decode_t64_workspace(T, H, I, E, k) > splitk_bytes)
+          die("encode_moe", "scratch smaller than the decode MoE needs");
+        if (r8) router8_logits(0);
+        ok(ifd_moe_decode_t64(xn.ptr<void>(), T, H, r8 ? nullptr : ly.router.wq.ptr<void>(),
+                              r8 ? rlog.ptr<float>() : nullptr, E, k, 1, E1 > E ? 1 : 0, ly.egu.t64.ptr<void>(),
+                              ly.edown.t64.ptr<void>(), I, has_shared ? ly.gate_up.t64.ptr<void>() : nullptr,
+                              has_shared ? ly.down.t64.ptr<void>() : nullptr, x.ptr<void>(), 0, ridx.ptr<int>(),
+                              rw.ptr<float>(), rsg.ptr<float>(), r8 ? nullptr : rlog.ptr<float>(), splitk.ptr<void>(),
+                              splitk_bytes, e.stream),
+           "encode_moe");
+        return;
+      }
       if (r8) {
         router8_logits(0);
         ok(ifd_moe_decode_logits_ex(rlog.ptr<float>(), xn.ptr<void>(), T, H, E, k, 1, E1 > E ? 1 : 0,

@@ -472,6 +472,33 @@ def moe_decode(xn: torch.Tensor, router: Optional[torch.Tensor], egu: MoeW, edn:
     return out, idx, wt, sg, logits
 
 
+def moe_decode_t64(xn: torch.Tensor, router: Optional[torch.Tensor], egu: T64Stack, edn: T64Stack, k: int,
+                   shared: Optional[tuple] = None, shared_gate: bool = True, norm: bool = True,
+                   out: Optional[torch.Tensor] = None, assign: bool = True, logits_in: Optional[torch.Tensor] = None):
+    """The decode MoE on T64 stacks (T <= 8): shared = (T64Linear gate_up [2I, H], T64Linear down [H, I]), 4-bit.
+    With logits_in (fp32 [T, E + shared_gate]) the router is not read. Returns (out, idx, wt, sg, logits)."""
+    T, H = xn.shape
+    E, I = egu.E, egu.N // 2
+    dev = xn.device
+    if out is None:
+        out = torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    wt = torch.empty((T, k), dtype=torch.float32, device=dev)
+    sg = torch.empty((T,), dtype=torch.float32, device=dev)
+    logits = torch.empty((T, E + (1 if shared_gate else 0)), dtype=torch.float32, device=dev)
+    ws = workspace(lib().ifd_moe_decode_t64_workspace(T, H, I, E, k), dev)
+    sgu, sdn = shared if shared is not None else (None, None)
+    if logits_in is not None:
+        assert logits_in.dtype == torch.float32 and logits_in.is_contiguous()
+        assert logits_in.shape == (T, E + (1 if shared_gate else 0))
+    check(lib().ifd_moe_decode_t64(
+        _p(xn), T, H, _p(router) if logits_in is None else None, _p(logits_in) if logits_in is not None else None, E,
+        k, 1 if norm else 0, 1 if shared_gate else 0, _p(egu.wt), _p(edn.wt), I, _p(sgu.wt) if sgu else None,
+        _p(sdn.wt) if sdn else None, _p(out), 1 if assign else 0, _p(idx), _p(wt), _p(sg),
+        _p(logits) if logits_in is None else None, _p(ws), ws.numel(), _stream()))
+    return out, idx, wt, sg, (logits if logits_in is None else logits_in)
+
+
 def mlp_decode(x: torch.Tensor, norm_w: torch.Tensor, eps: float, gu: T64Linear, dn: T64Linear) -> torch.Tensor:
     """The dense decode MLP block in place: x += down(SwiGLU(gate_up(rmsnorm(x)))) (T64 weights)."""
     M, H = x.shape

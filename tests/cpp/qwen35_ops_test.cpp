@@ -553,6 +553,21 @@ void test_encode_moe(std::mt19937& rng) {
                   0, 0, 1, sgu_t64, nullptr),
      "pack_t64");
   const QLinear sgu_mlx = ly.gate_up;
+  // T64 copies of the routed stacks and of the shared down: the decode route then streams them (up to 8 tokens) when
+  // the shared expert has both copies
+  void* et64[3] = {};
+  {
+    const int NN[3] = {2 * I, H, H}, KK[3] = {H, I, Is}, EE[3] = {E, E, 1};
+    const BufRef wq[3] = {ly.egu.wq, ly.edown.wq, ly.down.wq}, sc[3] = {ly.egu.s, ly.edown.s, ly.down.s},
+                 bi[3] = {ly.egu.b, ly.edown.b, ly.down.b};
+    for (int i = 0; i < 3; i++) {
+      hip_ok(hipMalloc(&et64[i], ifd_t64_bytes(NN[i], KK[i], EE[i])), "t64");
+      ok(ifd_pack_t64(wq[i].ptr<uint32_t>(), sc[i].ptr<uint16_t>(), bi[i].ptr<uint16_t>(), NN[i], KK[i], 0, 0u, EE[i],
+                      et64[i], nullptr),
+         "pack_t64");
+    }
+    hip_ok(hipDeviceSynchronize(), "pack_t64");
+  }
   // an 8-bit router [E + 1, H] (the shared gate last), w = s q + b with b = -128 s
   std::vector<uint32_t> r8wq((size_t)(E + 1) * H / 4);
   std::vector<uint16_t> r8s((size_t)(E + 1) * H / 64), r8b(r8s.size());
@@ -586,20 +601,27 @@ void test_encode_moe(std::mt19937& rng) {
   router8.E = 1, router8.N = E + 1, router8.K = H, router8.bits = 8;
   struct Case {
     int T, max_rows;
-    bool t64, r8, s8 = false;
+    bool t64, r8, s8 = false, et64 = false;
   };
   // the decode route (up to qmv_max tokens; up to 8 with the 8-bit router), the per-row route below 128 routed rows
   // (T <= 31 at top-4, 16 tokens per launch group), the sorted route beyond; the fused T64 shared gate/up; state
-  // allocated for more rows than the call (its scratch covers every row count); the 8-bit router on all three
+  // allocated for more rows than the call (its scratch covers every row count); the 8-bit router on all three; the
+  // decode route on the routed experts' T64 copies (et64), streamed when the shared expert has both T64 copies
+  // (4-bit) and on the MLX layout otherwise
   for (const Case cs : {Case{1, 1, false, false}, Case{24, 24, false, false}, Case{31, 40, false, true},
                         Case{3, 3, false, false}, Case{8, 8, false, false}, Case{16, 16, false, false},
                         Case{100, 100, false, false}, Case{16, 16, true, false}, Case{100, 100, true, false},
                         Case{100, 256, true, false}, Case{3, 3, false, true}, Case{12, 12, false, true},
-                        Case{40, 40, false, true}, Case{3, 3, false, false, true}, Case{8, 8, false, true, true}}) {
+                        Case{40, 40, false, true}, Case{3, 3, false, false, true}, Case{8, 8, false, true, true},
+                        Case{1, 1, true, false, false, true}, Case{2, 4, true, false, false, true},
+                        Case{8, 8, true, true, false, true}, Case{5, 5, false, true, false, true},
+                        Case{8, 8, false, true, true, true}}) {
     const int T = cs.T;
     ly.gate_up = cs.s8 ? sgu8_d : sgu_mlx;
     ly.down = cs.s8 ? sdn8_d : sdn_mlx;
     if (cs.t64) ly.gate_up.t64 = BufRef(sgu_t64);
+    ly.egu.t64 = cs.et64 ? BufRef(et64[0]) : BufRef(), ly.edown.t64 = cs.et64 ? BufRef(et64[1]) : BufRef();
+    if (cs.et64 && !cs.s8) ly.down.t64 = BufRef(et64[2]);
     ly.router = cs.r8 ? router8 : router16;
     Qwen35 m(c, cs.max_rows, Is, 0);
     Enc e;
@@ -616,10 +638,12 @@ void test_encode_moe(std::mt19937& rng) {
     const std::string tag = " T=" + std::to_string(T) + (cs.max_rows > T ? " of " + std::to_string(cs.max_rows) : "") +
                             (ly.gate_up.t64 ? " (T64 shared gate/up)" : "") + (cs.r8 ? " (8-bit router)" : "") +
                             (cs.s8 ? " (8-bit shared expert)" : "") +
-                            (dec ? " [decode]" : rows ? " [per-row]" : " [sorted]");
+                            (dec ? (m.moe_decode_t64(ly, T) ? " [decode, T64]" : " [decode]")
+                                 : rows ? " [per-row]" : " [sorted]");
     // the reference's routes: moe2 up to 8 tokens with an 8-bit router (and here up to qmv_max tokens with any),
     // the per-row products below 128 routed rows, the sorted path from there
-    report(dec == (T <= m.qmv_max || (T <= 8 && cs.r8)) && rows == (!dec && T * k < 128),
+    report(dec == (T <= m.qmv_max || (T <= 8 && cs.r8)) && rows == (!dec && T * k < 128) &&
+               m.moe_decode_t64(ly, T) == (dec && cs.et64 && cs.t64 && !cs.s8),
            "encode_moe route" + tag, 0);
     if (cs.r8) {  // the logits against the oracle's qmv8 on the GPU's normalised rows
       std::vector<float> yl((size_t)T * (E + 1));
@@ -670,6 +694,7 @@ void test_encode_moe(std::mt19937& rng) {
            "encode_moe x += moe(xn) (end to end)" + tag, g_raw);
   }
   (void)hipFree(sgu_t64);
+  for (void* q : et64) (void)hipFree(q);
   (void)hipFree(router8.wq.buf), (void)hipFree(router8.s.buf), (void)hipFree(router8.b.buf);
   for (void* q : {sgu8_d.wq.buf, sgu8_d.s.buf, sgu8_d.b.buf, sdn8_d.wq.buf, sdn8_d.s.buf, sdn8_d.b.buf})
     (void)hipFree(q);
@@ -748,11 +773,17 @@ void run_moe_t64(MoeLayer& L, int T, int max_rows, int shared, int check, int nt
   const auto wt = download<float>(m.rw, (size_t)T * k);
   const auto sg = download<float>(m.rsg, (size_t)T);
   const bool dec = m.moe_decode_route(ly, T), t64 = m.moe_t64_route(ly), fold = m.shared_as_expert(ly, T);
+  const bool dt64 = m.moe_decode_t64(ly, T);
   const std::string tag = " T=" + std::to_string(T) + " H=" + std::to_string(H) + " E=" + std::to_string(E) +
                           " k=" + std::to_string(k) + " I=" + std::to_string(I) +
-                          (shared == 0 ? " (no shared expert)" : fold ? " (shared = expert E)" : " (shared via gemm)") +
-                          (dec ? " [decode]" : t64 ? " [sorted, T64]" : " [sorted, MLX]");
-  report(!dec && t64 && fold == (shared == 1), "encode_moe takes the T64 sorted route" + tag, 0);
+                          (shared == 0 ? " (no shared expert)"
+                           : dec       ? (shared == 1 ? " (shared on T64)" : " (shared on the MLX layout)")
+                           : fold      ? " (shared = expert E)"
+                                       : " (shared via gemm)") +
+                          (dec ? (dt64 ? " [decode, T64]" : " [decode]") : t64 ? " [sorted, T64]" : " [sorted, MLX]");
+  // up to qmv_max tokens the decode route, on the T64 copies when the shared expert (if any) has them too
+  if (T <= m.qmv_max) report(dec && dt64 == (shared != 2), "encode_moe takes the decode route" + tag, 0);
+  else report(!dec && t64 && fold == (shared == 1), "encode_moe takes the T64 sorted route" + tag, 0);
   // rmsnorm: within one bf16 step of the oracle (the sum of squares runs in another order)
   std::vector<uint16_t> xr((size_t)T * H);
   orc_rmsnorm(x0.data(), H, L.post.data(), xr.data(), H, T, H, c.eps);
@@ -785,10 +816,15 @@ void run_moe_t64(MoeLayer& L, int T, int max_rows, int shared, int check, int nt
   // the shared expert as expert E gets the gathered GEMM's qmm rounding; through gemm() on the MLX layout, the decode
   // GEMV arithmetic up to 32 rows (ifd_gemm_w4) and qmm's above
   const int shared_qmv = shared == 2 && T <= 32 ? 1 : 0;
-  orc_moe_experts(xs.data(), C, H, I, E, k, si.data(), sw.data(), ss.data(), L.egu.wq.data(), L.egu.s.data(),
-                  L.egu.b.data(), L.edn.wq.data(), L.edn.s.data(), L.edn.b.data(),
-                  shared ? L.sgu.wq.data() : nullptr, L.sgu.s.data(), L.sgu.b.data(), L.sdn.wq.data(), L.sdn.s.data(),
-                  L.sdn.b.data(), shared_qmv, want.data(), 0, nthreads);
+  if (dec)  // the decode GEMV arithmetic for every expert product
+    orc_moe_decode(xs.data(), C, H, I, k, si.data(), sw.data(), ss.data(), L.egu.wq.data(), L.egu.s.data(),
+                   L.egu.b.data(), L.edn.wq.data(), L.edn.s.data(), L.edn.b.data(), shared ? L.sgu.wq.data() : nullptr,
+                   L.sgu.s.data(), L.sgu.b.data(), L.sdn.wq.data(), L.sdn.s.data(), L.sdn.b.data(), want.data(), 0);
+  else
+    orc_moe_experts(xs.data(), C, H, I, E, k, si.data(), sw.data(), ss.data(), L.egu.wq.data(), L.egu.s.data(),
+                    L.egu.b.data(), L.edn.wq.data(), L.edn.s.data(), L.edn.b.data(),
+                    shared ? L.sgu.wq.data() : nullptr, L.sgu.s.data(), L.sgu.b.data(), L.sdn.wq.data(),
+                    L.sdn.s.data(), L.sdn.b.data(), shared_qmv, want.data(), 0, nthreads);
   std::vector<float> wf(want.size());
   for (size_t i = 0; i < want.size(); i++) wf[i] = bf2f(want[i]);
   // a chain of bf16 stages on both sides, compared end to end (the stages are checked one by one at the bar in
@@ -807,6 +843,10 @@ void test_encode_moe_t64(std::mt19937& rng) {
   run_moe_t64(L, 300, 300, 1, 1 << 30, 0, rng);
   run_moe_t64(L, 300, 300, 2, 1 << 30, 0, rng);
   run_moe_t64(L, 64, 64, 0, 1 << 30, 0, rng);
+  // the decode route on the same stacks: the shared expert on its T64 copies, on the MLX layout, or absent
+  run_moe_t64(L, 1, 1, 1, 1 << 30, 0, rng);
+  run_moe_t64(L, 2, 8, 2, 1 << 30, 0, rng);
+  run_moe_t64(L, 2, 2, 0, 1 << 30, 0, rng);
 }
 
 // The QA8 routes (QA8=1): gemm() of at least qa8_min rows on the qa8 int8 rows (MLX layout, unflipped and flipped, and

@@ -422,6 +422,68 @@ def test_moe_decode_out_alignment(T):
     assert not np.array_equal(g.host(a16), g.host(x0))
 
 
+@pytest.mark.parametrize("T,E,H,I,k,shared,shared_gate,assign", [
+    (1, 512, 2048, 512, 10, True, True, True),     # gate/up on 8 K splits
+    (4, 512, 2048, 512, 10, True, False, False),
+    (8, 512, 2048, 512, 10, True, True, True),     # 3 K splits
+    (3, 32, 512, 128, 4, False, False, True),      # no shared expert; short K (2 splits of 4 groups)
+    (8, 8, 1024, 256, 3, True, False, False),      # most experts picked by several tokens
+    (5, 16, 512, 192, 2, True, False, True),       # I = 192: three groups per down band, a ping-pong block across bands
+])
+def test_moe_decode_t64(T, E, H, I, k, shared, shared_gate, assign):
+    """The decode MoE on T64 stacks against the MLX-layout decode MoE on the same weights (the same router kernel:
+    routing bit-exact; expert sums in another order: within two bf16 steps of a few elements) and against the
+    oracle's composition; a second call gives the same bits (the split and combine counters reset themselves)."""
+    g, ops = _gu(), _ops()
+    seed = 180 + T + E
+    egu, edn = (_config4_stacks()[:2] if (E, H, I) == (512, 2048, 512)
+                else (experts(E, 2 * I, H, seed=seed), experts(E, H, I, seed=seed + 1)))
+    sgu = experts(1, 2 * I, H, seed=seed + 2)
+    sdn = experts(1, H, I, seed=seed + 3)
+    R = g.dev(router(E + (1 if shared_gate else 0), H, seed=seed + 4))
+    xn = gen.activations(T, H, seed=seed + 5)
+    x0 = gen.activations(T, H, seed=seed + 6)
+    EGU, EDN = g.moew(*egu), g.moew(*edn)
+    sh = (g.qlinear(sgu[0][0], sgu[1][0], sgu[2][0]), g.qlinear(sdn[0][0], sdn[1][0], sdn[2][0])) if shared else None
+    sh_t = (ops.pack_t64(sh[0]), ops.pack_t64(sh[1])) if shared else None
+    TGU, TDN = ops.pack_t64_stack(EGU), ops.pack_t64_stack(EDN)
+    m_out, m_idx, m_wt, _, _ = ops.moe_decode(g.dev(xn), R, EGU, EDN, k, shared=sh, shared_gate=shared_gate,
+                                              out=g.dev(x0), assign=assign)
+    outs = []
+    for _ in range(2):
+        out, idx, wt, sg, logits = ops.moe_decode_t64(g.dev(xn), R, TGU, TDN, k, shared=sh_t,
+                                                      shared_gate=shared_gate, out=g.dev(x0), assign=assign)
+        torch.cuda.synchronize()
+        outs.append(g.host(out))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(g.host(idx), g.host(m_idx)) and np.array_equal(g.host(wt), g.host(m_wt))
+    got, mlx = gen.bf16_to_f32(outs[0]), gen.bf16_to_f32(g.host(m_out))
+    scale = max(float(np.abs(mlx).max()), 1e-6)
+    assert np.abs(got - mlx).max() <= 2 ** -6 * scale, "T64 and MLX-layout decode beyond summation-order rounding"
+    ri, rw, rs = orc.moe_route(g.host(logits), E, k, shared_gate=shared_gate)
+    assert np.array_equal(g.host(idx), ri)
+    shw = ((sgu[0][0], sgu[1][0], sgu[2][0]), (sdn[0][0], sdn[1][0], sdn[2][0])) if shared else None
+    ref = orc.moe_decode(xn, ri, rw, rs, egu, edn, shw, I, out=x0, assign=assign)
+    gen.check_bf16(outs[0], ref, 1e-2, ("t64", T, E, H, I, k), ref_is_bf16=True, composition=True)
+
+
+def test_moe_decode_t64_logits_in():
+    """With the caller's fp32 logits (an 8-bit router's) the T64 decode routes them as the MLX-layout decode does."""
+    g, ops = _gu(), _ops()
+    T, E, H, I, k = 2, 64, 512, 128, 4
+    egu, edn = experts(E, 2 * I, H, seed=190), experts(E, H, I, seed=191)
+    EGU, EDN = g.moew(*egu), g.moew(*edn)
+    lg = g.dev((np.random.default_rng(192).standard_normal((T, E)) * 0.5).astype(np.float32))
+    xn = g.dev(gen.activations(T, H, seed=193))
+    m_out, m_idx, _, _, _ = ops.moe_decode(xn, None, EGU, EDN, k, shared_gate=False, logits_in=lg)
+    out, idx, _, _, _ = ops.moe_decode_t64(xn, None, ops.pack_t64_stack(EGU), ops.pack_t64_stack(EDN), k,
+                                           shared_gate=False, logits_in=lg)
+    torch.cuda.synchronize()
+    assert np.array_equal(g.host(idx), g.host(m_idx))
+    got, mlx = gen.bf16_to_f32(g.host(out)), gen.bf16_to_f32(g.host(m_out))
+    assert np.abs(got - mlx).max() <= 2 ** -6 * max(float(np.abs(mlx).max()), 1e-6)
+
+
 def test_moe_decode_no_shared_expert_long_k():
     """No shared expert; I = 1152 (two K chunks of 8 groups in the down kernel), H = 4608 (gate/up chunks too), k = 16."""
     _decode_case(3, 64, 4608, 1152, 16, False, False, seed=150)

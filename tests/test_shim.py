@@ -58,14 +58,17 @@ def test_device_loaders_upload_and_gemm(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T", [16, 128, 2048])
+@pytest.mark.parametrize("T", [1, 16, 128, 2048])
 def test_encode_moe_t64_config4_geometry(T):
     """encode_moe on the loader's T64 expert stacks at BASELINE config 4's geometry (H 2048, 512 experts, top-10,
-    I 512, the shared expert as expert E of the gathered launches): routing indices bit-exact on the GPU's logits,
-    the norm within one bf16 step, and x += MoE(xn) against the oracle's composition on 96 tokens spread over the
-    batch."""
+    I 512, the shared expert as expert E of the gathered launches; at one token the decode route streaming the same
+    T64 copies): routing indices bit-exact on the GPU's logits, the norm within one bf16 step, and x += MoE(xn)
+    against the oracle's composition on 96 tokens spread over the batch."""
     assert os.path.exists(BIN), "tests/cpp/qwen35_ops_test is not built"
     r = subprocess.run([BIN, "--moe-c4", str(T)], capture_output=True, text=True, timeout=600)
     print(r.stdout)
     assert r.returncode == 0 and "ALL OK" in r.stdout, r.stdout + r.stderr
-    assert "[sorted, T64]" in r.stdout and "(shared = expert E)" in r.stdout, r.stdout
+    if T == 1:
+        assert "[decode, T64]" in r.stdout and "(shared on T64)" in r.stdout, r.stdout
+    else:
+        assert "[sorted, T64]" in r.stdout and "(shared = expert E)" in r.stdout, r.stdout
