@@ -397,17 +397,19 @@ def main():
                 moe[f"T{T}"] = dict(us=ms * 1e3, tok_s=T / (ms * 1e-3), gbs=byts / (ms * 1e-3) / 1e9,
                                     frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, mlx_layout_us=ms_mlx * 1e3)
             # the drop-in operator itself: Qwen35::encode_moe (rmsnorm, router, routing, the sorted route on the
-            # loader's T64 copies with the shared expert as expert E, combine into x), timed by its own C++ program
-            # over this library; and the same operator on the MLX-layout stacks alone
+            # loader's T64 copies with the shared expert as expert E, combine into x; at T = 8 the per-row route on
+            # those copies, the shared expert through gemm()), timed by its own C++ program over this library; and
+            # the same operator on the MLX-layout stacks alone
             for key, extra in (("encode_moe_t64", []), ("encode_moe_mlx", ["--mlx"])):
                 prog = os.path.join(ROOT, "inferd_amd", "encode_moe_bench")
                 if not os.path.exists(prog):
                     raise RuntimeError(f"{prog} is missing: run `python -m inferd_amd.build`")
-                r = subprocess.run([prog, *extra, "16", "128", "2048"], capture_output=True, text=True, timeout=600)
+                r = subprocess.run([prog, *extra, "8", "16", "128", "2048"], capture_output=True, text=True,
+                                   timeout=600)
                 if r.returncode != 0:
                     raise RuntimeError(f"encode_moe_bench failed ({r.returncode}): {r.stdout} {r.stderr}")
                 op = json.loads(r.stdout.strip().splitlines()[-1])
-                for T in (16, 128, 2048):
+                for T in (8, 16, 128, 2048):
                     U = E * (1.0 - (1.0 - k / E) ** T)
                     byts = (U + 1) * e_bytes + E * H * 2 + 2 * T * H * 2
                     op[f"T{T}"]["frac_hbm"] = byts / (op[f"T{T}"]["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS

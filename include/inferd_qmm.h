@@ -401,6 +401,12 @@ int ifd_moe_rows(const void* xn, int T, int H, int E, int k, const int* idx, con
                  const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b, const uint32_t* edn_wq,
                  const uint16_t* edn_s, const uint16_t* edn_b, int I, const void* ys, void* out, int assign,
                  void* workspace, size_t ws_bytes, void* stream);
+/* ifd_moe_rows on the routed experts' T64 stacks (ifd_pack_t64 with E; as ifd_moe_decode_t64): the same routing,
+ * arithmetic and combine, 8 tokens per launch group. Workspace: ifd_moe_rows_t64_workspace. */
+size_t ifd_moe_rows_t64_workspace(int T, int H, int I, int E, int k);
+int ifd_moe_rows_t64(const void* xn, int T, int H, int E, int k, const int* idx, const float* wt, const float* sg,
+                     const void* egu_t64, const void* edn_t64, int I, const void* ys, void* out, int assign,
+                     void* workspace, size_t ws_bytes, void* stream);
 
 /* ---- measurement probes (outside the operator path) ----------------------------------------------------------
  * The HBM and MFMA ceilings a benchmark reports beside the datasheet peaks, in the role of the reference's

@@ -855,6 +855,35 @@ int ifd_moe_rows(const void* xn, int T, int H, int E, int k, const int* idx, con
   return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
 }
 
+size_t ifd_moe_rows_t64_workspace(int T, int H, int I, int E, int k) {
+  if (T <= 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  size_t need = 0;  // the launch groups hold up to 8 tokens, the last one fewer
+  for (int t = 1; t <= std::min(T, 8); t++) need = std::max(need, mdec_layout(t, H, I, E, k, true).total);
+  return with_header(need);
+}
+
+int ifd_moe_rows_t64(const void* xn, int T, int H, int E, int k, const int* idx, const float* wt, const float* sg,
+                     const void* egu_t64, const void* edn_t64, int I, const void* ys, void* out, int assign,
+                     void* workspace, size_t ws_bytes, void* stream) {
+  IFD_CHECK(T >= 0, "T=%d", T);
+  IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
+                k <= 16 && k <= E,
+            "bad MoE row shape H=%d I=%d E=%d k=%d (H multiple of 512, I of 64, E <= 512, k <= 16)", H, I, E, k);
+  if (T == 0) return IFD_OK;
+  IFD_CHECK(xn && idx && wt && egu_t64 && edn_t64 && out, "null pointer");
+  IFD_CHECK(!ys || sg, "the shared expert's rows need their gate weights sg");
+  IFD_CHECK(aligned(xn, 16) && aligned(egu_t64, 16) && aligned(edn_t64, 16) && aligned(idx, 4) && aligned(wt, 4) &&
+                (!ys || aligned(ys, 2)),
+            "tokens and stacks must be 16-byte aligned");
+  const WsView wv = ws_view(workspace, ws_bytes);
+  MdecCall c{xn, nullptr, T, H, E, k, I, 1, 0, assign ? 1 : 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+             nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, out, const_cast<int*>(idx), const_cast<float*>(wt),
+             const_cast<float*>(sg), nullptr, nullptr, 4};
+  c.routed = 1, c.ys = ys;
+  c.egu_t64 = egu_t64, c.edn_t64 = edn_t64;
+  return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
+}
+
 int ifd_moe_decode_logits(const float* logits_in, const void* xn, int T, int H, int E, int k, int norm,
                           int shared_gate, const uint32_t* egu_wq, const uint16_t* egu_s, const uint16_t* egu_b,
                           const uint32_t* edn_wq, const uint16_t* edn_s, const uint16_t* edn_b, int I,

@@ -3,8 +3,8 @@
 // always-on shared expert (no gate row: its weight is 1), SwiGLU experts of width 512, 4-bit group-64 affine weights
 // (q ~ U{0..15}, s ~ U(0.005, 0.02) rounded to bf16, b = -8 s), a bf16 N(0, 0.02) router. The layer is held the way
 // the device loader leaves it: the MLX-layout stacks plus their T64 copies (ckpt_dev.h upload_moe / upload_qlinear),
-// so the sorted route runs the T64 gathered GEMMs with the shared expert as expert E; `--mlx` drops the copies and
-// times the MLX-layout route instead. Two weight copies alternate (1.85 GB, over 3x the 256 MB Infinity Cache).
+// so the sorted route runs the T64 gathered GEMMs with the shared expert as expert E (below 128 routed rows, T <= 12,
+// the per-row route on the same copies); `--mlx` drops the copies and times the MLX-layout routes instead. Two weight copies alternate (1.85 GB, over 3x the 256 MB Infinity Cache).
 //
 //   encode_moe_bench [--mlx] [--graph] T...    one JSON line: {"T16": {"us": ..., "tok_s": ...}, ...}
 //
@@ -187,10 +187,14 @@ int main(int argc, char** argv) {
     }
     const double us = ms * 1e3 / iters;
     for (auto x : gx) hip_ok(hipGraphExecDestroy(x), "graph");
+    // the route the operator took at this T, and whether it ran on the T64 copies
+    const Layer& l0 = layers[0];
+    const bool dec = m.moe_decode_route(l0, T), rows = m.moe_rows_route(l0, T);
+    const bool on_t64 = dec ? m.moe_decode_t64(l0, T) : rows ? (bool)l0.egu.t64 : m.moe_t64_route(l0);
     char buf[160];
-    snprintf(buf, sizeof buf, "%s\"T%d\": {\"us\": %.2f, \"tok_s\": %.1f, \"decode_route\": %s, \"t64_route\": %s}",
-             ti ? ", " : "", T, us, T / (us * 1e-6), m.moe_decode_route(layers[0], T) ? "true" : "false",
-             m.moe_t64_route(layers[0]) && !m.moe_decode_route(layers[0], T) ? "true" : "false");
+    snprintf(buf, sizeof buf, "%s\"T%d\": {\"us\": %.2f, \"tok_s\": %.1f, \"route\": \"%s\", \"t64\": %s}",
+             ti ? ", " : "", T, us, T / (us * 1e-6), dec ? "decode" : rows ? "per-row" : "sorted",
+             on_t64 ? "true" : "false");
     out += buf;
   }
   out += "}";

@@ -582,6 +582,7 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
 // tile is read once). The arithmetic is the qmv4 arithmetic of the MLX-layout kernels: codes as exact bf16 128 + q,
 // P = sum x (128 + q) by bf16 MFMA, s P + (b - 128 s) X per group with the group sums X of the staged token rows.
 constexpr int kMdtTB = 2;
+constexpr int kMdtMaxT = 8;  // tokens per launch (the RT = 4 accumulator rows)
 struct MdtBlk {
   u32x4 w[kMdtTB];
   uint32_t sb[kMdtTB];
@@ -865,12 +866,13 @@ static int launch_mdec(const MdecArgs& p, const MdecCall& c, hipStream_t st) {
 
 int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_bytes, hipStream_t st) {
   if (c.T == 0) return IFD_OK;
-  if (c.routed && c.T > kMdecMaxT) {
-    // the caller's routing: every token's result depends on its own row only, so the launches take 16 tokens at a
-    // time on the one workspace (stream-ordered)
-    for (int t0 = 0; t0 < c.T; t0 += kMdecMaxT) {
+  // the caller's routing: every token's result depends on its own row only, so the launches take 16 tokens (8 on
+  // T64 stacks) at a time on the one workspace (stream-ordered)
+  const int group = c.egu_t64 ? kMdtMaxT : kMdecMaxT;
+  if (c.routed && c.T > group) {
+    for (int t0 = 0; t0 < c.T; t0 += group) {
       MdecCall cc = c;
-      cc.T = std::min(kMdecMaxT, c.T - t0);
+      cc.T = std::min(group, c.T - t0);
       cc.xn = (const uint16_t*)c.xn + (size_t)t0 * c.H;
       cc.out = (uint16_t*)c.out + (size_t)t0 * c.H;
       cc.idx = c.idx + (size_t)t0 * c.k, cc.wt = c.wt + (size_t)t0 * c.k, cc.sg = c.sg ? c.sg + t0 : nullptr;
@@ -881,8 +883,8 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
   }
   if (c.T > kMdecMaxT) return fail(IFD_ERR_UNSUPPORTED, "moe_decode takes at most %d tokens", kMdecMaxT);
   const bool t64 = c.egu_t64 != nullptr;
-  if (t64 && (c.T > 8 || c.routed || c.sh_bits != 4 || (c.sgu_t64 == nullptr) != (c.sdn_t64 == nullptr)))
-    return fail(IFD_ERR_UNSUPPORTED, "moe_decode on T64 stacks: up to 8 tokens, router in, 4-bit shared expert");
+  if (t64 && (c.T > kMdtMaxT || c.sh_bits != 4 || (c.sgu_t64 == nullptr) != (c.sdn_t64 == nullptr)))
+    return fail(IFD_ERR_UNSUPPORTED, "moe_decode on T64 stacks: up to %d tokens, 4-bit shared expert", kMdtMaxT);
   const MdecLayout L = mdec_layout(c.T, c.H, c.I, c.E, c.k, t64);
   if (!ws || ws_bytes < L.total || !cnt)
     return fail(IFD_ERR_WORKSPACE, "moe_decode needs %zu bytes of workspace after the header, got %zu", L.total,

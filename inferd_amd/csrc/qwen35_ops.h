@@ -204,6 +204,7 @@ struct Qwen35 {
         need = std::max(need, ifd_moe_dispatch_workspace(T * k, E));
         if (T <= 16) need = std::max(need, ifd_moe_decode_workspace(T, H, I, E, k));
         if (T <= 8) need = std::max(need, ifd_moe_decode_t64_workspace(T, H, I, E, k));
+        need = std::max(need, ifd_moe_rows_t64_workspace(T, H, I, E, k));
         need = std::max(need, ifd_gemm_w8_workspace(T, E + 1, H));  // an 8-bit router's logits
         if (shared_inter > 0) {
           need = std::max(need, ifd_gemm_w4_workspace(T, 2 * shared_inter, H));
@@ -425,15 +426,14 @@ struct Qwen35 {
   }
   // The reference's per-row expert products (moe_qmv4 + moe_silu_mul + moe_combine, qwen35.h:1947-1955) on
   // ifd_moe_rows, with the shared expert through gemm() (:1909-1914): any T below moe_sort_min routed rows that the
-  // decode launches do not take, 4-bit routed experts of the decode kernels' shapes.
+  // decode launches do not take, 4-bit routed experts of the decode kernels' shapes (ifd_moe_rows_t64 on the routed
+  // experts' T64 copies when they exist).
   bool moe_rows_route(const Layer& ly, int T) const {
     const int H = cfg.hidden, E = cfg.experts, k = cfg.topk, I = cfg.moe_inter;
     return !moe_decode_route(ly, T) && T * k < moe_sort_min && k <= 16 && E <= 512 && H % 512 == 0 && I % 64 == 0 &&
            ly.egu.bits == 4 && ly.edown.bits == 4;
   }
 
-  // The sorted route on the experts' T64 stacks (ifd_moe_gather_qmm_t64: the same bf16(s q + b) dequant and fp32 sums
-  // as the MLX-layout gathered GEMM): both stacks 4-bit with T64 copies, H and I multiples of 256.
   // On the decode route, the T64 copies of the routed experts (and of a 4-bit shared expert, if any) are streamed
   // in place of the MLX-layout stacks, up to 8 tokens: the same per-row qmv4 arithmetic
   bool moe_decode_t64(const Layer& ly, int T) const {
@@ -441,6 +441,8 @@ struct Qwen35 {
     return moe_decode_route(ly, T) && T <= 8 && ly.egu.t64 && ly.edown.t64 &&
            (!has_shared || (ly.gate_up.bits == 4 && ly.gate_up.t64 && ly.down.t64));
   }
+  // The sorted route on the experts' T64 stacks (ifd_moe_gather_qmm_t64: the same bf16(s q + b) dequant and fp32 sums
+  // as the MLX-layout gathered GEMM): both stacks 4-bit with T64 copies, H and I multiples of 256.
   bool moe_t64_route(const Layer& ly) const {
     return ly.egu.t64 && ly.edown.t64 && ly.egu.bits == 4 && ly.edown.bits == 4 && cfg.hidden % 256 == 0 &&
            cfg.moe_inter % 256 == 0;
@@ -563,6 +565,15 @@ struct Qwen35 {
     ok(ifd_moe_route(rlog.ptr<void>(), lbf, T, E, k, E1, 1, E1 > E ? 1 : 0, ridx.ptr<int>(), rw.ptr<float>(),
                      rsg.ptr<float>(), e.stream),
        "encode_moe");
+    if (rows && ly.egu.t64 && ly.edown.t64) {  // the same on the routed experts' T64 copies
+      if (ifd_moe_rows_t64_workspace(T, H, I, E, k) > splitk_bytes)
+        die("encode_moe", "scratch smaller than the per-row MoE needs");
+      ok(ifd_moe_rows_t64(xn.ptr<void>(), T, H, E, k, ridx.ptr<int>(), rw.ptr<float>(), rsg.ptr<float>(),
+                          ly.egu.t64.ptr<void>(), ly.edown.t64.ptr<void>(), I, shared ? sh_out.ptr<void>() : nullptr,
+                          x.ptr<void>(), 0, splitk.ptr<void>(), splitk_bytes, e.stream),
+         "encode_moe");
+      return;
+    }
     if (rows) {  // a few routed rows: one decode-GEMV product per (token, expert) row, the shared rows in the combine
       const size_t need = ifd_moe_rows_workspace(T, H, I, E, k);
       if (need > splitk_bytes) die("encode_moe", "scratch smaller than the per-row MoE needs");

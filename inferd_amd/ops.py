@@ -431,6 +431,23 @@ def moe_rows(xn: torch.Tensor, idx: torch.Tensor, wt: torch.Tensor, sg: Optional
     return out
 
 
+def moe_rows_t64(xn: torch.Tensor, idx: torch.Tensor, wt: torch.Tensor, sg: Optional[torch.Tensor], egu: T64Stack,
+                 edn: T64Stack, ys: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                 assign: bool = True) -> torch.Tensor:
+    """moe_rows on T64 stacks (ifd_moe_rows_t64): the same arguments, 8 tokens per launch group."""
+    T, H = xn.shape
+    k = idx.shape[1]
+    E, I = egu.E, egu.N // 2
+    assert idx.dtype == torch.int32 and wt.dtype == torch.float32 and idx.is_contiguous() and wt.is_contiguous()
+    assert ys is None or (ys.dtype == torch.bfloat16 and ys.shape == (T, H) and ys.is_contiguous() and sg is not None)
+    if out is None:
+        out = torch.zeros((T, H), dtype=torch.bfloat16, device=xn.device)
+    ws = workspace(lib().ifd_moe_rows_t64_workspace(T, H, I, E, k), xn.device)
+    check(lib().ifd_moe_rows_t64(_p(xn), T, H, E, k, _p(idx), _p(wt), _p(sg), _p(egu.wt), _p(edn.wt), I, _p(ys),
+                                 _p(out), 1 if assign else 0, _p(ws), ws.numel(), _stream()))
+    return out
+
+
 def moe_decode(xn: torch.Tensor, router: Optional[torch.Tensor], egu: MoeW, edn: MoeW, k: int,
                shared: Optional[tuple] = None, shared_gate: bool = True, norm: bool = True,
                out: Optional[torch.Tensor] = None, assign: bool = True, logits_in: Optional[torch.Tensor] = None):

@@ -607,7 +607,7 @@ void test_encode_moe(std::mt19937& rng) {
   // (T <= 31 at top-4, 16 tokens per launch group), the sorted route beyond; the fused T64 shared gate/up; state
   // allocated for more rows than the call (its scratch covers every row count); the 8-bit router on all three; the
   // decode route on the routed experts' T64 copies (et64), streamed when the shared expert has both T64 copies
-  // (4-bit) and on the MLX layout otherwise
+  // (4-bit) and on the MLX layout otherwise; the per-row route on those copies (8-token launch groups)
   for (const Case cs : {Case{1, 1, false, false}, Case{24, 24, false, false}, Case{31, 40, false, true},
                         Case{3, 3, false, false}, Case{8, 8, false, false}, Case{16, 16, false, false},
                         Case{100, 100, false, false}, Case{16, 16, true, false}, Case{100, 100, true, false},
@@ -615,7 +615,8 @@ void test_encode_moe(std::mt19937& rng) {
                         Case{40, 40, false, true}, Case{3, 3, false, false, true}, Case{8, 8, false, true, true},
                         Case{1, 1, true, false, false, true}, Case{2, 4, true, false, false, true},
                         Case{8, 8, true, true, false, true}, Case{5, 5, false, true, false, true},
-                        Case{8, 8, false, true, true, true}}) {
+                        Case{8, 8, false, true, true, true}, Case{5, 5, true, false, false, true},
+                        Case{20, 24, true, false, false, true}}) {
     const int T = cs.T;
     ly.gate_up = cs.s8 ? sgu8_d : sgu_mlx;
     ly.down = cs.s8 ? sdn8_d : sdn_mlx;
@@ -638,8 +639,9 @@ void test_encode_moe(std::mt19937& rng) {
     const std::string tag = " T=" + std::to_string(T) + (cs.max_rows > T ? " of " + std::to_string(cs.max_rows) : "") +
                             (ly.gate_up.t64 ? " (T64 shared gate/up)" : "") + (cs.r8 ? " (8-bit router)" : "") +
                             (cs.s8 ? " (8-bit shared expert)" : "") +
-                            (dec ? (m.moe_decode_t64(ly, T) ? " [decode, T64]" : " [decode]")
-                                 : rows ? " [per-row]" : " [sorted]");
+                            (dec    ? (m.moe_decode_t64(ly, T) ? " [decode, T64]" : " [decode]")
+                             : rows ? (ly.egu.t64 ? " [per-row, T64]" : " [per-row]")
+                                    : " [sorted]");
     // the reference's routes: moe2 up to 8 tokens with an 8-bit router (and here up to qmv_max tokens with any),
     // the per-row products below 128 routed rows, the sorted path from there
     report(dec == (T <= m.qmv_max || (T <= 8 && cs.r8)) && rows == (!dec && T * k < 128) &&

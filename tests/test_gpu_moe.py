@@ -321,6 +321,45 @@ def test_moe_rows(T, k, shared):
                        composition=True)
 
 
+@pytest.mark.parametrize("T,k,shared", [(3, 10, True), (12, 10, True), (17, 4, False), (8, 16, True)])
+def test_moe_rows_t64(T, k, shared):
+    """ifd_moe_rows_t64: the per-row route on the routed experts' T64 stacks, 8 tokens per launch group (T = 12, 17
+    cross group edges): against ifd_moe_rows on the same weights and routing (the same arithmetic, sums in another
+    order: within 2^-6 of the output's scale) and against the oracle's per-token decode composition."""
+    g, ops = _gu(), _ops()
+    E, H, I, seed = 64, 1024, 256, 430 + T
+    egu, edn = experts(E, 2 * I, H, seed=seed), experts(E, H, I, seed=seed + 1)
+    rng = np.random.default_rng(seed)
+    xn = gen.activations(T, H, seed=seed + 2)
+    x0 = gen.activations(T, H, seed=seed + 3)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    wt = rng.random((T, k)).astype(np.float32)
+    wt /= wt.sum(axis=1, keepdims=True)
+    sg = rng.random(T).astype(np.float32) if shared else np.ones(T, np.float32)
+    ys = gen.activations(T, H, seed=seed + 4) if shared else None
+    W1, W2 = g.moew(*egu), g.moew(*edn)
+    T1, T2 = ops.pack_t64_stack(W1), ops.pack_t64_stack(W2)
+    args = (g.dev(xn), g.dev(idx), g.dev(wt), g.dev(sg))
+    ysd = g.dev(ys) if shared else None
+    d = np.empty((T * k, H), np.uint16)
+    for t in range(T):
+        for j in range(k):
+            e = idx[t, j]
+            gu = gen.f32_to_bf16(orc.qmv(xn[t:t + 1], egu[0][e], egu[1][e], egu[2][e]))
+            d[t * k + j] = gen.f32_to_bf16(orc.qmv(orc.silu_mul(gu), edn[0][e], edn[1][e], edn[2][e]))[0]
+    ident = np.arange(T * k, dtype=np.int32)
+    for assign in (True, False):
+        out = ops.moe_rows_t64(*args, T1, T2, ysd, out=g.dev(x0), assign=assign)
+        again = ops.moe_rows_t64(*args, T1, T2, ysd, out=g.dev(x0), assign=assign)
+        mlx = ops.moe_rows(*args, W1, W2, ysd, out=g.dev(x0), assign=assign)
+        torch.cuda.synchronize()
+        assert np.array_equal(g.host(out), g.host(again))
+        got, m = gen.bf16_to_f32(g.host(out)), gen.bf16_to_f32(g.host(mlx))
+        assert np.abs(got - m).max() <= 2 ** -6 * max(float(np.abs(m).max()), 1e-6)
+        ref = orc.moe_combine(x0, d, wt, ys, sg, ident, k, assign)
+        gen.check_bf16(g.host(out), ref, 1e-2, (T, k, shared, assign), ref_is_bf16=True, composition=True)
+
+
 @pytest.mark.parametrize("T", [1, 4, 8, 12, 16])
 def test_moe_decode_8bit_shared_expert(T):
     """An 8-bit shared expert beside the 4-bit routed experts (the reference's moe_gu2_4_8 / moe_dn2_4_8,
