@@ -350,7 +350,7 @@ int ifd_moe_decode(const void* xn, int T, int H, const void* router, int E, int 
                    size_t ws_bytes, void* stream);
 /* The decode MoE of ifd_moe_decode on T64 stacks (the layout ifd_pack_t64 writes, the device loader's default copy):
  * egu_t64 = E experts [E][2I][H], edn_t64 = [E][H][I], the shared expert's T64 copies sgu_t64 [2I][H] / sdn_t64
- * [H][I] (4-bit) or NULL. Up to 8 tokens (the reference's moe2 range). The router is either `router` (bf16 [E1][H],
+ * [H][I] (4-bit) or NULL. Up to 16 tokens, as ifd_moe_decode. The router is either `router` (bf16 [E1][H],
  * as ifd_moe_decode) or the caller's fp32 logits `logits_in` [T][E1] (as ifd_moe_decode_logits_ex): exactly one is
  * non-NULL. The same per-row qmv4 arithmetic (fp32 sums in another order); each wave streams one 32-column band's
  * 1152-byte tiles, and gate/up splits K over blocks. Workspace: ifd_moe_decode_t64_workspace. */
@@ -402,7 +402,7 @@ int ifd_moe_rows(const void* xn, int T, int H, int E, int k, const int* idx, con
                  const uint16_t* edn_s, const uint16_t* edn_b, int I, const void* ys, void* out, int assign,
                  void* workspace, size_t ws_bytes, void* stream);
 /* ifd_moe_rows on the routed experts' T64 stacks (ifd_pack_t64 with E; as ifd_moe_decode_t64): the same routing,
- * arithmetic and combine, 8 tokens per launch group. Workspace: ifd_moe_rows_t64_workspace. */
+ * arithmetic and combine, 16 tokens per launch group. Workspace: ifd_moe_rows_t64_workspace. */
 size_t ifd_moe_rows_t64_workspace(int T, int H, int I, int E, int k);
 int ifd_moe_rows_t64(const void* xn, int T, int H, int E, int k, const int* idx, const float* wt, const float* sg,
                      const void* egu_t64, const void* edn_t64, int I, const void* ys, void* out, int assign,

@@ -762,7 +762,7 @@ int ifd_moe_decode_ex(const void* xn, int T, int H, const void* router, int E, i
 }
 
 size_t ifd_moe_decode_t64_workspace(int T, int H, int I, int E, int k) {
-  if (T <= 0 || T > 8 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  if (T <= 0 || T > 16 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
   return with_header(mdec_layout(T, H, I, E, k, true).total);
 }
 
@@ -770,7 +770,7 @@ int ifd_moe_decode_t64(const void* xn, int T, int H, const void* router, const f
                        int norm, int shared_gate, const void* egu_t64, const void* edn_t64, int I, const void* sgu_t64,
                        const void* sdn_t64, void* out, int assign, int* idx, float* wt, float* sg, float* logits,
                        void* workspace, size_t ws_bytes, void* stream) {
-  IFD_CHECK(T >= 0 && T <= 8, "the decode MoE on T64 stacks takes T <= 8 tokens (T=%d)", T);
+  IFD_CHECK(T >= 0 && T <= 16, "the decode MoE on T64 stacks takes T <= 16 tokens (T=%d)", T);
   IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
                 k <= 16 && k <= E,
             "bad decode MoE shape H=%d I=%d E=%d k=%d (H multiple of 512, I of 64, E <= 512, k <= 16)", H, I, E, k);
@@ -857,8 +857,8 @@ int ifd_moe_rows(const void* xn, int T, int H, int E, int k, const int* idx, con
 
 size_t ifd_moe_rows_t64_workspace(int T, int H, int I, int E, int k) {
   if (T <= 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
-  size_t need = 0;  // the launch groups hold up to 8 tokens, the last one fewer
-  for (int t = 1; t <= std::min(T, 8); t++) need = std::max(need, mdec_layout(t, H, I, E, k, true).total);
+  size_t need = 0;  // the launch groups hold up to 16 tokens, the last one fewer
+  for (int t = 1; t <= std::min(T, 16); t++) need = std::max(need, mdec_layout(t, H, I, E, k, true).total);
   return with_header(need);
 }
 

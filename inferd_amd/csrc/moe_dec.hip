@@ -76,7 +76,7 @@ struct MdecArgs {
   const uint16_t* ys;      // with routed: the shared expert's output rows [T][H] for the combine, or null
   int out16;               // out and ys 16-byte aligned: the combine loads and stores 8 columns at a time
   int has_sh;              // a shared expert (either layout)
-  // the T64 path (T <= 8): routed experts packed by ifd_pack_t64 with E (expert e at e gu_eb, e dn_eb bytes), the
+  // the T64 path: routed experts packed by ifd_pack_t64 with E (expert e at e gu_eb, e dn_eb bytes), the
   // shared expert's T64 copies or null; the gate/up K split (gS splits of gps groups) and its partials
   const uint8_t* egu_t;
   const uint8_t* edn_t;
@@ -576,13 +576,13 @@ __global__ __launch_bounds__(256) void k_mdec_dn(MdecArgs p) {
   mdec_combine(p, rd);
 }
 
-// ---- the T64 path (T <= 8 tokens): expert stacks in the T64 layout, each wave streaming one band --------------------
+// ---- the T64 path: expert stacks in the T64 layout, each wave streaming one band -----------------------------------
 // A wave streams its band's 1152-byte (group, band) tiles, 16 bytes per lane of one tile per group, in ping-pong
 // blocks of kMdtTB groups with the next block requested before the current one is used (non-temporal loads: each
 // tile is read once). The arithmetic is the qmv4 arithmetic of the MLX-layout kernels: codes as exact bf16 128 + q,
 // P = sum x (128 + q) by bf16 MFMA, s P + (b - 128 s) X per group with the group sums X of the staged token rows.
 constexpr int kMdtTB = 2;
-constexpr int kMdtMaxT = 8;  // tokens per launch (the RT = 4 accumulator rows)
+constexpr int kMdtMaxT = kMdecMaxT;  // tokens per launch: RT = 4 accumulator rows up to 8, 8 up to 16
 struct MdtBlk {
   u32x4 w[kMdtTB];
   uint32_t sb[kMdtTB];
@@ -598,9 +598,9 @@ __device__ __forceinline__ void mdt_stage(Src src, int T, int ng, uint16_t* As, 
 // One wave's product over groups [g0, g1) of NB bands, streamed as one sequence band by band (with NB > 1, g1 - g0
 // is a multiple of kMdtTB, so that a ping-pong block never spans two bands): tcol = the first band's first tile,
 // bstride = bytes
-// between the bands, gstride = bytes between groups; As / Xs staged from group g0 on. acc[b][r]: token row
+// between the bands, gstride = bytes between groups; As / Xs staged from group g0 on. acc[b][r] (r < RT): token row
 // mdec_row(r, h), column j of band b.
-template <int NB>
+template <int NB, int RT>
 __device__ __forceinline__ void mdt_band(const uint8_t* tcol, size_t bstride, size_t gstride, int g0, int g1,
                                          const uint16_t* As, int lda, const float* Xs, int T, f32x16 (&acc)[NB]) {
   const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
@@ -626,17 +626,19 @@ __device__ __forceinline__ void mdt_band(const uint8_t* tcol, size_t bstride, si
 #pragma unroll
       for (int t = 0; t < 4; t++) af[t] = aok ? *(const u32x4*)(arow + (size_t)gl * 64 + 8 * t) : u32x4{0u, 0u, 0u, 0u};
       const float4 x0 = *(const float4*)(Xs + gl * kMdecMaxT + 4 * h);
+      float4 x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (RT > 4) x1 = *(const float4*)(Xs + gl * kMdecMaxT + 8 + 4 * h);
       f32x16 P = zero16();
 #pragma unroll
       for (int t = 0; t < 4; t++) P = mfma_bf16(af[t], t64_off128(B.w[i][t]), P);
-      const float xs[4] = {x0.x, x0.y, x0.z, x0.w};
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       const float sc = bf2f((uint16_t)(B.sb[i] & 0xFFFFu)), bi = bf2f((uint16_t)(B.sb[i] >> 16));
       const float bp = __builtin_fmaf(-128.f, sc, bi);
 #pragma unroll
       for (int bb = 0; bb < NB; bb++)
         if (bb == b)
 #pragma unroll
-          for (int r = 0; r < 4; r++) acc[bb][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[bb][r]));
+          for (int r = 0; r < RT; r++) acc[bb][r] = __builtin_fmaf(sc, P[r], __builtin_fmaf(bp, xs[r], acc[bb][r]));
     }
   };
   MdtBlk b0, b1;
@@ -655,9 +657,10 @@ __device__ __forceinline__ void mdt_band(const uint8_t* tcol, size_t bstride, si
 // slot's expert, waves 2, 3 the matching up bands I / 32 + 2c, + 1, over groups [z gps, (z + 1) gps). With one split
 // the block pairs gate and up through LDS and writes h; with several each block writes its fp32 sums (write-through)
 // and the last of a (slot, c)'s splits (a counter in the workspace header) sums them in split order and writes h.
+template <int RT>
 __global__ __launch_bounds__(256) void k_mdt_gu(MdecArgs p) {
   extern __shared__ __align__(16) uint16_t lds[];
-  __shared__ float red[4][64][4];
+  __shared__ float red[4][64][RT];
   __shared__ unsigned s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 31, h = lane >> 5;
   const int c = blockIdx.x, u = blockIdx.y, z = blockIdx.z, T = p.T, H = p.H, I = p.I, nct = I / 64;
@@ -671,13 +674,20 @@ __global__ __launch_bounds__(256) void k_mdt_gu(MdecArgs p) {
   const uint8_t* stack = sl.e < 0 ? p.sgu_t : p.egu_t + (size_t)sl.e * p.gu_eb;
   const int band = wave < 2 ? 2 * c + wave : I / 32 + 2 * c + wave - 2, nb = 2 * I / 32;
   f32x16 accs[1] = {zero16()};
-  mdt_band<1>(stack + (size_t)band * kT64Tile, 0, (size_t)nb * kT64Tile, g0, g1, As, lda, Xs, T, accs);
+  mdt_band<1, RT>(stack + (size_t)band * kT64Tile, 0, (size_t)nb * kT64Tile, g0, g1, As, lda, Xs, T, accs);
   f32x16& acc = accs[0];
   if (p.gS > 1) {  // this split's sums, then the (slot, c) tile's last split sums them all
     const __amdgpu_buffer_rsrc_t rg = part_rsrc(p.gpart, p.gpart_bytes);
+    // a split's sums: [4 waves][RT / 4 quads][64 lanes] 16-byte quads
+    constexpr int NQ = RT / 4;
     const int slot = (u * nct + c) * p.gS + z;
-    const u32x4 v = {__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]), __float_as_uint(acc[3])};
-    __builtin_amdgcn_raw_buffer_store_b128(v, rg, (int)((((size_t)slot * 4 + wave) * 64 + lane) * 16), 0, kSc1);
+#pragma unroll
+    for (int q4 = 0; q4 < NQ; q4++) {
+      const u32x4 v = {__float_as_uint(acc[4 * q4]), __float_as_uint(acc[4 * q4 + 1]), __float_as_uint(acc[4 * q4 + 2]),
+                       __float_as_uint(acc[4 * q4 + 3])};
+      __builtin_amdgcn_raw_buffer_store_b128(v, rg, (int)(((((size_t)slot * 4 + wave) * NQ + q4) * 64 + lane) * 16),
+                                             0, kSc1);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
@@ -689,31 +699,36 @@ __global__ __launch_bounds__(256) void k_mdt_gu(MdecArgs p) {
     }
     __syncthreads();
     if (!s_last) return;
-    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    float a[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) a[r] = 0.f;
     for (int z0 = 0; z0 < p.gS; z0 += 4) {  // four splits' loads in flight, summed in split order
-      u32x4 w[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        if (z0 + q < p.gS)
-          w[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rg, (int)(((((size_t)(u * nct + c) * p.gS + z0 + q) * 4 + wave) * 64 +
-                                                          lane) * 16), 0, kSc1));
+      u32x4 w[4][NQ];
 #pragma unroll
       for (int q = 0; q < 4; q++)
         if (z0 + q < p.gS)
 #pragma unroll
-          for (int r = 0; r < 4; r++) a[r] += __uint_as_float(w[q][r]);
+          for (int q4 = 0; q4 < NQ; q4++)
+            w[q][q4] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           rg, (int)((((((size_t)(u * nct + c) * p.gS + z0 + q) * 4 + wave) * NQ + q4) * 64 + lane) *
+                                     16), 0, kSc1));
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (z0 + q < p.gS)
+#pragma unroll
+          for (int r = 0; r < RT; r++) a[r] += __uint_as_float(w[q][r / 4][r % 4]);
     }
 #pragma unroll
-    for (int r = 0; r < 4; r++) acc[r] = a[r];
+    for (int r = 0; r < RT; r++) acc[r] = a[r];
   }
   // gate (waves 0, 1) with up (waves 2, 3): h = silu(bf16(gate)) bf16(up) for the tokens that picked the slot
 #pragma unroll
-  for (int r = 0; r < 4; r++) red[wave][lane][r] = acc[r];
+  for (int r = 0; r < RT; r++) red[wave][lane][r] = acc[r];
   __syncthreads();
   if (wave >= 2) return;
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
+  for (int r = 0; r < RT; r++) {
     const int t = mdec_row(r, h), pk = mdec_pick(p, u, t);
     if (pk < 0) continue;
     const float g = red[wave][lane][r], v = red[wave + 2][lane][r];
@@ -725,7 +740,7 @@ __global__ __launch_bounds__(256) void k_mdt_gu(MdecArgs p) {
 // of the slot's down rows over all I / 64 groups against the act rows of the tokens that picked it (the staging and
 // the block's fixed costs shared by more weight bytes), d[t][pick][h] = bf16(result) written through; the last block
 // of a chunk (a counter in the workspace header) combines its columns, as k_mdec_dn.
-template <int NB>
+template <int NB, int RT>
 __global__ __launch_bounds__(256) void k_mdt_dn(MdecArgs p) {
   extern __shared__ __align__(16) uint16_t lds[];
   __shared__ unsigned s_last;
@@ -748,13 +763,13 @@ __global__ __launch_bounds__(256) void k_mdt_dn(MdecArgs p) {
   f32x16 acc[NB];
 #pragma unroll
   for (int bb = 0; bb < NB; bb++) acc[bb] = zero16();
-  mdt_band<NB>(stack + (size_t)band * kT64Tile, kT64Tile, (size_t)nb * kT64Tile, 0, Gi, As, lda, Xs, T, acc);
+  mdt_band<NB, RT>(stack + (size_t)band * kT64Tile, kT64Tile, (size_t)nb * kT64Tile, 0, Gi, As, lda, Xs, T, acc);
   const __amdgpu_buffer_rsrc_t rd = part_rsrc(p.d, p.d_bytes);
 #pragma unroll
   for (int bb = 0; bb < NB; bb++) {
     const int h0 = (band + bb) * 32;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < RT; r++) {
       const int t = mdec_row(r, h), pk = mdec_pick(p, u, t);
       if (pk >= 0)
         __builtin_amdgcn_raw_buffer_store_b16(f2bf(acc[bb][r]), rd,
@@ -811,7 +826,7 @@ MdecLayout mdec_layout(int T, int H, int I, int E, int k, bool t64) {
   L.gS = 1, L.gps = H / kGroup;
   if (t64) {
     mdt_split(T, H, I, k, L.gS, L.gps);
-    take(L.gpart, L.gS > 1 ? (size_t)(T * k + 1) * (I / 64) * L.gS * 4 * 64 * 16 : 0);
+    take(L.gpart, L.gS > 1 ? (size_t)(T * k + 1) * (I / 64) * L.gS * 4 * 64 * 16 * (T > 8 ? 2 : 1) : 0);
   }
   return L;
 }
@@ -832,21 +847,21 @@ static int launch_mdec(const MdecArgs& p, const MdecCall& c, hipStream_t st) {
     }
     return IFD_OK;
   };
-  if (p.egu_t) {  // the T64 path (RT = 4: up to 8 tokens)
+  if (p.egu_t) {  // the T64 path
     const size_t glds = ((size_t)c.T * (p.gps * 64 + 8) + 8) * 2 + (size_t)p.gps * kMdecMaxT * 4;
-    IFD_TRY(allow_lds((const void*)k_mdt_gu, glds, "gate_up"));
-    hipLaunchKernelGGL(k_mdt_gu, dim3(c.I / 64, slots, p.gS), dim3(256), glds, st, p);
+    IFD_TRY(allow_lds((const void*)k_mdt_gu<RT>, glds, "gate_up"));
+    hipLaunchKernelGGL(k_mdt_gu<RT>, dim3(c.I / 64, slots, p.gS), dim3(256), glds, st, p);
     IFD_TRY(check_launch("moe_decode gate_up"));
     const size_t dlds = ((size_t)c.T * (c.I + 8) + 8) * 2 + (size_t)(c.I / kGroup) * kMdecMaxT * 4;
     // two bands per wave when one per wave would give more than four blocks per CU (config 4 at T = 8: 61.3 against
     // 66.1 us for the whole decode; at T <= 4 one band per wave keeps more blocks in flight: T = 1 / 2 / 4 32.9 /
     // 37.1 / 46.6 against 36.0 / 39.9 / 47.6 us) and a band's groups fill whole ping-pong blocks
     if ((long)slots * (c.H / 128) > 4l * cu_count() && (c.I / kGroup) % kMdtTB == 0) {
-      IFD_TRY(allow_lds((const void*)k_mdt_dn<2>, dlds, "down"));
-      hipLaunchKernelGGL(k_mdt_dn<2>, dim3(c.H / 256, slots), dim3(256), dlds, st, p);
+      IFD_TRY(allow_lds((const void*)k_mdt_dn<2, RT>, dlds, "down"));
+      hipLaunchKernelGGL((k_mdt_dn<2, RT>), dim3(c.H / 256, slots), dim3(256), dlds, st, p);
     } else {
-      IFD_TRY(allow_lds((const void*)k_mdt_dn<1>, dlds, "down"));
-      hipLaunchKernelGGL(k_mdt_dn<1>, dim3(c.H / 128, slots), dim3(256), dlds, st, p);
+      IFD_TRY(allow_lds((const void*)k_mdt_dn<1, RT>, dlds, "down"));
+      hipLaunchKernelGGL((k_mdt_dn<1, RT>), dim3(c.H / 128, slots), dim3(256), dlds, st, p);
     }
     return check_launch("moe_decode down");
   }
@@ -921,7 +936,7 @@ int launch_moe_decode(const MdecCall& c, unsigned* cnt, void* ws, size_t ws_byte
     p.gu_eb = t64_bytes(2 * c.I, c.H), p.dn_eb = t64_bytes(c.H, c.I);
     p.gS = L.gS, p.gps = L.gps;
     p.gpart = (float*)(w + L.gpart);
-    p.gpart_bytes = (uint32_t)((size_t)(c.T * c.k + 1) * (c.I / 64) * L.gS * 4 * 64 * 16);
+    p.gpart_bytes = (uint32_t)((size_t)(c.T * c.k + 1) * (c.I / 64) * L.gS * 4 * 64 * 16 * (c.T > 8 ? 2 : 1));
   }
   // vector scale / bias loads: every chunk holds 8 groups (the wave's group count a multiple of 8) and rows start
   // 16-byte aligned

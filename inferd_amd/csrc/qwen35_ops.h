@@ -203,7 +203,7 @@ struct Qwen35 {
       for (int T = 1; T <= max_rows; T++) {
         need = std::max(need, ifd_moe_dispatch_workspace(T * k, E));
         if (T <= 16) need = std::max(need, ifd_moe_decode_workspace(T, H, I, E, k));
-        if (T <= 8) need = std::max(need, ifd_moe_decode_t64_workspace(T, H, I, E, k));
+        if (T <= 16) need = std::max(need, ifd_moe_decode_t64_workspace(T, H, I, E, k));
         need = std::max(need, ifd_moe_rows_t64_workspace(T, H, I, E, k));
         need = std::max(need, ifd_gemm_w8_workspace(T, E + 1, H));  // an 8-bit router's logits
         if (shared_inter > 0) {
@@ -435,10 +435,10 @@ struct Qwen35 {
   }
 
   // On the decode route, the T64 copies of the routed experts (and of a 4-bit shared expert, if any) are streamed
-  // in place of the MLX-layout stacks, up to 8 tokens: the same per-row qmv4 arithmetic
+  // in place of the MLX-layout stacks: the same per-row qmv4 arithmetic
   bool moe_decode_t64(const Layer& ly, int T) const {
     const bool has_shared = ly.gate_up.N > 0;
-    return moe_decode_route(ly, T) && T <= 8 && ly.egu.t64 && ly.edown.t64 &&
+    return moe_decode_route(ly, T) && T <= 16 && ly.egu.t64 && ly.edown.t64 &&
            (!has_shared || (ly.gate_up.bits == 4 && ly.gate_up.t64 && ly.down.t64));
   }
   // The sorted route on the experts' T64 stacks (ifd_moe_gather_qmm_t64: the same bf16(s q + b) dequant and fp32 sums

@@ -434,7 +434,7 @@ def moe_rows(xn: torch.Tensor, idx: torch.Tensor, wt: torch.Tensor, sg: Optional
 def moe_rows_t64(xn: torch.Tensor, idx: torch.Tensor, wt: torch.Tensor, sg: Optional[torch.Tensor], egu: T64Stack,
                  edn: T64Stack, ys: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                  assign: bool = True) -> torch.Tensor:
-    """moe_rows on T64 stacks (ifd_moe_rows_t64): the same arguments, 8 tokens per launch group."""
+    """moe_rows on T64 stacks (ifd_moe_rows_t64): the same arguments, 16 tokens per launch group."""
     T, H = xn.shape
     k = idx.shape[1]
     E, I = egu.E, egu.N // 2
@@ -492,7 +492,7 @@ def moe_decode(xn: torch.Tensor, router: Optional[torch.Tensor], egu: MoeW, edn:
 def moe_decode_t64(xn: torch.Tensor, router: Optional[torch.Tensor], egu: T64Stack, edn: T64Stack, k: int,
                    shared: Optional[tuple] = None, shared_gate: bool = True, norm: bool = True,
                    out: Optional[torch.Tensor] = None, assign: bool = True, logits_in: Optional[torch.Tensor] = None):
-    """The decode MoE on T64 stacks (T <= 8): shared = (T64Linear gate_up [2I, H], T64Linear down [H, I]), 4-bit.
+    """The decode MoE on T64 stacks (T <= 16): shared = (T64Linear gate_up [2I, H], T64Linear down [H, I]), 4-bit.
     With logits_in (fp32 [T, E + shared_gate]) the router is not read. Returns (out, idx, wt, sg, logits)."""
     T, H = xn.shape
     E, I = egu.E, egu.N // 2

@@ -225,9 +225,11 @@ def test_moe_rows_checks():
     assert call(sg=None) == E and b"gate weights" in L.ifd_last_error()
     assert call(T=0) == _lib.IFD_OK
     assert call() == _lib.IFD_ERR_WORKSPACE  # no workspace past the header
-    # on T64 stacks: 8-token launch groups, one workspace size from 8 tokens up, the same checks
-    assert L.ifd_moe_rows_t64_workspace(300, 2048, 512, 512, 10) == L.ifd_moe_rows_t64_workspace(8, 2048, 512, 512, 10)
-    assert L.ifd_moe_rows_t64_workspace(8, 2048, 512, 512, 10) >= L.ifd_moe_decode_t64_workspace(8, 2048, 512, 512, 10)
+    # on T64 stacks: 16-token launch groups, one workspace size from 16 tokens up, the same checks
+    assert L.ifd_moe_rows_t64_workspace(300, 2048, 512, 512, 10) == L.ifd_moe_rows_t64_workspace(16, 2048, 512, 512, 10)
+    assert L.ifd_moe_rows_t64_workspace(16, 2048, 512, 512, 10) >= L.ifd_moe_decode_t64_workspace(16, 2048, 512, 512,
+                                                                                                  10)
+    assert L.ifd_moe_decode_t64_workspace(17, 2048, 512, 512, 10) == 0
     call64 = lambda T=20, H=2048, Ex=512, k=10, idx=4096, sg=4096, I=512, ys=4096: L.ifd_moe_rows_t64(
         4096, T, H, Ex, k, idx, 4096, sg, 4096, 4096, I, ys, 4096, 0, 4096, 0, None)
     assert call64(H=1280) == E and b"H multiple of 512" in L.ifd_last_error()

@@ -321,9 +321,9 @@ def test_moe_rows(T, k, shared):
                        composition=True)
 
 
-@pytest.mark.parametrize("T,k,shared", [(3, 10, True), (12, 10, True), (17, 4, False), (8, 16, True)])
+@pytest.mark.parametrize("T,k,shared", [(3, 10, True), (12, 10, True), (17, 4, False), (8, 16, True), (40, 2, True)])
 def test_moe_rows_t64(T, k, shared):
-    """ifd_moe_rows_t64: the per-row route on the routed experts' T64 stacks, 8 tokens per launch group (T = 12, 17
+    """ifd_moe_rows_t64: the per-row route on the routed experts' T64 stacks, 16 tokens per launch group (T = 17, 40
     cross group edges): against ifd_moe_rows on the same weights and routing (the same arithmetic, sums in another
     order: within 2^-6 of the output's scale) and against the oracle's per-token decode composition."""
     g, ops = _gu(), _ops()
@@ -468,6 +468,8 @@ def test_moe_decode_out_alignment(T):
     (3, 32, 512, 128, 4, False, False, True),      # no shared expert; short K (2 splits of 4 groups)
     (8, 8, 1024, 256, 3, True, False, False),      # most experts picked by several tokens
     (5, 16, 512, 192, 2, True, False, True),       # I = 192: three groups per down band, a ping-pong block across bands
+    (12, 512, 2048, 512, 10, True, True, False),   # 9 to 16 tokens: eight accumulator rows per lane
+    (16, 64, 1024, 256, 4, False, False, True),
 ])
 def test_moe_decode_t64(T, E, H, I, k, shared, shared_gate, assign):
     """The decode MoE on T64 stacks against the MLX-layout decode MoE on the same weights (the same router kernel:
