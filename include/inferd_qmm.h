@@ -402,11 +402,14 @@ int ifd_moe_rows(const void* xn, int T, int H, int E, int k, const int* idx, con
                  const uint16_t* edn_s, const uint16_t* edn_b, int I, const void* ys, void* out, int assign,
                  void* workspace, size_t ws_bytes, void* stream);
 /* ifd_moe_rows on the routed experts' T64 stacks (ifd_pack_t64 with E; as ifd_moe_decode_t64): the same routing,
- * arithmetic and combine, 16 tokens per launch group. Workspace: ifd_moe_rows_t64_workspace. */
+ * arithmetic and combine, 16 tokens per launch group. The shared expert (weight sg[t]) comes either as its output rows
+ * ys, as in ifd_moe_rows, or as its 4-bit T64 copies sgu_t64 [2I][H] / sdn_t64 [H][I], which the same launches run
+ * as one more slot in the qmv4 arithmetic (the arithmetic of the T64 gemm() up to 16 rows, sums in another order);
+ * or neither. Workspace: ifd_moe_rows_t64_workspace. */
 size_t ifd_moe_rows_t64_workspace(int T, int H, int I, int E, int k);
 int ifd_moe_rows_t64(const void* xn, int T, int H, int E, int k, const int* idx, const float* wt, const float* sg,
-                     const void* egu_t64, const void* edn_t64, int I, const void* ys, void* out, int assign,
-                     void* workspace, size_t ws_bytes, void* stream);
+                     const void* egu_t64, const void* edn_t64, int I, const void* sgu_t64, const void* sdn_t64,
+                     const void* ys, void* out, int assign, void* workspace, size_t ws_bytes, void* stream);
 
 /* ---- measurement probes (outside the operator path) ----------------------------------------------------------
  * The HBM and MFMA ceilings a benchmark reports beside the datasheet peaks, in the role of the reference's

@@ -88,7 +88,8 @@ SIGNATURES = {
                                 _vp, _vp, _sz, _vp]),
     "ifd_moe_rows_workspace": (_sz, [_i, _i, _i, _i, _i]),
     "ifd_moe_rows_t64_workspace": (_sz, [_i, _i, _i, _i, _i]),
-    "ifd_moe_rows_t64": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _sz, _vp]),
+    "ifd_moe_rows_t64": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _sz,
+                              _vp]),
     "ifd_moe_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _sz,
                           _vp]),
     "ifd_moe_decode": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i,

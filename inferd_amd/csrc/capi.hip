@@ -863,24 +863,27 @@ size_t ifd_moe_rows_t64_workspace(int T, int H, int I, int E, int k) {
 }
 
 int ifd_moe_rows_t64(const void* xn, int T, int H, int E, int k, const int* idx, const float* wt, const float* sg,
-                     const void* egu_t64, const void* edn_t64, int I, const void* ys, void* out, int assign,
-                     void* workspace, size_t ws_bytes, void* stream) {
+                     const void* egu_t64, const void* edn_t64, int I, const void* sgu_t64, const void* sdn_t64,
+                     const void* ys, void* out, int assign, void* workspace, size_t ws_bytes, void* stream) {
   IFD_CHECK(T >= 0, "T=%d", T);
   IFD_CHECK(H > 0 && H % 512 == 0 && H / 128 < kWsCounters && I > 0 && I % 64 == 0 && E > 0 && E <= 512 && k > 0 &&
                 k <= 16 && k <= E,
             "bad MoE row shape H=%d I=%d E=%d k=%d (H multiple of 512, I of 64, E <= 512, k <= 16)", H, I, E, k);
   if (T == 0) return IFD_OK;
   IFD_CHECK(xn && idx && wt && egu_t64 && edn_t64 && out, "null pointer");
-  IFD_CHECK(!ys || sg, "the shared expert's rows need their gate weights sg");
+  const bool shared = sgu_t64 != nullptr;
+  IFD_CHECK(shared == (sdn_t64 != nullptr), "the shared expert needs both stacks");
+  IFD_CHECK(!(shared && ys), "the shared expert as weights or as rows, not both");
+  IFD_CHECK(!(ys || shared) || sg, "the shared expert needs its gate weights sg");
   IFD_CHECK(aligned(xn, 16) && aligned(egu_t64, 16) && aligned(edn_t64, 16) && aligned(idx, 4) && aligned(wt, 4) &&
-                (!ys || aligned(ys, 2)),
+                (!ys || aligned(ys, 2)) && (!shared || (aligned(sgu_t64, 16) && aligned(sdn_t64, 16))),
             "tokens and stacks must be 16-byte aligned");
   const WsView wv = ws_view(workspace, ws_bytes);
   MdecCall c{xn, nullptr, T, H, E, k, I, 1, 0, assign ? 1 : 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, out, const_cast<int*>(idx), const_cast<float*>(wt),
              const_cast<float*>(sg), nullptr, nullptr, 4};
   c.routed = 1, c.ys = ys;
-  c.egu_t64 = egu_t64, c.edn_t64 = edn_t64;
+  c.egu_t64 = egu_t64, c.edn_t64 = edn_t64, c.sgu_t64 = sgu_t64, c.sdn_t64 = sdn_t64;
   return launch_moe_decode(c, wv.cnt, wv.body, wv.bytes, S(stream));
 }
 

@@ -450,6 +450,17 @@ struct Qwen35 {
   // On that route the shared expert runs as expert E of the same two launches when it is a 4-bit linear pair of the
   // routed experts' width with T64 copies that gemm() would also run in bf16 (not the W4A8 route): its rows get the
   // qmm rounding gemm() gives them past qmv_max rows (qwen35.h:1525-1558, 1909-1914).
+  // On the per-row route over the routed experts' T64 copies, the shared expert runs as one more slot of those
+  // launches (the decode GEMV's qmv4 arithmetic, which gemm() on its T64 copies also computes up to 16 rows) when it
+  // is a 4-bit linear pair of the routed experts' width with T64 copies that gemm() would run in bf16.
+  bool shared_in_rows_t64(const Layer& ly, int T) const {
+    const int H = cfg.hidden, I = cfg.moe_inter;
+    const QLinear &gu = ly.gate_up, &dn = ly.down;
+    return moe_rows_route(ly, T) && ly.egu.t64 && ly.edown.t64 && T <= 16 && gu.N > 0 && gu.bits == 4 &&
+           dn.bits == 4 && gu.t64 && dn.t64 && gu.N == 2 * I && gu.K == H && dn.N == H && dn.K == I && !gu.ldk &&
+           !dn.ldk && !gu.flipped && !dn.flipped && !w4a8_route(gu, T) && !w4a8_route(dn, T) && !qa8_route(gu, T) &&
+           !qa8_route(dn, T);
+  }
   bool shared_as_expert(const Layer& ly, int T) const {
     const int H = cfg.hidden, I = cfg.moe_inter;
     const QLinear &gu = ly.gate_up, &dn = ly.down;
@@ -550,7 +561,9 @@ struct Qwen35 {
     const bool rows = moe_rows_route(ly, T), q8 = !rows && qa8g_route(ly, T);
     if (q8 && !q8u.buf) die("encode_moe", "the MoE's QA8 route needs its int8 staging: construct with QA8=1");
     const bool t64 = !rows && !q8 && moe_t64_route(ly), fold = t64 && shared_as_expert(ly, T);
-    const bool shared = has_shared && !fold;
+    // on the per-row route over T64 copies the shared expert can run as one more slot of the same launches
+    const bool srow = shared_in_rows_t64(ly, T);
+    const bool shared = has_shared && !fold && !srow;
     if (shared) {
       gemm_swiglu(e, xn, ly.gate_up, act, T);
       a8_ready = false;
@@ -569,8 +582,10 @@ struct Qwen35 {
       if (ifd_moe_rows_t64_workspace(T, H, I, E, k) > splitk_bytes)
         die("encode_moe", "scratch smaller than the per-row MoE needs");
       ok(ifd_moe_rows_t64(xn.ptr<void>(), T, H, E, k, ridx.ptr<int>(), rw.ptr<float>(), rsg.ptr<float>(),
-                          ly.egu.t64.ptr<void>(), ly.edown.t64.ptr<void>(), I, shared ? sh_out.ptr<void>() : nullptr,
-                          x.ptr<void>(), 0, splitk.ptr<void>(), splitk_bytes, e.stream),
+                          ly.egu.t64.ptr<void>(), ly.edown.t64.ptr<void>(), I,
+                          srow ? ly.gate_up.t64.ptr<void>() : nullptr, srow ? ly.down.t64.ptr<void>() : nullptr,
+                          shared ? sh_out.ptr<void>() : nullptr, x.ptr<void>(), 0, splitk.ptr<void>(), splitk_bytes,
+                          e.stream),
          "encode_moe");
       return;
     }

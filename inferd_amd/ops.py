@@ -433,8 +433,9 @@ def moe_rows(xn: torch.Tensor, idx: torch.Tensor, wt: torch.Tensor, sg: Optional
 
 def moe_rows_t64(xn: torch.Tensor, idx: torch.Tensor, wt: torch.Tensor, sg: Optional[torch.Tensor], egu: T64Stack,
                  edn: T64Stack, ys: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-                 assign: bool = True) -> torch.Tensor:
-    """moe_rows on T64 stacks (ifd_moe_rows_t64): the same arguments, 16 tokens per launch group."""
+                 assign: bool = True, shared: Optional[tuple] = None) -> torch.Tensor:
+    """moe_rows on T64 stacks (ifd_moe_rows_t64): the same arguments, 16 tokens per launch group; or the shared
+    expert as shared = (T64Linear gate_up, T64Linear down) run in the same launches instead of its rows ys."""
     T, H = xn.shape
     k = idx.shape[1]
     E, I = egu.E, egu.N // 2
@@ -443,8 +444,10 @@ def moe_rows_t64(xn: torch.Tensor, idx: torch.Tensor, wt: torch.Tensor, sg: Opti
     if out is None:
         out = torch.zeros((T, H), dtype=torch.bfloat16, device=xn.device)
     ws = workspace(lib().ifd_moe_rows_t64_workspace(T, H, I, E, k), xn.device)
-    check(lib().ifd_moe_rows_t64(_p(xn), T, H, E, k, _p(idx), _p(wt), _p(sg), _p(egu.wt), _p(edn.wt), I, _p(ys),
-                                 _p(out), 1 if assign else 0, _p(ws), ws.numel(), _stream()))
+    sgu, sdn = shared if shared is not None else (None, None)
+    check(lib().ifd_moe_rows_t64(_p(xn), T, H, E, k, _p(idx), _p(wt), _p(sg), _p(egu.wt), _p(edn.wt), I,
+                                 _p(sgu.wt) if sgu else None, _p(sdn.wt) if sdn else None, _p(ys), _p(out),
+                                 1 if assign else 0, _p(ws), ws.numel(), _stream()))
     return out
 
 

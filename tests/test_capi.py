@@ -230,11 +230,14 @@ def test_moe_rows_checks():
     assert L.ifd_moe_rows_t64_workspace(16, 2048, 512, 512, 10) >= L.ifd_moe_decode_t64_workspace(16, 2048, 512, 512,
                                                                                                   10)
     assert L.ifd_moe_decode_t64_workspace(17, 2048, 512, 512, 10) == 0
-    call64 = lambda T=20, H=2048, Ex=512, k=10, idx=4096, sg=4096, I=512, ys=4096: L.ifd_moe_rows_t64(
-        4096, T, H, Ex, k, idx, 4096, sg, 4096, 4096, I, ys, 4096, 0, 4096, 0, None)
+    call64 = lambda T=20, H=2048, Ex=512, k=10, idx=4096, sg=4096, I=512, ys=4096, sw=None: L.ifd_moe_rows_t64(
+        4096, T, H, Ex, k, idx, 4096, sg, 4096, 4096, I, sw, sw, ys, 4096, 0, 4096, 0, None)
     assert call64(H=1280) == E and b"H multiple of 512" in L.ifd_last_error()
     assert call64(Ex=513) == E and call64(k=17) == E and call64(I=100) == E
     assert call64(idx=None) == E and b"null" in L.ifd_last_error()
     assert call64(sg=None) == E and b"gate weights" in L.ifd_last_error()
+    assert call64(sw=4096) == E and b"not both" in L.ifd_last_error()
+    assert call64(sw=4096, ys=None, sg=None) == E and b"gate weights" in L.ifd_last_error()
     assert call64(T=0) == _lib.IFD_OK
     assert call64() == _lib.IFD_ERR_WORKSPACE
+    assert call64(sw=4096, ys=None) == _lib.IFD_ERR_WORKSPACE

@@ -321,11 +321,14 @@ def test_moe_rows(T, k, shared):
                        composition=True)
 
 
-@pytest.mark.parametrize("T,k,shared", [(3, 10, True), (12, 10, True), (17, 4, False), (8, 16, True), (40, 2, True)])
+@pytest.mark.parametrize("T,k,shared", [(3, 10, True), (12, 10, True), (17, 4, False), (8, 16, True), (40, 2, True),
+                                          (5, 10, "weights"), (16, 4, "weights")])
 def test_moe_rows_t64(T, k, shared):
     """ifd_moe_rows_t64: the per-row route on the routed experts' T64 stacks, 16 tokens per launch group (T = 17, 40
     cross group edges): against ifd_moe_rows on the same weights and routing (the same arithmetic, sums in another
-    order: within 2^-6 of the output's scale) and against the oracle's per-token decode composition."""
+    order: within 2^-6 of the output's scale) and against the oracle's per-token decode composition. shared =
+    "weights": the shared expert's T64 copies run as one more slot of the launches, against its rows computed in the
+    same (qmv4) arithmetic and passed as ys."""
     g, ops = _gu(), _ops()
     E, H, I, seed = 64, 1024, 256, 430 + T
     egu, edn = experts(E, 2 * I, H, seed=seed), experts(E, H, I, seed=seed + 1)
@@ -337,10 +340,17 @@ def test_moe_rows_t64(T, k, shared):
     wt /= wt.sum(axis=1, keepdims=True)
     sg = rng.random(T).astype(np.float32) if shared else np.ones(T, np.float32)
     ys = gen.activations(T, H, seed=seed + 4) if shared else None
+    sw = None
+    if shared == "weights":  # the shared expert's rows in the decode arithmetic, and its T64 copies
+        s1, s2 = experts(1, 2 * I, H, seed=seed + 5), experts(1, H, I, seed=seed + 6)
+        gu = gen.f32_to_bf16(orc.qmv(xn, s1[0][0], s1[1][0], s1[2][0]))
+        ys = gen.f32_to_bf16(orc.qmv(orc.silu_mul(gu), s2[0][0], s2[1][0], s2[2][0]))
+        sw = (ops.pack_t64(g.qlinear(s1[0][0], s1[1][0], s1[2][0])), ops.pack_t64(g.qlinear(s2[0][0], s2[1][0], s2[2][0])))
     W1, W2 = g.moew(*egu), g.moew(*edn)
     T1, T2 = ops.pack_t64_stack(W1), ops.pack_t64_stack(W2)
     args = (g.dev(xn), g.dev(idx), g.dev(wt), g.dev(sg))
     ysd = g.dev(ys) if shared else None
+    yst = None if sw else ysd  # the T64 call's rows: none when the weights are given
     d = np.empty((T * k, H), np.uint16)
     for t in range(T):
         for j in range(k):
@@ -349,8 +359,8 @@ def test_moe_rows_t64(T, k, shared):
             d[t * k + j] = gen.f32_to_bf16(orc.qmv(orc.silu_mul(gu), edn[0][e], edn[1][e], edn[2][e]))[0]
     ident = np.arange(T * k, dtype=np.int32)
     for assign in (True, False):
-        out = ops.moe_rows_t64(*args, T1, T2, ysd, out=g.dev(x0), assign=assign)
-        again = ops.moe_rows_t64(*args, T1, T2, ysd, out=g.dev(x0), assign=assign)
+        out = ops.moe_rows_t64(*args, T1, T2, yst, out=g.dev(x0), assign=assign, shared=sw)
+        again = ops.moe_rows_t64(*args, T1, T2, yst, out=g.dev(x0), assign=assign, shared=sw)
         mlx = ops.moe_rows(*args, W1, W2, ysd, out=g.dev(x0), assign=assign)
         torch.cuda.synchronize()
         assert np.array_equal(g.host(out), g.host(again))
