@@ -398,7 +398,7 @@ def main():
                                     frac_hbm=byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, mlx_layout_us=ms_mlx * 1e3)
             # the drop-in operator itself: Qwen35::encode_moe (rmsnorm, router, routing, the sorted route on the
             # loader's T64 copies with the shared expert as expert E, combine into x; at T = 8 the per-row route on
-            # those copies, the shared expert through gemm()), timed by its own C++ program over this library; and
+            # those copies, the shared expert as one more slot), timed by its own C++ program over this library; and
             # the same operator on the MLX-layout stacks alone
             for key, extra in (("encode_moe_t64", []), ("encode_moe_mlx", ["--mlx"])):
                 prog = os.path.join(ROOT, "inferd_amd", "encode_moe_bench")
