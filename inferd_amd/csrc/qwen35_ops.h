@@ -508,9 +508,10 @@ struct Qwen35 {
     };
     // the decode MoE (the reference's moe2 route), each distinct expert read once; it needs the shared expert (if
     // any) unflipped, 4- or 8-bit, with the routed experts' intermediate size. The per-row route over the routed
-    // experts' T64 copies, with the shared expert (if any) as one more slot, is the same computation up to 16 tokens
-    // (every routed and shared product in the qmv4 arithmetic), so it takes the same launches, router included.
-    const bool rows_dec = moe_rows_route(ly, T) && T <= 16 && ly.egu.t64 && ly.edown.t64 &&
+    // experts' T64 copies, with the shared expert (if any) as one more slot, is the same computation (every routed
+    // and shared product in the qmv4 arithmetic), so up to 8 tokens it takes the same launches, router included
+    // (from 9 tokens the router kernel's last block routes two tokens per wave, and the separate routing is faster).
+    const bool rows_dec = moe_rows_route(ly, T) && T <= 8 && ly.egu.t64 && ly.edown.t64 &&
                           (!has_shared || shared_in_rows_t64(ly, T));
     if (moe_decode_route(ly, T) || rows_dec) {
       a8_ready = false;  // the norm's int8 rows (if it made them) are not the next GEMM's input (qwen35.h:1906)
